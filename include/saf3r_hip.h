@@ -1,0 +1,178 @@
+/*
+ * saf3r_hip.h — C ABI of the MI355X (gfx950) kernels for SAF3R head-wise sparse global
+ * attention in VGGT-style alternating frame/global transformers.
+ *
+ * Conventions
+ *   - Every entry returns an int status (SAF3R_OK = 0). On failure nothing is launched and
+ *     saf3r_last_error() returns a message (thread-local). No C++ exception crosses the ABI.
+ *   - Every device buffer is allocated by the caller; the library never allocates or frees
+ *     device memory and keeps no device state. `stream` is a hipStream_t (NULL = default
+ *     stream); every entry is asynchronous on it and performs no host synchronisation.
+ *   - bf16 buffers are passed as void* (IEEE bfloat16, 2 bytes per element).
+ *   - Host-side arrays (head tables, frequency tables) are read during the call only.
+ *
+ * Geometry (one global-attention layer, batch 1)
+ *   F frames of T tokens: the first `num_special` tokens of each frame are special (camera +
+ *   registers), the remaining P = T - num_special are patch tokens; N = F*T. head_dim = 64,
+ *   block = 64. Patch tokens of a frame form NBf = ceil(P/64) blocks (the last may be partial);
+ *   block b of frame f has the global block id f*NBf + b.
+ *
+ * Packed layout (written by saf3r_pack_qkv, read by the attention / pooling / selection kernels)
+ *   Slots per head: L = Sp + F*Pp with S = F*num_special special slots first (slot s holds token
+ *   (s / num_special)*T + s % num_special), padded to Sp = roundup(S, 64); then frame f's patch
+ *   p at slot Sp + f*Pp + p, Pp = NBf*64. Padding slots hold zeros.
+ *   Q, K: [H][L][64] bf16, rows of 128 bytes.
+ *   V:    [H][L/64][64][64] bf16, one transposed 64x64 tile per 64 slots:
+ *         tile[i][c] = V[slot = 64*tile + kappa(c)][d = 32*(i/32) + phi(i%32)], where
+ *         kappa(c) swaps bits 2 and 3 of c, and phi(i) = 16*((i>>2)&1) + 4*(i>>3) + (i&3).
+ *         (These permutations match the register layout of the MFMA 32x32x16 bf16 operands so
+ *         that every LDS read in the attention kernel is a 16-byte vector.)
+ */
+#ifndef SAF3R_HIP_H
+#define SAF3R_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SAF3R_ABI_VERSION 1
+
+enum saf3r_status {
+  SAF3R_OK = 0,
+  SAF3R_ERR_INVALID = 1,      /* bad argument, shape or pointer */
+  SAF3R_ERR_UNSUPPORTED = 2,  /* valid request this build does not implement (e.g. head_dim != 64) */
+  SAF3R_ERR_LAUNCH = 3,       /* the HIP runtime rejected a launch */
+  SAF3R_ERR_INJECTED = 4      /* failure forced through SAF3R_FAULT_INJECT (tests of error paths) */
+};
+
+/* Per-head attention pattern ids. Masks are given for query token i and key token j. */
+enum saf3r_pattern {
+  SAF3R_DENSE = 0,         /* every key.                          ref: saf3r/patch/wrapper.py:99-100 (mode "full") */
+  SAF3R_FRAME_LOCAL = 1,   /* frame(j) == frame(i).               ref: saf3r/patch/sparse_attention.py:234-253 (global_to_frame) */
+  SAF3R_ANCHOR_LOCAL = 2,  /* frame(j) in {0, frame(i)}.          ref: union of sparse_attention.py:134-140 and :234-253 */
+  SAF3R_BLOCK_DYNAMIC = 3, /* special i: every key; patch i: patch keys of the blocks listed for
+                              block(i) in the selection list.     ref: block analogue of sparse_attention.py:189-231 */
+  SAF3R_TOKEN_DYNAMIC = 4, /* reference dino_topk: special rows attend every key (this entry);
+                              patch rows go through saf3r_gather_attn_fwd.  ref: sparse_attention.py:189-231 */
+  SAF3R_ANCHOR = 5,        /* frame(j) == 0.                      ref: sparse_attention.py:134-140 (all_to_first) */
+  SAF3R_SKIP = 6           /* output zero.                        ref: sparse_attention.py:40-41 */
+};
+
+/* Row addressing of a token-row buffer: logical row r lives at
+ *   ptr + (base_row + (r / rows_per_frame) * frame_row_stride + r % rows_per_frame) * row_stride
+ * elements. A plain [n, 64] matrix is {ptr, 64, 0, n, 0}. */
+typedef struct saf3r_rows {
+  const void* ptr;
+  int64_t row_stride;
+  int64_t base_row;
+  int64_t rows_per_frame;
+  int64_t frame_row_stride;
+} saf3r_rows;
+
+int saf3r_abi_version(void);
+const char* saf3r_last_error(void);
+
+/* Number of packed slots per head (L above). Returns -1 for an invalid geometry. */
+int64_t saf3r_packed_slots(int frames, int tokens_per_frame, int num_special);
+
+/*
+ * Prologue of the patched global attention: per-head QK-LayerNorm(64) and 2-D RoPE in fp32,
+ * then bf16 packing into the layout above.
+ *   q, k, v: bf16, element (token t, head h, d) at ptr[t*tok_stride + h*head_stride + d]
+ *            (the qkv Linear output [N, 3*H*64] is q = base, k = base + H*64, v = base + 2*H*64,
+ *            tok_stride = 3*H*64, head_stride = 64).
+ *   ln_*:    fp32 [64] device arrays (weight, bias), used when apply_ln != 0.
+ *   pos:     int32 [N][2] device (y, x) positions, used when rope_inv_freq != NULL.
+ *   rope_inv_freq: host fp32 [16] inverse frequencies (1 / base^(2i/32)); NULL disables RoPE.
+ * Replaces: saf3r/patch/patch_vggt.py:577-583 (qkv reshape, q_norm/k_norm, rope) and
+ *           saf3r/models/official_vggt/layers/rope.py:154-188.
+ */
+int saf3r_pack_qkv(const void* q, const void* k, const void* v, int64_t tok_stride, int64_t head_stride,
+                   int frames, int tokens_per_frame, int num_special, int num_heads,
+                   const float* q_ln_weight, const float* q_ln_bias, const float* k_ln_weight,
+                   const float* k_ln_bias, float ln_eps, int apply_ln,
+                   const int32_t* pos, const float* rope_inv_freq,
+                   void* q_packed, void* k_packed, void* v_packed, void* stream);
+
+/*
+ * Pooled patch-block means (fp32) of the packed Q and K of the listed heads.
+ *   head_ids: host int32 [n_heads_sel]; pooled_q / pooled_k: [n_heads_sel][F*NBf][64].
+ *   k_packed / pooled_k may both be NULL (pool Q only).
+ * Each column is summed sequentially over the block's patch tokens in order (fp32) and divided
+ * once by the block population, so results are bit-identical to that definition.
+ * Replaces: block pooling of the dynamic pattern (reference precedent
+ *           saf3r/patch/adaptive_block_value.py:16-24).
+ */
+int saf3r_block_pool(const void* q_packed, const void* k_packed, int frames, int tokens_per_frame,
+                     int num_special, int num_heads, const int32_t* head_ids, int n_heads_sel,
+                     float* pooled_q, float* pooled_k, void* stream);
+
+/*
+ * Per-frame top-k from fp32 scores (bit-exact entry).
+ *   scores: [n][rows][frames*cands_per_frame]; idx: int32 [n][rows][frames*min(k, cands_per_frame)].
+ *   For each row and frame: the min(k, C) best candidates by the sortable fp32 key, descending,
+ *   ties to the lower index; values are global candidate ids f*C + c. 1 <= k <= 32.
+ * Replaces: the selection of saf3r/triton/fused_qk_topk.py:73-100 (composite key, frame-major
+ *           flush) applied to a given score matrix.
+ */
+int saf3r_topk_from_scores(const float* scores, int n, int rows, int frames, int cands_per_frame, int k,
+                           int32_t* idx, void* stream);
+
+/*
+ * Block selection of the BLOCK_DYNAMIC pattern from pooled Q/K.
+ *   pooled_q: [n][NBq][64]; pooled_k: [n][frames*blocks_per_frame][64] (fp32).
+ *   score(i, j) = sequential fmaf over d = 0..63 starting from 0.
+ *   scope 0 (per frame): idx [n][NBq][frames*min(k, NBf)], frame-major;
+ *   scope 1 (global):    idx [n][NBq][min(k, frames*NBf)].
+ *   Order: score key descending, ties to the lower block id. 1 <= k <= 32.
+ * Replaces: the block top-k of the dynamic pattern (no reference symbol; per-frame semantics of
+ *           saf3r/patch/wrapper.py:48 and saf3r/triton/fused_qk_topk.py:120-217 at block level).
+ */
+int saf3r_block_select(const float* pooled_q, const float* pooled_k, int n, int nbq, int frames,
+                       int blocks_per_frame, int k, int scope, int32_t* idx, void* stream);
+
+/*
+ * Block-sparse attention forward over the packed layout, every head in one launch.
+ *   head_pattern: host int32 [num_heads] of saf3r_pattern ids.
+ *   sel: int32 [n_block_dynamic][F*NBf][sel_width] block ids (-1 = empty), one list per
+ *        BLOCK_DYNAMIC head in increasing head order; may be NULL when no head is BLOCK_DYNAMIC.
+ *   out: bf16 natural layout, element (token t, head h, d) at out[t*out_row_stride + h*64 + d].
+ *        TOKEN_DYNAMIC heads get only their special rows written here.
+ *   scale: softmax scale (1/8 for head_dim 64).
+ * Replaces: the per-head loop saf3r/patch/wrapper.py:94-106 and the mode implementations of
+ *           saf3r/patch/sparse_attention.py:12-90 for full / global_to_frame / all_to_first / skip,
+ *           the dense special rows of dino_topk (:197-208), and the block-dynamic pattern.
+ */
+int saf3r_sparse_attn_fwd(const void* q_packed, const void* k_packed, const void* v_packed, int frames,
+                          int tokens_per_frame, int num_special, int num_heads, const int32_t* head_pattern,
+                          const int32_t* sel, int sel_width, float scale, void* out, int64_t out_row_stride,
+                          void* stream);
+
+/*
+ * Gather attention: out[r] = sum_j softmax_j(q[r] . k[idx[r][j]] * scale) v[idx[r][j]], fp32
+ * accumulation, bf16 in/out, head_dim 64; idx entries < 0 or >= num_keys are skipped.
+ *   idx: int32 [n][topk] (row stride topk, or 0 to share one list across rows).
+ * Replaces: saf3r/triton/sparse_topk_attention.py:115-166 (fused_sparse_topk_attention) and
+ *           :261-286 (the TopK > 2048 variant).
+ */
+int saf3r_gather_attn_fwd(const saf3r_rows* q, const saf3r_rows* k, const saf3r_rows* v, const int32_t* idx,
+                          int64_t idx_row_stride, int n, int topk, int64_t num_keys, float scale,
+                          const saf3r_rows* out, void* stream);
+
+/*
+ * Per-frame token top-k of q.k (bf16 inputs, fp32 MFMA accumulation).
+ *   q: n_q rows; k: frames*per_frame rows (frame f = rows [f*per_frame, (f+1)*per_frame));
+ *   idx: int32 [n_q][frames*min(topk, per_frame)] global key rows, frame-major, score descending,
+ *   ties to the lower index. 1 <= topk <= 16.
+ * Replaces: saf3r/triton/fused_qk_topk.py:120-217 (compute_qk_topk_indices_fused).
+ */
+int saf3r_token_topk(const saf3r_rows* q, const saf3r_rows* k, int n_q, int frames, int per_frame, int topk,
+                     int32_t* idx, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SAF3R_HIP_H */

@@ -1,0 +1,131 @@
+"""numpy/ctypes front end of the C selection oracle (``oracle/selection.c``).
+
+TEST INFRASTRUCTURE ONLY (see ``oracle/__init__.py``).
+
+Reference anchors: ``saf3r/triton/topk_utils.py:26-29`` (sortable key),
+``saf3r/triton/fused_qk_topk.py:73-100`` (composite key, tie rule, frame-major output),
+``saf3r/patch/adaptive_block_value.py:16-24`` (population-weighted block mean).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+_lib = None
+
+
+def build() -> str:
+    """Compile ``liboracle.so`` with the committed Makefile (gcc)."""
+    subprocess.run(["make", "-s", "-C", _HERE, "-B", "liboracle.so"], check=True)
+    return _LIB_PATH
+
+
+def _load():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        lib = ctypes.CDLL(_LIB_PATH)
+        i32, i64, p = ctypes.c_int, ctypes.c_int64, ctypes.c_void_p
+        lib.oracle_fkey.argtypes = [ctypes.c_uint32]
+        lib.oracle_fkey.restype = ctypes.c_uint32
+        lib.oracle_block_pool.argtypes = [p, i64, i32, i32, i32, i32, i32, p]
+        lib.oracle_block_pool.restype = None
+        lib.oracle_block_scores.argtypes = [p, p, i32, i32, i32, p]
+        lib.oracle_block_scores.restype = None
+        lib.oracle_frame_topk.argtypes = [p, i32, i32, i32, i32, p]
+        lib.oracle_frame_topk.restype = i32
+        lib.oracle_global_topk.argtypes = [p, i32, i32, i32, p]
+        lib.oracle_global_topk.restype = i32
+        _lib = lib
+    return _lib
+
+
+def _ptr(a: np.ndarray):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def fkey(x) -> np.ndarray:
+    """Sortable uint32 key of fp32 values (vectorised restatement of the C transform)."""
+    b = np.ascontiguousarray(np.asarray(x, dtype=np.float32)).view(np.uint32)
+    return np.where(b & np.uint32(0x80000000), ~b, b | np.uint32(0x80000000)).astype(np.uint32)
+
+
+def fkey_c(bits: int) -> int:
+    return int(_load().oracle_fkey(ctypes.c_uint32(bits)))
+
+
+def bf16_bits(x: np.ndarray) -> np.ndarray:
+    """Round fp32 -> bf16 (nearest-even) and return the 16-bit patterns."""
+    b = np.ascontiguousarray(np.asarray(x, dtype=np.float32)).view(np.uint32).astype(np.uint64)
+    rounded = (b + 0x7FFF + ((b >> 16) & 1)) >> 16
+    # NaN stays NaN (quiet); none of the oracle inputs are NaN.
+    return rounded.astype(np.uint16)
+
+
+def bf16_to_f32(h: np.ndarray) -> np.ndarray:
+    return (np.asarray(h, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def block_pool(x_bf16: np.ndarray, frames: int, tokens_per_frame: int, num_special: int,
+               block: int = 64) -> np.ndarray:
+    """Pooled patch-block means of one head. ``x_bf16``: uint16 [F*T, D] (bf16 bits)."""
+    x = np.ascontiguousarray(x_bf16, dtype=np.uint16)
+    n, d = x.shape
+    assert n == frames * tokens_per_frame
+    p = tokens_per_frame - num_special
+    nbf = -(-p // block)
+    out = np.zeros((frames * nbf, d), dtype=np.float32)
+    _load().oracle_block_pool(_ptr(x), d, frames, tokens_per_frame, num_special, d, block, _ptr(out))
+    return out
+
+
+def block_scores(pq: np.ndarray, pk: np.ndarray) -> np.ndarray:
+    """scores[i, j] = sequential-fmaf dot of pooled query block i and pooled key block j."""
+    q = np.ascontiguousarray(pq, dtype=np.float32)
+    k = np.ascontiguousarray(pk, dtype=np.float32)
+    assert q.shape[1] == k.shape[1]
+    out = np.zeros((q.shape[0], k.shape[0]), dtype=np.float32)
+    _load().oracle_block_scores(_ptr(q), _ptr(k), q.shape[0], k.shape[0], q.shape[1], _ptr(out))
+    return out
+
+
+def frame_topk(scores: np.ndarray, frames: int, k: int) -> np.ndarray:
+    """Per-frame top-k over a [NQ, F*C] score matrix -> int32 [NQ, F*min(k, C)]."""
+    s = np.ascontiguousarray(scores, dtype=np.float32)
+    nq, nc = s.shape
+    assert nc % frames == 0
+    c = nc // frames
+    ke = min(k, c)
+    out = np.full((nq, frames * ke), -1, dtype=np.int32)
+    rc = _load().oracle_frame_topk(_ptr(s), nq, frames, c, k, _ptr(out))
+    if rc != 0:
+        raise ValueError(f"oracle_frame_topk failed ({rc})")
+    return out
+
+
+def global_topk(scores: np.ndarray, k: int) -> np.ndarray:
+    s = np.ascontiguousarray(scores, dtype=np.float32)
+    nq, nc = s.shape
+    ke = min(k, nc)
+    out = np.full((nq, ke), -1, dtype=np.int32)
+    rc = _load().oracle_global_topk(_ptr(s), nq, nc, k, _ptr(out))
+    if rc != 0:
+        raise ValueError(f"oracle_global_topk failed ({rc})")
+    return out
+
+
+def block_select(q_bf16: np.ndarray, k_bf16: np.ndarray, frames: int, tokens_per_frame: int,
+                 num_special: int, topk: int, block: int = 64, scope: str = "frame") -> np.ndarray:
+    """Full block-selection pipeline of one head: pool -> score -> top-k."""
+    pq = block_pool(q_bf16, frames, tokens_per_frame, num_special, block)
+    pk = block_pool(k_bf16, frames, tokens_per_frame, num_special, block)
+    s = block_scores(pq, pk)
+    if scope == "frame":
+        return frame_topk(s, frames, topk)
+    return global_topk(s, topk)

@@ -1,0 +1,101 @@
+// Shared definitions of the gfx950 kernels: geometry of the packed layout, vector types,
+// the sortable fp32 key and the thread-local error channel of the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+
+#include "saf3r_hip.h"
+
+namespace saf3r {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kHeadDim = 64;
+constexpr int kBlock = 64;
+constexpr int kMaxHeads = 64;
+
+// ---------------------------------------------------------------------------------------
+// Error channel
+// ---------------------------------------------------------------------------------------
+void set_error(const char* fmt, ...);
+int fail(int code, const char* fmt, ...);
+// Returns SAF3R_ERR_INJECTED when the environment variable SAF3R_FAULT_INJECT names `entry`
+// (or is "all"); used by the error-path tests to force a failure before any launch.
+int injected(const char* entry);
+int check_launch(const char* what);
+
+// ---------------------------------------------------------------------------------------
+// Geometry of one layer in the packed layout
+// ---------------------------------------------------------------------------------------
+struct Geom {
+  int F;      // frames
+  int T;      // tokens per frame
+  int ns;     // special tokens per frame
+  int P;      // patch tokens per frame
+  int NBf;    // patch blocks per frame
+  int Pp;     // padded patch slots per frame (NBf * 64)
+  int S;      // special slots (F * ns)
+  int Sp;     // padded special slots
+  int nst;    // special tiles (Sp / 64)
+  int NT;     // tiles per head (L / 64)
+  int64_t L;  // slots per head
+};
+
+inline bool make_geom(int F, int T, int ns, Geom* g) {
+  if (F <= 0 || T <= 0 || ns < 0 || ns >= T) return false;
+  g->F = F;
+  g->T = T;
+  g->ns = ns;
+  g->P = T - ns;
+  g->NBf = (g->P + kBlock - 1) / kBlock;
+  g->Pp = g->NBf * kBlock;
+  g->S = F * ns;
+  g->Sp = (g->S + kBlock - 1) / kBlock * kBlock;
+  g->nst = g->Sp / kBlock;
+  g->L = (int64_t)g->Sp + (int64_t)F * g->Pp;
+  if (g->L / kBlock > (int64_t)0x7fffffff) return false;
+  g->NT = (int)(g->L / kBlock);
+  return true;
+}
+
+// Token index of a packed slot, or -1 for padding.
+__host__ __device__ inline int64_t slot_token(const Geom& g, int64_t slot) {
+  if (slot < g.Sp) {
+    if (slot >= g.S) return -1;
+    return (slot / g.ns) * g.T + slot % g.ns;
+  }
+  int64_t o = slot - g.Sp;
+  int64_t f = o / g.Pp, p = o % g.Pp;
+  if (p >= g.P) return -1;
+  return f * g.T + g.ns + p;
+}
+
+// ---------------------------------------------------------------------------------------
+// Sortable key: integer order == float order; -0.0 < +0.0; +NaN above +inf, -NaN below -inf.
+// ref: saf3r/triton/topk_utils.py:26-29
+// ---------------------------------------------------------------------------------------
+__host__ __device__ inline uint32_t fkey(float x) {
+  uint32_t b = __builtin_bit_cast(uint32_t, x);
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+// Composite 64-bit key: higher score first, then lower index. Any real candidate is > 0.
+__host__ __device__ inline uint64_t ckey(float x, uint32_t idx) {
+  return ((uint64_t)fkey(x) << 32) | (uint64_t)(0xFFFFFFFEu - idx);
+}
+__host__ __device__ inline uint32_t ckey_index(uint64_t c) { return 0xFFFFFFFEu - (uint32_t)(c & 0xFFFFFFFFu); }
+
+__device__ inline float bf16_lo(uint32_t w) { return __builtin_bit_cast(float, w << 16); }
+__device__ inline float bf16_hi(uint32_t w) { return __builtin_bit_cast(float, w & 0xFFFF0000u); }
+
+}  // namespace saf3r

@@ -1,0 +1,199 @@
+// Prologue of the patched global attention: QK-LayerNorm(64) + 2-D RoPE in fp32, bf16 packing
+// of Q, K (row-major slots) and V (transposed, permuted 64x64 tiles).
+//
+// ref: saf3r/patch/patch_vggt.py:577-583 (qkv reshape, q_norm / k_norm, rope on q and k),
+//      saf3r/models/official_vggt/layers/rope.py:86-188 (RoPE-2D: first 32 features rotated by
+//      the y position, last 32 by x; within each 32: rotate(t) = cat(-t[16:], t[:16])).
+// Under autocast(bf16) the reference runs LayerNorm and RoPE in fp32 and hands bf16 q/k/v to
+// attention; this kernel does the same and rounds once, to nearest-even bf16.
+#include "common.h"
+
+namespace saf3r {
+
+struct PackParams {
+  const __bf16* q;
+  const __bf16* k;
+  const __bf16* v;
+  int64_t tok_stride, head_stride;
+  const float* qw;
+  const float* qb;
+  const float* kw;
+  const float* kb;
+  float eps;
+  int apply_ln;
+  int apply_rope;
+  const int32_t* pos;
+  float inv_freq[16];
+  __bf16* qp;
+  __bf16* kp;
+  __bf16* vp;
+  Geom g;
+};
+
+// One 256-thread workgroup per (64-slot tile, head). Four threads own one slot row, 16 features
+// each; LayerNorm reduces across the four, RoPE pairs feature d with d +- 16 (partner thread ^ 1).
+__global__ __launch_bounds__(256) void pack_qkv_kernel(PackParams p) {
+  __shared__ __align__(16) __bf16 vs[64 * 72];  // V rows of the tile, 144-byte row pitch
+  const Geom& g = p.g;
+  const int tile = blockIdx.x, h = blockIdx.y;
+  const int t = threadIdx.x, row = t >> 2, c = t & 3;
+  const int64_t slot = (int64_t)tile * 64 + row;
+  const int64_t tok = slot_token(g, slot);
+  const int64_t src = tok * p.tok_stride + (int64_t)h * p.head_stride + 16 * c;
+  const int64_t dst = ((int64_t)h * g.L + slot) * 64 + 16 * c;
+
+  float cs[16], sn[16];
+  if (p.apply_rope && tok >= 0) {
+    const float pv = (float)p.pos[tok * 2 + (c >> 1)];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      float a = pv * p.inv_freq[j];
+      cs[j] = cosf(a);
+      sn[j] = sinf(a);
+    }
+  }
+
+#pragma unroll
+  for (int which = 0; which < 2; ++which) {
+    const __bf16* in = which == 0 ? p.q : p.k;
+    __bf16* outp = which == 0 ? p.qp : p.kp;
+    float x[16];
+    if (tok >= 0) {
+      const u32x4* s4 = reinterpret_cast<const u32x4*>(in + src);
+      u32x4 a = s4[0], b = s4[1];
+      uint32_t w[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        x[2 * j] = bf16_lo(w[j]);
+        x[2 * j + 1] = bf16_hi(w[j]);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) x[j] = 0.f;
+    }
+    if (p.apply_ln) {
+      float s = 0.f;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) s += x[j];
+      s += __shfl_xor(s, 1);
+      s += __shfl_xor(s, 2);
+      const float mean = s * (1.0f / 64.0f);
+      float v2 = 0.f;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        float dlt = x[j] - mean;
+        v2 += dlt * dlt;
+      }
+      v2 += __shfl_xor(v2, 1);
+      v2 += __shfl_xor(v2, 2);
+      const float rstd = 1.0f / sqrtf(v2 * (1.0f / 64.0f) + p.eps);
+      const float* w = which == 0 ? p.qw : p.kw;
+      const float* b = which == 0 ? p.qb : p.kb;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) x[j] = (x[j] - mean) * rstd * w[16 * c + j] + b[16 * c + j];
+    }
+    if (p.apply_rope) {
+      float y[16];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) y[j] = __shfl_xor(x[j], 1);
+      // even thread holds t1 (features 0..15 of its half), odd thread holds t2 (16..31)
+      const float sg = (c & 1) ? 1.0f : -1.0f;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) x[j] = x[j] * cs[j] + sg * y[j] * sn[j];
+    }
+    if (tok < 0) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) x[j] = 0.f;
+    }
+    u32x4 o0, o1;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      bf16x2 a = {(__bf16)x[2 * j], (__bf16)x[2 * j + 1]};
+      bf16x2 b = {(__bf16)x[8 + 2 * j], (__bf16)x[8 + 2 * j + 1]};
+      o0[j] = __builtin_bit_cast(uint32_t, a);
+      o1[j] = __builtin_bit_cast(uint32_t, b);
+    }
+    u32x4* d4 = reinterpret_cast<u32x4*>(outp + dst);
+    d4[0] = o0;
+    d4[1] = o1;
+  }
+
+  // V: stage the tile's 64 rows, then write the transposed, permuted tile.
+  {
+    u32x4 a = {0, 0, 0, 0}, b = {0, 0, 0, 0};
+    if (tok >= 0) {
+      const u32x4* s4 = reinterpret_cast<const u32x4*>(p.v + src);
+      a = s4[0];
+      b = s4[1];
+    }
+    u32x4* l4 = reinterpret_cast<u32x4*>(vs + row * 72 + 16 * c);
+    l4[0] = a;
+    l4[1] = b;
+  }
+  __syncthreads();
+  {
+    const int i = t >> 2;                               // tile row (d after permutation)
+    const int ii = i & 31;
+    const int d = 32 * (i >> 5) + 16 * ((ii >> 2) & 1) + 4 * (ii >> 3) + (ii & 3);  // phi
+    uint32_t w[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      int c0 = 16 * c + 2 * j, c1 = c0 + 1;
+      int k0 = (c0 & ~12) | ((c0 & 4) << 1) | ((c0 & 8) >> 1);  // kappa
+      int k1 = (c1 & ~12) | ((c1 & 4) << 1) | ((c1 & 8) >> 1);
+      uint16_t lo = __builtin_bit_cast(uint16_t, vs[k0 * 72 + d]);
+      uint16_t hi = __builtin_bit_cast(uint16_t, vs[k1 * 72 + d]);
+      w[j] = (uint32_t)lo | ((uint32_t)hi << 16);
+    }
+    u32x4* d4 = reinterpret_cast<u32x4*>(p.vp + ((int64_t)h * g.L + (int64_t)tile * 64) * 64 + i * 64 + 16 * c);
+    d4[0] = u32x4{w[0], w[1], w[2], w[3]};
+    d4[1] = u32x4{w[4], w[5], w[6], w[7]};
+  }
+}
+
+}  // namespace saf3r
+
+using namespace saf3r;
+
+extern "C" int saf3r_pack_qkv(const void* q, const void* k, const void* v, int64_t tok_stride, int64_t head_stride,
+                              int frames, int tokens_per_frame, int num_special, int num_heads,
+                              const float* q_ln_weight, const float* q_ln_bias, const float* k_ln_weight,
+                              const float* k_ln_bias, float ln_eps, int apply_ln, const int32_t* pos,
+                              const float* rope_inv_freq, void* q_packed, void* k_packed, void* v_packed,
+                              void* stream) {
+  if (int e = injected("saf3r_pack_qkv")) return e;
+  PackParams p;
+  if (!make_geom(frames, tokens_per_frame, num_special, &p.g))
+    return fail(SAF3R_ERR_INVALID, "saf3r_pack_qkv: invalid geometry F=%d T=%d ns=%d", frames, tokens_per_frame,
+                num_special);
+  if (num_heads <= 0 || num_heads > 65535) return fail(SAF3R_ERR_INVALID, "saf3r_pack_qkv: bad num_heads %d", num_heads);
+  if (!q || !k || !v || !q_packed || !k_packed || !v_packed)
+    return fail(SAF3R_ERR_INVALID, "saf3r_pack_qkv: null tensor pointer");
+  if (tok_stride % 8 || head_stride % 8 || ((uintptr_t)q | (uintptr_t)k | (uintptr_t)v) % 16)
+    return fail(SAF3R_ERR_INVALID, "saf3r_pack_qkv: inputs must be 16-byte aligned with strides a multiple of 8");
+  if (((uintptr_t)q_packed | (uintptr_t)k_packed | (uintptr_t)v_packed) % 16)
+    return fail(SAF3R_ERR_INVALID, "saf3r_pack_qkv: packed outputs must be 16-byte aligned");
+  if (apply_ln && (!q_ln_weight || !q_ln_bias || !k_ln_weight || !k_ln_bias))
+    return fail(SAF3R_ERR_INVALID, "saf3r_pack_qkv: LayerNorm requested without parameters");
+  if (rope_inv_freq && !pos) return fail(SAF3R_ERR_INVALID, "saf3r_pack_qkv: RoPE requested without positions");
+  p.q = (const __bf16*)q;
+  p.k = (const __bf16*)k;
+  p.v = (const __bf16*)v;
+  p.tok_stride = tok_stride;
+  p.head_stride = head_stride;
+  p.qw = q_ln_weight;
+  p.qb = q_ln_bias;
+  p.kw = k_ln_weight;
+  p.kb = k_ln_bias;
+  p.eps = ln_eps;
+  p.apply_ln = apply_ln != 0;
+  p.apply_rope = rope_inv_freq != nullptr;
+  p.pos = pos;
+  for (int j = 0; j < 16; ++j) p.inv_freq[j] = rope_inv_freq ? rope_inv_freq[j] : 0.f;
+  p.qp = (__bf16*)q_packed;
+  p.kp = (__bf16*)k_packed;
+  p.vp = (__bf16*)v_packed;
+  dim3 grid(p.g.NT, num_heads);
+  hipLaunchKernelGGL(pack_qkv_kernel, grid, dim3(256), 0, (hipStream_t)stream, p);
+  return check_launch("saf3r_pack_qkv");
+}

@@ -1,0 +1,234 @@
+"""torch-facing wrappers of the C-ABI kernels. Buffers are allocated here with torch (the library
+never allocates); every call is asynchronous on the current HIP stream.
+
+Tensor conventions: bf16 CUDA tensors, head_dim 64, contiguous unless stated otherwise.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+from typing import Sequence
+
+import torch
+
+from . import _lib
+from .layout import BLOCK, HEAD_DIM, Geometry
+
+# Pattern ids (``enum saf3r_pattern``).
+DENSE, FRAME_LOCAL, ANCHOR_LOCAL, BLOCK_DYNAMIC, TOKEN_DYNAMIC, ANCHOR, SKIP = range(7)
+PATTERN_NAMES = {
+    DENSE: "dense", FRAME_LOCAL: "frame_local", ANCHOR_LOCAL: "anchor_local",
+    BLOCK_DYNAMIC: "block_topk", TOKEN_DYNAMIC: "dino_topk", ANCHOR: "all_to_first", SKIP: "skip",
+}
+
+
+def _ptr(t: torch.Tensor | None):
+    return ctypes.c_void_p(0 if t is None else t.data_ptr())
+
+
+def _need_cuda(*ts):
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise ValueError("saf3r kernels take GPU tensors")
+
+
+def _i32_array(vals: Sequence[int]):
+    arr = (ctypes.c_int32 * len(vals))(*[int(v) for v in vals])
+    return arr
+
+
+def rope_inv_freq(base: float = 100.0, feature_dim: int = 32) -> torch.Tensor:
+    """Inverse frequencies of the 2-D RoPE (``rope.py:103-104``) for fp32 tokens (CPU tensor)."""
+    exponents = torch.arange(0, feature_dim, 2).float() / feature_dim
+    return 1.0 / (base ** exponents)
+
+
+def packed_buffers(geom: Geometry, num_heads: int, device) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    L = geom.slots
+    q = torch.empty(num_heads, L, HEAD_DIM, dtype=torch.bfloat16, device=device)
+    k = torch.empty_like(q)
+    v = torch.empty(num_heads, L // BLOCK, BLOCK, HEAD_DIM, dtype=torch.bfloat16, device=device)
+    return q, k, v
+
+
+def pack_qkv(q, k, v, tok_stride: int, head_stride: int, geom: Geometry, num_heads: int,
+             ln_q=None, ln_k=None, ln_eps: float = 1e-5, pos=None, inv_freq=None, out=None):
+    """QK-LayerNorm + RoPE-2D + packing (``saf3r_pack_qkv``). ``q``/``k``/``v`` are tensors (or
+    views) whose element (t, h, d) is at ``data_ptr + t*tok_stride + h*head_stride + d``."""
+    _need_cuda(q, k, v)
+    lib = _lib.load()
+    qp, kp, vp = out if out is not None else packed_buffers(geom, num_heads, q.device)
+    apply_ln = ln_q is not None
+    if apply_ln:
+        qw, qb = (t.detach().float().contiguous() for t in ln_q)
+        kw, kb = (t.detach().float().contiguous() for t in ln_k)
+    else:
+        qw = qb = kw = kb = None
+    freq = None
+    if inv_freq is not None:
+        if pos is None:
+            raise ValueError("RoPE needs positions")
+        pos = pos.to(device=q.device, dtype=torch.int32).contiguous()
+        f = inv_freq.detach().float().cpu().contiguous()
+        freq = (ctypes.c_float * 16)(*f.tolist())
+    _lib.check(lib.saf3r_pack_qkv(
+        _ptr(q), _ptr(k), _ptr(v), tok_stride, head_stride, geom.frames, geom.tokens_per_frame, geom.num_special,
+        num_heads, _ptr(qw), _ptr(qb), _ptr(kw), _ptr(kb), float(ln_eps), int(apply_ln),
+        _ptr(pos) if freq is not None else None, freq, _ptr(qp), _ptr(kp), _ptr(vp), _lib.stream_ptr()))
+    return qp, kp, vp
+
+
+def pack_heads(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, geom: Geometry, **kw):
+    """Pack per-head tensors [H, N, 64] (no LayerNorm / RoPE unless requested)."""
+    H, N, D = q.shape
+    assert D == HEAD_DIM and N == geom.tokens and k.shape == q.shape == v.shape
+    q, k, v = (t.to(torch.bfloat16).contiguous() for t in (q, k, v))
+    return pack_qkv(q, k, v, HEAD_DIM, N * HEAD_DIM, geom, H, **kw)
+
+
+def _check_packed(qp, kp, vp, geom: Geometry):
+    H = qp.shape[0]
+    exp_rows = (H, geom.slots, HEAD_DIM)
+    for t in (qp, kp):
+        if t is not None and (tuple(t.shape) != exp_rows or t.dtype != torch.bfloat16 or not t.is_contiguous()):
+            raise ValueError(f"packed Q/K must be contiguous bf16 {exp_rows}, got {tuple(t.shape)}")
+    if vp is not None and (tuple(vp.shape) != (H, geom.tiles, BLOCK, HEAD_DIM) or not vp.is_contiguous()):
+        raise ValueError(f"packed V must be contiguous bf16 {(H, geom.tiles, BLOCK, HEAD_DIM)}")
+
+
+def block_pool(qp: torch.Tensor, kp: torch.Tensor | None, geom: Geometry, heads: Sequence[int]):
+    """fp32 block means [n_heads, F*NBf, 64] of packed Q (and K)."""
+    _need_cuda(qp, kp)
+    lib = _lib.load()
+    _check_packed(qp, kp, None, geom)
+    H = qp.shape[0]
+    n = len(heads)
+    pq = torch.empty(n, geom.num_blocks, HEAD_DIM, dtype=torch.float32, device=qp.device)
+    pk = torch.empty_like(pq) if kp is not None else None
+    _lib.check(lib.saf3r_block_pool(_ptr(qp), _ptr(kp), geom.frames, geom.tokens_per_frame, geom.num_special, H,
+                                    _i32_array(heads), n, _ptr(pq), _ptr(pk), _lib.stream_ptr()))
+    return pq, pk
+
+
+def topk_from_scores(scores: torch.Tensor, frames: int, k: int) -> torch.Tensor:
+    """Per-frame top-k of fp32 scores [..., rows, frames*C] -> int32 [..., rows, frames*min(k, C)]."""
+    _need_cuda(scores)
+    lib = _lib.load()
+    s = scores.float().contiguous()
+    rows, ncol = s.shape[-2], s.shape[-1]
+    n = s.numel() // (rows * ncol) if s.numel() else 0
+    C = ncol // frames
+    if C * frames != ncol:
+        raise ValueError("columns are not frames * candidates")
+    ke = min(k, C)
+    idx = torch.empty(*s.shape[:-1], frames * ke, dtype=torch.int32, device=s.device)
+    _lib.check(lib.saf3r_topk_from_scores(_ptr(s), max(n, 1), rows, frames, C, k, _ptr(idx), _lib.stream_ptr()))
+    return idx
+
+
+def block_select(pooled_q: torch.Tensor, pooled_k: torch.Tensor, frames: int, blocks_per_frame: int, k: int,
+                 scope: str = "frame") -> torch.Tensor:
+    """Block top-k from pooled Q/K: int32 [n, NBq, width] of global block ids."""
+    _need_cuda(pooled_q, pooled_k)
+    lib = _lib.load()
+    n, nbq, _ = pooled_q.shape
+    if scope == "frame":
+        width = frames * min(k, blocks_per_frame)
+    elif scope == "global":
+        width = min(k, frames * blocks_per_frame)
+    else:
+        raise ValueError(f"unknown topk scope {scope!r}")
+    idx = torch.empty(n, nbq, width, dtype=torch.int32, device=pooled_q.device)
+    _lib.check(lib.saf3r_block_select(_ptr(pooled_q.contiguous()), _ptr(pooled_k.contiguous()), n, nbq, frames,
+                                      blocks_per_frame, k, 0 if scope == "frame" else 1, _ptr(idx),
+                                      _lib.stream_ptr()))
+    return idx
+
+
+def sparse_attn_fwd(qp, kp, vp, geom: Geometry, patterns: Sequence[int], sel: torch.Tensor | None = None,
+                    scale: float | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """All heads in one launch. Returns (or fills) ``out`` bf16 [N, H*64] in natural token order."""
+    _need_cuda(qp, kp, vp)
+    lib = _lib.load()
+    H = qp.shape[0]
+    if len(patterns) != H:
+        raise ValueError("one pattern per head")
+    _check_packed(qp, kp, vp, geom)
+    if out is None:
+        out = torch.empty(geom.tokens, H * HEAD_DIM, dtype=torch.bfloat16, device=qp.device)
+    elif (out.dtype != torch.bfloat16 or out.dim() != 2 or out.shape[0] != geom.tokens
+          or out.shape[1] < H * HEAD_DIM or out.stride(1) != 1):
+        raise ValueError(f"out must be bf16 [N, >= H*64] with unit column stride, got {tuple(out.shape)}")
+    scale = 1.0 / math.sqrt(HEAD_DIM) if scale is None else scale
+    width = 0
+    n_dyn = sum(1 for p in patterns if p == BLOCK_DYNAMIC)
+    if n_dyn:
+        if sel is None:
+            raise ValueError("block-dynamic heads need a selection list")
+        sel = sel.to(torch.int32).contiguous()
+        if sel.dim() != 3 or sel.shape[0] != n_dyn or sel.shape[1] != geom.num_blocks:
+            raise ValueError(f"sel must be [{n_dyn}, {geom.num_blocks}, W], got {tuple(sel.shape)}")
+        width = sel.shape[-1]
+    else:
+        sel = None
+    _lib.check(lib.saf3r_sparse_attn_fwd(
+        _ptr(qp), _ptr(kp), _ptr(vp), geom.frames, geom.tokens_per_frame, geom.num_special, H,
+        _i32_array(patterns), _ptr(sel), width, float(scale), _ptr(out), out.stride(0), _lib.stream_ptr()))
+    return out
+
+
+def rows(t: torch.Tensor, row_stride: int | None = None, base_row: int = 0, rows_per_frame: int | None = None,
+         frame_row_stride: int = 0, offset: int = 0) -> _lib.Rows:
+    """Row descriptor over a bf16 tensor (``offset`` in elements from its data pointer)."""
+    rs = t.stride(-2) if row_stride is None else row_stride
+    rpf = (1 << 62) if rows_per_frame is None else rows_per_frame
+    return _lib.Rows(t.data_ptr() + 2 * offset, rs, base_row, rpf, frame_row_stride)
+
+
+def gather_attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, idx: torch.Tensor,
+                    scale: float | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """``fused_sparse_topk_attention`` (``saf3r/triton/sparse_topk_attention.py:115-166``):
+    q [N, 64], k/v [Nk, 64] bf16, idx int32 [N, TopK] (a stride-0 row view shares one list)."""
+    _need_cuda(q, k, v, idx)
+    n, d = q.shape
+    if d != HEAD_DIM:
+        raise ValueError("head_dim must be 64")
+    q, k, v = (t.to(torch.bfloat16).contiguous() for t in (q, k, v))
+    if idx.stride(-1) != 1:
+        idx = idx.contiguous()
+    idx = idx.to(torch.int32)
+    if out is None:
+        out = torch.empty(n, v.shape[1], dtype=torch.bfloat16, device=q.device)
+    return gather_attn_rows(rows(q), rows(k), rows(v), idx, idx.stride(0), n, idx.shape[1], k.shape[0], scale,
+                            rows(out), out)
+
+
+def gather_attn_rows(qr, kr, vr, idx, idx_row_stride, n, topk, num_keys, scale, outr, keep=None):
+    lib = _lib.load()
+    scale = 1.0 / math.sqrt(HEAD_DIM) if scale is None else scale
+    _lib.check(lib.saf3r_gather_attn_fwd(ctypes.byref(qr), ctypes.byref(kr), ctypes.byref(vr), _ptr(idx),
+                                         idx_row_stride, n, topk, num_keys, float(scale), ctypes.byref(outr),
+                                         _lib.stream_ptr()))
+    return keep
+
+
+def token_topk(q: torch.Tensor, k: torch.Tensor, frames: int, per_frame: int, topk: int,
+               qrows: _lib.Rows | None = None, krows: _lib.Rows | None = None, n_q: int | None = None):
+    """``compute_qk_topk_indices_fused`` (``saf3r/triton/fused_qk_topk.py:120-217``) for one batch:
+    q [Nq, 64], k [frames*per_frame, 64] bf16 -> int32 [Nq, frames*min(topk, per_frame)]."""
+    _need_cuda(q, k)
+    lib = _lib.load()
+    if qrows is None:
+        q = q.to(torch.bfloat16).contiguous()
+        qrows = rows(q)
+        n_q = q.shape[0]
+    if krows is None:
+        k = k.to(torch.bfloat16).contiguous()
+        if k.shape[0] != frames * per_frame:
+            raise ValueError("k must hold frames * per_frame rows")
+        krows = rows(k)
+    ke = min(topk, per_frame)
+    idx = torch.empty(n_q, frames * ke, dtype=torch.int32, device=q.device)
+    _lib.check(lib.saf3r_token_topk(ctypes.byref(qrows), ctypes.byref(krows), n_q, frames, per_frame, topk,
+                                    _ptr(idx), _lib.stream_ptr()))
+    return idx

@@ -1,0 +1,78 @@
+"""CPU-side checks of the C ABI: the library loads, exports exactly what the header declares,
+validates arguments before touching a GPU, and reports injected failures."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared():
+    text = open(os.path.join(ROOT, "include", "saf3r_hip.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(saf3r_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol(pkg):
+    from importlib import import_module
+    lib_mod = import_module(pkg.__name__ + "._lib")
+    lib = lib_mod.load()
+    names = _declared()
+    assert len(names) >= 10
+    for n in names:
+        assert hasattr(lib, n), n
+    assert set(names) == set(lib_mod.EXPORTS)
+    assert lib.saf3r_abi_version() == 1
+
+
+def test_packed_slots_matches_layout(pkg):
+    from importlib import import_module
+    lib = import_module(pkg.__name__ + "._lib").load()
+    for F, T, ns in [(4, 1374, 5), (128, 1374, 5), (3, 155, 5), (2, 64, 0), (96, 1301, 5), (1, 6, 5)]:
+        g = pkg.Geometry(F, T, ns)
+        assert lib.saf3r_packed_slots(F, T, ns) == g.slots
+    assert pkg.Geometry(128, 1374).slots == 640 + 128 * 1408
+    assert lib.saf3r_packed_slots(0, 10, 1) == -1
+    assert lib.saf3r_packed_slots(2, 5, 5) == -1
+
+
+def test_invalid_arguments_fail_before_launch(pkg):
+    from importlib import import_module
+    L = import_module(pkg.__name__ + "._lib")
+    lib = L.load()
+    pat = (ctypes.c_int32 * 2)(0, 0)
+    rc = lib.saf3r_sparse_attn_fwd(None, None, None, 2, 100, 5, 2, pat, None, 0, 0.125, None, 128, None)
+    assert rc == 1 and b"null" in lib.saf3r_last_error()
+    bad = (ctypes.c_int32 * 1)(9)
+    rc = lib.saf3r_sparse_attn_fwd(ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16), 2, 100, 5, 1, bad,
+                                   None, 0, 0.125, ctypes.c_void_p(16), 64, None)
+    assert rc == 1 and b"unknown pattern" in lib.saf3r_last_error()
+    rc = lib.saf3r_block_select(ctypes.c_void_p(16), ctypes.c_void_p(16), 1, 4, 2, 2, 33, 0, ctypes.c_void_p(16), None)
+    assert rc == 2  # k beyond the supported range
+    rc = lib.saf3r_pack_qkv(None, None, None, 64, 64, 0, 10, 1, 1, None, None, None, None, 1e-5, 0, None, None,
+                            None, None, None, None)
+    assert rc == 1 and b"geometry" in lib.saf3r_last_error()
+    with pytest.raises(L.Saf3rError):
+        L.check(1)
+
+
+def test_fault_injection_is_reported(pkg, monkeypatch):
+    from importlib import import_module
+    lib = import_module(pkg.__name__ + "._lib").load()
+    monkeypatch.setenv("SAF3R_FAULT_INJECT", "saf3r_block_select")
+    rc = lib.saf3r_block_select(None, None, 1, 1, 1, 1, 1, 0, None, None)
+    assert rc == 4 and b"injected" in lib.saf3r_last_error()
+    monkeypatch.setenv("SAF3R_FAULT_INJECT", "")
+    rc = lib.saf3r_block_select(None, None, 1, 1, 1, 1, 1, 0, None, None)
+    assert rc == 1
+
+
+def test_geometry_derived_sizes(pkg):
+    g = pkg.Geometry(128, 1374, 5)
+    assert (g.patches, g.blocks_per_frame, g.num_blocks, g.tokens) == (1369, 22, 2816, 175872)
+    g5 = pkg.Geometry(96, 1301, 5)
+    assert (g5.blocks_per_frame, g5.num_blocks, g5.tokens) == (21, 2016, 124896)
+    with pytest.raises(ValueError):
+        pkg.Geometry.from_tokens(100, 30)

@@ -1,0 +1,240 @@
+"""GPU parity of every kernel against the CPU oracle on the same seeded inputs.
+
+Bars: packing without LayerNorm/RoPE, pooling, top-k and block selection are bit-exact; attention
+outputs are within max-abs 2e-2 and mean-abs 2e-3 (bf16 kernel vs fp32/fp64 oracle on identical
+bf16 inputs and identical index lists); LayerNorm+RoPE packing is within 1 bf16 ulp-scale error.
+"""
+import importlib
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as OA
+from oracle import selection as OS
+from tests.layout_ref import slot_tokens, unpack_rows, unpack_v
+
+pytestmark = pytest.mark.gpu
+ATOL_MAX, ATOL_MEAN = 2e-2, 2e-3
+
+
+@pytest.fixture(scope="module")
+def ops(pkg):
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    return importlib.import_module(pkg.__name__ + ".ops")
+
+
+DEV = "cuda:0"
+GEOMS = [(3, 155, 5), (4, 1374, 5), (2, 64, 0), (1, 70, 5), (14, 60, 5)]
+
+
+def _qkv(H, N, seed, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return [(torch.randn(H, N, 64, generator=g) * scale).to(torch.bfloat16) for _ in range(3)]
+
+
+def _check_close(got, ref, what):
+    err = (got.float() - ref.float()).abs()
+    print(f"{what}: max {err.max().item():.3g} mean {err.mean().item():.3g}", flush=True)
+    assert err.max().item() <= ATOL_MAX, f"{what}: max abs {err.max().item()}"
+    assert err.mean().item() <= ATOL_MEAN, f"{what}: mean abs {err.mean().item()}"
+
+
+@pytest.mark.parametrize("F,T,ns", GEOMS)
+def test_pack_layout_bit_exact(ops, pkg, F, T, ns):
+    geom = pkg.Geometry(F, T, ns)
+    H = 3
+    q, k, v = _qkv(H, geom.tokens, seed=F * 7 + T)
+    qp, kp, vp = ops.pack_heads(q.to(DEV), k.to(DEV), v.to(DEV), geom)
+    torch.cuda.synchronize()
+    toks = slot_tokens(F, T, ns)
+    for src, pk in ((q, qp), (k, kp)):
+        nat, pad = unpack_rows(pk.cpu(), toks, geom.tokens)
+        assert torch.equal(nat, src) and (pad == 0).all()
+    nat, pad = unpack_v(vp.cpu(), toks, geom.tokens)
+    assert torch.equal(nat, v) and (pad == 0).all()
+
+
+def test_pack_layernorm_rope(ops, pkg):
+    geom = pkg.Geometry(3, 5 + 7 * 9, 5)
+    H, N = 4, geom.tokens
+    g = torch.Generator().manual_seed(11)
+    qkv = (torch.randn(N, 3 * H * 64, generator=g) * 2 + 0.5).to(torch.bfloat16)
+    lnq = (torch.rand(64, generator=g) + 0.5, torch.randn(64, generator=g) * 0.1)
+    lnk = (torch.rand(64, generator=g) + 0.5, torch.randn(64, generator=g) * 0.1)
+    pos = OA.vggt_positions(geom.frames, 7, 9)
+    d = qkv.to(DEV)
+    C = H * 64
+    qp, kp, vp = ops.pack_qkv(d, d[:, C:], d[:, 2 * C:], 3 * C, 64, geom, H,
+                              ln_q=[t.to(DEV) for t in lnq], ln_k=[t.to(DEV) for t in lnk], ln_eps=1e-5,
+                              pos=pos.to(DEV), inv_freq=ops.rope_inv_freq(100.0))
+    torch.cuda.synchronize()
+    qr, kr, vr = OA.qkv_prologue(qkv, H, lnq, lnk, pos)
+    toks = slot_tokens(geom.frames, geom.tokens_per_frame, 5)
+    qn, _ = unpack_rows(qp.cpu(), toks, N)
+    kn, _ = unpack_rows(kp.cpu(), toks, N)
+    vn, _ = unpack_v(vp.cpu(), toks, N)
+    assert torch.equal(vn, vr)
+    for got, ref, nm in ((qn, qr, "q"), (kn, kr, "k")):
+        err = (got.float() - ref.float()).abs()
+        tol = ref.float().abs() * 2 ** -7 + 1e-3  # one bf16 ulp of rounding-point difference
+        assert (err <= tol).all(), f"{nm}: worst {err.max()}"
+
+
+@pytest.mark.parametrize("F,T,ns", GEOMS)
+def test_block_pool_bit_exact(ops, pkg, F, T, ns):
+    geom = pkg.Geometry(F, T, ns)
+    H = 3
+    q, k, v = _qkv(H, geom.tokens, seed=5 + F)
+    qp, kp, _ = ops.pack_heads(q.to(DEV), k.to(DEV), v.to(DEV), geom)
+    pq, pk = ops.block_pool(qp, kp, geom, [2, 0])
+    torch.cuda.synchronize()
+    for slot, h in enumerate([2, 0]):
+        for src, got in ((q, pq), (k, pk)):
+            ref = OS.block_pool(OS.bf16_bits(src[h].float().numpy()), F, T, ns)
+            assert np.array_equal(got[slot].cpu().numpy().view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("frames,C,k", [(4, 22, 4), (128, 22, 4), (3, 7, 8), (2, 1369, 4), (5, 9, 32), (1, 33, 16)])
+def test_topk_from_scores_bit_exact(ops, frames, C, k):
+    rng = np.random.default_rng(frames * 31 + C)
+    s = rng.integers(-4, 5, size=(2, 37, frames * C)).astype(np.float32)  # ties everywhere
+    s[0, 0, :4] = [-0.0, 0.0, np.inf, -np.inf]
+    s[1, 3] = rng.standard_normal(frames * C).astype(np.float32)
+    got = ops.topk_from_scores(torch.from_numpy(s).to(DEV), frames, k).cpu().numpy()
+    for b in range(2):
+        assert np.array_equal(got[b], OS.frame_topk(s[b], frames, k))
+
+
+@pytest.mark.parametrize("frames,nbf,k,scope", [(4, 22, 4, "frame"), (32, 22, 4, "frame"), (6, 21, 8, "frame"),
+                                                 (3, 5, 8, "frame"), (4, 22, 4, "global"), (7, 3, 16, "global")])
+def test_block_select_bit_exact(ops, frames, nbf, k, scope):
+    rng = np.random.default_rng(frames + nbf + k)
+    pq = rng.standard_normal((2, frames * nbf, 64)).astype(np.float32)
+    pk = rng.standard_normal((2, frames * nbf, 64)).astype(np.float32)
+    pk[1, 3] = pk[1, 5]  # exact duplicate candidates: tie -> lower block id
+    got = ops.block_select(torch.from_numpy(pq).to(DEV), torch.from_numpy(pk).to(DEV), frames, nbf, k, scope)
+    got = got.cpu().numpy()
+    for h in range(2):
+        s = OS.block_scores(pq[h], pk[h])
+        ref = OS.frame_topk(s, frames, k) if scope == "frame" else OS.global_topk(s, k)
+        assert np.array_equal(got[h], ref)
+
+
+def _run_layer(ops, pkg, geom, q, k, v, patterns, k_sel=2):
+    qp, kp, vp = ops.pack_heads(q.to(DEV), k.to(DEV), v.to(DEV), geom)
+    dyn = [h for h, p in enumerate(patterns) if p == ops.BLOCK_DYNAMIC]
+    sel = None
+    if dyn:
+        pq, pk = ops.block_pool(qp, kp, geom, dyn)
+        sel = ops.block_select(pq, pk, geom.frames, geom.blocks_per_frame, k_sel)
+    out = ops.sparse_attn_fwd(qp, kp, vp, geom, patterns, sel)
+    torch.cuda.synchronize()
+    return out, sel, dyn
+
+
+@pytest.mark.parametrize("F,T,ns", GEOMS)
+def test_sparse_attention_all_patterns(ops, pkg, F, T, ns):
+    geom = pkg.Geometry(F, T, ns)
+    patterns = [ops.DENSE, ops.FRAME_LOCAL, ops.ANCHOR_LOCAL, ops.BLOCK_DYNAMIC, ops.ANCHOR, ops.SKIP,
+                ops.BLOCK_DYNAMIC, ops.FRAME_LOCAL]
+    H = len(patterns)
+    q, k, v = _qkv(H, geom.tokens, seed=F * 13 + T, scale=1.5)
+    out, sel, dyn = _run_layer(ops, pkg, geom, q, k, v, patterns)
+    og = OA.Geometry(F, T, ns)
+    sel_by_head = {h: sel[i].cpu() for i, h in enumerate(dyn)}
+    got = out.float().cpu().reshape(geom.tokens, H, 64).permute(1, 0, 2)
+    for h, pat in enumerate(patterns):
+        ref = OA.sparse_attention_gathered(q[h].float(), k[h].float(), v[h].float(), pat, og, sel_by_head.get(h),
+                                           dtype=torch.float64)
+        _check_close(got[h], ref, f"F{F} T{T} ns{ns} head {h} pattern {pat}")
+
+
+def test_sparse_attention_selection_edge_cases(ops, pkg):
+    """Hand-made selection lists: -1 entries, a single block, whole-frame selections."""
+    geom = pkg.Geometry(3, 155, 5)
+    nb = geom.num_blocks
+    H = 2
+    q, k, v = _qkv(H, geom.tokens, seed=77)
+    qp, kp, vp = ops.pack_heads(q.to(DEV), k.to(DEV), v.to(DEV), geom)
+    sel = torch.full((2, nb, 5), -1, dtype=torch.int32)
+    for b in range(nb):
+        sel[0, b, 0] = (b * 5) % nb
+        sel[0, b, 3] = (b + 1) % nb if (b + 1) % nb != (b * 5) % nb else -1
+        sel[1, b, :3] = torch.tensor([b % 3, 3 + b % 3, 6 + b % 3])
+    out = ops.sparse_attn_fwd(qp, kp, vp, geom, [ops.BLOCK_DYNAMIC, ops.BLOCK_DYNAMIC], sel.to(DEV))
+    torch.cuda.synchronize()
+    og = OA.Geometry(3, 155, 5)
+    got = out.float().cpu().reshape(geom.tokens, H, 64).permute(1, 0, 2)
+    for h in range(H):
+        ref = OA.pattern_attention(q[h].float(), k[h].float(), v[h].float(), OA.BLOCK_DYNAMIC, og, sel[h])
+        _check_close(got[h], ref, f"edge head {h}")
+
+
+def test_sparse_attention_structured_c1(ops, pkg):
+    """The 4-frame VGGT shape with the structured generator and round-robin patterns."""
+    synth = importlib.import_module(pkg.__name__ + ".synth")
+    wl = synth.structured_qkv(frames=4, heads=4, seed=0)
+    geom = wl.geom
+    patterns = synth.round_robin_patterns(4)
+    q, k, v = (t.to(torch.bfloat16) for t in (wl.q, wl.k, wl.v))
+    out, sel, dyn = _run_layer(ops, pkg, geom, q, k, v, patterns, k_sel=4)
+    og = OA.Geometry(geom.frames, geom.tokens_per_frame, geom.num_special)
+    got = out.float().cpu().reshape(geom.tokens, 4, 64).permute(1, 0, 2)
+    # the selection is bit-exact against the oracle pipeline
+    for i, h in enumerate(dyn):
+        ref_sel = OS.block_select(OS.bf16_bits(q[h].float().numpy()), OS.bf16_bits(k[h].float().numpy()),
+                                  geom.frames, geom.tokens_per_frame, geom.num_special, 4)
+        assert np.array_equal(sel[i].cpu().numpy(), ref_sel)
+    sel_by_head = {h: sel[i].cpu() for i, h in enumerate(dyn)}
+    for h, pat in enumerate(patterns):
+        ref = OA.sparse_attention_gathered(q[h].float(), k[h].float(), v[h].float(), pat, og, sel_by_head.get(h),
+                                           dtype=torch.float64)
+        _check_close(got[h], ref, f"C1 head {h} pattern {pat}")
+
+
+@pytest.mark.parametrize("n,nk,topk", [(100, 300, 7), (37, 64, 64), (64, 5000, 512), (5, 3000, 2100)])
+def test_gather_attention(ops, n, nk, topk):
+    g = torch.Generator().manual_seed(n + topk)
+    q, k, v = (torch.randn(m, 64, generator=g).to(torch.bfloat16) for m in (n, nk, nk))
+    idx = torch.randint(0, nk, (n, topk), generator=g, dtype=torch.int32)
+    idx[0, :3] = -1
+    got = ops.gather_attn_fwd(q.to(DEV), k.to(DEV), v.to(DEV), idx.to(DEV))
+    torch.cuda.synchronize()
+    ref = OA.gather_attention(q.float(), k.float(), v.float(), idx, dtype=torch.float64)
+    _check_close(got.cpu(), ref, f"gather n{n} topk{topk}")
+
+
+def test_gather_attention_shared_list(ops):
+    g = torch.Generator().manual_seed(3)
+    q, k, v = (torch.randn(m, 64, generator=g).to(torch.bfloat16) for m in (50, 400, 400))
+    lst = torch.randperm(400, generator=g)[:96].int()
+    idx = lst[None, :].expand(50, 96)  # stride-0 rows
+    got = ops.gather_attn_fwd(q.to(DEV), k.to(DEV), v.to(DEV), idx.to(DEV))
+    torch.cuda.synchronize()
+    ref = OA.gather_attention(q.float(), k.float(), v.float(), idx.contiguous(), dtype=torch.float64)
+    _check_close(got.cpu(), ref, "gather shared list")
+
+
+@pytest.mark.parametrize("frames,P,topk", [(4, 1369, 4), (3, 100, 8), (2, 30, 16), (5, 64, 1)])
+def test_token_topk(ops, frames, P, topk):
+    g = torch.Generator().manual_seed(frames * P)
+    nq = 300
+    q = torch.randn(nq, 64, generator=g).to(torch.bfloat16)
+    k = torch.randn(frames * P, 64, generator=g).to(torch.bfloat16)
+    got = ops.token_topk(q.to(DEV), k.to(DEV), frames, P, topk).cpu()
+    torch.cuda.synchronize()
+    s = (q.double() @ k.double().T).float().numpy()  # exact products, fp32-rounded sums
+    ref = OS.frame_topk(s, frames, topk)
+    ke = min(topk, P)
+    assert got.shape == ref.shape
+    # identical except where the oracle's scores are within fp32 accumulation noise of a tie
+    gs = np.take_along_axis(s, got.numpy().astype(np.int64), axis=1)
+    rs = np.take_along_axis(s, ref.astype(np.int64), axis=1)
+    assert np.allclose(gs, rs, atol=1e-4, rtol=0), "selected scores differ beyond rounding noise"
+    same = (got.numpy() == ref).mean()
+    assert same > 0.99, f"only {same:.4f} of the indices agree"
+    for f in range(frames):  # frame-major: entries of frame f index frame f's keys
+        blk = got[:, f * ke:(f + 1) * ke]
+        assert ((blk // P) == f).all()

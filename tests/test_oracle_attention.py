@@ -1,0 +1,153 @@
+"""Pins the attention oracle: library SDPA, closed forms, invariances and a per-query brute force."""
+import math
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import attention as A
+
+
+def _qkv(n, d=64, seed=0, dtype=torch.float64):
+    g = torch.Generator().manual_seed(seed)
+    return [torch.randn(n, d, generator=g, dtype=dtype) for _ in range(3)]
+
+
+G = A.Geometry(frames=3, tokens_per_frame=5 + 150)  # 150 patches: blocks of 64, 64, 22
+
+
+def test_dense_is_library_sdpa():
+    q, k, v = _qkv(G.tokens)
+    got = A.pattern_attention(q, k, v, A.DENSE, G)
+    exp = F.scaled_dot_product_attention(q[None, None], k[None, None], v[None, None])[0, 0]
+    torch.testing.assert_close(got, exp, rtol=1e-10, atol=1e-10)
+
+
+def test_frame_local_is_per_frame_sdpa_and_ignores_other_frames():
+    q, k, v = _qkv(G.tokens, seed=1)
+    got = A.pattern_attention(q, k, v, A.FRAME_LOCAL, G)
+    T = G.tokens_per_frame
+    for f in range(G.frames):
+        s = slice(f * T, (f + 1) * T)
+        exp = F.scaled_dot_product_attention(q[s][None], k[s][None], v[s][None])[0]
+        torch.testing.assert_close(got[s], exp, rtol=1e-10, atol=1e-10)
+    k2, v2 = k.clone(), v.clone()
+    k2[T:2 * T] = torch.randn(T, 64, dtype=k.dtype)
+    v2[T:2 * T] = torch.randn(T, 64, dtype=k.dtype)
+    got2 = A.pattern_attention(q, k2, v2, A.FRAME_LOCAL, G)
+    torch.testing.assert_close(got2[2 * T:], got[2 * T:])
+
+
+def test_anchor_local_frame0_queries_equal_frame_local():
+    q, k, v = _qkv(G.tokens, seed=2)
+    T = G.tokens_per_frame
+    al = A.pattern_attention(q, k, v, A.ANCHOR_LOCAL, G)
+    fl = A.pattern_attention(q, k, v, A.FRAME_LOCAL, G)
+    torch.testing.assert_close(al[:T], fl[:T])
+    # frame 2 queries: keys are frames {0, 2}
+    keys = torch.cat([torch.arange(0, T), torch.arange(2 * T, 3 * T)])
+    exp = F.scaled_dot_product_attention(q[2 * T:][None], k[keys][None], v[keys][None])[0]
+    torch.testing.assert_close(al[2 * T:], exp, rtol=1e-10, atol=1e-10)
+
+
+@pytest.mark.parametrize("pattern", [A.DENSE, A.FRAME_LOCAL, A.ANCHOR_LOCAL, A.ANCHOR, A.BLOCK_DYNAMIC])
+def test_equal_keys_give_mean_of_allowed_values(pattern):
+    q, _, v = _qkv(G.tokens, seed=3)
+    k = torch.ones(G.tokens, 64, dtype=torch.float64)
+    nb = G.frames * G.blocks_per_frame
+    sel = torch.tensor([[(i + 1) % nb, (i + 4) % nb] for i in range(nb)], dtype=torch.int32)
+    got = A.pattern_attention(q, k, v, pattern, G, sel)
+    rows = torch.arange(G.tokens)
+    m = A.allowed_mask(pattern, rows, G, sel).double()
+    exp = (m @ v) / m.sum(1, keepdim=True)
+    torch.testing.assert_close(got, exp, rtol=1e-10, atol=1e-10)
+
+
+def test_block_dynamic_full_selection_is_patch_only_attention():
+    q, k, v = _qkv(G.tokens, seed=4)
+    nb = G.frames * G.blocks_per_frame
+    sel = torch.arange(nb, dtype=torch.int32).repeat(nb, 1)  # every block selected
+    got = A.pattern_attention(q, k, v, A.BLOCK_DYNAMIC, G, sel)
+    _, special, _ = A.token_info(G)
+    patch = (~special).nonzero().flatten()
+    exp_patch = F.scaled_dot_product_attention(q[patch][None], k[patch][None], v[patch][None])[0]
+    torch.testing.assert_close(got[patch], exp_patch, rtol=1e-10, atol=1e-10)
+    dense = A.pattern_attention(q, k, v, A.DENSE, G)
+    torch.testing.assert_close(got[special], dense[special])
+
+
+@pytest.mark.parametrize("pattern", [A.DENSE, A.FRAME_LOCAL, A.ANCHOR_LOCAL, A.ANCHOR, A.BLOCK_DYNAMIC])
+def test_gathered_equals_masked(pattern):
+    q, k, v = _qkv(G.tokens, seed=5)
+    nb = G.frames * G.blocks_per_frame
+    g = torch.Generator().manual_seed(9)
+    sel = torch.stack([torch.randperm(nb, generator=g)[:4] for _ in range(nb)]).int()
+    sel[0, 1] = -1
+    got = A.sparse_attention_gathered(q, k, v, pattern, G, sel, dtype=torch.float64)
+    exp = A.pattern_attention(q, k, v, pattern, G, sel)
+    torch.testing.assert_close(got, exp, rtol=1e-9, atol=1e-9)
+
+
+def test_gather_attention_brute_force():
+    q, k, v = _qkv(40, d=16, seed=6)
+    g = torch.Generator().manual_seed(1)
+    idx = torch.randint(0, 40, (40, 7), generator=g)
+    idx[3, 2] = -1
+    got = A.gather_attention(q, k, v, idx, dtype=torch.float64)
+    for i in range(40):
+        ids = [j for j in idx[i].tolist() if j >= 0]
+        s = [float(q[i] @ k[j]) / 4.0 for j in ids]
+        m = max(s)
+        w = [math.exp(x - m) for x in s]
+        tot = sum(w)
+        exp = sum((wi / tot) * v[j] for wi, j in zip(w, ids))
+        torch.testing.assert_close(got[i], exp, rtol=1e-9, atol=1e-9)
+
+
+def test_token_dynamic_rows():
+    q, k, v = _qkv(G.tokens, seed=7)
+    nimg = G.frames * G.patches
+    g = torch.Generator().manual_seed(2)
+    est = torch.randint(0, nimg, (nimg, 6), generator=g).int()
+    got = A.token_dynamic_attention(q, k, v, est, G)
+    _, special, _ = A.token_info(G)
+    dense = A.pattern_attention(q, k, v, A.DENSE, G)
+    torch.testing.assert_close(got[special], dense[special])
+    # image rows never see special keys: changing special keys/values leaves them unchanged
+    k2, v2 = k.clone(), v.clone()
+    k2[special] += 5.0
+    v2[special] -= 3.0
+    got2 = A.token_dynamic_attention(q, k2, v2, est, G)
+    torch.testing.assert_close(got2[~special], got[~special])
+    # stride-s special rows attend keys 0, s, 2s, ...
+    gs = A.token_dynamic_attention(q, k, v, est, G, sp2sp_stride=3)
+    keys = torch.arange(0, G.tokens, 3)
+    exp = F.scaled_dot_product_attention(q[special][None], k[keys][None], v[keys][None])[0]
+    torch.testing.assert_close(gs[special], exp, rtol=1e-10, atol=1e-10)
+
+
+def test_rope2d_closed_form():
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(2, 30, 64, generator=g)
+    pos = torch.randint(0, 38, (30, 2), generator=g)
+    pos[0] = 0
+    y = A.rope2d(x, pos)
+    torch.testing.assert_close(y[:, 0], x[:, 0])  # position (0, 0) is the identity
+    # complex-number form: pairs (i, i+16) of each 32-wide half rotate by pos * base^(-2i/32)
+    inv = 1.0 / (100.0 ** (torch.arange(0, 32, 2, dtype=torch.float64) / 32))
+    for half, axis in ((0, 0), (1, 1)):
+        xs = x[..., half * 32:(half + 1) * 32].double()
+        z = torch.complex(xs[..., :16], xs[..., 16:])
+        rot = z * torch.exp(1j * pos[:, axis, None].double() * inv)
+        exp = torch.cat([rot.real, rot.imag], dim=-1)
+        torch.testing.assert_close(y[..., half * 32:(half + 1) * 32].double(), exp, rtol=0, atol=2e-5)
+    # norm preserving per rotated pair
+    torch.testing.assert_close(y.norm(dim=-1), x.norm(dim=-1), rtol=1e-5, atol=1e-5)
+
+
+def test_vggt_positions_layout():
+    pos = A.vggt_positions(2, 3, 4)
+    assert pos.shape == (2 * 17, 2)
+    assert pos[:5].abs().sum() == 0
+    assert pos[5].tolist() == [1, 1] and pos[16].tolist() == [3, 4]
+    assert torch.equal(pos[17:], pos[:17])
