@@ -1,0 +1,252 @@
+"""Benchmark of the patched VGGT global-attention layer on one MI355X.
+
+Workload (one step): all 24 global-attention layers of VGGT-1B (dim 1024, 16 heads, d 64, RoPE-2D,
+QK-LayerNorm) over 128 frames x 1374 tokens = 175,872 tokens, random-init bf16 weights (seed 0),
+N(0,1) input tokens (seed 0); every layer gets its own seeded head table (7 block-top-4 /
+4 frame-local / 3 anchor+local / 2 dense, seed 1 + layer), block 64, top-k 4 per frame. Each layer
+runs the plugin's HeadwiseSparseAttentionWrapper: qkv Linear -> LayerNorm + RoPE packing -> block
+pooling + selection -> single-launch sparse attention -> proj Linear. All inputs are resident in
+HBM before timing.
+
+Prints one JSON line: value = effective TFLOP/s of the layer (algorithmic attention FLOP +
+projection FLOP per layer / measured time per layer), plus ms per layer, tokens/s, the live
+roofline of the sparse attention kernel (algorithmic FLOP per launch / its average duration from
+stream events) and a CPU baseline (the oracle's masked fp32 path on the 4-frame shape).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+import __graft_entry__  # noqa: E402
+
+PEAK_BF16_TFLOPS = 2516.6   # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+
+
+class EventRecorder:
+    """Brackets each kernel launch with events recorded on the current (launching) stream."""
+
+    def __init__(self):
+        self.enabled = False
+        self.pending = {}
+        self.pairs = {}
+
+    def __call__(self, name, phase):
+        if not self.enabled:
+            return
+        ev = torch.cuda.Event(enable_timing=True)
+        ev.record()
+        if phase == "start":
+            self.pending[name] = ev
+        else:
+            self.pairs.setdefault(name, []).append((self.pending.pop(name), ev))
+
+    def durations_ms(self):
+        torch.cuda.synchronize()
+        return {k: [a.elapsed_time(b) for a, b in v] for k, v in self.pairs.items()}
+
+
+def layer_config(layers, heads, seed_base, synth, ops):
+    names = {ops.BLOCK_DYNAMIC: "block_topk", ops.FRAME_LOCAL: "frame_local", ops.ANCHOR_LOCAL: "anchor_local",
+             ops.DENSE: "dense"}
+    cfg, tables = {}, []
+    for li in range(layers):
+        table = synth.seeded_patterns(heads, seed=seed_base + li)
+        tables.append(table)
+        groups = {}
+        for h, p in enumerate(table):
+            groups.setdefault(names[p], []).append(h)
+        cfg[str(li)] = [{"mode": m, "head_ids": ids} for m, ids in groups.items()]
+    return cfg, tables
+
+
+def cpu_baseline(pkg, frames=4, heads=16, repeats=5, budget_s=25.0):
+    """The oracle's masked fp32 attention path on the 4-frame VGGT shape, timed on host cores."""
+    import importlib
+
+    import numpy as np
+    from oracle import attention as OA
+    from oracle import selection as OS
+    synth = importlib.import_module(pkg.__name__ + ".synth")
+    acc = importlib.import_module(pkg.__name__ + ".accounting")
+    ops = importlib.import_module(pkg.__name__ + ".ops")
+    wl = synth.structured_qkv(frames=frames, heads=heads, seed=0)
+    q, k, v = (t.to(torch.bfloat16).float() for t in (wl.q, wl.k, wl.v))
+    patterns = synth.round_robin_patterns(heads)
+    g = wl.geom
+    og = OA.Geometry(g.frames, g.tokens_per_frame, g.num_special)
+
+    def run():
+        sel = {}
+        for h, p in enumerate(patterns):
+            if p == ops.BLOCK_DYNAMIC:
+                sel[h] = torch.from_numpy(OS.block_select(OS.bf16_bits(q[h].numpy()), OS.bf16_bits(k[h].numpy()),
+                                                          g.frames, g.tokens_per_frame, g.num_special, 4))
+        outs = [OA.pattern_attention(q[h], k[h], v[h], p, og, sel.get(h), dtype=torch.float32)
+                for h, p in enumerate(patterns)]
+        return sel, outs
+
+    t0 = time.perf_counter()
+    sel, _ = run()  # warm-up
+    first = time.perf_counter() - t0
+    n = max(1, min(repeats, int(budget_s / max(first, 1e-3))))
+    times = []
+    for _ in range(n):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    dyn = [h for h, p in enumerate(patterns) if p == ops.BLOCK_DYNAMIC]
+    sel_t = torch.stack([sel[h] for h in dyn]) if dyn else None
+    flops = acc.attention_flops(patterns, g, sel_t)
+    return {
+        "value": round(flops / med / 1e12, 6),
+        "unit": "TFLOP/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"{frames} frames x {g.tokens_per_frame} tokens ({g.tokens}), {heads} heads round-robin "
+                   "dense/frame-local/anchor+local/block-top4, oracle masked fp32 attention incl. block selection, "
+                   f"no projections; median of {n} runs, {med * 1e3:.0f} ms/layer"),
+        "ms_per_layer": round(med * 1e3, 2),
+        "algorithmic_flop": flops,
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--frames", type=int, default=128)
+    ap.add_argument("--layers", type=int, default=24)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU: --gpus {args.gpus} is not supported (the path is measured on one "
+              "MI355X; multi-GPU sharding is design-only)", file=sys.stderr)
+        sys.exit(2)
+
+    import importlib
+    pkg = __graft_entry__.package()
+    ops = importlib.import_module(pkg.__name__ + ".ops")
+    synth = importlib.import_module(pkg.__name__ + ".synth")
+    vggt = importlib.import_module(pkg.__name__ + ".vggt")
+    plug = importlib.import_module(pkg.__name__ + ".patch")
+    acc = importlib.import_module(pkg.__name__ + ".accounting")
+
+    dev = torch.device("cuda:0")
+    dim, heads, ph, pw = 1024, 16, 37, 37
+    torch.manual_seed(0)
+    model = vggt.GlobalAttentionStack(depth=args.layers, dim=dim, num_heads=heads)
+    model = model.to(dev).to(torch.bfloat16).eval()
+    cfg, tables = layer_config(args.layers, heads, 1, synth, ops)
+    plug.patch_model(model, "vggt", {"patch_module": {"type": "headsparse", "topk_mode": "token", "block_topk": 4,
+                                                      "topk_scope": "frame"}, "sparse_config": cfg})
+    plug.update_args_per_forward(model, "vggt", ph * 14, pw * 14)
+    T = ph * pw + 5
+    N = args.frames * T
+    geom = pkg.Geometry(args.frames, T, 5)
+    g = torch.Generator(device=dev).manual_seed(0)
+    x = torch.randn(1, N, dim, generator=g, device=dev).to(torch.bfloat16)
+    pos = synth.vggt_positions(args.frames, ph, pw, device=dev)[None]
+    layers = [b.attn for b in model.aggregator.global_blocks]
+
+    def step():
+        for layer in layers:
+            layer(x, pos)
+
+    rec = EventRecorder()
+    ops.set_event_recorder(rec)
+    with torch.no_grad():
+        for _ in range(args.warmup):
+            step()
+        torch.cuda.synchronize()
+        rec.enabled = True
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            step()
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        rec.enabled = False
+    ops.set_event_recorder(None)
+    ms_step = (t1 - t0) * 1e3 / args.steps
+    ms_layer = ms_step / args.layers
+    dur = rec.durations_ms()
+
+    # algorithmic work of every layer (selection lists of the last step)
+    attn_flops = [acc.attention_flops(tables[i], geom, layers[i].last_selection) for i in range(args.layers)]
+    proj = acc.projection_flops(N, dim)
+    layer_flops = sum(attn_flops) / args.layers + proj
+    attn_ms = dur.get("sparse_attn", [])
+    attn_ms_avg = statistics.fmean(attn_ms) if attn_ms else float("nan")
+    attn_tflops = (sum(attn_flops) * args.steps) / (sum(attn_ms) * 1e-3) / 1e12 if attn_ms else None
+    n_dyn = sum(1 for p in tables[0] if p == ops.BLOCK_DYNAMIC)
+    width = args.frames * min(4, geom.blocks_per_frame)
+    sb = acc.selection_bytes(geom, n_dyn, width)
+    pool_ms = dur.get("block_pool", [])
+    sel_ms = dur.get("block_select", [])
+    sel_extra = {}
+    if pool_ms and sel_ms:
+        sel_extra = {
+            "pool_ms": round(statistics.fmean(pool_ms), 4),
+            "select_ms": round(statistics.fmean(sel_ms), 4),
+            "pool_GBs": round(sb["pool"] / (statistics.fmean(pool_ms) * 1e-3) / 1e9, 1),
+            "select_GBs": round(sb["select"] / (statistics.fmean(sel_ms) * 1e-3) / 1e9, 1),
+            "fused_path_GBs": round(sb["fused_path"] / ((statistics.fmean(pool_ms) + statistics.fmean(sel_ms)) * 1e-3) / 1e9, 1),
+            "heads": n_dyn,
+        }
+    result = {
+        "metric": "ms per global-attn layer + effective TFLOP/s, VGGT shape 128 frames bf16",
+        "value": round(layer_flops / (ms_layer * 1e-3) / 1e12, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 3),
+        "ms_per_layer": round(ms_layer, 3),
+        "tokens_per_s": round(N / (ms_layer * 1e-3), 1),
+        "attn_ms_per_layer": round(attn_ms_avg, 3),
+        "attn_tflops": None if attn_tflops is None else round(attn_tflops, 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: N(0,1) tokens and random-init bf16 weights (seed 0), seeded head tables",
+        "config": {
+            "workload": (f"VGGT-1B global attention: {args.layers} layers x {args.frames} frames x {T} tokens "
+                         f"({N}), 16 heads, d 64, dim 1024, RoPE-2D + QK-LayerNorm, head mix 7 block-top4 / "
+                         "4 frame-local / 3 anchor+local / 2 dense per layer (seed 1+layer), block 64"),
+            "frames": args.frames, "tokens": N, "layers": args.layers, "heads": heads, "block": 64, "topk": 4,
+            "parallelism": "single GPU",
+        },
+        "flop_per_layer": {"attention": round(sum(attn_flops) / args.layers), "projection": proj},
+        "roofline": {
+            "bound": "mfma",
+            "kernel": "sparse_attn_kernel",
+            "achieved": None if attn_tflops is None else round(attn_tflops, 2),
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": None if attn_tflops is None else round(attn_tflops / PEAK_BF16_TFLOPS, 4),
+            "traffic": None,
+            "launch_ms": round(attn_ms_avg, 3),
+        },
+        "selection": dict(sel_extra, bound="hbm", peak=PEAK_HBM_GBS, unit="GB/s"),
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(pkg)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

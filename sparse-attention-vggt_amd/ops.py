@@ -22,6 +22,22 @@ PATTERN_NAMES = {
 }
 
 
+_recorder = None
+
+
+def set_event_recorder(recorder) -> None:
+    """Install (or clear with None) a callable ``recorder(name, phase)`` invoked right before
+    (phase "start") and after (phase "end") each launch of the attention and selection kernels,
+    on the launching thread; used by the benchmark to bracket kernels with stream events."""
+    global _recorder
+    _recorder = recorder
+
+
+def _mark(name, phase):
+    if _recorder is not None:
+        _recorder(name, phase)
+
+
 def _ptr(t: torch.Tensor | None):
     return ctypes.c_void_p(0 if t is None else t.data_ptr())
 
@@ -105,8 +121,11 @@ def block_pool(qp: torch.Tensor, kp: torch.Tensor | None, geom: Geometry, heads:
     n = len(heads)
     pq = torch.empty(n, geom.num_blocks, HEAD_DIM, dtype=torch.float32, device=qp.device)
     pk = torch.empty_like(pq) if kp is not None else None
+    hs = _i32_array(heads)
+    _mark("block_pool", "start")
     _lib.check(lib.saf3r_block_pool(_ptr(qp), _ptr(kp), geom.frames, geom.tokens_per_frame, geom.num_special, H,
-                                    _i32_array(heads), n, _ptr(pq), _ptr(pk), _lib.stream_ptr()))
+                                    hs, n, _ptr(pq), _ptr(pk), _lib.stream_ptr()))
+    _mark("block_pool", "end")
     return pq, pk
 
 
@@ -139,9 +158,11 @@ def block_select(pooled_q: torch.Tensor, pooled_k: torch.Tensor, frames: int, bl
     else:
         raise ValueError(f"unknown topk scope {scope!r}")
     idx = torch.empty(n, nbq, width, dtype=torch.int32, device=pooled_q.device)
-    _lib.check(lib.saf3r_block_select(_ptr(pooled_q.contiguous()), _ptr(pooled_k.contiguous()), n, nbq, frames,
-                                      blocks_per_frame, k, 0 if scope == "frame" else 1, _ptr(idx),
-                                      _lib.stream_ptr()))
+    pq, pk = pooled_q.contiguous(), pooled_k.contiguous()
+    _mark("block_select", "start")
+    _lib.check(lib.saf3r_block_select(_ptr(pq), _ptr(pk), n, nbq, frames, blocks_per_frame, k,
+                                      0 if scope == "frame" else 1, _ptr(idx), _lib.stream_ptr()))
+    _mark("block_select", "end")
     return idx
 
 
@@ -171,9 +192,12 @@ def sparse_attn_fwd(qp, kp, vp, geom: Geometry, patterns: Sequence[int], sel: to
         width = sel.shape[-1]
     else:
         sel = None
+    pat = _i32_array(patterns)
+    _mark("sparse_attn", "start")
     _lib.check(lib.saf3r_sparse_attn_fwd(
         _ptr(qp), _ptr(kp), _ptr(vp), geom.frames, geom.tokens_per_frame, geom.num_special, H,
-        _i32_array(patterns), _ptr(sel), width, float(scale), _ptr(out), out.stride(0), _lib.stream_ptr()))
+        pat, _ptr(sel), width, float(scale), _ptr(out), out.stride(0), _lib.stream_ptr()))
+    _mark("sparse_attn", "end")
     return out
 
 

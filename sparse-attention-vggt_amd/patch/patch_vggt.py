@@ -1,0 +1,110 @@
+"""VGGT plugin: ``headsparse`` patching of the global attention layers.
+
+ref: saf3r/patch/patch_vggt.py:178-222 (headsparse branch: read the sparse-config JSON, require
+     topk_mode == "token" when a dino_topk head exists, choose lazy / precomputed top-k, replace
+     ``aggregator.global_blocks.{i}.attn``), :274-310 (update_args_per_forward: patch grid from
+     the image size, reset of the lazy flag), :571-590 (HeadwiseSparseAttentionWrapper.forward).
+
+Configuration (plain dict or attribute object, as the reference's addict ``model_cfg``):
+    sparse_config_path | sparse_config     JSON path or the parsed {layer: [group, ...]} mapping
+    patch_module.type                      "headsparse"
+    patch_module.topk_mode                 "token" (required when a dino_topk head exists)
+    patch_module.lazy_dino_topk            indices from the first correspondence head (True), or
+                                           supplied through ``wrapper.est_topk_idx`` (False)
+    patch_module.topk                      per-frame token top-k of dino_topk heads
+    patch_module.block_topk                per-frame block top-k of block_topk heads (default 4)
+    patch_module.topk_scope                "frame" (default) or "global" for block_topk heads
+The lazy indices are shared through one ``SelectionState`` per model instead of rebinding the
+aggregator forward: every dino_topk layer after the one holding the first correspondence head
+reads them, exactly the layers the reference copies them to.
+"""
+from __future__ import annotations
+
+import json
+
+import torch
+from torch import Tensor
+
+from ..layout import HEAD_DIM
+from .wrapper import BaseHeadwiseSparseAttentionWrapper, SelectionState, _get
+
+NUM_SPECIAL_TOKENS = 5
+NUM_GLOBAL_BLOCKS = 24
+NUM_ATTENTION_HEADS = 16
+PATCH_SIZE = 14
+
+
+def _load_config(model_cfg):
+    cfg = _get(model_cfg, "sparse_config")
+    if cfg is None:
+        path = _get(model_cfg, "sparse_config_path")
+        if path is None:
+            raise ValueError("headsparse patching needs sparse_config_path (or sparse_config)")
+        with open(path, "r") as f:
+            cfg = json.load(f)
+    return cfg
+
+
+def patch_model(model, model_cfg):
+    pm = _get(model_cfg, "patch_module")
+    ptype = _get(pm, "type")
+    if ptype != "headsparse":
+        raise NotImplementedError(f"patch_module.type={ptype!r}: only 'headsparse' is built")
+    config = _load_config(model_cfg)
+    has_dino = any(g["mode"] == "dino_topk" for groups in config.values() for g in groups)
+    lazy = bool(_get(pm, "lazy_dino_topk", False))
+    if has_dino and _get(pm, "topk_mode", "token") != "token":
+        raise AssertionError("dino_topk heads need patch_module.topk_mode == 'token'")
+    state = SelectionState()
+    blocks = model.aggregator.global_blocks
+    for layer_key, layer_config in config.items():
+        i = int(layer_key)
+        if i >= len(blocks):
+            raise ValueError(f"Failed to get module aggregator.global_blocks.{i}.attn from the model.")
+        orig = blocks[i].attn
+        blocks[i].attn = HeadwiseSparseAttentionWrapper(
+            orig, layer_idx=i, dino_topk=_get(pm, "topk", 4), lazy_dino_topk=lazy, config=layer_config,
+            block_topk=_get(pm, "block_topk", 4), topk_scope=_get(pm, "topk_scope", "frame"), shared=state)
+    model.saf3r_selection_state = state
+    return model
+
+
+def update_args_per_forward(model, img_h, img_w):
+    patch_height = img_h // PATCH_SIZE
+    patch_width = img_w // PATCH_SIZE
+    state = getattr(model, "saf3r_selection_state", None)
+    if state is not None:
+        state.reset()
+    for block in model.aggregator.global_blocks:
+        attn = block.attn
+        if not isinstance(attn, BaseHeadwiseSparseAttentionWrapper):
+            continue
+        attn.patch_height = patch_height
+        attn.patch_width = patch_width
+        attn.first_dino_flag = False
+
+
+class HeadwiseSparseAttentionWrapper(BaseHeadwiseSparseAttentionWrapper):
+    def __init__(self, orig_module, **kwargs):
+        super().__init__(orig_module, NUM_SPECIAL_TOKENS, orig_module.num_heads, **kwargs)
+        if orig_module.head_dim != HEAD_DIM:
+            raise NotImplementedError(f"head_dim {orig_module.head_dim}: the kernels are built for 64")
+
+    def forward(self, x: Tensor, pos=None) -> Tensor:
+        B, N, C = x.shape
+        if B != 1:
+            raise AssertionError("Currently only support batch size of 1 for simplicity")
+        if not x.is_cuda:
+            raise RuntimeError("HeadwiseSparseAttentionWrapper runs on the GPU kernels only")
+        om = self.orig_module
+        geom = self.geometry(N)
+        qkv = om.qkv(x).reshape(N, 3 * C)
+        if qkv.dtype != torch.bfloat16:
+            qkv = qkv.to(torch.bfloat16)
+        qkv = qkv.contiguous()
+        out = self.compute_multihead_attention_packed(qkv, None if pos is None else pos[0], geom)
+        y = out.reshape(B, N, C)
+        if not torch.is_autocast_enabled("cuda") and y.dtype != om.proj.weight.dtype:
+            y = y.to(om.proj.weight.dtype)
+        y = om.proj(y)
+        return om.proj_drop(y)

@@ -1,0 +1,155 @@
+"""Head-wise sparse attention wrapper: head-config parsing and the accelerated layer forward.
+
+ref: saf3r/patch/wrapper.py:8-106 (BaseHeadwiseSparseAttentionWrapper: head_cfg from groups with
+     "full" as default and a ValueError for a head listed twice; lazy first-correspondence-head
+     top-k; per-head loop), saf3r/patch/patch_vggt.py:494-510 (the lazy indices are shared with
+     every later layer), :575-590 (qkv -> q/k norm -> RoPE -> attention -> proj).
+
+One forward of a layer on the GPU:
+  qkv Linear (torch) -> saf3r_pack_qkv (LayerNorm + RoPE + packing) -> [block-dynamic heads:
+  saf3r_block_pool + saf3r_block_select] -> [lazy dino_topk: saf3r_token_topk once per forward]
+  -> saf3r_sparse_attn_fwd (all heads, one launch) -> [dino_topk image rows: saf3r_gather_attn_fwd]
+  -> proj Linear (torch).
+Instead of a Python loop over heads, every head runs in the single attention launch.
+"""
+from __future__ import annotations
+
+import torch
+from torch import nn
+
+from .. import ops
+from ..layout import HEAD_DIM, Geometry
+from .sparse_attention import pattern_of
+
+
+class SelectionState:
+    """Per-model store of the lazily computed token top-k (``est_topk_idx``), shared by every
+    dino_topk head; reset by ``update_args_per_forward``."""
+
+    def __init__(self):
+        self.reset()
+
+    def reset(self):
+        self.est_topk_idx = None
+        self.source_layer = None
+
+
+def _get(cfg, key, default=None):
+    if cfg is None:
+        return default
+    if isinstance(cfg, dict):
+        return cfg.get(key, default)
+    return getattr(cfg, key, default)
+
+
+class BaseHeadwiseSparseAttentionWrapper(nn.Module):
+    def __init__(self, orig_module, num_special_tokens, num_heads, **kwargs):
+        super().__init__()
+        self.orig_module = orig_module
+        self.num_special_tokens = num_special_tokens
+        self.num_heads = num_heads
+        self.layer_idx = kwargs.get("layer_idx", None)
+        self.patch_width = kwargs.get("patch_width", None)
+        self.patch_height = kwargs.get("patch_height", None)
+        self.est_topk_idx = torch.empty(0)
+        self.lazy_dino_topk = bool(kwargs.get("lazy_dino_topk", False))
+        self.dino_topk = int(kwargs.get("dino_topk", 4))
+        self.first_dino_flag = False
+        self.block_topk = int(kwargs.get("block_topk", 4))
+        self.topk_scope = kwargs.get("topk_scope", "frame")
+        self.shared = kwargs.get("shared", None) or SelectionState()
+        self.last_selection = None
+
+        cfg = kwargs.get("config", [])
+        self.head_cfg = [{"mode": "full"} for _ in range(num_heads)]
+        seen = set()
+        for group in cfg:
+            group = dict(group)
+            ids = group.pop("head_ids")
+            for h in ids:
+                if h in seen:
+                    raise ValueError(f"Head {h} assigned to multiple patterns!")
+                seen.add(h)
+                self.head_cfg[h].update(group)
+        self.patterns = [pattern_of(c) for c in self.head_cfg]
+        for h, c in enumerate(self.head_cfg):
+            if self.patterns[h] == ops.TOKEN_DYNAMIC and c.get("dino_sp2sp_stride", 1) != 1:
+                raise NotImplementedError("dino_topk with dino_sp2sp_stride != 1 has no kernel in this build")
+        ks = {int(c.get("topk", self.block_topk)) for c, p in zip(self.head_cfg, self.patterns)
+              if p == ops.BLOCK_DYNAMIC}
+        if len(ks) > 1:
+            raise ValueError(f"block_topk heads of one layer must share one k, got {sorted(ks)}")
+        self.layer_block_topk = ks.pop() if ks else self.block_topk
+        self.dyn_heads = [h for h, p in enumerate(self.patterns) if p == ops.BLOCK_DYNAMIC]
+        self.dino_heads = [h for h, p in enumerate(self.patterns) if p == ops.TOKEN_DYNAMIC]
+        self.first_dino_head = next((h for h in self.dino_heads if self.head_cfg[h].get("is_first_dino", False)), None)
+
+    # ------------------------------------------------------------------------------------
+    def geometry(self, num_tokens: int) -> Geometry:
+        if self.patch_height is None or self.patch_width is None:
+            raise RuntimeError("patch size unknown: call update_args_per_forward before the forward pass")
+        T = self.patch_height * self.patch_width + self.num_special_tokens
+        return Geometry.from_tokens(num_tokens, T, self.num_special_tokens)
+
+    def compute_multihead_attention_packed(self, qkv: torch.Tensor, pos, geom: Geometry) -> torch.Tensor:
+        """qkv: bf16 [N, 3*H*64] (the qkv Linear output). Returns bf16 [N, H*64]."""
+        om = self.orig_module
+        H = self.num_heads
+        C = H * HEAD_DIM
+        ln_q = ln_k = None
+        eps = 1e-5
+        if isinstance(om.q_norm, nn.LayerNorm):
+            ln_q = (om.q_norm.weight, om.q_norm.bias)
+            ln_k = (om.k_norm.weight, om.k_norm.bias)
+            eps = om.q_norm.eps
+        elif not isinstance(om.q_norm, nn.Identity):
+            raise NotImplementedError(f"q_norm {type(om.q_norm).__name__} is not LayerNorm / Identity")
+        inv_freq = p2 = None
+        if om.rope is not None and pos is not None:
+            inv_freq = ops.rope_inv_freq(float(om.rope.base_frequency))
+            p2 = pos.reshape(-1, 2)
+        qp, kp, vp = ops.pack_qkv(qkv, qkv[:, C:], qkv[:, 2 * C:], 3 * C, HEAD_DIM, geom, H, ln_q=ln_q, ln_k=ln_k,
+                                  ln_eps=eps, pos=p2, inv_freq=inv_freq)
+        sel = None
+        if self.dyn_heads:
+            pq, pk = ops.block_pool(qp, kp, geom, self.dyn_heads)
+            sel = ops.block_select(pq, pk, geom.frames, geom.blocks_per_frame, self.layer_block_topk, self.topk_scope)
+        self.last_selection = sel  # block lists of the block_topk heads, in head order
+        if self.dino_heads:
+            self._lazy_token_topk(qp, kp, geom)
+        out = ops.sparse_attn_fwd(qp, kp, vp, geom, self.patterns, sel)
+        if self.dino_heads:
+            est = self.est_topk_idx
+            P, W = geom.patches, est.shape[1]
+            for h in self.dino_heads:
+                qr = ops.rows(qp[h], 64, geom.special_slots, P, geom.padded_patches)
+                kr = ops.rows(kp[h], 64, geom.special_slots, P, geom.padded_patches)
+                vr = ops.rows(qkv, 3 * C, geom.num_special, P, geom.tokens_per_frame, offset=2 * C + h * HEAD_DIM)
+                orr = ops.rows(out, C, geom.num_special, P, geom.tokens_per_frame, offset=h * HEAD_DIM)
+                ops.gather_attn_rows(qr, kr, vr, est, W, geom.frames * P, W, geom.frames * P, None, orr)
+        return out
+
+    def _lazy_token_topk(self, qp, kp, geom: Geometry):
+        """Lazy per-frame token top-k from the first correspondence head (``wrapper.py:42-86``)."""
+        if self.lazy_dino_topk and self.first_dino_head is not None and not self.first_dino_flag:
+            self.first_dino_flag = True
+            h = self.first_dino_head
+            P = geom.patches
+            r = ops.rows(qp[h], 64, geom.special_slots, P, geom.padded_patches)
+            kr = ops.rows(kp[h], 64, geom.special_slots, P, geom.padded_patches)
+            idx = ops.token_topk(qp, kp, geom.frames, P, self.dino_topk, qrows=r, krows=kr, n_q=geom.frames * P)
+            self.est_topk_idx = idx
+            self.shared.est_topk_idx = idx
+            self.shared.source_layer = self.layer_idx
+        elif self.shared.est_topk_idx is not None:
+            self.est_topk_idx = self.shared.est_topk_idx
+        if self.est_topk_idx is None or self.est_topk_idx.numel() == 0:
+            raise RuntimeError("dino_topk head has no top-k indices: no earlier correspondence head computed them "
+                               "and none were provided")
+        n_img = geom.frames * geom.patches
+        if self.est_topk_idx.shape[0] != n_img or not self.est_topk_idx.is_cuda:
+            raise RuntimeError(f"est_topk_idx must be a GPU tensor with {n_img} rows")
+        self.est_topk_idx = self.est_topk_idx.to(torch.int32).contiguous()
+
+    def forward(self, *args, **kwargs):
+        raise NotImplementedError("This is a base wrapper and should not be used directly.")

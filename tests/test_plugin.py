@@ -1,0 +1,117 @@
+"""CPU checks of the plugin surface: config parsing, module replacement, per-forward geometry, and
+the error behaviour the reference defines (duplicate head, unknown mode, batch size, model name)."""
+import json
+import os
+from types import SimpleNamespace
+
+import pytest
+import torch
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+@pytest.fixture(scope="module")
+def plug(pkg):
+    import importlib
+    return importlib.import_module(pkg.__name__ + ".patch")
+
+
+@pytest.fixture(scope="module")
+def vggt(pkg):
+    import importlib
+    return importlib.import_module(pkg.__name__ + ".vggt")
+
+
+def _model(vggt, depth=3, dim=64, heads=4):
+    return vggt.GlobalAttentionStack(depth=depth, dim=dim, num_heads=heads)
+
+
+def test_head_cfg_defaults_and_groups(plug, vggt, pkg):
+    import importlib
+    ops = importlib.import_module(pkg.__name__ + ".ops")
+    m = _model(vggt, depth=2, dim=256, heads=4)
+    cfg = {"patch_module": {"type": "headsparse", "topk_mode": "token", "lazy_dino_topk": True, "topk": 4},
+           "sparse_config": {"0": [{"mode": "global_to_frame", "head_ids": [1]},
+                                   {"mode": "block_topk", "head_ids": [2, 3], "topk": 8}],
+                             "1": [{"mode": "all_to_first", "head_ids": [0]}]}}
+    group = cfg["sparse_config"]["0"][0]
+    plug.patch_model(m, "vggt", cfg)
+    w0 = m.aggregator.global_blocks[0].attn
+    assert isinstance(w0, plug.HeadwiseSparseAttentionWrapper)
+    assert [c["mode"] for c in w0.head_cfg] == ["full", "global_to_frame", "block_topk", "block_topk"]
+    assert w0.patterns == [ops.DENSE, ops.FRAME_LOCAL, ops.BLOCK_DYNAMIC, ops.BLOCK_DYNAMIC]
+    assert w0.layer_block_topk == 8 and w0.dyn_heads == [2, 3]
+    assert "head_ids" in group  # the caller's config is not mutated
+    w1 = m.aggregator.global_blocks[1].attn
+    assert w1.patterns == [ops.ANCHOR, ops.DENSE, ops.DENSE, ops.DENSE]
+    assert w1.shared is w0.shared is m.saf3r_selection_state
+
+
+def test_errors_follow_reference(plug, vggt):
+    m = _model(vggt)
+    dup = {"patch_module": {"type": "headsparse"},
+           "sparse_config": {"0": [{"mode": "skip", "head_ids": [1]}, {"mode": "all_to_first", "head_ids": [1]}]}}
+    with pytest.raises(ValueError, match="multiple"):
+        plug.patch_model(m, "vggt", dup)
+    bad = {"patch_module": {"type": "headsparse"}, "sparse_config": {"0": [{"mode": "bogus", "head_ids": [0]}]}}
+    with pytest.raises(ValueError, match="Unsupported mode"):
+        plug.patch_model(_model(vggt), "vggt", bad)
+    with pytest.raises(ValueError, match="Unsupported model"):
+        plug.patch_model(_model(vggt), "pi3x", bad)
+    with pytest.raises(NotImplementedError):
+        plug.patch_model(_model(vggt), "vggt", {"patch_module": {"type": "headprofile"}, "sparse_config": {}})
+    with pytest.raises(AssertionError):
+        plug.patch_model(_model(vggt), "vggt", {"patch_module": {"type": "headsparse", "topk_mode": "global"},
+                                               "sparse_config": {"0": [{"mode": "dino_topk", "head_ids": [0]}]}})
+
+
+def test_update_args_per_forward_sets_geometry(plug, vggt):
+    m = _model(vggt, depth=2, dim=256, heads=4)
+    cfg = {"patch_module": {"type": "headsparse", "lazy_dino_topk": True, "topk": 4},
+           "sparse_config": {"0": [{"mode": "dino_topk", "head_ids": [0], "is_first_dino": True}], "1": []}}
+    plug.patch_model(m, "vggt", cfg)
+    w = m.aggregator.global_blocks[0].attn
+    w.first_dino_flag = True
+    m.saf3r_selection_state.est_topk_idx = torch.zeros(1)
+    plug.update_args_per_forward(m, "vggt", 518, 518)
+    for b in m.aggregator.global_blocks:
+        assert b.attn.patch_height == b.attn.patch_width == 37
+        assert b.attn.first_dino_flag is False
+    assert m.saf3r_selection_state.est_topk_idx is None
+    g = w.geometry(4 * 1374)
+    assert (g.frames, g.tokens_per_frame, g.patches) == (4, 1374, 1369)
+    with pytest.raises(ValueError):
+        w.geometry(1000)
+
+
+def test_wrapper_refuses_cpu_and_batches(plug, vggt):
+    m = _model(vggt, depth=1, dim=256, heads=4)
+    plug.patch_model(m, "vggt", {"patch_module": {"type": "headsparse"}, "sparse_config": {"0": []}})
+    plug.update_args_per_forward(m, "vggt", 28, 28)
+    w = m.aggregator.global_blocks[0].attn
+    with pytest.raises(AssertionError):
+        w(torch.randn(2, 18, 256))
+    with pytest.raises(RuntimeError, match="GPU"):
+        w(torch.randn(1, 18, 256))
+
+
+def test_reference_vggt_profile_fixture(plug, vggt):
+    """The reference's VGGT head profile (24 layers x 16 heads, each head exactly once)."""
+    with open(os.path.join(GOLDEN, "vggt_eth3d_profile.json")) as f:
+        prof = json.load(f)
+    assert set(prof) == {str(i) for i in range(24)}
+    for groups in prof.values():
+        assert sorted(h for g in groups for h in g["head_ids"]) == list(range(16))
+    firsts = [(k, g["head_ids"]) for k, gs in prof.items() for g in gs if g.get("is_first_dino")]
+    assert firsts == [("11", [14])]
+    # layers whose modes all have kernels patch cleanly; stride / q_probe_topk are not built yet
+    m = _model(vggt, depth=24, dim=1024, heads=16)
+    ok = {k: v for k, v in prof.items() if all(g["mode"] in ("all_to_first", "global_to_frame", "dino_topk", "full")
+                                                 for g in v)}
+    assert ok, "expected some layers without stride heads"
+    plug.patch_model(m, "vggt", {"patch_module": {"type": "headsparse", "topk_mode": "token",
+                                                  "lazy_dino_topk": True, "topk": 4}, "sparse_config": ok})
+    with pytest.raises(NotImplementedError, match="stride"):
+        plug.patch_model(_model(vggt, depth=24, dim=1024, heads=16), "vggt",
+                         {"patch_module": {"type": "headsparse", "topk_mode": "token", "lazy_dino_topk": True,
+                                           "topk": 4}, "sparse_config": prof})
