@@ -8,18 +8,33 @@
 //      :189-231 (dino_topk: special rows dense, image rows over selected keys only),
 //      :234-253 (global_to_frame).
 //
-// Work decomposition: a workgroup of two waves owns one (head, 64-slot query tile); wave w owns
-// query rows 32w..32w+31. Key tiles (64 slots x 64 features, 8 KB for K and 8 KB for V) are
-// staged in LDS, double-buffered, and consumed with v_mfma_f32_32x32x16_bf16:
-//   S^T (64 keys x 32 queries) = K . Q^T   (A = K rows from LDS, B = Q kept in registers)
-//   O^T (64 d x 32 queries)   += V^T . P^T (A = transposed V tile from LDS, B = P in registers)
-// In the S^T accumulator a lane holds one query and 32 keys, so row max / row sum need a single
-// cross-half exchange (v_permlane32_swap). Work items are ordered by decreasing per-item cost.
+// MFMA core (every mode): a wave owns 64 query rows as two 32-query column groups and consumes
+// key tiles staged in LDS with v_mfma_f32_32x32x16_bf16:
+//   S^T (32 keys x 32 queries)  = K . Q^T    A = K rows from LDS, B = Q kept in registers
+//   O^T (64 d    x 32 queries) += V^T . P^T  A = transposed V tile from LDS, B = P in registers
+// In the S^T accumulator a lane holds one query and 16 keys of every 32, so row max / row sum
+// need one cross-half exchange (v_permlane32_swap). Softmax uses base-2 exponentials against a
+// lazily moved reference maximum (O / l are rescaled only when the row maximum grows by more than
+// 2^8) and row sums are dot2 products of the bf16 P values that feed the PV product.
+//
+// Shared mode (dense, frame-local, anchor+local, anchor, special rows of the dynamic patterns):
+// a workgroup of four waves owns up to four consecutive query tiles with one key sequence. Full
+// key tiles (8 KB K + 8 KB transposed V) stream through a 4-stage LDS ring filled by
+// global_load_lds_dwordx4 (no register staging) with one barrier per tile; all four waves consume
+// each staged tile.
+// Split mode (patch rows of block-dynamic heads): a workgroup owns one query tile; its four waves
+// split the tile's block list into quarters and each streams its own 32-key half tiles through a
+// private 2-slot LDS ring (no barriers). Half tiles beyond a partial block's population are never
+// loaded. The four partial (max, sum, O) are merged through LDS at the end.
 #include "common.h"
 
 namespace saf3r {
 
-constexpr int kMaxSel = 2048;
+constexpr int kRing = 65536;     // LDS arena shared by both modes
+constexpr int kStages = 4;       // shared mode: 4 x 16 KB
+constexpr int kMaxList = 3968;   // compacted block list of a split-mode tile
+
+enum ItemKind { kShared = 0, kSplit = 1, kSkip = 2 };
 
 struct AttnParams {
   const __bf16* q;
@@ -38,26 +53,160 @@ struct AttnParams {
   int8_t slot[kMaxHeads];
 };
 
-__device__ inline float permlane_partner_max(float x) {
+typedef __attribute__((address_space(3))) void lds_void;
+
+__device__ inline float partner_max(float x) {
   uint32_t u = __builtin_bit_cast(uint32_t, x);
   auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
   return fmaxf(__builtin_bit_cast(float, (uint32_t)r[0]), __builtin_bit_cast(float, (uint32_t)r[1]));
 }
-__device__ inline float permlane_partner_sum(float x) {
+__device__ inline float partner_sum(float x) {
   uint32_t u = __builtin_bit_cast(uint32_t, x);
   auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
   return __builtin_bit_cast(float, (uint32_t)r[0]) + __builtin_bit_cast(float, (uint32_t)r[1]);
 }
 
-// Key-tile sequence of one work item: up to four contiguous ranges, or a compacted list in LDS.
-// Fields are scalars (no indexed arrays) so the sequence stays in registers.
+// s_waitcnt on vmcnt only (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14]),
+// followed by a compiler barrier so no LDS read is hoisted above it.
+template <int N>
+__device__ inline void wait_vm() {
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+  asm volatile("" ::: "memory");
+}
+__device__ inline void barrier_only() {
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// XOR swizzles of the 16-byte chunk index. 128-byte rows (8 chunks): rows r and r ^ 8 get
+// different masks, so 16 lanes reading 16 consecutive rows at one logical chunk hit 16 distinct
+// 16-byte bank groups whether the LDS serves 8 lanes over 32 banks or 16 lanes over 64 banks.
+// 64-byte rows (4 chunks) use the analogous mask.
+__device__ inline int swz8(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+__device__ inline int swz4(int r) { return ((r >> 1) & 3) ^ ((r >> 3) & 1); }
+
+struct Acc {
+  f32x16 o[2][2];  // [dh][gq]: O^T rows 32*dh + (16*half + a), query 32*gq + col
+  float m[2];      // reference maximum (raw score units) per query group
+  float l[2];      // partial row sum over this lane's keys
+};
+
+struct TileMask {
+  bool need;     // some element of the tile is masked
+  bool kspecial; // key tile lies in the special region
+  int kt;        // key tile index
+  int kvalid;    // patch tile: valid keys from key 0 of the tile
+  int kframe;    // patch tile: frame of its keys
+  int eff;       // pattern whose frame relation applies (DENSE / BLOCK_DYNAMIC: none)
+};
+
+// One staged key tile (NKH = 2: 64 keys, K rows 128 B, V rows 128 B) or half tile (NKH = 1:
+// 32 keys, V rows 64 B); key0 is the first key of the staged keys within their 64-slot tile.
+template <int NKH>
+__device__ __forceinline__ void attend(const char* __restrict__ kst, const char* __restrict__ vst,
+                                       const bf16x8 (&qfrag)[2][4], Acc& A, const int (&frow)[2],
+                                       const TileMask& tm, const Geom& g, int key0, int half, int col, float c) {
+  f32x16 s[NKH][2];
+#pragma unroll
+  for (int kh = 0; kh < NKH; ++kh) s[kh][0] = s[kh][1] = f32x16{};
+#pragma unroll
+  for (int st = 0; st < 4; ++st) {
+    const int chn = 4 * half + st;
+#pragma unroll
+    for (int kh = 0; kh < NKH; ++kh) {
+      const int r = 32 * kh + col;
+      const bf16x8 kf = *reinterpret_cast<const bf16x8*>(kst + r * 128 + ((chn ^ swz8(r)) << 4));
+      s[kh][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qfrag[0][st], s[kh][0], 0, 0, 0);
+      s[kh][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qfrag[1][st], s[kh][1], 0, 0, 0);
+    }
+  }
+
+  if (tm.need) {
+#pragma unroll
+    for (int kh = 0; kh < NKH; ++kh) {
+#pragma unroll
+      for (int a = 0; a < 16; ++a) {
+        const int key = key0 + 32 * kh + 8 * (a >> 2) + 4 * half + (a & 3);
+        bool ok;
+        int fc;
+        if (tm.kspecial) {
+          const int sl = tm.kt * 64 + key;
+          ok = sl < g.S;
+          fc = sl / g.ns;
+        } else {
+          ok = key < tm.kvalid;
+          fc = tm.kframe;
+        }
+#pragma unroll
+        for (int gq = 0; gq < 2; ++gq) {
+          bool okg = ok;
+          if (tm.eff == SAF3R_FRAME_LOCAL) okg = okg && fc == frow[gq];
+          else if (tm.eff == SAF3R_ANCHOR_LOCAL) okg = okg && (fc == 0 || fc == frow[gq]);
+          else if (tm.eff == SAF3R_ANCHOR) okg = okg && fc == 0;
+          if (!okg) s[kh][gq][a] = -__builtin_inff();
+        }
+      }
+    }
+  }
+
+  bf16x8 pf[2][2 * NKH];
+  const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
+#pragma unroll
+  for (int gq = 0; gq < 2; ++gq) {
+    float mx = fmaxf(s[0][gq][0], s[0][gq][1]);
+#pragma unroll
+    for (int kh = 0; kh < NKH; ++kh)
+#pragma unroll
+      for (int a = (kh ? 0 : 2); a < 16; a += 2) mx = fmaxf(mx, fmaxf(s[kh][gq][a], s[kh][gq][a + 1]));
+    mx = partner_max(mx);
+    const bool need = mx * c > A.m[gq] * c + 8.0f;
+    if (__ballot(need) != 0) {
+      const float m_new = need ? mx : A.m[gq];
+      const float alpha = need ? __builtin_amdgcn_exp2f((A.m[gq] - m_new) * c) : 1.0f;
+      A.l[gq] *= alpha;
+#pragma unroll
+      for (int a = 0; a < 16; ++a) {
+        A.o[0][gq][a] *= alpha;
+        A.o[1][gq][a] *= alpha;
+      }
+      A.m[gq] = m_new;
+    }
+    const float mc = A.m[gq] == -__builtin_inff() ? 0.f : A.m[gq] * c;
+#pragma unroll
+    for (int j = 0; j < 2 * NKH; ++j) {
+      const int a0 = 8 * (j & 1);
+#pragma unroll
+      for (int t = 0; t < 8; t += 2) {
+        const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[j >> 1][gq][a0 + t], c, -mc));
+        const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[j >> 1][gq][a0 + t + 1], c, -mc));
+        const bf16x2 pr = {(__bf16)e0, (__bf16)e1};
+        pf[gq][j][t] = pr[0];
+        pf[gq][j][t + 1] = pr[1];
+        A.l[gq] = __builtin_amdgcn_fdot2_f32_bf16(pr, ones, A.l[gq], false);
+      }
+    }
+  }
+
+#pragma unroll
+  for (int j = 0; j < 2 * NKH; ++j) {
+    const int chn = 2 * j + half;
+#pragma unroll
+    for (int dh = 0; dh < 2; ++dh) {
+      const int r = 32 * dh + col;
+      const bf16x8 vf = NKH == 2 ? *reinterpret_cast<const bf16x8*>(vst + r * 128 + ((chn ^ swz8(r)) << 4))
+                                 : *reinterpret_cast<const bf16x8*>(vst + r * 64 + ((chn ^ swz4(r)) << 4));
+      A.o[dh][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[0][j], A.o[dh][0], 0, 0, 0);
+      A.o[dh][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[1][j], A.o[dh][1], 0, 0, 0);
+    }
+  }
+}
+
+// Key-tile sequence of a shared-mode group: up to four contiguous ranges.
 struct TileSeq {
   int s0, l0, s1, l1, s2, l2, s3, l3;
   int nr;
   int count;
-  const int* list;  // LDS, when non-null
   __device__ inline int at(int n) const {
-    if (list) return list[n];
     if (n < l0) return s0 + n;
     n -= l0;
     if (n < l1) return s1 + n;
@@ -76,11 +225,49 @@ struct TileSeq {
   }
 };
 
-__global__ __launch_bounds__(128) void sparse_attn_kernel(AttnParams p) {
-  __shared__ __align__(16) char kbuf[2][8192];
-  __shared__ __align__(16) char vbuf[2][8192];
-  __shared__ int tiles[kMaxSel];
-  __shared__ int wave_cnt[2];
+__device__ inline void tile_mask(const Geom& g, int kt, int eff, bool frame_rel, bool qspecial, TileMask& tm) {
+  tm.kt = kt;
+  tm.kspecial = kt < g.nst;
+  tm.eff = eff;
+  if (tm.kspecial) {
+    tm.kvalid = 64;
+    tm.kframe = 0;
+    tm.need = (kt + 1) * 64 > g.S || frame_rel;
+  } else {
+    const int b = (kt - g.nst) % g.NBf;
+    tm.kframe = (kt - g.nst) / g.NBf;
+    tm.kvalid = min(64, g.P - 64 * b);
+    tm.need = tm.kvalid < 64 || (frame_rel && qspecial);
+  }
+}
+
+__device__ inline void store_rows(const AttnParams& p, const Acc& A, const int64_t (&qtok)[2], int h, int half) {
+#pragma unroll
+  for (int gq = 0; gq < 2; ++gq) {
+    const float lt = partner_sum(A.l[gq]);
+    const float inv = lt > 0.f ? 1.0f / lt : 0.f;
+    if (qtok[gq] >= 0) {
+      uint32_t wv[16];
+#pragma unroll
+      for (int a = 0; a < 8; ++a) {
+        const bf16x2 x0 = {(__bf16)(A.o[0][gq][2 * a] * inv), (__bf16)(A.o[0][gq][2 * a + 1] * inv)};
+        const bf16x2 x1 = {(__bf16)(A.o[1][gq][2 * a] * inv), (__bf16)(A.o[1][gq][2 * a + 1] * inv)};
+        wv[a] = __builtin_bit_cast(uint32_t, x0);
+        wv[8 + a] = __builtin_bit_cast(uint32_t, x1);
+      }
+      u32x4* o4 = reinterpret_cast<u32x4*>(p.out + qtok[gq] * p.out_stride + (int64_t)h * 64 + 16 * half);
+      o4[0] = u32x4{wv[0], wv[1], wv[2], wv[3]};
+      o4[1] = u32x4{wv[4], wv[5], wv[6], wv[7]};
+      o4[4] = u32x4{wv[8], wv[9], wv[10], wv[11]};
+      o4[5] = u32x4{wv[12], wv[13], wv[14], wv[15]};
+    }
+  }
+}
+
+__global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
+  __shared__ __align__(16) char ring[kRing];
+  __shared__ int list[kMaxList];
+  __shared__ int wcnt[4];
 
   const Geom& g = p.g;
   const int tid = threadIdx.x;
@@ -92,257 +279,321 @@ __global__ __launch_bounds__(128) void sparse_attn_kernel(AttnParams p) {
   while (oh + 1 < p.n_order && bid >= p.item_start[oh + 1]) ++oh;
   const int h = p.order[oh];
   const int pat = p.pattern[h];
-  const int qt = bid - p.item_start[oh];
-  const bool qspecial = qt < g.nst;
-  const int qf = qspecial ? 0 : (qt - g.nst) / g.NBf;  // frame of a patch query tile
-  const int qb = qspecial ? 0 : (qt - g.nst) % g.NBf;
-
-  // query row owned by this lane and its frame / validity
-  const int qrow = 32 * w + col;
-  const int64_t qslot = (int64_t)qt * 64 + qrow;
-  int64_t qtok;
-  int frow;
-  if (qspecial) {
-    qtok = qslot < g.S ? (qslot / g.ns) * g.T + qslot % g.ns : -1;
-    frow = g.ns > 0 ? (int)(qslot / g.ns) : 0;
+  const int it = bid - p.item_start[oh];
+  const int ns4 = (g.nst + 3) >> 2;
+  const int groups_pf = (g.NBf + 3) >> 2;
+  int qt0, nw, kind;
+  if (pat == SAF3R_DENSE || pat == SAF3R_SKIP) {
+    qt0 = 4 * it;
+    nw = min(4, g.NT - qt0);
+    kind = pat == SAF3R_SKIP ? kSkip : kShared;
+  } else if (pat == SAF3R_TOKEN_DYNAMIC || (pat == SAF3R_BLOCK_DYNAMIC && it < ns4)) {
+    qt0 = 4 * it;
+    nw = min(4, g.nst - qt0);
+    kind = kShared;
+  } else if (pat == SAF3R_BLOCK_DYNAMIC) {
+    qt0 = g.nst + (it - ns4);
+    nw = 4;  // four waves on one query tile
+    kind = kSplit;
+  } else if (it < g.nst) {
+    qt0 = it;
+    nw = 1;
+    kind = kShared;
   } else {
-    int pp = qb * 64 + qrow;
-    qtok = pp < g.P ? (int64_t)qf * g.T + g.ns + pp : -1;
-    frow = qf;
+    const int j = it - g.nst, f = j / groups_pf, gg = j % groups_pf;
+    qt0 = g.nst + f * g.NBf + 4 * gg;
+    nw = min(4, g.NBf - 4 * gg);
+    kind = kShared;
   }
+  const bool wactive = w < nw;
+  const int qt = kind == kSplit ? qt0 : qt0 + (wactive ? w : 0);
+  const bool qspecial = qt < g.nst;
+  const int qf = qspecial ? 0 : (qt - g.nst) / g.NBf;
+  const int qb = qspecial ? 0 : (qt - g.nst) % g.NBf;
+  const bool writer = kind == kSplit ? true : wactive;
 
-  const int64_t head_base = (int64_t)h * g.L;  // slot offset of this head
-  __bf16* orow = p.out + (qtok >= 0 ? qtok : 0) * p.out_stride + (int64_t)h * 64;
+  int64_t qtok[2];
+  int frow[2];
+#pragma unroll
+  for (int gq = 0; gq < 2; ++gq) {
+    const int r = 32 * gq + col;
+    if (qspecial) {
+      const int64_t sl = (int64_t)qt * 64 + r;
+      qtok[gq] = (writer && sl < g.S) ? (sl / g.ns) * g.T + sl % g.ns : -1;
+      frow[gq] = g.ns > 0 ? (int)(sl / g.ns) : 0;
+    } else {
+      const int pp = qb * 64 + r;
+      qtok[gq] = (writer && pp < g.P) ? (int64_t)qf * g.T + g.ns + pp : -1;
+      frow[gq] = qf;
+    }
+  }
+  const int64_t head_base = (int64_t)h * g.L;
 
-  if (pat == SAF3R_SKIP) {
-    if (qtok >= 0) {
-      u32x4 z = {0, 0, 0, 0};
-      u32x4* o4 = reinterpret_cast<u32x4*>(orow + 16 * half);
-      o4[0] = z;
-      o4[1] = z;
-      o4[4] = z;
-      o4[5] = z;
+  if (kind == kSkip) {
+#pragma unroll
+    for (int gq = 0; gq < 2; ++gq) {
+      if (qtok[gq] >= 0) {
+        u32x4* o4 = reinterpret_cast<u32x4*>(p.out + qtok[gq] * p.out_stride + (int64_t)h * 64 + 16 * half);
+        const u32x4 z = {0, 0, 0, 0};
+        o4[0] = z;
+        o4[1] = z;
+        o4[4] = z;
+        o4[5] = z;
+      }
     }
     return;
   }
 
-  // ---- key-tile sequence (uniform) ----
-  TileSeq seq;
-  seq.s0 = seq.s1 = seq.s2 = seq.s3 = 0;
-  seq.l0 = seq.l1 = seq.l2 = seq.l3 = 0;
-  seq.nr = 0;
-  seq.count = 0;
-  seq.list = nullptr;
-  const int eff = (pat == SAF3R_TOKEN_DYNAMIC || (pat == SAF3R_BLOCK_DYNAMIC && qspecial)) ? SAF3R_DENSE : pat;
-  bool frame_rel = false;
-  if (eff == SAF3R_DENSE) {
-    seq.add(0, g.NT);
-  } else if (eff == SAF3R_BLOCK_DYNAMIC) {
-    // compact the selection row into LDS (drop -1 entries, keep order)
-    const int32_t* srow = p.sel + ((int64_t)p.slot[h] * ((int64_t)g.F * g.NBf) + (qt - g.nst)) * p.sel_width;
-    int base = 0;
-    for (int c0 = 0; c0 < p.sel_width; c0 += 128) {
-      int j = c0 + tid;
-      int v = j < p.sel_width ? srow[j] : -1;
-      bool ok = v >= 0 && v < g.F * g.NBf;
-      uint64_t m = __ballot(ok);
-      int pre = __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0));
-      if (lane == 0) wave_cnt[w] = __popcll(m);
-      __syncthreads();
-      int off = base + (w ? wave_cnt[0] : 0) + pre;
-      if (ok) tiles[off] = g.nst + v;
-      base += wave_cnt[0] + wave_cnt[1];
-      __syncthreads();
-    }
-    seq.count = base;
-    seq.list = tiles;
-  } else {
-    frame_rel = true;
-    // frames covered by the query tile
-    int f0 = qf, f1 = qf;
-    if (qspecial) {
-      int last = min(g.S, (qt + 1) * 64) - 1;
-      f0 = (qt * 64) / g.ns;
-      f1 = last / g.ns;
-    }
-    const bool need_anchor = (eff == SAF3R_ANCHOR_LOCAL || eff == SAF3R_ANCHOR);
-    const bool need_local = (eff != SAF3R_ANCHOR);
-    // special key tiles
-    int ls0 = 1, ls1 = 0;  // local special tile range [ls0, ls1]
-    if (g.ns > 0 && need_local) {
-      ls0 = (f0 * g.ns) / 64;
-      ls1 = ((f1 + 1) * g.ns - 1) / 64;
-    }
-    if (g.ns > 0 && need_anchor && !(need_local && ls0 == 0)) seq.add(0, (g.ns - 1) / 64 + 1);
-    if (g.ns > 0 && need_local) seq.add(ls0, ls1 - ls0 + 1);
-    // patch key tiles
-    if (need_anchor && !(need_local && f0 == 0)) seq.add(g.nst, g.NBf);
-    if (need_local) seq.add(g.nst + f0 * g.NBf, (f1 - f0 + 1) * g.NBf);
-  }
-
-  // ---- Q fragments: lane holds features 32*half .. 32*half+31 of its query row ----
-  bf16x8 qfrag[4];
-  {
-    const u32x4* qsrc = reinterpret_cast<const u32x4*>(p.q + (head_base + qslot) * 64 + 32 * half);
+  // ---- Q fragments: lane holds features 32*half .. 32*half+31 of rows 32*gq + col ----
+  bf16x8 qfrag[2][4];
 #pragma unroll
-    for (int s = 0; s < 4; ++s) qfrag[s] = __builtin_bit_cast(bf16x8, qsrc[s]);
+  for (int gq = 0; gq < 2; ++gq) {
+    const u32x4* qsrc =
+        reinterpret_cast<const u32x4*>(p.q + (head_base + (int64_t)qt * 64 + 32 * gq + col) * 64 + 32 * half);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) qfrag[gq][s] = __builtin_bit_cast(bf16x8, qsrc[s]);
   }
 
-  f32x16 o0 = {}, o1 = {};
-  float m_run = -__builtin_inff();
-  float l_run = 0.f;
+  Acc A;
+#pragma unroll
+  for (int a = 0; a < 2; ++a) {
+    A.o[a][0] = A.o[a][1] = f32x16{};
+    A.m[a] = -__builtin_inff();
+    A.l[a] = 0.f;
+  }
   const float c = p.c;
 
-  // staging: thread handles 16-byte chunks tid + 128*u of the 8 KB K and V tiles
-  u32x4 kreg[4], vreg[4];
-  auto load_tile = [&](int kt) {
-    const u32x4* ks = reinterpret_cast<const u32x4*>(p.k + (head_base + (int64_t)kt * 64) * 64);
-    const u32x4* vs = reinterpret_cast<const u32x4*>(p.v + (head_base + (int64_t)kt * 64) * 64);
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      kreg[u] = ks[tid + 128 * u];
-      vreg[u] = vs[tid + 128 * u];
+  if (kind == kShared) {
+    // ---- key-tile sequence (uniform) ----
+    TileSeq seq;
+    seq.s0 = seq.s1 = seq.s2 = seq.s3 = 0;
+    seq.l0 = seq.l1 = seq.l2 = seq.l3 = 0;
+    seq.nr = 0;
+    seq.count = 0;
+    bool frame_rel = false;
+    const int eff = (pat == SAF3R_DENSE || pat == SAF3R_TOKEN_DYNAMIC || pat == SAF3R_BLOCK_DYNAMIC) ? SAF3R_DENSE : pat;
+    if (eff == SAF3R_DENSE) {
+      seq.add(0, g.NT);
+    } else {
+      frame_rel = true;
+      int f0 = qf, f1 = qf;
+      if (qspecial) {
+        const int last = min(g.S, (qt + 1) * 64) - 1;
+        f0 = (qt * 64) / g.ns;
+        f1 = last / g.ns;
+      }
+      const bool need_anchor = (pat == SAF3R_ANCHOR_LOCAL || pat == SAF3R_ANCHOR);
+      const bool need_local = (pat != SAF3R_ANCHOR);
+      int ls0 = 1, ls1 = 0;
+      if (g.ns > 0 && need_local) {
+        ls0 = (f0 * g.ns) / 64;
+        ls1 = ((f1 + 1) * g.ns - 1) / 64;
+      }
+      if (g.ns > 0 && need_anchor && !(need_local && ls0 == 0)) seq.add(0, (g.ns - 1) / 64 + 1);
+      if (g.ns > 0 && need_local) seq.add(ls0, ls1 - ls0 + 1);
+      if (need_anchor && !(need_local && f0 == 0)) seq.add(g.nst, g.NBf);
+      if (need_local) seq.add(g.nst + f0 * g.NBf, (f1 - f0 + 1) * g.NBf);
     }
-  };
-  auto store_tile = [&](int buf) {
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      int id = tid + 128 * u, r = id >> 3, ch = id & 7;
-      int off = r * 128 + ((ch ^ (r & 7)) << 4);
-      *reinterpret_cast<u32x4*>(&kbuf[buf][off]) = kreg[u];
-      *reinterpret_cast<u32x4*>(&vbuf[buf][off]) = vreg[u];
-    }
-  };
+    const int count = seq.count;
 
-  const int count = seq.count;
-  if (count > 0) {
-    load_tile(seq.at(0));
-    store_tile(0);
+    // thread tid owns 16-byte chunks tid and tid + 256 of the K and the V tile; LDS chunk
+    // position P holds row P/8, global chunk (P % 8) ^ swz8(row)
+    auto issue = [&](int n) {
+      const int kt = seq.at(n);
+      char* st = ring + (n % kStages) * 16384;
+      const __bf16* kb = p.k + (head_base + (int64_t)kt * 64) * 64;
+      const __bf16* vb = p.v + (head_base + (int64_t)kt * 64) * 64;
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int P = tid + 256 * u, r = P >> 3, cg = (P & 7) ^ swz8(r);
+        __builtin_amdgcn_global_load_lds((const void*)(kb + r * 64 + cg * 8),
+                                         (lds_void*)(st + (256 * u + 64 * w) * 16), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((const void*)(vb + r * 64 + cg * 8),
+                                         (lds_void*)(st + 8192 + (256 * u + 64 * w) * 16), 16, 0, 0);
+      }
+    };
+
+    wait_vm<0>();  // Q fragments landed; from here vmcnt counts ring loads only
+    for (int n = 0; n < kStages - 1 && n < count; ++n) issue(n);
+    for (int n = 0; n < count; ++n) {
+      const int ahead = min(kStages - 2, count - 1 - n);  // tiles issued after tile n
+      if (ahead >= 2) wait_vm<8>();
+      else if (ahead == 1) wait_vm<4>();
+      else wait_vm<0>();
+      barrier_only();
+      if (n + kStages - 1 < count) issue(n + kStages - 1);
+      if (!wactive) continue;
+      const int kt = seq.at(n);
+      TileMask tm;
+      tile_mask(g, kt, eff, frame_rel, qspecial, tm);
+      const char* kst = ring + (n % kStages) * 16384;
+      attend<2>(kst, kst + 8192, qfrag, A, frow, tm, g, 0, half, col, c);
+    }
+    store_rows(p, A, qtok, h, half);
+    return;
   }
-  __syncthreads();
 
-  for (int n = 0; n < count; ++n) {
-    const int cur = n & 1;
-    const int kt = seq.at(n);
-    if (n + 1 < count) load_tile(seq.at(n + 1));
+  // ================= split mode: one query tile, block list split across the four waves ======
+  {
+    // compact the selection row into LDS (drop invalid entries, keep order)
+    const int32_t* srow = p.sel + ((int64_t)p.slot[h] * ((int64_t)g.F * g.NBf) + (qt - g.nst)) * p.sel_width;
+    int total = 0;
+    for (int c0 = 0; c0 < p.sel_width; c0 += 256) {
+      const int j = c0 + tid;
+      const int v = j < p.sel_width ? srow[j] : -1;
+      const bool ok = v >= 0 && v < g.F * g.NBf;
+      const uint64_t m = __ballot(ok);
+      const int pre = __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0));
+      if (lane == 0) wcnt[w] = __popcll(m);
+      __syncthreads();
+      int off = total;
+      for (int i = 0; i < w; ++i) off += wcnt[i];
+      if (ok && off + pre < kMaxList) list[off + pre] = g.nst + v;
+      total += wcnt[0] + wcnt[1] + wcnt[2] + wcnt[3];
+      __syncthreads();
+    }
+    total = min(total, kMaxList);
+    const int pos0 = (total * w) >> 2, pos1 = (total * (w + 1)) >> 2;
 
-    // ---- S^T = K . Q^T ----
-    f32x16 s0 = {}, s1 = {};
+    // half-tile stream of this wave: (list position, half); a half is present when its first key
+    // is a valid key of the block
+    auto half_valid = [&](int kt, int hh) { return hh == 0 || g.P - 64 * ((kt - g.nst) % g.NBf) > 32; };
+    char* slots = ring + w * 16384;  // two 8 KB slots: K half (4 KB) + V half (4 KB)
+    auto issue = [&](int pos, int hh, int sl) {
+      const int kt = list[pos];
+      char* st = slots + sl * 8192;
+      const __bf16* kb = p.k + (head_base + (int64_t)kt * 64 + 32 * hh) * 64;
+      const __bf16* vb = p.v + (head_base + (int64_t)kt * 64) * 64 + 32 * hh;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const int chn = 4 * half + s;
-      const int r0 = col, r1 = 32 + col;
-      bf16x8 ka = *reinterpret_cast<const bf16x8*>(&kbuf[cur][r0 * 128 + ((chn ^ (r0 & 7)) << 4)]);
-      bf16x8 kb = *reinterpret_cast<const bf16x8*>(&kbuf[cur][r1 * 128 + ((chn ^ (r1 & 7)) << 4)]);
-      s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qfrag[s], s0, 0, 0, 0);
-      s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kb, qfrag[s], s1, 0, 0, 0);
+      for (int u = 0; u < 4; ++u) {
+        const int P = 64 * u + lane;
+        const int r = P >> 3, ck = (P & 7) ^ swz8(r);   // K half: 32 rows x 8 chunks
+        __builtin_amdgcn_global_load_lds((const void*)(kb + r * 64 + ck * 8), (lds_void*)(st + 64 * u * 16), 16, 0, 0);
+        const int i = P >> 2, cv = (P & 3) ^ swz4(i);   // V half: 64 rows x 4 chunks
+        __builtin_amdgcn_global_load_lds((const void*)(vb + i * 64 + cv * 8), (lds_void*)(st + 4096 + 64 * u * 16),
+                                         16, 0, 0);
+      }
+    };
+
+    wait_vm<0>();
+    int pos = pos0, hh = 0, cur = 0;
+    if (pos < pos1) issue(pos, hh, 0);
+    while (pos < pos1) {
+      int npos = pos, nhh = hh;
+      if (hh == 0 && half_valid(list[pos], 1)) nhh = 1;
+      else {
+        nhh = 0;
+        ++npos;
+      }
+      const bool more = npos < pos1;
+      if (more) {
+        issue(npos, nhh, cur ^ 1);
+        wait_vm<8>();
+      } else {
+        wait_vm<0>();
+      }
+      const int kt = list[pos];
+      TileMask tm;
+      tile_mask(g, kt, SAF3R_DENSE, false, false, tm);
+      tm.need = tm.kvalid < 32 * (hh + 1);
+      const char* st = slots + cur * 8192;
+      attend<1>(st, st + 4096, qfrag, A, frow, tm, g, 32 * hh, half, col, c);
+      pos = npos;
+      hh = nhh;
+      cur ^= 1;
     }
 
-    // ---- masking of partial / multi-frame tiles ----
-    const bool kspecial = kt < g.nst;
-    bool partial;
-    if (kspecial) partial = (kt + 1) * 64 > g.S;
-    else partial = (g.P & 63) != 0 && ((kt - g.nst) % g.NBf) == g.NBf - 1;
-    const bool need_mask = partial || (frame_rel && (kspecial || qspecial));
-    if (need_mask) {
-      const int kfrm_patch = kspecial ? 0 : (kt - g.nst) / g.NBf;
-      const int kp0 = kspecial ? 0 : ((kt - g.nst) % g.NBf) * 64;
+    // ---- merge the four partial results through LDS ----
 #pragma unroll
-      for (int a = 0; a < 32; ++a) {
-        const int key = 32 * (a >> 4) + 8 * ((a & 15) >> 2) + 4 * half + (a & 3);
-        bool ok;
-        int fc;
-        if (kspecial) {
-          const int sl = kt * 64 + key;
-          ok = sl < g.S;
-          fc = sl / g.ns;
-        } else {
-          ok = kp0 + key < g.P;
-          fc = kfrm_patch;
-        }
-        if (eff == SAF3R_FRAME_LOCAL) ok = ok && fc == frow;
-        else if (eff == SAF3R_ANCHOR_LOCAL) ok = ok && (fc == 0 || fc == frow);
-        else if (eff == SAF3R_ANCHOR) ok = ok && fc == 0;
-        if (!ok) {
-          if (a < 16) s0[a] = -__builtin_inff();
-          else s1[a - 16] = -__builtin_inff();
-        }
+    for (int gq = 0; gq < 2; ++gq) A.l[gq] = partner_sum(A.l[gq]);
+    __syncthreads();  // every wave is done with its slots and with the list
+    float* obuf = reinterpret_cast<float*>(ring) + w * 4096;  // [64 rows][64 d] fp32 per wave
+    float* mls = reinterpret_cast<float*>(list);                // m[4][64], l[4][64]
+#pragma unroll
+    for (int gq = 0; gq < 2; ++gq) {
+      const int row = 32 * gq + col;
+#pragma unroll
+      for (int dh = 0; dh < 2; ++dh) {
+        f32x4* dst = reinterpret_cast<f32x4*>(obuf + row * 64 + 32 * dh + 16 * half);
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4)
+          dst[q4] = f32x4{A.o[dh][gq][4 * q4], A.o[dh][gq][4 * q4 + 1], A.o[dh][gq][4 * q4 + 2], A.o[dh][gq][4 * q4 + 3]};
+      }
+      if (half == 0) {
+        mls[w * 64 + row] = A.m[gq];
+        mls[256 + w * 64 + row] = A.l[gq];
       }
     }
-
-    // ---- online softmax (base 2) ----
-    float mx = -__builtin_inff();
-#pragma unroll
-    for (int a = 0; a < 16; ++a) mx = fmaxf(mx, fmaxf(s0[a], s1[a]));
-    mx = permlane_partner_max(mx);
-    const float m_new = fmaxf(m_run, mx);
-    const float m_use = m_new == -__builtin_inff() ? 0.f : m_new;
-    const float alpha = __builtin_amdgcn_exp2f((m_run - m_use) * c);
-    const float mc = m_use * c;
-    float ls = 0.f;
-#pragma unroll
-    for (int a = 0; a < 16; ++a) {
-      s0[a] = __builtin_amdgcn_exp2f(__builtin_fmaf(s0[a], c, -mc));
-      s1[a] = __builtin_amdgcn_exp2f(__builtin_fmaf(s1[a], c, -mc));
-      ls += s0[a] + s1[a];
-    }
-    l_run = l_run * alpha + ls;
-    m_run = m_new;
-#pragma unroll
-    for (int a = 0; a < 16; ++a) {
-      o0[a] *= alpha;
-      o1[a] *= alpha;
-    }
-
-    // ---- O^T += V^T . P^T ----
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const f32x16& sj = (j < 2) ? s0 : s1;
-      const int a0 = 8 * (j & 1);
-      bf16x8 pf;
-#pragma unroll
-      for (int t = 0; t < 8; ++t) pf[t] = (__bf16)sj[a0 + t];
-      const int chn = 2 * j + half;
-      const int r0 = col, r1 = 32 + col;
-      bf16x8 va = *reinterpret_cast<const bf16x8*>(&vbuf[cur][r0 * 128 + ((chn ^ (r0 & 7)) << 4)]);
-      bf16x8 vb = *reinterpret_cast<const bf16x8*>(&vbuf[cur][r1 * 128 + ((chn ^ (r1 & 7)) << 4)]);
-      o0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pf, o0, 0, 0, 0);
-      o1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vb, pf, o1, 0, 0, 0);
-    }
-
-    if (n + 1 < count) store_tile(cur ^ 1);
     __syncthreads();
-  }
-
-  // ---- epilogue: normalise and store 2 x 32 bytes per lane ----
-  const float lt = permlane_partner_sum(l_run);
-  const float inv = lt > 0.f ? 1.0f / lt : 0.f;
-  if (qtok >= 0) {
-    uint32_t wv[16];
-#pragma unroll
-    for (int a = 0; a < 8; ++a) {
-      bf16x2 x0 = {(__bf16)(o0[2 * a] * inv), (__bf16)(o0[2 * a + 1] * inv)};
-      bf16x2 x1 = {(__bf16)(o1[2 * a] * inv), (__bf16)(o1[2 * a + 1] * inv)};
-      wv[a] = __builtin_bit_cast(uint32_t, x0);
-      wv[8 + a] = __builtin_bit_cast(uint32_t, x1);
+    const int row = tid >> 2, d0 = (tid & 3) * 16;
+    int64_t tok;
+    if (qspecial) tok = -1;  // split mode only serves patch tiles
+    else {
+      const int pp = qb * 64 + row;
+      tok = pp < g.P ? (int64_t)qf * g.T + g.ns + pp : -1;
     }
-    u32x4* o4 = reinterpret_cast<u32x4*>(orow + 16 * half);
-    o4[0] = u32x4{wv[0], wv[1], wv[2], wv[3]};
-    o4[1] = u32x4{wv[4], wv[5], wv[6], wv[7]};
-    o4[4] = u32x4{wv[8], wv[9], wv[10], wv[11]};
-    o4[5] = u32x4{wv[12], wv[13], wv[14], wv[15]};
+    float mw[4], M = -__builtin_inff();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      mw[i] = mls[i * 64 + row];
+      M = fmaxf(M, mw[i]);
+    }
+    float L = 0.f, fw[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      fw[i] = mw[i] == -__builtin_inff() ? 0.f : __builtin_amdgcn_exp2f((mw[i] - M) * c);
+      L += fw[i] * mls[256 + i * 64 + row];
+    }
+    const float inv = L > 0.f ? 1.0f / L : 0.f;
+    if (tok >= 0) {
+      float acc[16];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const f32x4* src = reinterpret_cast<const f32x4*>(reinterpret_cast<float*>(ring) + i * 4096 + row * 64 + d0);
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+          const f32x4 x = src[q4];
+          acc[4 * q4 + 0] += fw[i] * x[0];
+          acc[4 * q4 + 1] += fw[i] * x[1];
+          acc[4 * q4 + 2] += fw[i] * x[2];
+          acc[4 * q4 + 3] += fw[i] * x[3];
+        }
+      }
+      uint32_t wv[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const bf16x2 x = {(__bf16)(acc[2 * e] * inv), (__bf16)(acc[2 * e + 1] * inv)};
+        wv[e] = __builtin_bit_cast(uint32_t, x);
+      }
+      u32x4* o4 = reinterpret_cast<u32x4*>(p.out + tok * p.out_stride + (int64_t)h * 64 + d0);
+      o4[0] = u32x4{wv[0], wv[1], wv[2], wv[3]};
+      o4[1] = u32x4{wv[4], wv[5], wv[6], wv[7]};
+    }
   }
 }
 
-// Relative cost of one work item (key tiles visited), used to order heads longest-first.
+// Work items of a head and their relative cost, used to order heads longest-first.
+static int head_items(int pat, const Geom& g) {
+  const int ns4 = (g.nst + 3) / 4, groups_pf = (g.NBf + 3) / 4;
+  switch (pat) {
+    case SAF3R_DENSE:
+    case SAF3R_SKIP: return (g.NT + 3) / 4;
+    case SAF3R_TOKEN_DYNAMIC: return ns4;
+    case SAF3R_BLOCK_DYNAMIC: return ns4 + g.F * g.NBf;
+    default: return g.nst + g.F * groups_pf;
+  }
+}
+
 static int64_t item_cost(int pat, const Geom& g, int sel_width) {
   switch (pat) {
-    case SAF3R_DENSE: return g.NT;
-    case SAF3R_TOKEN_DYNAMIC: return g.NT;
+    case SAF3R_DENSE:
+    case SAF3R_TOKEN_DYNAMIC: return 4LL * g.NT;
     case SAF3R_BLOCK_DYNAMIC: return sel_width;
-    case SAF3R_ANCHOR_LOCAL: return 2 * (g.NBf + 1);
-    case SAF3R_FRAME_LOCAL: return g.NBf + 1;
-    case SAF3R_ANCHOR: return g.NBf + 1;
+    case SAF3R_ANCHOR_LOCAL: return 8LL * (g.NBf + 1);
+    case SAF3R_FRAME_LOCAL:
+    case SAF3R_ANCHOR: return 4LL * (g.NBf + 1);
     default: return 0;
   }
 }
@@ -375,8 +626,8 @@ extern "C" int saf3r_sparse_attn_fwd(const void* q_packed, const void* k_packed,
   }
   if (n_dyn > 0) {
     if (!sel) return fail(SAF3R_ERR_INVALID, "saf3r_sparse_attn_fwd: block-dynamic heads need a selection list");
-    if (sel_width <= 0 || sel_width > kMaxSel)
-      return fail(SAF3R_ERR_UNSUPPORTED, "saf3r_sparse_attn_fwd: sel_width must be in [1, %d] (got %d)", kMaxSel,
+    if (sel_width <= 0 || sel_width > kMaxList)
+      return fail(SAF3R_ERR_UNSUPPORTED, "saf3r_sparse_attn_fwd: sel_width must be in [1, %d] (got %d)", kMaxList,
                   sel_width);
   }
   p.q = (const __bf16*)q_packed;
@@ -387,7 +638,6 @@ extern "C" int saf3r_sparse_attn_fwd(const void* q_packed, const void* k_packed,
   p.out = (__bf16*)out;
   p.out_stride = out_row_stride;
   p.c = scale * 1.4426950408889634f;
-  // heads ordered by decreasing item cost (stable by head id), each with its item range
   int idx[kMaxHeads];
   for (int h = 0; h < num_heads; ++h) idx[h] = h;
   for (int i = 1; i < num_heads; ++i) {
@@ -403,7 +653,7 @@ extern "C" int saf3r_sparse_attn_fwd(const void* q_packed, const void* k_packed,
   p.n_order = 0;
   for (int i = 0; i < num_heads; ++i) {
     int h = idx[i];
-    int items = p.pattern[h] == SAF3R_TOKEN_DYNAMIC ? p.g.nst : p.g.NT;
+    int items = head_items(p.pattern[h], p.g);
     if (items == 0) continue;
     p.order[p.n_order] = h;
     p.item_start[p.n_order] = (int)total;
@@ -413,6 +663,6 @@ extern "C" int saf3r_sparse_attn_fwd(const void* q_packed, const void* k_packed,
   p.item_start[p.n_order] = (int)total;
   if (total == 0) return SAF3R_OK;
   if (total > 0x7fffffff) return fail(SAF3R_ERR_UNSUPPORTED, "saf3r_sparse_attn_fwd: too many work items");
-  hipLaunchKernelGGL(sparse_attn_kernel, dim3((unsigned)total), dim3(128), 0, (hipStream_t)stream, p);
+  hipLaunchKernelGGL(sparse_attn_kernel, dim3((unsigned)total), dim3(256), 0, (hipStream_t)stream, p);
   return check_launch("saf3r_sparse_attn_fwd");
 }
