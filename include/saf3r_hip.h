@@ -84,8 +84,10 @@ int64_t saf3r_packed_slots(int frames, int tokens_per_frame, int num_special);
  *            (the qkv Linear output [N, 3*H*64] is q = base, k = base + H*64, v = base + 2*H*64,
  *            tok_stride = 3*H*64, head_stride = 64).
  *   ln_*:    fp32 [64] device arrays (weight, bias), used when apply_ln != 0.
- *   pos:     int32 [N][2] device (y, x) positions, used when rope_inv_freq != NULL.
- *   rope_inv_freq: host fp32 [16] inverse frequencies (1 / base^(2i/32)); NULL disables RoPE.
+ *   pos:     int32 [N][2] device (y, x) positions, used when rope_cos != NULL.
+ *   rope_cos, rope_sin: device fp32 [rope_positions][16] tables, cos / sin of
+ *            position * inv_freq[i] (inv_freq[i] = 1 / base^(2i/32)); NULL disables RoPE.
+ *            Positions are clamped to [0, rope_positions - 1].
  * Replaces: saf3r/patch/patch_vggt.py:577-583 (qkv reshape, q_norm/k_norm, rope) and
  *           saf3r/models/official_vggt/layers/rope.py:154-188.
  */
@@ -93,7 +95,7 @@ int saf3r_pack_qkv(const void* q, const void* k, const void* v, int64_t tok_stri
                    int frames, int tokens_per_frame, int num_special, int num_heads,
                    const float* q_ln_weight, const float* q_ln_bias, const float* k_ln_weight,
                    const float* k_ln_bias, float ln_eps, int apply_ln,
-                   const int32_t* pos, const float* rope_inv_freq,
+                   const int32_t* pos, const float* rope_cos, const float* rope_sin, int rope_positions,
                    void* q_packed, void* k_packed, void* v_packed, void* stream);
 
 /*

@@ -55,7 +55,7 @@ def load():
         "saf3r_abi_version": ([], i32),
         "saf3r_last_error": ([], ctypes.c_char_p),
         "saf3r_packed_slots": ([i32, i32, i32], i64),
-        "saf3r_pack_qkv": ([p, p, p, i64, i64, i32, i32, i32, i32, p, p, p, p, f32, i32, p, p, p, p, p, p], i32),
+        "saf3r_pack_qkv": ([p, p, p, i64, i64, i32, i32, i32, i32, p, p, p, p, f32, i32, p, p, p, i32, p, p, p, p], i32),
         "saf3r_block_pool": ([p, p, i32, i32, i32, i32, p, i32, p, p, p], i32),
         "saf3r_topk_from_scores": ([p, i32, i32, i32, i32, i32, p, p], i32),
         "saf3r_block_select": ([p, p, i32, i32, i32, i32, i32, i32, p, p], i32),

@@ -20,7 +20,7 @@
 // Shared mode (dense, frame-local, anchor+local, anchor, special rows of the dynamic patterns):
 // a workgroup of four waves owns up to four consecutive query tiles with one key sequence. Full
 // key tiles (8 KB K + 8 KB transposed V) stream through a 4-stage LDS ring filled by
-// global_load_lds_dwordx4 (no register staging) with one barrier per tile; all four waves consume
+// global_load_lds_dwordx4 (no register staging), two tiles per barrier; all four waves consume
 // each staged tile.
 // Split mode (patch rows of block-dynamic heads): a workgroup owns one query tile; its four waves
 // split the tile's block list into quarters and each streams its own 32-key half tiles through a
@@ -414,20 +414,26 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
     };
 
     wait_vm<0>();  // Q fragments landed; from here vmcnt counts ring loads only
-    for (int n = 0; n < kStages - 1 && n < count; ++n) issue(n);
-    for (int n = 0; n < count; ++n) {
-      const int ahead = min(kStages - 2, count - 1 - n);  // tiles issued after tile n
-      if (ahead >= 2) wait_vm<8>();
-      else if (ahead == 1) wait_vm<4>();
-      else wait_vm<0>();
+    // tiles move in pairs: pair i+1 loads into the two free stages while pair i is consumed,
+    // one barrier per pair
+    issue(0);
+    if (count > 1) issue(1);
+    for (int n = 0; n < count; n += 2) {
+      wait_vm<0>();
       barrier_only();
-      if (n + kStages - 1 < count) issue(n + kStages - 1);
+      if (n + 2 < count) issue(n + 2);
+      if (n + 3 < count) issue(n + 3);
       if (!wactive) continue;
-      const int kt = seq.at(n);
-      TileMask tm;
-      tile_mask(g, kt, eff, frame_rel, qspecial, tm);
-      const char* kst = ring + (n % kStages) * 16384;
-      attend<2>(kst, kst + 8192, qfrag, A, frow, tm, g, 0, half, col, c);
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        if (n + u < count) {
+          const int kt = seq.at(n + u);
+          TileMask tm;
+          tile_mask(g, kt, eff, frame_rel, qspecial, tm);
+          const char* kst = ring + ((n + u) % kStages) * 16384;
+          attend<2>(kst, kst + 8192, qfrag, A, frow, tm, g, 0, half, col, c);
+        }
+      }
     }
     store_rows(p, A, qtok, h, half);
     return;

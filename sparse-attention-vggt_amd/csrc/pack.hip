@@ -5,7 +5,8 @@
 //      saf3r/models/official_vggt/layers/rope.py:86-188 (RoPE-2D: first 32 features rotated by
 //      the y position, last 32 by x; within each 32: rotate(t) = cat(-t[16:], t[:16])).
 // Under autocast(bf16) the reference runs LayerNorm and RoPE in fp32 and hands bf16 q/k/v to
-// attention; this kernel does the same and rounds once, to nearest-even bf16.
+// attention; this kernel does the same and rounds once, to nearest-even bf16. The cos/sin tables
+// come from the caller, computed as the reference does (fp32 angles = position * inv_freq).
 #include "common.h"
 
 namespace saf3r {
@@ -23,7 +24,9 @@ struct PackParams {
   int apply_ln;
   int apply_rope;
   const int32_t* pos;
-  float inv_freq[16];
+  const float* rcos;
+  const float* rsin;
+  int rpos;
   __bf16* qp;
   __bf16* kp;
   __bf16* vp;
@@ -44,12 +47,20 @@ __global__ __launch_bounds__(256) void pack_qkv_kernel(PackParams p) {
 
   float cs[16], sn[16];
   if (p.apply_rope && tok >= 0) {
-    const float pv = (float)p.pos[tok * 2 + (c >> 1)];
+    const int pv = min(max(p.pos[tok * 2 + (c >> 1)], 0), p.rpos - 1);
+    const f32x4* c4 = reinterpret_cast<const f32x4*>(p.rcos + pv * 16);
+    const f32x4* s4 = reinterpret_cast<const f32x4*>(p.rsin + pv * 16);
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      float a = pv * p.inv_freq[j];
-      cs[j] = cosf(a);
-      sn[j] = sinf(a);
+    for (int j = 0; j < 4; ++j) {
+      const f32x4 cv = c4[j], sv = s4[j];
+      cs[4 * j] = cv[0];
+      cs[4 * j + 1] = cv[1];
+      cs[4 * j + 2] = cv[2];
+      cs[4 * j + 3] = cv[3];
+      sn[4 * j] = sv[0];
+      sn[4 * j + 1] = sv[1];
+      sn[4 * j + 2] = sv[2];
+      sn[4 * j + 3] = sv[3];
     }
   }
 
@@ -159,8 +170,8 @@ extern "C" int saf3r_pack_qkv(const void* q, const void* k, const void* v, int64
                               int frames, int tokens_per_frame, int num_special, int num_heads,
                               const float* q_ln_weight, const float* q_ln_bias, const float* k_ln_weight,
                               const float* k_ln_bias, float ln_eps, int apply_ln, const int32_t* pos,
-                              const float* rope_inv_freq, void* q_packed, void* k_packed, void* v_packed,
-                              void* stream) {
+                              const float* rope_cos, const float* rope_sin, int rope_positions, void* q_packed,
+                              void* k_packed, void* v_packed, void* stream) {
   if (int e = injected("saf3r_pack_qkv")) return e;
   PackParams p;
   if (!make_geom(frames, tokens_per_frame, num_special, &p.g))
@@ -175,7 +186,8 @@ extern "C" int saf3r_pack_qkv(const void* q, const void* k, const void* v, int64
     return fail(SAF3R_ERR_INVALID, "saf3r_pack_qkv: packed outputs must be 16-byte aligned");
   if (apply_ln && (!q_ln_weight || !q_ln_bias || !k_ln_weight || !k_ln_bias))
     return fail(SAF3R_ERR_INVALID, "saf3r_pack_qkv: LayerNorm requested without parameters");
-  if (rope_inv_freq && !pos) return fail(SAF3R_ERR_INVALID, "saf3r_pack_qkv: RoPE requested without positions");
+  if (rope_cos && (!pos || !rope_sin || rope_positions <= 0 || ((uintptr_t)rope_cos | (uintptr_t)rope_sin) % 16))
+    return fail(SAF3R_ERR_INVALID, "saf3r_pack_qkv: RoPE needs positions and 16-byte aligned cos/sin tables");
   p.q = (const __bf16*)q;
   p.k = (const __bf16*)k;
   p.v = (const __bf16*)v;
@@ -187,9 +199,11 @@ extern "C" int saf3r_pack_qkv(const void* q, const void* k, const void* v, int64
   p.kb = k_ln_bias;
   p.eps = ln_eps;
   p.apply_ln = apply_ln != 0;
-  p.apply_rope = rope_inv_freq != nullptr;
+  p.apply_rope = rope_cos != nullptr;
   p.pos = pos;
-  for (int j = 0; j < 16; ++j) p.inv_freq[j] = rope_inv_freq ? rope_inv_freq[j] : 0.f;
+  p.rcos = rope_cos;
+  p.rsin = rope_sin;
+  p.rpos = rope_positions;
   p.qp = (__bf16*)q_packed;
   p.kp = (__bf16*)k_packed;
   p.vp = (__bf16*)v_packed;

@@ -25,7 +25,8 @@ __device__ inline void topk_insert(uint64_t (&a)[K], uint64_t x) {
 }
 
 // ---------------------------------------------------------------------------------------
-// Pooling: one wave per (head, patch block), lane = feature.
+// Pooling: eight lanes per (head, patch block), each lane owning 8 features (16-byte loads), so a
+// wave streams eight blocks at once. Every feature is still summed sequentially in row order.
 // ---------------------------------------------------------------------------------------
 struct PoolParams {
   const __bf16* q;
@@ -37,55 +38,70 @@ struct PoolParams {
   int heads[kMaxHeads];
 };
 
+__device__ inline void add_row8(float (&acc)[8], const u32x4& x) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    acc[2 * e] = acc[2 * e] + bf16_lo(x[e]);
+    acc[2 * e + 1] = acc[2 * e + 1] + bf16_hi(x[e]);
+  }
+}
+
 __global__ __launch_bounds__(256) void block_pool_kernel(PoolParams p) {
   const Geom& g = p.g;
-  const int lane = threadIdx.x & 63;
-  const int bi = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63, sub = lane & 7;
+  const int bi = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 8 + (lane >> 3);
   if (bi >= p.nb) return;
   const int hs = blockIdx.y;
   const int h = p.heads[hs];
   const int f = bi / g.NBf, b = bi % g.NBf;
   const int cnt = min(64, g.P - 64 * b);
   const int64_t row0 = (int64_t)h * g.L + g.Sp + (int64_t)f * g.Pp + 64 * b;
-  const __bf16* qs = p.q + row0 * 64 + lane;
-  const __bf16* ks = p.k ? p.k + row0 * 64 + lane : nullptr;
-  float aq = 0.f, ak = 0.f;
-  int r = 0;
-  for (; r + 8 <= cnt; r += 8) {
-    float vq[8], vk[8];
+  const u32x4* qs = reinterpret_cast<const u32x4*>(p.q + row0 * 64) + sub;
+  const u32x4* ks = p.k ? reinterpret_cast<const u32x4*>(p.k + row0 * 64) + sub : nullptr;
+  float aq[8], ak[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) vq[j] = (float)qs[(r + j) * 64];
+  for (int e = 0; e < 8; ++e) aq[e] = ak[e] = 0.f;
+  int r = 0;
+  for (; r + 4 <= cnt; r += 4) {
+    u32x4 xq[4], xk[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) xq[j] = qs[(r + j) * 8];
     if (ks) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) vk[j] = (float)ks[(r + j) * 64];
+      for (int j = 0; j < 4; ++j) xk[j] = ks[(r + j) * 8];
     }
 #pragma unroll
-    for (int j = 0; j < 8; ++j) aq = aq + vq[j];
+    for (int j = 0; j < 4; ++j) add_row8(aq, xq[j]);
     if (ks) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) ak = ak + vk[j];
+      for (int j = 0; j < 4; ++j) add_row8(ak, xk[j]);
     }
   }
   for (; r < cnt; ++r) {
-    aq = aq + (float)qs[r * 64];
-    if (ks) ak = ak + (float)ks[r * 64];
+    add_row8(aq, qs[r * 8]);
+    if (ks) add_row8(ak, ks[r * 8]);
   }
-  const int64_t o = ((int64_t)hs * p.nb + bi) * 64 + lane;
-  p.pq[o] = aq / (float)cnt;
-  if (ks) p.pk[o] = ak / (float)cnt;
+  const float fc = (float)cnt;
+  const int64_t o = ((int64_t)hs * p.nb + bi) * 64 + 8 * sub;
+  f32x4* dq = reinterpret_cast<f32x4*>(p.pq + o);
+  dq[0] = f32x4{aq[0] / fc, aq[1] / fc, aq[2] / fc, aq[3] / fc};
+  dq[1] = f32x4{aq[4] / fc, aq[5] / fc, aq[6] / fc, aq[7] / fc};
+  if (ks) {
+    f32x4* dk = reinterpret_cast<f32x4*>(p.pk + o);
+    dk[0] = f32x4{ak[0] / fc, ak[1] / fc, ak[2] / fc, ak[3] / fc};
+    dk[1] = f32x4{ak[4] / fc, ak[5] / fc, ak[6] / fc, ak[7] / fc};
+  }
 }
 
 // ---------------------------------------------------------------------------------------
-// Top-k from a score matrix: one thread per (row, frame).
+// Top-k from a score matrix. Rows of up to kRowLds floats are staged in LDS with coalesced
+// 16-byte loads (one workgroup per row) and each thread then selects one frame; longer rows are
+// read directly, one thread per (row, frame).
 // ---------------------------------------------------------------------------------------
+constexpr int kRowLds = 12288;
+
 template <int K>
-__global__ __launch_bounds__(256) void topk_scores_kernel(const float* __restrict__ s, int64_t nrows, int F, int C,
-                                                          int ke, int32_t* __restrict__ idx) {
-  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (gid >= nrows * F) return;
-  const int64_t row = gid / F;
-  const int f = (int)(gid % F);
-  const float* sp = s + row * ((int64_t)F * C) + (int64_t)f * C;
+__device__ inline void select_frame(const float* sp, int C, int f, int ke, int32_t* o) {
   uint64_t a[K];
 #pragma unroll
   for (int t = 0; t < K; ++t) a[t] = 0;
@@ -93,49 +109,106 @@ __global__ __launch_bounds__(256) void topk_scores_kernel(const float* __restric
     uint64_t x = ckey(sp[c], (uint32_t)c);
     if (x > a[K - 1]) topk_insert<K>(a, x);
   }
-  int32_t* o = idx + row * ((int64_t)F * ke) + (int64_t)f * ke;
 #pragma unroll
   for (int t = 0; t < K; ++t)
     if (t < ke) o[t] = a[t] ? (int32_t)(f * C + ckey_index(a[t])) : -1;
 }
 
-// ---------------------------------------------------------------------------------------
-// Fused block select from pooled Q/K: one workgroup per (head, query block); the pooled query
-// vector is broadcast from LDS, each thread scores one frame's candidates and keeps its top-k.
-// ---------------------------------------------------------------------------------------
 template <int K>
-__global__ __launch_bounds__(128) void block_select_frame_kernel(const float* __restrict__ pq,
+__global__ __launch_bounds__(256) void topk_scores_row_kernel(const float* __restrict__ s, int F, int C, int ke,
+                                                              int32_t* __restrict__ idx) {
+  __shared__ __align__(16) float row[kRowLds];
+  const int64_t r = blockIdx.x;
+  const int n = F * C;
+  const float* src = s + r * (int64_t)n;
+  if ((n & 3) == 0) {
+    for (int i = threadIdx.x; i < (n >> 2); i += 256)
+      reinterpret_cast<f32x4*>(row)[i] = reinterpret_cast<const f32x4*>(src)[i];
+  } else {
+    for (int i = threadIdx.x; i < n; i += 256) row[i] = src[i];
+  }
+  __syncthreads();
+  for (int f = threadIdx.x; f < F; f += 256)
+    select_frame<K>(row + f * C, C, f, ke, idx + r * ((int64_t)F * ke) + (int64_t)f * ke);
+}
+
+template <int K>
+__global__ __launch_bounds__(256) void topk_scores_kernel(const float* __restrict__ s, int64_t nrows, int F, int C,
+                                                          int ke, int32_t* __restrict__ idx) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= nrows * F) return;
+  const int64_t row = gid / F;
+  const int f = (int)(gid % F);
+  select_frame<K>(s + row * ((int64_t)F * C) + (int64_t)f * C, C, f, ke, idx + row * ((int64_t)F * ke) + (int64_t)f * ke);
+}
+
+// ---------------------------------------------------------------------------------------
+// Fused block select from pooled Q/K. A workgroup owns 256 query blocks of one head (one per
+// thread, its pooled vector in registers) and a range of key frames; each frame's pooled key
+// blocks are staged once in LDS (double-buffered) and read as broadcasts, every score is the
+// sequential fmaf chain over d = 0..63, and each thread keeps its top-k per frame.
+// ---------------------------------------------------------------------------------------
+constexpr int kSelFramesPerGroup = 8;
+
+template <int K>
+__global__ __launch_bounds__(256) void block_select_frame_kernel(const float* __restrict__ pq,
                                                                  const float* __restrict__ pk, int nbq, int F,
                                                                  int NBf, int ke, int32_t* __restrict__ idx) {
-  __shared__ float qv[64];
-  const int i = blockIdx.x, hs = blockIdx.y;
-  if (threadIdx.x < 64) qv[threadIdx.x] = pq[((int64_t)hs * nbq + i) * 64 + threadIdx.x];
-  __syncthreads();
+  __shared__ __align__(16) float kt[2][32 * 64];
+  const int hs = blockIdx.y;
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  const int f0 = blockIdx.z * kSelFramesPerGroup;
+  const int f1 = min(F, f0 + kSelFramesPerGroup);
+  const bool active = i < nbq;
+  float qv[64];
+  {
+    const f32x4* qr = reinterpret_cast<const f32x4*>(pq + ((int64_t)hs * nbq + (active ? i : 0)) * 64);
+#pragma unroll
+    for (int d4 = 0; d4 < 16; ++d4) {
+      const f32x4 x = qr[d4];
+      qv[4 * d4] = x[0];
+      qv[4 * d4 + 1] = x[1];
+      qv[4 * d4 + 2] = x[2];
+      qv[4 * d4 + 3] = x[3];
+    }
+  }
   const int64_t nbk = (int64_t)F * NBf;
   const float* kbase = pk + (int64_t)hs * nbk * 64;
-  int32_t* orow = idx + ((int64_t)hs * nbq + i) * ((int64_t)F * ke);
-  for (int f = threadIdx.x; f < F; f += blockDim.x) {
+  const int nvec = NBf * 16;  // f32x4 per frame
+  auto stage = [&](int f, int b) {
+    const f32x4* src = reinterpret_cast<const f32x4*>(kbase + (int64_t)f * NBf * 64);
+    for (int v = threadIdx.x; v < nvec; v += 256) reinterpret_cast<f32x4*>(kt[b])[v] = src[v];
+  };
+  stage(f0, 0);
+  __syncthreads();
+  int32_t* orow = idx + ((int64_t)hs * nbq + (active ? i : 0)) * ((int64_t)F * ke);
+  for (int f = f0; f < f1; ++f) {
+    const int b = (f - f0) & 1;
+    if (f + 1 < f1) stage(f + 1, b ^ 1);
     uint64_t a[K];
 #pragma unroll
     for (int t = 0; t < K; ++t) a[t] = 0;
     for (int c = 0; c < NBf; ++c) {
-      const f32x4* kr = reinterpret_cast<const f32x4*>(kbase + ((int64_t)f * NBf + c) * 64);
+      const f32x4* kr = reinterpret_cast<const f32x4*>(kt[b] + c * 64);
       float acc = 0.f;
 #pragma unroll
       for (int d4 = 0; d4 < 16; ++d4) {
-        f32x4 kv = kr[d4];
+        const f32x4 kv = kr[d4];
         acc = __builtin_fmaf(qv[4 * d4 + 0], kv[0], acc);
         acc = __builtin_fmaf(qv[4 * d4 + 1], kv[1], acc);
         acc = __builtin_fmaf(qv[4 * d4 + 2], kv[2], acc);
         acc = __builtin_fmaf(qv[4 * d4 + 3], kv[3], acc);
       }
-      uint64_t x = ckey(acc, (uint32_t)c);
+      const uint64_t x = ckey(acc, (uint32_t)c);
       if (x > a[K - 1]) topk_insert<K>(a, x);
     }
-    int32_t* o = orow + (int64_t)f * ke;
+    if (active) {
+      int32_t* o = orow + (int64_t)f * ke;
 #pragma unroll
-    for (int t = 0; t < K; ++t)
-      if (t < ke) o[t] = a[t] ? (int32_t)(f * NBf + ckey_index(a[t])) : -1;
+      for (int t = 0; t < K; ++t)
+        if (t < ke) o[t] = a[t] ? (int32_t)(f * NBf + ckey_index(a[t])) : -1;
+    }
+    __syncthreads();
   }
 }
 
@@ -204,9 +277,13 @@ int dispatch_k(int k, Args... args) {
 template <int K>
 struct TopkScoresLaunch {
   static int run(const float* s, int64_t nrows, int F, int C, int ke, int32_t* idx, hipStream_t st) {
-    int64_t n = nrows * F;
-    hipLaunchKernelGGL(topk_scores_kernel<K>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, s, nrows, F, C, ke,
-                       idx);
+    if ((int64_t)F * C <= kRowLds && nrows <= 0x7fffffff) {
+      hipLaunchKernelGGL(topk_scores_row_kernel<K>, dim3((unsigned)nrows), dim3(256), 0, st, s, F, C, ke, idx);
+    } else {
+      int64_t n = nrows * F;
+      hipLaunchKernelGGL(topk_scores_kernel<K>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, s, nrows, F, C,
+                         ke, idx);
+    }
     return check_launch("saf3r_topk_from_scores");
   }
 };
@@ -215,7 +292,8 @@ template <int K>
 struct SelectFrameLaunch {
   static int run(const float* pq, const float* pk, int n, int nbq, int F, int NBf, int ke, int32_t* idx,
                  hipStream_t st) {
-    hipLaunchKernelGGL(block_select_frame_kernel<K>, dim3(nbq, n), dim3(128), 0, st, pq, pk, nbq, F, NBf, ke, idx);
+    dim3 grid((nbq + 255) / 256, n, (F + kSelFramesPerGroup - 1) / kSelFramesPerGroup);
+    hipLaunchKernelGGL(block_select_frame_kernel<K>, grid, dim3(256), 0, st, pq, pk, nbq, F, NBf, ke, idx);
     return check_launch("saf3r_block_select");
   }
 };
@@ -253,7 +331,7 @@ extern "C" int saf3r_block_pool(const void* q_packed, const void* k_packed, int 
   p.pq = pooled_q;
   p.pk = pooled_k;
   p.nb = frames * p.g.NBf;
-  hipLaunchKernelGGL(block_pool_kernel, dim3((p.nb + 3) / 4, n_heads_sel), dim3(256), 0, (hipStream_t)stream, p);
+  hipLaunchKernelGGL(block_pool_kernel, dim3((p.nb + 31) / 32, n_heads_sel), dim3(256), 0, (hipStream_t)stream, p);
   return check_launch("saf3r_block_pool");
 }
 
@@ -277,6 +355,8 @@ extern "C" int saf3r_block_select(const float* pooled_q, const float* pooled_k, 
     return fail(SAF3R_ERR_INVALID, "saf3r_block_select: bad shape");
   if (k < 1 || k > 32) return fail(SAF3R_ERR_UNSUPPORTED, "saf3r_block_select: k must be in [1, 32] (got %d)", k);
   if (scope == 0) {
+    if (blocks_per_frame > 32)
+      return fail(SAF3R_ERR_UNSUPPORTED, "saf3r_block_select: per-frame scope supports at most 32 blocks per frame");
     int ke = k < blocks_per_frame ? k : blocks_per_frame;
     return dispatch_k<SelectFrameLaunch>(ke, pooled_q, pooled_k, n, nbq, frames, blocks_per_frame, ke, idx,
                                          (hipStream_t)stream);

@@ -59,6 +59,20 @@ def rope_inv_freq(base: float = 100.0, feature_dim: int = 32) -> torch.Tensor:
     return 1.0 / (base ** exponents)
 
 
+_rope_cache = {}
+
+
+def rope_tables(positions: int, base: float = 100.0, device="cuda"):
+    """cos / sin tables [positions, 16] fp32 of the 2-D RoPE for fp32 tokens, computed as
+    ``rope.py:100-115`` does (angles = position * inv_freq in fp32, then cos / sin), cached."""
+    key = (int(positions), float(base), str(device))
+    if key not in _rope_cache:
+        inv = rope_inv_freq(base)
+        ang = torch.arange(int(positions), dtype=torch.float32)[:, None] * inv[None, :]
+        _rope_cache[key] = (ang.cos().contiguous().to(device), ang.sin().contiguous().to(device))
+    return _rope_cache[key]
+
+
 def packed_buffers(geom: Geometry, num_heads: int, device) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     L = geom.slots
     q = torch.empty(num_heads, L, HEAD_DIM, dtype=torch.bfloat16, device=device)
@@ -68,9 +82,11 @@ def packed_buffers(geom: Geometry, num_heads: int, device) -> tuple[torch.Tensor
 
 
 def pack_qkv(q, k, v, tok_stride: int, head_stride: int, geom: Geometry, num_heads: int,
-             ln_q=None, ln_k=None, ln_eps: float = 1e-5, pos=None, inv_freq=None, out=None):
+             ln_q=None, ln_k=None, ln_eps: float = 1e-5, pos=None, rope_base=None, rope_positions=None, out=None):
     """QK-LayerNorm + RoPE-2D + packing (``saf3r_pack_qkv``). ``q``/``k``/``v`` are tensors (or
-    views) whose element (t, h, d) is at ``data_ptr + t*tok_stride + h*head_stride + d``."""
+    views) whose element (t, h, d) is at ``data_ptr + t*tok_stride + h*head_stride + d``.
+    RoPE is applied when ``rope_base`` is given; ``rope_positions`` is the table length
+    (default: max position + 1, which costs one device-to-host read)."""
     _need_cuda(q, k, v)
     lib = _lib.load()
     qp, kp, vp = out if out is not None else packed_buffers(geom, num_heads, q.device)
@@ -80,17 +96,19 @@ def pack_qkv(q, k, v, tok_stride: int, head_stride: int, geom: Geometry, num_hea
         kw, kb = (t.detach().float().contiguous() for t in ln_k)
     else:
         qw = qb = kw = kb = None
-    freq = None
-    if inv_freq is not None:
+    rc = rs = None
+    npos = 0
+    if rope_base is not None:
         if pos is None:
             raise ValueError("RoPE needs positions")
         pos = pos.to(device=q.device, dtype=torch.int32).contiguous()
-        f = inv_freq.detach().float().cpu().contiguous()
-        freq = (ctypes.c_float * 16)(*f.tolist())
+        npos = int(rope_positions) if rope_positions is not None else int(pos.max().item()) + 1
+        rc, rs = rope_tables(npos, rope_base, q.device)
     _lib.check(lib.saf3r_pack_qkv(
         _ptr(q), _ptr(k), _ptr(v), tok_stride, head_stride, geom.frames, geom.tokens_per_frame, geom.num_special,
         num_heads, _ptr(qw), _ptr(qb), _ptr(kw), _ptr(kb), float(ln_eps), int(apply_ln),
-        _ptr(pos) if freq is not None else None, freq, _ptr(qp), _ptr(kp), _ptr(vp), _lib.stream_ptr()))
+        _ptr(pos) if rc is not None else None, _ptr(rc), _ptr(rs), npos, _ptr(qp), _ptr(kp), _ptr(vp),
+        _lib.stream_ptr()))
     return qp, kp, vp
 
 

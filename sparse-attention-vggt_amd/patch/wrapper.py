@@ -104,12 +104,14 @@ class BaseHeadwiseSparseAttentionWrapper(nn.Module):
             eps = om.q_norm.eps
         elif not isinstance(om.q_norm, nn.Identity):
             raise NotImplementedError(f"q_norm {type(om.q_norm).__name__} is not LayerNorm / Identity")
-        inv_freq = p2 = None
+        base = p2 = npos = None
         if om.rope is not None and pos is not None:
-            inv_freq = ops.rope_inv_freq(float(om.rope.base_frequency))
+            base = float(om.rope.base_frequency)
             p2 = pos.reshape(-1, 2)
+            # table length: the patch grid bounds every position ((y+1, x+1) with specials at 0)
+            npos = max(self.patch_height, self.patch_width) + 1 if self.patch_height else None
         qp, kp, vp = ops.pack_qkv(qkv, qkv[:, C:], qkv[:, 2 * C:], 3 * C, HEAD_DIM, geom, H, ln_q=ln_q, ln_k=ln_k,
-                                  ln_eps=eps, pos=p2, inv_freq=inv_freq)
+                                  ln_eps=eps, pos=p2, rope_base=base, rope_positions=npos)
         sel = None
         if self.dyn_heads:
             pq, pk = ops.block_pool(qp, kp, geom, self.dyn_heads)

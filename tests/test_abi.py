@@ -52,7 +52,7 @@ def test_invalid_arguments_fail_before_launch(pkg):
     rc = lib.saf3r_block_select(ctypes.c_void_p(16), ctypes.c_void_p(16), 1, 4, 2, 2, 33, 0, ctypes.c_void_p(16), None)
     assert rc == 2  # k beyond the supported range
     rc = lib.saf3r_pack_qkv(None, None, None, 64, 64, 0, 10, 1, 1, None, None, None, None, 1e-5, 0, None, None,
-                            None, None, None, None)
+                            None, 0, None, None, None, None)
     assert rc == 1 and b"geometry" in lib.saf3r_last_error()
     with pytest.raises(L.Saf3rError):
         L.check(1)

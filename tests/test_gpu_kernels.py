@@ -68,7 +68,7 @@ def test_pack_layernorm_rope(ops, pkg):
     C = H * 64
     qp, kp, vp = ops.pack_qkv(d, d[:, C:], d[:, 2 * C:], 3 * C, 64, geom, H,
                               ln_q=[t.to(DEV) for t in lnq], ln_k=[t.to(DEV) for t in lnk], ln_eps=1e-5,
-                              pos=pos.to(DEV), inv_freq=ops.rope_inv_freq(100.0))
+                              pos=pos.to(DEV), rope_base=100.0)
     torch.cuda.synchronize()
     qr, kr, vr = OA.qkv_prologue(qkv, H, lnq, lnk, pos)
     toks = slot_tokens(geom.frames, geom.tokens_per_frame, 5)

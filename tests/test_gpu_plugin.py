@@ -68,7 +68,7 @@ def test_layer_matches_oracle_all_modes(mods, pkg):
             # exact q/k/v the kernels consumed (packing is deterministic)
             qp, kp, vp = ops.pack_qkv(qkv, qkv[:, dim:], qkv[:, 2 * dim:], 3 * dim, 64, geom, H,
                                       ln_q=(om.q_norm.weight, om.q_norm.bias), ln_k=(om.k_norm.weight, om.k_norm.bias),
-                                      pos=pos[0], inv_freq=ops.rope_inv_freq(100.0))
+                                      pos=pos[0], rope_base=100.0)
             torch.cuda.synchronize()
             q, _ = unpack_rows(qp.cpu(), toks, N)
             k, _ = unpack_rows(kp.cpu(), toks, N)
