@@ -18,6 +18,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import re
 import statistics
 import sys
 import time
@@ -123,6 +124,31 @@ def cpu_baseline(pkg, frames=4, heads=16, repeats=5, budget_s=25.0):
     }
 
 
+def calibrate_copy():
+    """A plain elementwise copy (negation) of 2^28 fp32 values: 1 GiB read and 1 GiB written once."""
+    dev = torch.device("cuda:0")
+    src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_kernel": "torch.neg fp32", "read_bytes": src.numel() * 4,
+                      "write_bytes": dst.numel() * 4, "launches": 3}), flush=True)
+
+
+def measured_traffic(kernel="sparse_attn_kernel"):
+    """HBM bytes per launch of the attention kernel at this workload, as recorded from the
+    FETCH_SIZE and WRITE_SIZE counter runs (scaled by the copy calibration) in the committed
+    traffic summary; None when that summary is absent."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic_vggt1b_global_f128.md")
+    try:
+        text = open(path).read()
+    except OSError:
+        return None
+    m = re.search(rf"^{kernel}_bytes_per_launch:\s*(\d+)", text, flags=re.M)
+    return int(m.group(1)) if m else None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -131,11 +157,18 @@ def main():
     ap.add_argument("--frames", type=int, default=128)
     ap.add_argument("--layers", type=int, default=24)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="run only a plain copy kernel of known size (reads 1 GiB, writes 1 GiB), for scaling "
+                         "the FETCH_SIZE / WRITE_SIZE counters of a profiling run")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU: --gpus {args.gpus} is not supported (the path is measured on one "
               "MI355X; multi-GPU sharding is design-only)", file=sys.stderr)
         sys.exit(2)
+
+    if args.calibrate_copy:
+        calibrate_copy()
+        return
 
     import importlib
     pkg = __graft_entry__.package()
@@ -238,7 +271,7 @@ def main():
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": None if attn_tflops is None else round(attn_tflops / PEAK_BF16_TFLOPS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(),
             "launch_ms": round(attn_ms_avg, 3),
         },
         "selection": dict(sel_extra, bound="hbm", peak=PEAK_HBM_GBS, unit="GB/s"),
