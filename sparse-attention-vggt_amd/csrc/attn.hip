@@ -14,18 +14,27 @@
 //   O^T (64 d    x 32 queries) += V^T . P^T  A = transposed V tile from LDS, B = P in registers
 // In the S^T accumulator a lane holds one query and 16 keys of every 32, so row max / row sum
 // need one cross-half exchange (v_permlane32_swap). Softmax uses base-2 exponentials against a
-// lazily moved reference maximum (O / l are rescaled only when the row maximum grows by more than
-// 2^8) and row sums are dot2 products of the bf16 P values that feed the PV product.
+// lazily moved reference maximum: no per-tile maximum is taken; the reference (and O, l) move only
+// when a tile's partial row sum exceeds 2^64. Row sums are dot2 products of the bf16 P values
+// that feed the PV product.
 //
 // Shared mode (dense, frame-local, anchor+local, anchor, special rows of the dynamic patterns):
 // a workgroup of four waves owns up to four consecutive query tiles with one key sequence. Full
 // key tiles (8 KB K + 8 KB transposed V) stream through a 4-stage LDS ring filled by
 // global_load_lds_dwordx4 (no register staging), two tiles per barrier; all four waves consume
-// each staged tile.
+// each staged tile. A wave issues its share of the next pair's loads right after the score MFMAs
+// of the current tile, so the memory-pipeline stall overlaps matrix work.
 // Split mode (patch rows of block-dynamic heads): a workgroup owns one query tile; its four waves
 // split the tile's block list into quarters and each streams its own 32-key half tiles through a
 // private 2-slot LDS ring (no barriers). Half tiles beyond a partial block's population are never
 // loaded. The four partial (max, sum, O) are merged through LDS at the end.
+// Phase alignment: work-groups start at scattered times, so if every one walked its key sequence
+// from the start, the tiles in use at any moment would span the whole head (45 MB at 128 frames)
+// and L2 (4 MB per XCD) would miss on most of them. Instead a work-group starts its walk (and wraps
+// around) at the position that the device's constant-rate clock, divided by the expected time per
+// step, points to: all resident work-groups then touch nearby key frames at the same moment. The
+// walk order changes only the summation order; the host can turn it off for run-to-run identical
+// output.
 #include "common.h"
 
 namespace saf3r {
@@ -46,6 +55,8 @@ struct AttnParams {
   Geom g;
   int sel_width;
   float c;  // softmax scale * log2(e)
+  uint64_t phase_dense;  // wall-clock ticks per key-tile step of a dense walk (0: fixed order)
+  uint64_t phase_split;  // wall-clock ticks per list position of a split-mode wave (0: fixed order)
   int n_order;
   int order[kMaxHeads];
   int item_start[kMaxHeads + 1];
@@ -102,67 +113,104 @@ struct TileMask {
 
 // One staged key tile (NKH = 2: 64 keys, K rows 128 B, V rows 128 B) or half tile (NKH = 1:
 // 32 keys, V rows 64 B); key0 is the first key of the staged keys within their 64-slot tile.
-template <int NKH>
+template <int NKH, typename Hook>
 __device__ __forceinline__ void attend(const char* __restrict__ kst, const char* __restrict__ vst,
                                        const bf16x8 (&qfrag)[2][4], Acc& A, const int (&frow)[2],
-                                       const TileMask& tm, const Geom& g, int key0, int half, int col, float c) {
+                                       const TileMask& tm, const Geom& g, int key0, int half, int col, float c,
+                                       Hook&& hook) {
   f32x16 s[NKH][2];
+  // S^T of the staged keys, masked; also re-run by the exact path below, which keeps s from
+  // having to stay live next to P
+  auto scores = [&]() {
 #pragma unroll
-  for (int kh = 0; kh < NKH; ++kh) s[kh][0] = s[kh][1] = f32x16{};
+    for (int kh = 0; kh < NKH; ++kh) s[kh][0] = s[kh][1] = f32x16{};
 #pragma unroll
-  for (int st = 0; st < 4; ++st) {
-    const int chn = 4 * half + st;
+    for (int st = 0; st < 4; ++st) {
+      const int chn = 4 * half + st;
 #pragma unroll
-    for (int kh = 0; kh < NKH; ++kh) {
-      const int r = 32 * kh + col;
-      const bf16x8 kf = *reinterpret_cast<const bf16x8*>(kst + r * 128 + ((chn ^ swz8(r)) << 4));
-      s[kh][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qfrag[0][st], s[kh][0], 0, 0, 0);
-      s[kh][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qfrag[1][st], s[kh][1], 0, 0, 0);
+      for (int kh = 0; kh < NKH; ++kh) {
+        const int r = 32 * kh + col;
+        const bf16x8 kf = *reinterpret_cast<const bf16x8*>(kst + r * 128 + ((chn ^ swz8(r)) << 4));
+        s[kh][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qfrag[0][st], s[kh][0], 0, 0, 0);
+        s[kh][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qfrag[1][st], s[kh][1], 0, 0, 0);
+      }
     }
-  }
-
-  if (tm.need) {
+    if (tm.need) {
 #pragma unroll
-    for (int kh = 0; kh < NKH; ++kh) {
+      for (int kh = 0; kh < NKH; ++kh) {
 #pragma unroll
-      for (int a = 0; a < 16; ++a) {
-        const int key = key0 + 32 * kh + 8 * (a >> 2) + 4 * half + (a & 3);
-        bool ok;
-        int fc;
-        if (tm.kspecial) {
-          const int sl = tm.kt * 64 + key;
-          ok = sl < g.S;
-          fc = sl / g.ns;
-        } else {
-          ok = key < tm.kvalid;
-          fc = tm.kframe;
-        }
+        for (int a = 0; a < 16; ++a) {
+          const int key = key0 + 32 * kh + 8 * (a >> 2) + 4 * half + (a & 3);
+          bool ok;
+          int fc;
+          if (tm.kspecial) {
+            const int sl = tm.kt * 64 + key;
+            ok = sl < g.S;
+            fc = sl / g.ns;
+          } else {
+            ok = key < tm.kvalid;
+            fc = tm.kframe;
+          }
 #pragma unroll
-        for (int gq = 0; gq < 2; ++gq) {
-          bool okg = ok;
-          if (tm.eff == SAF3R_FRAME_LOCAL) okg = okg && fc == frow[gq];
-          else if (tm.eff == SAF3R_ANCHOR_LOCAL) okg = okg && (fc == 0 || fc == frow[gq]);
-          else if (tm.eff == SAF3R_ANCHOR) okg = okg && fc == 0;
-          if (!okg) s[kh][gq][a] = -__builtin_inff();
+          for (int gq = 0; gq < 2; ++gq) {
+            bool okg = ok;
+            if (tm.eff == SAF3R_FRAME_LOCAL) okg = okg && fc == frow[gq];
+            else if (tm.eff == SAF3R_ANCHOR_LOCAL) okg = okg && (fc == 0 || fc == frow[gq]);
+            else if (tm.eff == SAF3R_ANCHOR) okg = okg && fc == 0;
+            if (!okg) s[kh][gq][a] = -__builtin_inff();
+          }
         }
       }
     }
-  }
+  };
+  scores();
+  // loads issued here wait in the memory pipeline while the score MFMAs execute
+  __builtin_amdgcn_sched_barrier(0);
+  hook();
+  __builtin_amdgcn_sched_barrier(0);
 
+  // P = exp2(s*c - m*c) against the row's reference maximum m, and this tile's partial row sums.
+  // m is raised only when a tile's partial sum exceeds 2^64 (the first tile of a row with an
+  // unmasked key, whose m is still -inf, always does): values up to 2^64 keep every bf16 P, every
+  // fp32 sum and O finite, so no per-tile maximum is needed. The exact path then takes the tile's
+  // row maximum, rescales O and l, and recomputes P.
   bf16x8 pf[2][2 * NKH];
+  float ts[2];
+  // row sums over the bf16-rounded P that the PV product uses, so l and O agree
   const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
+  auto exps = [&](int gq, float mc) {
+    float t = 0.f;
 #pragma unroll
-  for (int gq = 0; gq < 2; ++gq) {
-    float mx = fmaxf(s[0][gq][0], s[0][gq][1]);
+    for (int j = 0; j < 2 * NKH; ++j) {
+      const int a0 = 8 * (j & 1);
 #pragma unroll
-    for (int kh = 0; kh < NKH; ++kh)
+      for (int u = 0; u < 8; u += 2) {
+        const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[j >> 1][gq][a0 + u], c, -mc));
+        const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[j >> 1][gq][a0 + u + 1], c, -mc));
+        const bf16x2 pr = {(__bf16)e0, (__bf16)e1};
+        pf[gq][j][u] = pr[0];
+        pf[gq][j][u + 1] = pr[1];
+        t = __builtin_amdgcn_fdot2_f32_bf16(pr, ones, t, false);
+      }
+    }
+    ts[gq] = t;
+  };
+  // a row without a reference yet uses -2^127: unmasked keys then give +inf (and the exact
+  // path), masked keys 0, and no inf - inf (NaN) ever forms
 #pragma unroll
-      for (int a = (kh ? 0 : 2); a < 16; a += 2) mx = fmaxf(mx, fmaxf(s[kh][gq][a], s[kh][gq][a + 1]));
-    mx = partner_max(mx);
-    const bool need = mx * c > A.m[gq] * c + 8.0f;
-    if (__ballot(need) != 0) {
-      const float m_new = need ? mx : A.m[gq];
-      const float alpha = need ? __builtin_amdgcn_exp2f((A.m[gq] - m_new) * c) : 1.0f;
+  for (int gq = 0; gq < 2; ++gq) exps(gq, A.m[gq] == -__builtin_inff() ? -0x1p127f : A.m[gq] * c);
+  if (__ballot(ts[0] > 0x1p64f || ts[1] > 0x1p64f) != 0) {
+    scores();
+#pragma unroll
+    for (int gq = 0; gq < 2; ++gq) {
+      float mx = s[0][gq][0];
+#pragma unroll
+      for (int kh = 0; kh < NKH; ++kh)
+#pragma unroll
+        for (int a = 0; a < 16; ++a) mx = fmaxf(mx, s[kh][gq][a]);
+      mx = partner_max(mx);
+      const float m_new = fmaxf(A.m[gq], mx);
+      const float alpha = A.m[gq] == -__builtin_inff() ? 0.f : __builtin_amdgcn_exp2f((A.m[gq] - m_new) * c);
       A.l[gq] *= alpha;
 #pragma unroll
       for (int a = 0; a < 16; ++a) {
@@ -170,22 +218,11 @@ __device__ __forceinline__ void attend(const char* __restrict__ kst, const char*
         A.o[1][gq][a] *= alpha;
       }
       A.m[gq] = m_new;
-    }
-    const float mc = A.m[gq] == -__builtin_inff() ? 0.f : A.m[gq] * c;
-#pragma unroll
-    for (int j = 0; j < 2 * NKH; ++j) {
-      const int a0 = 8 * (j & 1);
-#pragma unroll
-      for (int t = 0; t < 8; t += 2) {
-        const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[j >> 1][gq][a0 + t], c, -mc));
-        const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[j >> 1][gq][a0 + t + 1], c, -mc));
-        const bf16x2 pr = {(__bf16)e0, (__bf16)e1};
-        pf[gq][j][t] = pr[0];
-        pf[gq][j][t + 1] = pr[1];
-        A.l[gq] = __builtin_amdgcn_fdot2_f32_bf16(pr, ones, A.l[gq], false);
-      }
+      exps(gq, m_new == -__builtin_inff() ? 0.f : m_new * c);
     }
   }
+  A.l[0] += ts[0];
+  A.l[1] += ts[1];
 
 #pragma unroll
   for (int j = 0; j < 2 * NKH; ++j) {
@@ -201,27 +238,29 @@ __device__ __forceinline__ void attend(const char* __restrict__ kst, const char*
   }
 }
 
-// Key-tile sequence of a shared-mode group: up to four contiguous ranges.
+// Key-tile sequence of a shared-mode group: four contiguous ranges (some possibly empty), walked
+// from step rot. Fixed fields only: a range array indexed at run time would live in scratch.
 struct TileSeq {
   int s0, l0, s1, l1, s2, l2, s3, l3;
-  int nr;
   int count;
+  int rot;
+  __device__ inline void set(int a0, int b0, int a1, int b1, int a2, int b2, int a3, int b3) {
+    s0 = a0; l0 = max(b0, 0);
+    s1 = a1; l1 = max(b1, 0);
+    s2 = a2; l2 = max(b2, 0);
+    s3 = a3; l3 = max(b3, 0);
+    count = l0 + l1 + l2 + l3;
+    rot = 0;
+  }
   __device__ inline int at(int n) const {
+    n += rot;
+    if (n >= count) n -= count;
     if (n < l0) return s0 + n;
     n -= l0;
     if (n < l1) return s1 + n;
     n -= l1;
     if (n < l2) return s2 + n;
     return s3 + (n - l2);
-  }
-  __device__ inline void add(int s, int l) {
-    if (l <= 0) return;
-    if (nr == 0) { s0 = s; l0 = l; }
-    else if (nr == 1) { s1 = s; l1 = l; }
-    else if (nr == 2) { s2 = s; l2 = l; }
-    else { s3 = s; l3 = l; }
-    ++nr;
-    count += l;
   }
 };
 
@@ -366,35 +405,39 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
   if (kind == kShared) {
     // ---- key-tile sequence (uniform) ----
     TileSeq seq;
-    seq.s0 = seq.s1 = seq.s2 = seq.s3 = 0;
-    seq.l0 = seq.l1 = seq.l2 = seq.l3 = 0;
-    seq.nr = 0;
-    seq.count = 0;
     bool frame_rel = false;
     const int eff = (pat == SAF3R_DENSE || pat == SAF3R_TOKEN_DYNAMIC || pat == SAF3R_BLOCK_DYNAMIC) ? SAF3R_DENSE : pat;
     if (eff == SAF3R_DENSE) {
-      seq.add(0, g.NT);
+      seq.set(0, g.NT, 0, 0, 0, 0, 0, 0);
     } else {
       frame_rel = true;
-      int f0 = qf, f1 = qf;
-      if (qspecial) {
-        const int last = min(g.S, (qt + 1) * 64) - 1;
-        f0 = (qt * 64) / g.ns;
+      int f0, f1;
+      if (qt0 < g.nst) {
+        const int last = min(g.S, (qt0 + nw) * 64) - 1;
+        f0 = (qt0 * 64) / g.ns;
         f1 = last / g.ns;
+      } else {
+        f0 = f1 = (qt0 - g.nst) / g.NBf;
       }
       const bool need_anchor = (pat == SAF3R_ANCHOR_LOCAL || pat == SAF3R_ANCHOR);
       const bool need_local = (pat != SAF3R_ANCHOR);
-      int ls0 = 1, ls1 = 0;
-      if (g.ns > 0 && need_local) {
-        ls0 = (f0 * g.ns) / 64;
-        ls1 = ((f1 + 1) * g.ns - 1) / 64;
-      }
-      if (g.ns > 0 && need_anchor && !(need_local && ls0 == 0)) seq.add(0, (g.ns - 1) / 64 + 1);
-      if (g.ns > 0 && need_local) seq.add(ls0, ls1 - ls0 + 1);
-      if (need_anchor && !(need_local && f0 == 0)) seq.add(g.nst, g.NBf);
-      if (need_local) seq.add(g.nst + f0 * g.NBf, (f1 - f0 + 1) * g.NBf);
+      const bool has_sp = g.ns > 0;
+      const int ls0 = has_sp ? (f0 * g.ns) / 64 : 0;
+      const int ls1 = has_sp ? ((f1 + 1) * g.ns - 1) / 64 : -1;
+      const bool anc_sp = has_sp && need_anchor && !(need_local && ls0 == 0);
+      const bool anc_pt = need_anchor && !(need_local && f0 == 0);
+      seq.set(0, anc_sp ? (g.ns - 1) / 64 + 1 : 0,
+              ls0, (has_sp && need_local) ? ls1 - ls0 + 1 : 0,
+              g.nst, anc_pt ? g.NBf : 0,
+              g.nst + f0 * g.NBf, need_local ? (f1 - f0 + 1) * g.NBf : 0);
     }
     const int count = seq.count;
+    if (eff == SAF3R_DENSE && p.phase_dense > 0) {
+      // one clock reading per work-group: the four waves share the ring and must agree
+      if (tid == 0) wcnt[0] = (int)((wall_clock64() / p.phase_dense) % (uint64_t)count);
+      __syncthreads();
+      seq.rot = wcnt[0];
+    }
 
     // thread tid owns 16-byte chunks tid and tid + 256 of the K and the V tile; LDS chunk
     // position P holds row P/8, global chunk (P % 8) ^ swz8(row)
@@ -421,9 +464,11 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
     for (int n = 0; n < count; n += 2) {
       wait_vm<0>();
       barrier_only();
-      if (n + 2 < count) issue(n + 2);
-      if (n + 3 < count) issue(n + 3);
-      if (!wactive) continue;
+      if (!wactive) {
+        if (n + 2 < count) issue(n + 2);
+        if (n + 3 < count) issue(n + 3);
+        continue;
+      }
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
         if (n + u < count) {
@@ -431,7 +476,11 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
           TileMask tm;
           tile_mask(g, kt, eff, frame_rel, qspecial, tm);
           const char* kst = ring + ((n + u) % kStages) * 16384;
-          attend<2>(kst, kst + 8192, qfrag, A, frow, tm, g, 0, half, col, c);
+          attend<2>(kst, kst + 8192, qfrag, A, frow, tm, g, 0, half, col, c, [&]() {
+            if (n + 2 + u < count) issue(n + 2 + u);
+          });
+        } else if (n + 2 + u < count) {
+          issue(n + 2 + u);
         }
       }
     }
@@ -459,7 +508,17 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
       __syncthreads();
     }
     total = min(total, kMaxList);
-    const int pos0 = (total * w) >> 2, pos1 = (total * (w + 1)) >> 2;
+    // wave w takes list positions w, w + 4, w + 8, ...: with lists in frame-major order, the four
+    // waves (and, through the clock phase, every resident work-group) advance through the key
+    // frames together
+    const int nw = total > w ? (total - w + 3) >> 2 : 0;
+    int i0 = 0;
+    if (p.phase_split > 0 && nw > 0) i0 = (int)((wall_clock64() / p.phase_split) % (uint64_t)nw);
+    auto list_pos = [&](int i) {
+      int ii = i + i0;
+      if (ii >= nw) ii -= nw;
+      return w + 4 * ii;
+    };
 
     // half-tile stream of this wave: (list position, half); a half is present when its first key
     // is a valid key of the block
@@ -482,18 +541,19 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
     };
 
     wait_vm<0>();
-    int pos = pos0, hh = 0, cur = 0;
-    if (pos < pos1) issue(pos, hh, 0);
-    while (pos < pos1) {
-      int npos = pos, nhh = hh;
+    int i = 0, hh = 0, cur = 0;
+    if (nw > 0) issue(list_pos(0), 0, 0);
+    while (i < nw) {
+      const int pos = list_pos(i);
+      int ni = i, nhh;
       if (hh == 0 && half_valid(list[pos], 1)) nhh = 1;
       else {
         nhh = 0;
-        ++npos;
+        ++ni;
       }
-      const bool more = npos < pos1;
+      const bool more = ni < nw;
       if (more) {
-        issue(npos, nhh, cur ^ 1);
+        issue(list_pos(ni), nhh, cur ^ 1);
         wait_vm<8>();
       } else {
         wait_vm<0>();
@@ -503,8 +563,8 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
       tile_mask(g, kt, SAF3R_DENSE, false, false, tm);
       tm.need = tm.kvalid < 32 * (hh + 1);
       const char* st = slots + cur * 8192;
-      attend<1>(st, st + 4096, qfrag, A, frow, tm, g, 32 * hh, half, col, c);
-      pos = npos;
+      attend<1>(st, st + 4096, qfrag, A, frow, tm, g, 32 * hh, half, col, c, []() {});
+      i = ni;
       hh = nhh;
       cur ^= 1;
     }
@@ -604,6 +664,30 @@ static int64_t item_cost(int pat, const Geom& g, int sel_width) {
   }
 }
 
+// Clock phases of the key walks. Defaults are the measured time per step at the 128-frame VGGT
+// shape; SAF3R_ATTN_PHASE="off" keeps the fixed walk order (run-to-run identical output), and
+// SAF3R_ATTN_PHASE="<dense ns>,<split ns>" overrides the step times.
+static void set_phase(AttnParams* p) {
+  double dense_ns = 2600.0, split_ns = 3000.0;
+  if (const char* e = getenv("SAF3R_ATTN_PHASE")) {
+    if (strcmp(e, "off") == 0) dense_ns = split_ns = 0.0;
+    else if (sscanf(e, "%lf,%lf", &dense_ns, &split_ns) != 2) dense_ns = split_ns = 0.0;
+  }
+  static int rate_khz[64];  // per device; 0 = not queried yet, -1 = unavailable
+  int dev = 0, khz = 0;
+  if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64) {
+    if (rate_khz[dev] == 0) {
+      int r = 0;
+      rate_khz[dev] = hipDeviceGetAttribute(&r, hipDeviceAttributeWallClockRate, dev) == hipSuccess && r > 0 ? r : -1;
+    }
+    khz = rate_khz[dev] > 0 ? rate_khz[dev] : 0;
+  }
+  const double ticks_per_ns = khz * 1e-6;
+  p->phase_dense = dense_ns > 0.0 ? (uint64_t)fmax(1.0, dense_ns * ticks_per_ns) : 0;
+  p->phase_split = split_ns > 0.0 ? (uint64_t)fmax(1.0, split_ns * ticks_per_ns) : 0;
+  if (khz == 0) p->phase_dense = p->phase_split = 0;
+}
+
 }  // namespace saf3r
 
 using namespace saf3r;
@@ -644,6 +728,7 @@ extern "C" int saf3r_sparse_attn_fwd(const void* q_packed, const void* k_packed,
   p.out = (__bf16*)out;
   p.out_stride = out_row_stride;
   p.c = scale * 1.4426950408889634f;
+  set_phase(&p);
   int idx[kMaxHeads];
   for (int h = 0; h < num_heads; ++h) idx[h] = h;
   for (int i = 1; i < num_heads; ++i) {
