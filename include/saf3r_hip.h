@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define SAF3R_ABI_VERSION 1
+#define SAF3R_ABI_VERSION 2
 
 enum saf3r_status {
   SAF3R_OK = 0,
@@ -57,7 +57,15 @@ enum saf3r_pattern {
   SAF3R_TOKEN_DYNAMIC = 4, /* reference dino_topk: special rows attend every key (this entry);
                               patch rows go through saf3r_gather_attn_fwd.  ref: sparse_attention.py:189-231 */
   SAF3R_ANCHOR = 5,        /* frame(j) == 0.                      ref: sparse_attention.py:134-140 (all_to_first) */
-  SAF3R_SKIP = 6           /* output zero.                        ref: sparse_attention.py:40-41 */
+  SAF3R_SKIP = 6,          /* output zero.                        ref: sparse_attention.py:40-41 */
+  SAF3R_KEYSET = 7         /* j in the head's shared key set (saf3r_keyset_build / _gather).
+                              ref: sparse_attention.py:256-273 (stride), :143-186 (q_probe_topk) */
+};
+
+/* Key-set kinds of saf3r_keyset_build. */
+enum saf3r_keyset_mode {
+  SAF3R_KEYSET_STRIDE = 0, /* tokens start, start + stride, ...      ref: sparse_attention.py:256-273 */
+  SAF3R_KEYSET_TOPK = 1    /* the k best probe scores, ties to the lower token. ref: :143-186 */
 };
 
 /* Row addressing of a token-row buffer: logical row r lives at
@@ -136,6 +144,48 @@ int saf3r_block_select(const float* pooled_q, const float* pooled_k, int n, int 
                        int blocks_per_frame, int k, int scope, int32_t* idx, void* stream);
 
 /*
+ * Mean query and probe scores of the q_probe_topk key set, for n_sel heads (head_ids, device
+ * int32) of the packed Q/K.
+ *   qbar[s][d]: mean over all N = frames*tokens_per_frame tokens: chunks of ceil(N/256) tokens
+ *               summed sequentially in token order, chunk sums added in order, one division by N.
+ *   scores[s][t] (row stride scores_stride >= N, token order): sequential fmaf over d of
+ *               qbar[d] * k[t][d], times scale (1/8 for head_dim 64).
+ *   partial: device workspace of n_sel * 256 * 64 floats.
+ * Replaces: saf3r/patch/sparse_attention.py:160-168 (q_bar and the probe scores).
+ */
+int saf3r_probe_scores(const void* q_packed, const void* k_packed, int frames, int tokens_per_frame,
+                       int num_special, const int32_t* head_ids, int n_sel, float scale, float* partial,
+                       float* qbar, float* scores, int64_t scores_stride, void* stream);
+
+/*
+ * Shared key sets of n_heads heads (device int32 arrays of n_heads entries each):
+ *   mode SAF3R_KEYSET_STRIDE: tokens t >= start with (t - start) % param == 0;
+ *   mode SAF3R_KEYSET_TOPK:   the min(param, N) best scores[h][t] (row stride scores_stride),
+ *                             ties to the lower token;
+ *   include != 0: plus every token of frame 0 and every special token.
+ *   idx[h] (row stride idx_stride >= N): the members in increasing token order; count[h]: their number.
+ * Replaces: saf3r/patch/sparse_attention.py:170-178 (topk + unique) and :262-269 (strided + unique).
+ */
+int saf3r_keyset_build(const float* scores, int64_t scores_stride, int n_heads, const int32_t* mode,
+                       const int32_t* param, const int32_t* start, const int32_t* include, int frames,
+                       int tokens_per_frame, int num_special, int32_t* idx, int64_t idx_stride, int32_t* count,
+                       void* stream);
+
+/*
+ * Compact K/V of the key sets, in the layout SAF3R_KEYSET heads read: for set s (head head_ids[s]),
+ *   keyset_k: bf16 [n_sel][capacity][64], row j = packed K of token idx[s][j];
+ *   keyset_v: bf16 [n_sel][capacity/64] transposed, permuted 64x64 tiles (as packed V) of the
+ *             natural V rows v[t*v_tok_stride + h*v_head_stride + d].
+ *   Tiles below ceil(count[s]/64) (at most max_tiles, max_tiles*64 <= capacity) are written,
+ *   rows at or beyond count[s] as zeros.
+ * Replaces: saf3r/patch/sparse_attention.py:181-182, :271-272 (k/v[:, :, idx, :]).
+ */
+int saf3r_keyset_gather(const void* k_packed, int frames, int tokens_per_frame, int num_special,
+                        const int32_t* head_ids, int n_sel, const void* v, int64_t v_tok_stride,
+                        int64_t v_head_stride, const int32_t* idx, int64_t idx_stride, const int32_t* count,
+                        int max_tiles, void* keyset_k, void* keyset_v, int64_t capacity, void* stream);
+
+/*
  * Block-sparse attention forward over the packed layout, every head in one launch.
  *   head_pattern: host int32 [num_heads] of saf3r_pattern ids.
  *   sel: int32 [n_block_dynamic][F*NBf][sel_width] block ids (-1 = empty), one list per
@@ -143,14 +193,19 @@ int saf3r_block_select(const float* pooled_q, const float* pooled_k, int n, int 
  *   out: bf16 natural layout, element (token t, head h, d) at out[t*out_row_stride + h*64 + d].
  *        TOKEN_DYNAMIC heads get only their special rows written here.
  *   scale: softmax scale (1/8 for head_dim 64).
+ *   keyset_k / keyset_v / keyset_count / keyset_capacity: the saf3r_keyset_gather buffers of the
+ *        KEYSET heads, set s serving the s-th KEYSET head in increasing head order; every query of
+ *        such a head attends keys 0 .. keyset_count[s]-1. NULL / 0 when no head is KEYSET.
  * Replaces: the per-head loop saf3r/patch/wrapper.py:94-106 and the mode implementations of
- *           saf3r/patch/sparse_attention.py:12-90 for full / global_to_frame / all_to_first / skip,
- *           the dense special rows of dino_topk (:197-208), and the block-dynamic pattern.
+ *           saf3r/patch/sparse_attention.py:12-90 for full / global_to_frame / all_to_first / skip /
+ *           stride / q_probe_topk (over their key sets), the dense special rows of dino_topk
+ *           (:197-208), and the block-dynamic pattern.
  */
 int saf3r_sparse_attn_fwd(const void* q_packed, const void* k_packed, const void* v_packed, int frames,
                           int tokens_per_frame, int num_special, int num_heads, const int32_t* head_pattern,
                           const int32_t* sel, int sel_width, float scale, void* out, int64_t out_row_stride,
-                          void* stream);
+                          const void* keyset_k, const void* keyset_v, const int32_t* keyset_count,
+                          int64_t keyset_capacity, void* stream);
 
 /*
  * Gather attention: out[r] = sum_j softmax_j(q[r] . k[idx[r][j]] * scale) v[idx[r][j]], fp32

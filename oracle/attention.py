@@ -20,6 +20,9 @@ Patterns (per head; mask M[i, j] = 1 iff query i may attend key j):
                  ``saf3r/triton/sparse_topk_attention.py:36-112``)
   ANCHOR         frame(j) == 0 (``all_to_first``, ``:134-140``)
   SKIP           output zero (``:40-41``)
+  KEYSET         j in one key set shared by every query of the head (``stride``, ``:256-273``;
+                 ``q_probe_topk``, ``:143-186``; the set itself comes from
+                 ``oracle.selection.keyset``)
 Scores are q.k / sqrt(d); softmax in the working precision; rows are independent.
 """
 from __future__ import annotations
@@ -29,7 +32,7 @@ from dataclasses import dataclass
 
 import torch
 
-DENSE, FRAME_LOCAL, ANCHOR_LOCAL, BLOCK_DYNAMIC, TOKEN_DYNAMIC, ANCHOR, SKIP = range(7)
+DENSE, FRAME_LOCAL, ANCHOR_LOCAL, BLOCK_DYNAMIC, TOKEN_DYNAMIC, ANCHOR, SKIP, KEYSET = range(8)
 
 
 @dataclass(frozen=True)
@@ -88,6 +91,11 @@ def allowed_mask(pattern: int, rows: torch.Tensor, g: Geometry, sel: torch.Tenso
         return (fq[:, None] == frame[None, :]) | (frame[None, :] == 0)
     if pattern == ANCHOR:
         return (frame[None, :] == 0).expand(len(rows), n).clone()
+    if pattern == KEYSET:
+        assert sel is not None, "KEYSET needs the key set (token ids) as sel"
+        member = torch.zeros(n, dtype=torch.bool)
+        member[torch.as_tensor(sel).long()] = True
+        return member[None, :].expand(len(rows), n).clone()
     if pattern == BLOCK_DYNAMIC:
         assert sel is not None
         m = torch.zeros(len(rows), n, dtype=torch.bool)
@@ -216,6 +224,11 @@ def sparse_attention_gathered(q, k, v, pattern, g: Geometry, sel=None, dtype=tor
                     c0 = cbb * g.block
                     keys.append(torch.arange(cf * T + g.num_special + c0, cf * T + g.num_special + min(P, c0 + g.block)))
                 attend(rows, torch.cat(keys))
+        return out
+    if pattern == KEYSET:
+        keys = torch.as_tensor(sel).long()
+        for s0 in range(0, n, chunk):
+            attend(slice(s0, min(n, s0 + chunk)), keys)
         return out
     raise ValueError(f"pattern {pattern} has no gathered form")
 

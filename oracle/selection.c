@@ -27,6 +27,7 @@
  */
 #include <math.h>
 #include <stdint.h>
+#include <stdlib.h>
 #include <string.h>
 
 /* fp32 bits -> unsigned key whose integer order is the float order.
@@ -160,4 +161,95 @@ int oracle_global_topk(const float* scores, int NQ, int NC, int k, int32_t* out)
         for (int t = 0; t < ke; ++t) out[(int64_t)i * ke + t] = t < n ? ids[t] : -1;
     }
     return 0;
+}
+
+/* ----------------------------------------------------------------------------------------
+ * Shared key sets of the `stride` and `q_probe_topk` modes.
+ *   saf3r/patch/sparse_attention.py:143-186 (q_probe_topk_attention: mean query over all
+ *     tokens, scores = qbar . k / sqrt(D) in fp32, top-k keys, optional union with the
+ *     anchor-frame + special indices, sorted unique key set, dense attention over it),
+ *   :256-273 (stride_attention: keys start, start + stride, ..., union, unique),
+ *   :56-85 (dispatch: q_probe topk = N // stride when the group has a stride, else
+ *     min(topk, N); include_as defaults False for q_probe and True for stride;
+ *     start = head % stride when shift is set).
+ * The operation order below is the one the HIP kernels follow.
+ * ---------------------------------------------------------------------------------------- */
+
+/* Tokens per partial sum of the mean query: the N tokens split into at most 256 chunks. */
+int oracle_probe_chunk(int N) { return (N + 255) / 256; }
+
+/* Mean query of one head. q: bf16 bits, natural token order, row stride `row_stride`.
+ * For each feature: each chunk of R = oracle_probe_chunk(N) consecutive tokens is summed
+ * sequentially (fp32 adds, token order), the chunk sums are added sequentially in chunk
+ * order, and the total is divided once by N. */
+void oracle_probe_mean(const uint16_t* q, int64_t row_stride, int N, int D, float* out) {
+    const int R = oracle_probe_chunk(N);
+    for (int d = 0; d < D; ++d) {
+        float total = 0.0f;
+        for (int c0 = 0; c0 < N; c0 += R) {
+            float part = 0.0f;
+            const int c1 = c0 + R < N ? c0 + R : N;
+            for (int t = c0; t < c1; ++t) part = part + bf16_to_f32(q[(int64_t)t * row_stride + d]);
+            total = total + part;
+        }
+        out[d] = total / (float)N;
+    }
+}
+
+/* Probe scores of one head: score[t] = (sequential fmaf over d of qbar[d] * k[t][d]) * scale,
+ * with scale = 1/sqrt(D) (a power of two for D = 64, so the product is exact). */
+void oracle_probe_scores(const float* qbar, const uint16_t* k, int64_t row_stride, int N, int D, float scale,
+                         float* out) {
+    for (int t = 0; t < N; ++t) {
+        float acc = 0.0f;
+        for (int d = 0; d < D; ++d) acc = fmaf(qbar[d], bf16_to_f32(k[(int64_t)t * row_stride + d]), acc);
+        out[t] = acc * scale;
+    }
+}
+
+static int cmp_u64_desc(const void* a, const void* b) {
+    uint64_t x = *(const uint64_t*)a, y = *(const uint64_t*)b;
+    return x < y ? 1 : (x > y ? -1 : 0);
+}
+
+/*
+ * Sorted key set of one head over N = F*T tokens.
+ *   mode 0 (stride): token t is in if t >= start and (t - start) % param == 0.
+ *   mode 1 (top-k):  the param best tokens by (key(score) descending, index ascending),
+ *                    i.e. ties go to the lower index; param >= N takes every token.
+ *   include != 0:    every token of frame 0 and every special token (t % T < ns) is in.
+ * out receives the member tokens in increasing order; returns their number (or < 0).
+ */
+int oracle_keyset(const float* scores, int N, int T, int ns, int mode, int param, int start, int include,
+                  int32_t* out) {
+    if (N <= 0 || T <= 0 || param <= 0) return -1;
+    unsigned char* in = (unsigned char*)calloc((size_t)N, 1);
+    if (!in) return -2;
+    if (mode == 0) {
+        for (int t = start; t < N; t += param) in[t] = 1;
+    } else if (mode == 1) {
+        int k = param < N ? param : N;
+        uint64_t* ck = (uint64_t*)malloc((size_t)N * sizeof(uint64_t));
+        if (!ck) {
+            free(in);
+            return -2;
+        }
+        for (int t = 0; t < N; ++t) ck[t] = ((uint64_t)fkey_of(scores[t]) << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)t);
+        qsort(ck, (size_t)N, sizeof(uint64_t), cmp_u64_desc);
+        for (int i = 0; i < k; ++i) in[0xFFFFFFFFu - (uint32_t)(ck[i] & 0xFFFFFFFFu)] = 1;
+        free(ck);
+    } else {
+        free(in);
+        return -1;
+    }
+    if (include) {
+        for (int t = 0; t < N && t < T; ++t) in[t] = 1;
+        for (int t = 0; t < N; ++t)
+            if (t % T < ns) in[t] = 1;
+    }
+    int n = 0;
+    for (int t = 0; t < N; ++t)
+        if (in[t]) out[n++] = t;
+    free(in);
+    return n;
 }

@@ -4,7 +4,8 @@ TEST INFRASTRUCTURE ONLY (see ``oracle/__init__.py``).
 
 Reference anchors: ``saf3r/triton/topk_utils.py:26-29`` (sortable key),
 ``saf3r/triton/fused_qk_topk.py:73-100`` (composite key, tie rule, frame-major output),
-``saf3r/patch/adaptive_block_value.py:16-24`` (population-weighted block mean).
+``saf3r/patch/adaptive_block_value.py:16-24`` (population-weighted block mean),
+``saf3r/patch/sparse_attention.py:143-186, 256-273`` (q_probe / stride key sets).
 """
 from __future__ import annotations
 
@@ -42,6 +43,14 @@ def _load():
         lib.oracle_frame_topk.restype = i32
         lib.oracle_global_topk.argtypes = [p, i32, i32, i32, p]
         lib.oracle_global_topk.restype = i32
+        lib.oracle_probe_chunk.argtypes = [i32]
+        lib.oracle_probe_chunk.restype = i32
+        lib.oracle_probe_mean.argtypes = [p, i64, i32, i32, p]
+        lib.oracle_probe_mean.restype = None
+        lib.oracle_probe_scores.argtypes = [p, p, i64, i32, i32, ctypes.c_float, p]
+        lib.oracle_probe_scores.restype = None
+        lib.oracle_keyset.argtypes = [p, i32, i32, i32, i32, i32, i32, i32, p]
+        lib.oracle_keyset.restype = i32
         _lib = lib
     return _lib
 
@@ -129,3 +138,42 @@ def block_select(q_bf16: np.ndarray, k_bf16: np.ndarray, frames: int, tokens_per
     if scope == "frame":
         return frame_topk(s, frames, topk)
     return global_topk(s, topk)
+
+
+KEYSET_STRIDE, KEYSET_TOPK = 0, 1
+
+
+def probe_chunk(n: int) -> int:
+    return int(_load().oracle_probe_chunk(n))
+
+
+def probe_mean(q_bf16: np.ndarray) -> np.ndarray:
+    """Mean query of one head over all tokens; ``q_bf16`` uint16 [N, D] in token order."""
+    q = np.ascontiguousarray(q_bf16, dtype=np.uint16)
+    n, d = q.shape
+    out = np.zeros(d, dtype=np.float32)
+    _load().oracle_probe_mean(_ptr(q), d, n, d, _ptr(out))
+    return out
+
+
+def probe_scores(qbar: np.ndarray, k_bf16: np.ndarray, scale: float | None = None) -> np.ndarray:
+    """score[t] = sequential-fmaf(qbar . k[t]) * scale (scale defaults to 1/sqrt(D))."""
+    qb = np.ascontiguousarray(qbar, dtype=np.float32)
+    k = np.ascontiguousarray(k_bf16, dtype=np.uint16)
+    n, d = k.shape
+    out = np.zeros(n, dtype=np.float32)
+    sc = float(np.float32(1.0 / np.sqrt(d))) if scale is None else float(scale)
+    _load().oracle_probe_scores(_ptr(qb), _ptr(k), d, n, d, sc, _ptr(out))
+    return out
+
+
+def keyset(scores, n: int, tokens_per_frame: int, num_special: int, mode: int, param: int, start: int = 0,
+           include: bool = False) -> np.ndarray:
+    """Sorted key set of one head (see ``oracle_keyset``); ``scores`` may be None for mode 0."""
+    s = np.zeros(1, dtype=np.float32) if scores is None else np.ascontiguousarray(scores, dtype=np.float32)
+    out = np.zeros(n, dtype=np.int32)
+    cnt = _load().oracle_keyset(_ptr(s), n, tokens_per_frame, num_special, mode, param, start, int(bool(include)),
+                                _ptr(out))
+    if cnt < 0:
+        raise ValueError(f"oracle_keyset failed ({cnt})")
+    return out[:cnt].copy()

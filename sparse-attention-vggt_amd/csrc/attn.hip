@@ -35,6 +35,8 @@
 // step, points to: all resident work-groups then touch nearby key frames at the same moment. The
 // walk order changes only the summation order; the host can turn it off for run-to-run identical
 // output.
+#include <type_traits>
+
 #include "common.h"
 
 namespace saf3r {
@@ -57,6 +59,10 @@ struct AttnParams {
   float c;  // softmax scale * log2(e)
   uint64_t phase_dense;  // wall-clock ticks per key-tile step of a dense walk (0: fixed order)
   uint64_t phase_split;  // wall-clock ticks per list position of a split-mode wave (0: fixed order)
+  const __bf16* kc;      // KEYSET heads: compact K [set][cap][64]
+  const __bf16* vc;      // KEYSET heads: compact transposed V tiles [set][cap/64][64][64]
+  const int32_t* ks_count;
+  int64_t ks_cap;
   int n_order;
   int order[kMaxHeads];
   int item_start[kMaxHeads + 1];
@@ -244,11 +250,16 @@ struct TileSeq {
   int s0, l0, s1, l1, s2, l2, s3, l3;
   int count;
   int rot;
+  // the ranges are work-group uniform; readfirstlane keeps them (and every at()) in scalar registers
   __device__ inline void set(int a0, int b0, int a1, int b1, int a2, int b2, int a3, int b3) {
-    s0 = a0; l0 = max(b0, 0);
-    s1 = a1; l1 = max(b1, 0);
-    s2 = a2; l2 = max(b2, 0);
-    s3 = a3; l3 = max(b3, 0);
+    s0 = __builtin_amdgcn_readfirstlane(a0);
+    l0 = __builtin_amdgcn_readfirstlane(max(b0, 0));
+    s1 = __builtin_amdgcn_readfirstlane(a1);
+    l1 = __builtin_amdgcn_readfirstlane(max(b1, 0));
+    s2 = __builtin_amdgcn_readfirstlane(a2);
+    l2 = __builtin_amdgcn_readfirstlane(max(b2, 0));
+    s3 = __builtin_amdgcn_readfirstlane(a3);
+    l3 = __builtin_amdgcn_readfirstlane(max(b3, 0));
     count = l0 + l1 + l2 + l3;
     rot = 0;
   }
@@ -322,7 +333,7 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
   const int ns4 = (g.nst + 3) >> 2;
   const int groups_pf = (g.NBf + 3) >> 2;
   int qt0, nw, kind;
-  if (pat == SAF3R_DENSE || pat == SAF3R_SKIP) {
+  if (pat == SAF3R_DENSE || pat == SAF3R_SKIP || pat == SAF3R_KEYSET) {
     qt0 = 4 * it;
     nw = min(4, g.NT - qt0);
     kind = pat == SAF3R_SKIP ? kSkip : kShared;
@@ -403,11 +414,22 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
   const float c = p.c;
 
   if (kind == kShared) {
+    // The shared-mode walk, instantiated separately for KEYSET heads (compact key-set tiles) and
+    // for every other pattern, so neither carries the other's state in registers.
+    auto shared_walk = [&](auto ks_tag) {
     // ---- key-tile sequence (uniform) ----
     TileSeq seq;
     bool frame_rel = false;
-    const int eff = (pat == SAF3R_DENSE || pat == SAF3R_TOKEN_DYNAMIC || pat == SAF3R_BLOCK_DYNAMIC) ? SAF3R_DENSE : pat;
-    if (eff == SAF3R_DENSE) {
+    constexpr bool keyset = decltype(ks_tag)::value;
+    const int eff = (pat == SAF3R_DENSE || pat == SAF3R_TOKEN_DYNAMIC || pat == SAF3R_BLOCK_DYNAMIC || keyset)
+                        ? SAF3R_DENSE
+                        : pat;
+    // KEYSET heads walk the compact tiles of their key set; key k of the set is slot k there
+    int ks_keys = 0;
+    if constexpr (keyset) ks_keys = __builtin_amdgcn_readfirstlane(p.ks_count[p.slot[h]]);
+    if constexpr (keyset) {
+      seq.set(0, (ks_keys + 63) / 64, 0, 0, 0, 0, 0, 0);
+    } else if (eff == SAF3R_DENSE) {
       seq.set(0, g.NT, 0, 0, 0, 0, 0, 0);
     } else {
       frame_rel = true;
@@ -432,11 +454,11 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
               g.nst + f0 * g.NBf, need_local ? (f1 - f0 + 1) * g.NBf : 0);
     }
     const int count = seq.count;
-    if (eff == SAF3R_DENSE && p.phase_dense > 0) {
+    if (eff == SAF3R_DENSE && p.phase_dense > 0 && count > 0) {
       // one clock reading per work-group: the four waves share the ring and must agree
       if (tid == 0) wcnt[0] = (int)((wall_clock64() / p.phase_dense) % (uint64_t)count);
       __syncthreads();
-      seq.rot = wcnt[0];
+      seq.rot = __builtin_amdgcn_readfirstlane(wcnt[0]);  // an LDS value, uniform: keep the walk scalar
     }
 
     // thread tid owns 16-byte chunks tid and tid + 256 of the K and the V tile; LDS chunk
@@ -444,8 +466,9 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
     auto issue = [&](int n) {
       const int kt = seq.at(n);
       char* st = ring + (n % kStages) * 16384;
-      const __bf16* kb = p.k + (head_base + (int64_t)kt * 64) * 64;
-      const __bf16* vb = p.v + (head_base + (int64_t)kt * 64) * 64;
+      const int64_t row0 = keyset ? (int64_t)p.slot[h] * p.ks_cap + (int64_t)kt * 64 : head_base + (int64_t)kt * 64;
+      const __bf16* kb = (keyset ? p.kc : p.k) + row0 * 64;
+      const __bf16* vb = (keyset ? p.vc : p.v) + row0 * 64;
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
         const int P = tid + 256 * u, r = P >> 3, cg = (P & 7) ^ swz8(r);
@@ -459,7 +482,7 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
     wait_vm<0>();  // Q fragments landed; from here vmcnt counts ring loads only
     // tiles move in pairs: pair i+1 loads into the two free stages while pair i is consumed,
     // one barrier per pair
-    issue(0);
+    if (count > 0) issue(0);
     if (count > 1) issue(1);
     for (int n = 0; n < count; n += 2) {
       wait_vm<0>();
@@ -474,7 +497,16 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
         if (n + u < count) {
           const int kt = seq.at(n + u);
           TileMask tm;
-          tile_mask(g, kt, eff, frame_rel, qspecial, tm);
+          if constexpr (keyset) {
+            tm.kt = kt;
+            tm.kspecial = false;
+            tm.kframe = 0;
+            tm.eff = SAF3R_DENSE;
+            tm.kvalid = min(64, ks_keys - 64 * kt);
+            tm.need = tm.kvalid < 64;
+          } else {
+            tile_mask(g, kt, eff, frame_rel, qspecial, tm);
+          }
           const char* kst = ring + ((n + u) % kStages) * 16384;
           attend<2>(kst, kst + 8192, qfrag, A, frow, tm, g, 0, half, col, c, [&]() {
             if (n + 2 + u < count) issue(n + 2 + u);
@@ -485,6 +517,9 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
       }
     }
     store_rows(p, A, qtok, h, half);
+    };
+    if (pat == SAF3R_KEYSET) shared_walk(std::true_type{});
+    else shared_walk(std::false_type{});
     return;
   }
 
@@ -645,6 +680,7 @@ static int head_items(int pat, const Geom& g) {
   const int ns4 = (g.nst + 3) / 4, groups_pf = (g.NBf + 3) / 4;
   switch (pat) {
     case SAF3R_DENSE:
+    case SAF3R_KEYSET:
     case SAF3R_SKIP: return (g.NT + 3) / 4;
     case SAF3R_TOKEN_DYNAMIC: return ns4;
     case SAF3R_BLOCK_DYNAMIC: return ns4 + g.F * g.NBf;
@@ -652,10 +688,11 @@ static int head_items(int pat, const Geom& g) {
   }
 }
 
-static int64_t item_cost(int pat, const Geom& g, int sel_width) {
+static int64_t item_cost(int pat, const Geom& g, int sel_width, int64_t ks_cap) {
   switch (pat) {
     case SAF3R_DENSE:
     case SAF3R_TOKEN_DYNAMIC: return 4LL * g.NT;
+    case SAF3R_KEYSET: return 4LL * (ks_cap / 64);
     case SAF3R_BLOCK_DYNAMIC: return sel_width;
     case SAF3R_ANCHOR_LOCAL: return 8LL * (g.NBf + 1);
     case SAF3R_FRAME_LOCAL:
@@ -695,7 +732,8 @@ using namespace saf3r;
 extern "C" int saf3r_sparse_attn_fwd(const void* q_packed, const void* k_packed, const void* v_packed, int frames,
                                      int tokens_per_frame, int num_special, int num_heads,
                                      const int32_t* head_pattern, const int32_t* sel, int sel_width, float scale,
-                                     void* out, int64_t out_row_stride, void* stream) {
+                                     void* out, int64_t out_row_stride, const void* keyset_k, const void* keyset_v,
+                                     const int32_t* keyset_count, int64_t keyset_capacity, void* stream) {
   if (int e = injected("saf3r_sparse_attn_fwd")) return e;
   AttnParams p;
   if (!make_geom(frames, tokens_per_frame, num_special, &p.g))
@@ -706,14 +744,26 @@ extern "C" int saf3r_sparse_attn_fwd(const void* q_packed, const void* k_packed,
     return fail(SAF3R_ERR_INVALID, "saf3r_sparse_attn_fwd: null pointer");
   if (((uintptr_t)out % 16) || (out_row_stride % 8) || out_row_stride < (int64_t)num_heads * 64)
     return fail(SAF3R_ERR_INVALID, "saf3r_sparse_attn_fwd: out must be 16-byte aligned with row stride >= H*64, %% 8");
-  int n_dyn = 0;
+  int n_dyn = 0, n_ks = 0;
   for (int h = 0; h < num_heads; ++h) {
     int pt = head_pattern[h];
-    if (pt < SAF3R_DENSE || pt > SAF3R_SKIP)
+    if (pt < SAF3R_DENSE || pt > SAF3R_KEYSET)
       return fail(SAF3R_ERR_INVALID, "saf3r_sparse_attn_fwd: head %d has unknown pattern %d", h, pt);
     p.pattern[h] = (int8_t)pt;
-    p.slot[h] = (int8_t)(pt == SAF3R_BLOCK_DYNAMIC ? n_dyn++ : -1);
+    p.slot[h] = (int8_t)(pt == SAF3R_BLOCK_DYNAMIC ? n_dyn++ : pt == SAF3R_KEYSET ? n_ks++ : -1);
   }
+  if (n_ks > 0) {
+    if (!keyset_k || !keyset_v || !keyset_count)
+      return fail(SAF3R_ERR_INVALID, "saf3r_sparse_attn_fwd: KEYSET heads need the compact key-set buffers");
+    if (keyset_capacity <= 0 || keyset_capacity % 64)
+      return fail(SAF3R_ERR_INVALID, "saf3r_sparse_attn_fwd: keyset_capacity must be a positive multiple of 64");
+    if (((uintptr_t)keyset_k | (uintptr_t)keyset_v) % 16)
+      return fail(SAF3R_ERR_INVALID, "saf3r_sparse_attn_fwd: key-set buffers must be 16-byte aligned");
+  }
+  p.kc = (const __bf16*)keyset_k;
+  p.vc = (const __bf16*)keyset_v;
+  p.ks_count = keyset_count;
+  p.ks_cap = n_ks > 0 ? keyset_capacity : 0;
   if (n_dyn > 0) {
     if (!sel) return fail(SAF3R_ERR_INVALID, "saf3r_sparse_attn_fwd: block-dynamic heads need a selection list");
     if (sel_width <= 0 || sel_width > kMaxList)
@@ -733,8 +783,8 @@ extern "C" int saf3r_sparse_attn_fwd(const void* q_packed, const void* k_packed,
   for (int h = 0; h < num_heads; ++h) idx[h] = h;
   for (int i = 1; i < num_heads; ++i) {
     int x = idx[i], j = i;
-    int64_t cx = item_cost(p.pattern[x], p.g, sel_width);
-    while (j > 0 && item_cost(p.pattern[idx[j - 1]], p.g, sel_width) < cx) {
+    int64_t cx = item_cost(p.pattern[x], p.g, sel_width, keyset_capacity);
+    while (j > 0 && item_cost(p.pattern[idx[j - 1]], p.g, sel_width, keyset_capacity) < cx) {
       idx[j] = idx[j - 1];
       --j;
     }

@@ -1,0 +1,357 @@
+// Shared key sets of the `stride` and `q_probe_topk` modes: one key set per head, attended by
+// every query of the head.
+//
+// ref: saf3r/patch/sparse_attention.py:56-85 (dispatch: q_probe topk = N // stride when the group
+//      has a stride, else min(topk, N); include_as defaults False for q_probe, True for stride;
+//      start = head % stride with `shift`), :143-186 (q_probe_topk_attention: mean query over
+//      every token, fp32 scores qbar . k / sqrt(D), top-k keys, union with the anchor frame and
+//      the special tokens, sorted unique set), :256-273 (stride_attention: keys start,
+//      start + stride, ..., same union).
+//
+// Kernels:
+//   probe_partial_kernel / probe_finish_kernel: the mean query in a fixed order (chunks of
+//     R = ceil(N / 256) tokens summed sequentially, chunk sums added in order, one division).
+//   probe_scores_kernel: score[t] = sequential fmaf over d of qbar[d] k[t][d], times 1/sqrt(D).
+//   keyset_build_kernel: one work-group per head. Top-k by a 4-pass radix select on the
+//     sortable key (ties to the lower index), then one ordered pass over the tokens that marks
+//     members (top-k or strided, plus the anchor frame and specials) and compacts them in
+//     increasing token order with work-group prefix counts.
+//   keyset_gather_kernel: compact K rows and transposed, permuted V tiles of the members, in
+//     the packed layout the attention kernel reads.
+#include "common.h"
+
+namespace saf3r {
+
+constexpr int kProbeChunks = 256;
+constexpr int kBuildThreads = 1024;
+
+// Packed slot of token t (the inverse of slot_token).
+__device__ inline int64_t token_slot(const Geom& g, int64_t t) {
+  const int64_t f = t / g.T, r = t % g.T;
+  if (r < g.ns) return f * g.ns + r;
+  return (int64_t)g.Sp + f * g.Pp + (r - g.ns);
+}
+
+struct ProbeParams {
+  const __bf16* q;
+  const __bf16* k;
+  Geom g;
+  int n;  // tokens F * T
+  int chunk;
+  int nchunks;
+  const int32_t* head_ids;
+  float* partial;  // [n_sel][kProbeChunks][64]
+  float* qbar;     // [n_sel][64]
+  float* scores;   // [n_sel][scores_stride]
+  int64_t scores_stride;
+  float scale;
+};
+
+// grid (nchunks, n_sel), 64 threads: feature d of chunk c, summed in token order
+__global__ __launch_bounds__(64) void probe_partial_kernel(ProbeParams p) {
+  const int c = blockIdx.x, hs = blockIdx.y, d = threadIdx.x;
+  const int h = p.head_ids[hs];
+  const int t0 = c * p.chunk, t1 = min(p.n, t0 + p.chunk);
+  const __bf16* base = p.q + (int64_t)h * p.g.L * 64 + d;
+  float acc = 0.f;
+  for (int t = t0; t < t1; ++t) acc = acc + (float)base[token_slot(p.g, t) * 64];
+  p.partial[((int64_t)hs * kProbeChunks + c) * 64 + d] = acc;
+}
+
+// grid (n_sel), 64 threads: chunk sums in chunk order, then one correctly rounded division
+__global__ __launch_bounds__(64) void probe_finish_kernel(ProbeParams p) {
+  const int hs = blockIdx.x, d = threadIdx.x;
+  float total = 0.f;
+  for (int c = 0; c < p.nchunks; ++c) total = total + p.partial[((int64_t)hs * kProbeChunks + c) * 64 + d];
+  p.qbar[hs * 64 + d] = __fdiv_rn(total, (float)p.n);
+}
+
+// grid (ceil(N / 256), n_sel), 256 threads: one token per thread
+__global__ __launch_bounds__(256) void probe_scores_kernel(ProbeParams p) {
+  __shared__ float qb[64];
+  const int hs = blockIdx.y, h = p.head_ids[hs];
+  if (threadIdx.x < 64) qb[threadIdx.x] = p.qbar[hs * 64 + threadIdx.x];
+  __syncthreads();
+  const int t = blockIdx.x * 256 + threadIdx.x;
+  if (t >= p.n) return;
+  const u32x4* row = reinterpret_cast<const u32x4*>(p.k + ((int64_t)h * p.g.L + token_slot(p.g, t)) * 64);
+  float acc = 0.f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const u32x4 w = row[j];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      acc = __builtin_fmaf(qb[8 * j + 2 * e], bf16_lo(w[e]), acc);
+      acc = __builtin_fmaf(qb[8 * j + 2 * e + 1], bf16_hi(w[e]), acc);
+    }
+  }
+  p.scores[hs * p.scores_stride + t] = acc * p.scale;
+}
+
+struct BuildParams {
+  const float* scores;  // [n_heads][scores_stride] (top-k heads)
+  int64_t scores_stride;
+  const int32_t* mode;   // per head: 0 stride, 1 top-k
+  const int32_t* param;  // stride, or k
+  const int32_t* start;  // first strided token
+  const int32_t* include;
+  int n, T, ns;
+  int32_t* idx;  // [n_heads][idx_stride]
+  int64_t idx_stride;
+  int32_t* count;
+};
+
+// Exclusive prefix count of a per-thread flag over the work-group, and the total. wsum holds
+// one slot per wave; two barriers.
+__device__ inline int block_prefix(bool flag, int* wsum, int& total) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const uint64_t m = __ballot(flag);
+  const int pre = __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0));
+  if (lane == 0) wsum[w] = __popcll(m);
+  __syncthreads();
+  int before = 0, all = 0;
+  for (int i = 0; i < kBuildThreads / 64; ++i) {
+    const int v = wsum[i];
+    before += i < w ? v : 0;
+    all += v;
+  }
+  __syncthreads();
+  total = all;
+  return before + pre;
+}
+
+// grid (n_heads), kBuildThreads threads
+__global__ __launch_bounds__(kBuildThreads) void keyset_build_kernel(BuildParams p) {
+  __shared__ int hist[256];
+  __shared__ int wsum[kBuildThreads / 64];
+  __shared__ uint32_t sh_prefix;
+  __shared__ int sh_remaining;
+  const int hh = blockIdx.x, tid = threadIdx.x;
+  const int mode = p.mode[hh], param = p.param[hh], start = p.start[hh];
+  const bool include = p.include[hh] != 0;
+  const float* sc = p.scores + (int64_t)hh * p.scores_stride;
+
+  // ---- top-k: threshold key by radix select (most significant digit first) ----
+  // (a non-positive k or stride selects no token)
+  uint32_t thr = 0xFFFFFFFFu;
+  int need_eq = 0;
+  if (mode == 1 && param > 0) {
+    const int k = min(param, p.n);
+    uint32_t prefix = 0, mask = 0;
+    int remaining = k;
+    for (int shift = 24; shift >= 0; shift -= 8) {
+      if (tid < 256) hist[tid] = 0;
+      __syncthreads();
+      for (int t = tid; t < p.n; t += kBuildThreads) {
+        const uint32_t key = fkey(sc[t]);
+        if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255], 1);
+      }
+      __syncthreads();
+      if (tid == 0) {
+        int above = 0, b = 255;
+        for (; b > 0; --b) {
+          if (above + hist[b] >= remaining) break;
+          above += hist[b];
+        }
+        sh_prefix = prefix | ((uint32_t)b << shift);
+        sh_remaining = remaining - above;
+      }
+      __syncthreads();
+      prefix = sh_prefix;
+      remaining = sh_remaining;
+      mask |= 255u << shift;
+      __syncthreads();
+    }
+    thr = prefix;        // key of the k-th best token
+    need_eq = remaining; // how many tokens with exactly that key are taken (lowest indices)
+  }
+
+  // ---- members in token order: select, union, compact ----
+  int32_t* out = p.idx + (int64_t)hh * p.idx_stride;
+  int run_eq = 0, run_out = 0;
+  for (int base = 0; base < p.n; base += kBuildThreads) {
+    const int t = base + tid;
+    const bool valid = t < p.n;
+    bool sel;
+    if (mode == 1) {
+      const uint32_t key = valid ? fkey(sc[t]) : 0u;
+      const bool eq = valid && key == thr;
+      int tot_eq;
+      const int rank = run_eq + block_prefix(eq, wsum, tot_eq);
+      run_eq += tot_eq;
+      sel = valid && param > 0 && (key > thr || (eq && rank < need_eq));
+    } else {
+      sel = valid && param > 0 && t >= start && (t - start) % param == 0;
+    }
+    const bool flag = sel || (include && valid && (t < p.T || t % p.T < p.ns));
+    int tot;
+    const int pos = run_out + block_prefix(flag, wsum, tot);
+    if (flag) out[pos] = t;
+    run_out += tot;
+  }
+  if (tid == 0) p.count[hh] = run_out;
+}
+
+struct GatherKParams {
+  const __bf16* k;  // packed K
+  Geom g;
+  const int32_t* head_ids;
+  const __bf16* v;  // natural V rows
+  int64_t v_tok_stride, v_head_stride;
+  const int32_t* idx;
+  int64_t idx_stride;
+  const int32_t* count;
+  __bf16* kc;  // [n_sel][capacity][64]
+  __bf16* vc;  // [n_sel][capacity / 64][64][64] transposed, permuted tiles
+  int64_t capacity;
+};
+
+// grid (tiles, n_sel), 256 threads; four threads per key row, 16 features each (as the packing
+// kernel). Tiles at or beyond the member count are skipped; rows beyond it are zero.
+__global__ __launch_bounds__(256) void keyset_gather_kernel(GatherKParams p) {
+  __shared__ __align__(16) __bf16 vs[64 * 72];
+  const int tile = blockIdx.x, hs = blockIdx.y;
+  const int cnt = p.count[hs];
+  if (tile * 64 >= cnt) return;
+  const int h = p.head_ids[hs];
+  const int t = threadIdx.x, row = t >> 2, c = t & 3;
+  const int j = tile * 64 + row;
+  const int64_t tok = j < cnt ? p.idx[hs * p.idx_stride + j] : -1;
+  u32x4 a = {0, 0, 0, 0}, b = {0, 0, 0, 0};
+  if (tok >= 0) {
+    const u32x4* s4 =
+        reinterpret_cast<const u32x4*>(p.k + ((int64_t)h * p.g.L + token_slot(p.g, tok)) * 64 + 16 * c);
+    a = s4[0];
+    b = s4[1];
+  }
+  u32x4* d4 = reinterpret_cast<u32x4*>(p.kc + ((int64_t)hs * p.capacity + j) * 64 + 16 * c);
+  d4[0] = a;
+  d4[1] = b;
+
+  u32x4 va = {0, 0, 0, 0}, vb = {0, 0, 0, 0};
+  if (tok >= 0) {
+    const u32x4* s4 = reinterpret_cast<const u32x4*>(p.v + tok * p.v_tok_stride + h * p.v_head_stride + 16 * c);
+    va = s4[0];
+    vb = s4[1];
+  }
+  u32x4* l4 = reinterpret_cast<u32x4*>(vs + row * 72 + 16 * c);
+  l4[0] = va;
+  l4[1] = vb;
+  __syncthreads();
+  // transposed tile: row i = feature phi(i), column position kappa(key); see the packing kernel
+  const int i = t >> 2, ii = i & 31;
+  const int dd = 32 * (i >> 5) + 16 * ((ii >> 2) & 1) + 4 * (ii >> 3) + (ii & 3);
+  uint32_t wv[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int c0 = 16 * c + 2 * e, c1 = c0 + 1;
+    const int k0 = (c0 & ~12) | ((c0 & 4) << 1) | ((c0 & 8) >> 1);
+    const int k1 = (c1 & ~12) | ((c1 & 4) << 1) | ((c1 & 8) >> 1);
+    const uint16_t lo = __builtin_bit_cast(uint16_t, vs[k0 * 72 + dd]);
+    const uint16_t hi = __builtin_bit_cast(uint16_t, vs[k1 * 72 + dd]);
+    wv[e] = (uint32_t)lo | ((uint32_t)hi << 16);
+  }
+  u32x4* o4 = reinterpret_cast<u32x4*>(p.vc + ((int64_t)hs * p.capacity + (int64_t)tile * 64) * 64 + i * 64 + 16 * c);
+  o4[0] = u32x4{wv[0], wv[1], wv[2], wv[3]};
+  o4[1] = u32x4{wv[4], wv[5], wv[6], wv[7]};
+}
+
+}  // namespace saf3r
+
+using namespace saf3r;
+
+extern "C" int saf3r_probe_scores(const void* q_packed, const void* k_packed, int frames, int tokens_per_frame,
+                                  int num_special, const int32_t* head_ids, int n_sel, float scale, float* partial,
+                                  float* qbar, float* scores, int64_t scores_stride, void* stream) {
+  if (int e = injected("saf3r_probe_scores")) return e;
+  ProbeParams p;
+  if (!make_geom(frames, tokens_per_frame, num_special, &p.g))
+    return fail(SAF3R_ERR_INVALID, "saf3r_probe_scores: invalid geometry");
+  const int64_t n = (int64_t)frames * tokens_per_frame;
+  if (n > 0x7fffffff) return fail(SAF3R_ERR_UNSUPPORTED, "saf3r_probe_scores: too many tokens");
+  if (!q_packed || !k_packed || !head_ids || !partial || !qbar || !scores)
+    return fail(SAF3R_ERR_INVALID, "saf3r_probe_scores: null pointer");
+  if (n_sel <= 0 || n_sel > 65535 || scores_stride < n)
+    return fail(SAF3R_ERR_INVALID, "saf3r_probe_scores: bad n_sel %d or scores_stride", n_sel);
+  if (((uintptr_t)q_packed | (uintptr_t)k_packed) % 16)
+    return fail(SAF3R_ERR_INVALID, "saf3r_probe_scores: packed inputs must be 16-byte aligned");
+  p.q = (const __bf16*)q_packed;
+  p.k = (const __bf16*)k_packed;
+  p.n = (int)n;
+  p.chunk = (int)((n + kProbeChunks - 1) / kProbeChunks);
+  p.nchunks = (int)((n + p.chunk - 1) / p.chunk);
+  p.head_ids = head_ids;
+  p.partial = partial;
+  p.qbar = qbar;
+  p.scores = scores;
+  p.scores_stride = scores_stride;
+  p.scale = scale;
+  hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL(probe_partial_kernel, dim3(p.nchunks, n_sel), dim3(64), 0, s, p);
+  hipLaunchKernelGGL(probe_finish_kernel, dim3(n_sel), dim3(64), 0, s, p);
+  hipLaunchKernelGGL(probe_scores_kernel, dim3((unsigned)((n + 255) / 256), n_sel), dim3(256), 0, s, p);
+  return check_launch("saf3r_probe_scores");
+}
+
+extern "C" int saf3r_keyset_build(const float* scores, int64_t scores_stride, int n_heads, const int32_t* mode,
+                                  const int32_t* param, const int32_t* start, const int32_t* include, int frames,
+                                  int tokens_per_frame, int num_special, int32_t* idx, int64_t idx_stride,
+                                  int32_t* count, void* stream) {
+  if (int e = injected("saf3r_keyset_build")) return e;
+  Geom g;
+  if (!make_geom(frames, tokens_per_frame, num_special, &g))
+    return fail(SAF3R_ERR_INVALID, "saf3r_keyset_build: invalid geometry");
+  const int64_t n = (int64_t)frames * tokens_per_frame;
+  if (n > 0x7fffffff) return fail(SAF3R_ERR_UNSUPPORTED, "saf3r_keyset_build: too many tokens");
+  if (n_heads <= 0 || n_heads > 65535) return fail(SAF3R_ERR_INVALID, "saf3r_keyset_build: bad n_heads %d", n_heads);
+  if (!mode || !param || !start || !include || !idx || !count)
+    return fail(SAF3R_ERR_INVALID, "saf3r_keyset_build: null pointer");
+  if (idx_stride < n) return fail(SAF3R_ERR_INVALID, "saf3r_keyset_build: idx_stride below the token count");
+  BuildParams p;
+  p.scores = scores;
+  p.scores_stride = scores_stride;
+  p.mode = mode;
+  p.param = param;
+  p.start = start;
+  p.include = include;
+  p.n = (int)n;
+  p.T = tokens_per_frame;
+  p.ns = num_special;
+  p.idx = idx;
+  p.idx_stride = idx_stride;
+  p.count = count;
+  hipLaunchKernelGGL(keyset_build_kernel, dim3(n_heads), dim3(kBuildThreads), 0, (hipStream_t)stream, p);
+  return check_launch("saf3r_keyset_build");
+}
+
+extern "C" int saf3r_keyset_gather(const void* k_packed, int frames, int tokens_per_frame, int num_special,
+                                   const int32_t* head_ids, int n_sel, const void* v, int64_t v_tok_stride,
+                                   int64_t v_head_stride, const int32_t* idx, int64_t idx_stride,
+                                   const int32_t* count, int max_tiles, void* keyset_k, void* keyset_v,
+                                   int64_t capacity, void* stream) {
+  if (int e = injected("saf3r_keyset_gather")) return e;
+  GatherKParams p;
+  if (!make_geom(frames, tokens_per_frame, num_special, &p.g))
+    return fail(SAF3R_ERR_INVALID, "saf3r_keyset_gather: invalid geometry");
+  if (!k_packed || !head_ids || !v || !idx || !count || !keyset_k || !keyset_v)
+    return fail(SAF3R_ERR_INVALID, "saf3r_keyset_gather: null pointer");
+  if (n_sel <= 0 || n_sel > 65535 || max_tiles <= 0 || capacity % 64 || (int64_t)max_tiles * 64 > capacity)
+    return fail(SAF3R_ERR_INVALID, "saf3r_keyset_gather: bad n_sel %d, max_tiles %d or capacity %lld", n_sel,
+                max_tiles, (long long)capacity);
+  if (v_tok_stride % 8 || v_head_stride % 8 || ((uintptr_t)v | (uintptr_t)k_packed) % 16 ||
+      ((uintptr_t)keyset_k | (uintptr_t)keyset_v) % 16)
+    return fail(SAF3R_ERR_INVALID, "saf3r_keyset_gather: 16-byte alignment required");
+  p.k = (const __bf16*)k_packed;
+  p.head_ids = head_ids;
+  p.v = (const __bf16*)v;
+  p.v_tok_stride = v_tok_stride;
+  p.v_head_stride = v_head_stride;
+  p.idx = idx;
+  p.idx_stride = idx_stride;
+  p.count = count;
+  p.kc = (__bf16*)keyset_k;
+  p.vc = (__bf16*)keyset_v;
+  p.capacity = capacity;
+  hipLaunchKernelGGL(keyset_gather_kernel, dim3(max_tiles, n_sel), dim3(256), 0, (hipStream_t)stream, p);
+  return check_launch("saf3r_keyset_gather");
+}

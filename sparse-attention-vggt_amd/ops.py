@@ -7,6 +7,7 @@ from __future__ import annotations
 
 import ctypes
 import math
+from dataclasses import dataclass
 from typing import Sequence
 
 import torch
@@ -15,10 +16,11 @@ from . import _lib
 from .layout import BLOCK, HEAD_DIM, Geometry
 
 # Pattern ids (``enum saf3r_pattern``).
-DENSE, FRAME_LOCAL, ANCHOR_LOCAL, BLOCK_DYNAMIC, TOKEN_DYNAMIC, ANCHOR, SKIP = range(7)
+DENSE, FRAME_LOCAL, ANCHOR_LOCAL, BLOCK_DYNAMIC, TOKEN_DYNAMIC, ANCHOR, SKIP, KEYSET = range(8)
 PATTERN_NAMES = {
     DENSE: "dense", FRAME_LOCAL: "frame_local", ANCHOR_LOCAL: "anchor_local",
     BLOCK_DYNAMIC: "block_topk", TOKEN_DYNAMIC: "dino_topk", ANCHOR: "all_to_first", SKIP: "skip",
+    KEYSET: "keyset",
 }
 
 
@@ -185,8 +187,10 @@ def block_select(pooled_q: torch.Tensor, pooled_k: torch.Tensor, frames: int, bl
 
 
 def sparse_attn_fwd(qp, kp, vp, geom: Geometry, patterns: Sequence[int], sel: torch.Tensor | None = None,
-                    scale: float | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
-    """All heads in one launch. Returns (or fills) ``out`` bf16 [N, H*64] in natural token order."""
+                    scale: float | None = None, out: torch.Tensor | None = None,
+                    keysets: "KeySets | None" = None) -> torch.Tensor:
+    """All heads in one launch. Returns (or fills) ``out`` bf16 [N, H*64] in natural token order.
+    ``keysets`` carries the compact K/V of the KEYSET heads (in increasing head order)."""
     _need_cuda(qp, kp, vp)
     lib = _lib.load()
     H = qp.shape[0]
@@ -210,11 +214,19 @@ def sparse_attn_fwd(qp, kp, vp, geom: Geometry, patterns: Sequence[int], sel: to
         width = sel.shape[-1]
     else:
         sel = None
+    n_ks = sum(1 for p in patterns if p == KEYSET)
+    ks_k = ks_v = ks_n = None
+    ks_cap = 0
+    if n_ks:
+        if keysets is None or keysets.k.shape[0] != n_ks:
+            raise ValueError(f"{n_ks} KEYSET heads need {n_ks} gathered key sets")
+        ks_k, ks_v, ks_n, ks_cap = keysets.k, keysets.v, keysets.count, keysets.capacity
     pat = _i32_array(patterns)
     _mark("sparse_attn", "start")
     _lib.check(lib.saf3r_sparse_attn_fwd(
         _ptr(qp), _ptr(kp), _ptr(vp), geom.frames, geom.tokens_per_frame, geom.num_special, H,
-        pat, _ptr(sel), width, float(scale), _ptr(out), out.stride(0), _lib.stream_ptr()))
+        pat, _ptr(sel), width, float(scale), _ptr(out), out.stride(0), _ptr(ks_k), _ptr(ks_v), _ptr(ks_n),
+        ks_cap, _lib.stream_ptr()))
     _mark("sparse_attn", "end")
     return out
 
@@ -274,3 +286,104 @@ def token_topk(q: torch.Tensor, k: torch.Tensor, frames: int, per_frame: int, to
     _lib.check(lib.saf3r_token_topk(ctypes.byref(qrows), ctypes.byref(krows), n_q, frames, per_frame, topk,
                                     _ptr(idx), _lib.stream_ptr()))
     return idx
+
+
+# ----------------------------------------------------------------------------------------
+# Shared key sets of the stride and q_probe_topk modes
+# ----------------------------------------------------------------------------------------
+KEYSET_STRIDE, KEYSET_TOPK = 0, 1
+
+
+@dataclass
+class KeySetSpec:
+    """One KEYSET head: ``mode`` KEYSET_STRIDE (``param`` = stride, first key ``start``) or
+    KEYSET_TOPK (``param`` = k best probe scores); ``include`` adds frame 0 and every special token.
+    ref: saf3r/patch/sparse_attention.py:56-85."""
+    head: int
+    mode: int
+    param: int
+    start: int = 0
+    include: bool = False
+
+    def bound(self, geom: Geometry) -> int:
+        """Upper bound of the member count (host side, sizes the compact buffers)."""
+        n = geom.tokens
+        if self.mode == KEYSET_STRIDE:
+            m = 0 if self.start >= n else -(-(n - self.start) // self.param)
+        else:
+            m = min(self.param, n)
+        if self.include:
+            m += min(n, geom.tokens_per_frame) + geom.frames * geom.num_special
+        return min(m, n)
+
+
+@dataclass
+class KeySets:
+    """Compact K/V of the KEYSET heads of a layer: ``k`` [n][capacity][64], ``v`` [n][capacity/64][64][64]
+    (transposed tiles), ``count`` int32 [n] members, ``idx`` int32 [n][N] members in token order."""
+    k: torch.Tensor
+    v: torch.Tensor
+    count: torch.Tensor
+    idx: torch.Tensor
+    capacity: int
+    scores: torch.Tensor | None = None
+    qbar: torch.Tensor | None = None
+
+
+def probe_scores(qp: torch.Tensor, kp: torch.Tensor, geom: Geometry, head_ids: Sequence[int],
+                 scale: float | None = None):
+    """Mean query and probe scores of ``head_ids`` (``saf3r/patch/sparse_attention.py:160-168``):
+    returns (qbar fp32 [n][64], scores fp32 [n][N] in token order)."""
+    _need_cuda(qp, kp)
+    lib = _lib.load()
+    _check_packed(qp, kp, None, geom)
+    n = len(head_ids)
+    dev = qp.device
+    hs = torch.tensor(list(head_ids), dtype=torch.int32, device=dev)
+    partial = torch.empty(n, 256, HEAD_DIM, dtype=torch.float32, device=dev)
+    qbar = torch.empty(n, HEAD_DIM, dtype=torch.float32, device=dev)
+    scores = torch.empty(n, geom.tokens, dtype=torch.float32, device=dev)
+    scale = 1.0 / math.sqrt(HEAD_DIM) if scale is None else scale
+    _lib.check(lib.saf3r_probe_scores(_ptr(qp), _ptr(kp), geom.frames, geom.tokens_per_frame, geom.num_special,
+                                      _ptr(hs), n, float(scale), _ptr(partial), _ptr(qbar), _ptr(scores),
+                                      scores.stride(0), _lib.stream_ptr()))
+    return qbar, scores
+
+
+def keyset_build(specs: Sequence[KeySetSpec], geom: Geometry, scores: torch.Tensor | None, device):
+    """Members of each key set in token order: (idx int32 [n][N], count int32 [n]). ``scores``
+    holds one row per spec (rows of KEYSET_STRIDE specs are not read)."""
+    lib = _lib.load()
+    n = len(specs)
+    if any(s.param <= 0 for s in specs):
+        raise ValueError("key-set stride / k must be positive")
+    arr = torch.tensor([[s.mode, s.param, s.start, int(bool(s.include))] for s in specs], dtype=torch.int32)
+    arr = arr.t().contiguous().to(device)
+    idx = torch.empty(n, geom.tokens, dtype=torch.int32, device=device)
+    count = torch.empty(n, dtype=torch.int32, device=device)
+    if scores is not None:
+        if scores.dtype != torch.float32 or scores.shape[0] != n or scores.shape[1] < geom.tokens:
+            raise ValueError("scores must be fp32 [n_specs, >= N]")
+        scores = scores.contiguous()
+    _lib.check(lib.saf3r_keyset_build(_ptr(scores), 0 if scores is None else scores.stride(0), n, _ptr(arr[0]),
+                                      _ptr(arr[1]), _ptr(arr[2]), _ptr(arr[3]), geom.frames, geom.tokens_per_frame,
+                                      geom.num_special, _ptr(idx), idx.stride(0), _ptr(count), _lib.stream_ptr()))
+    return idx, count
+
+
+def keyset_gather(kp: torch.Tensor, geom: Geometry, specs: Sequence[KeySetSpec], v: torch.Tensor,
+                  v_tok_stride: int, v_head_stride: int, idx: torch.Tensor, count: torch.Tensor) -> KeySets:
+    """Compact K (packed rows) and transposed V tiles of each key set. ``v`` points at head 0's V of
+    token 0 in the natural layout; head h, token t at ``v_tok_stride * t + v_head_stride * h``."""
+    _need_cuda(kp, v, idx, count)
+    lib = _lib.load()
+    n = len(specs)
+    cap = max(64, -(-max(s.bound(geom) for s in specs) // 64) * 64)
+    dev = kp.device
+    kc = torch.empty(n, cap, HEAD_DIM, dtype=torch.bfloat16, device=dev)
+    vc = torch.empty(n, cap // 64, 64, 64, dtype=torch.bfloat16, device=dev)
+    hs = torch.tensor([s.head for s in specs], dtype=torch.int32, device=dev)
+    _lib.check(lib.saf3r_keyset_gather(_ptr(kp), geom.frames, geom.tokens_per_frame, geom.num_special, _ptr(hs), n,
+                                       _ptr(v), v_tok_stride, v_head_stride, _ptr(idx), idx.stride(0), _ptr(count),
+                                       cap // 64, _ptr(kc), _ptr(vc), cap, _lib.stream_ptr()))
+    return KeySets(kc, vc, count, idx, cap)

@@ -14,13 +14,20 @@ Block patterns (same JSON format, new mode names)
   frame_local            FRAME_LOCAL
   anchor_local           ANCHOR_LOCAL (frame 0 and the query's own frame)
   block_topk             BLOCK_DYNAMIC (per-head pooled block scores, top-k blocks per frame)
-Reference modes without a kernel in this build: stride, q_probe_topk, broadcast_first -> NotImplementedError.
+  stride                 KEYSET (keys start, start + stride, ... plus, with include_as (default
+                         True), frame 0 and every special token; start = head % stride with shift)
+  q_probe_topk           KEYSET (the N // stride (or min(topk, N), default topk 1024) keys with the
+                         best mean-query scores, plus frame 0 and the specials with include_as
+                         (default False))
+Reference modes without a kernel in this build: broadcast_first, and q_probe_topk with
+q_sample_ratio != 1 -> NotImplementedError.
 """
 from __future__ import annotations
 
 import torch
 
-from ..ops import ANCHOR, ANCHOR_LOCAL, BLOCK_DYNAMIC, DENSE, FRAME_LOCAL, SKIP, TOKEN_DYNAMIC
+from ..ops import (ANCHOR, ANCHOR_LOCAL, BLOCK_DYNAMIC, DENSE, FRAME_LOCAL, KEYSET, KEYSET_STRIDE, KEYSET_TOPK,
+                   SKIP, TOKEN_DYNAMIC, KeySetSpec)
 
 MODE_TO_PATTERN = {
     "full": DENSE,
@@ -32,8 +39,10 @@ MODE_TO_PATTERN = {
     "dino_topk": TOKEN_DYNAMIC,
     "all_to_first": ANCHOR,
     "skip": SKIP,
+    "stride": KEYSET,
+    "q_probe_topk": KEYSET,
 }
-UNBUILT_MODES = ("stride", "q_probe_topk", "broadcast_first")
+UNBUILT_MODES = ("broadcast_first",)
 
 
 def pattern_of(cfg: dict) -> int:
@@ -43,6 +52,24 @@ def pattern_of(cfg: dict) -> int:
     if mode in UNBUILT_MODES:
         raise NotImplementedError(f"mode {mode!r} has no kernel in this build")
     raise ValueError(f"Unsupported mode: {mode}")
+
+
+def keyset_spec(cfg: dict, head: int, num_tokens: int) -> KeySetSpec:
+    """Key set of a ``stride`` or ``q_probe_topk`` head (``saf3r/patch/sparse_attention.py:56-85``)."""
+    mode = cfg["mode"]
+    if mode == "stride":
+        stride = int(cfg.get("stride", 4))
+        start = head % stride if cfg.get("shift", False) else 0
+        return KeySetSpec(head, KEYSET_STRIDE, stride, start, bool(cfg.get("include_as", True)))
+    if mode == "q_probe_topk":
+        if cfg.get("q_sample_ratio", 1) != 1:
+            raise NotImplementedError("q_probe_topk with q_sample_ratio != 1 has no kernel in this build")
+        if "stride" in cfg:
+            k = max(1, num_tokens // int(cfg["stride"]))
+        else:
+            k = min(int(cfg.get("topk", 1024)), num_tokens)
+        return KeySetSpec(head, KEYSET_TOPK, k, 0, bool(cfg.get("include_as", False)))
+    raise ValueError(f"mode {mode!r} has no key set")
 
 
 def get_separate_indices(num_imgs: int, num_toks_per_img: int, num_special_tokens: int):

@@ -19,7 +19,7 @@ from torch import nn
 
 from .. import ops
 from ..layout import HEAD_DIM, Geometry
-from .sparse_attention import pattern_of
+from .sparse_attention import keyset_spec, pattern_of
 
 
 class SelectionState:
@@ -81,6 +81,8 @@ class BaseHeadwiseSparseAttentionWrapper(nn.Module):
             raise ValueError(f"block_topk heads of one layer must share one k, got {sorted(ks)}")
         self.layer_block_topk = ks.pop() if ks else self.block_topk
         self.dyn_heads = [h for h, p in enumerate(self.patterns) if p == ops.BLOCK_DYNAMIC]
+        self.keyset_heads = [h for h, p in enumerate(self.patterns) if p == ops.KEYSET]
+        self.last_keysets = None
         self.dino_heads = [h for h, p in enumerate(self.patterns) if p == ops.TOKEN_DYNAMIC]
         self.first_dino_head = next((h for h in self.dino_heads if self.head_cfg[h].get("is_first_dino", False)), None)
 
@@ -119,7 +121,11 @@ class BaseHeadwiseSparseAttentionWrapper(nn.Module):
         self.last_selection = sel  # block lists of the block_topk heads, in head order
         if self.dino_heads:
             self._lazy_token_topk(qp, kp, geom)
-        out = ops.sparse_attn_fwd(qp, kp, vp, geom, self.patterns, sel)
+        keysets = None
+        if self.keyset_heads:
+            keysets = self._keysets(qp, kp, qkv, geom, C)
+        self.last_keysets = keysets
+        out = ops.sparse_attn_fwd(qp, kp, vp, geom, self.patterns, sel, keysets=keysets)
         if self.dino_heads:
             est = self.est_topk_idx
             P, W = geom.patches, est.shape[1]
@@ -130,6 +136,24 @@ class BaseHeadwiseSparseAttentionWrapper(nn.Module):
                 orr = ops.rows(out, C, geom.num_special, P, geom.tokens_per_frame, offset=h * HEAD_DIM)
                 ops.gather_attn_rows(qr, kr, vr, est, W, geom.frames * P, W, geom.frames * P, None, orr)
         return out
+
+    def _keysets(self, qp, kp, qkv, geom: Geometry, C: int):
+        """Shared key sets of the stride / q_probe_topk heads (``sparse_attention.py:143-186, 256-273``):
+        probe scores of the top-k heads, members in token order, then the compact K / V they attend."""
+        specs = [keyset_spec(self.head_cfg[h], h, geom.tokens) for h in self.keyset_heads]
+        probe_rows = [i for i, s in enumerate(specs) if s.mode == ops.KEYSET_TOPK]
+        scores = None
+        if probe_rows:
+            _, sc = ops.probe_scores(qp, kp, geom, [specs[i].head for i in probe_rows])
+            if len(probe_rows) == len(specs):
+                scores = sc
+            else:
+                scores = torch.zeros(len(specs), geom.tokens, dtype=torch.float32, device=qp.device)
+                scores[probe_rows] = sc
+        idx, count = ops.keyset_build(specs, geom, scores, qp.device)
+        ks = ops.keyset_gather(kp, geom, specs, qkv[:, 2 * C:], qkv.stride(0), HEAD_DIM, idx, count)
+        ks.scores = scores
+        return ks
 
     def _lazy_token_topk(self, qp, kp, geom: Geometry):
         """Lazy per-frame token top-k from the first correspondence head (``wrapper.py:42-86``)."""

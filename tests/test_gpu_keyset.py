@@ -1,0 +1,124 @@
+"""GPU parity of the key-set path of the `stride` and `q_probe_topk` modes
+(saf3r/patch/sparse_attention.py:143-186, 256-273) against the oracle on the same inputs.
+
+Bars: mean query, probe scores, key-set members and the gathered K rows are bit-exact; attention
+over the key sets is within max-abs 2e-2 / mean-abs 2e-3 of the fp64 oracle."""
+import importlib
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as OA
+from oracle import selection as OS
+from tests.layout_ref import slot_tokens, unpack_rows, unpack_v
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+ATOL_MAX, ATOL_MEAN = 2e-2, 2e-3
+
+
+@pytest.fixture(scope="module")
+def ops(pkg):
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    return importlib.import_module(pkg.__name__ + ".ops")
+
+
+def _qkv(H, N, seed, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return [(torch.randn(H, N, 64, generator=g) * scale).to(torch.bfloat16) for _ in range(3)]
+
+
+def _bits(x: torch.Tensor) -> np.ndarray:
+    return x.contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+@pytest.mark.parametrize("F,T,ns", [(3, 155, 5), (4, 1374, 5), (2, 64, 0), (1, 70, 5)])
+def test_probe_scores_bit_exact(ops, pkg, F, T, ns):
+    geom = pkg.Geometry(F, T, ns)
+    H = 3
+    q, k, v = _qkv(H, geom.tokens, seed=F + T, scale=2.0)
+    qp, kp, vp = ops.pack_heads(q.to(DEV), k.to(DEV), v.to(DEV), geom)
+    heads = [2, 0]
+    qbar, scores = ops.probe_scores(qp, kp, geom, heads)
+    torch.cuda.synchronize()
+    for i, h in enumerate(heads):
+        want_q = OS.probe_mean(_bits(q[h]))
+        assert np.array_equal(qbar[i].cpu().numpy().view(np.uint32), want_q.view(np.uint32)), f"qbar head {h}"
+        want_s = OS.probe_scores(want_q, _bits(k[h]))
+        assert np.array_equal(scores[i].cpu().numpy().view(np.uint32), want_s.view(np.uint32)), f"scores head {h}"
+
+
+@pytest.mark.parametrize("F,T,ns", [(3, 155, 5), (4, 1374, 5), (2, 64, 0)])
+def test_keyset_build_bit_exact(ops, pkg, F, T, ns):
+    geom = pkg.Geometry(F, T, ns)
+    n = geom.tokens
+    rng = np.random.default_rng(n)
+    specs = [ops.KeySetSpec(0, ops.KEYSET_STRIDE, 4, 0, True), ops.KeySetSpec(1, ops.KEYSET_TOPK, n // 4, 0, False),
+             ops.KeySetSpec(2, ops.KEYSET_TOPK, 37, 0, True), ops.KeySetSpec(3, ops.KEYSET_STRIDE, 128, 3, False),
+             ops.KeySetSpec(4, ops.KEYSET_TOPK, n + 5, 0, False), ops.KeySetSpec(5, ops.KEYSET_STRIDE, 7, 2, True)]
+    scores = np.zeros((len(specs), n), np.float32)
+    scores[1] = rng.standard_normal(n).astype(np.float32)
+    scores[2] = rng.integers(-3, 4, n).astype(np.float32)  # ties decided by the lower token
+    scores[2][::5] = -0.0
+    scores[4] = rng.standard_normal(n).astype(np.float32)
+    idx, count = ops.keyset_build(specs, geom, torch.from_numpy(scores).to(DEV), DEV)
+    torch.cuda.synchronize()
+    idx, count = idx.cpu().numpy(), count.cpu().numpy()
+    for i, s in enumerate(specs):
+        want = OS.keyset(scores[i], n, T, ns, s.mode, s.param, s.start, s.include)
+        assert count[i] == len(want) <= s.bound(geom), f"spec {i}"
+        assert np.array_equal(idx[i, :count[i]], want), f"spec {i}"
+
+
+def test_keyset_gather_rows_and_tiles(ops, pkg):
+    geom = pkg.Geometry(3, 155, 5)
+    n, H = geom.tokens, 4
+    q, k, v = _qkv(H, n, seed=5)
+    qp, kp, vp = ops.pack_heads(q.to(DEV), k.to(DEV), v.to(DEV), geom)
+    specs = [ops.KeySetSpec(3, ops.KEYSET_STRIDE, 3, 1, True), ops.KeySetSpec(1, ops.KEYSET_STRIDE, 50, 0, False)]
+    idx, count = ops.keyset_build(specs, geom, None, DEV)
+    vnat = v.permute(1, 0, 2).contiguous().to(DEV)  # [N, H, 64]: head stride 64, token stride H*64
+    ks = ops.keyset_gather(kp, geom, specs, vnat, H * 64, 64, idx, count)
+    torch.cuda.synchronize()
+    kc, vc, cnt, ix = ks.k.cpu(), ks.v.cpu(), count.cpu(), idx.cpu()
+    for i, s in enumerate(specs):
+        c = int(cnt[i])
+        keys = ix[i, :c].long()
+        assert torch.equal(kc[i, :c], k[s.head][keys])
+        tiles = -(-c // 64)
+        assert (kc[i, c:tiles * 64] == 0).all()
+        toks = torch.arange(tiles * 64)
+        toks = torch.where(toks < c, toks, torch.full_like(toks, -1))
+        nat, pad = unpack_v(vc[i:i + 1, :tiles], toks, c)
+        assert torch.equal(nat[0], v[s.head][keys]) and (pad == 0).all()
+
+
+@pytest.mark.parametrize("F,T,ns", [(3, 155, 5), (4, 1374, 5), (1, 70, 5), (2, 64, 0)])
+def test_keyset_attention_in_one_launch(ops, pkg, F, T, ns):
+    geom = pkg.Geometry(F, T, ns)
+    n = geom.tokens
+    patterns = [ops.KEYSET, ops.DENSE, ops.KEYSET, ops.FRAME_LOCAL, ops.KEYSET, ops.ANCHOR]
+    H = len(patterns)
+    q, k, v = _qkv(H, n, seed=F * 3 + T, scale=1.5)
+    qp, kp, vp = ops.pack_heads(q.to(DEV), k.to(DEV), v.to(DEV), geom)
+    specs = [ops.KeySetSpec(0, ops.KEYSET_STRIDE, 4, 0, True), ops.KeySetSpec(2, ops.KEYSET_TOPK, max(1, n // 4)),
+             ops.KeySetSpec(4, ops.KEYSET_STRIDE, 128, 0, True)]
+    _, sc = ops.probe_scores(qp, kp, geom, [2])
+    scores = torch.zeros(3, n, device=DEV)
+    scores[1] = sc[0]
+    idx, count = ops.keyset_build(specs, geom, scores, DEV)
+    vnat = v.permute(1, 0, 2).contiguous().to(DEV)
+    ks = ops.keyset_gather(kp, geom, specs, vnat, H * 64, 64, idx, count)
+    out = ops.sparse_attn_fwd(qp, kp, vp, geom, patterns, keysets=ks)
+    torch.cuda.synchronize()
+    og = OA.Geometry(F, T, ns)
+    got = out.float().cpu().reshape(n, H, 64).permute(1, 0, 2)
+    ks_of = {s.head: idx[i, :int(count[i])].cpu() for i, s in enumerate(specs)}
+    for h, pat in enumerate(patterns):
+        ref = OA.sparse_attention_gathered(q[h].float(), k[h].float(), v[h].float(), pat, og, ks_of.get(h),
+                                           dtype=torch.float64)
+        err = (got[h] - ref.float()).abs()
+        print(f"F{F} T{T} head {h} pattern {pat}: max {err.max().item():.3g} mean {err.mean().item():.3g}", flush=True)
+        assert err.max().item() <= ATOL_MAX and err.mean().item() <= ATOL_MEAN

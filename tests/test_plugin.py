@@ -104,14 +104,27 @@ def test_reference_vggt_profile_fixture(plug, vggt):
         assert sorted(h for g in groups for h in g["head_ids"]) == list(range(16))
     firsts = [(k, g["head_ids"]) for k, gs in prof.items() for g in gs if g.get("is_first_dino")]
     assert firsts == [("11", [14])]
-    # layers whose modes all have kernels patch cleanly; stride / q_probe_topk are not built yet
+    # the whole profile patches: every mode it uses has a kernel
     m = _model(vggt, depth=24, dim=1024, heads=16)
-    ok = {k: v for k, v in prof.items() if all(g["mode"] in ("all_to_first", "global_to_frame", "dino_topk", "full")
-                                                 for g in v)}
-    assert ok, "expected some layers without stride heads"
     plug.patch_model(m, "vggt", {"patch_module": {"type": "headsparse", "topk_mode": "token",
-                                                  "lazy_dino_topk": True, "topk": 4}, "sparse_config": ok})
-    with pytest.raises(NotImplementedError, match="stride"):
-        plug.patch_model(_model(vggt, depth=24, dim=1024, heads=16), "vggt",
-                         {"patch_module": {"type": "headsparse", "topk_mode": "token", "lazy_dino_topk": True,
-                                           "topk": 4}, "sparse_config": prof})
+                                                  "lazy_dino_topk": True, "topk": 4}, "sparse_config": prof})
+    wrappers = [b.attn for b in m.aggregator.global_blocks]
+    assert sum(len(w.keyset_heads) for w in wrappers) == 212 + 75
+    assert [w.layer_idx for w in wrappers if w.first_dino_head is not None] == [11]
+    # key sets of the profile's groups at the 128-frame shape
+    from importlib import import_module
+    spa = import_module(plug.__name__ + ".sparse_attention")
+    ops = import_module(plug.__name__.rsplit(".", 1)[0] + ".ops")
+    n = 128 * 1374
+    s4 = spa.keyset_spec({"mode": "stride", "stride": 4, "include_as": True, "is_base": True}, 3, n)
+    assert (s4.mode, s4.param, s4.start, s4.include) == (ops.KEYSET_STRIDE, 4, 0, True)
+    qp = spa.keyset_spec({"mode": "q_probe_topk", "stride": 4, "is_base": False}, 5, n)
+    assert (qp.mode, qp.param, qp.include) == (ops.KEYSET_TOPK, n // 4, False)
+    assert spa.keyset_spec({"mode": "q_probe_topk"}, 0, n).param == 1024
+    assert spa.keyset_spec({"mode": "stride", "stride": 3, "shift": True}, 7, n).start == 1
+    with pytest.raises(NotImplementedError, match="q_sample_ratio"):
+        spa.keyset_spec({"mode": "q_probe_topk", "q_sample_ratio": 0.5}, 0, n)
+    with pytest.raises(NotImplementedError, match="broadcast_first"):
+        plug.patch_model(_model(vggt, depth=1, dim=64, heads=2), "vggt",
+                         {"patch_module": {"type": "headsparse"},
+                          "sparse_config": {"0": [{"mode": "broadcast_first", "head_ids": [0]}]}})
