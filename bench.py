@@ -157,6 +157,9 @@ def main():
     ap.add_argument("--frames", type=int, default=128)
     ap.add_argument("--layers", type=int, default=24)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--sparse-config", default=None,
+                    help="a head-profile JSON in the reference's format (e.g. its VGGT ETH3D profile) to run "
+                         "instead of the seeded block-pattern tables; dino_topk heads use lazy top-4 indices")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only a plain copy kernel of known size (reads 1 GiB, writes 1 GiB), for scaling "
                          "the FETCH_SIZE / WRITE_SIZE counters of a profiling run")
@@ -183,9 +186,16 @@ def main():
     torch.manual_seed(0)
     model = vggt.GlobalAttentionStack(depth=args.layers, dim=dim, num_heads=heads)
     model = model.to(dev).to(torch.bfloat16).eval()
-    cfg, tables = layer_config(args.layers, heads, 1, synth, ops)
-    plug.patch_model(model, "vggt", {"patch_module": {"type": "headsparse", "topk_mode": "token", "block_topk": 4,
-                                                      "topk_scope": "frame"}, "sparse_config": cfg})
+    if args.sparse_config:
+        with open(args.sparse_config) as f:
+            cfg = {k: v for k, v in json.load(f).items() if int(k) < args.layers}
+        plug.patch_model(model, "vggt", {"patch_module": {"type": "headsparse", "topk_mode": "token",
+                                                          "lazy_dino_topk": True, "topk": 4}, "sparse_config": cfg})
+    else:
+        cfg, _ = layer_config(args.layers, heads, 1, synth, ops)
+        plug.patch_model(model, "vggt", {"patch_module": {"type": "headsparse", "topk_mode": "token",
+                                                          "block_topk": 4, "topk_scope": "frame"},
+                                         "sparse_config": cfg})
     plug.update_args_per_forward(model, "vggt", ph * 14, pw * 14)
     T = ph * pw + 5
     N = args.frames * T
@@ -195,7 +205,10 @@ def main():
     pos = synth.vggt_positions(args.frames, ph, pw, device=dev)[None]
     layers = [b.attn for b in model.aggregator.global_blocks]
 
+    tables = [w.patterns for w in layers]
+
     def step():
+        plug.update_args_per_forward(model, "vggt", ph * 14, pw * 14)  # a new forward: lazy indices recomputed
         for layer in layers:
             layer(x, pos)
 
@@ -217,14 +230,22 @@ def main():
     ms_layer = ms_step / args.layers
     dur = rec.durations_ms()
 
-    # algorithmic work of every layer (selection lists of the last step)
-    attn_flops = [acc.attention_flops(tables[i], geom, layers[i].last_selection) for i in range(args.layers)]
+    # algorithmic work of every layer (selection lists and key sets of the last step); the attention
+    # kernel's own share excludes the image rows of dino_topk heads (done by the gather kernel)
+    def layer_work(w, full):
+        width = w.est_topk_idx.shape[1] if (full and w.dino_heads) else 0
+        counts = w.last_keysets.count.tolist() if w.keyset_heads else None
+        return acc.attention_flops(w.patterns, geom, w.last_selection, width, counts)
+
+    attn_flops = [layer_work(w, True) for w in layers]
+    kernel_flops = [layer_work(w, False) for w in layers]
     proj = acc.projection_flops(N, dim)
     layer_flops = sum(attn_flops) / args.layers + proj
     attn_ms = dur.get("sparse_attn", [])
     attn_ms_avg = statistics.fmean(attn_ms) if attn_ms else float("nan")
-    attn_tflops = (sum(attn_flops) * args.steps) / (sum(attn_ms) * 1e-3) / 1e12 if attn_ms else None
+    attn_tflops = (sum(kernel_flops) * args.steps) / (sum(attn_ms) * 1e-3) / 1e12 if attn_ms else None
     n_dyn = sum(1 for p in tables[0] if p == ops.BLOCK_DYNAMIC)
+    other_ms = {k: round(statistics.fmean(v), 4) for k, v in dur.items() if k not in ("sparse_attn",)}
     width = args.frames * min(4, geom.blocks_per_frame)
     sb = acc.selection_bytes(geom, n_dyn, width)
     pool_ms = dur.get("block_pool", [])
@@ -258,8 +279,11 @@ def main():
         "data": "synthetic: N(0,1) tokens and random-init bf16 weights (seed 0), seeded head tables",
         "config": {
             "workload": (f"VGGT-1B global attention: {args.layers} layers x {args.frames} frames x {T} tokens "
-                         f"({N}), 16 heads, d 64, dim 1024, RoPE-2D + QK-LayerNorm, head mix 7 block-top4 / "
-                         "4 frame-local / 3 anchor+local / 2 dense per layer (seed 1+layer), block 64"),
+                         f"({N}), 16 heads, d 64, dim 1024, RoPE-2D + QK-LayerNorm, "
+                         + (f"head profile {os.path.basename(args.sparse_config)} (lazy dino top-4)"
+                            if args.sparse_config else
+                            "head mix 7 block-top4 / 4 frame-local / 3 anchor+local / 2 dense per layer "
+                            "(seed 1+layer), block 64")),
             "frames": args.frames, "tokens": N, "layers": args.layers, "heads": heads, "block": 64, "topk": 4,
             "parallelism": "single GPU",
         },
@@ -275,8 +299,9 @@ def main():
             "launch_ms": round(attn_ms_avg, 3),
         },
         "selection": dict(sel_extra, bound="hbm", peak=PEAK_HBM_GBS, unit="GB/s"),
+        "other_kernels_ms": other_ms,
     }
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and not args.sparse_config:
         result["cpu_baseline"] = cpu_baseline(pkg)
     print(json.dumps(result), flush=True)
 

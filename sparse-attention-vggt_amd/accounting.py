@@ -3,14 +3,15 @@ pattern, projection FLOP, and the bytes the block selection must move.
 
 Attention FLOP of a head = 4 * d * |allowed pairs| (QK^T and PV, 2 FLOP per multiply-add); padding
 slots and masked pairs are not counted. For block-dynamic heads the pairs are counted from the
-actual selection lists (the last patch block of a frame holds P - 64*(NBf-1) tokens).
+actual selection lists (the last patch block of a frame holds P - 64*(NBf-1) tokens); for key-set
+heads from the member count of their key set.
 """
 from __future__ import annotations
 
 import torch
 
 from .layout import BLOCK, HEAD_DIM, Geometry
-from .ops import ANCHOR, ANCHOR_LOCAL, BLOCK_DYNAMIC, DENSE, FRAME_LOCAL, SKIP, TOKEN_DYNAMIC
+from .ops import ANCHOR, ANCHOR_LOCAL, BLOCK_DYNAMIC, DENSE, FRAME_LOCAL, KEYSET, SKIP, TOKEN_DYNAMIC
 
 
 def block_population(geom: Geometry, block_ids: torch.Tensor) -> torch.Tensor:
@@ -30,7 +31,8 @@ def dynamic_pairs(geom: Geometry, sel: torch.Tensor) -> int:
     return int((keys * rows).sum().item()) + S * geom.tokens
 
 
-def head_pairs(pattern: int, geom: Geometry, sel: torch.Tensor | None = None, topk_width: int = 0) -> int:
+def head_pairs(pattern: int, geom: Geometry, sel: torch.Tensor | None = None, topk_width: int = 0,
+               keyset_count: int = 0) -> int:
     N, F, T = geom.tokens, geom.frames, geom.tokens_per_frame
     S = F * geom.num_special
     if pattern == DENSE:
@@ -47,19 +49,27 @@ def head_pairs(pattern: int, geom: Geometry, sel: torch.Tensor | None = None, to
         return dynamic_pairs(geom, sel)
     if pattern == TOKEN_DYNAMIC:
         return S * N + F * geom.patches * topk_width
+    if pattern == KEYSET:
+        return N * keyset_count
     raise ValueError(pattern)
 
 
-def attention_flops(patterns, geom: Geometry, sel: torch.Tensor | None = None, topk_width: int = 0) -> int:
-    """Sum over heads; ``sel`` holds one list per BLOCK_DYNAMIC head in head order."""
+def attention_flops(patterns, geom: Geometry, sel: torch.Tensor | None = None, topk_width: int = 0,
+                    keyset_counts=None) -> int:
+    """Sum over heads; ``sel`` holds one list per BLOCK_DYNAMIC head and ``keyset_counts`` one member
+    count per KEYSET head, each in head order."""
     total = 0
-    j = 0
+    j = jk = 0
     for p in patterns:
         s = None
+        c = 0
         if p == BLOCK_DYNAMIC:
             s = sel[j]
             j += 1
-        total += head_pairs(p, geom, s, topk_width)
+        elif p == KEYSET:
+            c = int(keyset_counts[jk])
+            jk += 1
+        total += head_pairs(p, geom, s, topk_width, c)
     return 4 * HEAD_DIM * total
 
 

@@ -260,9 +260,11 @@ def gather_attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, idx: torc
 def gather_attn_rows(qr, kr, vr, idx, idx_row_stride, n, topk, num_keys, scale, outr, keep=None):
     lib = _lib.load()
     scale = 1.0 / math.sqrt(HEAD_DIM) if scale is None else scale
+    _mark("gather_attn", "start")
     _lib.check(lib.saf3r_gather_attn_fwd(ctypes.byref(qr), ctypes.byref(kr), ctypes.byref(vr), _ptr(idx),
                                          idx_row_stride, n, topk, num_keys, float(scale), ctypes.byref(outr),
                                          _lib.stream_ptr()))
+    _mark("gather_attn", "end")
     return keep
 
 
@@ -283,8 +285,10 @@ def token_topk(q: torch.Tensor, k: torch.Tensor, frames: int, per_frame: int, to
         krows = rows(k)
     ke = min(topk, per_frame)
     idx = torch.empty(n_q, frames * ke, dtype=torch.int32, device=q.device)
+    _mark("token_topk", "start")
     _lib.check(lib.saf3r_token_topk(ctypes.byref(qrows), ctypes.byref(krows), n_q, frames, per_frame, topk,
                                     _ptr(idx), _lib.stream_ptr()))
+    _mark("token_topk", "end")
     return idx
 
 
@@ -344,9 +348,11 @@ def probe_scores(qp: torch.Tensor, kp: torch.Tensor, geom: Geometry, head_ids: S
     qbar = torch.empty(n, HEAD_DIM, dtype=torch.float32, device=dev)
     scores = torch.empty(n, geom.tokens, dtype=torch.float32, device=dev)
     scale = 1.0 / math.sqrt(HEAD_DIM) if scale is None else scale
+    _mark("probe", "start")
     _lib.check(lib.saf3r_probe_scores(_ptr(qp), _ptr(kp), geom.frames, geom.tokens_per_frame, geom.num_special,
                                       _ptr(hs), n, float(scale), _ptr(partial), _ptr(qbar), _ptr(scores),
                                       scores.stride(0), _lib.stream_ptr()))
+    _mark("probe", "end")
     return qbar, scores
 
 
@@ -365,9 +371,11 @@ def keyset_build(specs: Sequence[KeySetSpec], geom: Geometry, scores: torch.Tens
         if scores.dtype != torch.float32 or scores.shape[0] != n or scores.shape[1] < geom.tokens:
             raise ValueError("scores must be fp32 [n_specs, >= N]")
         scores = scores.contiguous()
+    _mark("keyset_build", "start")
     _lib.check(lib.saf3r_keyset_build(_ptr(scores), 0 if scores is None else scores.stride(0), n, _ptr(arr[0]),
                                       _ptr(arr[1]), _ptr(arr[2]), _ptr(arr[3]), geom.frames, geom.tokens_per_frame,
                                       geom.num_special, _ptr(idx), idx.stride(0), _ptr(count), _lib.stream_ptr()))
+    _mark("keyset_build", "end")
     return idx, count
 
 
@@ -383,7 +391,9 @@ def keyset_gather(kp: torch.Tensor, geom: Geometry, specs: Sequence[KeySetSpec],
     kc = torch.empty(n, cap, HEAD_DIM, dtype=torch.bfloat16, device=dev)
     vc = torch.empty(n, cap // 64, 64, 64, dtype=torch.bfloat16, device=dev)
     hs = torch.tensor([s.head for s in specs], dtype=torch.int32, device=dev)
+    _mark("keyset_gather", "start")
     _lib.check(lib.saf3r_keyset_gather(_ptr(kp), geom.frames, geom.tokens_per_frame, geom.num_special, _ptr(hs), n,
                                        _ptr(v), v_tok_stride, v_head_stride, _ptr(idx), idx.stride(0), _ptr(count),
                                        cap // 64, _ptr(kc), _ptr(vc), cap, _lib.stream_ptr()))
+    _mark("keyset_gather", "end")
     return KeySets(kc, vc, count, idx, cap)
