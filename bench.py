@@ -124,6 +124,26 @@ def cpu_baseline(pkg, frames=4, heads=16, repeats=5, budget_s=25.0):
     }
 
 
+def scores_path(ops, geom, n_dyn, reps=5):
+    """The scores-input selection path: per-frame top-4 of a synthetic fp32 block-score matrix
+    [n_dyn * NB, NB] (N(0,1) scores), the same shape the fused selection scores internally."""
+    nb = geom.num_blocks
+    s = torch.randn(n_dyn * nb, nb, device="cuda:0")
+    idx = ops.topk_from_scores(s, geom.frames, 4)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        idx = ops.topk_from_scores(s, geom.frames, 4)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    nbytes = s.numel() * 4 + idx.numel() * 4
+    del s
+    return {"scores_path_ms": round(ms, 4), "scores_path_GBs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+            "scores_path_frac": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+
+
 def calibrate_copy():
     """A plain elementwise copy (negation) of 2^28 fp32 values: 1 GiB read and 1 GiB written once."""
     dev = torch.device("cuda:0")
@@ -246,6 +266,10 @@ def main():
     attn_tflops = (sum(kernel_flops) * args.steps) / (sum(attn_ms) * 1e-3) / 1e12 if attn_ms else None
     n_dyn = sum(1 for p in tables[0] if p == ops.BLOCK_DYNAMIC)
     other_ms = {k: round(statistics.fmean(v), 4) for k, v in dur.items() if k not in ("sparse_attn",)}
+    if n_dyn:
+        sel_extra_scores = scores_path(ops, geom, n_dyn)
+    else:
+        sel_extra_scores = {}
     width = args.frames * min(4, geom.blocks_per_frame)
     sb = acc.selection_bytes(geom, n_dyn, width)
     pool_ms = dur.get("block_pool", [])
@@ -260,6 +284,7 @@ def main():
             "fused_path_GBs": round(sb["fused_path"] / ((statistics.fmean(pool_ms) + statistics.fmean(sel_ms)) * 1e-3) / 1e9, 1),
             "heads": n_dyn,
         }
+        sel_extra.update(sel_extra_scores)
     result = {
         "metric": "ms per global-attn layer + effective TFLOP/s, VGGT shape 128 frames bf16",
         "value": round(layer_flops / (ms_layer * 1e-3) / 1e12, 3),

@@ -7,6 +7,8 @@
 //      saf3r/patch/adaptive_block_value.py:16-24 (block mean over the real population).
 // Every fp32 result is produced in a fixed operation order (sequential sums, one division,
 // sequential fma), so it is bit-identical to that definition.
+#include <algorithm>
+
 #include "common.h"
 
 namespace saf3r {
@@ -95,8 +97,8 @@ __global__ __launch_bounds__(256) void block_pool_kernel(PoolParams p) {
 
 // ---------------------------------------------------------------------------------------
 // Top-k from a score matrix. Rows of up to kRowLds floats are staged in LDS with coalesced
-// 16-byte loads (one workgroup per row) and each thread then selects one frame; longer rows are
-// read directly, one thread per (row, frame).
+// 16-byte loads (as many rows per workgroup as keep its threads busy) and each thread then selects
+// one (row, frame); longer rows are read directly, one thread per (row, frame).
 // ---------------------------------------------------------------------------------------
 constexpr int kRowLds = 12288;
 
@@ -109,27 +111,44 @@ __device__ inline void select_frame(const float* sp, int C, int f, int ke, int32
     uint64_t x = ckey(sp[c], (uint32_t)c);
     if (x > a[K - 1]) topk_insert<K>(a, x);
   }
+  int32_t v[K];
 #pragma unroll
-  for (int t = 0; t < K; ++t)
-    if (t < ke) o[t] = a[t] ? (int32_t)(f * C + ckey_index(a[t])) : -1;
+  for (int t = 0; t < K; ++t) v[t] = a[t] ? (int32_t)(f * C + ckey_index(a[t])) : -1;
+  if (K >= 4 && ke == K && ((uintptr_t)o & 15) == 0) {
+    // whole 16-byte groups: one vector store each (consecutive frames are consecutive groups)
+#pragma unroll
+    for (int t = 0; t + 3 < K; t += 4) reinterpret_cast<u32x4*>(o)[t >> 2] = u32x4{(uint32_t)v[t], (uint32_t)v[t + 1],
+                                                                                     (uint32_t)v[t + 2], (uint32_t)v[t + 3]};
+  } else {
+#pragma unroll
+    for (int t = 0; t < K; ++t)
+      if (t < ke) o[t] = v[t];
+  }
 }
 
+// A workgroup stages `rpw` consecutive rows (contiguous in memory) with coalesced 16-byte loads
+// and then every thread selects one (row, frame): with F = 128 frames two rows keep all 256
+// threads busy.
 template <int K>
-__global__ __launch_bounds__(256) void topk_scores_row_kernel(const float* __restrict__ s, int F, int C, int ke,
-                                                              int32_t* __restrict__ idx) {
-  __shared__ __align__(16) float row[kRowLds];
-  const int64_t r = blockIdx.x;
+__global__ __launch_bounds__(256) void topk_scores_row_kernel(const float* __restrict__ s, int64_t nrows, int F,
+                                                              int C, int ke, int rpw, int32_t* __restrict__ idx) {
+  extern __shared__ __align__(16) float buf[];  // rpw * F * C floats (dynamic: sized per launch)
+  const int64_t r0 = (int64_t)blockIdx.x * rpw;
+  const int nr = (int)min((int64_t)rpw, nrows - r0);
   const int n = F * C;
-  const float* src = s + r * (int64_t)n;
-  if ((n & 3) == 0) {
-    for (int i = threadIdx.x; i < (n >> 2); i += 256)
-      reinterpret_cast<f32x4*>(row)[i] = reinterpret_cast<const f32x4*>(src)[i];
+  const int tot = nr * n;
+  const float* src = s + r0 * n;
+  if ((tot & 3) == 0 && ((r0 * n) & 3) == 0) {
+    for (int i = threadIdx.x; i < (tot >> 2); i += 256)
+      reinterpret_cast<f32x4*>(buf)[i] = reinterpret_cast<const f32x4*>(src)[i];
   } else {
-    for (int i = threadIdx.x; i < n; i += 256) row[i] = src[i];
+    for (int i = threadIdx.x; i < tot; i += 256) buf[i] = src[i];
   }
   __syncthreads();
-  for (int f = threadIdx.x; f < F; f += 256)
-    select_frame<K>(row + f * C, C, f, ke, idx + r * ((int64_t)F * ke) + (int64_t)f * ke);
+  for (int t = threadIdx.x; t < nr * F; t += 256) {
+    const int rr = t / F, f = t % F;
+    select_frame<K>(buf + rr * n + f * C, C, f, ke, idx + (r0 + rr) * ((int64_t)F * ke) + (int64_t)f * ke);
+  }
 }
 
 template <int K>
@@ -277,11 +296,16 @@ int dispatch_k(int k, Args... args) {
 template <int K>
 struct TopkScoresLaunch {
   static int run(const float* s, int64_t nrows, int F, int C, int ke, int32_t* idx, hipStream_t st) {
-    if ((int64_t)F * C <= kRowLds && nrows <= 0x7fffffff) {
-      hipLaunchKernelGGL(topk_scores_row_kernel<K>, dim3((unsigned)nrows), dim3(256), 0, st, s, F, C, ke, idx);
+    const int64_t n = (int64_t)F * C;
+    if (n <= kRowLds && nrows <= 0x7fffffff) {
+      const int rpw = (int)std::max<int64_t>(1, std::min<int64_t>(256 / std::max(F, 1), kRowLds / n));
+      const int64_t groups = (nrows + rpw - 1) / rpw;
+      const size_t lds = (size_t)rpw * n * sizeof(float);
+      hipLaunchKernelGGL(topk_scores_row_kernel<K>, dim3((unsigned)groups), dim3(256), lds, st, s, nrows, F, C, ke,
+                         rpw, idx);
     } else {
-      int64_t n = nrows * F;
-      hipLaunchKernelGGL(topk_scores_kernel<K>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, s, nrows, F, C,
+      const int64_t nt = nrows * F;
+      hipLaunchKernelGGL(topk_scores_kernel<K>, dim3((unsigned)((nt + 255) / 256)), dim3(256), 0, st, s, nrows, F, C,
                          ke, idx);
     }
     return check_launch("saf3r_topk_from_scores");
