@@ -1,0 +1,186 @@
+"""GPU parity at the full single-GPU shapes: 32 frames x 1374 tokens (43,968 tokens, 16 heads),
+128 frames x 1374 (175,872 tokens, 16 heads) and the DA3-Giant-style 96 frames x 1301 tokens
+(124,896 tokens, 24 heads, top-k 8).
+
+The oracle cannot attend every query row of these shapes in seconds, so each head is checked on a
+sample of rows (every special token and the first / last rows of the first, second and last
+blocks of four frames, the last row of those frames, plus seeded random rows) against the
+oracle's masked attention over all N keys, with the block lists the kernels produced. Those lists
+are themselves checked bit-exact against the oracle's selection for every dynamic head, and key
+sets against the oracle's key sets. Every row is covered by a property that needs no oracle: with
+Q = K = 0 all allowed keys get the same weight, so each output row is the mean of V over the
+keys its pattern allows, and block top-k over all-zero scores keeps the lowest blocks of each
+frame. Bars as everywhere: max-abs 2e-2, mean-abs 2e-3; indices bit-exact.
+"""
+import importlib
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as OA
+from oracle import selection as OS
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+ATOL_MAX, ATOL_MEAN = 2e-2, 2e-3
+
+
+@pytest.fixture(scope="module")
+def mods(pkg):
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    return tuple(importlib.import_module(pkg.__name__ + m) for m in (".ops", ".synth"))
+
+
+def _bits(x: torch.Tensor) -> np.ndarray:
+    return x.contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def _sample_rows(geom, n_random: int, seed: int) -> torch.Tensor:
+    T, ns, F = geom.tokens_per_frame, geom.num_special, geom.frames
+    picks = set()
+    for f in sorted({0, 1 % F, F // 2, F - 1}):
+        base = f * T
+        picks.update(base + i for i in range(ns))
+        for b in (0, 1, geom.blocks_per_frame - 1):
+            p0 = ns + 64 * b
+            picks.update((base + p0, base + min(T - 1, p0 + 63)))
+        picks.add(base + T - 1)
+    g = torch.Generator().manual_seed(seed)
+    picks.update(torch.randint(0, geom.tokens, (n_random,), generator=g).tolist())
+    return torch.tensor(sorted(picks))
+
+
+def _check_rows(out, q, k, v, patterns, og, sel_of, rows, what):
+    """Rows ``rows`` of every head of ``out`` ([N, H*64] on the GPU) against the oracle."""
+    H = len(patterns)
+    got = out[rows.to(out.device)].float().cpu().reshape(len(rows), H, 64)
+    for h, pat in enumerate(patterns):
+        mask = OA.allowed_mask(pat, rows, og, sel_of.get(h))
+        ref = OA.masked_attention(q[h][rows].float(), k[h].float(), v[h].float(), mask, dtype=torch.float32)
+        err = (got[:, h] - ref).abs()
+        print(f"{what} head {h} pattern {pat}: max {err.max().item():.3g} mean {err.mean().item():.3g}", flush=True)
+        assert err.max().item() <= ATOL_MAX and err.mean().item() <= ATOL_MEAN, f"{what} head {h}"
+
+
+def _run_selected_layer(ops, geom, q, k, v, patterns, k_sel):
+    qp, kp, vp = ops.pack_heads(q.to(DEV), k.to(DEV), v.to(DEV), geom)
+    dyn = [h for h, p in enumerate(patterns) if p == ops.BLOCK_DYNAMIC]
+    pq, pk = ops.block_pool(qp, kp, geom, dyn)
+    sel = ops.block_select(pq, pk, geom.frames, geom.blocks_per_frame, k_sel)
+    out = ops.sparse_attn_fwd(qp, kp, vp, geom, patterns, sel)
+    torch.cuda.synchronize()
+    return out, sel.cpu(), dyn
+
+
+def _structured_layer(ops, synth, frames, heads, tokens_per_frame, patterns, k_sel, seed, n_random):
+    wl = synth.structured_qkv(frames=frames, heads=heads, tokens_per_frame=tokens_per_frame, seed=0)
+    geom = wl.geom
+    q, k, v = (t.to(torch.bfloat16) for t in (wl.q, wl.k, wl.v))
+    del wl
+    out, sel, dyn = _run_selected_layer(ops, geom, q, k, v, patterns, k_sel)
+    print(f"F{frames} T{tokens_per_frame} H{heads}: layer ran, checking {len(dyn)} block lists", flush=True)
+    for i, h in enumerate(dyn):
+        want = OS.block_select(_bits(q[h]), _bits(k[h]), geom.frames, geom.tokens_per_frame, geom.num_special, k_sel)
+        assert np.array_equal(sel[i].numpy(), want), f"block list of head {h}"
+    og = OA.Geometry(geom.frames, geom.tokens_per_frame, geom.num_special)
+    rows = _sample_rows(geom, n_random, seed)
+    _check_rows(out, q, k, v, patterns, og, {h: sel[i] for i, h in enumerate(dyn)}, rows,
+                f"F{frames} T{tokens_per_frame}")
+
+
+def test_layer_32_frames(mods):
+    ops, synth = mods
+    _structured_layer(ops, synth, 32, 16, 1374, synth.seeded_patterns(16, seed=1), 4, seed=32, n_random=256)
+
+
+def test_layer_128_frames(mods):
+    ops, synth = mods
+    _structured_layer(ops, synth, 128, 16, 1374, synth.seeded_patterns(16, seed=1), 4, seed=128, n_random=192)
+
+
+def test_layer_da3_shape(mods):
+    ops, synth = mods
+    _structured_layer(ops, synth, 96, 24, 1301, synth.da3_patterns(24, seed=1), 8, seed=96, n_random=128)
+
+
+@pytest.mark.parametrize("frames,tokens_per_frame,k_sel", [(128, 1374, 4), (96, 1301, 8)])
+def test_uniform_weights_every_row(mods, pkg, frames, tokens_per_frame, k_sel):
+    """Q = K = 0: each output row is the plain mean of V over the keys its pattern allows."""
+    ops, synth = mods
+    geom = pkg.Geometry(frames, tokens_per_frame, 5)
+    patterns = [ops.DENSE, ops.FRAME_LOCAL, ops.ANCHOR_LOCAL, ops.BLOCK_DYNAMIC, ops.ANCHOR, ops.SKIP,
+                ops.BLOCK_DYNAMIC, ops.FRAME_LOCAL]
+    H, N, T, ns = len(patterns), geom.tokens, tokens_per_frame, 5
+    g = torch.Generator().manual_seed(frames)
+    v = torch.randn(H, N, 64, generator=g).to(torch.bfloat16)
+    zero = torch.zeros(H, N, 64, dtype=torch.bfloat16)
+    out, sel, dyn = _run_selected_layer(ops, geom, zero, zero, v, patterns, k_sel)
+    nbf = geom.blocks_per_frame
+    kb = min(k_sel, nbf)
+    lowest = (torch.arange(frames)[:, None] * nbf + torch.arange(kb)[None, :]).reshape(-1).to(torch.int32)
+    assert torch.equal(sel, lowest.expand_as(sel)), "zero scores keep the lowest blocks of each frame"
+    # expected means from per-frame sums in float64
+    vd = v.double().reshape(H, frames, T, 64)
+    fsum = vd.sum(2)                                   # [H, F, 64]
+    total = fsum.sum(1)                                # [H, 64]
+    sel_keys = vd[:, :, ns:ns + min(64 * kb, T - ns)]  # patch tokens of the kept blocks of every frame
+    sel_mean = sel_keys.sum((1, 2)) / (frames * sel_keys.shape[2])
+    got = out.float().cpu().reshape(frames, T, H, 64)
+    special = torch.arange(T) < ns
+    for h, pat in enumerate(patterns):
+        if pat == ops.DENSE:
+            want = (total[h] / N).expand(frames, T, 64)
+        elif pat == ops.FRAME_LOCAL:
+            want = (fsum[h] / T)[:, None, :].expand(frames, T, 64)
+        elif pat == ops.ANCHOR:
+            want = (fsum[h, 0] / T).expand(frames, T, 64)
+        elif pat == ops.ANCHOR_LOCAL:
+            m = (fsum[h, 0][None] + fsum[h]) / (2 * T)
+            m[0] = fsum[h, 0] / T
+            want = m[:, None, :].expand(frames, T, 64)
+        elif pat == ops.BLOCK_DYNAMIC:
+            want = torch.where(special[None, :, None], total[h] / N, sel_mean[h]).expand(frames, T, 64)
+        else:
+            want = torch.zeros(frames, T, 64, dtype=torch.float64)
+        err = (got[:, :, h].double() - want).abs()
+        print(f"uniform F{frames} head {h} pattern {pat}: max {err.max().item():.3g} mean {err.mean().item():.3g}",
+              flush=True)
+        assert err.max().item() <= ATOL_MAX and err.mean().item() <= ATOL_MEAN, f"head {h}"
+
+
+def test_keysets_128_frames(mods):
+    """stride and q_probe_topk heads of the reference profile's kinds at 175,872 tokens: key sets
+    bit-exact, sampled rows against the oracle."""
+    ops, synth = mods
+    wl = synth.structured_qkv(frames=128, heads=6, seed=3)
+    geom = wl.geom
+    n = geom.tokens
+    q, k, v = (t.to(torch.bfloat16) for t in (wl.q, wl.k, wl.v))
+    del wl
+    patterns = [ops.KEYSET, ops.KEYSET, ops.DENSE, ops.KEYSET, ops.FRAME_LOCAL, ops.KEYSET]
+    specs = [ops.KeySetSpec(0, ops.KEYSET_STRIDE, 4, 0, True), ops.KeySetSpec(1, ops.KEYSET_TOPK, n // 4, 0, False),
+             ops.KeySetSpec(3, ops.KEYSET_TOPK, 1024, 0, True), ops.KeySetSpec(5, ops.KEYSET_STRIDE, 4, 1, False)]
+    qp, kp, vp = ops.pack_heads(q.to(DEV), k.to(DEV), v.to(DEV), geom)
+    _, sc = ops.probe_scores(qp, kp, geom, [1, 3])
+    scores = torch.zeros(len(specs), n, device=DEV)
+    scores[1], scores[2] = sc[0], sc[1]
+    idx, count = ops.keyset_build(specs, geom, scores, DEV)
+    vnat = v.permute(1, 0, 2).contiguous().to(DEV)
+    ks = ops.keyset_gather(kp, geom, specs, vnat, len(patterns) * 64, 64, idx, count)
+    out = ops.sparse_attn_fwd(qp, kp, vp, geom, patterns, keysets=ks)
+    torch.cuda.synchronize()
+    del vnat
+    print("keyset layer ran at 128 frames", flush=True)
+    ks_of = {}
+    for i, s in enumerate(specs):
+        sco = None
+        if s.mode == ops.KEYSET_TOPK:
+            sco = OS.probe_scores(OS.probe_mean(_bits(q[s.head])), _bits(k[s.head]))
+        want = OS.keyset(sco, n, geom.tokens_per_frame, geom.num_special, s.mode, s.param, s.start, s.include)
+        c = int(count[i])
+        assert c == len(want) and np.array_equal(idx[i, :c].cpu().numpy(), want), f"key set of head {s.head}"
+        ks_of[s.head] = torch.from_numpy(want)
+    og = OA.Geometry(geom.frames, geom.tokens_per_frame, geom.num_special)
+    _check_rows(out, q, k, v, patterns, og, ks_of, _sample_rows(geom, 128, 7), "keysets F128")
