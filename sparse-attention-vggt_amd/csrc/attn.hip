@@ -244,14 +244,21 @@ __device__ __forceinline__ void attend(const char* __restrict__ kst, const char*
   }
 }
 
-// Key-tile sequence of a shared-mode group: four contiguous ranges (some possibly empty), walked
-// from step rot. Fixed fields only: a range array indexed at run time would live in scratch.
-struct TileSeq {
-  int s0, l0, s1, l1, s2, l2, s3, l3;
+// Key-tile walk of a shared-mode group: up to four contiguous tile ranges (empty ones skipped),
+// entered at any step and wrapping around. Patch tiles carry their block within the frame and
+// their frame, advanced incrementally, so a step costs a few scalar instructions and no division.
+// Every field is work-group uniform and lives in scalar registers.
+struct Walk {
+  int s0, l0, s1, l1, s2, l2, s3, l3;  // the ranges (length 0: empty)
   int count;
-  int rot;
-  // the ranges are work-group uniform; readfirstlane keeps them (and every at()) in scalar registers
-  __device__ inline void set(int a0, int b0, int a1, int b1, int a2, int b2, int a3, int b3) {
+  int r, kt, rem;  // current range, current tile, tiles left in the range from kt on
+  int b, f;        // patch tile: block within its frame, frame (b = -1 on special tiles)
+
+  // ranges are selected by value, never through an indexed array: an array indexed at run time
+  // would live in scratch memory, and values loaded from there count as per-lane values
+  __device__ inline int rs(int i) const { return i == 0 ? s0 : i == 1 ? s1 : i == 2 ? s2 : s3; }
+  __device__ inline int rl(int i) const { return i == 0 ? l0 : i == 1 ? l1 : i == 2 ? l2 : l3; }
+  __device__ inline void init(int a0, int b0, int a1, int b1, int a2, int b2, int a3, int b3) {
     s0 = __builtin_amdgcn_readfirstlane(a0);
     l0 = __builtin_amdgcn_readfirstlane(max(b0, 0));
     s1 = __builtin_amdgcn_readfirstlane(a1);
@@ -261,35 +268,64 @@ struct TileSeq {
     s3 = __builtin_amdgcn_readfirstlane(a3);
     l3 = __builtin_amdgcn_readfirstlane(max(b3, 0));
     count = l0 + l1 + l2 + l3;
-    rot = 0;
+    r = kt = rem = b = f = 0;
   }
-  __device__ inline int at(int n) const {
-    n += rot;
-    if (n >= count) n -= count;
-    if (n < l0) return s0 + n;
-    n -= l0;
-    if (n < l1) return s1 + n;
-    n -= l1;
-    if (n < l2) return s2 + n;
-    return s3 + (n - l2);
+  __device__ inline void locate(const Geom& g) {
+    if (kt >= g.nst) {
+      f = (kt - g.nst) / g.NBf;
+      b = kt - g.nst - f * g.NBf;
+    } else {
+      b = -1;
+      f = 0;
+    }
+  }
+  // position at step pos of the sequence (0 <= pos < count)
+  __device__ inline void seek(int pos, const Geom& g) {
+    r = 0;
+    while (pos >= rl(r)) {  // ends: pos < count
+      pos -= rl(r);
+      ++r;
+    }
+    kt = rs(r) + pos;
+    rem = rl(r) - pos;
+    locate(g);
+  }
+  __device__ inline void next(const Geom& g) {
+    if (--rem > 0) {
+      ++kt;
+      if (kt == g.nst) {
+        b = 0;
+        f = 0;
+      } else if (b >= 0 && ++b == g.NBf) {
+        b = 0;
+        ++f;
+      }
+    } else {
+      do r = (r + 1) & 3;
+      while (rl(r) == 0);  // ends: count > 0
+      kt = rs(r);
+      rem = rl(r);
+      locate(g);
+    }
+  }
+  // mask description of the current tile for a shared-mode query tile
+  __device__ inline TileMask mask(const Geom& g, int eff, bool frame_rel, bool qspecial) const {
+    TileMask tm;
+    tm.kt = kt;
+    tm.eff = eff;
+    tm.kspecial = kt < g.nst;
+    if (tm.kspecial) {
+      tm.kvalid = 64;
+      tm.kframe = 0;
+      tm.need = (kt + 1) * 64 > g.S || frame_rel;
+    } else {
+      tm.kframe = f;
+      tm.kvalid = b == g.NBf - 1 ? g.P - 64 * b : 64;
+      tm.need = tm.kvalid < 64 || (frame_rel && qspecial);
+    }
+    return tm;
   }
 };
-
-__device__ inline void tile_mask(const Geom& g, int kt, int eff, bool frame_rel, bool qspecial, TileMask& tm) {
-  tm.kt = kt;
-  tm.kspecial = kt < g.nst;
-  tm.eff = eff;
-  if (tm.kspecial) {
-    tm.kvalid = 64;
-    tm.kframe = 0;
-    tm.need = (kt + 1) * 64 > g.S || frame_rel;
-  } else {
-    const int b = (kt - g.nst) % g.NBf;
-    tm.kframe = (kt - g.nst) / g.NBf;
-    tm.kvalid = min(64, g.P - 64 * b);
-    tm.need = tm.kvalid < 64 || (frame_rel && qspecial);
-  }
-}
 
 __device__ inline void store_rows(const AttnParams& p, const Acc& A, const int64_t (&qtok)[2], int h, int half) {
 #pragma unroll
@@ -320,9 +356,13 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
   __shared__ int wcnt[4];
 
   const Geom& g = p.g;
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, w = tid >> 6, half = lane >> 5, col = lane & 31;
-  const int bid = blockIdx.x;
+  // the id builtins, not threadIdx / blockIdx: in a kernel this large the latter stay calls, whose
+  // results the compiler must treat as per-lane values, and everything derived from the work-group
+  // id (the whole work-item decode and key walk) would run on the vector unit
+  const int tid = __builtin_amdgcn_workitem_id_x();
+  const int lane = tid & 63, half = lane >> 5, col = lane & 31;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, uniform
+  const int bid = __builtin_amdgcn_workgroup_id_x();
 
   // ---- decode the work item (uniform) ----
   int oh = 0;
@@ -418,7 +458,7 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
     // for every other pattern, so neither carries the other's state in registers.
     auto shared_walk = [&](auto ks_tag) {
     // ---- key-tile sequence (uniform) ----
-    TileSeq seq;
+    Walk wk;
     bool frame_rel = false;
     constexpr bool keyset = decltype(ks_tag)::value;
     const int eff = (pat == SAF3R_DENSE || pat == SAF3R_TOKEN_DYNAMIC || pat == SAF3R_BLOCK_DYNAMIC || keyset)
@@ -428,9 +468,9 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
     int ks_keys = 0;
     if constexpr (keyset) ks_keys = __builtin_amdgcn_readfirstlane(p.ks_count[p.slot[h]]);
     if constexpr (keyset) {
-      seq.set(0, (ks_keys + 63) / 64, 0, 0, 0, 0, 0, 0);
+      wk.init(0, (ks_keys + 63) / 64, 0, 0, 0, 0, 0, 0);
     } else if (eff == SAF3R_DENSE) {
-      seq.set(0, g.NT, 0, 0, 0, 0, 0, 0);
+      wk.init(0, g.NT, 0, 0, 0, 0, 0, 0);
     } else {
       frame_rel = true;
       int f0, f1;
@@ -448,35 +488,44 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
       const int ls1 = has_sp ? ((f1 + 1) * g.ns - 1) / 64 : -1;
       const bool anc_sp = has_sp && need_anchor && !(need_local && ls0 == 0);
       const bool anc_pt = need_anchor && !(need_local && f0 == 0);
-      seq.set(0, anc_sp ? (g.ns - 1) / 64 + 1 : 0,
+      wk.init(0, anc_sp ? (g.ns - 1) / 64 + 1 : 0,
               ls0, (has_sp && need_local) ? ls1 - ls0 + 1 : 0,
               g.nst, anc_pt ? g.NBf : 0,
               g.nst + f0 * g.NBf, need_local ? (f1 - f0 + 1) * g.NBf : 0);
     }
-    const int count = seq.count;
+    const int count = wk.count;
+    int rot = 0;
     if (eff == SAF3R_DENSE && p.phase_dense > 0 && count > 0) {
       // one clock reading per work-group: the four waves share the ring and must agree
-      if (tid == 0) wcnt[0] = (int)((wall_clock64() / p.phase_dense) % (uint64_t)count);
+      if (tid == 0) wcnt[0] = (int)((__builtin_amdgcn_s_memrealtime() / p.phase_dense) % (uint64_t)count);
       __syncthreads();
-      seq.rot = __builtin_amdgcn_readfirstlane(wcnt[0]);  // an LDS value, uniform: keep the walk scalar
+      rot = __builtin_amdgcn_readfirstlane(wcnt[0]);  // an LDS value, uniform: keep the walk scalar
     }
+    if (count > 0) wk.seek(rot, g);
+    Walk wi = wk;  // the tiles to load run two steps ahead of the tiles consumed
 
-    // thread tid owns 16-byte chunks tid and tid + 256 of the K and the V tile; LDS chunk
-    // position P holds row P/8, global chunk (P % 8) ^ swz8(row)
-    auto issue = [&](int n) {
-      const int kt = seq.at(n);
-      char* st = ring + (n % kStages) * 16384;
-      const int64_t row0 = keyset ? (int64_t)p.slot[h] * p.ks_cap + (int64_t)kt * 64 : head_base + (int64_t)kt * 64;
-      const __bf16* kb = (keyset ? p.kc : p.k) + row0 * 64;
-      const __bf16* vb = (keyset ? p.vc : p.v) + row0 * 64;
+    // thread tid owns 16-byte chunks tid and tid + 256 of the K and the V tile (64 rows of 128 B,
+    // same offsets for both); LDS chunk position P holds row P/8, global chunk (P % 8) ^ swz8(row)
+    int dofs[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int P = tid + 256 * u, r = P >> 3;
+      dofs[u] = r * 128 + (((P & 7) ^ swz8(r)) << 4);
+    }
+    const char* kbase = keyset ? reinterpret_cast<const char*>(p.kc + (int64_t)p.slot[h] * p.ks_cap * 64)
+                               : reinterpret_cast<const char*>(p.k + head_base * 64);
+    const char* vbase = keyset ? reinterpret_cast<const char*>(p.vc + (int64_t)p.slot[h] * p.ks_cap * 64)
+                               : reinterpret_cast<const char*>(p.v + head_base * 64);
+    auto issue = [&](int stage) {
+      const char* kb = kbase + (int64_t)wi.kt * 8192;
+      const char* vb = vbase + (int64_t)wi.kt * 8192;
+      char* st = ring + stage * 16384 + 64 * w * 16;
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
-        const int P = tid + 256 * u, r = P >> 3, cg = (P & 7) ^ swz8(r);
-        __builtin_amdgcn_global_load_lds((const void*)(kb + r * 64 + cg * 8),
-                                         (lds_void*)(st + (256 * u + 64 * w) * 16), 16, 0, 0);
-        __builtin_amdgcn_global_load_lds((const void*)(vb + r * 64 + cg * 8),
-                                         (lds_void*)(st + 8192 + (256 * u + 64 * w) * 16), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((const void*)(kb + dofs[u]), (lds_void*)(st + 4096 * u), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((const void*)(vb + dofs[u]), (lds_void*)(st + 8192 + 4096 * u), 16, 0, 0);
       }
+      wi.next(g);
     };
 
     wait_vm<0>();  // Q fragments landed; from here vmcnt counts ring loads only
@@ -488,31 +537,29 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
       wait_vm<0>();
       barrier_only();
       if (!wactive) {
-        if (n + 2 < count) issue(n + 2);
-        if (n + 3 < count) issue(n + 3);
+        if (n + 2 < count) issue((n + 2) % kStages);
+        if (n + 3 < count) issue((n + 3) % kStages);
         continue;
       }
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
         if (n + u < count) {
-          const int kt = seq.at(n + u);
           TileMask tm;
           if constexpr (keyset) {
-            tm.kt = kt;
+            tm.kt = wk.kt;
             tm.kspecial = false;
             tm.kframe = 0;
             tm.eff = SAF3R_DENSE;
-            tm.kvalid = min(64, ks_keys - 64 * kt);
+            tm.kvalid = min(64, ks_keys - 64 * wk.kt);
             tm.need = tm.kvalid < 64;
           } else {
-            tile_mask(g, kt, eff, frame_rel, qspecial, tm);
+            tm = wk.mask(g, eff, frame_rel, qspecial);
           }
           const char* kst = ring + ((n + u) % kStages) * 16384;
           attend<2>(kst, kst + 8192, qfrag, A, frow, tm, g, 0, half, col, c, [&]() {
-            if (n + 2 + u < count) issue(n + 2 + u);
+            if (n + 2 + u < count) issue((n + 2 + u) % kStages);
           });
-        } else if (n + 2 + u < count) {
-          issue(n + 2 + u);
+          wk.next(g);
         }
       }
     }
@@ -525,7 +572,8 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
 
   // ================= split mode: one query tile, block list split across the four waves ======
   {
-    // compact the selection row into LDS (drop invalid entries, keep order)
+    // compact the selection row into LDS (drop invalid entries, keep order); an entry holds the
+    // key tile and the number of valid keys of its block: tile << 7 | valid (1..64)
     const int32_t* srow = p.sel + ((int64_t)p.slot[h] * ((int64_t)g.F * g.NBf) + (qt - g.nst)) * p.sel_width;
     int total = 0;
     for (int c0 = 0; c0 < p.sel_width; c0 += 256) {
@@ -538,7 +586,7 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
       __syncthreads();
       int off = total;
       for (int i = 0; i < w; ++i) off += wcnt[i];
-      if (ok && off + pre < kMaxList) list[off + pre] = g.nst + v;
+      if (ok && off + pre < kMaxList) list[off + pre] = ((g.nst + v) << 7) | min(64, g.P - 64 * (v % g.NBf));
       total += wcnt[0] + wcnt[1] + wcnt[2] + wcnt[3];
       __syncthreads();
     }
@@ -548,59 +596,71 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
     // frames together
     const int nw = total > w ? (total - w + 3) >> 2 : 0;
     int i0 = 0;
-    if (p.phase_split > 0 && nw > 0) i0 = (int)((wall_clock64() / p.phase_split) % (uint64_t)nw);
-    auto list_pos = [&](int i) {
+    if (p.phase_split > 0 && nw > 0) i0 = (int)((__builtin_amdgcn_s_memrealtime() / p.phase_split) % (uint64_t)nw);
+    i0 = __builtin_amdgcn_readfirstlane(i0);
+    auto entry = [&](int i) {
       int ii = i + i0;
       if (ii >= nw) ii -= nw;
-      return w + 4 * ii;
+      return __builtin_amdgcn_readfirstlane(list[w + 4 * ii]);
     };
 
-    // half-tile stream of this wave: (list position, half); a half is present when its first key
-    // is a valid key of the block
-    auto half_valid = [&](int kt, int hh) { return hh == 0 || g.P - 64 * ((kt - g.nst) % g.NBf) > 32; };
+    // half-tile stream of this wave: (entry, half); the second half of a block is present when
+    // the block has more than 32 valid keys. Per-lane byte offsets of the 16-byte chunks a lane
+    // moves: K half = 32 rows x 8 chunks, V half = 64 rows x 4 chunks of 128-byte rows.
+    int kofs[4], vofs[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int P = 64 * u + lane;
+      const int r = P >> 3, i = P >> 2;
+      kofs[u] = r * 128 + (((P & 7) ^ swz8(r)) << 4);
+      vofs[u] = i * 128 + (((P & 3) ^ swz4(i)) << 4);
+    }
+    const char* kbase = reinterpret_cast<const char*>(p.k + head_base * 64);
+    const char* vbase = reinterpret_cast<const char*>(p.v + head_base * 64);
     char* slots = ring + w * 16384;  // two 8 KB slots: K half (4 KB) + V half (4 KB)
-    auto issue = [&](int pos, int hh, int sl) {
-      const int kt = list[pos];
+    auto issue = [&](int e, int hh, int sl) {
+      const int64_t t = (int64_t)(e >> 7) * 8192;
+      const char* kb = kbase + t + hh * 4096;
+      const char* vb = vbase + t + hh * 64;
       char* st = slots + sl * 8192;
-      const __bf16* kb = p.k + (head_base + (int64_t)kt * 64 + 32 * hh) * 64;
-      const __bf16* vb = p.v + (head_base + (int64_t)kt * 64) * 64 + 32 * hh;
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        const int P = 64 * u + lane;
-        const int r = P >> 3, ck = (P & 7) ^ swz8(r);   // K half: 32 rows x 8 chunks
-        __builtin_amdgcn_global_load_lds((const void*)(kb + r * 64 + ck * 8), (lds_void*)(st + 64 * u * 16), 16, 0, 0);
-        const int i = P >> 2, cv = (P & 3) ^ swz4(i);   // V half: 64 rows x 4 chunks
-        __builtin_amdgcn_global_load_lds((const void*)(vb + i * 64 + cv * 8), (lds_void*)(st + 4096 + 64 * u * 16),
-                                         16, 0, 0);
+        __builtin_amdgcn_global_load_lds((const void*)(kb + kofs[u]), (lds_void*)(st + 64 * u * 16), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((const void*)(vb + vofs[u]), (lds_void*)(st + 4096 + 64 * u * 16), 16, 0, 0);
       }
     };
 
     wait_vm<0>();
     int i = 0, hh = 0, cur = 0;
-    if (nw > 0) issue(list_pos(0), 0, 0);
+    int e = nw > 0 ? entry(0) : 0;
+    if (nw > 0) issue(e, 0, 0);
     while (i < nw) {
-      const int pos = list_pos(i);
-      int ni = i, nhh;
-      if (hh == 0 && half_valid(list[pos], 1)) nhh = 1;
+      int ni = i, nhh, ne = e;
+      if (hh == 0 && (e & 127) > 32) nhh = 1;
       else {
         nhh = 0;
         ++ni;
+        if (ni < nw) ne = entry(ni);
       }
       const bool more = ni < nw;
       if (more) {
-        issue(list_pos(ni), nhh, cur ^ 1);
+        issue(ne, nhh, cur ^ 1);
         wait_vm<8>();
       } else {
         wait_vm<0>();
       }
-      const int kt = list[pos];
       TileMask tm;
-      tile_mask(g, kt, SAF3R_DENSE, false, false, tm);
+      tm.kt = e >> 7;
+      tm.kspecial = false;
+      tm.kframe = 0;
+      tm.eff = SAF3R_DENSE;
+      tm.kvalid = e & 127;
       tm.need = tm.kvalid < 32 * (hh + 1);
       const char* st = slots + cur * 8192;
       attend<1>(st, st + 4096, qfrag, A, frow, tm, g, 32 * hh, half, col, c, []() {});
       i = ni;
       hh = nhh;
+      e = ne;
       cur ^= 1;
     }
 
