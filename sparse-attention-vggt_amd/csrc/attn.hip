@@ -57,6 +57,7 @@ struct AttnParams {
   Geom g;
   int sel_width;
   float c;  // softmax scale * log2(e)
+  uint32_t nsmagic;  // ceil(2^32 / ns): frame of a special slot = umulhi(slot, nsmagic)
   uint64_t phase_dense;  // wall-clock ticks per key-tile step of a dense walk (0: fixed order)
   uint64_t phase_split;  // wall-clock ticks per list position of a split-mode wave (0: fixed order)
   const __bf16* kc;      // KEYSET heads: compact K [set][cap][64]
@@ -122,8 +123,8 @@ struct TileMask {
 template <int NKH, typename Hook>
 __device__ __forceinline__ void attend(const char* __restrict__ kst, const char* __restrict__ vst,
                                        const bf16x8 (&qfrag)[2][4], Acc& A, const int (&frow)[2],
-                                       const TileMask& tm, const Geom& g, int key0, int half, int col, float c,
-                                       Hook&& hook) {
+                                       const TileMask& tm, const Geom& g, uint32_t nsmagic, int key0, int half,
+                                       int col, float c, Hook&& hook) {
   f32x16 s[NKH][2];
   // S^T of the staged keys, masked; also re-run by the exact path below, which keeps s from
   // having to stay live next to P
@@ -150,9 +151,10 @@ __device__ __forceinline__ void attend(const char* __restrict__ kst, const char*
           bool ok;
           int fc;
           if (tm.kspecial) {
-            const int sl = tm.kt * 64 + key;
-            ok = sl < g.S;
-            fc = sl / g.ns;
+            // frame = slot / ns as a multiply-high with ceil(2^32 / ns), exact below 2^32 / ns
+            const uint32_t sl = (uint32_t)(tm.kt * 64 + key);
+            ok = sl < (uint32_t)g.S;
+            fc = (int)__umulhi(sl, nsmagic);
           } else {
             ok = key < tm.kvalid;
             fc = tm.kframe;
@@ -506,11 +508,12 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
 
     // thread tid owns 16-byte chunks tid and tid + 256 of the K and the V tile (64 rows of 128 B,
     // same offsets for both); LDS chunk position P holds row P/8, global chunk (P % 8) ^ swz8(row)
-    int dofs[2];
+    // (unsigned 32-bit offsets from a uniform base: the loads take the scalar-base address form)
+    uint32_t dofs[2];
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       const int P = tid + 256 * u, r = P >> 3;
-      dofs[u] = r * 128 + (((P & 7) ^ swz8(r)) << 4);
+      dofs[u] = (uint32_t)(r * 128 + (((P & 7) ^ swz8(r)) << 4));
     }
     const char* kbase = keyset ? reinterpret_cast<const char*>(p.kc + (int64_t)p.slot[h] * p.ks_cap * 64)
                                : reinterpret_cast<const char*>(p.k + head_base * 64);
@@ -556,7 +559,7 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
             tm = wk.mask(g, eff, frame_rel, qspecial);
           }
           const char* kst = ring + ((n + u) % kStages) * 16384;
-          attend<2>(kst, kst + 8192, qfrag, A, frow, tm, g, 0, half, col, c, [&]() {
+          attend<2>(kst, kst + 8192, qfrag, A, frow, tm, g, p.nsmagic, 0, half, col, c, [&]() {
             if (n + 2 + u < count) issue((n + 2 + u) % kStages);
           });
           wk.next(g);
@@ -607,13 +610,13 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
     // half-tile stream of this wave: (entry, half); the second half of a block is present when
     // the block has more than 32 valid keys. Per-lane byte offsets of the 16-byte chunks a lane
     // moves: K half = 32 rows x 8 chunks, V half = 64 rows x 4 chunks of 128-byte rows.
-    int kofs[4], vofs[4];
+    uint32_t kofs[4], vofs[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int P = 64 * u + lane;
       const int r = P >> 3, i = P >> 2;
-      kofs[u] = r * 128 + (((P & 7) ^ swz8(r)) << 4);
-      vofs[u] = i * 128 + (((P & 3) ^ swz4(i)) << 4);
+      kofs[u] = (uint32_t)(r * 128 + (((P & 7) ^ swz8(r)) << 4));
+      vofs[u] = (uint32_t)(i * 128 + (((P & 3) ^ swz4(i)) << 4));
     }
     const char* kbase = reinterpret_cast<const char*>(p.k + head_base * 64);
     const char* vbase = reinterpret_cast<const char*>(p.v + head_base * 64);
@@ -657,7 +660,7 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
       tm.kvalid = e & 127;
       tm.need = tm.kvalid < 32 * (hh + 1);
       const char* st = slots + cur * 8192;
-      attend<1>(st, st + 4096, qfrag, A, frow, tm, g, 32 * hh, half, col, c, []() {});
+      attend<1>(st, st + 4096, qfrag, A, frow, tm, g, p.nsmagic, 32 * hh, half, col, c, []() {});
       i = ni;
       hh = nhh;
       e = ne;
@@ -838,6 +841,9 @@ extern "C" int saf3r_sparse_attn_fwd(const void* q_packed, const void* k_packed,
   p.out = (__bf16*)out;
   p.out_stride = out_row_stride;
   p.c = scale * 1.4426950408889634f;
+  if (p.g.ns > 0 && (uint64_t)p.g.Sp * (uint64_t)p.g.ns >= 0x100000000ull)
+    return fail(SAF3R_ERR_UNSUPPORTED, "saf3r_sparse_attn_fwd: too many special tokens");
+  p.nsmagic = p.g.ns > 0 ? (uint32_t)((0x100000000ull + (uint64_t)p.g.ns - 1) / (uint64_t)p.g.ns) : 0u;
   set_phase(&p);
   int idx[kMaxHeads];
   for (int h = 0; h < num_heads; ++h) idx[h] = h;
