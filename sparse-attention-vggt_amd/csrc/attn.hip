@@ -44,6 +44,7 @@ namespace saf3r {
 constexpr int kRing = 65536;     // LDS arena shared by both modes
 constexpr int kStages = 4;       // shared mode: 4 x 16 KB
 constexpr int kMaxList = 3968;   // compacted block list of a split-mode tile
+constexpr int kMaxSegs = 2 * kMaxHeads;
 
 enum ItemKind { kShared = 0, kSplit = 1, kSkip = 2 };
 
@@ -64,9 +65,13 @@ struct AttnParams {
   const __bf16* vc;      // KEYSET heads: compact transposed V tiles [set][cap/64][64][64]
   const int32_t* ks_count;
   int64_t ks_cap;
+  // work items in segments of one head each (a head has at most two: special-row and patch-row
+  // items), ordered longest item first; segment i covers blocks item_start[i] .. item_start[i+1]-1
+  // and items item_base[i] ... of head order[i]
   int n_order;
-  int order[kMaxHeads];
-  int item_start[kMaxHeads + 1];
+  int16_t order[kMaxSegs];
+  int item_start[kMaxSegs + 1];
+  int item_base[kMaxSegs];
   int8_t pattern[kMaxHeads];
   int8_t slot[kMaxHeads];
 };
@@ -371,7 +376,7 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
   while (oh + 1 < p.n_order && bid >= p.item_start[oh + 1]) ++oh;
   const int h = p.order[oh];
   const int pat = p.pattern[h];
-  const int it = bid - p.item_start[oh];
+  const int it = bid - p.item_start[oh] + p.item_base[oh];
   const int ns4 = (g.nst + 3) >> 2;
   const int groups_pf = (g.NBf + 3) >> 2;
   int qt0, nw, kind;
@@ -738,30 +743,37 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
   }
 }
 
-// Work items of a head and their relative cost, used to order heads longest-first.
-static int head_items(int pat, const Geom& g) {
-  const int ns4 = (g.nst + 3) / 4, groups_pf = (g.NBf + 3) / 4;
-  switch (pat) {
-    case SAF3R_DENSE:
-    case SAF3R_KEYSET:
-    case SAF3R_SKIP: return (g.NT + 3) / 4;
-    case SAF3R_TOKEN_DYNAMIC: return ns4;
-    case SAF3R_BLOCK_DYNAMIC: return ns4 + g.F * g.NBf;
-    default: return g.nst + g.F * groups_pf;
-  }
-}
+// Work items of a head, in up to two segments of similar items, with the number of key-tile steps
+// one item walks (its duration); the launch orders segments longest item first, so the long walks
+// (dense rows, special rows of the frame patterns) do not start last and leave a tail.
+struct Seg {
+  int h, base, items;
+  int64_t steps;
+};
 
-static int64_t item_cost(int pat, const Geom& g, int sel_width, int64_t ks_cap) {
+static int head_segments(int h, int pat, const Geom& g, int sel_width, int64_t ks_cap, Seg* out) {
+  const int ns4 = (g.nst + 3) / 4, groups_pf = (g.NBf + 3) / 4;
+  int n = 0;
+  auto add = [&](int base, int items, int64_t steps) {
+    if (items > 0) out[n++] = Seg{h, base, items, steps};
+  };
   switch (pat) {
-    case SAF3R_DENSE:
-    case SAF3R_TOKEN_DYNAMIC: return 4LL * g.NT;
-    case SAF3R_KEYSET: return 4LL * (ks_cap / 64);
-    case SAF3R_BLOCK_DYNAMIC: return sel_width;
-    case SAF3R_ANCHOR_LOCAL: return 8LL * (g.NBf + 1);
-    case SAF3R_FRAME_LOCAL:
-    case SAF3R_ANCHOR: return 4LL * (g.NBf + 1);
-    default: return 0;
+    case SAF3R_DENSE: add(0, (g.NT + 3) / 4, g.NT); break;
+    case SAF3R_KEYSET: add(0, (g.NT + 3) / 4, ks_cap / 64); break;
+    case SAF3R_SKIP: add(0, (g.NT + 3) / 4, 1); break;
+    case SAF3R_TOKEN_DYNAMIC: add(0, ns4, g.NT); break;
+    case SAF3R_BLOCK_DYNAMIC:
+      add(0, ns4, g.NT);
+      add(ns4, g.F * g.NBf, max(1, sel_width / 2));
+      break;
+    default: {  // frame-relative patterns: one special tile per item, four patch tiles per item
+      const int64_t mult = pat == SAF3R_ANCHOR_LOCAL ? 2 : 1;
+      const int64_t span = pat == SAF3R_ANCHOR ? 1 : (g.ns > 0 ? (64 + g.ns - 1) / g.ns + 1 : 1);
+      add(0, g.nst, span * (g.NBf + 1) * mult);
+      add(g.nst, g.F * groups_pf, (g.NBf + 1) * mult);
+    }
   }
+  return n;
 }
 
 // Clock phases of the key walks. Defaults are the measured time per step at the 128-frame VGGT
@@ -845,31 +857,30 @@ extern "C" int saf3r_sparse_attn_fwd(const void* q_packed, const void* k_packed,
     return fail(SAF3R_ERR_UNSUPPORTED, "saf3r_sparse_attn_fwd: too many special tokens");
   p.nsmagic = p.g.ns > 0 ? (uint32_t)((0x100000000ull + (uint64_t)p.g.ns - 1) / (uint64_t)p.g.ns) : 0u;
   set_phase(&p);
-  int idx[kMaxHeads];
-  for (int h = 0; h < num_heads; ++h) idx[h] = h;
-  for (int i = 1; i < num_heads; ++i) {
-    int x = idx[i], j = i;
-    int64_t cx = item_cost(p.pattern[x], p.g, sel_width, keyset_capacity);
-    while (j > 0 && item_cost(p.pattern[idx[j - 1]], p.g, sel_width, keyset_capacity) < cx) {
-      idx[j] = idx[j - 1];
+  Seg segs[kMaxSegs];
+  int nseg = 0;
+  for (int h = 0; h < num_heads; ++h)
+    nseg += head_segments(h, p.pattern[h], p.g, sel_width, keyset_capacity, segs + nseg);
+  for (int i = 1; i < nseg; ++i) {  // stable: longest item first
+    const Seg x = segs[i];
+    int j = i;
+    while (j > 0 && segs[j - 1].steps < x.steps) {
+      segs[j] = segs[j - 1];
       --j;
     }
-    idx[j] = x;
+    segs[j] = x;
   }
   int64_t total = 0;
-  p.n_order = 0;
-  for (int i = 0; i < num_heads; ++i) {
-    int h = idx[i];
-    int items = head_items(p.pattern[h], p.g);
-    if (items == 0) continue;
-    p.order[p.n_order] = h;
-    p.item_start[p.n_order] = (int)total;
-    ++p.n_order;
-    total += items;
+  p.n_order = nseg;
+  for (int i = 0; i < nseg; ++i) {
+    p.order[i] = (int16_t)segs[i].h;
+    p.item_start[i] = (int)total;
+    p.item_base[i] = segs[i].base;
+    total += segs[i].items;
+    if (total > 0x7fffffff) return fail(SAF3R_ERR_UNSUPPORTED, "saf3r_sparse_attn_fwd: too many work items");
   }
   p.item_start[p.n_order] = (int)total;
   if (total == 0) return SAF3R_OK;
-  if (total > 0x7fffffff) return fail(SAF3R_ERR_UNSUPPORTED, "saf3r_sparse_attn_fwd: too many work items");
   hipLaunchKernelGGL(sparse_attn_kernel, dim3((unsigned)total), dim3(256), 0, (hipStream_t)stream, p);
   return check_launch("saf3r_sparse_attn_fwd");
 }
