@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define SAF3R_ABI_VERSION 2
+#define SAF3R_ABI_VERSION 3
 
 enum saf3r_status {
   SAF3R_OK = 0,
@@ -58,8 +58,11 @@ enum saf3r_pattern {
                               patch rows go through saf3r_gather_attn_fwd.  ref: sparse_attention.py:189-231 */
   SAF3R_ANCHOR = 5,        /* frame(j) == 0.                      ref: sparse_attention.py:134-140 (all_to_first) */
   SAF3R_SKIP = 6,          /* output zero.                        ref: sparse_attention.py:40-41 */
-  SAF3R_KEYSET = 7         /* j in the head's shared key set (saf3r_keyset_build / _gather).
+  SAF3R_KEYSET = 7,        /* j in the head's shared key set (saf3r_keyset_build / _gather).
                               ref: sparse_attention.py:256-273 (stride), :143-186 (q_probe_topk) */
+  SAF3R_BROADCAST = 8      /* frame 0's attention map applied to every frame: the row of token
+                              f*T + i is sum_j softmax_j(q[i] . k[j] * scale) v[f*T + j], i, j < T.
+                              ref: sparse_attention.py:110-131 (broadcast_first) */
 };
 
 /* Key-set kinds of saf3r_keyset_build. */
@@ -196,16 +199,24 @@ int saf3r_keyset_gather(const void* k_packed, int frames, int tokens_per_frame, 
  *   keyset_k / keyset_v / keyset_count / keyset_capacity: the saf3r_keyset_gather buffers of the
  *        KEYSET heads, set s serving the s-th KEYSET head in increasing head order; every query of
  *        such a head attends keys 0 .. keyset_count[s]-1. NULL / 0 when no head is KEYSET.
+ *   bcast_q / bcast_k / bcast_v: frame 0 and per-frame buffers of the BROADCAST heads, b-th buffer
+ *        for the b-th BROADCAST head in increasing head order, C = ceil(T/64)*64 rows per frame:
+ *          bcast_q: bf16 [n_broadcast][C][64], row i = packed Q of token i (frame 0), zeros past T;
+ *          bcast_k: bf16 [n_broadcast][C][64], the same for K;
+ *          bcast_v: bf16 [n_broadcast][F][C/64] key-set V tiles (saf3r_keyset_gather layout) of
+ *                   frame f's tokens f*T .. f*T+T-1.
+ *        NULL when no head is BROADCAST.
  * Replaces: the per-head loop saf3r/patch/wrapper.py:94-106 and the mode implementations of
  *           saf3r/patch/sparse_attention.py:12-90 for full / global_to_frame / all_to_first / skip /
- *           stride / q_probe_topk (over their key sets), the dense special rows of dino_topk
- *           (:197-208), and the block-dynamic pattern.
+ *           stride / q_probe_topk (over their key sets) / broadcast_first, the dense special rows of
+ *           dino_topk (:197-208), and the block-dynamic pattern.
  */
 int saf3r_sparse_attn_fwd(const void* q_packed, const void* k_packed, const void* v_packed, int frames,
                           int tokens_per_frame, int num_special, int num_heads, const int32_t* head_pattern,
                           const int32_t* sel, int sel_width, float scale, void* out, int64_t out_row_stride,
                           const void* keyset_k, const void* keyset_v, const int32_t* keyset_count,
-                          int64_t keyset_capacity, void* stream);
+                          int64_t keyset_capacity, const void* bcast_q, const void* bcast_k,
+                          const void* bcast_v, void* stream);
 
 /*
  * Gather attention: out[r] = sum_j softmax_j(q[r] . k[idx[r][j]] * scale) v[idx[r][j]], fp32

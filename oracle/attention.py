@@ -23,6 +23,9 @@ Patterns (per head; mask M[i, j] = 1 iff query i may attend key j):
   KEYSET         j in one key set shared by every query of the head (``stride``, ``:256-273``;
                  ``q_probe_topk``, ``:143-186``; the set itself comes from
                  ``oracle.selection.keyset``)
+  BROADCAST      ``broadcast_first`` (``:110-131``): frame 0's attention map applied to every frame,
+                 row f*T + i = sum_j softmax_j(q_i . k_j / sqrt(d)) v_{f*T + j}, i, j < T (not a mask
+                 over the row's own q; see :func:`broadcast_attention`)
 Scores are q.k / sqrt(d); softmax in the working precision; rows are independent.
 """
 from __future__ import annotations
@@ -32,7 +35,7 @@ from dataclasses import dataclass
 
 import torch
 
-DENSE, FRAME_LOCAL, ANCHOR_LOCAL, BLOCK_DYNAMIC, TOKEN_DYNAMIC, ANCHOR, SKIP, KEYSET = range(8)
+DENSE, FRAME_LOCAL, ANCHOR_LOCAL, BLOCK_DYNAMIC, TOKEN_DYNAMIC, ANCHOR, SKIP, KEYSET, BROADCAST = range(9)
 
 
 @dataclass(frozen=True)
@@ -176,6 +179,16 @@ def token_dynamic_attention(q, k, v, est_topk_idx, g: Geometry, sp2sp_stride=1, 
     return out
 
 
+def broadcast_attention(q, k, v, g: Geometry, dtype=torch.float64):
+    """Reference ``broadcast_anchorframe_attention`` (``saf3r/patch/sparse_attention.py:110-131``):
+    A = softmax(q0 k0^T / sqrt(d)) over frame 0's T tokens, then out_f = A v_f for every frame f."""
+    T, d = g.tokens_per_frame, q.shape[-1]
+    q0, k0 = q[:T].to(dtype), k[:T].to(dtype)
+    a = torch.softmax((q0 @ k0.T) / math.sqrt(d), dim=-1)  # [T, T]
+    vf = v.to(dtype).reshape(g.frames, T, v.shape[-1])
+    return (a[None] @ vf).reshape(g.tokens, v.shape[-1])
+
+
 def sparse_attention_gathered(q, k, v, pattern, g: Geometry, sel=None, dtype=torch.float32,
                               chunk=4096):
     """Same result as :func:`pattern_attention`, computed on restricted key sets (cost follows
@@ -192,6 +205,8 @@ def sparse_attention_gathered(q, k, v, pattern, g: Geometry, sel=None, dtype=tor
 
     if pattern == SKIP:
         return torch.zeros(n, v.shape[1], dtype=dtype)
+    if pattern == BROADCAST:
+        return broadcast_attention(q, k, v, g, dtype)
     if pattern == DENSE:
         for s0 in range(0, n, chunk):
             attend(slice(s0, min(n, s0 + chunk)), slice(0, n))
@@ -297,6 +312,8 @@ def head_outputs(q, k, v, patterns, g: Geometry, sel_by_head=None, est_topk_idx=
         sel = None if sel_by_head is None else sel_by_head.get(h)
         if pat == TOKEN_DYNAMIC:
             o = token_dynamic_attention(q[h], k[h], v[h], est_topk_idx, g, dtype=dtype)
+        elif pat == BROADCAST:
+            o = broadcast_attention(q[h], k[h], v[h], g, dtype=dtype)
         elif gathered:
             o = sparse_attention_gathered(q[h], k[h], v[h], pat, g, sel, dtype=dtype)
         else:

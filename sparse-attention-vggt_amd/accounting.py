@@ -11,7 +11,7 @@ from __future__ import annotations
 import torch
 
 from .layout import BLOCK, HEAD_DIM, Geometry
-from .ops import ANCHOR, ANCHOR_LOCAL, BLOCK_DYNAMIC, DENSE, FRAME_LOCAL, KEYSET, SKIP, TOKEN_DYNAMIC
+from .ops import ANCHOR, ANCHOR_LOCAL, BLOCK_DYNAMIC, BROADCAST, DENSE, FRAME_LOCAL, KEYSET, SKIP, TOKEN_DYNAMIC
 
 
 def block_population(geom: Geometry, block_ids: torch.Tensor) -> torch.Tensor:
@@ -51,6 +51,8 @@ def head_pairs(pattern: int, geom: Geometry, sel: torch.Tensor | None = None, to
         return S * N + F * geom.patches * topk_width
     if pattern == KEYSET:
         return N * keyset_count
+    if pattern == BROADCAST:  # every row weighs frame 0's T keys (its scores taken from frame 0)
+        return F * T * T
     raise ValueError(pattern)
 
 

@@ -65,6 +65,10 @@ struct AttnParams {
   const __bf16* vc;      // KEYSET heads: compact transposed V tiles [set][cap/64][64][64]
   const int32_t* ks_count;
   int64_t ks_cap;
+  const __bf16* bq;      // BROADCAST heads: frame 0 Q rows [head][bcap][64]
+  const __bf16* bk;      // BROADCAST heads: frame 0 K rows [head][bcap][64]
+  const __bf16* bv;      // BROADCAST heads: V tiles [head][frame][bcap/64][64][64]
+  int bcap;              // ceil(T/64)*64
   // work items in segments of one head each (a head has at most two: special-row and patch-row
   // items), ordered longest item first; segment i covers blocks item_start[i] .. item_start[i+1]-1
   // and items item_base[i] ... of head order[i]
@@ -380,10 +384,18 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
   const int ns4 = (g.nst + 3) >> 2;
   const int groups_pf = (g.NBf + 3) >> 2;
   int qt0, nw, kind;
+  int bfr = 0;  // BROADCAST: the frame whose rows the item writes
   if (pat == SAF3R_DENSE || pat == SAF3R_SKIP || pat == SAF3R_KEYSET) {
     qt0 = 4 * it;
     nw = min(4, g.NT - qt0);
     kind = pat == SAF3R_SKIP ? kSkip : kShared;
+  } else if (pat == SAF3R_BROADCAST) {
+    // query tile qt of frame 0's compact rows, written for frame bfr
+    const int nq = p.bcap / 64, gpf = (nq + 3) >> 2;
+    bfr = it / gpf;
+    qt0 = 4 * (it - bfr * gpf);
+    nw = min(4, nq - qt0);
+    kind = kShared;
   } else if (pat == SAF3R_TOKEN_DYNAMIC || (pat == SAF3R_BLOCK_DYNAMIC && it < ns4)) {
     qt0 = 4 * it;
     nw = min(4, g.nst - qt0);
@@ -404,7 +416,7 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
   }
   const bool wactive = w < nw;
   const int qt = kind == kSplit ? qt0 : qt0 + (wactive ? w : 0);
-  const bool qspecial = qt < g.nst;
+  const bool qspecial = pat != SAF3R_BROADCAST && qt < g.nst;
   const int qf = qspecial ? 0 : (qt - g.nst) / g.NBf;
   const int qb = qspecial ? 0 : (qt - g.nst) % g.NBf;
   const bool writer = kind == kSplit ? true : wactive;
@@ -414,7 +426,11 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
 #pragma unroll
   for (int gq = 0; gq < 2; ++gq) {
     const int r = 32 * gq + col;
-    if (qspecial) {
+    if (pat == SAF3R_BROADCAST) {
+      const int i = qt * 64 + r;
+      qtok[gq] = (writer && i < g.T) ? (int64_t)bfr * g.T + i : -1;
+      frow[gq] = bfr;
+    } else if (qspecial) {
       const int64_t sl = (int64_t)qt * 64 + r;
       qtok[gq] = (writer && sl < g.S) ? (sl / g.ns) * g.T + sl % g.ns : -1;
       frow[gq] = g.ns > 0 ? (int)(sl / g.ns) : 0;
@@ -443,10 +459,10 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
 
   // ---- Q fragments: lane holds features 32*half .. 32*half+31 of rows 32*gq + col ----
   bf16x8 qfrag[2][4];
+  const __bf16* qrows = pat == SAF3R_BROADCAST ? p.bq + (int64_t)p.slot[h] * p.bcap * 64 : p.q + head_base * 64;
 #pragma unroll
   for (int gq = 0; gq < 2; ++gq) {
-    const u32x4* qsrc =
-        reinterpret_cast<const u32x4*>(p.q + (head_base + (int64_t)qt * 64 + 32 * gq + col) * 64 + 32 * half);
+    const u32x4* qsrc = reinterpret_cast<const u32x4*>(qrows + ((int64_t)qt * 64 + 32 * gq + col) * 64 + 32 * half);
 #pragma unroll
     for (int s = 0; s < 4; ++s) qfrag[gq][s] = __builtin_bit_cast(bf16x8, qsrc[s]);
   }
@@ -471,9 +487,11 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
     const int eff = (pat == SAF3R_DENSE || pat == SAF3R_TOKEN_DYNAMIC || pat == SAF3R_BLOCK_DYNAMIC || keyset)
                         ? SAF3R_DENSE
                         : pat;
-    // KEYSET heads walk the compact tiles of their key set; key k of the set is slot k there
+    // KEYSET heads walk the compact tiles of their key set, key k of the set being slot k there;
+    // BROADCAST heads walk frame 0's compact K with the V tiles of the item's frame
     int ks_keys = 0;
-    if constexpr (keyset) ks_keys = __builtin_amdgcn_readfirstlane(p.ks_count[p.slot[h]]);
+    if constexpr (keyset)
+      ks_keys = __builtin_amdgcn_readfirstlane(pat == SAF3R_BROADCAST ? g.T : p.ks_count[p.slot[h]]);
     if constexpr (keyset) {
       wk.init(0, (ks_keys + 63) / 64, 0, 0, 0, 0, 0, 0);
     } else if (eff == SAF3R_DENSE) {
@@ -520,10 +538,17 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
       const int P = tid + 256 * u, r = P >> 3;
       dofs[u] = (uint32_t)(r * 128 + (((P & 7) ^ swz8(r)) << 4));
     }
-    const char* kbase = keyset ? reinterpret_cast<const char*>(p.kc + (int64_t)p.slot[h] * p.ks_cap * 64)
-                               : reinterpret_cast<const char*>(p.k + head_base * 64);
-    const char* vbase = keyset ? reinterpret_cast<const char*>(p.vc + (int64_t)p.slot[h] * p.ks_cap * 64)
-                               : reinterpret_cast<const char*>(p.v + head_base * 64);
+    const char* kbase = reinterpret_cast<const char*>(p.k + head_base * 64);
+    const char* vbase = reinterpret_cast<const char*>(p.v + head_base * 64);
+    if constexpr (keyset) {
+      if (pat == SAF3R_BROADCAST) {
+        kbase = reinterpret_cast<const char*>(p.bk + (int64_t)p.slot[h] * p.bcap * 64);
+        vbase = reinterpret_cast<const char*>(p.bv + ((int64_t)p.slot[h] * g.F + bfr) * p.bcap * 64);
+      } else {
+        kbase = reinterpret_cast<const char*>(p.kc + (int64_t)p.slot[h] * p.ks_cap * 64);
+        vbase = reinterpret_cast<const char*>(p.vc + (int64_t)p.slot[h] * p.ks_cap * 64);
+      }
+    }
     auto issue = [&](int stage) {
       const char* kb = kbase + (int64_t)wi.kt * 8192;
       const char* vb = vbase + (int64_t)wi.kt * 8192;
@@ -573,7 +598,7 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
     }
     store_rows(p, A, qtok, h, half);
     };
-    if (pat == SAF3R_KEYSET) shared_walk(std::true_type{});
+    if (pat == SAF3R_KEYSET || pat == SAF3R_BROADCAST) shared_walk(std::true_type{});
     else shared_walk(std::false_type{});
     return;
   }
@@ -760,6 +785,11 @@ static int head_segments(int h, int pat, const Geom& g, int sel_width, int64_t k
   switch (pat) {
     case SAF3R_DENSE: add(0, (g.NT + 3) / 4, g.NT); break;
     case SAF3R_KEYSET: add(0, (g.NT + 3) / 4, ks_cap / 64); break;
+    case SAF3R_BROADCAST: {
+      const int nq = (g.T + 63) / 64;
+      add(0, g.F * ((nq + 3) / 4), nq);
+      break;
+    }
     case SAF3R_SKIP: add(0, (g.NT + 3) / 4, 1); break;
     case SAF3R_TOKEN_DYNAMIC: add(0, ns4, g.NT); break;
     case SAF3R_BLOCK_DYNAMIC:
@@ -808,7 +838,8 @@ extern "C" int saf3r_sparse_attn_fwd(const void* q_packed, const void* k_packed,
                                      int tokens_per_frame, int num_special, int num_heads,
                                      const int32_t* head_pattern, const int32_t* sel, int sel_width, float scale,
                                      void* out, int64_t out_row_stride, const void* keyset_k, const void* keyset_v,
-                                     const int32_t* keyset_count, int64_t keyset_capacity, void* stream) {
+                                     const int32_t* keyset_count, int64_t keyset_capacity, const void* bcast_q,
+                                     const void* bcast_k, const void* bcast_v, void* stream) {
   if (int e = injected("saf3r_sparse_attn_fwd")) return e;
   AttnParams p;
   if (!make_geom(frames, tokens_per_frame, num_special, &p.g))
@@ -819,14 +850,27 @@ extern "C" int saf3r_sparse_attn_fwd(const void* q_packed, const void* k_packed,
     return fail(SAF3R_ERR_INVALID, "saf3r_sparse_attn_fwd: null pointer");
   if (((uintptr_t)out % 16) || (out_row_stride % 8) || out_row_stride < (int64_t)num_heads * 64)
     return fail(SAF3R_ERR_INVALID, "saf3r_sparse_attn_fwd: out must be 16-byte aligned with row stride >= H*64, %% 8");
-  int n_dyn = 0, n_ks = 0;
+  int n_dyn = 0, n_ks = 0, n_bc = 0;
   for (int h = 0; h < num_heads; ++h) {
     int pt = head_pattern[h];
-    if (pt < SAF3R_DENSE || pt > SAF3R_KEYSET)
+    if (pt < SAF3R_DENSE || pt > SAF3R_BROADCAST)
       return fail(SAF3R_ERR_INVALID, "saf3r_sparse_attn_fwd: head %d has unknown pattern %d", h, pt);
     p.pattern[h] = (int8_t)pt;
-    p.slot[h] = (int8_t)(pt == SAF3R_BLOCK_DYNAMIC ? n_dyn++ : pt == SAF3R_KEYSET ? n_ks++ : -1);
+    p.slot[h] = (int8_t)(pt == SAF3R_BLOCK_DYNAMIC ? n_dyn++
+                         : pt == SAF3R_KEYSET      ? n_ks++
+                         : pt == SAF3R_BROADCAST   ? n_bc++
+                                                   : -1);
   }
+  if (n_bc > 0) {
+    if (!bcast_q || !bcast_k || !bcast_v)
+      return fail(SAF3R_ERR_INVALID, "saf3r_sparse_attn_fwd: BROADCAST heads need the frame-0 and per-frame buffers");
+    if (((uintptr_t)bcast_q | (uintptr_t)bcast_k | (uintptr_t)bcast_v) % 16)
+      return fail(SAF3R_ERR_INVALID, "saf3r_sparse_attn_fwd: broadcast buffers must be 16-byte aligned");
+  }
+  p.bq = (const __bf16*)bcast_q;
+  p.bk = (const __bf16*)bcast_k;
+  p.bv = (const __bf16*)bcast_v;
+  p.bcap = (p.g.T + 63) / 64 * 64;
   if (n_ks > 0) {
     if (!keyset_k || !keyset_v || !keyset_count)
       return fail(SAF3R_ERR_INVALID, "saf3r_sparse_attn_fwd: KEYSET heads need the compact key-set buffers");

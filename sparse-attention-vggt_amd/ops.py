@@ -16,11 +16,11 @@ from . import _lib
 from .layout import BLOCK, HEAD_DIM, Geometry
 
 # Pattern ids (``enum saf3r_pattern``).
-DENSE, FRAME_LOCAL, ANCHOR_LOCAL, BLOCK_DYNAMIC, TOKEN_DYNAMIC, ANCHOR, SKIP, KEYSET = range(8)
+DENSE, FRAME_LOCAL, ANCHOR_LOCAL, BLOCK_DYNAMIC, TOKEN_DYNAMIC, ANCHOR, SKIP, KEYSET, BROADCAST = range(9)
 PATTERN_NAMES = {
     DENSE: "dense", FRAME_LOCAL: "frame_local", ANCHOR_LOCAL: "anchor_local",
     BLOCK_DYNAMIC: "block_topk", TOKEN_DYNAMIC: "dino_topk", ANCHOR: "all_to_first", SKIP: "skip",
-    KEYSET: "keyset",
+    KEYSET: "keyset", BROADCAST: "broadcast_first",
 }
 
 
@@ -188,9 +188,10 @@ def block_select(pooled_q: torch.Tensor, pooled_k: torch.Tensor, frames: int, bl
 
 def sparse_attn_fwd(qp, kp, vp, geom: Geometry, patterns: Sequence[int], sel: torch.Tensor | None = None,
                     scale: float | None = None, out: torch.Tensor | None = None,
-                    keysets: "KeySets | None" = None) -> torch.Tensor:
+                    keysets: "KeySets | None" = None, broadcast: "Broadcast | None" = None) -> torch.Tensor:
     """All heads in one launch. Returns (or fills) ``out`` bf16 [N, H*64] in natural token order.
-    ``keysets`` carries the compact K/V of the KEYSET heads (in increasing head order)."""
+    ``keysets`` carries the compact K/V of the KEYSET heads and ``broadcast`` the frame-0 / per-frame
+    buffers of the BROADCAST heads (each in increasing head order)."""
     _need_cuda(qp, kp, vp)
     lib = _lib.load()
     H = qp.shape[0]
@@ -221,12 +222,18 @@ def sparse_attn_fwd(qp, kp, vp, geom: Geometry, patterns: Sequence[int], sel: to
         if keysets is None or keysets.k.shape[0] != n_ks:
             raise ValueError(f"{n_ks} KEYSET heads need {n_ks} gathered key sets")
         ks_k, ks_v, ks_n, ks_cap = keysets.k, keysets.v, keysets.count, keysets.capacity
+    n_bc = sum(1 for p in patterns if p == BROADCAST)
+    bq = bk = bv = None
+    if n_bc:
+        if broadcast is None or broadcast.q.shape[0] != n_bc:
+            raise ValueError(f"{n_bc} BROADCAST heads need {n_bc} gathered frame-0 / per-frame buffers")
+        bq, bk, bv = broadcast.q, broadcast.k, broadcast.v
     pat = _i32_array(patterns)
     _mark("sparse_attn", "start")
     _lib.check(lib.saf3r_sparse_attn_fwd(
         _ptr(qp), _ptr(kp), _ptr(vp), geom.frames, geom.tokens_per_frame, geom.num_special, H,
         pat, _ptr(sel), width, float(scale), _ptr(out), out.stride(0), _ptr(ks_k), _ptr(ks_v), _ptr(ks_n),
-        ks_cap, _lib.stream_ptr()))
+        ks_cap, _ptr(bq), _ptr(bk), _ptr(bv), _lib.stream_ptr()))
     _mark("sparse_attn", "end")
     return out
 
@@ -397,3 +404,48 @@ def keyset_gather(kp: torch.Tensor, geom: Geometry, specs: Sequence[KeySetSpec],
                                        cap // 64, _ptr(kc), _ptr(vc), cap, _lib.stream_ptr()))
     _mark("keyset_gather", "end")
     return KeySets(kc, vc, count, idx, cap)
+
+
+@dataclass
+class Broadcast:
+    """Buffers of the BROADCAST heads of a layer (``broadcast_first``,
+    ``saf3r/patch/sparse_attention.py:110-131``), C = ceil(T/64)*64: ``q`` / ``k`` [n][C][64] packed
+    rows of frame 0's tokens in token order (zeros past T), ``v`` [n][F][C/64][64][64] the key-set V
+    tiles of every frame's tokens."""
+    q: torch.Tensor
+    k: torch.Tensor
+    v: torch.Tensor
+
+
+def broadcast_gather(qp: torch.Tensor, kp: torch.Tensor, geom: Geometry, heads: Sequence[int], v: torch.Tensor,
+                     v_tok_stride: int, v_head_stride: int) -> Broadcast:
+    """Frame 0's Q and K rows and every frame's V tiles of ``heads``, through saf3r_keyset_gather
+    (one key set per (head, frame): tokens f*T .. f*T+T-1). ``v`` is head 0's V of token 0 in the
+    natural layout (head h, token t at ``v_tok_stride * t + v_head_stride * h``)."""
+    _need_cuda(qp, kp, v)
+    lib = _lib.load()
+    n, F, T = len(heads), geom.frames, geom.tokens_per_frame
+    cap = -(-T // 64) * 64
+    dev = kp.device
+    idx = (torch.arange(F, device=dev, dtype=torch.int32)[:, None] * T
+           + torch.arange(T, device=dev, dtype=torch.int32)[None, :]).repeat(n, 1).contiguous()
+    count = torch.full((n * F,), T, dtype=torch.int32, device=dev)
+    hs = torch.tensor([h for h in heads for _ in range(F)], dtype=torch.int32, device=dev)
+    kc = torch.empty(n * F, cap, HEAD_DIM, dtype=torch.bfloat16, device=dev)
+    vc = torch.empty(n, F, cap // 64, 64, 64, dtype=torch.bfloat16, device=dev)
+    _mark("broadcast_gather", "start")
+    _lib.check(lib.saf3r_keyset_gather(_ptr(kp), F, T, geom.num_special, _ptr(hs), n * F, _ptr(v), v_tok_stride,
+                                       v_head_stride, _ptr(idx), idx.stride(0), _ptr(count), cap // 64, _ptr(kc),
+                                       _ptr(vc), cap, _lib.stream_ptr()))
+    # frame 0's query rows: the same gather over the packed Q (its V output is not used)
+    hs0 = torch.tensor(list(heads), dtype=torch.int32, device=dev)
+    idx0 = idx[::F].contiguous()
+    qc = torch.empty(n, cap, HEAD_DIM, dtype=torch.bfloat16, device=dev)
+    scratch_v = torch.empty(n, cap // 64, 64, 64, dtype=torch.bfloat16, device=dev)
+    _lib.check(lib.saf3r_keyset_gather(_ptr(qp), F, T, geom.num_special, _ptr(hs0), n, _ptr(v), v_tok_stride,
+                                       v_head_stride, _ptr(idx0), idx0.stride(0), _ptr(count), cap // 64, _ptr(qc),
+                                       _ptr(scratch_v), cap, _lib.stream_ptr()))
+    kc0 = kc.view(n, F, cap, HEAD_DIM)[:, 0].contiguous()
+    _mark("broadcast_gather", "end")
+    return Broadcast(qc, kc0, vc)
+

@@ -19,15 +19,16 @@ Block patterns (same JSON format, new mode names)
   q_probe_topk           KEYSET (the N // stride (or min(topk, N), default topk 1024) keys with the
                          best mean-query scores, plus frame 0 and the specials with include_as
                          (default False))
-Reference modes without a kernel in this build: broadcast_first, and q_probe_topk with
-q_sample_ratio != 1 -> NotImplementedError.
+  broadcast_first        BROADCAST (frame 0's attention map applied to every frame's V, :110-131)
+Reference option without a kernel in this build: q_probe_topk with q_sample_ratio != 1
+-> NotImplementedError.
 """
 from __future__ import annotations
 
 import torch
 
-from ..ops import (ANCHOR, ANCHOR_LOCAL, BLOCK_DYNAMIC, DENSE, FRAME_LOCAL, KEYSET, KEYSET_STRIDE, KEYSET_TOPK,
-                   SKIP, TOKEN_DYNAMIC, KeySetSpec)
+from ..ops import (ANCHOR, ANCHOR_LOCAL, BLOCK_DYNAMIC, BROADCAST, DENSE, FRAME_LOCAL, KEYSET, KEYSET_STRIDE,
+                   KEYSET_TOPK, SKIP, TOKEN_DYNAMIC, KeySetSpec)
 
 MODE_TO_PATTERN = {
     "full": DENSE,
@@ -41,8 +42,9 @@ MODE_TO_PATTERN = {
     "skip": SKIP,
     "stride": KEYSET,
     "q_probe_topk": KEYSET,
+    "broadcast_first": BROADCAST,
 }
-UNBUILT_MODES = ("broadcast_first",)
+UNBUILT_MODES = ()
 
 
 def pattern_of(cfg: dict) -> int:

@@ -82,6 +82,7 @@ class BaseHeadwiseSparseAttentionWrapper(nn.Module):
         self.layer_block_topk = ks.pop() if ks else self.block_topk
         self.dyn_heads = [h for h, p in enumerate(self.patterns) if p == ops.BLOCK_DYNAMIC]
         self.keyset_heads = [h for h, p in enumerate(self.patterns) if p == ops.KEYSET]
+        self.broadcast_heads = [h for h, p in enumerate(self.patterns) if p == ops.BROADCAST]
         self.last_keysets = None
         self.dino_heads = [h for h, p in enumerate(self.patterns) if p == ops.TOKEN_DYNAMIC]
         self.first_dino_head = next((h for h in self.dino_heads if self.head_cfg[h].get("is_first_dino", False)), None)
@@ -125,7 +126,10 @@ class BaseHeadwiseSparseAttentionWrapper(nn.Module):
         if self.keyset_heads:
             keysets = self._keysets(qp, kp, qkv, geom, C)
         self.last_keysets = keysets
-        out = ops.sparse_attn_fwd(qp, kp, vp, geom, self.patterns, sel, keysets=keysets)
+        bcast = None
+        if self.broadcast_heads:  # broadcast_first: frame 0's Q/K rows and every frame's V tiles
+            bcast = ops.broadcast_gather(qp, kp, geom, self.broadcast_heads, qkv[:, 2 * C:], qkv.stride(0), HEAD_DIM)
+        out = ops.sparse_attn_fwd(qp, kp, vp, geom, self.patterns, sel, keysets=keysets, broadcast=bcast)
         if self.dino_heads:
             est = self.est_topk_idx
             P, W = geom.patches, est.shape[1]

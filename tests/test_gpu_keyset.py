@@ -122,3 +122,42 @@ def test_keyset_attention_in_one_launch(ops, pkg, F, T, ns):
         err = (got[h] - ref.float()).abs()
         print(f"F{F} T{T} head {h} pattern {pat}: max {err.max().item():.3g} mean {err.mean().item():.3g}", flush=True)
         assert err.max().item() <= ATOL_MAX and err.mean().item() <= ATOL_MEAN
+
+
+@pytest.mark.parametrize("F,T,ns", [(3, 155, 5), (4, 1374, 5), (2, 64, 0), (1, 70, 5), (5, 37, 5)])
+def test_broadcast_first_in_one_launch(ops, pkg, F, T, ns):
+    """broadcast_first heads (saf3r/patch/sparse_attention.py:110-131) next to other patterns: the
+    gathered frame-0 rows and V tiles are exact copies, the outputs within the attention bars."""
+    geom = pkg.Geometry(F, T, ns)
+    n = geom.tokens
+    patterns = [ops.BROADCAST, ops.DENSE, ops.KEYSET, ops.BROADCAST, ops.FRAME_LOCAL]
+    H = len(patterns)
+    q, k, v = _qkv(H, n, seed=F * 5 + T, scale=1.5)
+    qp, kp, vp = ops.pack_heads(q.to(DEV), k.to(DEV), v.to(DEV), geom)
+    specs = [ops.KeySetSpec(2, ops.KEYSET_STRIDE, 3, 1, True)]
+    idx, count = ops.keyset_build(specs, geom, None, DEV)
+    vnat = v.permute(1, 0, 2).contiguous().to(DEV)
+    ks = ops.keyset_gather(kp, geom, specs, vnat, H * 64, 64, idx, count)
+    bc = ops.broadcast_gather(qp, kp, geom, [0, 3], vnat, H * 64, 64)
+    out = ops.sparse_attn_fwd(qp, kp, vp, geom, patterns, keysets=ks, broadcast=bc)
+    torch.cuda.synchronize()
+    C = -(-T // 64) * 64
+    for b, h in enumerate((0, 3)):
+        for buf, src in ((bc.q, q), (bc.k, k)):
+            rows = buf[b].cpu()
+            assert torch.equal(rows[:T], src[h][:T]) and (rows[T:C] == 0).all(), f"head {h} frame-0 rows"
+        toks = torch.arange(C)
+        toks = torch.where(toks < T, toks, torch.full_like(toks, -1))
+        for f in (0, F - 1):
+            nat, pad = unpack_v(bc.v[b, f:f + 1].cpu(), toks, T)
+            assert torch.equal(nat[0], v[h][f * T:(f + 1) * T]) and (pad == 0).all(), f"head {h} frame {f} V"
+    og = OA.Geometry(F, T, ns)
+    got = out.float().cpu().reshape(n, H, 64).permute(1, 0, 2)
+    ks_of = {2: idx[0, :int(count[0])].cpu()}
+    for h, pat in enumerate(patterns):
+        ref = OA.sparse_attention_gathered(q[h].float(), k[h].float(), v[h].float(), pat, og, ks_of.get(h),
+                                           dtype=torch.float64)
+        err = (got[h] - ref.float()).abs()
+        print(f"F{F} T{T} head {h} pattern {pat}: max {err.max().item():.3g} mean {err.mean().item():.3g}", flush=True)
+        assert err.max().item() <= ATOL_MAX and err.mean().item() <= ATOL_MEAN
+

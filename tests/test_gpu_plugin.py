@@ -210,7 +210,8 @@ def test_layer_keyset_modes(mods, pkg):
                {"mode": "q_probe_topk", "head_ids": [2, 3], "stride": 4},
                {"mode": "q_probe_topk", "head_ids": [4], "topk": 100, "include_as": True},
                {"mode": "stride", "head_ids": [5], "stride": 3, "shift": True, "include_as": False},
-               {"mode": "global_to_frame", "head_ids": [6]}]}}
+               {"mode": "global_to_frame", "head_ids": [6]},
+               {"mode": "broadcast_first", "head_ids": [7]}]}}
     plug.patch_model(m, "vggt", cfg)
     plug.update_args_per_forward(m, "vggt", ph * 14, pw * 14)
     geom = pkg.Geometry(F_, ph * pw + 5, 5)

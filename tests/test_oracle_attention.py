@@ -151,3 +151,38 @@ def test_vggt_positions_layout():
     assert pos[:5].abs().sum() == 0
     assert pos[5].tolist() == [1, 1] and pos[16].tolist() == [3, 4]
     assert torch.equal(pos[17:], pos[:17])
+
+
+def test_broadcast_first_pins():
+    """broadcast_first (saf3r/patch/sparse_attention.py:110-131): frame 0 is frame-local attention,
+    shifting a frame's V by a constant shifts its rows by it (the map's rows sum to one), and a
+    per-element loop over the formula agrees on a tiny case."""
+    q, k, v = _qkv(G.tokens, seed=11)
+    T = G.tokens_per_frame
+    got = A.broadcast_attention(q, k, v, G)
+    fl = A.pattern_attention(q, k, v, A.FRAME_LOCAL, G)
+    torch.testing.assert_close(got[:T], fl[:T], rtol=1e-10, atol=1e-10)
+    # frames 1, 2 given frame 0's V plus a constant: rows equal frame 0's rows plus that constant
+    shift = torch.randn(G.frames, 64, dtype=torch.float64)
+    v2 = v[:T].repeat(G.frames, 1) + shift.repeat_interleave(T, dim=0)
+    got2 = A.broadcast_attention(q, k, v2, G)
+    for f in range(G.frames):
+        torch.testing.assert_close(got2[f * T:(f + 1) * T], got2[:T] - shift[0] + shift[f], rtol=1e-9, atol=1e-9)
+    # the rows never read q or k beyond frame 0
+    q3, k3 = q.clone(), k.clone()
+    q3[T:] = 0.0
+    k3[T:] = 7.0
+    torch.testing.assert_close(A.broadcast_attention(q3, k3, v, G), got)
+    # element loop, 2 frames x 3 tokens, d = 2
+    g = A.Geometry(frames=2, tokens_per_frame=3, num_special=1)
+    qs, ks, vs = _qkv(6, d=2, seed=12)
+    out = A.broadcast_attention(qs, ks, vs, g)
+    for f in range(2):
+        for i in range(3):
+            w = [math.exp(float(qs[i] @ ks[j]) / math.sqrt(2)) for j in range(3)]
+            for d in range(2):
+                exp = sum(w[j] * float(vs[3 * f + j, d]) for j in range(3)) / sum(w)
+                assert abs(float(out[3 * f + i, d]) - exp) < 1e-12
+    # the gathered entry point dispatches to it
+    torch.testing.assert_close(A.sparse_attention_gathered(q, k, v, A.BROADCAST, G, dtype=torch.float64), got)
+

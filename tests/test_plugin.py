@@ -124,7 +124,8 @@ def test_reference_vggt_profile_fixture(plug, vggt):
     assert spa.keyset_spec({"mode": "stride", "stride": 3, "shift": True}, 7, n).start == 1
     with pytest.raises(NotImplementedError, match="q_sample_ratio"):
         spa.keyset_spec({"mode": "q_probe_topk", "q_sample_ratio": 0.5}, 0, n)
-    with pytest.raises(NotImplementedError, match="broadcast_first"):
-        plug.patch_model(_model(vggt, depth=1, dim=64, heads=2), "vggt",
-                         {"patch_module": {"type": "headsparse"},
-                          "sparse_config": {"0": [{"mode": "broadcast_first", "head_ids": [0]}]}})
+    m = _model(vggt, depth=1, dim=128, heads=2)
+    plug.patch_model(m, "vggt", {"patch_module": {"type": "headsparse"},
+                                 "sparse_config": {"0": [{"mode": "broadcast_first", "head_ids": [0]}]}})
+    w = m.aggregator.global_blocks[0].attn
+    assert w.patterns == [ops.BROADCAST, ops.DENSE] and w.broadcast_heads == [0]
