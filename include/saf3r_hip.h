@@ -239,6 +239,24 @@ int saf3r_gather_attn_fwd(const saf3r_rows* q, const saf3r_rows* k, const saf3r_
 int saf3r_token_topk(const saf3r_rows* q, const saf3r_rows* k, int n_q, int frames, int per_frame, int topk,
                      int32_t* idx, void* stream);
 
+/*
+ * Token top-k from blocks of bf16 scores: the selection of the non-lazy DINO-feature path.
+ *   scores: bf16 bits [rows][score_stride]; key j of frame f at column f*per_frame + j.
+ *   per_frame_mode 1: the min(topk, per_frame) best keys of every frame (frames >= 1 with
+ *     exclude_first), increasing key order within a frame, frame-major; 0: the min(topk, keys) best
+ *     keys of the row (beyond frame 0 with exclude_first), in increasing key order.
+ *   exclude_first: columns 0 .. ceil(per_frame/first_stride)-1 hold frame 0's samples 0, s, 2s, ...
+ *     (s = first_stride > 0), the selected keys follow.
+ *   cap > 0: at most cap selected keys (the best), in increasing key order; in per_frame_mode that
+ *     needs cand_idx int32 / cand_key uint16 buffers of [rows][frames * min(topk, per_frame)].
+ *   Ranking: the bf16 score, ties to the lower key. rows <= 65535, per_frame <= 4096.
+ * Replaces: saf3r/patch/utils.py:54-184 (compute_qk_topk_indices_batched, its torch.topk selection,
+ *           first-frame samples and max_topk cap).
+ */
+int saf3r_frame_topk_scores(const void* scores, int64_t score_stride, int rows, int frames, int per_frame,
+                            int exclude_first, int first_stride, int per_frame_mode, int topk, int cap,
+                            int32_t* idx, int64_t idx_stride, int32_t* cand_idx, uint16_t* cand_key, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -5,7 +5,8 @@ TEST INFRASTRUCTURE ONLY (see ``oracle/__init__.py``).
 Reference anchors: ``saf3r/triton/topk_utils.py:26-29`` (sortable key),
 ``saf3r/triton/fused_qk_topk.py:73-100`` (composite key, tie rule, frame-major output),
 ``saf3r/patch/adaptive_block_value.py:16-24`` (population-weighted block mean),
-``saf3r/patch/sparse_attention.py:143-186, 256-273`` (q_probe / stride key sets).
+``saf3r/patch/sparse_attention.py:143-186, 256-273`` (q_probe / stride key sets),
+``saf3r/patch/utils.py:54-184`` (token top-k from feature scores, :func:`token_topk_from_scores`).
 """
 from __future__ import annotations
 
@@ -177,3 +178,46 @@ def keyset(scores, n: int, tokens_per_frame: int, num_special: int, mode: int, p
     if cnt < 0:
         raise ValueError(f"oracle_keyset failed ({cnt})")
     return out[:cnt].copy()
+
+
+def sortable16(bits: np.ndarray) -> np.ndarray:
+    """Order key of bf16 bit patterns: larger score -> larger key, -0.0 below +0.0."""
+    b = np.asarray(bits, dtype=np.uint16).astype(np.int64)
+    return np.where(b & 0x8000, b ^ 0xFFFF, b ^ 0x8000)
+
+
+def _best(keys: np.ndarray, idx: np.ndarray, k: int) -> np.ndarray:
+    """The k best of (keys, idx) by key, ties to the lower idx, returned in increasing idx order."""
+    order = np.lexsort((idx, -keys))[:k]
+    return np.sort(idx[order])
+
+
+def token_topk_from_scores(bits: np.ndarray, frames: int, per_frame: int, topk: int, per_frame_mode: bool = True,
+                           exclude_first: bool = False, first_stride: int = 1, cap: int = 0) -> np.ndarray:
+    """Selection of ``compute_qk_topk_indices_batched`` (``saf3r/patch/utils.py:54-184``) from bf16 score
+    rows ``bits`` uint16 [rows, frames*per_frame]: optional frame-0 samples 0, s, 2s, ... first
+    (exclude_first, :94-99, :176-178), then per-frame top-min(topk, P) of frames >= f0
+    (:146-156) or the global top-k beyond frame 0 (:157-160), then at most ``cap`` of those (:162-169).
+    Order within the kept keys: increasing key index (the reference's sorted=False order is
+    unspecified); ties go to the lower key."""
+    bits = np.asarray(bits, dtype=np.uint16)
+    rows = bits.shape[0]
+    f0 = 1 if exclude_first else 0
+    keys = sortable16(bits[:, :frames * per_frame])
+    first = np.arange(0, per_frame, first_stride, dtype=np.int64) if exclude_first else np.zeros(0, np.int64)
+    out = []
+    for r in range(rows):
+        if per_frame_mode:
+            k = min(topk, per_frame)
+            parts = [_best(keys[r, f * per_frame:(f + 1) * per_frame], np.arange(per_frame) + f * per_frame, k)
+                     for f in range(f0, frames)]
+            cand = np.concatenate(parts) if parts else np.zeros(0, np.int64)
+        else:
+            lo = f0 * per_frame
+            n = frames * per_frame - lo
+            cand = _best(keys[r, lo:], np.arange(lo, lo + n), min(topk, n))
+        if 0 < cap < len(cand):
+            cand = _best(keys[r, cand], cand, cap)
+        out.append(np.concatenate([first, cand]))
+    return np.asarray(out, dtype=np.int32).reshape(rows, -1)
+

@@ -449,3 +449,37 @@ def broadcast_gather(qp: torch.Tensor, kp: torch.Tensor, geom: Geometry, heads: 
     _mark("broadcast_gather", "end")
     return Broadcast(qc, kc0, vc)
 
+
+def frame_topk_scores(scores: torch.Tensor, frames: int, per_frame: int, topk: int, per_frame_mode: bool = True,
+                      exclude_first: bool = False, first_stride: int = 1, cap: int = 0) -> torch.Tensor:
+    """Token top-k of every row of a bf16 score block [rows, frames*per_frame] (``saf3r_frame_topk_scores``):
+    int32 [rows, F_sel + kept], F_sel frame-0 samples first when ``exclude_first``, then the kept keys
+    (per frame or per row, at most ``cap`` when ``cap`` > 0) in increasing key order. Ties go to the
+    lower key (ref: saf3r/patch/utils.py:54-184)."""
+    _need_cuda(scores)
+    lib = _lib.load()
+    if scores.dtype != torch.bfloat16 or scores.dim() != 2 or scores.stride(1) != 1:
+        raise ValueError("scores must be a bf16 [rows, keys] tensor with unit column stride")
+    rows = scores.shape[0]
+    nk = frames * per_frame
+    if scores.shape[1] < nk:
+        raise ValueError(f"scores have {scores.shape[1]} columns, need {nk}")
+    f0 = 1 if exclude_first else 0
+    fsel = -(-per_frame // first_stride) if exclude_first else 0
+    if per_frame_mode:
+        rest = min(topk, per_frame) * (frames - f0)
+    else:
+        rest = min(topk, nk - f0 * per_frame)
+    kept = min(rest, cap) if cap > 0 else rest
+    idx = torch.empty(rows, fsel + kept, dtype=torch.int32, device=scores.device)
+    cand_i = cand_k = None
+    if per_frame_mode and kept < rest:
+        cand_i = torch.empty(rows, rest, dtype=torch.int32, device=scores.device)
+        cand_k = torch.empty(rows, rest, dtype=torch.int16, device=scores.device)
+    _mark("frame_topk", "start")
+    _lib.check(lib.saf3r_frame_topk_scores(_ptr(scores), scores.stride(0), rows, frames, per_frame, int(exclude_first),
+                                           first_stride if exclude_first else 0, int(per_frame_mode), topk, cap,
+                                           _ptr(idx), idx.stride(0), _ptr(cand_i), _ptr(cand_k), _lib.stream_ptr()))
+    _mark("frame_topk", "end")
+    return idx
+

@@ -10,7 +10,9 @@ Configuration (plain dict or attribute object, as the reference's addict ``model
     patch_module.type                      "headsparse"
     patch_module.topk_mode                 "token" (required when a dino_topk head exists)
     patch_module.lazy_dino_topk            indices from the first correspondence head (True), or
-                                           supplied through ``wrapper.est_topk_idx`` (False)
+                                           from DINO patch features each forward (False):
+                                           ``set_dino_topk_from_features`` with per_frame_topk,
+                                           max_topk, include_first_frame, first_frame_stride
     patch_module.topk                      per-frame token top-k of dino_topk heads
     patch_module.block_topk                per-frame block top-k of block_topk heads (default 4)
     patch_module.topk_scope                "frame" (default) or "global" for block_topk heads
@@ -26,6 +28,7 @@ import torch
 from torch import Tensor
 
 from ..layout import HEAD_DIM
+from .utils import compute_qk_topk_indices_batched
 from .wrapper import BaseHeadwiseSparseAttentionWrapper, SelectionState, _get
 
 NUM_SPECIAL_TOKENS = 5
@@ -82,6 +85,29 @@ def update_args_per_forward(model, img_h, img_w):
         attn.patch_height = patch_height
         attn.patch_width = patch_width
         attn.first_dino_flag = False
+
+
+def set_dino_topk_from_features(model, patch_tokens: Tensor, model_cfg):
+    """The selection step of the reference's non-lazy aggregator forward (``patch_vggt.py:313-357``):
+    ``patch_tokens`` [S, P, C] are the DINO patch tokens (post-norm) of the S frames; their
+    L2-normalised features give every image token its keys (``compute_qk_topk_indices_batched``),
+    which every dino_topk head of every patched layer reads in this forward. Call it after
+    ``update_args_per_forward``. Returns int32 [S*P, width]."""
+    pm = _get(model_cfg, "patch_module")
+    S, P, C = patch_tokens.shape
+    feat = torch.nn.functional.normalize(patch_tokens.reshape(1, S * P, C), p=2, dim=-1)
+    idx = compute_qk_topk_indices_batched(
+        feat, feat, topk=_get(pm, "topk", 4), q_blocksize=4096, per_frame=bool(_get(pm, "per_frame_topk", True)),
+        num_toks_per_img=P, max_topk=_get(pm, "max_topk", 2048),
+        include_first_frame=bool(_get(pm, "include_first_frame", False)),
+        first_frame_stride=_get(pm, "first_frame_stride", 4)).reshape(S * P, -1)
+    state = getattr(model, "saf3r_selection_state", None)
+    if state is not None:
+        state.est_topk_idx = idx
+    for block in model.aggregator.global_blocks:
+        if isinstance(block.attn, BaseHeadwiseSparseAttentionWrapper):
+            block.attn.est_topk_idx = idx
+    return idx
 
 
 class HeadwiseSparseAttentionWrapper(BaseHeadwiseSparseAttentionWrapper):

@@ -66,6 +66,14 @@ def test_invalid_arguments_fail_before_launch(pkg):
     assert rc == 1 and b"idx_stride" in lib.saf3r_last_error()
     rc = lib.saf3r_keyset_gather(dev, 2, 100, 5, dev, 1, dev, 3072, 64, dev, 200, dev, 3, dev, dev, 128, None)
     assert rc == 1 and b"max_tiles" in lib.saf3r_last_error()
+    rc = lib.saf3r_frame_topk_scores(dev, 50, 2, 2, 30, 0, 0, 1, 4, 0, dev, 8, None, None, None)
+    assert rc == 1 and b"score stride" in lib.saf3r_last_error()
+    rc = lib.saf3r_frame_topk_scores(dev, 60, 2, 2, 30, 0, 0, 1, 4, 0, dev, 7, None, None, None)
+    assert rc == 1 and b"idx_stride" in lib.saf3r_last_error()
+    rc = lib.saf3r_frame_topk_scores(dev, 60, 2, 2, 30, 0, 0, 1, 4, 5, dev, 8, None, None, None)
+    assert rc == 1 and b"candidate" in lib.saf3r_last_error()
+    rc = lib.saf3r_frame_topk_scores(dev, 9000, 2, 2, 4500, 0, 0, 1, 4, 0, dev, 8, None, None, None)
+    assert rc == 2  # frames beyond 4096 keys
     rc = lib.saf3r_probe_scores(dev, dev, 2, 100, 5, dev, 1, 0.125, dev, dev, dev, 10, None)
     assert rc == 1 and b"scores_stride" in lib.saf3r_last_error()
     rc = lib.saf3r_block_select(ctypes.c_void_p(16), ctypes.c_void_p(16), 1, 4, 2, 2, 33, 0, ctypes.c_void_p(16), None)
