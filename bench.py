@@ -144,6 +144,44 @@ def scores_path(ops, geom, n_dyn, reps=5):
             "scores_path_frac": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
 
 
+def non_lazy_selection(pkg, frames, reps=2):
+    """The non-lazy DINO-feature selection at full size: L2-normalised random features
+    [frames * 1369, 1024] (the DINOv2-L patch-token width), per-frame top-k through the host mirror of
+    compute_qk_topk_indices_batched (bf16 score blocks of 4096 queries, then saf3r_frame_topk_scores),
+    for top-4 (the lazy default's k) and top-64 (the paper's non-lazy setting). Also times the
+    selection kernel alone on one score block (its HBM rate)."""
+    import importlib
+    U = importlib.import_module(pkg.__name__ + ".patch.utils")
+    ops = importlib.import_module(pkg.__name__ + ".ops")
+    P, D = 1369, 1024
+    n = frames * P
+    g = torch.Generator(device="cuda:0").manual_seed(0)
+    feat = torch.nn.functional.normalize(torch.randn(1, n, D, device="cuda:0", generator=g), dim=-1)
+    res = {"features": f"{n} x {D}", "gemm_tflop": round(2.0 * n * n * D / 1e12, 2)}
+    for k in (4, 64):
+        U.compute_qk_topk_indices_batched(feat, feat, k, per_frame=True, num_toks_per_img=P, max_topk=1 << 30)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            U.compute_qk_topk_indices_batched(feat, feat, k, per_frame=True, num_toks_per_img=P, max_topk=1 << 30)
+        torch.cuda.synchronize()
+        res[f"top{k}_ms"] = round((time.perf_counter() - t0) * 1e3 / reps, 2)
+    scores = torch.matmul(feat[0, :4096].to(torch.bfloat16), feat[0].to(torch.bfloat16).t().contiguous())
+    ops.frame_topk_scores(scores, frames, P, 64)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(5):
+        idx = ops.frame_topk_scores(scores, frames, P, 64)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / 5
+    nbytes = scores.numel() * 2 + idx.numel() * 4
+    res["select_block_ms"] = round(ms, 4)
+    res["select_block_GBs"] = round(nbytes / (ms * 1e-3) / 1e9, 1)
+    return res
+
+
 def calibrate_copy():
     """A plain elementwise copy (negation) of 2^28 fp32 values: 1 GiB read and 1 GiB written once."""
     dev = torch.device("cuda:0")
@@ -180,6 +218,8 @@ def main():
     ap.add_argument("--sparse-config", default=None,
                     help="a head-profile JSON in the reference's format (e.g. its VGGT ETH3D profile) to run "
                          "instead of the seeded block-pattern tables; dino_topk heads use lazy top-4 indices")
+    ap.add_argument("--non-lazy-select", action="store_true",
+                    help="also time the non-lazy DINO-feature token selection at the full frame count")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only a plain copy kernel of known size (reads 1 GiB, writes 1 GiB), for scaling "
                          "the FETCH_SIZE / WRITE_SIZE counters of a profiling run")
@@ -326,6 +366,8 @@ def main():
         "selection": dict(sel_extra, bound="hbm", peak=PEAK_HBM_GBS, unit="GB/s"),
         "other_kernels_ms": other_ms,
     }
+    if args.non_lazy_select:
+        result["non_lazy_selection"] = non_lazy_selection(pkg, args.frames)
     if not args.no_cpu_baseline and not args.sparse_config:
         result["cpu_baseline"] = cpu_baseline(pkg)
     print(json.dumps(result), flush=True)

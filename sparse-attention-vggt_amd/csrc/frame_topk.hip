@@ -6,8 +6,9 @@
 //
 // Scores are bf16 bit patterns; a key is ranked by the score, ties go to the lower key index. The
 // 16-bit order key of a score is its sortable transform (larger score -> larger key, -0 < +0).
-//   frame stage: one wave per (row, frame) takes the frame's top-k by a two-pass byte radix select
-//                in registers and LDS, then writes the k keys in increasing key order;
+//   frame stage: one wave per (row, frame) holds the frame's scores in registers, finds the k-th
+//                largest order key by bisection with wave-wide counts, and writes the k keys in
+//                increasing key order;
 //   cap stage:   one work-group per row takes the best `cap` of a candidate list (the frame stage's
 //                output, or every key of the row when selection is not per frame) the same way,
 //                in list order, which is increasing key order.
@@ -15,7 +16,7 @@
 
 namespace saf3r {
 
-constexpr int kMaxSegRegs = 64;  // frame stage: per_frame <= 64 * 64
+constexpr int kMaxPerFrame = 4096;  // frame stage: at most 9 chunks of 8 keys per lane
 
 struct FrameTopkParams {
   const uint16_t* scores;
@@ -85,104 +86,190 @@ __device__ inline int radix_bin(uint32_t* counts, int need, int* above, int lane
   return b;
 }
 
+// Wave-wide exclusive prefix of a small per-lane count (0..15) and the wave total, from four
+// ballots of its bits.
+__device__ inline int wave_prefix4(int cnt, int* total) {
+  int pre = 0, tot = 0;
+#pragma unroll
+  for (int bit = 0; bit < 4; ++bit) {
+    const uint64_t m = __ballot((cnt >> bit) & 1);
+    pre += (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0)) << bit;
+    tot += __popcll(m) << bit;
+  }
+  *total = tot;
+  return pre;
+}
+
 // ---- frame stage: four waves, one (row, frame) each ----
-template <int RM>  // key registers per lane: per_frame <= 64 * RM
+// A lane holds RC 16-byte chunks (8 scores each) of its frame: chunk c = lane + 64 r of the frame's
+// aligned span, so element order (r, lane, e) is increasing key order. The threshold t (the k-th
+// largest order key) is found by bisection over the 16-bit key range with wave-wide counts.
+template <int RC>
 __global__ __launch_bounds__(256) void frame_select_kernel(FrameTopkParams p) {
-  __shared__ uint32_t hist[4][256];
-  __shared__ uint32_t scan[4][64];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int row = blockIdx.y;
   const int nfr = p.F - p.f0;
   const int fs = blockIdx.x * 4 + w;  // selected-frame index
-  const bool active = fs < nfr;
-  const int f = p.f0 + (active ? fs : 0);
-  const int R = (p.P + 63) >> 6;
-  const uint16_t* src = p.scores + (int64_t)row * p.srs + (int64_t)f * p.P;
-  uint32_t key[RM];
+  if (fs >= nfr) return;              // whole wave: no barrier below
+  const int f = p.f0 + fs;
+  const int64_t s0 = (int64_t)f * p.P;        // first key of the frame in the row
+  const int64_t a0 = s0 & ~(int64_t)7;        // aligned span start
+  const uint16_t* rowp = p.scores + (int64_t)row * p.srs;
+  uint32_t key[RC][8];  // 0xFFFFFFFF: no key
 #pragma unroll
-  for (int r = 0; r < RM; ++r) {
-    const int j = r * 64 + lane;
-    key[r] = (r < R && j < p.P && active) ? sortable16(src[j]) : 0xFFFFFFFFu;  // 0xFFFFFFFF: no key
+  for (int r = 0; r < RC; ++r) {
+    const int64_t e0 = a0 + 8 * (int64_t)(lane + 64 * r);
+    u32x4 v = {0, 0, 0, 0};
+    if (e0 < s0 + p.P) v = *reinterpret_cast<const u32x4*>(rowp + e0);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int64_t x = e0 + e;
+      const uint16_t b = (uint16_t)(v[e >> 1] >> (16 * (e & 1)));
+      key[r][e] = (x >= s0 && x < s0 + p.P) ? sortable16(b) : 0xFFFFFFFFu;
+    }
   }
-  uint32_t* h = hist[w];
-  uint32_t* sc = scan[w];
-  // wave-local passes (waves share nothing; the barriers keep the work-group in step)
-  auto clear = [&]() {
+  auto count_ge = [&](uint32_t t) {  // valid keys >= t, wave-wide
+    int c = 0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) h[lane * 4 + i] = 0;
-  };
-  auto wave_bin = [&](int need, int* above) {
-    // lane owns bins 255 - 4*lane - i; inclusive counts from the top via a wave scan
-    uint32_t c[4], s = 0;
+    for (int r = 0; r < RC; ++r)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      c[i] = h[255 - (lane * 4 + i)];
-      s += c[i];
-    }
-    sc[lane] = s;
-    __builtin_amdgcn_wave_barrier();
-    uint32_t pre = 0;
-    for (int t = 0; t < lane; ++t) pre += sc[t];
-    int bin = -1, ab = 0;
-    if ((int)pre < need && (int)(pre + s) >= need) {
-      uint32_t acc = pre;
+      for (int e = 0; e < 8; ++e) c += (key[r][e] != 0xFFFFFFFFu && key[r][e] >= t) ? 1 : 0;
+    // per-lane counts summed by ballots of their bits (c <= 8 * RC <= 72)
+    int sum = 0;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        if (bin < 0 && (int)(acc + c[i]) >= need) {
-          bin = 255 - (lane * 4 + i);
-          ab = (int)acc;
-        }
-        acc += c[i];
-      }
-    }
-    const uint64_t m = __ballot(bin >= 0);
-    const int src_lane = m ? __builtin_ctzll(m) : 0;
-    *above = __shfl(ab, src_lane, 64);
-    return __shfl(bin, src_lane, 64);
+    for (int bit = 0; bit < 7; ++bit) sum += __popcll(__ballot((c >> bit) & 1)) << bit;
+    return sum;
   };
   const int k = p.k;
-  clear();
-  __syncthreads();
-#pragma unroll
-  for (int r = 0; r < RM; ++r)
-    if (r < R && key[r] != 0xFFFFFFFFu) atomicAdd(&h[key[r] >> 8], 1u);
-  __syncthreads();
-  int above1 = 0;
-  const int b1 = wave_bin(k, &above1);
-  __syncthreads();
-  clear();
-  __syncthreads();
-#pragma unroll
-  for (int r = 0; r < RM; ++r)
-    if (r < R && key[r] != 0xFFFFFFFFu && (int)(key[r] >> 8) == b1) atomicAdd(&h[key[r] & 255], 1u);
-  __syncthreads();
-  int above2 = 0;
-  const int b2 = wave_bin(k - above1, &above2);
-  const uint32_t t = ((uint32_t)b1 << 8) | (uint32_t)b2;
-  const int need_eq = k - above1 - above2;  // keys equal to t to keep, lowest index first
-  // ordered compaction: element order r-major, lane-minor = increasing key index
-  int base = 0, eq_seen = 0;
+  uint32_t lo = 0, hi = 65535;  // count(key >= lo) >= k holds for lo = 0
+  while (lo < hi) {
+    const uint32_t mid = (lo + hi + 1) >> 1;
+    if (count_ge(mid) >= k) lo = mid;
+    else hi = mid - 1;
+  }
+  const uint32_t t = lo;
+  const int need_eq = k - (t < 65535 ? count_ge(t + 1) : 0);  // keys equal to t to keep, lowest first
   int32_t* o = p.out + (int64_t)row * p.ors + p.ocol + (int64_t)fs * k;
   uint16_t* ok = p.okey ? p.okey + (int64_t)row * p.ors + (int64_t)fs * k : nullptr;
+  int base = 0, eq_seen = 0;
 #pragma unroll
-  for (int r = 0; r < RM; ++r) {
-    if (r < R) {
-      const bool valid = key[r] != 0xFFFFFFFFu;
-      const bool eq = valid && key[r] == t;
-      const uint64_t me = __ballot(eq);
-      const int eq_rank = eq_seen + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(me >> 32),
-                                                                 __builtin_amdgcn_mbcnt_lo((uint32_t)me, 0));
-      const bool sel = valid && (key[r] > t || (eq && eq_rank < need_eq));
-      const uint64_t ms = __ballot(sel);
-      const int pos = base + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(ms >> 32),
-                                                          __builtin_amdgcn_mbcnt_lo((uint32_t)ms, 0));
-      if (sel && active) {
-        o[pos] = f * p.P + r * 64 + lane;
-        if (ok) ok[pos] = (uint16_t)key[r];
-      }
-      base += __popcll(ms);
-      eq_seen += __popcll(me);
+  for (int r = 0; r < RC; ++r) {
+    int neq = 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) neq += key[r][e] == t ? 1 : 0;
+    int eq_tot;
+    const int eq_pre = eq_seen + wave_prefix4(neq, &eq_tot);
+    int nsel = 0, eq_run = 0;
+    bool sel[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const bool valid = key[r][e] != 0xFFFFFFFFu;
+      const bool eq = valid && key[r][e] == t;
+      sel[e] = valid && (key[r][e] > t || (eq && eq_pre + eq_run < need_eq));
+      eq_run += eq ? 1 : 0;
+      nsel += sel[e] ? 1 : 0;
     }
+    int sel_tot;
+    int pos = base + wave_prefix4(nsel, &sel_tot);
+    const int64_t e0 = a0 + 8 * (int64_t)(lane + 64 * r);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      if (sel[e]) {
+        o[pos] = (int32_t)(e0 + e);
+        if (ok) ok[pos] = (uint16_t)key[r][e];
+        ++pos;
+      }
+    }
+    base += sel_tot;
+    eq_seen += eq_tot;
+  }
+}
+
+// ---- frame stage for k <= 16: running per-lane top-K lists merged across the wave ----
+// Composite key (order key << 16 | 0xFFFF - j) of key j of the frame: larger is better, equal
+// scores order by the lower j. Each lane keeps the K best of its keys, a butterfly over the wave
+// merges the lists (bitonic merge of two descending lists), and the K winners are written in
+// increasing key order.
+template <int K>
+__device__ inline void cas_desc(uint32_t (&c)[K], int i, int j) {
+  const uint32_t hi = max(c[i], c[j]), lo = min(c[i], c[j]);
+  c[i] = hi;
+  c[j] = lo;
+}
+
+template <int K>
+__device__ inline void sort_bitonic_desc(uint32_t (&c)[K]) {
+  // c is bitonic: half-cleaners of sizes K, K/2, ..., 2 sort it descending
+#pragma unroll
+  for (int len = K; len >= 2; len >>= 1)
+#pragma unroll
+    for (int i = 0; i < K; ++i)
+      if ((i % len) < len / 2) cas_desc<K>(c, i, i + len / 2);
+}
+
+template <int RC, int K>
+__global__ __launch_bounds__(256) void frame_select_small_kernel(FrameTopkParams p) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int row = blockIdx.y;
+  const int nfr = p.F - p.f0;
+  const int fs = blockIdx.x * 4 + w;
+  if (fs >= nfr) return;
+  const int f = p.f0 + fs;
+  const int64_t s0 = (int64_t)f * p.P;
+  const int64_t a0 = s0 & ~(int64_t)7;
+  const uint16_t* rowp = p.scores + (int64_t)row * p.srs;
+  uint32_t c[K];
+#pragma unroll
+  for (int i = 0; i < K; ++i) c[i] = 0;  // 0 ranks below every key (j < 0xFFFF keeps the low half > 0)
+#pragma unroll
+  for (int r = 0; r < RC; ++r) {
+    const int64_t e0 = a0 + 8 * (int64_t)(lane + 64 * r);
+    u32x4 v = {0, 0, 0, 0};
+    if (e0 < s0 + p.P) v = *reinterpret_cast<const u32x4*>(rowp + e0);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int64_t x = e0 + e;
+      if (x >= s0 && x < s0 + p.P) {
+        const uint16_t b = (uint16_t)(v[e >> 1] >> (16 * (e & 1)));
+        uint32_t y = (sortable16(b) << 16) | (0xFFFFu - (uint32_t)(x - s0));
+        // insertion into the descending list
+#pragma unroll
+        for (int i = 0; i < K; ++i) {
+          const uint32_t hi = max(c[i], y), lo = min(c[i], y);
+          c[i] = hi;
+          y = lo;
+        }
+      }
+    }
+  }
+  // butterfly merge: after step d every lane holds the best K of its 2^d-lane group
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    uint32_t o[K];
+#pragma unroll
+    for (int i = 0; i < K; ++i) o[i] = (uint32_t)__shfl_xor((int)c[i], d, 64);
+#pragma unroll
+    for (int i = 0; i < K; ++i) c[i] = max(c[i], o[K - 1 - i]);
+    sort_bitonic_desc<K>(c);
+  }
+  // the k winners (k <= K), in increasing key order: reversed order of the low halves
+  const int k = p.k;
+  int32_t* out = p.out + (int64_t)row * p.ors + p.ocol + (int64_t)fs * k;
+  uint16_t* ok = p.okey ? p.okey + (int64_t)row * p.ors + (int64_t)fs * k : nullptr;
+  if (lane < k) {
+    // rank of winner `lane` by key index among the k winners
+    uint32_t mine = 0;
+    int jm = 0;
+#pragma unroll
+    for (int i = 0; i < K; ++i)
+      if (i == lane) mine = c[i];
+    jm = 0xFFFF - (int)(mine & 0xFFFFu);
+    int rank = 0;
+#pragma unroll
+    for (int i = 0; i < K; ++i)
+      if (i < k) rank += (0xFFFF - (int)(c[i] & 0xFFFFu)) < jm ? 1 : 0;
+    out[rank] = (int32_t)(s0 + jm);
+    if (ok) ok[rank] = (uint16_t)(mine >> 16);
   }
 }
 
@@ -293,8 +380,10 @@ extern "C" int saf3r_frame_topk_scores(const void* scores, int64_t score_stride,
   else rest = min((int64_t)topk, nk - (int64_t)f0 * per_frame);
   const int64_t kept = cap > 0 ? min(rest, (int64_t)cap) : rest;
   if (idx_stride < fsel + kept) return fail(SAF3R_ERR_INVALID, "saf3r_frame_topk_scores: idx_stride too small");
-  if (per_frame_mode && per_frame > 64 * kMaxSegRegs)
-    return fail(SAF3R_ERR_UNSUPPORTED, "saf3r_frame_topk_scores: per_frame must be <= %d", 64 * kMaxSegRegs);
+  if (per_frame_mode && per_frame > kMaxPerFrame)
+    return fail(SAF3R_ERR_UNSUPPORTED, "saf3r_frame_topk_scores: per_frame must be <= %d", kMaxPerFrame);
+  if (score_stride % 8 || (uintptr_t)scores % 16)
+    return fail(SAF3R_ERR_INVALID, "saf3r_frame_topk_scores: score rows must be 16-byte aligned (stride %% 8)");
   if (rows == 0) return SAF3R_OK;
   hipStream_t st = (hipStream_t)stream;
   if (fsel > 0) {
@@ -320,12 +409,22 @@ extern "C" int saf3r_frame_topk_scores(const void* scores, int64_t score_stride,
     p.ocol = capped ? 0 : fsel;
     p.okey = capped ? cand_key : nullptr;
     const dim3 grid((nfr + 3) / 4, rows);
-    const int R = (per_frame + 63) / 64;
-    if (R <= 8) hipLaunchKernelGGL(frame_select_kernel<8>, grid, dim3(256), 0, st, p);
-    else if (R <= 16) hipLaunchKernelGGL(frame_select_kernel<16>, grid, dim3(256), 0, st, p);
-    else if (R <= 24) hipLaunchKernelGGL(frame_select_kernel<24>, grid, dim3(256), 0, st, p);
-    else if (R <= 32) hipLaunchKernelGGL(frame_select_kernel<32>, grid, dim3(256), 0, st, p);
-    else hipLaunchKernelGGL(frame_select_kernel<kMaxSegRegs>, grid, dim3(256), 0, st, p);
+    const int RC = (per_frame / 8 + 2 + 63) / 64;  // 16-byte chunks per lane
+#define SAF3R_SMALL(RCV)                                                                                  \
+  if (k <= 4) hipLaunchKernelGGL((frame_select_small_kernel<RCV, 4>), grid, dim3(256), 0, st, p);           \
+  else if (k <= 8) hipLaunchKernelGGL((frame_select_small_kernel<RCV, 8>), grid, dim3(256), 0, st, p);      \
+  else hipLaunchKernelGGL((frame_select_small_kernel<RCV, 16>), grid, dim3(256), 0, st, p);
+    if (k <= 16) {
+      if (RC <= 1) { SAF3R_SMALL(1) }
+      else if (RC <= 2) { SAF3R_SMALL(2) }
+      else if (RC <= 3) { SAF3R_SMALL(3) }
+      else if (RC <= 4) { SAF3R_SMALL(4) }
+      else { SAF3R_SMALL(9) }
+    } else if (RC <= 1) hipLaunchKernelGGL(frame_select_kernel<1>, grid, dim3(256), 0, st, p);
+    else if (RC <= 2) hipLaunchKernelGGL(frame_select_kernel<2>, grid, dim3(256), 0, st, p);
+    else if (RC <= 3) hipLaunchKernelGGL(frame_select_kernel<3>, grid, dim3(256), 0, st, p);
+    else if (RC <= 4) hipLaunchKernelGGL(frame_select_kernel<4>, grid, dim3(256), 0, st, p);
+    else hipLaunchKernelGGL(frame_select_kernel<9>, grid, dim3(256), 0, st, p);
     if (int e = check_launch("saf3r_frame_topk_scores")) return e;
     if (!capped) return SAF3R_OK;
   }

@@ -458,8 +458,8 @@ def frame_topk_scores(scores: torch.Tensor, frames: int, per_frame: int, topk: i
     lower key (ref: saf3r/patch/utils.py:54-184)."""
     _need_cuda(scores)
     lib = _lib.load()
-    if scores.dtype != torch.bfloat16 or scores.dim() != 2 or scores.stride(1) != 1:
-        raise ValueError("scores must be a bf16 [rows, keys] tensor with unit column stride")
+    if scores.dtype != torch.bfloat16 or scores.dim() != 2 or scores.stride(1) != 1 or scores.stride(0) % 8:
+        raise ValueError("scores must be a bf16 [rows, keys] tensor with unit column stride and row stride % 8")
     rows = scores.shape[0]
     nk = frames * per_frame
     if scores.shape[1] < nk:

@@ -57,13 +57,16 @@ def compute_qk_topk_indices_batched(q: torch.Tensor, k: torch.Tensor, topk: int,
     P = num_toks_per_img if (per_frame or include_first_frame) else Nk
     frames = Nk // P
     qb = q.to(torch.bfloat16)
-    kt = k.to(torch.bfloat16).transpose(1, 2).contiguous()
+    # keys padded to a multiple of 8 columns: score rows then start on 16-byte boundaries
+    nk8 = -(-Nk // 8) * 8
+    kt = torch.zeros(B, k.shape[2], nk8, dtype=torch.bfloat16, device=k.device)
+    kt[:, :, :Nk] = k.to(torch.bfloat16).transpose(1, 2)
     out = torch.empty(B, Nq, first + rest_final, dtype=torch.int32, device=q.device)
     cap = rest_final if rest_final < rest_eff else 0
     for b in range(B):
         for qs in range(0, Nq, q_blocksize):
             qe = min(qs + q_blocksize, Nq)
-            scores = torch.matmul(qb[b, qs:qe], kt[b])  # bf16 [Bq, Nk]
+            scores = torch.matmul(qb[b, qs:qe], kt[b])[:, :Nk]  # bf16 [Bq, Nk], row stride nk8
             out[b, qs:qe] = ops.frame_topk_scores(scores, frames, P, topk, per_frame_mode=per_frame,
                                                   exclude_first=include_first_frame,
                                                   first_stride=first_frame_stride, cap=cap)

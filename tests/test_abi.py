@@ -68,9 +68,11 @@ def test_invalid_arguments_fail_before_launch(pkg):
     assert rc == 1 and b"max_tiles" in lib.saf3r_last_error()
     rc = lib.saf3r_frame_topk_scores(dev, 50, 2, 2, 30, 0, 0, 1, 4, 0, dev, 8, None, None, None)
     assert rc == 1 and b"score stride" in lib.saf3r_last_error()
-    rc = lib.saf3r_frame_topk_scores(dev, 60, 2, 2, 30, 0, 0, 1, 4, 0, dev, 7, None, None, None)
+    rc = lib.saf3r_frame_topk_scores(dev, 64, 2, 2, 30, 0, 0, 1, 4, 0, dev, 7, None, None, None)
     assert rc == 1 and b"idx_stride" in lib.saf3r_last_error()
-    rc = lib.saf3r_frame_topk_scores(dev, 60, 2, 2, 30, 0, 0, 1, 4, 5, dev, 8, None, None, None)
+    rc = lib.saf3r_frame_topk_scores(dev, 60, 2, 2, 30, 0, 0, 1, 4, 0, dev, 8, None, None, None)
+    assert rc == 1 and b"16-byte" in lib.saf3r_last_error()
+    rc = lib.saf3r_frame_topk_scores(dev, 64, 2, 2, 30, 0, 0, 1, 4, 5, dev, 8, None, None, None)
     assert rc == 1 and b"candidate" in lib.saf3r_last_error()
     rc = lib.saf3r_frame_topk_scores(dev, 9000, 2, 2, 4500, 0, 0, 1, 4, 0, dev, 8, None, None, None)
     assert rc == 2  # frames beyond 4096 keys

@@ -43,7 +43,10 @@ def test_frame_topk_scores_bit_exact(mods, F, P, k, pf, ex, st, cap):
     # integer-valued scores: many ties, decided by the lower key
     x = torch.randint(-6, 7, (rows, F * P), generator=g).to(torch.bfloat16)
     x[:, ::11] = -0.0
-    got = ops.frame_topk_scores(x.to(DEV), F, P, k, per_frame_mode=pf, exclude_first=ex, first_stride=st, cap=cap)
+    xd = torch.full((rows, -(-F * P // 8) * 8 + 8), 7.0, dtype=torch.bfloat16, device=DEV)  # padded row stride
+    xd[:, :F * P] = x.to(DEV)
+    got = ops.frame_topk_scores(xd[:, :F * P], F, P, k, per_frame_mode=pf, exclude_first=ex, first_stride=st,
+                                cap=cap)
     torch.cuda.synchronize()
     want = OS.token_topk_from_scores(_bits(x), F, P, k, per_frame_mode=pf, exclude_first=ex, first_stride=st,
                                      cap=cap)
@@ -57,7 +60,7 @@ def test_compute_qk_topk_indices_batched(mods, per_frame, include_first, max_top
     """The host mirror on L2-normalised features (D = 1024): every block's indices equal the oracle's
     selection from the same block's bf16 scores."""
     ops, U, _ = mods
-    S, P, D = 5, 120, 1024
+    S, P, D = 5, 121, 1024
     g = torch.Generator().manual_seed(int(per_frame) + 2 * int(include_first) + max_topk)
     feat = torch.nn.functional.normalize(torch.randn(1, S * P, D, generator=g), dim=-1).to(DEV)
     idx = U.compute_qk_topk_indices_batched(feat, feat, topk=8, per_frame=per_frame, num_toks_per_img=P,
@@ -67,10 +70,11 @@ def test_compute_qk_topk_indices_batched(mods, per_frame, include_first, max_top
     first, rest_eff, rest_final = U.output_width(S * P, 8, per_frame, P, max_topk, include_first, 4)
     assert idx.shape == (1, S * P, first + rest_final)
     q = feat.to(torch.bfloat16)[0]
-    kt = feat.to(torch.bfloat16)[0].t().contiguous()
+    kt = torch.zeros(D, -(-S * P // 8) * 8, dtype=torch.bfloat16, device=DEV)
+    kt[:, :S * P] = feat.to(torch.bfloat16)[0].t()
     Pm = P if (per_frame or include_first) else S * P
     for qs in range(0, S * P, 256):
-        scores = torch.matmul(q[qs:qs + 256], kt)
+        scores = torch.matmul(q[qs:qs + 256], kt)[:, :S * P]
         want = OS.token_topk_from_scores(_bits(scores), (S * P) // Pm, Pm, 8, per_frame_mode=per_frame,
                                          exclude_first=include_first, first_stride=4,
                                          cap=rest_final if rest_final < rest_eff else 0)
