@@ -2,7 +2,8 @@
 ``patch_model`` and ``update_args_per_forward``. VGGT is the model family of this build; other
 names raise ``ValueError`` like the reference does for unknown models."""
 from . import patch_vggt
-from .patch_vggt import HeadwiseSparseAttentionWrapper  # noqa: F401
+from .patch_vggt import HeadwiseSparseAttentionWrapper, set_dino_topk_from_features  # noqa: F401
+from .profiler import SparseAttentionProfiler, save_profile_results  # noqa: F401
 from .wrapper import BaseHeadwiseSparseAttentionWrapper  # noqa: F401
 
 

@@ -51,8 +51,13 @@ def _load_config(model_cfg):
 def patch_model(model, model_cfg):
     pm = _get(model_cfg, "patch_module")
     ptype = _get(pm, "type")
+    if ptype == "headprofile":  # offline profiler writing the head-profile JSON (profiler.py)
+        from .profiler import patch_model_profile
+        return patch_model_profile(model, model_cfg, HeadwiseSparseAttentionWrapper, NUM_SPECIAL_TOKENS,
+                                   model.aggregator.global_blocks[0].attn.num_heads,
+                                   len(model.aggregator.global_blocks), SelectionState())
     if ptype != "headsparse":
-        raise NotImplementedError(f"patch_module.type={ptype!r}: only 'headsparse' is built")
+        raise NotImplementedError(f"patch_module.type={ptype!r}: only 'headsparse' and 'headprofile' are built")
     config = _load_config(model_cfg)
     has_dino = any(g["mode"] == "dino_topk" for groups in config.values() for g in groups)
     lazy = bool(_get(pm, "lazy_dino_topk", False))
@@ -78,8 +83,13 @@ def update_args_per_forward(model, img_h, img_w):
     state = getattr(model, "saf3r_selection_state", None)
     if state is not None:
         state.reset()
+    from .profiler import SparseAttentionProfiler
     for block in model.aggregator.global_blocks:
         attn = block.attn
+        if isinstance(attn, SparseAttentionProfiler):
+            attn.patch_height = patch_height
+            attn.patch_width = patch_width
+            continue
         if not isinstance(attn, BaseHeadwiseSparseAttentionWrapper):
             continue
         attn.patch_height = patch_height

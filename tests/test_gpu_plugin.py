@@ -243,3 +243,57 @@ def test_reference_profile_layers(mods, pkg):
     with torch.no_grad():
         for li in (11, 12, 13):
             _check_layer(m.aggregator.global_blocks[li].attn, x, pos, geom, ops, li)
+
+
+def test_headprofile_records_oracle_nmse(mods, pkg):
+    """headprofile on one layer: the layer returns full attention, and every recorded candidate error
+    is the oracle's NMSE of that candidate against full attention (saf3r/patch/wrapper.py:163-205)."""
+    plug, vggt, ops, synth = mods
+    ph, pw, F_, H = 6, 7, 3, 4
+    dim = 64 * H
+    m = _make(vggt, 13, dim, H, seed=11).to(DEV).to(torch.bfloat16)
+    cfg = {"patch_module": {"type": "headprofile", "topk": 6, "per_frame_topk": True, "max_topk": 2048,
+                            "include_first_frame": False}}
+    plug.patch_model(m, "vggt", cfg)
+    plug.update_args_per_forward(m, "vggt", ph * 14, pw * 14)
+    geom = pkg.Geometry(F_, ph * pw + 5, 5)
+    g = torch.Generator().manual_seed(12)
+    tokens = torch.randn(F_, ph * pw, 1024, generator=g).to(DEV)
+    plug.set_dino_topk_from_features(m, tokens, cfg)
+    x = torch.randn(1, geom.tokens, dim, generator=g).to(torch.bfloat16).to(DEV)
+    pos = synth.vggt_positions(F_, ph, pw).to(DEV)[None]
+    prof = m.aggregator.global_blocks[12].attn
+    with torch.no_grad():
+        y = prof(x, pos)
+        yd = prof.full(x, pos)  # the all-dense wrapper
+    assert _err(y, yd)[0] <= 2e-2  # the same full attention (walk order may differ in the last bits)
+    N = geom.tokens
+    om = prof.orig_module
+    qkv = om.qkv(x).reshape(N, 3 * dim).contiguous()
+    qp, kp, vp = ops.pack_qkv(qkv, qkv[:, dim:], qkv[:, 2 * dim:], 3 * dim, 64, geom, H,
+                              ln_q=(om.q_norm.weight, om.q_norm.bias), ln_k=(om.k_norm.weight, om.k_norm.bias),
+                              pos=pos[0], rope_base=100.0)
+    toks = slot_tokens(geom.frames, geom.tokens_per_frame, geom.num_special)
+    q, _ = unpack_rows(qp.cpu(), toks, N)
+    k, _ = unpack_rows(kp.cpu(), toks, N)
+    v, _ = unpack_v(vp.cpu(), toks, N)
+    og = OA.Geometry(geom.frames, geom.tokens_per_frame, geom.num_special)
+    dense = OA.head_outputs(q.float(), k.float(), v.float(), [ops.DENSE] * H, og, dtype=torch.float64)
+    energy = (dense ** 2).mean(dim=(1, 2))
+    est = prof.shared.est_topk_idx.cpu()
+    checked = 0
+    for i, (c, w) in enumerate(zip(prof.cfgs, prof.candidates)):
+        sel = {}
+        if w.keyset_heads:
+            ks = w.last_keysets
+            sel = {h: ks.idx[j, :int(ks.count[j])].cpu() for j, h in enumerate(w.keyset_heads)}
+        out = OA.head_outputs(q.float(), k.float(), v.float(), list(w.patterns), og, sel, est_topk_idx=est,
+                              dtype=torch.float64)
+        nmse = ((out - dense) ** 2).mean(dim=(1, 2)) / energy
+        for h in range(H):
+            got = prof.head_errors[h][i]["mse"][0]
+            want = float(nmse[h])
+            print(f"cand {i} {c['mode']} head {h}: kernel {got:.5f} oracle {want:.5f}", flush=True)
+            assert abs(got - want) <= 1e-3 + 0.05 * want, (i, h)
+            checked += 1
+    assert checked == H * len(prof.cfgs)

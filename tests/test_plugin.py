@@ -59,7 +59,7 @@ def test_errors_follow_reference(plug, vggt):
     with pytest.raises(ValueError, match="Unsupported model"):
         plug.patch_model(_model(vggt), "pi3x", bad)
     with pytest.raises(NotImplementedError):
-        plug.patch_model(_model(vggt), "vggt", {"patch_module": {"type": "headprofile"}, "sparse_config": {}})
+        plug.patch_model(_model(vggt), "vggt", {"patch_module": {"type": "headcache"}, "sparse_config": {}})
     with pytest.raises(AssertionError):
         plug.patch_model(_model(vggt), "vggt", {"patch_module": {"type": "headsparse", "topk_mode": "global"},
                                                "sparse_config": {"0": [{"mode": "dino_topk", "head_ids": [0]}]}})
@@ -129,3 +129,39 @@ def test_reference_vggt_profile_fixture(plug, vggt):
                                  "sparse_config": {"0": [{"mode": "broadcast_first", "head_ids": [0]}]}})
     w = m.aggregator.global_blocks[0].attn
     assert w.patterns == [ops.BROADCAST, ops.DENSE] and w.broadcast_heads == [0]
+
+
+def test_headprofile_candidates_and_json(plug, vggt, pkg, tmp_path):
+    """headprofile patching and the JSON writer (saf3r/patch/wrapper.py:163-190,
+    saf3r/patch/patch_vggt.py:521-566): candidate list per layer, lowest mean error per head,
+    heads grouped per chosen candidate, the first dino_topk head marked."""
+    import importlib
+    prof = importlib.import_module(plug.__name__ + ".profiler")
+    c3 = prof.candidate_configs(3)
+    c12 = prof.candidate_configs(12)
+    assert len(c3) == 16 and c3[0] == {"mode": "stride", "stride": 128, "include_as": True, "is_base": True}
+    assert c12[0]["stride"] == 4 and [c["stride"] for c in c12[4:9]] == [8, 16, 32, 64, 128]
+    assert [c["stride"] for c in c12[9:15]] == [4, 8, 16, 32, 64, 128] and c12[15]["mode"] == "dino_topk"
+    m = _model(vggt, depth=2, dim=256, heads=4)
+    plug.patch_model(m, "vggt", {"patch_module": {"type": "headprofile"}})
+    p0, p1 = (b.attn for b in m.aggregator.global_blocks)
+    assert isinstance(p0, plug.SparseAttentionProfiler) and p0.heads == [0, 1, 2, 3]
+    plug.update_args_per_forward(m, "vggt", 28, 42)
+    assert (p0.patch_height, p0.patch_width) == (2, 3)
+    # synthetic errors over two samples: head -> candidate -> [e1, e2]
+    errs = {0: {2: [0.1, 0.3], 5: [0.2, 0.1]}, 1: {15: [0.01, 0.02], 2: [0.5, 0.5]},
+            2: {5: [0.05, 0.1], 15: [0.2, 0.2]}, 3: {2: [0.0, 0.1], 15: [0.3, 0.3]}}
+    for h, d in errs.items():
+        p0.head_errors[h] = {i: {"cfg": p0.cfgs[i], "mse": v} for i, v in d.items()}
+    p1.head_errors = {1: {15: {"cfg": p1.cfgs[15], "mse": [0.0]}}}
+    res = plug.save_profile_results(m, str(tmp_path / "prof.json"), "cmp_mse")
+    import json
+    saved = json.load(open(tmp_path / "prof.json"))
+    assert set(saved) == {"0", "1"}
+    by_mode = {c["mode"]: c for c in saved["0"]}
+    assert by_mode["stride"]["head_ids"] == [0, 2] and by_mode["stride"]["stride"] == 4 * 128
+    assert by_mode["dino_topk"]["head_ids"] == [1] and by_mode["dino_topk"]["is_first_dino"] is True
+    assert by_mode["all_to_first"]["head_ids"] == [3]
+    assert saved["1"] == [dict(p1.cfgs[15], head_ids=[1])]  # only the first dino head is marked
+    assert res[0] == saved["0"]
+
