@@ -255,6 +255,144 @@ __device__ __forceinline__ void attend(const char* __restrict__ kst, const char*
   }
 }
 
+// ---- single-range walks: software pipeline over 32-key half steps ------------------------------
+// Half step h covers keys 32 * (h & 1) .. + 31 of the h / 2-th tile of the walk. One block of
+// straight-line code runs the PV MFMAs of step h - 1, the score MFMAs of step h + 1 and the softmax
+// of step h, one MFMA to one softmax group (2 fma, 2 exp, 1 convert), so a wave keeps the matrix
+// unit busy while it computes exponentials instead of alternating between the two.
+
+// K fragments of keys 32 kh .. 32 kh + 31 of a staged tile (128-byte rows, swz8)
+__device__ __forceinline__ void load_k(const char* __restrict__ kst, int kh, bf16x8 (&kf)[4], int half, int col) {
+  const int r = 32 * kh + col;
+#pragma unroll
+  for (int st = 0; st < 4; ++st)
+    kf[st] = *reinterpret_cast<const bf16x8*>(kst + r * 128 + (((4 * half + st) ^ swz8(r)) << 4));
+}
+// V^T fragments of keys 32 kh .. 32 kh + 31 of a staged transposed tile (128-byte rows, swz8)
+__device__ __forceinline__ void load_v(const char* __restrict__ vst, int kh, bf16x8 (&vf)[2][2], int half, int col) {
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int dh = 0; dh < 2; ++dh) {
+      const int r = 32 * dh + col, chn = 2 * (2 * kh + j) + half;
+      vf[j][dh] = *reinterpret_cast<const bf16x8*>(vst + r * 128 + ((chn ^ swz8(r)) << 4));
+    }
+}
+
+// Masks keys key0 + i >= kvalid of a half step (single-range walks: no frame relation applies).
+__device__ __forceinline__ void mask_valid(f32x16 (&s)[2], int kvalid, int key0, int half) {
+#pragma unroll
+  for (int a = 0; a < 16; ++a) {
+    const int key = key0 + 8 * (a >> 2) + 4 * half + (a & 3);
+    if (key >= kvalid) s[0][a] = s[1][a] = -__builtin_inff();
+  }
+}
+
+// a row without a reference maximum yet uses -2^127: unmasked keys then give +inf (and the exact
+// path), masked keys 0, and no inf - inf (NaN) ever forms
+__device__ __forceinline__ float ref_mc(float m, float c) { return m == -__builtin_inff() ? -0x1p127f : m * c; }
+
+// P = exp2(s*c - mc) of one query group's 16 keys and their partial row sum over the bf16-rounded
+// values the PV product uses (exact path)
+__device__ __forceinline__ float exps_half(const f32x16& s, float c, float mc, bf16x8 (&p)[2]) {
+  const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
+  float t = 0.f;
+#pragma unroll
+  for (int u = 0; u < 16; u += 2) {
+    const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[u], c, -mc));
+    const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[u + 1], c, -mc));
+    const bf16x2 pr = {(__bf16)e0, (__bf16)e1};
+    p[u >> 3][u & 7] = pr[0];
+    p[u >> 3][(u & 7) + 1] = pr[1];
+    t = __builtin_amdgcn_fdot2_f32_bf16(pr, ones, t, false);
+  }
+  return t;
+}
+
+// The block of half step h: O += V(h-1) P(h-1), sn = K(h+1) Q^T, pn = P(h) from s with row sums ts.
+__device__ __forceinline__ void half_block(const bf16x8 (&kf)[4], const bf16x8 (&vf)[2][2],
+                                           const bf16x8 (&qfrag)[2][4], const f32x16 (&s)[2], f32x16 (&sn)[2],
+                                           const bf16x8 (&p)[2][2], bf16x8 (&pn)[2][2], float (&ts)[2], Acc& A,
+                                           float c) {
+  const float mc0 = ref_mc(A.m[0], c), mc1 = ref_mc(A.m[1], c);
+  sn[0] = sn[1] = f32x16{};
+  float ta[2] = {0.f, 0.f}, tb[2] = {0.f, 0.f};  // two chains per row sum
+  auto matrix = [&](int i) {
+    if (i < 8) {
+      const int j = i >> 2, dh = (i >> 1) & 1, gq = i & 1;
+      A.o[dh][gq] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[j][dh], p[gq][j], A.o[dh][gq], 0, 0, 0);
+    } else {
+      const int k = i - 8, st = k >> 1, gq = k & 1;
+      sn[gq] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[st], qfrag[gq][st], sn[gq], 0, 0, 0);
+    }
+  };
+  auto vector = [&](int i) {
+    const int g2 = i >> 3, u = 2 * (i & 7);
+    const float mc = g2 ? mc1 : mc0;
+    const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[g2][u], c, -mc));
+    const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[g2][u + 1], c, -mc));
+    const bf16x2 pr = {(__bf16)e0, (__bf16)e1};
+    pn[g2][u >> 3][u & 7] = pr[0];
+    pn[g2][u >> 3][(u & 7) + 1] = pr[1];
+  };
+  // fixed order: the first softmax group covers the LDS latency of the fragments, then each MFMA
+  // is followed by one softmax group (scheduling barriers keep the compiler from regrouping)
+  vector(0);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    matrix(i);
+    if (i + 1 < 16) vector(i + 1);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  // row sums of the rounded P (so l and O agree), as one burst of dot2 at the end: each dot2
+  // waits for the matrix pipe, so spread between the MFMAs they would stall every one of them
+  const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
+#pragma unroll
+  for (int g = 0; g < 2; ++g) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int u = 0; u < 8; u += 2) {
+        const bf16x2 pr = {pn[g][j][u], pn[g][j][u + 1]};
+        if (u & 2) tb[g] = __builtin_amdgcn_fdot2_f32_bf16(pr, ones, tb[g], false);
+        else ta[g] = __builtin_amdgcn_fdot2_f32_bf16(pr, ones, ta[g], false);
+      }
+  }
+  ts[0] = ta[0] + tb[0];
+  ts[1] = ta[1] + tb[1];
+  // every result is due here: otherwise the compiler sinks the softmax (and MFMAs) past the
+  // masking branch that follows, into blocks of their own, and nothing overlaps any more
+  asm volatile("" : "+v"(pn[0][0]), "+v"(pn[0][1]), "+v"(pn[1][0]), "+v"(pn[1][1]), "+v"(ts[0]), "+v"(ts[1]));
+  asm volatile("" : "+v"(sn[0]), "+v"(sn[1]));
+  asm volatile("" : "+v"(A.o[0][0]), "+v"(A.o[0][1]), "+v"(A.o[1][0]), "+v"(A.o[1][1]));
+}
+
+// The reference maximum m moves only when a step's partial row sum exceeds 2^64 (the first step of
+// a row with an unmasked key, whose m is still -inf, always does): values up to 2^64 keep every
+// bf16 P, fp32 sum and O finite, so no per-step maximum is needed. The exact path takes the row
+// maximum of s, rescales O (which then holds every step before h) and l, and recomputes P(h).
+__device__ __forceinline__ void exact_fix(const f32x16 (&s)[2], bf16x8 (&pn)[2][2], float (&ts)[2], Acc& A, float c) {
+  if (__ballot(ts[0] > 0x1p64f || ts[1] > 0x1p64f) == 0) return;
+#pragma unroll
+  for (int gq = 0; gq < 2; ++gq) {
+    float mx = s[gq][0];
+#pragma unroll
+    for (int a = 1; a < 16; ++a) mx = fmaxf(mx, s[gq][a]);
+    mx = partner_max(mx);
+    const float m_new = fmaxf(A.m[gq], mx);
+    const float alpha = A.m[gq] == -__builtin_inff() ? 0.f : __builtin_amdgcn_exp2f((A.m[gq] - m_new) * c);
+    A.l[gq] *= alpha;
+#pragma unroll
+    for (int a = 0; a < 16; ++a) {
+      A.o[0][gq][a] *= alpha;
+      A.o[1][gq][a] *= alpha;
+    }
+    A.m[gq] = m_new;
+    ts[gq] = exps_half(s[gq], c, m_new == -__builtin_inff() ? 0.f : m_new * c, pn[gq]);
+  }
+}
+
 // Key-tile walk of a shared-mode group: up to four contiguous tile ranges (empty ones skipped),
 // entered at any step and wrapping around. Patch tiles carry their block within the frame and
 // their frame, advanced incrementally, so a step costs a few scalar instructions and no division.
@@ -561,6 +699,110 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
       wi.next(g);
     };
 
+    if (keyset || eff == SAF3R_DENSE) {
+      // ---- single-range walk: tiles rot, rot + 1, ... (mod count), only partial tiles masked ----
+      // Control is kept to a few scalar selects per tile: the loop runs four tiles per trip so
+      // that every stage offset is a constant, waves without a query tile of their own compute
+      // on a duplicate (their rows are not stored), and the tile position and its valid-key
+      // count advance without branches.
+      const int nst = g.nst, NBf = g.NBf;
+      const int lastv = g.P - 64 * (NBf - 1);  // valid keys in the last patch tile of a frame
+      int kt = rot, bk = -1;                   // consumed tile and its block within its frame
+      if constexpr (!keyset) bk = kt >= nst ? (kt - nst) % NBf : -1;
+      auto kvalid_of = [&]() -> int {
+        if constexpr (keyset) return min(64, ks_keys - 64 * kt);
+        else return kt < nst ? min(64, g.S - 64 * kt) : (bk == NBf - 1 ? lastv : 64);
+      };
+      auto advance = [&]() {
+        kt = kt + 1 == count ? 0 : kt + 1;
+        if constexpr (!keyset) bk = kt < nst ? -1 : (kt == nst || bk + 1 == NBf ? 0 : bk + 1);
+      };
+      int kti = rot;  // next tile to load
+      auto issue_at = [&](int stage) {
+        const char* kb = kbase + (int64_t)kti * 8192;
+        const char* vb = vbase + (int64_t)kti * 8192;
+        char* st = ring + stage * 16384 + 64 * w * 16;
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          __builtin_amdgcn_global_load_lds((const void*)(kb + dofs[u]), (lds_void*)(st + 4096 * u), 16, 0, 0);
+          __builtin_amdgcn_global_load_lds((const void*)(vb + dofs[u]), (lds_void*)(st + 8192 + 4096 * u), 16, 0,
+                                           0);
+        }
+        kti = kti + 1 == count ? 0 : kti + 1;
+      };
+      if (count == 0) {
+        store_rows(p, A, qtok, h, half);
+        return;
+      }
+      wait_vm<0>();  // Q fragments landed; from here vmcnt counts ring loads only
+      for (int u = 0; u < 3; ++u)
+        if (u < count) issue_at(u);
+      if (count >= 3) wait_vm<8>();
+      else if (count == 2) wait_vm<4>();
+      else wait_vm<0>();
+      barrier_only();
+      f32x16 s_cur[2], s_nxt[2];
+      bf16x8 pc[2][2], pn[2][2], kf[4], vf[2][2];
+      float ts[2];
+      int kv_cur = kvalid_of();
+      load_k(ring, 0, kf, half, col);
+      s_cur[0] = s_cur[1] = f32x16{};
+#pragma unroll
+      for (int st = 0; st < 4; ++st) {
+        s_cur[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[st], qfrag[0][st], s_cur[0], 0, 0, 0);
+        s_cur[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[st], qfrag[1][st], s_cur[1], 0, 0, 0);
+      }
+      if (kv_cur < 64) mask_valid(s_cur, kv_cur, 0, half);
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int x = 0; x < 2; ++x) {
+          pc[j][x] = bf16x8{};
+          vf[j][x] = bf16x8{};
+        }
+      for (int t0 = 0; t0 < count; t0 += 4) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int t = t0 + v;
+          if (t >= count) break;
+          // half step 2t: PV of tile t-1 keys 32..63, scores of tile t keys 32..63
+          if (v > 0 || t0 > 0) load_v(ring + ((v + 3) & 3) * 16384 + 8192, 1, vf, half, col);
+          load_k(ring + v * 16384, 1, kf, half, col);
+          half_block(kf, vf, qfrag, s_cur, s_nxt, pc, pn, ts, A, c);
+          if (kv_cur < 64) mask_valid(s_nxt, kv_cur, 32, half);
+          exact_fix(s_cur, pn, ts, A, c);
+          A.l[0] += ts[0];
+          A.l[1] += ts[1];
+          advance();
+          const int kv_nxt = kvalid_of();  // tile t + 1 (past the end: never read)
+          if (t + 2 < count) wait_vm<4>();
+          else wait_vm<0>();
+          barrier_only();
+          if (t + 3 < count) issue_at((v + 3) & 3);
+          // half step 2t+1: PV of tile t keys 0..31, scores of tile t + 1 keys 0..31
+          load_v(ring + v * 16384 + 8192, 0, vf, half, col);
+          load_k(ring + ((v + 1) & 3) * 16384, 0, kf, half, col);
+          half_block(kf, vf, qfrag, s_nxt, s_cur, pn, pc, ts, A, c);
+          if (kv_nxt < 64) mask_valid(s_cur, kv_nxt, 0, half);
+          exact_fix(s_nxt, pc, ts, A, c);
+          A.l[0] += ts[0];
+          A.l[1] += ts[1];
+          kv_cur = kv_nxt;
+        }
+      }
+      load_v(ring + ((count - 1) & 3) * 16384 + 8192, 1, vf, half, col);
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int dh = 0; dh < 2; ++dh) {
+          A.o[dh][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[j][dh], pc[0][j], A.o[dh][0], 0, 0, 0);
+          A.o[dh][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[j][dh], pc[1][j], A.o[dh][1], 0, 0, 0);
+        }
+      store_rows(p, A, qtok, h, half);
+      return;
+    }
+
+    // ---- frame-relative walks (up to four ranges, frame masks): one tile per attend step ----
     wait_vm<0>();  // Q fragments landed; from here vmcnt counts ring loads only
     // tiles move in pairs: pair i+1 loads into the two free stages while pair i is consumed,
     // one barrier per pair
@@ -577,17 +819,7 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
         if (n + u < count) {
-          TileMask tm;
-          if constexpr (keyset) {
-            tm.kt = wk.kt;
-            tm.kspecial = false;
-            tm.kframe = 0;
-            tm.eff = SAF3R_DENSE;
-            tm.kvalid = min(64, ks_keys - 64 * wk.kt);
-            tm.need = tm.kvalid < 64;
-          } else {
-            tm = wk.mask(g, eff, frame_rel, qspecial);
-          }
+          const TileMask tm = wk.mask(g, eff, frame_rel, qspecial);
           const char* kst = ring + ((n + u) % kStages) * 16384;
           attend<2>(kst, kst + 8192, qfrag, A, frow, tm, g, p.nsmagic, 0, half, col, c, [&]() {
             if (n + 2 + u < count) issue((n + 2 + u) % kStages);
