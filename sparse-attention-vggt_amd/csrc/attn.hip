@@ -316,7 +316,6 @@ __device__ __forceinline__ void half_block(const bf16x8 (&kf)[4], const bf16x8 (
                                            float c) {
   const float mc0 = ref_mc(A.m[0], c), mc1 = ref_mc(A.m[1], c);
   sn[0] = sn[1] = f32x16{};
-  float ta[2] = {0.f, 0.f}, tb[2] = {0.f, 0.f};  // two chains per row sum
   auto matrix = [&](int i) {
     if (i < 8) {
       const int j = i >> 2, dh = (i >> 1) & 1, gq = i & 1;
@@ -348,19 +347,16 @@ __device__ __forceinline__ void half_block(const bf16x8 (&kf)[4], const bf16x8 (
   // row sums of the rounded P (so l and O agree), as one burst of dot2 at the end: each dot2
   // waits for the matrix pipe, so spread between the MFMAs they would stall every one of them
   const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
+  ts[0] = ts[1] = 0.f;
 #pragma unroll
-  for (int g = 0; g < 2; ++g) {
+  for (int j = 0; j < 2; ++j)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int u = 0; u < 8; u += 2)
 #pragma unroll
-      for (int u = 0; u < 8; u += 2) {
+      for (int g = 0; g < 2; ++g) {
         const bf16x2 pr = {pn[g][j][u], pn[g][j][u + 1]};
-        if (u & 2) tb[g] = __builtin_amdgcn_fdot2_f32_bf16(pr, ones, tb[g], false);
-        else ta[g] = __builtin_amdgcn_fdot2_f32_bf16(pr, ones, ta[g], false);
+        ts[g] = __builtin_amdgcn_fdot2_f32_bf16(pr, ones, ts[g], false);
       }
-  }
-  ts[0] = ta[0] + tb[0];
-  ts[1] = ta[1] + tb[1];
   // every result is due here: otherwise the compiler sinks the softmax (and MFMAs) past the
   // masking branch that follows, into blocks of their own, and nothing overlaps any more
   asm volatile("" : "+v"(pn[0][0]), "+v"(pn[0][1]), "+v"(pn[1][0]), "+v"(pn[1][1]), "+v"(ts[0]), "+v"(ts[1]));
@@ -559,28 +555,39 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
   const int qb = qspecial ? 0 : (qt - g.nst) % g.NBf;
   const bool writer = kind == kSplit ? true : wactive;
 
-  int64_t qtok[2];
-  int frow[2];
+  // output token (or -1) and frame of the lane's two query rows; evaluated where they are used
+  // rather than held in registers through the key walk
+  auto row_info = [&](int64_t(&qtok)[2], int(&frow)[2]) {
 #pragma unroll
-  for (int gq = 0; gq < 2; ++gq) {
-    const int r = 32 * gq + col;
-    if (pat == SAF3R_BROADCAST) {
-      const int i = qt * 64 + r;
-      qtok[gq] = (writer && i < g.T) ? (int64_t)bfr * g.T + i : -1;
-      frow[gq] = bfr;
-    } else if (qspecial) {
-      const int64_t sl = (int64_t)qt * 64 + r;
-      qtok[gq] = (writer && sl < g.S) ? (sl / g.ns) * g.T + sl % g.ns : -1;
-      frow[gq] = g.ns > 0 ? (int)(sl / g.ns) : 0;
-    } else {
-      const int pp = qb * 64 + r;
-      qtok[gq] = (writer && pp < g.P) ? (int64_t)qf * g.T + g.ns + pp : -1;
-      frow[gq] = qf;
+    for (int gq = 0; gq < 2; ++gq) {
+      const int r = 32 * gq + col;
+      if (pat == SAF3R_BROADCAST) {
+        const int i = qt * 64 + r;
+        qtok[gq] = (writer && i < g.T) ? (int64_t)bfr * g.T + i : -1;
+        frow[gq] = bfr;
+      } else if (qspecial) {
+        const int64_t sl = (int64_t)qt * 64 + r;
+        qtok[gq] = (writer && sl < g.S) ? (sl / g.ns) * g.T + sl % g.ns : -1;
+        frow[gq] = g.ns > 0 ? (int)(sl / g.ns) : 0;
+      } else {
+        const int pp = qb * 64 + r;
+        qtok[gq] = (writer && pp < g.P) ? (int64_t)qf * g.T + g.ns + pp : -1;
+        frow[gq] = qf;
+      }
     }
-  }
+  };
+  auto store = [&](const Acc& A) {
+    int64_t qtok[2];
+    int frow[2];
+    row_info(qtok, frow);
+    store_rows(p, A, qtok, h, half);
+  };
   const int64_t head_base = (int64_t)h * g.L;
 
   if (kind == kSkip) {
+    int64_t qtok[2];
+    int frow[2];
+    row_info(qtok, frow);
 #pragma unroll
     for (int gq = 0; gq < 2; ++gq) {
       if (qtok[gq] >= 0) {
@@ -670,11 +677,11 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
     // thread tid owns 16-byte chunks tid and tid + 256 of the K and the V tile (64 rows of 128 B,
     // same offsets for both); LDS chunk position P holds row P/8, global chunk (P % 8) ^ swz8(row)
     // (unsigned 32-bit offsets from a uniform base: the loads take the scalar-base address form)
-    uint32_t dofs[2];
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int P = tid + 256 * u, r = P >> 3;
-      dofs[u] = (uint32_t)(r * 128 + (((P & 7) ^ swz8(r)) << 4));
+    // (chunk tid + 256 is row tid/8 + 32 with the same swizzle: offset + 4096)
+    uint32_t dofs;
+    {
+      const int r = tid >> 3;
+      dofs = (uint32_t)(r * 128 + (((tid & 7) ^ swz8(r)) << 4));
     }
     const char* kbase = reinterpret_cast<const char*>(p.k + head_base * 64);
     const char* vbase = reinterpret_cast<const char*>(p.v + head_base * 64);
@@ -693,8 +700,12 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
       char* st = ring + stage * 16384 + 64 * w * 16;
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
-        __builtin_amdgcn_global_load_lds((const void*)(kb + dofs[u]), (lds_void*)(st + 4096 * u), 16, 0, 0);
-        __builtin_amdgcn_global_load_lds((const void*)(vb + dofs[u]), (lds_void*)(st + 8192 + 4096 * u), 16, 0, 0);
+        uint32_t o = dofs;
+        const char* bk = kb + 4096 * u;
+        const char* bv = vb + 4096 * u;
+        asm volatile("" : "+v"(o), "+s"(bk), "+s"(bv));  // scalar-base address form (see split mode)
+        __builtin_amdgcn_global_load_lds((const void*)(bk + o), (lds_void*)(st + 4096 * u), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((const void*)(bv + o), (lds_void*)(st + 8192 + 4096 * u), 16, 0, 0);
       }
       wi.next(g);
     };
@@ -724,14 +735,17 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
         char* st = ring + stage * 16384 + 64 * w * 16;
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-          __builtin_amdgcn_global_load_lds((const void*)(kb + dofs[u]), (lds_void*)(st + 4096 * u), 16, 0, 0);
-          __builtin_amdgcn_global_load_lds((const void*)(vb + dofs[u]), (lds_void*)(st + 8192 + 4096 * u), 16, 0,
-                                           0);
+          uint32_t o = dofs;
+          const char* bk = kb + 4096 * u;
+          const char* bv = vb + 4096 * u;
+          asm volatile("" : "+v"(o), "+s"(bk), "+s"(bv));  // scalar-base address form (see split mode)
+          __builtin_amdgcn_global_load_lds((const void*)(bk + o), (lds_void*)(st + 4096 * u), 16, 0, 0);
+          __builtin_amdgcn_global_load_lds((const void*)(bv + o), (lds_void*)(st + 8192 + 4096 * u), 16, 0, 0);
         }
         kti = kti + 1 == count ? 0 : kti + 1;
       };
       if (count == 0) {
-        store_rows(p, A, qtok, h, half);
+        store(A);
         return;
       }
       wait_vm<0>();  // Q fragments landed; from here vmcnt counts ring loads only
@@ -798,11 +812,14 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
           A.o[dh][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[j][dh], pc[0][j], A.o[dh][0], 0, 0, 0);
           A.o[dh][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[j][dh], pc[1][j], A.o[dh][1], 0, 0, 0);
         }
-      store_rows(p, A, qtok, h, half);
+      store(A);
       return;
     }
 
     // ---- frame-relative walks (up to four ranges, frame masks): one tile per attend step ----
+    int64_t qtok_unused[2];
+    int frow[2];
+    row_info(qtok_unused, frow);
     wait_vm<0>();  // Q fragments landed; from here vmcnt counts ring loads only
     // tiles move in pairs: pair i+1 loads into the two free stages while pair i is consumed,
     // one barrier per pair
@@ -828,7 +845,7 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
         }
       }
     }
-    store_rows(p, A, qtok, h, half);
+    store(A);
     };
     if (pat == SAF3R_KEYSET || pat == SAF3R_BROADCAST) shared_walk(std::true_type{});
     else shared_walk(std::false_type{});
@@ -869,64 +886,132 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
       return __builtin_amdgcn_readfirstlane(list[w + 4 * ii]);
     };
 
-    // half-tile stream of this wave: (entry, half); the second half of a block is present when
-    // the block has more than 32 valid keys. Per-lane byte offsets of the 16-byte chunks a lane
-    // moves: K half = 32 rows x 8 chunks, V half = 64 rows x 4 chunks of 128-byte rows.
-    uint32_t kofs[4], vofs[4];
+    // Half-step stream of this wave: every listed block takes two 32-key half steps (a block with
+    // at most 32 valid keys has an all-masked second half), software-pipelined as in the
+    // single-range walk. The wave's 16 KB are two slots, one per half: slot hh holds K and V^T of
+    // half hh of a block, 4 KB each. At the end of half step h the wave loads K of step h + 3 and
+    // V of step h + 1 into the regions step h has just finished with; past the end of the list
+    // the last block is loaded again, so every step issues the same 8 loads a lane and one
+    // vmcnt wait serves every step. Per-lane byte offsets of the 16-byte chunks a lane moves:
+    // K half = 32 rows x 8 chunks, V half = 64 rows x 4 chunks of 128-byte rows.
+    // Lane offsets of the 16-byte chunks: K chunk u of a lane = row 8u + lane/8, whose swizzle
+    // differs between even and odd u only (2 offsets + multiples of 1024); V chunk u = row
+    // 16u + lane/4, whose swizzle does not depend on u (1 offset + multiples of 2048). The offsets
+    // pass through an empty asm so that the compiler cannot fold them into hoisted 64-bit per-lane
+    // addresses (two registers per load held through the loop): the loads keep the scalar-base
+    // form, uniform address plus 32-bit lane offset.
+    uint32_t ko[2], vo;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int P = 64 * u + lane;
-      const int r = P >> 3, i = P >> 2;
-      kofs[u] = (uint32_t)(r * 128 + (((P & 7) ^ swz8(r)) << 4));
-      vofs[u] = (uint32_t)(i * 128 + (((P & 3) ^ swz4(i)) << 4));
+    for (int u = 0; u < 2; ++u) {
+      const int P = 64 * u + lane, r = P >> 3;
+      ko[u] = (uint32_t)(r * 128 + (((P & 7) ^ swz8(r)) << 4));
+    }
+    {
+      const int i = lane >> 2;
+      vo = (uint32_t)(i * 128 + (((lane & 3) ^ swz4(i)) << 4));
     }
     const char* kbase = reinterpret_cast<const char*>(p.k + head_base * 64);
     const char* vbase = reinterpret_cast<const char*>(p.v + head_base * 64);
-    char* slots = ring + w * 16384;  // two 8 KB slots: K half (4 KB) + V half (4 KB)
-    auto issue = [&](int e, int hh, int sl) {
-      const int64_t t = (int64_t)(e >> 7) * 8192;
-      const char* kb = kbase + t + hh * 4096;
-      const char* vb = vbase + t + hh * 64;
-      char* st = slots + sl * 8192;
+    char* slots = ring + w * 16384;
+    auto issue_k = [&](int e, int hh) {
+      const char* kb = kbase + (int64_t)(e >> 7) * 8192 + hh * 4096;
+      char* st = slots + hh * 8192;
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        __builtin_amdgcn_global_load_lds((const void*)(kb + kofs[u]), (lds_void*)(st + 64 * u * 16), 16, 0, 0);
-        __builtin_amdgcn_global_load_lds((const void*)(vb + vofs[u]), (lds_void*)(st + 4096 + 64 * u * 16), 16, 0, 0);
+        uint32_t o = ko[u & 1];
+        const char* b = kb + 1024 * (u & 2);
+        asm volatile("" : "+v"(o), "+s"(b));
+        __builtin_amdgcn_global_load_lds((const void*)(b + o), (lds_void*)(st + 64 * u * 16), 16, 0, 0);
       }
+    };
+    auto issue_v = [&](int e, int hh) {
+      const char* vb = vbase + (int64_t)(e >> 7) * 8192 + hh * 64;
+      char* st = slots + hh * 8192 + 4096;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        uint32_t o = vo;
+        const char* b = vb + 2048 * u;
+        asm volatile("" : "+v"(o), "+s"(b));
+        __builtin_amdgcn_global_load_lds((const void*)(b + o), (lds_void*)(st + 64 * u * 16), 16, 0, 0);
+      }
+    };
+    // V^T fragments of a staged half (64-byte rows, swz4)
+    auto load_vh = [&](const char* vst, bf16x8(&vf)[2][2]) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int dh = 0; dh < 2; ++dh) {
+          const int r = 32 * dh + col, chn = 2 * j + half;
+          vf[j][dh] = *reinterpret_cast<const bf16x8*>(vst + r * 64 + ((chn ^ swz4(r)) << 4));
+        }
     };
 
     wait_vm<0>();
-    int i = 0, hh = 0, cur = 0;
-    int e = nw > 0 ? entry(0) : 0;
-    if (nw > 0) issue(e, 0, 0);
-    while (i < nw) {
-      int ni = i, nhh, ne = e;
-      if (hh == 0 && (e & 127) > 32) nhh = 1;
-      else {
-        nhh = 0;
-        ++ni;
-        if (ni < nw) ne = entry(ni);
+    if (nw > 0) {
+      const auto ent = [&](int i) { return entry(min(i, nw - 1)); };
+      int e0 = ent(0), e1 = ent(1), e2 = ent(2);
+      issue_k(e0, 0);
+      issue_k(e0, 1);
+      issue_v(e0, 0);
+      wait_vm<8>();
+      f32x16 s_cur[2], s_nxt[2];
+      bf16x8 pc[2][2], pn[2][2], kf[4], vf[2][2];
+      float ts[2];
+      load_k(slots, 0, kf, half, col);
+      s_cur[0] = s_cur[1] = f32x16{};
+#pragma unroll
+      for (int st = 0; st < 4; ++st) {
+        s_cur[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[st], qfrag[0][st], s_cur[0], 0, 0, 0);
+        s_cur[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[st], qfrag[1][st], s_cur[1], 0, 0, 0);
       }
-      const bool more = ni < nw;
-      if (more) {
-        issue(ne, nhh, cur ^ 1);
+      if ((e0 & 127) < 32) mask_valid(s_cur, e0 & 127, 0, half);
+      issue_k(e1, 0);  // the K fragments above have been read: slot 0's K is free
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int x = 0; x < 2; ++x) {
+          pc[j][x] = bf16x8{};
+          vf[j][x] = bf16x8{};
+        }
+      for (int t = 0; t < nw; ++t) {
+        // half step 2t: PV of block t-1 half 1, scores of block t half 1, softmax of block t half 0
         wait_vm<8>();
-      } else {
-        wait_vm<0>();
+        if (t > 0) load_vh(slots + 8192 + 4096, vf);
+        load_k(slots + 8192, 0, kf, half, col);
+        half_block(kf, vf, qfrag, s_cur, s_nxt, pc, pn, ts, A, c);
+        issue_k(e1, 1);
+        issue_v(e0, 1);
+        const int kv0 = e0 & 127;
+        if (kv0 < 64) mask_valid(s_nxt, kv0, 32, half);
+        exact_fix(s_cur, pn, ts, A, c);
+        A.l[0] += ts[0];
+        A.l[1] += ts[1];
+        // half step 2t+1: PV of block t half 0, scores of block t+1 half 0, softmax of block t half 1
+        wait_vm<8>();
+        load_vh(slots + 4096, vf);
+        load_k(slots, 0, kf, half, col);
+        half_block(kf, vf, qfrag, s_nxt, s_cur, pn, pc, ts, A, c);
+        issue_k(e2, 0);
+        issue_v(e1, 0);
+        const int kv1 = e1 & 127;
+        if (kv1 < 32) mask_valid(s_cur, kv1, 0, half);
+        exact_fix(s_nxt, pc, ts, A, c);
+        A.l[0] += ts[0];
+        A.l[1] += ts[1];
+        e0 = e1;
+        e1 = e2;
+        e2 = ent(t + 3);
       }
-      TileMask tm;
-      tm.kt = e >> 7;
-      tm.kspecial = false;
-      tm.kframe = 0;
-      tm.eff = SAF3R_DENSE;
-      tm.kvalid = e & 127;
-      tm.need = tm.kvalid < 32 * (hh + 1);
-      const char* st = slots + cur * 8192;
-      attend<1>(st, st + 4096, qfrag, A, frow, tm, g, p.nsmagic, 32 * hh, half, col, c, []() {});
-      i = ni;
-      hh = nhh;
-      e = ne;
-      cur ^= 1;
+      // PV of the last block's second half
+      wait_vm<0>();
+      load_vh(slots + 8192 + 4096, vf);
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int dh = 0; dh < 2; ++dh) {
+          A.o[dh][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[j][dh], pc[0][j], A.o[dh][0], 0, 0, 0);
+          A.o[dh][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[j][dh], pc[1][j], A.o[dh][1], 0, 0, 0);
+        }
     }
 
     // ---- merge the four partial results through LDS ----
