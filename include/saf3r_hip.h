@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define SAF3R_ABI_VERSION 3
+#define SAF3R_ABI_VERSION 4
 
 enum saf3r_status {
   SAF3R_OK = 0,
@@ -99,6 +99,9 @@ int64_t saf3r_packed_slots(int frames, int tokens_per_frame, int num_special);
  *   rope_cos, rope_sin: device fp32 [rope_positions][16] tables, cos / sin of
  *            position * inv_freq[i] (inv_freq[i] = 1 / base^(2i/32)); NULL disables RoPE.
  *            Positions are clamped to [0, rope_positions - 1].
+ *   token_order: host uint8 [num_heads] or NULL. A head h < 64 with token_order[h] != 0 is packed
+ *            in token order instead: slot t holds token t (t < F*T), no special or per-frame
+ *            padding (the layout saf3r_sparse_attn_fwd reads for a DENSE head flagged the same way).
  * Replaces: saf3r/patch/patch_vggt.py:577-583 (qkv reshape, q_norm/k_norm, rope) and
  *           saf3r/models/official_vggt/layers/rope.py:154-188.
  */
@@ -107,7 +110,7 @@ int saf3r_pack_qkv(const void* q, const void* k, const void* v, int64_t tok_stri
                    const float* q_ln_weight, const float* q_ln_bias, const float* k_ln_weight,
                    const float* k_ln_bias, float ln_eps, int apply_ln,
                    const int32_t* pos, const float* rope_cos, const float* rope_sin, int rope_positions,
-                   void* q_packed, void* k_packed, void* v_packed, void* stream);
+                   void* q_packed, void* k_packed, void* v_packed, const uint8_t* token_order, void* stream);
 
 /*
  * Pooled patch-block means (fp32) of the packed Q and K of the listed heads.
@@ -206,6 +209,9 @@ int saf3r_keyset_gather(const void* k_packed, int frames, int tokens_per_frame, 
  *          bcast_v: bf16 [n_broadcast][F][C/64] key-set V tiles (saf3r_keyset_gather layout) of
  *                   frame f's tokens f*T .. f*T+T-1.
  *        NULL when no head is BROADCAST.
+ *   token_order: host uint8 [num_heads] or NULL: DENSE heads packed in token order by
+ *        saf3r_pack_qkv (the flag is an error on any other pattern). Their key and query tiles
+ *        then cover the F*T tokens without padding.
  * Replaces: the per-head loop saf3r/patch/wrapper.py:94-106 and the mode implementations of
  *           saf3r/patch/sparse_attention.py:12-90 for full / global_to_frame / all_to_first / skip /
  *           stride / q_probe_topk (over their key sets) / broadcast_first, the dense special rows of
@@ -216,7 +222,7 @@ int saf3r_sparse_attn_fwd(const void* q_packed, const void* k_packed, const void
                           const int32_t* sel, int sel_width, float scale, void* out, int64_t out_row_stride,
                           const void* keyset_k, const void* keyset_v, const int32_t* keyset_count,
                           int64_t keyset_capacity, const void* bcast_q, const void* bcast_k,
-                          const void* bcast_v, void* stream);
+                          const void* bcast_v, const uint8_t* token_order, void* stream);
 
 /*
  * Gather attention: out[r] = sum_j softmax_j(q[r] . k[idx[r][j]] * scale) v[idx[r][j]], fp32

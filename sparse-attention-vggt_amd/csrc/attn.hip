@@ -69,6 +69,9 @@ struct AttnParams {
   const __bf16* bk;      // BROADCAST heads: frame 0 K rows [head][bcap][64]
   const __bf16* bv;      // BROADCAST heads: V tiles [head][frame][bcap/64][64][64]
   int bcap;              // ceil(T/64)*64
+  uint64_t tok_order;    // DENSE heads (bit h) packed in token order: tile t = tokens 64t .. 64t+63
+  int ntok;              // F*T tokens
+  int ntt;               // ceil(F*T/64) token-order tiles
   // work items in segments of one head each (a head has at most two: special-row and patch-row
   // items), ordered longest item first; segment i covers blocks item_start[i] .. item_start[i+1]-1
   // and items item_base[i] ... of head order[i]
@@ -519,9 +522,10 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
   const int groups_pf = (g.NBf + 3) >> 2;
   int qt0, nw, kind;
   int bfr = 0;  // BROADCAST: the frame whose rows the item writes
+  const bool tokord = pat == SAF3R_DENSE && ((p.tok_order >> h) & 1);
   if (pat == SAF3R_DENSE || pat == SAF3R_SKIP || pat == SAF3R_KEYSET) {
     qt0 = 4 * it;
-    nw = min(4, g.NT - qt0);
+    nw = min(4, (tokord ? p.ntt : g.NT) - qt0);
     kind = pat == SAF3R_SKIP ? kSkip : kShared;
   } else if (pat == SAF3R_BROADCAST) {
     // query tile qt of frame 0's compact rows, written for frame bfr
@@ -550,7 +554,7 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
   }
   const bool wactive = w < nw;
   const int qt = kind == kSplit ? qt0 : qt0 + (wactive ? w : 0);
-  const bool qspecial = pat != SAF3R_BROADCAST && qt < g.nst;
+  const bool qspecial = pat != SAF3R_BROADCAST && !tokord && qt < g.nst;
   const int qf = qspecial ? 0 : (qt - g.nst) / g.NBf;
   const int qb = qspecial ? 0 : (qt - g.nst) % g.NBf;
   const bool writer = kind == kSplit ? true : wactive;
@@ -565,6 +569,10 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
         const int i = qt * 64 + r;
         qtok[gq] = (writer && i < g.T) ? (int64_t)bfr * g.T + i : -1;
         frow[gq] = bfr;
+      } else if (tokord) {
+        const int i = qt * 64 + r;
+        qtok[gq] = (writer && i < p.ntok) ? (int64_t)i : -1;
+        frow[gq] = 0;
       } else if (qspecial) {
         const int64_t sl = (int64_t)qt * 64 + r;
         qtok[gq] = (writer && sl < g.S) ? (sl / g.ns) * g.T + sl % g.ns : -1;
@@ -633,10 +641,13 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
                         ? SAF3R_DENSE
                         : pat;
     // KEYSET heads walk the compact tiles of their key set, key k of the set being slot k there;
-    // BROADCAST heads walk frame 0's compact K with the V tiles of the item's frame
+    // BROADCAST heads walk frame 0's compact K with the V tiles of the item's frame; token-order
+    // DENSE heads walk their own rows, every token a key
     int ks_keys = 0;
     if constexpr (keyset)
-      ks_keys = __builtin_amdgcn_readfirstlane(pat == SAF3R_BROADCAST ? g.T : p.ks_count[p.slot[h]]);
+      ks_keys = __builtin_amdgcn_readfirstlane(pat == SAF3R_BROADCAST ? g.T
+                                               : tokord               ? p.ntok
+                                                                      : p.ks_count[p.slot[h]]);
     if constexpr (keyset) {
       wk.init(0, (ks_keys + 63) / 64, 0, 0, 0, 0, 0, 0);
     } else if (eff == SAF3R_DENSE) {
@@ -689,6 +700,8 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
       if (pat == SAF3R_BROADCAST) {
         kbase = reinterpret_cast<const char*>(p.bk + (int64_t)p.slot[h] * p.bcap * 64);
         vbase = reinterpret_cast<const char*>(p.bv + ((int64_t)p.slot[h] * g.F + bfr) * p.bcap * 64);
+      } else if (tokord) {
+        // token-order DENSE head: its own packed rows, walked like a key set of all F*T tokens
       } else {
         kbase = reinterpret_cast<const char*>(p.kc + (int64_t)p.slot[h] * p.ks_cap * 64);
         vbase = reinterpret_cast<const char*>(p.vc + (int64_t)p.slot[h] * p.ks_cap * 64);
@@ -847,7 +860,7 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
     }
     store(A);
     };
-    if (pat == SAF3R_KEYSET || pat == SAF3R_BROADCAST) shared_walk(std::true_type{});
+    if (pat == SAF3R_KEYSET || pat == SAF3R_BROADCAST || tokord) shared_walk(std::true_type{});
     else shared_walk(std::false_type{});
     return;
   }
@@ -1093,14 +1106,18 @@ struct Seg {
   int64_t steps;
 };
 
-static int head_segments(int h, int pat, const Geom& g, int sel_width, int64_t ks_cap, Seg* out) {
+static int head_segments(int h, int pat, bool tokord, int ntt, const Geom& g, int sel_width, int64_t ks_cap,
+                         Seg* out) {
   const int ns4 = (g.nst + 3) / 4, groups_pf = (g.NBf + 3) / 4;
   int n = 0;
   auto add = [&](int base, int items, int64_t steps) {
     if (items > 0) out[n++] = Seg{h, base, items, steps};
   };
   switch (pat) {
-    case SAF3R_DENSE: add(0, (g.NT + 3) / 4, g.NT); break;
+    case SAF3R_DENSE:
+      if (tokord) add(0, (ntt + 3) / 4, ntt);
+      else add(0, (g.NT + 3) / 4, g.NT);
+      break;
     case SAF3R_KEYSET: add(0, (g.NT + 3) / 4, ks_cap / 64); break;
     case SAF3R_BROADCAST: {
       const int nq = (g.T + 63) / 64;
@@ -1156,7 +1173,8 @@ extern "C" int saf3r_sparse_attn_fwd(const void* q_packed, const void* k_packed,
                                      const int32_t* head_pattern, const int32_t* sel, int sel_width, float scale,
                                      void* out, int64_t out_row_stride, const void* keyset_k, const void* keyset_v,
                                      const int32_t* keyset_count, int64_t keyset_capacity, const void* bcast_q,
-                                     const void* bcast_k, const void* bcast_v, void* stream) {
+                                     const void* bcast_k, const void* bcast_v, const uint8_t* token_order,
+                                     void* stream) {
   if (int e = injected("saf3r_sparse_attn_fwd")) return e;
   AttnParams p;
   if (!make_geom(frames, tokens_per_frame, num_special, &p.g))
@@ -1206,6 +1224,19 @@ extern "C" int saf3r_sparse_attn_fwd(const void* q_packed, const void* k_packed,
       return fail(SAF3R_ERR_UNSUPPORTED, "saf3r_sparse_attn_fwd: sel_width must be in [1, %d] (got %d)", kMaxList,
                   sel_width);
   }
+  p.tok_order = 0;
+  if ((int64_t)frames * tokens_per_frame > 0x7fffffc0ll)
+    return fail(SAF3R_ERR_UNSUPPORTED, "saf3r_sparse_attn_fwd: too many tokens");
+  p.ntok = frames * tokens_per_frame;
+  p.ntt = (p.ntok + 63) / 64;
+  if (token_order) {
+    for (int h = 0; h < num_heads; ++h) {
+      if (!token_order[h]) continue;
+      if (p.pattern[h] != SAF3R_DENSE)
+        return fail(SAF3R_ERR_INVALID, "saf3r_sparse_attn_fwd: head %d: only DENSE heads take the token-order layout", h);
+      p.tok_order |= 1ull << h;
+    }
+  }
   p.q = (const __bf16*)q_packed;
   p.k = (const __bf16*)k_packed;
   p.v = (const __bf16*)v_packed;
@@ -1221,7 +1252,8 @@ extern "C" int saf3r_sparse_attn_fwd(const void* q_packed, const void* k_packed,
   Seg segs[kMaxSegs];
   int nseg = 0;
   for (int h = 0; h < num_heads; ++h)
-    nseg += head_segments(h, p.pattern[h], p.g, sel_width, keyset_capacity, segs + nseg);
+    nseg += head_segments(h, p.pattern[h], (p.tok_order >> h) & 1, p.ntt, p.g, sel_width, keyset_capacity,
+                          segs + nseg);
   for (int i = 1; i < nseg; ++i) {  // stable: longest item first
     const Seg x = segs[i];
     int j = i;

@@ -31,6 +31,7 @@ struct PackParams {
   __bf16* kp;
   __bf16* vp;
   Geom g;
+  uint64_t tok_order;  // heads (bit h) packed in token order: slot = token, no special/frame padding
 };
 
 // One 256-thread workgroup per (64-slot tile, head). Four threads own one slot row, 16 features
@@ -41,7 +42,8 @@ __global__ __launch_bounds__(256) void pack_qkv_kernel(PackParams p) {
   const int tile = blockIdx.x, h = blockIdx.y;
   const int t = threadIdx.x, row = t >> 2, c = t & 3;
   const int64_t slot = (int64_t)tile * 64 + row;
-  const int64_t tok = slot_token(g, slot);
+  const int64_t ntok = (int64_t)g.F * g.T;
+  const int64_t tok = (h < 64 && ((p.tok_order >> h) & 1)) ? (slot < ntok ? slot : -1) : slot_token(g, slot);
   const int64_t src = tok * p.tok_stride + (int64_t)h * p.head_stride + 16 * c;
   const int64_t dst = ((int64_t)h * g.L + slot) * 64 + 16 * c;
 
@@ -171,7 +173,7 @@ extern "C" int saf3r_pack_qkv(const void* q, const void* k, const void* v, int64
                               const float* q_ln_weight, const float* q_ln_bias, const float* k_ln_weight,
                               const float* k_ln_bias, float ln_eps, int apply_ln, const int32_t* pos,
                               const float* rope_cos, const float* rope_sin, int rope_positions, void* q_packed,
-                              void* k_packed, void* v_packed, void* stream) {
+                              void* k_packed, void* v_packed, const uint8_t* token_order, void* stream) {
   if (int e = injected("saf3r_pack_qkv")) return e;
   PackParams p;
   if (!make_geom(frames, tokens_per_frame, num_special, &p.g))
@@ -207,6 +209,14 @@ extern "C" int saf3r_pack_qkv(const void* q, const void* k, const void* v, int64
   p.qp = (__bf16*)q_packed;
   p.kp = (__bf16*)k_packed;
   p.vp = (__bf16*)v_packed;
+  p.tok_order = 0;
+  if (token_order) {
+    for (int h = 0; h < num_heads; ++h) {
+      if (!token_order[h]) continue;
+      if (h >= 64) return fail(SAF3R_ERR_UNSUPPORTED, "saf3r_pack_qkv: token order is supported for heads 0..63");
+      p.tok_order |= 1ull << h;
+    }
+  }
   dim3 grid(p.g.NT, num_heads);
   hipLaunchKernelGGL(pack_qkv_kernel, grid, dim3(256), 0, (hipStream_t)stream, p);
   return check_launch("saf3r_pack_qkv");

@@ -55,6 +55,22 @@ def _i32_array(vals: Sequence[int]):
     return arr
 
 
+def _u8_flags(flags: Sequence[bool] | None, n: int):
+    """Host uint8 [n] flag array for the C ABI (None: no array)."""
+    if flags is None:
+        return None
+    flags = list(flags)
+    if len(flags) != n:
+        raise ValueError(f"one flag per head: got {len(flags)} for {n} heads")
+    return (ctypes.c_uint8 * n)(*[1 if f else 0 for f in flags])
+
+
+def token_order_heads(patterns: Sequence[int]) -> list[bool]:
+    """Heads that take the token-order packed layout: the DENSE ones (no special or per-frame
+    padding, so none of their query or key tiles is partly empty)."""
+    return [int(p) == DENSE for p in patterns]
+
+
 def rope_inv_freq(base: float = 100.0, feature_dim: int = 32) -> torch.Tensor:
     """Inverse frequencies of the 2-D RoPE (``rope.py:103-104``) for fp32 tokens (CPU tensor)."""
     exponents = torch.arange(0, feature_dim, 2).float() / feature_dim
@@ -84,11 +100,13 @@ def packed_buffers(geom: Geometry, num_heads: int, device) -> tuple[torch.Tensor
 
 
 def pack_qkv(q, k, v, tok_stride: int, head_stride: int, geom: Geometry, num_heads: int,
-             ln_q=None, ln_k=None, ln_eps: float = 1e-5, pos=None, rope_base=None, rope_positions=None, out=None):
+             ln_q=None, ln_k=None, ln_eps: float = 1e-5, pos=None, rope_base=None, rope_positions=None, out=None,
+             token_order: Sequence[bool] | None = None):
     """QK-LayerNorm + RoPE-2D + packing (``saf3r_pack_qkv``). ``q``/``k``/``v`` are tensors (or
     views) whose element (t, h, d) is at ``data_ptr + t*tok_stride + h*head_stride + d``.
     RoPE is applied when ``rope_base`` is given; ``rope_positions`` is the table length
-    (default: max position + 1, which costs one device-to-host read)."""
+    (default: max position + 1, which costs one device-to-host read). Heads flagged in
+    ``token_order`` are packed in token order (see ``token_order_heads``)."""
     _need_cuda(q, k, v)
     lib = _lib.load()
     qp, kp, vp = out if out is not None else packed_buffers(geom, num_heads, q.device)
@@ -110,7 +128,7 @@ def pack_qkv(q, k, v, tok_stride: int, head_stride: int, geom: Geometry, num_hea
         _ptr(q), _ptr(k), _ptr(v), tok_stride, head_stride, geom.frames, geom.tokens_per_frame, geom.num_special,
         num_heads, _ptr(qw), _ptr(qb), _ptr(kw), _ptr(kb), float(ln_eps), int(apply_ln),
         _ptr(pos) if rc is not None else None, _ptr(rc), _ptr(rs), npos, _ptr(qp), _ptr(kp), _ptr(vp),
-        _lib.stream_ptr()))
+        _u8_flags(token_order, num_heads), _lib.stream_ptr()))
     return qp, kp, vp
 
 
@@ -188,10 +206,12 @@ def block_select(pooled_q: torch.Tensor, pooled_k: torch.Tensor, frames: int, bl
 
 def sparse_attn_fwd(qp, kp, vp, geom: Geometry, patterns: Sequence[int], sel: torch.Tensor | None = None,
                     scale: float | None = None, out: torch.Tensor | None = None,
-                    keysets: "KeySets | None" = None, broadcast: "Broadcast | None" = None) -> torch.Tensor:
+                    keysets: "KeySets | None" = None, broadcast: "Broadcast | None" = None,
+                    token_order: Sequence[bool] | None = None) -> torch.Tensor:
     """All heads in one launch. Returns (or fills) ``out`` bf16 [N, H*64] in natural token order.
     ``keysets`` carries the compact K/V of the KEYSET heads and ``broadcast`` the frame-0 / per-frame
-    buffers of the BROADCAST heads (each in increasing head order)."""
+    buffers of the BROADCAST heads (each in increasing head order); ``token_order`` flags the
+    DENSE heads that ``pack_qkv`` packed in token order."""
     _need_cuda(qp, kp, vp)
     lib = _lib.load()
     H = qp.shape[0]
@@ -233,7 +253,7 @@ def sparse_attn_fwd(qp, kp, vp, geom: Geometry, patterns: Sequence[int], sel: to
     _lib.check(lib.saf3r_sparse_attn_fwd(
         _ptr(qp), _ptr(kp), _ptr(vp), geom.frames, geom.tokens_per_frame, geom.num_special, H,
         pat, _ptr(sel), width, float(scale), _ptr(out), out.stride(0), _ptr(ks_k), _ptr(ks_v), _ptr(ks_n),
-        ks_cap, _ptr(bq), _ptr(bk), _ptr(bv), _lib.stream_ptr()))
+        ks_cap, _ptr(bq), _ptr(bk), _ptr(bv), _u8_flags(token_order, H), _lib.stream_ptr()))
     _mark("sparse_attn", "end")
     return out
 

@@ -113,8 +113,9 @@ class BaseHeadwiseSparseAttentionWrapper(nn.Module):
             p2 = pos.reshape(-1, 2)
             # table length: the patch grid bounds every position ((y+1, x+1) with specials at 0)
             npos = max(self.patch_height, self.patch_width) + 1 if self.patch_height else None
+        tord = ops.token_order_heads(self.patterns)  # dense heads: unpadded token-order tiles
         qp, kp, vp = ops.pack_qkv(qkv, qkv[:, C:], qkv[:, 2 * C:], 3 * C, HEAD_DIM, geom, H, ln_q=ln_q, ln_k=ln_k,
-                                  ln_eps=eps, pos=p2, rope_base=base, rope_positions=npos)
+                                  ln_eps=eps, pos=p2, rope_base=base, rope_positions=npos, token_order=tord)
         sel = None
         if self.dyn_heads:
             pq, pk = ops.block_pool(qp, kp, geom, self.dyn_heads)
@@ -129,7 +130,8 @@ class BaseHeadwiseSparseAttentionWrapper(nn.Module):
         bcast = None
         if self.broadcast_heads:  # broadcast_first: frame 0's Q/K rows and every frame's V tiles
             bcast = ops.broadcast_gather(qp, kp, geom, self.broadcast_heads, qkv[:, 2 * C:], qkv.stride(0), HEAD_DIM)
-        out = ops.sparse_attn_fwd(qp, kp, vp, geom, self.patterns, sel, keysets=keysets, broadcast=bcast)
+        out = ops.sparse_attn_fwd(qp, kp, vp, geom, self.patterns, sel, keysets=keysets, broadcast=bcast,
+                                  token_order=tord)
         if self.dino_heads:
             est = self.est_topk_idx
             P, W = geom.patches, est.shape[1]

@@ -56,6 +56,26 @@ def test_pack_layout_bit_exact(ops, pkg, F, T, ns):
     assert torch.equal(nat, v) and (pad == 0).all()
 
 
+@pytest.mark.parametrize("F,T,ns", GEOMS)
+def test_pack_token_order_bit_exact(ops, pkg, F, T, ns):
+    """Flagged heads: slot t holds token t, zeros past F*T; the others keep the padded layout."""
+    geom = pkg.Geometry(F, T, ns)
+    H = 3
+    q, k, v = _qkv(H, geom.tokens, seed=F * 5 + T)
+    flags = [True, False, True]
+    qp, kp, vp = ops.pack_heads(q.to(DEV), k.to(DEV), v.to(DEV), geom, token_order=flags)
+    torch.cuda.synchronize()
+    padded = slot_tokens(F, T, ns)
+    tokord = torch.tensor([t if t < geom.tokens else -1 for t in range(geom.slots)])
+    for h, fl in enumerate(flags):
+        toks = tokord if fl else padded
+        for src, pk in ((q, qp), (k, kp)):
+            nat, pad = unpack_rows(pk[h:h + 1].cpu(), toks, geom.tokens)
+            assert torch.equal(nat[0], src[h]) and (pad == 0).all()
+        nat, pad = unpack_v(vp[h:h + 1].cpu(), toks, geom.tokens)
+        assert torch.equal(nat[0], v[h]) and (pad == 0).all()
+
+
 def test_pack_layernorm_rope(ops, pkg):
     geom = pkg.Geometry(3, 5 + 7 * 9, 5)
     H, N = 4, geom.tokens
@@ -149,6 +169,27 @@ def test_sparse_attention_all_patterns(ops, pkg, F, T, ns):
         ref = OA.sparse_attention_gathered(q[h].float(), k[h].float(), v[h].float(), pat, og, sel_by_head.get(h),
                                            dtype=torch.float64)
         _check_close(got[h], ref, f"F{F} T{T} ns{ns} head {h} pattern {pat}")
+
+
+@pytest.mark.parametrize("F,T,ns", GEOMS)
+def test_sparse_attention_token_order_dense(ops, pkg, F, T, ns):
+    """DENSE heads in the token-order layout, in one launch with padded-layout heads."""
+    geom = pkg.Geometry(F, T, ns)
+    patterns = [ops.DENSE, ops.FRAME_LOCAL, ops.DENSE, ops.BLOCK_DYNAMIC, ops.DENSE]
+    H = len(patterns)
+    q, k, v = _qkv(H, geom.tokens, seed=F * 17 + T, scale=1.5)
+    flags = ops.token_order_heads(patterns)
+    qp, kp, vp = ops.pack_heads(q.to(DEV), k.to(DEV), v.to(DEV), geom, token_order=flags)
+    pq, pk = ops.block_pool(qp, kp, geom, [3])
+    sel = ops.block_select(pq, pk, geom.frames, geom.blocks_per_frame, 2)
+    out = ops.sparse_attn_fwd(qp, kp, vp, geom, patterns, sel, token_order=flags)
+    torch.cuda.synchronize()
+    og = OA.Geometry(F, T, ns)
+    got = out.float().cpu().reshape(geom.tokens, H, 64).permute(1, 0, 2)
+    for h, pat in enumerate(patterns):
+        ref = OA.sparse_attention_gathered(q[h].float(), k[h].float(), v[h].float(), pat, og,
+                                           sel[0].cpu() if h == 3 else None, dtype=torch.float64)
+        _check_close(got[h], ref, f"token order F{F} T{T} ns{ns} head {h} pattern {pat}")
 
 
 def test_sparse_attention_selection_edge_cases(ops, pkg):
