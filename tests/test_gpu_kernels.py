@@ -192,6 +192,40 @@ def test_sparse_attention_token_order_dense(ops, pkg, F, T, ns):
         _check_close(got[h], ref, f"token order F{F} T{T} ns{ns} head {h} pattern {pat}")
 
 
+@pytest.mark.parametrize("phase", ["off", None])
+def test_sparse_attention_outrun_reference(ops, pkg, monkeypatch, phase):
+    """Keys whose scores exceed the lazily moved reference maximum by more than 2^64 in P (and one
+    beyond the fp32 exponent range) must take the exact path: rescale O and l, recompute P. Every
+    pattern must still match the oracle. With the walk phase off every walk starts at its first
+    tile, so the outliers (last frame) are met late."""
+    if phase is not None:
+        monkeypatch.setenv("SAF3R_ATTN_PHASE", phase)
+    geom = pkg.Geometry(3, 155, 5)
+    patterns = [ops.DENSE, ops.DENSE, ops.BLOCK_DYNAMIC, ops.FRAME_LOCAL, ops.ANCHOR_LOCAL]
+    H = len(patterns)
+    g = torch.Generator().manual_seed(5)
+    N = geom.tokens
+    q = (0.5 + 0.1 * torch.randn(H, N, 64, generator=g)).to(torch.bfloat16)
+    k = (0.3 * torch.randn(H, N, 64, generator=g)).to(torch.bfloat16)
+    v = torch.randn(H, N, 64, generator=g).to(torch.bfloat16)
+    last = (geom.frames - 1) * geom.tokens_per_frame
+    k[:, last + 40] = 12.0   # q.k ~ 384: about 69 log2 units above the first steps
+    k[:, last + 100] = 30.0  # about 173 log2 units: exp2 overflows fp32 in the fast pass
+    flags = [True, False, False, False, False]  # dense head 0 token order, head 1 padded
+    qp, kp, vp = ops.pack_heads(q.to(DEV), k.to(DEV), v.to(DEV), geom, token_order=flags)
+    pq, pk = ops.block_pool(qp, kp, geom, [2])
+    sel = ops.block_select(pq, pk, geom.frames, geom.blocks_per_frame, 2)
+    out = ops.sparse_attn_fwd(qp, kp, vp, geom, patterns, sel, token_order=flags)
+    torch.cuda.synchronize()
+    og = OA.Geometry(3, 155, 5)
+    got = out.float().cpu().reshape(N, H, 64).permute(1, 0, 2)
+    assert torch.isfinite(got).all()
+    for h, pat in enumerate(patterns):
+        ref = OA.sparse_attention_gathered(q[h].float(), k[h].float(), v[h].float(), pat, og,
+                                           sel[0].cpu() if h == 2 else None, dtype=torch.float64)
+        _check_close(got[h], ref, f"outrun phase={phase} head {h} pattern {pat}")
+
+
 def test_sparse_attention_selection_edge_cases(ops, pkg):
     """Hand-made selection lists: -1 entries, a single block, whole-frame selections."""
     geom = pkg.Geometry(3, 155, 5)
