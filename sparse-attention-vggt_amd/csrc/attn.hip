@@ -58,7 +58,7 @@ struct AttnParams {
   Geom g;
   int sel_width;
   float c;  // softmax scale * log2(e)
-  uint32_t nsmagic;  // ceil(2^32 / ns): frame of a special slot = umulhi(slot, nsmagic)
+  uint32_t nsmagic;  // ceil(2^32 / ns): frame of a special slot = umulhi(slot, nsmagic); 0 for ns <= 1
   uint64_t phase_dense;  // wall-clock ticks per key-tile step of a dense walk (0: fixed order)
   uint64_t phase_split;  // wall-clock ticks per list position of a split-mode wave (0: fixed order)
   const __bf16* kc;      // KEYSET heads: compact K [set][cap][64]
@@ -112,6 +112,10 @@ __device__ inline void barrier_only() {
 // different masks, so 16 lanes reading 16 consecutive rows at one logical chunk hit 16 distinct
 // 16-byte bank groups whether the LDS serves 8 lanes over 32 banks or 16 lanes over 64 banks.
 // 64-byte rows (4 chunks) use the analogous mask.
+// high word of a 32 x 32-bit product as one multiply instruction (the __umulhi library routine is
+// an out-of-line call here, with the call's register saves, once per use)
+__device__ __forceinline__ uint32_t mulhi_u32(uint32_t a, uint32_t b) { return (uint32_t)(((uint64_t)a * b) >> 32); }
+
 __device__ inline int swz8(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 __device__ inline int swz4(int r) { return ((r >> 1) & 3) ^ ((r >> 3) & 1); }
 
@@ -164,9 +168,10 @@ __device__ __forceinline__ void attend(const char* __restrict__ kst, const char*
           int fc;
           if (tm.kspecial) {
             // frame = slot / ns as a multiply-high with ceil(2^32 / ns), exact below 2^32 / ns
+            // (magic 0: ns = 1)
             const uint32_t sl = (uint32_t)(tm.kt * 64 + key);
             ok = sl < (uint32_t)g.S;
-            fc = (int)__umulhi(sl, nsmagic);
+            fc = nsmagic ? (int)mulhi_u32(sl, nsmagic) : (int)sl;
           } else {
             ok = key < tm.kvalid;
             fc = tm.kframe;
@@ -909,10 +914,13 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
     // K half = 32 rows x 8 chunks, V half = 64 rows x 4 chunks of 128-byte rows.
     // Lane offsets of the 16-byte chunks: K chunk u of a lane = row 8u + lane/8, whose swizzle
     // differs between even and odd u only (2 offsets + multiples of 1024); V chunk u = row
-    // 16u + lane/4, whose swizzle does not depend on u (1 offset + multiples of 2048). The offsets
-    // pass through an empty asm so that the compiler cannot fold them into hoisted 64-bit per-lane
-    // addresses (two registers per load held through the loop): the loads keep the scalar-base
-    // form, uniform address plus 32-bit lane offset.
+    // 16u + lane/4, whose swizzle does not depend on u (1 offset + multiples of 2048). The
+    // instruction's immediate offset moves the global and the LDS address alike, so K chunks u and
+    // u + 2 share one base, one lane offset and one M0 (immediate 2048), and V chunks 2i and 2i + 1
+    // share a base and M0 with lane offsets vo and vo + 1024 (immediate 1024: global +2048, LDS
+    // +1024). The offsets pass through an empty asm so that the compiler cannot fold them into
+    // hoisted 64-bit per-lane addresses (two registers per load held through the loop): the loads
+    // keep the scalar-base form, uniform address plus 32-bit lane offset.
     uint32_t ko[2], vo;
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
@@ -923,30 +931,32 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
       const int i = lane >> 2;
       vo = (uint32_t)(i * 128 + (((lane & 3) ^ swz4(i)) << 4));
     }
+    const uint32_t vo1 = vo + 1024;
     const char* kbase = reinterpret_cast<const char*>(p.k + head_base * 64);
     const char* vbase = reinterpret_cast<const char*>(p.v + head_base * 64);
     char* slots = ring + w * 16384;
     auto issue_k = [&](int e, int hh) {
       const char* kb = kbase + (int64_t)(e >> 7) * 8192 + hh * 4096;
       char* st = slots + hh * 8192;
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        uint32_t o = ko[u & 1];
-        const char* b = kb + 1024 * (u & 2);
-        asm volatile("" : "+v"(o), "+s"(b));
-        __builtin_amdgcn_global_load_lds((const void*)(b + o), (lds_void*)(st + 64 * u * 16), 16, 0, 0);
-      }
+      asm volatile("" : "+s"(kb));
+      uint32_t o0 = ko[0], o1 = ko[1], o2 = ko[0], o3 = ko[1];
+      asm volatile("" : "+v"(o0), "+v"(o1), "+v"(o2), "+v"(o3));
+      __builtin_amdgcn_global_load_lds((const void*)(kb + o0), (lds_void*)st, 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)(kb + o1), (lds_void*)(st + 1024), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)(kb + o2), (lds_void*)st, 16, 2048, 0);
+      __builtin_amdgcn_global_load_lds((const void*)(kb + o3), (lds_void*)(st + 1024), 16, 2048, 0);
     };
     auto issue_v = [&](int e, int hh) {
       const char* vb = vbase + (int64_t)(e >> 7) * 8192 + hh * 64;
       char* st = slots + hh * 8192 + 4096;
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        uint32_t o = vo;
-        const char* b = vb + 2048 * u;
-        asm volatile("" : "+v"(o), "+s"(b));
-        __builtin_amdgcn_global_load_lds((const void*)(b + o), (lds_void*)(st + 64 * u * 16), 16, 0, 0);
-      }
+      const char* b0 = vb;
+      const char* b1 = vb + 4096;
+      uint32_t o0 = vo, o1 = vo1, o2 = vo, o3 = vo1;
+      asm volatile("" : "+v"(o0), "+v"(o1), "+v"(o2), "+v"(o3), "+s"(b0), "+s"(b1));
+      __builtin_amdgcn_global_load_lds((const void*)(b0 + o0), (lds_void*)st, 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)(b0 + o1), (lds_void*)st, 16, 1024, 0);
+      __builtin_amdgcn_global_load_lds((const void*)(b1 + o2), (lds_void*)(st + 2048), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)(b1 + o3), (lds_void*)(st + 2048), 16, 1024, 0);
     };
     // V^T fragments of a staged half (64-byte rows, swz4)
     auto load_vh = [&](const char* vst, bf16x8(&vf)[2][2]) {
@@ -1248,7 +1258,8 @@ extern "C" int saf3r_sparse_attn_fwd(const void* q_packed, const void* k_packed,
   p.c = scale * 1.4426950408889634f;
   if (p.g.ns > 0 && (uint64_t)p.g.Sp * (uint64_t)p.g.ns >= 0x100000000ull)
     return fail(SAF3R_ERR_UNSUPPORTED, "saf3r_sparse_attn_fwd: too many special tokens");
-  p.nsmagic = p.g.ns > 0 ? (uint32_t)((0x100000000ull + (uint64_t)p.g.ns - 1) / (uint64_t)p.g.ns) : 0u;
+  // ceil(2^32 / ns) fits 32 bits for ns >= 2 only: ns = 1 is magic 0, which the kernel tests for
+  p.nsmagic = p.g.ns > 1 ? (uint32_t)((0x100000000ull + (uint64_t)p.g.ns - 1) / (uint64_t)p.g.ns) : 0u;
   set_phase(&p);
   Seg segs[kMaxSegs];
   int nseg = 0;

@@ -20,6 +20,13 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
+// Work-item and work-group ids read as the hardware registers they are: threadIdx / blockIdx compile
+// to out-of-line library calls here (a call with register saves per use).
+__device__ __forceinline__ int tid_x() { return (int)__builtin_amdgcn_workitem_id_x(); }
+__device__ __forceinline__ int bid_x() { return (int)__builtin_amdgcn_workgroup_id_x(); }
+__device__ __forceinline__ int bid_y() { return (int)__builtin_amdgcn_workgroup_id_y(); }
+__device__ __forceinline__ int bid_z() { return (int)__builtin_amdgcn_workgroup_id_z(); }
+
 constexpr int kHeadDim = 64;
 constexpr int kBlock = 64;
 constexpr int kMaxHeads = 64;

@@ -106,10 +106,10 @@ __device__ inline int wave_prefix4(int cnt, int* total) {
 // largest order key) is found by bisection over the 16-bit key range with wave-wide counts.
 template <int RC>
 __global__ __launch_bounds__(256) void frame_select_kernel(FrameTopkParams p) {
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int row = blockIdx.y;
+  const int lane = tid_x() & 63, w = tid_x() >> 6;
+  const int row = bid_y();
   const int nfr = p.F - p.f0;
-  const int fs = blockIdx.x * 4 + w;  // selected-frame index
+  const int fs = bid_x() * 4 + w;  // selected-frame index
   if (fs >= nfr) return;              // whole wave: no barrier below
   const int f = p.f0 + fs;
   const int64_t s0 = (int64_t)f * p.P;        // first key of the frame in the row
@@ -209,10 +209,10 @@ __device__ inline void sort_bitonic_desc(uint32_t (&c)[K]) {
 
 template <int RC, int K>
 __global__ __launch_bounds__(256) void frame_select_small_kernel(FrameTopkParams p) {
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int row = blockIdx.y;
+  const int lane = tid_x() & 63, w = tid_x() >> 6;
+  const int row = bid_y();
   const int nfr = p.F - p.f0;
-  const int fs = blockIdx.x * 4 + w;
+  const int fs = bid_x() * 4 + w;
   if (fs >= nfr) return;
   const int f = p.f0 + fs;
   const int64_t s0 = (int64_t)f * p.P;
@@ -288,8 +288,8 @@ __global__ __launch_bounds__(256) void cap_select_kernel(CapParams p) {
   __shared__ uint32_t hist[256];
   __shared__ uint32_t scan[256];
   __shared__ uint32_t wsum[4];
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int row = blockIdx.x;
+  const int tid = tid_x(), lane = tid & 63, w = tid >> 6;
+  const int row = bid_x();
   const int64_t n = p.cidx ? p.n : p.dense_n;
   const int m = p.cap;
   hist[tid] = 0;
@@ -351,8 +351,8 @@ __global__ __launch_bounds__(256) void cap_select_kernel(CapParams p) {
 }
 
 __global__ __launch_bounds__(256) void first_samples_kernel(int32_t* idx, int64_t idx_stride, int n, int stride) {
-  int32_t* o = idx + (int64_t)blockIdx.x * idx_stride;
-  for (int i = threadIdx.x; i < n; i += 256) o[i] = i * stride;
+  int32_t* o = idx + (int64_t)bid_x() * idx_stride;
+  for (int i = tid_x(); i < n; i += 256) o[i] = i * stride;
 }
 
 }  // namespace saf3r

@@ -43,8 +43,8 @@ __device__ inline float wave_sum(float x) {
 // 2 waves per workgroup, one query row per wave.
 __global__ __launch_bounds__(128) void gather_attn_kernel(GatherParams p) {
   __shared__ float red[2][64][65];
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int64_t r = (int64_t)blockIdx.x * 2 + w;
+  const int lane = tid_x() & 63, w = tid_x() >> 6;
+  const int64_t r = (int64_t)bid_x() * 2 + w;
   const bool active = r < p.n;
   const int64_t rr = active ? r : 0;
 

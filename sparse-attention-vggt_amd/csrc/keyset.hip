@@ -49,7 +49,7 @@ struct ProbeParams {
 
 // grid (nchunks, n_sel), 64 threads: feature d of chunk c, summed in token order
 __global__ __launch_bounds__(64) void probe_partial_kernel(ProbeParams p) {
-  const int c = blockIdx.x, hs = blockIdx.y, d = threadIdx.x;
+  const int c = bid_x(), hs = bid_y(), d = tid_x();
   const int h = p.head_ids[hs];
   const int t0 = c * p.chunk, t1 = min(p.n, t0 + p.chunk);
   const __bf16* base = p.q + (int64_t)h * p.g.L * 64 + d;
@@ -60,7 +60,7 @@ __global__ __launch_bounds__(64) void probe_partial_kernel(ProbeParams p) {
 
 // grid (n_sel), 64 threads: chunk sums in chunk order, then one correctly rounded division
 __global__ __launch_bounds__(64) void probe_finish_kernel(ProbeParams p) {
-  const int hs = blockIdx.x, d = threadIdx.x;
+  const int hs = bid_x(), d = tid_x();
   float total = 0.f;
   for (int c = 0; c < p.nchunks; ++c) total = total + p.partial[((int64_t)hs * kProbeChunks + c) * 64 + d];
   p.qbar[hs * 64 + d] = __fdiv_rn(total, (float)p.n);
@@ -69,10 +69,10 @@ __global__ __launch_bounds__(64) void probe_finish_kernel(ProbeParams p) {
 // grid (ceil(N / 256), n_sel), 256 threads: one token per thread
 __global__ __launch_bounds__(256) void probe_scores_kernel(ProbeParams p) {
   __shared__ float qb[64];
-  const int hs = blockIdx.y, h = p.head_ids[hs];
-  if (threadIdx.x < 64) qb[threadIdx.x] = p.qbar[hs * 64 + threadIdx.x];
+  const int hs = bid_y(), h = p.head_ids[hs];
+  if (tid_x() < 64) qb[tid_x()] = p.qbar[hs * 64 + tid_x()];
   __syncthreads();
-  const int t = blockIdx.x * 256 + threadIdx.x;
+  const int t = bid_x() * 256 + tid_x();
   if (t >= p.n) return;
   const u32x4* row = reinterpret_cast<const u32x4*>(p.k + ((int64_t)h * p.g.L + token_slot(p.g, t)) * 64);
   float acc = 0.f;
@@ -104,7 +104,7 @@ struct BuildParams {
 // Exclusive prefix count of a per-thread flag over the work-group, and the total. wsum holds
 // one slot per wave; two barriers.
 __device__ inline int block_prefix(bool flag, int* wsum, int& total) {
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int lane = tid_x() & 63, w = tid_x() >> 6;
   const uint64_t m = __ballot(flag);
   const int pre = __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0));
   if (lane == 0) wsum[w] = __popcll(m);
@@ -126,7 +126,7 @@ __global__ __launch_bounds__(kBuildThreads) void keyset_build_kernel(BuildParams
   __shared__ int wsum[kBuildThreads / 64];
   __shared__ uint32_t sh_prefix;
   __shared__ int sh_remaining;
-  const int hh = blockIdx.x, tid = threadIdx.x;
+  const int hh = bid_x(), tid = tid_x();
   const int mode = p.mode[hh], param = p.param[hh], start = p.start[hh];
   const bool include = p.include[hh] != 0;
   const float* sc = p.scores + (int64_t)hh * p.scores_stride;
@@ -210,11 +210,11 @@ struct GatherKParams {
 // kernel). Tiles at or beyond the member count are skipped; rows beyond it are zero.
 __global__ __launch_bounds__(256) void keyset_gather_kernel(GatherKParams p) {
   __shared__ __align__(16) __bf16 vs[64 * 72];
-  const int tile = blockIdx.x, hs = blockIdx.y;
+  const int tile = bid_x(), hs = bid_y();
   const int cnt = p.count[hs];
   if (tile * 64 >= cnt) return;
   const int h = p.head_ids[hs];
-  const int t = threadIdx.x, row = t >> 2, c = t & 3;
+  const int t = tid_x(), row = t >> 2, c = t & 3;
   const int j = tile * 64 + row;
   const int64_t tok = j < cnt ? p.idx[hs * p.idx_stride + j] : -1;
   u32x4 a = {0, 0, 0, 0}, b = {0, 0, 0, 0};

@@ -39,8 +39,8 @@ struct PackParams {
 __global__ __launch_bounds__(256) void pack_qkv_kernel(PackParams p) {
   __shared__ __align__(16) __bf16 vs[64 * 72];  // V rows of the tile, 144-byte row pitch
   const Geom& g = p.g;
-  const int tile = blockIdx.x, h = blockIdx.y;
-  const int t = threadIdx.x, row = t >> 2, c = t & 3;
+  const int tile = bid_x(), h = bid_y();
+  const int t = tid_x(), row = t >> 2, c = t & 3;
   const int64_t slot = (int64_t)tile * 64 + row;
   const int64_t ntok = (int64_t)g.F * g.T;
   const int64_t tok = (h < 64 && ((p.tok_order >> h) & 1)) ? (slot < ntok ? slot : -1) : slot_token(g, slot);

@@ -50,10 +50,10 @@ __device__ inline void add_row8(float (&acc)[8], const u32x4& x) {
 
 __global__ __launch_bounds__(256) void block_pool_kernel(PoolParams p) {
   const Geom& g = p.g;
-  const int lane = threadIdx.x & 63, sub = lane & 7;
-  const int bi = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 8 + (lane >> 3);
+  const int lane = tid_x() & 63, sub = lane & 7;
+  const int bi = (bid_x() * 4 + (tid_x() >> 6)) * 8 + (lane >> 3);
   if (bi >= p.nb) return;
-  const int hs = blockIdx.y;
+  const int hs = bid_y();
   const int h = p.heads[hs];
   const int f = bi / g.NBf, b = bi % g.NBf;
   const int cnt = min(64, g.P - 64 * b);
@@ -133,19 +133,19 @@ template <int K>
 __global__ __launch_bounds__(256) void topk_scores_row_kernel(const float* __restrict__ s, int64_t nrows, int F,
                                                               int C, int ke, int rpw, int32_t* __restrict__ idx) {
   extern __shared__ __align__(16) float buf[];  // rpw * F * C floats (dynamic: sized per launch)
-  const int64_t r0 = (int64_t)blockIdx.x * rpw;
+  const int64_t r0 = (int64_t)bid_x() * rpw;
   const int nr = (int)min((int64_t)rpw, nrows - r0);
   const int n = F * C;
   const int tot = nr * n;
   const float* src = s + r0 * n;
   if ((tot & 3) == 0 && ((r0 * n) & 3) == 0) {
-    for (int i = threadIdx.x; i < (tot >> 2); i += 256)
+    for (int i = tid_x(); i < (tot >> 2); i += 256)
       reinterpret_cast<f32x4*>(buf)[i] = reinterpret_cast<const f32x4*>(src)[i];
   } else {
-    for (int i = threadIdx.x; i < tot; i += 256) buf[i] = src[i];
+    for (int i = tid_x(); i < tot; i += 256) buf[i] = src[i];
   }
   __syncthreads();
-  for (int t = threadIdx.x; t < nr * F; t += 256) {
+  for (int t = tid_x(); t < nr * F; t += 256) {
     const int rr = t / F, f = t % F;
     select_frame<K>(buf + rr * n + f * C, C, f, ke, idx + (r0 + rr) * ((int64_t)F * ke) + (int64_t)f * ke);
   }
@@ -154,7 +154,7 @@ __global__ __launch_bounds__(256) void topk_scores_row_kernel(const float* __res
 template <int K>
 __global__ __launch_bounds__(256) void topk_scores_kernel(const float* __restrict__ s, int64_t nrows, int F, int C,
                                                           int ke, int32_t* __restrict__ idx) {
-  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t gid = (int64_t)bid_x() * 256 + tid_x();
   if (gid >= nrows * F) return;
   const int64_t row = gid / F;
   const int f = (int)(gid % F);
@@ -174,9 +174,9 @@ __global__ __launch_bounds__(256) void block_select_frame_kernel(const float* __
                                                                  const float* __restrict__ pk, int nbq, int F,
                                                                  int NBf, int ke, int32_t* __restrict__ idx) {
   __shared__ __align__(16) float kt[2][32 * 64];
-  const int hs = blockIdx.y;
-  const int i = blockIdx.x * 256 + threadIdx.x;
-  const int f0 = blockIdx.z * kSelFramesPerGroup;
+  const int hs = bid_y();
+  const int i = bid_x() * 256 + tid_x();
+  const int f0 = bid_z() * kSelFramesPerGroup;
   const int f1 = min(F, f0 + kSelFramesPerGroup);
   const bool active = i < nbq;
   float qv[64];
@@ -196,7 +196,7 @@ __global__ __launch_bounds__(256) void block_select_frame_kernel(const float* __
   const int nvec = NBf * 16;  // f32x4 per frame
   auto stage = [&](int f, int b) {
     const f32x4* src = reinterpret_cast<const f32x4*>(kbase + (int64_t)f * NBf * 64);
-    for (int v = threadIdx.x; v < nvec; v += 256) reinterpret_cast<f32x4*>(kt[b])[v] = src[v];
+    for (int v = tid_x(); v < nvec; v += 256) reinterpret_cast<f32x4*>(kt[b])[v] = src[v];
   };
   stage(f0, 0);
   __syncthreads();
@@ -238,14 +238,14 @@ __global__ __launch_bounds__(256) void block_select_global_kernel(const float* _
                                                                   int ke, int32_t* __restrict__ idx) {
   __shared__ float qv[64];
   __shared__ uint64_t lists[256 * K];
-  const int i = blockIdx.x, hs = blockIdx.y;
-  if (threadIdx.x < 64) qv[threadIdx.x] = pq[((int64_t)hs * nbq + i) * 64 + threadIdx.x];
+  const int i = bid_x(), hs = bid_y();
+  if (tid_x() < 64) qv[tid_x()] = pq[((int64_t)hs * nbq + i) * 64 + tid_x()];
   __syncthreads();
   const float* kbase = pk + (int64_t)hs * nbk * 64;
   uint64_t a[K];
 #pragma unroll
   for (int t = 0; t < K; ++t) a[t] = 0;
-  for (int c = threadIdx.x; c < nbk; c += 256) {
+  for (int c = tid_x(); c < nbk; c += 256) {
     const f32x4* kr = reinterpret_cast<const f32x4*>(kbase + (int64_t)c * 64);
     float acc = 0.f;
 #pragma unroll
@@ -260,22 +260,22 @@ __global__ __launch_bounds__(256) void block_select_global_kernel(const float* _
     if (x > a[K - 1]) topk_insert<K>(a, x);
   }
 #pragma unroll
-  for (int t = 0; t < K; ++t) lists[threadIdx.x * K + t] = a[t];
+  for (int t = 0; t < K; ++t) lists[tid_x() * K + t] = a[t];
   __syncthreads();
   // tree merge: at each step thread t < s merges list t + s into list t
   for (int s = 128; s > 0; s >>= 1) {
-    if (threadIdx.x < s) {
+    if (tid_x() < s) {
 #pragma unroll
       for (int t = 0; t < K; ++t) {
-        uint64_t x = lists[(threadIdx.x + s) * K + t];
+        uint64_t x = lists[(tid_x() + s) * K + t];
         if (x > a[K - 1]) topk_insert<K>(a, x);
       }
 #pragma unroll
-      for (int t = 0; t < K; ++t) lists[threadIdx.x * K + t] = a[t];
+      for (int t = 0; t < K; ++t) lists[tid_x() * K + t] = a[t];
     }
     __syncthreads();
   }
-  if (threadIdx.x == 0) {
+  if (tid_x() == 0) {
     int32_t* o = idx + ((int64_t)hs * nbq + i) * ke;
 #pragma unroll
     for (int t = 0; t < K; ++t)

@@ -43,7 +43,7 @@ __device__ inline uint64_t partner_u64(uint64_t x) {
   uint32_t lo = (uint32_t)x, hi = (uint32_t)(x >> 32);
   auto rl = __builtin_amdgcn_permlane32_swap(lo, lo, false, false);
   auto rh = __builtin_amdgcn_permlane32_swap(hi, hi, false, false);
-  const bool upper = (threadIdx.x & 63) >= 32;
+  const bool upper = (tid_x() & 63) >= 32;
   uint32_t plo = upper ? (uint32_t)rl[0] : (uint32_t)rl[1];
   uint32_t phi = upper ? (uint32_t)rh[0] : (uint32_t)rh[1];
   return ((uint64_t)phi << 32) | plo;
@@ -52,8 +52,8 @@ __device__ inline uint64_t partner_u64(uint64_t x) {
 template <int K>
 __global__ __launch_bounds__(256) void token_topk_kernel(TopkParams p) {
   __shared__ __align__(16) char kbuf[2][8192];
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, half = lane >> 5, col = lane & 31;
-  const int64_t q0 = (int64_t)blockIdx.x * 128;
+  const int tid = tid_x(), lane = tid & 63, w = tid >> 6, half = lane >> 5, col = lane & 31;
+  const int64_t q0 = (int64_t)bid_x() * 128;
   const int64_t qi = q0 + 32 * w + col;
   const bool qvalid = qi < p.nq;
 

@@ -26,7 +26,7 @@ def ops(pkg):
 
 
 DEV = "cuda:0"
-GEOMS = [(3, 155, 5), (4, 1374, 5), (2, 64, 0), (1, 70, 5), (14, 60, 5)]
+GEOMS = [(3, 155, 5), (4, 1374, 5), (2, 64, 0), (1, 70, 5), (14, 60, 5), (3, 65, 1)]
 
 
 def _qkv(H, N, seed, scale=1.0):
