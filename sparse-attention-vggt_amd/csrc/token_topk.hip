@@ -19,6 +19,7 @@ struct TopkParams {
   const __bf16* kptr;
   int64_t k_rs, k_base, k_rpf, k_frs;
   int nq, F, P, ke;
+  int kmode;  // key row of (frame f, token j): 1 = frame f row j (rows_per_frame == P), 0 = flat row f*P + j, 2 = general
   int32_t* idx;
 };
 
@@ -68,15 +69,17 @@ __global__ __launch_bounds__(256) void token_topk_kernel(TopkParams p) {
   const int tiles_pf = (p.P + 63) / 64;
   const int total = p.F * tiles_pf;
   u32x4 kreg[2];
-  auto load_tile = [&](int t) {
-    const int f = t / tiles_pf, u = t % tiles_pf;
+  auto load_tile = [&](int f, int u) {
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
       const int id = tid + 256 * e, r = id >> 3, ch = id & 7;
       const int pp = 64 * u + r;
       if (pp < p.P) {
-        const u32x4* src = reinterpret_cast<const u32x4*>(
-            rows_at(p.kptr, p.k_rs, p.k_base, p.k_rpf, p.k_frs, (int64_t)f * p.P + pp));
+        // the frame / row split of the key row without a 64-bit division where the layout allows
+        const __bf16* row = p.kmode == 1   ? p.kptr + (p.k_base + (int64_t)f * p.k_frs + pp) * p.k_rs
+                            : p.kmode == 0 ? p.kptr + (p.k_base + (int64_t)f * p.P + pp) * p.k_rs
+                                           : rows_at(p.kptr, p.k_rs, p.k_base, p.k_rpf, p.k_frs, (int64_t)f * p.P + pp);
+        const u32x4* src = reinterpret_cast<const u32x4*>(row);
         kreg[e] = src[ch];
       } else {
         kreg[e] = u32x4{0, 0, 0, 0};
@@ -95,13 +98,14 @@ __global__ __launch_bounds__(256) void token_topk_kernel(TopkParams p) {
 #pragma unroll
   for (int t = 0; t < K; ++t) a[t] = 0;
 
-  load_tile(0);
+  load_tile(0, 0);
   store_tile(0);
   __syncthreads();
+  int f = 0, u = 0;  // frame and tile of step t
   for (int t = 0; t < total; ++t) {
     const int cur = t & 1;
-    if (t + 1 < total) load_tile(t + 1);
-    const int f = t / tiles_pf, u = t % tiles_pf;
+    const int un = u + 1 == tiles_pf ? 0 : u + 1, fn = u + 1 == tiles_pf ? f + 1 : f;
+    if (t + 1 < total) load_tile(fn, un);
     f32x16 s0 = {}, s1 = {};
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
@@ -143,6 +147,8 @@ __global__ __launch_bounds__(256) void token_topk_kernel(TopkParams p) {
     }
     if (t + 1 < total) store_tile(cur ^ 1);
     __syncthreads();
+    f = fn;
+    u = un;
   }
 }
 
@@ -177,6 +183,7 @@ extern "C" int saf3r_token_topk(const saf3r_rows* q, const saf3r_rows* k, int n_
   p.k_base = k->base_row;
   p.k_rpf = k->rows_per_frame;
   p.k_frs = k->frame_row_stride;
+  p.kmode = k->rows_per_frame == per_frame ? 1 : k->rows_per_frame >= (int64_t)frames * per_frame ? 0 : 2;
   p.nq = n_q;
   p.F = frames;
   p.P = per_frame;

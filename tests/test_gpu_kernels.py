@@ -292,6 +292,25 @@ def test_gather_attention_shared_list(ops):
     _check_close(got.cpu(), ref, "gather shared list")
 
 
+@pytest.mark.parametrize("layout", ["framed", "paired"])
+def test_token_topk_key_row_layouts(ops, layout):
+    """Key rows described frame by frame (rows_per_frame == per_frame: the plugin's packed layout)
+    and with two key frames per stored frame (the general row map) select what the flat rows do."""
+    frames, P, topk, pad = 4, 100, 4, 3
+    g = torch.Generator().manual_seed(11)
+    q = torch.randn(200, 64, generator=g).to(torch.bfloat16).to(DEV)
+    k = torch.randn(frames * P, 64, generator=g).to(torch.bfloat16)
+    want = ops.token_topk(q, k.to(DEV), frames, P, topk).cpu()
+    rpf = P if layout == "framed" else 2 * P
+    store = torch.randn(frames * P // rpf, pad + rpf, 64, generator=g).to(torch.bfloat16)
+    store[:, pad:] = k.view(-1, rpf, 64)  # junk rows ahead of every stored frame
+    store = store.to(DEV)
+    kr = ops.rows(store.view(-1, 64), base_row=pad, rows_per_frame=rpf, frame_row_stride=pad + rpf)
+    got = ops.token_topk(q, None, frames, P, topk, krows=kr).cpu()
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+
+
 @pytest.mark.parametrize("frames,P,topk", [(4, 1369, 4), (3, 100, 8), (2, 30, 16), (5, 64, 1)])
 def test_token_topk(ops, frames, P, topk):
     g = torch.Generator().manual_seed(frames * P)
