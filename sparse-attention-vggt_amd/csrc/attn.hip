@@ -640,7 +640,8 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
     auto shared_walk = [&](auto ks_tag) {
     // ---- key-tile sequence (uniform) ----
     Walk wk;
-    bool frame_rel = false;
+    bool frame_rel = false, rel_patch = false;
+    int seg_s = 0, seg_l = 0;  // own-frame patch tiles of a frame-relative patch-row item
     constexpr bool keyset = decltype(ks_tag)::value;
     const int eff = (pat == SAF3R_DENSE || pat == SAF3R_TOKEN_DYNAMIC || pat == SAF3R_BLOCK_DYNAMIC || keyset)
                         ? SAF3R_DENSE
@@ -674,10 +675,19 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
       const int ls1 = has_sp ? ((f1 + 1) * g.ns - 1) / 64 : -1;
       const bool anc_sp = has_sp && need_anchor && !(need_local && ls0 == 0);
       const bool anc_pt = need_anchor && !(need_local && f0 == 0);
+      // ranges: frame 0's special tiles, the item's frames' special tiles, frame 0's patch tiles,
+      // the item's frames' patch tiles. A patch-row item (one frame) walks its own frame's patch
+      // tiles (only the last one partial) in the pipelined single-range walk and the other ranges
+      // here, with per-key frame masks.
+      rel_patch = qt0 >= g.nst && need_local;
       wk.init(0, anc_sp ? (g.ns - 1) / 64 + 1 : 0,
               ls0, (has_sp && need_local) ? ls1 - ls0 + 1 : 0,
               g.nst, anc_pt ? g.NBf : 0,
-              g.nst + f0 * g.NBf, need_local ? (f1 - f0 + 1) * g.NBf : 0);
+              g.nst + f0 * g.NBf, need_local && !rel_patch ? (f1 - f0 + 1) * g.NBf : 0);
+      if (rel_patch) {
+        seg_s = __builtin_amdgcn_readfirstlane(g.nst + f0 * g.NBf);
+        seg_l = __builtin_amdgcn_readfirstlane(g.NBf);
+      }
     }
     const int count = wk.count;
     int rot = 0;
@@ -728,25 +738,30 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
       wi.next(g);
     };
 
-    if (keyset || eff == SAF3R_DENSE) {
+    if (keyset || eff == SAF3R_DENSE || rel_patch) {
       // ---- single-range walk: tiles rot, rot + 1, ... (mod count), only partial tiles masked ----
+      // (dense and key-set walks: tiles 0 .. count-1 entered at rot; patch-row items of
+      // frame-relative heads: their own frame's patch tiles, then the frame-relative walk below)
       // Control is kept to a few scalar selects per tile: the loop runs four tiles per trip so
       // that every stage offset is a constant, waves without a query tile of their own compute
       // on a duplicate (their rows are not stored), and the tile position and its valid-key
       // count advance without branches.
       const int nst = g.nst, NBf = g.NBf;
       const int lastv = g.P - 64 * (NBf - 1);  // valid keys in the last patch tile of a frame
-      int kt = rot, bk = -1;                   // consumed tile and its block within its frame
+      const int sbeg = rel_patch ? seg_s : 0;
+      const int cnt = rel_patch ? seg_l : count;
+      const int send = sbeg + cnt;
+      int kt = rel_patch ? sbeg : rot, bk = -1;  // consumed tile and its block within its frame
       if constexpr (!keyset) bk = kt >= nst ? (kt - nst) % NBf : -1;
       auto kvalid_of = [&]() -> int {
         if constexpr (keyset) return min(64, ks_keys - 64 * kt);
         else return kt < nst ? min(64, g.S - 64 * kt) : (bk == NBf - 1 ? lastv : 64);
       };
       auto advance = [&]() {
-        kt = kt + 1 == count ? 0 : kt + 1;
+        kt = kt + 1 == send ? sbeg : kt + 1;
         if constexpr (!keyset) bk = kt < nst ? -1 : (kt == nst || bk + 1 == NBf ? 0 : bk + 1);
       };
-      int kti = rot;  // next tile to load
+      int kti = kt;  // next tile to load
       auto issue_at = [&](int stage) {
         const char* kb = kbase + (int64_t)kti * 8192;
         const char* vb = vbase + (int64_t)kti * 8192;
@@ -760,17 +775,17 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
           __builtin_amdgcn_global_load_lds((const void*)(bk + o), (lds_void*)(st + 4096 * u), 16, 0, 0);
           __builtin_amdgcn_global_load_lds((const void*)(bv + o), (lds_void*)(st + 8192 + 4096 * u), 16, 0, 0);
         }
-        kti = kti + 1 == count ? 0 : kti + 1;
+        kti = kti + 1 == send ? sbeg : kti + 1;
       };
-      if (count == 0) {
+      if (cnt == 0) {
         store(A);
         return;
       }
       wait_vm<0>();  // Q fragments landed; from here vmcnt counts ring loads only
       for (int u = 0; u < 3; ++u)
-        if (u < count) issue_at(u);
-      if (count >= 3) wait_vm<8>();
-      else if (count == 2) wait_vm<4>();
+        if (u < cnt) issue_at(u);
+      if (cnt >= 3) wait_vm<8>();
+      else if (cnt == 2) wait_vm<4>();
       else wait_vm<0>();
       barrier_only();
       f32x16 s_cur[2], s_nxt[2];
@@ -792,11 +807,11 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
           pc[j][x] = bf16x8{};
           vf[j][x] = bf16x8{};
         }
-      for (int t0 = 0; t0 < count; t0 += 4) {
+      for (int t0 = 0; t0 < cnt; t0 += 4) {
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
           const int t = t0 + v;
-          if (t >= count) break;
+          if (t >= cnt) break;
           // half step 2t: PV of tile t-1 keys 32..63, scores of tile t keys 32..63
           if (v > 0 || t0 > 0) load_v(ring + ((v + 3) & 3) * 16384 + 8192, 1, vf, half, col);
           load_k(ring + v * 16384, 1, kf, half, col);
@@ -807,10 +822,10 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
           A.l[1] += ts[1];
           advance();
           const int kv_nxt = kvalid_of();  // tile t + 1 (past the end: never read)
-          if (t + 2 < count) wait_vm<4>();
+          if (t + 2 < cnt) wait_vm<4>();
           else wait_vm<0>();
           barrier_only();
-          if (t + 3 < count) issue_at((v + 3) & 3);
+          if (t + 3 < cnt) issue_at((v + 3) & 3);
           // half step 2t+1: PV of tile t keys 0..31, scores of tile t + 1 keys 0..31
           load_v(ring + v * 16384 + 8192, 0, vf, half, col);
           load_k(ring + ((v + 1) & 3) * 16384, 0, kf, half, col);
@@ -822,7 +837,7 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
           kv_cur = kv_nxt;
         }
       }
-      load_v(ring + ((count - 1) & 3) * 16384 + 8192, 1, vf, half, col);
+      load_v(ring + ((cnt - 1) & 3) * 16384 + 8192, 1, vf, half, col);
 #pragma unroll
       for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -830,8 +845,11 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
           A.o[dh][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[j][dh], pc[0][j], A.o[dh][0], 0, 0, 0);
           A.o[dh][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[j][dh], pc[1][j], A.o[dh][1], 0, 0, 0);
         }
-      store(A);
-      return;
+      if (!rel_patch) {
+        store(A);
+        return;
+      }
+      __syncthreads();  // every wave is done with the ring before the frame-relative walk reuses it
     }
 
     // ---- frame-relative walks (up to four ranges, frame masks): one tile per attend step ----
