@@ -124,7 +124,7 @@ def cpu_baseline(pkg, frames=4, heads=16, repeats=5, budget_s=25.0):
     }
 
 
-def scores_path(ops, geom, n_dyn, reps=5):
+def scores_path(ops, geom, n_dyn, reps=20):
     """The scores-input selection path: per-frame top-4 of a synthetic fp32 block-score matrix
     [n_dyn * NB, NB] (N(0,1) scores), the same shape the fused selection scores internally."""
     nb = geom.num_blocks
@@ -132,6 +132,9 @@ def scores_path(ops, geom, n_dyn, reps=5):
     idx = ops.topk_from_scores(s, geom.frames, 4)
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    # a launch takes ~60 us on the GPU and about as long on the host (Python, ctypes, the output
+    # allocation): queue the timed launches behind a GPU spin so that they run back to back
+    torch.cuda._sleep(50_000_000)
     e0.record()
     for _ in range(reps):
         idx = ops.topk_from_scores(s, geom.frames, 4)

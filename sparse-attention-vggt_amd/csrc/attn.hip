@@ -83,8 +83,6 @@ struct AttnParams {
   int8_t slot[kMaxHeads];
 };
 
-typedef __attribute__((address_space(3))) void lds_void;
-
 __device__ inline float partner_max(float x) {
   uint32_t u = __builtin_bit_cast(uint32_t, x);
   auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
@@ -96,13 +94,6 @@ __device__ inline float partner_sum(float x) {
   return __builtin_bit_cast(float, (uint32_t)r[0]) + __builtin_bit_cast(float, (uint32_t)r[1]);
 }
 
-// s_waitcnt on vmcnt only (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14]),
-// followed by a compiler barrier so no LDS read is hoisted above it.
-template <int N>
-__device__ inline void wait_vm() {
-  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
-  asm volatile("" ::: "memory");
-}
 __device__ inline void barrier_only() {
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");

@@ -27,6 +27,17 @@ __device__ __forceinline__ int bid_x() { return (int)__builtin_amdgcn_workgroup_
 __device__ __forceinline__ int bid_y() { return (int)__builtin_amdgcn_workgroup_id_y(); }
 __device__ __forceinline__ int bid_z() { return (int)__builtin_amdgcn_workgroup_id_z(); }
 
+// LDS pointer type of the LDS-DMA loads (__builtin_amdgcn_global_load_lds)
+typedef __attribute__((address_space(3))) void lds_void;
+
+// s_waitcnt on vmcnt only (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14]),
+// followed by a compiler barrier so no LDS read is hoisted above it.
+template <int N>
+__device__ inline void wait_vm() {
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+  asm volatile("" ::: "memory");
+}
+
 constexpr int kHeadDim = 64;
 constexpr int kBlock = 64;
 constexpr int kMaxHeads = 64;

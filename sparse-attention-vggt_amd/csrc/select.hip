@@ -97,7 +97,7 @@ __global__ __launch_bounds__(256) void block_pool_kernel(PoolParams p) {
 
 // ---------------------------------------------------------------------------------------
 // Top-k from a score matrix. Rows of up to kRowLds floats are staged in LDS with coalesced
-// 16-byte loads (as many rows per workgroup as keep its threads busy) and each thread then selects
+// 16-byte LDS-DMA loads (as many rows per workgroup as keep its threads busy) and each thread then selects
 // one (row, frame); longer rows are read directly, one thread per (row, frame).
 // ---------------------------------------------------------------------------------------
 constexpr int kRowLds = 12288;
@@ -138,9 +138,17 @@ __global__ __launch_bounds__(256) void topk_scores_row_kernel(const float* __res
   const int n = F * C;
   const int tot = nr * n;
   const float* src = s + r0 * n;
-  if ((tot & 3) == 0 && ((r0 * n) & 3) == 0) {
-    for (int i = tid_x(); i < (tot >> 2); i += 256)
-      reinterpret_cast<f32x4*>(buf)[i] = reinterpret_cast<const f32x4*>(src)[i];
+  if ((tot & 3) == 0 && ((uintptr_t)src & 15) == 0) {
+    // LDS-DMA copy: every 16-byte chunk goes straight to LDS and a thread's loads are all in flight
+    // at once (wave w of pass i0 fills chunks i0 + 64w .. i0 + 64w + 63, lane by lane)
+    const int n4 = tot >> 2, w = tid_x() >> 6;
+    for (int i0 = 0; i0 < n4; i0 += 256) {
+      const int i = i0 + tid_x();
+      if (i < n4)
+        __builtin_amdgcn_global_load_lds((const void*)(src + 4 * (int64_t)i), (lds_void*)(buf + 4 * (i0 + 64 * w)), 16, 0,
+                                         0);
+    }
+    wait_vm<0>();
   } else {
     for (int i = tid_x(); i < tot; i += 256) buf[i] = src[i];
   }
