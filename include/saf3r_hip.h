@@ -42,7 +42,7 @@ extern "C" {
 enum saf3r_status {
   SAF3R_OK = 0,
   SAF3R_ERR_INVALID = 1,      /* bad argument, shape or pointer */
-  SAF3R_ERR_UNSUPPORTED = 2,  /* valid request this build does not implement (e.g. head_dim != 64) */
+  SAF3R_ERR_UNSUPPORTED = 2,  /* valid request this library does not implement (e.g. head_dim != 64) */
   SAF3R_ERR_LAUNCH = 3,       /* the HIP runtime rejected a launch */
   SAF3R_ERR_INJECTED = 4      /* failure forced through SAF3R_FAULT_INJECT (tests of error paths) */
 };

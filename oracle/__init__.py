@@ -3,7 +3,7 @@
 TEST INFRASTRUCTURE ONLY. This package restates the reference algorithm on the CPU so
 that the HIP kernels can be checked against it. Only ``tests/``,
 ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may import it,
-and only as the checker (or, for ``cpu_baseline``, as the timed CPU restatement). The
+and only to check results (or, for ``cpu_baseline``, as the timed CPU restatement). The
 product package never imports it and has no CPU fallback.
 
 Modules

@@ -1,4 +1,4 @@
-"""torch restatement of SAF3R head-wise sparse global attention (one GPU-free checker).
+"""torch restatement of SAF3R head-wise sparse global attention (a GPU-free reference for the tests).
 
 TEST INFRASTRUCTURE ONLY (see ``oracle/__init__.py``).
 

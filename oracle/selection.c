@@ -3,7 +3,7 @@
  *
  * TEST INFRASTRUCTURE ONLY. This file is the oracle that the HIP kernels are
  * checked against. Only tests/, __graft_entry__.smoke() and the cpu_baseline leg
- * of bench.py may load it, and only as the checker. The product path never calls
+ * of bench.py may load it, and only to check results. The product path never calls
  * it and has no CPU fallback.
  *
  * Everything here is integer-exact or uses a fully specified fp32 operation order

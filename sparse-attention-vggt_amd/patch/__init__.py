@@ -1,5 +1,5 @@
 """Plugin surface of the reference (``saf3r/patch/__init__.py:12-33``): model-name dispatch of
-``patch_model`` and ``update_args_per_forward``. VGGT is the model family of this build; other
+``patch_model`` and ``update_args_per_forward``. VGGT is the model family of this package; other
 names raise ``ValueError`` like the reference does for unknown models."""
 from . import patch_vggt
 from .patch_vggt import HeadwiseSparseAttentionWrapper, set_dino_topk_from_features  # noqa: F401

@@ -20,7 +20,7 @@ Block patterns (same JSON format, new mode names)
                          best mean-query scores, plus frame 0 and the specials with include_as
                          (default False))
   broadcast_first        BROADCAST (frame 0's attention map applied to every frame's V, :110-131)
-Reference option without a kernel in this build: q_probe_topk with q_sample_ratio != 1
+Reference option without a kernel in this package: q_probe_topk with q_sample_ratio != 1
 -> NotImplementedError.
 """
 from __future__ import annotations
@@ -52,7 +52,7 @@ def pattern_of(cfg: dict) -> int:
     if mode in MODE_TO_PATTERN:
         return MODE_TO_PATTERN[mode]
     if mode in UNBUILT_MODES:
-        raise NotImplementedError(f"mode {mode!r} has no kernel in this build")
+        raise NotImplementedError(f"mode {mode!r} has no kernel in this package")
     raise ValueError(f"Unsupported mode: {mode}")
 
 
@@ -65,7 +65,7 @@ def keyset_spec(cfg: dict, head: int, num_tokens: int) -> KeySetSpec:
         return KeySetSpec(head, KEYSET_STRIDE, stride, start, bool(cfg.get("include_as", True)))
     if mode == "q_probe_topk":
         if cfg.get("q_sample_ratio", 1) != 1:
-            raise NotImplementedError("q_probe_topk with q_sample_ratio != 1 has no kernel in this build")
+            raise NotImplementedError("q_probe_topk with q_sample_ratio != 1 has no kernel in this package")
         if "stride" in cfg:
             k = max(1, num_tokens // int(cfg["stride"]))
         else:
