@@ -1160,11 +1160,13 @@ static int head_segments(int h, int pat, bool tokord, int ntt, const Geom& g, in
 }
 
 // Clock phases of the key walks. Defaults come from sweeps at the 128-frame VGGT shape (dense
-// walks hardly depend on it; the split value sits in the middle of a plateau, 2100-2250 ns, of
-// best block-dynamic throughput and L2 reuse); SAF3R_ATTN_PHASE="off" keeps the fixed walk order
+// walks hardly depend on it). The split value sits at the long end of the plateau of best
+// block-dynamic throughput and L2 reuse (2100-2250 ns on a fast device, 2200-2300 ns on a slower
+// one): a phase shorter than the walk's real step time scatters the work-groups over the key frames
+// (-8% at 2100 ns on the slower device), a longer one costs little; SAF3R_ATTN_PHASE="off" keeps the fixed walk order
 // (run-to-run identical output), and SAF3R_ATTN_PHASE="<dense ns>,<split ns>" overrides them.
 static void set_phase(AttnParams* p) {
-  double dense_ns = 2600.0, split_ns = 2200.0;
+  double dense_ns = 2600.0, split_ns = 2250.0;
   if (const char* e = getenv("SAF3R_ATTN_PHASE")) {
     if (strcmp(e, "off") == 0) dense_ns = split_ns = 0.0;
     else if (sscanf(e, "%lf,%lf", &dense_ns, &split_ns) != 2) dense_ns = split_ns = 0.0;
