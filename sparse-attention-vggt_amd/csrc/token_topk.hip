@@ -94,9 +94,12 @@ __global__ __launch_bounds__(256) void token_topk_kernel(TopkParams p) {
     }
   };
 
-  uint64_t a[K];
+  // running top-k of the lane's even and of its odd candidates of the frame: two independent
+  // branch-free insertion chains whose instructions interleave (one chain alone waits on the
+  // compare-to-select hazards); keys are distinct, so merging the two lists loses nothing
+  uint64_t a[K], b2[K];
 #pragma unroll
-  for (int t = 0; t < K; ++t) a[t] = 0;
+  for (int t = 0; t < K; ++t) a[t] = b2[t] = 0;
 
   load_tile(0, 0);
   store_tile(0);
@@ -116,20 +119,28 @@ __global__ __launch_bounds__(256) void token_topk_kernel(TopkParams p) {
       s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qfrag[s], s0, 0, 0, 0);
       s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kb, qfrag[s], s1, 0, 0, 0);
     }
-    // candidates in increasing key order (strict-'>' insertion keeps lower indices first on ties)
+    // candidates of this lane (key 0 stands for a padding position: it never enters a list)
 #pragma unroll
-    for (int e = 0; e < 32; ++e) {
-      const float sv = e < 16 ? s0[e] : s1[e - 16];
-      const int r = e & 15;
-      const int key = 32 * (e >> 4) + 8 * (r >> 2) + 4 * half + (r & 3);
-      const int pp = 64 * u + key;
-      if (pp < p.P) {
-        const uint64_t x = ckey(sv, (uint32_t)pp);
-        if (x > a[K - 1]) insert_desc<K>(a, x);
+    for (int e = 0; e < 32; e += 2) {
+      uint64_t x[2];
+#pragma unroll
+      for (int o = 0; o < 2; ++o) {
+        const float sv = e + o < 16 ? s0[e + o] : s1[e + o - 16];
+        const int r = (e + o) & 15;
+        const int key = 32 * ((e + o) >> 4) + 8 * (r >> 2) + 4 * half + (r & 3);
+        const int pp = 64 * u + key;
+        x[o] = pp < p.P ? ckey(sv, (uint32_t)pp) : 0ull;
       }
+      insert_desc<K>(a, x[0]);
+      insert_desc<K>(b2, x[1]);
     }
     if (u == tiles_pf - 1) {
-      // merge the partner half's list, then flush this frame
+      // merge the odd list and the partner half's list, then flush this frame
+#pragma unroll
+      for (int e = 0; e < K; ++e) {
+        insert_desc<K>(a, b2[e]);
+        b2[e] = 0;
+      }
       uint64_t b[K];
 #pragma unroll
       for (int e = 0; e < K; ++e) b[e] = partner_u64(a[e]);
