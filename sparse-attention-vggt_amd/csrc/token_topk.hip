@@ -9,6 +9,8 @@
 // scored with v_mfma_f32_32x32x16_bf16 (S^T = K . Q^T), and every lane keeps a running top-k of
 // the 32 keys of the tile it holds; the two lane halves of a query merge their lists when the
 // frame ends.
+#include <type_traits>
+
 #include "common.h"
 
 namespace saf3r {
@@ -119,21 +121,27 @@ __global__ __launch_bounds__(256) void token_topk_kernel(TopkParams p) {
       s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qfrag[s], s0, 0, 0, 0);
       s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kb, qfrag[s], s1, 0, 0, 0);
     }
-    // candidates of this lane (key 0 stands for a padding position: it never enters a list)
+    // candidates of this lane (key 0 stands for a padding position: it never enters a list); only
+    // a frame's last tile can hold padding, so the other tiles skip the test
+    auto scan = [&](auto padded) {
 #pragma unroll
-    for (int e = 0; e < 32; e += 2) {
-      uint64_t x[2];
+      for (int e = 0; e < 32; e += 2) {
+        uint64_t x[2];
 #pragma unroll
-      for (int o = 0; o < 2; ++o) {
-        const float sv = e + o < 16 ? s0[e + o] : s1[e + o - 16];
-        const int r = (e + o) & 15;
-        const int key = 32 * ((e + o) >> 4) + 8 * (r >> 2) + 4 * half + (r & 3);
-        const int pp = 64 * u + key;
-        x[o] = pp < p.P ? ckey(sv, (uint32_t)pp) : 0ull;
+        for (int o = 0; o < 2; ++o) {
+          const float sv = e + o < 16 ? s0[e + o] : s1[e + o - 16];
+          const int r = (e + o) & 15;
+          const int key = 32 * ((e + o) >> 4) + 8 * (r >> 2) + 4 * half + (r & 3);
+          const int pp = 64 * u + key;
+          x[o] = ckey(sv, (uint32_t)pp);
+          if constexpr (decltype(padded)::value) x[o] = pp < p.P ? x[o] : 0ull;
+        }
+        insert_desc<K>(a, x[0]);
+        insert_desc<K>(b2, x[1]);
       }
-      insert_desc<K>(a, x[0]);
-      insert_desc<K>(b2, x[1]);
-    }
+    };
+    if (64 * u + 64 <= p.P) scan(std::false_type{});
+    else scan(std::true_type{});
     if (u == tiles_pf - 1) {
       // merge the odd list and the partner half's list, then flush this frame
 #pragma unroll
