@@ -103,8 +103,9 @@ __host__ __device__ inline int64_t slot_token(const Geom& g, int64_t slot) {
 // ref: saf3r/triton/topk_utils.py:26-29
 // ---------------------------------------------------------------------------------------
 __host__ __device__ inline uint32_t fkey(float x) {
-  uint32_t b = __builtin_bit_cast(uint32_t, x);
-  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+  // negative: all bits flipped; otherwise the sign bit set (an arithmetic shift spreads the sign)
+  const uint32_t b = __builtin_bit_cast(uint32_t, x);
+  return b ^ ((uint32_t)((int32_t)b >> 31) | 0x80000000u);
 }
 
 // Composite 64-bit key: higher score first, then lower index. Any real candidate is > 0.
