@@ -31,15 +31,17 @@ __device__ inline const __bf16* rows_at(const __bf16* ptr, int64_t rs, int64_t b
   return ptr + (base + f * frs + (r - f * rpf)) * rs;
 }
 
+// insert x into the descending list a (dropping the last entry): with a sorted, the K comparisons
+// are independent (x > a[t] implies x > a[t+1]) and each slot then takes one select: the slot
+// above it (x goes higher), x (x goes here) or itself
 template <int K>
 __device__ inline void insert_desc(uint64_t (&a)[K], uint64_t x) {
+  bool c[K];
 #pragma unroll
-  for (int t = 0; t < K; ++t) {
-    uint64_t hi = x > a[t] ? x : a[t];
-    uint64_t lo = x > a[t] ? a[t] : x;
-    a[t] = hi;
-    x = lo;
-  }
+  for (int t = 0; t < K; ++t) c[t] = x > a[t];
+#pragma unroll
+  for (int t = K - 1; t > 0; --t) a[t] = c[t - 1] ? a[t - 1] : (c[t] ? x : a[t]);
+  a[0] = c[0] ? x : a[0];
 }
 
 __device__ inline uint64_t partner_u64(uint64_t x) {
