@@ -114,6 +114,20 @@ __host__ __device__ inline uint64_t ckey(float x, uint32_t idx) {
 }
 __host__ __device__ inline uint32_t ckey_index(uint64_t c) { return 0xFFFFFFFEu - (uint32_t)(c & 0xFFFFFFFFu); }
 
+// Insert composite key x into a descending list a[0..K), dropping the last entry. Entries equal to
+// 0 are empty; real composites are > 0 and pairwise distinct, and x = 0 changes nothing. With a
+// sorted, the K comparisons are independent (x > a[t] implies x > a[t+1]) and each slot takes one
+// select: the slot above it (x goes higher), x (x goes here) or itself.
+template <int K>
+__device__ inline void topk_insert(uint64_t (&a)[K], uint64_t x) {
+  bool c[K];
+#pragma unroll
+  for (int t = 0; t < K; ++t) c[t] = x > a[t];
+#pragma unroll
+  for (int t = K - 1; t > 0; --t) a[t] = c[t - 1] ? a[t - 1] : (c[t] ? x : a[t]);
+  a[0] = c[0] ? x : a[0];
+}
+
 __device__ inline float bf16_lo(uint32_t w) { return __builtin_bit_cast(float, w << 16); }
 __device__ inline float bf16_hi(uint32_t w) { return __builtin_bit_cast(float, w & 0xFFFF0000u); }
 

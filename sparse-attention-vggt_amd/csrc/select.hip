@@ -13,19 +13,6 @@
 
 namespace saf3r {
 
-// Insert composite key x into a descending list a[0..K) (strict '>' bubble). Entries equal to
-// 0 are empty; real composites are > 0 and pairwise distinct.
-template <int K>
-__device__ inline void topk_insert(uint64_t (&a)[K], uint64_t x) {
-#pragma unroll
-  for (int t = 0; t < K; ++t) {
-    uint64_t hi = x > a[t] ? x : a[t];
-    uint64_t lo = x > a[t] ? a[t] : x;
-    a[t] = hi;
-    x = lo;
-  }
-}
-
 // ---------------------------------------------------------------------------------------
 // Pooling: eight lanes per (head, patch block), each lane owning 8 features (16-byte loads), so a
 // wave streams eight blocks at once. Every feature is still summed sequentially in row order.

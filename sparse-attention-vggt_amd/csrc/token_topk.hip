@@ -31,18 +31,6 @@ __device__ inline const __bf16* rows_at(const __bf16* ptr, int64_t rs, int64_t b
   return ptr + (base + f * frs + (r - f * rpf)) * rs;
 }
 
-// insert x into the descending list a (dropping the last entry): with a sorted, the K comparisons
-// are independent (x > a[t] implies x > a[t+1]) and each slot then takes one select: the slot
-// above it (x goes higher), x (x goes here) or itself
-template <int K>
-__device__ inline void insert_desc(uint64_t (&a)[K], uint64_t x) {
-  bool c[K];
-#pragma unroll
-  for (int t = 0; t < K; ++t) c[t] = x > a[t];
-#pragma unroll
-  for (int t = K - 1; t > 0; --t) a[t] = c[t - 1] ? a[t - 1] : (c[t] ? x : a[t]);
-  a[0] = c[0] ? x : a[0];
-}
 
 __device__ inline uint64_t partner_u64(uint64_t x) {
   uint32_t lo = (uint32_t)x, hi = (uint32_t)(x >> 32);
@@ -138,8 +126,8 @@ __global__ __launch_bounds__(256) void token_topk_kernel(TopkParams p) {
           x[o] = ckey(sv, (uint32_t)pp);
           if constexpr (decltype(padded)::value) x[o] = pp < p.P ? x[o] : 0ull;
         }
-        insert_desc<K>(a, x[0]);
-        insert_desc<K>(b2, x[1]);
+        topk_insert<K>(a, x[0]);
+        topk_insert<K>(b2, x[1]);
       }
     };
     if (64 * u + 64 <= p.P) scan(std::false_type{});
@@ -148,7 +136,7 @@ __global__ __launch_bounds__(256) void token_topk_kernel(TopkParams p) {
       // merge the odd list and the partner half's list, then flush this frame
 #pragma unroll
       for (int e = 0; e < K; ++e) {
-        insert_desc<K>(a, b2[e]);
+        topk_insert<K>(a, b2[e]);
         b2[e] = 0;
       }
       uint64_t b[K];
@@ -156,7 +144,7 @@ __global__ __launch_bounds__(256) void token_topk_kernel(TopkParams p) {
       for (int e = 0; e < K; ++e) b[e] = partner_u64(a[e]);
 #pragma unroll
       for (int e = 0; e < K; ++e)
-        if (b[e] > a[K - 1]) insert_desc<K>(a, b[e]);
+        if (b[e] > a[K - 1]) topk_insert<K>(a, b[e]);
       if (qvalid && half == 0) {
         int32_t* o = p.idx + qi * ((int64_t)p.F * p.ke) + (int64_t)f * p.ke;
 #pragma unroll
