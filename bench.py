@@ -72,42 +72,74 @@ def layer_config(layers, heads, seed_base, synth, ops):
     return cfg, tables
 
 
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or "unknown"
+
+
+def host_threads() -> int:
+    """Cores this process may run on (its affinity set; os.cpu_count() where that is unavailable)."""
+    try:
+        return len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        return os.cpu_count() or 1
+
+
 def cpu_baseline(pkg, frames=4, heads=16, repeats=5, budget_s=25.0):
-    """The oracle's masked fp32 attention path on the 4-frame VGGT shape, timed on host cores."""
+    """The oracle's fp32 attention path on the 4-frame VGGT shape, timed on the host cores: the masked
+    variant (per head, query chunks, full q.k^T plus the pattern's mask) and the gathered variant (keys
+    restricted per pattern), both including the block selection; 1 warm-up, then the median of up to
+    ``repeats`` runs within ``budget_s`` seconds."""
     import importlib
 
-    import numpy as np
     from oracle import attention as OA
     from oracle import selection as OS
     synth = importlib.import_module(pkg.__name__ + ".synth")
     acc = importlib.import_module(pkg.__name__ + ".accounting")
     ops = importlib.import_module(pkg.__name__ + ".ops")
+    threads = host_threads()
+    torch.set_num_threads(threads)
     wl = synth.structured_qkv(frames=frames, heads=heads, seed=0)
     q, k, v = (t.to(torch.bfloat16).float() for t in (wl.q, wl.k, wl.v))
     patterns = synth.round_robin_patterns(heads)
     g = wl.geom
     og = OA.Geometry(g.frames, g.tokens_per_frame, g.num_special)
 
-    def run():
+    def run(gathered):
         sel = {}
         for h, p in enumerate(patterns):
             if p == ops.BLOCK_DYNAMIC:
                 sel[h] = torch.from_numpy(OS.block_select(OS.bf16_bits(q[h].numpy()), OS.bf16_bits(k[h].numpy()),
                                                           g.frames, g.tokens_per_frame, g.num_special, 4))
-        outs = [OA.pattern_attention(q[h], k[h], v[h], p, og, sel.get(h), dtype=torch.float32)
-                for h, p in enumerate(patterns)]
+        if gathered:
+            outs = [OA.sparse_attention_gathered(q[h], k[h], v[h], p, og, sel.get(h), dtype=torch.float32)
+                    for h, p in enumerate(patterns)]
+        else:
+            outs = [OA.pattern_attention(q[h], k[h], v[h], p, og, sel.get(h), dtype=torch.float32)
+                    for h, p in enumerate(patterns)]
         return sel, outs
 
-    t0 = time.perf_counter()
-    sel, _ = run()  # warm-up
-    first = time.perf_counter() - t0
-    n = max(1, min(repeats, int(budget_s / max(first, 1e-3))))
-    times = []
-    for _ in range(n):
+    def timed(gathered):
         t0 = time.perf_counter()
-        run()
-        times.append(time.perf_counter() - t0)
-    med = statistics.median(times)
+        sel, _ = run(gathered)  # warm-up
+        first = time.perf_counter() - t0
+        n = max(1, min(repeats, int(budget_s / 2 / max(first, 1e-3))))
+        times = []
+        for _ in range(n):
+            t0 = time.perf_counter()
+            run(gathered)
+            times.append(time.perf_counter() - t0)
+        return sel, statistics.median(times), n
+
+    sel, med, n = timed(False)
+    _, med_g, n_g = timed(True)
     dyn = [h for h, p in enumerate(patterns) if p == ops.BLOCK_DYNAMIC]
     sel_t = torch.stack([sel[h] for h in dyn]) if dyn else None
     flops = acc.attention_flops(patterns, g, sel_t)
@@ -119,32 +151,47 @@ def cpu_baseline(pkg, frames=4, heads=16, repeats=5, budget_s=25.0):
         "sample": (f"{frames} frames x {g.tokens_per_frame} tokens ({g.tokens}), {heads} heads round-robin "
                    "dense/frame-local/anchor+local/block-top4, oracle masked fp32 attention incl. block selection, "
                    f"no projections; median of {n} runs, {med * 1e3:.0f} ms/layer"),
+        "cpu_model": cpu_model(),
+        "os_cpu_count": os.cpu_count(),
         "ms_per_layer": round(med * 1e3, 2),
+        "gathered_ms_per_layer": round(med_g * 1e3, 2),
+        "gathered_value": round(flops / med_g / 1e12, 6),
+        "gathered_runs": n_g,
         "algorithmic_flop": flops,
     }
 
 
-def scores_path(ops, geom, n_dyn, reps=20):
-    """The scores-input selection path: per-frame top-4 of a synthetic fp32 block-score matrix
-    [n_dyn * NB, NB] (N(0,1) scores), the same shape the fused selection scores internally."""
+def scores_path(ops, geom, n_dyn, buffers=3):
+    """The scores-input selection path (saf3r_topk_from_scores): per-frame top-4 of synthetic fp32
+    block-score matrices [n_dyn * NB, NB] (N(0,1) scores), the shape the fused selection scores
+    internally. The launches rotate over ``buffers`` distinct matrices (3 x 222 MB at 128 frames, more
+    than the 256 MB last-level cache), so each launch reads data the previous launches did not touch;
+    every launch is timed by its own stream events."""
     nb = geom.num_blocks
-    s = torch.randn(n_dyn * nb, nb, device="cuda:0")
-    idx = ops.topk_from_scores(s, geom.frames, 4)
+    mats = [torch.randn(n_dyn * nb, nb, device="cuda:0") for _ in range(buffers)]
+    idx = ops.topk_from_scores(mats[0], geom.frames, 4)
     torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    # a launch takes ~60 us on the GPU and about as long on the host (Python, ctypes, the output
-    # allocation): queue the timed launches behind a GPU spin so that they run back to back
+    n = 4 * buffers
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(n + 1)]
+    # the host needs about as long to submit a launch as the GPU to run it: queue every launch behind
+    # a GPU spin so that they run back to back, with an event between consecutive launches
     torch.cuda._sleep(50_000_000)
-    e0.record()
-    for _ in range(reps):
-        idx = ops.topk_from_scores(s, geom.frames, 4)
-    e1.record()
+    for r in range(n):
+        ev[r].record()
+        idx = ops.topk_from_scores(mats[(r + 1) % buffers], geom.frames, 4)
+    ev[n].record()
     torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / reps
-    nbytes = s.numel() * 4 + idx.numel() * 4
-    del s
+    times = [ev[r].elapsed_time(ev[r + 1]) for r in range(n)]
+    ms = statistics.median(times)
+    nbytes = mats[0].numel() * 4 + idx.numel() * 4
+    del mats
     return {"scores_path_ms": round(ms, 4), "scores_path_GBs": round(nbytes / (ms * 1e-3) / 1e9, 1),
-            "scores_path_frac": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+            "scores_path_frac": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+            "scores_path_note": f"{buffers} rotating {mats_mb(nb, n_dyn)} MB score matrices, cold per launch"}
+
+
+def mats_mb(nb, n_dyn):
+    return round(n_dyn * nb * nb * 4 / 1e6)
 
 
 def non_lazy_selection(pkg, frames, reps=2):
@@ -182,6 +229,94 @@ def non_lazy_selection(pkg, frames, reps=2):
     nbytes = scores.numel() * 2 + idx.numel() * 4
     res["select_block_ms"] = round(ms, 4)
     res["select_block_GBs"] = round(nbytes / (ms * 1e-3) / 1e9, 1)
+    return res
+
+
+def aggregator_leg(pkg, frames=64, warmup=1, repeats=3, profile=None):
+    """The full VGGT-1B-style aggregator forward (DINOv2-L/14 patch embedding, 24 frame + 24 global
+    blocks, dim 1024, random-init bf16 weights) over ``frames`` synthetic 518 x 518 frames (uniform [0, 1]
+    pixels blurred with a seeded Gaussian, sigma 4): ``warmup`` + ``repeats`` forwards, median ms, first
+    with dense global attention (torch SDPA), then with the global attention patched by the plugin with
+    the reference's VGGT head profile (lazy dino top-4). The global-attention share is the time between
+    stream events recorded around every global ``attn`` module call, over the forward's time."""
+    import importlib
+    agg = importlib.import_module(pkg.__name__ + ".aggregator")
+    plug = importlib.import_module(pkg.__name__ + ".patch")
+    dev = torch.device("cuda:0")
+    torch.manual_seed(0)
+    with torch.device(dev):
+        model = agg.VGGTAggregatorModel()
+    model = model.to(torch.bfloat16).eval()
+    images = agg.blurred_frames(frames, 518, 4.0, seed=0, device=dev).to(torch.bfloat16)
+    res = {"frames": frames, "image": "518x518", "tokens": frames * 1374,
+           "protocol": f"{warmup} warm-up + {repeats} timed forwards, median"}
+    # frame blocks and the patch embedding's blocks: torch's fused SDPA where this build has it
+    try:
+        with torch.no_grad():
+            model.aggregator.frame_blocks[0].attn(torch.zeros(2, 1374, 1024, device=dev, dtype=torch.bfloat16),
+                                                  pos=model.aggregator.positions(2, 37, 37, dev))
+        res["frame_attention"] = "torch SDPA (flash / memory-efficient)"
+    except RuntimeError as e:
+        model.aggregator.set_frame_attention("saf3r")
+        res["frame_attention"] = f"saf3r frame-local kernels (torch SDPA: {str(e)[:80]})"
+
+    def run(tag, patched):
+        spans = []
+
+        def pre(mod, args):
+            ev = torch.cuda.Event(enable_timing=True)
+            ev.record()
+            spans.append([ev, None])
+
+        def post(mod, args, out):
+            ev = torch.cuda.Event(enable_timing=True)
+            ev.record()
+            spans[-1][1] = ev
+
+        hooks = []
+        for b in model.aggregator.global_blocks:
+            hooks.append(b.attn.register_forward_pre_hook(pre))
+            hooks.append(b.attn.register_forward_hook(post))
+        walls, shares, glob = [], [], []
+        try:
+            for it in range(warmup + repeats):
+                spans.clear()
+                torch.cuda.synchronize()
+                torch.cuda.reset_peak_memory_stats()
+                t0 = time.perf_counter()
+                if patched:
+                    plug.update_args_per_forward(model, "vggt", 518, 518)
+                with torch.no_grad():
+                    out, _ = model(images)
+                torch.cuda.synchronize()
+                dt = (time.perf_counter() - t0) * 1e3
+                g_ms = sum(a.elapsed_time(b) for a, b in spans)
+                del out
+                if it >= warmup:
+                    walls.append(dt)
+                    glob.append(g_ms)
+                    shares.append(g_ms / dt)
+        finally:
+            for h in hooks:
+                h.remove()
+        res[tag] = {"forward_ms": round(statistics.median(walls), 1),
+                    "global_attn_ms": round(statistics.median(glob), 1),
+                    "global_attn_share": round(statistics.median(shares), 4),
+                    "peak_mem_gib": round(torch.cuda.max_memory_allocated() / 2 ** 30, 2)}
+
+    try:
+        run("dense", False)
+    except RuntimeError as e:
+        res["dense"] = f"unavailable: {str(e)[:120]}"
+    with open(profile or os.path.join(ROOT, "tests", "golden", "vggt_eth3d_profile.json")) as f:
+        prof = json.load(f)
+    plug.patch_model(model, "vggt", {"patch_module": {"type": "headsparse", "topk_mode": "token",
+                                                      "lazy_dino_topk": True, "topk": 4}, "sparse_config": prof})
+    run("saf3r_lazy_top4", True)
+    if isinstance(res.get("dense"), dict):
+        res["speedup_vs_dense"] = round(res["dense"]["forward_ms"] / res["saf3r_lazy_top4"]["forward_ms"], 3)
+    del model, images
+    torch.cuda.empty_cache()
     return res
 
 
@@ -223,6 +358,8 @@ def main():
                          "instead of the seeded block-pattern tables; dino_topk heads use lazy top-4 indices")
     ap.add_argument("--non-lazy-select", action="store_true",
                     help="also time the non-lazy DINO-feature token selection at the full frame count")
+    ap.add_argument("--aggregator-frames", type=int, default=64,
+                    help="frames of the full-aggregator forward leg (0 skips it)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only a plain copy kernel of known size (reads 1 GiB, writes 1 GiB), for scaling "
                          "the FETCH_SIZE / WRITE_SIZE counters of a profiling run")
@@ -302,6 +439,9 @@ def main():
 
     attn_flops = [layer_work(w, True) for w in layers]
     kernel_flops = [layer_work(w, False) for w in layers]
+    exec_flops = [acc.executed_tile_flops(w.patterns, geom, w.last_selection,
+                                          w.last_keysets.count.tolist() if w.keyset_heads else None,
+                                          ops.token_order_heads(w.patterns)) for w in layers]
     proj = acc.projection_flops(N, dim)
     layer_flops = sum(attn_flops) / args.layers + proj
     attn_ms = dur.get("sparse_attn", [])
@@ -364,13 +504,23 @@ def main():
             "unit": "TFLOP/s",
             "frac": None if attn_tflops is None else round(attn_tflops / PEAK_BF16_TFLOPS, 4),
             "traffic": measured_traffic(),
+            "traffic_source": ("FETCH_SIZE + WRITE_SIZE counter runs of this workload, scaled by a copy kernel: "
+                               "profiles/hbm_traffic_vggt1b_global_f128.md"),
             "launch_ms": round(attn_ms_avg, 3),
+            "executed_tile_flop": round(sum(exec_flops) / args.layers),
+            "algorithmic_flop": round(sum(kernel_flops) / args.layers),
+            "executed_frac": (None if attn_tflops is None else
+                              round(sum(exec_flops) * args.steps / (sum(attn_ms) * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)),
         },
         "selection": dict(sel_extra, bound="hbm", peak=PEAK_HBM_GBS, unit="GB/s"),
         "other_kernels_ms": other_ms,
     }
     if args.non_lazy_select:
         result["non_lazy_selection"] = non_lazy_selection(pkg, args.frames)
+    del layers, model, x
+    torch.cuda.empty_cache()
+    if args.aggregator_frames > 0 and not args.sparse_config:
+        result["aggregator"] = aggregator_leg(pkg, args.aggregator_frames)
     if not args.no_cpu_baseline and not args.sparse_config:
         result["cpu_baseline"] = cpu_baseline(pkg)
     print(json.dumps(result), flush=True)

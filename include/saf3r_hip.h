@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define SAF3R_ABI_VERSION 4
+#define SAF3R_ABI_VERSION 5
 
 enum saf3r_status {
   SAF3R_OK = 0,
@@ -60,9 +60,13 @@ enum saf3r_pattern {
   SAF3R_SKIP = 6,          /* output zero.                        ref: sparse_attention.py:40-41 */
   SAF3R_KEYSET = 7,        /* j in the head's shared key set (saf3r_keyset_build / _gather).
                               ref: sparse_attention.py:256-273 (stride), :143-186 (q_probe_topk) */
-  SAF3R_BROADCAST = 8      /* frame 0's attention map applied to every frame: the row of token
+  SAF3R_BROADCAST = 8,     /* frame 0's attention map applied to every frame: the row of token
                               f*T + i is sum_j softmax_j(q[i] . k[j] * scale) v[f*T + j], i, j < T.
                               ref: sparse_attention.py:110-131 (broadcast_first) */
+  SAF3R_TOKEN_DYNAMIC_KEYSET = 9 /* dino_topk with dino_sp2sp_stride s != 1: special rows attend the
+                              head's key set (keys 0, s, 2s, ...: a SAF3R_KEYSET_STRIDE set with start 0
+                              and no include), served from the key-set buffers like a KEYSET head;
+                              patch rows go through saf3r_gather_attn_fwd. ref: sparse_attention.py:197-208 */
 };
 
 /* Key-set kinds of saf3r_keyset_build. */
@@ -152,16 +156,21 @@ int saf3r_block_select(const float* pooled_q, const float* pooled_k, int n, int 
 /*
  * Mean query and probe scores of the q_probe_topk key set, for n_sel heads (head_ids, device
  * int32) of the packed Q/K.
- *   qbar[s][d]: mean over all N = frames*tokens_per_frame tokens: chunks of ceil(N/256) tokens
- *               summed sequentially in token order, chunk sums added in order, one division by N.
+ *   sample_idx: device int32 [n_samples] token ids in [0, N) (entries outside are clamped), or NULL
+ *               for every token (n_samples ignored). The reference's q_sample_ratio < 1 samples
+ *               torch.linspace(0, N-1, n).long() tokens; the caller passes that list.
+ *   qbar[s][d]: mean over the sampled rows (all N = frames*tokens_per_frame tokens without a list):
+ *               chunks of ceil(M/256) rows (M rows in list order) summed sequentially, chunk sums
+ *               added in order, one division by M.
  *   scores[s][t] (row stride scores_stride >= N, token order): sequential fmaf over d of
  *               qbar[d] * k[t][d], times scale (1/8 for head_dim 64).
  *   partial: device workspace of n_sel * 256 * 64 floats.
- * Replaces: saf3r/patch/sparse_attention.py:160-168 (q_bar and the probe scores).
+ * Replaces: saf3r/patch/sparse_attention.py:150-168 (query sampling, q_bar and the probe scores).
  */
 int saf3r_probe_scores(const void* q_packed, const void* k_packed, int frames, int tokens_per_frame,
-                       int num_special, const int32_t* head_ids, int n_sel, float scale, float* partial,
-                       float* qbar, float* scores, int64_t scores_stride, void* stream);
+                       int num_special, const int32_t* head_ids, int n_sel, const int32_t* sample_idx,
+                       int n_samples, float scale, float* partial, float* qbar, float* scores,
+                       int64_t scores_stride, void* stream);
 
 /*
  * Shared key sets of n_heads heads (device int32 arrays of n_heads entries each):
@@ -197,11 +206,13 @@ int saf3r_keyset_gather(const void* k_packed, int frames, int tokens_per_frame, 
  *   sel: int32 [n_block_dynamic][F*NBf][sel_width] block ids (-1 = empty), one list per
  *        BLOCK_DYNAMIC head in increasing head order; may be NULL when no head is BLOCK_DYNAMIC.
  *   out: bf16 natural layout, element (token t, head h, d) at out[t*out_row_stride + h*64 + d].
- *        TOKEN_DYNAMIC heads get only their special rows written here.
+ *        TOKEN_DYNAMIC(_KEYSET) heads get only their special rows written here.
  *   scale: softmax scale (1/8 for head_dim 64).
  *   keyset_k / keyset_v / keyset_count / keyset_capacity: the saf3r_keyset_gather buffers of the
- *        KEYSET heads, set s serving the s-th KEYSET head in increasing head order; every query of
- *        such a head attends keys 0 .. keyset_count[s]-1. NULL / 0 when no head is KEYSET.
+ *        KEYSET and TOKEN_DYNAMIC_KEYSET heads, set s serving the s-th of those heads in increasing
+ *        head order; every query of a KEYSET head (every special row of a TOKEN_DYNAMIC_KEYSET head)
+ *        attends keys 0 .. min(keyset_count[s], keyset_capacity)-1 (a count above the
+ *        capacity is clamped to it; keyset_capacity is a multiple of 64). NULL / 0 when no head is KEYSET.
  *   bcast_q / bcast_k / bcast_v: frame 0 and per-frame buffers of the BROADCAST heads, b-th buffer
  *        for the b-th BROADCAST head in increasing head order, C = ceil(T/64)*64 rows per frame:
  *          bcast_q: bf16 [n_broadcast][C][64], row i = packed Q of token i (frame 0), zeros past T;

@@ -23,6 +23,9 @@ Patterns (per head; mask M[i, j] = 1 iff query i may attend key j):
   KEYSET         j in one key set shared by every query of the head (``stride``, ``:256-273``;
                  ``q_probe_topk``, ``:143-186``; the set itself comes from
                  ``oracle.selection.keyset``)
+  TOKEN_DYNAMIC_KEYSET  ``dino_topk`` with ``dino_sp2sp_stride`` s != 1: special rows attend keys
+                 0, s, 2s, ... (``:199-204``; the list comes from ``oracle.selection.keyset``), image
+                 rows as TOKEN_DYNAMIC
   BROADCAST      ``broadcast_first`` (``:110-131``): frame 0's attention map applied to every frame,
                  row f*T + i = sum_j softmax_j(q_i . k_j / sqrt(d)) v_{f*T + j}, i, j < T (not a mask
                  over the row's own q; see :func:`broadcast_attention`)
@@ -35,7 +38,8 @@ from dataclasses import dataclass
 
 import torch
 
-DENSE, FRAME_LOCAL, ANCHOR_LOCAL, BLOCK_DYNAMIC, TOKEN_DYNAMIC, ANCHOR, SKIP, KEYSET, BROADCAST = range(9)
+(DENSE, FRAME_LOCAL, ANCHOR_LOCAL, BLOCK_DYNAMIC, TOKEN_DYNAMIC, ANCHOR, SKIP, KEYSET, BROADCAST,
+ TOKEN_DYNAMIC_KEYSET) = range(10)
 
 
 @dataclass(frozen=True)
@@ -162,16 +166,18 @@ def gather_attention(q, k, v, idx, scale=None, dtype=torch.float32):
     return out
 
 
-def token_dynamic_attention(q, k, v, est_topk_idx, g: Geometry, sp2sp_stride=1, dtype=torch.float64):
+def token_dynamic_attention(q, k, v, est_topk_idx, g: Geometry, sp2sp_stride=1, dtype=torch.float64,
+                            spec_keys=None):
     """Reference ``dino_topk_attention`` (``saf3r/patch/sparse_attention.py:189-231``).
 
-    Special rows attend keys 0, s, 2s, ... (s = ``sp2sp_stride``); image rows attend the image
-    tokens ``est_topk_idx[i]`` (indices into the image-token list) and never special keys.
+    Special rows attend keys 0, s, 2s, ... (s = ``sp2sp_stride``; or the token list ``spec_keys``);
+    image rows attend the image tokens ``est_topk_idx[i]`` (indices into the image-token list) and
+    never special keys.
     """
     frame, special, _ = token_info(g)
     out = torch.empty(g.tokens, v.shape[1], dtype=dtype)
     spec = special.nonzero().flatten()
-    keys = torch.arange(0, g.tokens, sp2sp_stride)
+    keys = torch.arange(0, g.tokens, sp2sp_stride) if spec_keys is None else torch.as_tensor(spec_keys).long()
     m = torch.ones(len(spec), len(keys), dtype=torch.bool)
     out[spec] = masked_attention(q[spec], k[keys], v[keys], m, dtype=dtype)
     img = image_token_ids(g)
@@ -312,6 +318,8 @@ def head_outputs(q, k, v, patterns, g: Geometry, sel_by_head=None, est_topk_idx=
         sel = None if sel_by_head is None else sel_by_head.get(h)
         if pat == TOKEN_DYNAMIC:
             o = token_dynamic_attention(q[h], k[h], v[h], est_topk_idx, g, dtype=dtype)
+        elif pat == TOKEN_DYNAMIC_KEYSET:  # sel: the special rows' key list
+            o = token_dynamic_attention(q[h], k[h], v[h], est_topk_idx, g, dtype=dtype, spec_keys=sel)
         elif pat == BROADCAST:
             o = broadcast_attention(q[h], k[h], v[h], g, dtype=dtype)
         elif gathered:

@@ -19,7 +19,7 @@ EXPORTS = (
     "saf3r_token_topk", "saf3r_probe_scores", "saf3r_keyset_build", "saf3r_keyset_gather",
     "saf3r_frame_topk_scores",
 )
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 _lib = None
 
@@ -65,7 +65,7 @@ def load():
                                   i32),
         "saf3r_gather_attn_fwd": ([rows, rows, rows, p, i64, i32, i32, i64, f32, rows, p], i32),
         "saf3r_token_topk": ([rows, rows, i32, i32, i32, i32, p, p], i32),
-        "saf3r_probe_scores": ([p, p, i32, i32, i32, p, i32, f32, p, p, p, i64, p], i32),
+        "saf3r_probe_scores": ([p, p, i32, i32, i32, p, i32, p, i32, f32, p, p, p, i64, p], i32),
         "saf3r_keyset_build": ([p, i64, i32, p, p, p, p, i32, i32, i32, p, i64, p, p], i32),
         "saf3r_keyset_gather": ([p, i32, i32, i32, p, i32, p, i64, i64, p, i64, p, i32, p, p, i64, p], i32),
         "saf3r_frame_topk_scores": ([p, i64, i32, i32, i32, i32, i32, i32, i32, i32, p, i64, p, p, p], i32),

@@ -530,7 +530,7 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
     qt0 = 4 * (it - bfr * gpf);
     nw = min(4, nq - qt0);
     kind = kShared;
-  } else if (pat == SAF3R_TOKEN_DYNAMIC || (pat == SAF3R_BLOCK_DYNAMIC && it < ns4)) {
+  } else if (pat == SAF3R_TOKEN_DYNAMIC || pat == SAF3R_TOKEN_DYNAMIC_KEYSET || (pat == SAF3R_BLOCK_DYNAMIC && it < ns4)) {
     qt0 = 4 * it;
     nw = min(4, g.nst - qt0);
     kind = kShared;
@@ -644,7 +644,7 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
     if constexpr (keyset)
       ks_keys = __builtin_amdgcn_readfirstlane(pat == SAF3R_BROADCAST ? g.T
                                                : tokord               ? p.ntok
-                                                                      : p.ks_count[p.slot[h]]);
+                                                                      : min(p.ks_count[p.slot[h]], (int)p.ks_cap));
     if constexpr (keyset) {
       wk.init(0, (ks_keys + 63) / 64, 0, 0, 0, 0, 0, 0);
     } else if (eff == SAF3R_DENSE) {
@@ -874,7 +874,8 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
     }
     store(A);
     };
-    if (pat == SAF3R_KEYSET || pat == SAF3R_BROADCAST || tokord) shared_walk(std::true_type{});
+    if (pat == SAF3R_KEYSET || pat == SAF3R_TOKEN_DYNAMIC_KEYSET || pat == SAF3R_BROADCAST || tokord)
+      shared_walk(std::true_type{});
     else shared_walk(std::false_type{});
     return;
   }
@@ -1145,6 +1146,7 @@ static int head_segments(int h, int pat, bool tokord, int ntt, const Geom& g, in
     }
     case SAF3R_SKIP: add(0, (g.NT + 3) / 4, 1); break;
     case SAF3R_TOKEN_DYNAMIC: add(0, ns4, g.NT); break;
+    case SAF3R_TOKEN_DYNAMIC_KEYSET: add(0, ns4, ks_cap / 64); break;
     case SAF3R_BLOCK_DYNAMIC:
       add(0, ns4, g.NT);
       add(ns4, g.F * g.NBf, max(1, sel_width / 2));
@@ -1210,11 +1212,11 @@ extern "C" int saf3r_sparse_attn_fwd(const void* q_packed, const void* k_packed,
   int n_dyn = 0, n_ks = 0, n_bc = 0;
   for (int h = 0; h < num_heads; ++h) {
     int pt = head_pattern[h];
-    if (pt < SAF3R_DENSE || pt > SAF3R_BROADCAST)
+    if (pt < SAF3R_DENSE || pt > SAF3R_TOKEN_DYNAMIC_KEYSET)
       return fail(SAF3R_ERR_INVALID, "saf3r_sparse_attn_fwd: head %d has unknown pattern %d", h, pt);
     p.pattern[h] = (int8_t)pt;
     p.slot[h] = (int8_t)(pt == SAF3R_BLOCK_DYNAMIC ? n_dyn++
-                         : pt == SAF3R_KEYSET      ? n_ks++
+                         : (pt == SAF3R_KEYSET || pt == SAF3R_TOKEN_DYNAMIC_KEYSET) ? n_ks++
                          : pt == SAF3R_BROADCAST   ? n_bc++
                                                    : -1);
   }

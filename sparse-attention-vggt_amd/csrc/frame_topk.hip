@@ -384,6 +384,9 @@ extern "C" int saf3r_frame_topk_scores(const void* scores, int64_t score_stride,
     return fail(SAF3R_ERR_UNSUPPORTED, "saf3r_frame_topk_scores: per_frame must be <= %d", kMaxPerFrame);
   if (score_stride % 8 || (uintptr_t)scores % 16)
     return fail(SAF3R_ERR_INVALID, "saf3r_frame_topk_scores: score rows must be 16-byte aligned (stride %% 8)");
+  const bool capped = kept < rest;
+  if (per_frame_mode && nfr > 0 && capped && (!cand_idx || !cand_key))
+    return fail(SAF3R_ERR_INVALID, "saf3r_frame_topk_scores: the cap needs the candidate buffers");
   if (rows == 0) return SAF3R_OK;
   hipStream_t st = (hipStream_t)stream;
   if (fsel > 0) {
@@ -391,11 +394,8 @@ extern "C" int saf3r_frame_topk_scores(const void* scores, int64_t score_stride,
     hipLaunchKernelGGL(first_samples_kernel, dim3(rows), dim3(256), 0, st, idx, idx_stride, fsel, first_stride);
     if (int e = check_launch("saf3r_frame_topk_scores")) return e;
   }
-  const bool capped = kept < rest;
   if (per_frame_mode && nfr > 0) {
     const int k = min(topk, per_frame);
-    if (capped && (!cand_idx || !cand_key))
-      return fail(SAF3R_ERR_INVALID, "saf3r_frame_topk_scores: the cap needs the candidate buffers");
     FrameTopkParams p;
     p.scores = (const uint16_t*)scores;
     p.srs = score_stride;

@@ -36,7 +36,9 @@ struct ProbeParams {
   const __bf16* q;
   const __bf16* k;
   Geom g;
-  int n;  // tokens F * T
+  int n;       // tokens F * T
+  int n_samp;  // rows of the mean: every token (sample == nullptr) or the listed ones
+  const int32_t* sample;
   int chunk;
   int nchunks;
   const int32_t* head_ids;
@@ -47,14 +49,37 @@ struct ProbeParams {
   float scale;
 };
 
-// grid (nchunks, n_sel), 64 threads: feature d of chunk c, summed in token order
+// Packed slot of token t < 2^31 in 32-bit arithmetic (t and the slot are uniform in the callers).
+__device__ inline int64_t token_slot32(const Geom& g, int t) {
+  const int f = t / g.T, r = t - f * g.T;
+  if (r < g.ns) return (int64_t)f * g.ns + r;
+  return (int64_t)g.Sp + (int64_t)f * g.Pp + (r - g.ns);
+}
+
+// grid (nchunks, n_sel), 64 threads: feature d of chunk c, summed over the chunk's rows in order.
+// Rows are read 16 at a time (independent loads in flight) and added in order, so the sum is the
+// sequential one.
 __global__ __launch_bounds__(64) void probe_partial_kernel(ProbeParams p) {
   const int c = bid_x(), hs = bid_y(), d = tid_x();
   const int h = p.head_ids[hs];
-  const int t0 = c * p.chunk, t1 = min(p.n, t0 + p.chunk);
+  const int i0 = c * p.chunk, i1 = min(p.n_samp, i0 + p.chunk);
   const __bf16* base = p.q + (int64_t)h * p.g.L * 64 + d;
   float acc = 0.f;
-  for (int t = t0; t < t1; ++t) acc = acc + (float)base[token_slot(p.g, t) * 64];
+  int i = i0;
+  for (; i + 16 <= i1; i += 16) {
+    float x[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int t = p.sample ? min(max(p.sample[i + j], 0), p.n - 1) : i + j;
+      x[j] = (float)base[token_slot32(p.g, t) * 64];
+    }
+#pragma unroll
+    for (int j = 0; j < 16; ++j) acc = acc + x[j];
+  }
+  for (; i < i1; ++i) {
+    const int t = p.sample ? min(max(p.sample[i], 0), p.n - 1) : i;
+    acc = acc + (float)base[token_slot32(p.g, t) * 64];
+  }
   p.partial[((int64_t)hs * kProbeChunks + c) * 64 + d] = acc;
 }
 
@@ -63,7 +88,7 @@ __global__ __launch_bounds__(64) void probe_finish_kernel(ProbeParams p) {
   const int hs = bid_x(), d = tid_x();
   float total = 0.f;
   for (int c = 0; c < p.nchunks; ++c) total = total + p.partial[((int64_t)hs * kProbeChunks + c) * 64 + d];
-  p.qbar[hs * 64 + d] = __fdiv_rn(total, (float)p.n);
+  p.qbar[hs * 64 + d] = __fdiv_rn(total, (float)p.n_samp);
 }
 
 // grid (ceil(N / 256), n_sel), 256 threads: one token per thread
@@ -74,7 +99,7 @@ __global__ __launch_bounds__(256) void probe_scores_kernel(ProbeParams p) {
   __syncthreads();
   const int t = bid_x() * 256 + tid_x();
   if (t >= p.n) return;
-  const u32x4* row = reinterpret_cast<const u32x4*>(p.k + ((int64_t)h * p.g.L + token_slot(p.g, t)) * 64);
+  const u32x4* row = reinterpret_cast<const u32x4*>(p.k + ((int64_t)h * p.g.L + token_slot32(p.g, t)) * 64);
   float acc = 0.f;
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
@@ -260,37 +285,58 @@ __global__ __launch_bounds__(256) void keyset_gather_kernel(GatherKParams p) {
 
 using namespace saf3r;
 
-extern "C" int saf3r_probe_scores(const void* q_packed, const void* k_packed, int frames, int tokens_per_frame,
-                                  int num_special, const int32_t* head_ids, int n_sel, float scale, float* partial,
-                                  float* qbar, float* scores, int64_t scores_stride, void* stream) {
-  if (int e = injected("saf3r_probe_scores")) return e;
-  ProbeParams p;
-  if (!make_geom(frames, tokens_per_frame, num_special, &p.g))
-    return fail(SAF3R_ERR_INVALID, "saf3r_probe_scores: invalid geometry");
+// Checks the arguments of both probe entries and fills everything but the workspace pointer.
+static int probe_setup(const char* who, const void* q_packed, const void* k_packed, int frames, int tokens_per_frame,
+                       int num_special, const int32_t* head_ids, int n_sel, const int32_t* sample_idx,
+                       int n_samples, float scale, float* qbar, float* scores, int64_t scores_stride,
+                       ProbeParams* pp) {
+  ProbeParams& p = *pp;
+  if (!make_geom(frames, tokens_per_frame, num_special, &p.g)) return fail(SAF3R_ERR_INVALID, "%s: invalid geometry", who);
   const int64_t n = (int64_t)frames * tokens_per_frame;
-  if (n > 0x7fffffff) return fail(SAF3R_ERR_UNSUPPORTED, "saf3r_probe_scores: too many tokens");
-  if (!q_packed || !k_packed || !head_ids || !partial || !qbar || !scores)
-    return fail(SAF3R_ERR_INVALID, "saf3r_probe_scores: null pointer");
+  if (n > 0x7fffffff) return fail(SAF3R_ERR_UNSUPPORTED, "%s: too many tokens", who);
+  if (!q_packed || !k_packed || !head_ids || !qbar || !scores) return fail(SAF3R_ERR_INVALID, "%s: null pointer", who);
   if (n_sel <= 0 || n_sel > 65535 || scores_stride < n)
-    return fail(SAF3R_ERR_INVALID, "saf3r_probe_scores: bad n_sel %d or scores_stride", n_sel);
+    return fail(SAF3R_ERR_INVALID, "%s: bad n_sel %d or scores_stride", who, n_sel);
+  if (sample_idx && (n_samples <= 0 || n_samples > n))
+    return fail(SAF3R_ERR_INVALID, "%s: n_samples must be in [1, %lld]", who, (long long)n);
   if (((uintptr_t)q_packed | (uintptr_t)k_packed) % 16)
-    return fail(SAF3R_ERR_INVALID, "saf3r_probe_scores: packed inputs must be 16-byte aligned");
+    return fail(SAF3R_ERR_INVALID, "%s: packed inputs must be 16-byte aligned", who);
   p.q = (const __bf16*)q_packed;
   p.k = (const __bf16*)k_packed;
   p.n = (int)n;
-  p.chunk = (int)((n + kProbeChunks - 1) / kProbeChunks);
-  p.nchunks = (int)((n + p.chunk - 1) / p.chunk);
+  p.sample = sample_idx;
+  p.n_samp = sample_idx ? n_samples : (int)n;
+  p.chunk = (p.n_samp + kProbeChunks - 1) / kProbeChunks;
+  p.nchunks = (p.n_samp + p.chunk - 1) / p.chunk;
   p.head_ids = head_ids;
-  p.partial = partial;
+  p.partial = nullptr;
   p.qbar = qbar;
   p.scores = scores;
   p.scores_stride = scores_stride;
   p.scale = scale;
+  return SAF3R_OK;
+}
+
+static int probe_launch(const ProbeParams& p, int n_sel, void* stream) {
   hipStream_t s = (hipStream_t)stream;
   hipLaunchKernelGGL(probe_partial_kernel, dim3(p.nchunks, n_sel), dim3(64), 0, s, p);
   hipLaunchKernelGGL(probe_finish_kernel, dim3(n_sel), dim3(64), 0, s, p);
-  hipLaunchKernelGGL(probe_scores_kernel, dim3((unsigned)((n + 255) / 256), n_sel), dim3(256), 0, s, p);
+  hipLaunchKernelGGL(probe_scores_kernel, dim3((unsigned)((p.n + 255) / 256), n_sel), dim3(256), 0, s, p);
   return check_launch("saf3r_probe_scores");
+}
+
+extern "C" int saf3r_probe_scores(const void* q_packed, const void* k_packed, int frames, int tokens_per_frame,
+                                  int num_special, const int32_t* head_ids, int n_sel, const int32_t* sample_idx,
+                                  int n_samples, float scale, float* partial, float* qbar, float* scores,
+                                  int64_t scores_stride, void* stream) {
+  if (int e = injected("saf3r_probe_scores")) return e;
+  ProbeParams p;
+  if (int e = probe_setup("saf3r_probe_scores", q_packed, k_packed, frames, tokens_per_frame, num_special, head_ids,
+                          n_sel, sample_idx, n_samples, scale, qbar, scores, scores_stride, &p))
+    return e;
+  if (!partial) return fail(SAF3R_ERR_INVALID, "saf3r_probe_scores: null workspace");
+  p.partial = partial;
+  return probe_launch(p, n_sel, stream);
 }
 
 extern "C" int saf3r_keyset_build(const float* scores, int64_t scores_stride, int n_heads, const int32_t* mode,

@@ -16,12 +16,15 @@ from . import _lib
 from .layout import BLOCK, HEAD_DIM, Geometry
 
 # Pattern ids (``enum saf3r_pattern``).
-DENSE, FRAME_LOCAL, ANCHOR_LOCAL, BLOCK_DYNAMIC, TOKEN_DYNAMIC, ANCHOR, SKIP, KEYSET, BROADCAST = range(9)
+(DENSE, FRAME_LOCAL, ANCHOR_LOCAL, BLOCK_DYNAMIC, TOKEN_DYNAMIC, ANCHOR, SKIP, KEYSET, BROADCAST,
+ TOKEN_DYNAMIC_KEYSET) = range(10)
 PATTERN_NAMES = {
     DENSE: "dense", FRAME_LOCAL: "frame_local", ANCHOR_LOCAL: "anchor_local",
     BLOCK_DYNAMIC: "block_topk", TOKEN_DYNAMIC: "dino_topk", ANCHOR: "all_to_first", SKIP: "skip",
-    KEYSET: "keyset", BROADCAST: "broadcast_first",
+    KEYSET: "keyset", BROADCAST: "broadcast_first", TOKEN_DYNAMIC_KEYSET: "dino_topk_strided",
 }
+KEYSET_PATTERNS = (KEYSET, TOKEN_DYNAMIC_KEYSET)  # heads served from the key-set buffers
+TOKEN_PATTERNS = (TOKEN_DYNAMIC, TOKEN_DYNAMIC_KEYSET)  # heads whose patch rows gather-attend est_topk_idx
 
 
 _recorder = None
@@ -235,12 +238,12 @@ def sparse_attn_fwd(qp, kp, vp, geom: Geometry, patterns: Sequence[int], sel: to
         width = sel.shape[-1]
     else:
         sel = None
-    n_ks = sum(1 for p in patterns if p == KEYSET)
+    n_ks = sum(1 for p in patterns if p in KEYSET_PATTERNS)
     ks_k = ks_v = ks_n = None
     ks_cap = 0
     if n_ks:
         if keysets is None or keysets.k.shape[0] != n_ks:
-            raise ValueError(f"{n_ks} KEYSET heads need {n_ks} gathered key sets")
+            raise ValueError(f"{n_ks} key-set heads need {n_ks} gathered key sets")
         ks_k, ks_v, ks_n, ks_cap = keysets.k, keysets.v, keysets.count, keysets.capacity
     n_bc = sum(1 for p in patterns if p == BROADCAST)
     bq = bk = bv = None
@@ -335,6 +338,7 @@ class KeySetSpec:
     param: int
     start: int = 0
     include: bool = False
+    sample_ratio: float = 1.0  # KEYSET_TOPK: q_sample_ratio of the mean query (1 = every token)
 
     def bound(self, geom: Geometry) -> int:
         """Upper bound of the member count (host side, sizes the compact buffers)."""
@@ -362,9 +366,10 @@ class KeySets:
 
 
 def probe_scores(qp: torch.Tensor, kp: torch.Tensor, geom: Geometry, head_ids: Sequence[int],
-                 scale: float | None = None):
-    """Mean query and probe scores of ``head_ids`` (``saf3r/patch/sparse_attention.py:160-168``):
-    returns (qbar fp32 [n][64], scores fp32 [n][N] in token order)."""
+                 scale: float | None = None, sample: torch.Tensor | None = None):
+    """Mean query and probe scores of ``head_ids`` (``saf3r/patch/sparse_attention.py:150-168``):
+    returns (qbar fp32 [n][64], scores fp32 [n][N] in token order). ``sample`` (int tokens) restricts
+    the mean to those query rows, in list order (the reference's ``q_sample_ratio < 1``)."""
     _need_cuda(qp, kp)
     lib = _lib.load()
     _check_packed(qp, kp, None, geom)
@@ -375,12 +380,27 @@ def probe_scores(qp: torch.Tensor, kp: torch.Tensor, geom: Geometry, head_ids: S
     qbar = torch.empty(n, HEAD_DIM, dtype=torch.float32, device=dev)
     scores = torch.empty(n, geom.tokens, dtype=torch.float32, device=dev)
     scale = 1.0 / math.sqrt(HEAD_DIM) if scale is None else scale
+    if sample is not None:
+        sample = sample.to(device=dev, dtype=torch.int32).contiguous()
+        if sample.dim() != 1 or not 1 <= sample.numel() <= geom.tokens:
+            raise ValueError("sample must list between 1 and N tokens")
     _mark("probe", "start")
     _lib.check(lib.saf3r_probe_scores(_ptr(qp), _ptr(kp), geom.frames, geom.tokens_per_frame, geom.num_special,
-                                      _ptr(hs), n, float(scale), _ptr(partial), _ptr(qbar), _ptr(scores),
-                                      scores.stride(0), _lib.stream_ptr()))
+                                      _ptr(hs), n, _ptr(sample), 0 if sample is None else sample.numel(),
+                                      float(scale), _ptr(partial), _ptr(qbar), _ptr(scores), scores.stride(0),
+                                      _lib.stream_ptr()))
     _mark("probe", "end")
     return qbar, scores
+
+
+def probe_sample(num_tokens: int, ratio: float) -> torch.Tensor | None:
+    """Query rows of the reference's ``q_sample_ratio`` (``sparse_attention.py:154-157``):
+    ``torch.linspace(0, N-1, steps=max(1, int(N * ratio))).long()`` for ratio < 1, else None (all rows).
+    The list is computed by the same torch call on the host, so it holds the reference's rows."""
+    if ratio >= 1:
+        return None
+    n = max(1, int(num_tokens * ratio))
+    return torch.linspace(0, num_tokens - 1, steps=n).long()
 
 
 def keyset_build(specs: Sequence[KeySetSpec], geom: Geometry, scores: torch.Tensor | None, device):

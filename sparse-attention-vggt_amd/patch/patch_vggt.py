@@ -10,7 +10,8 @@ Configuration (plain dict or attribute object, as the reference's addict ``model
     patch_module.type                      "headsparse"
     patch_module.topk_mode                 "token" (required when a dino_topk head exists)
     patch_module.lazy_dino_topk            indices from the first correspondence head (True), or
-                                           from DINO patch features each forward (False):
+                                           from DINO patch features each forward (False): a forward
+                                           hook on ``aggregator.patch_embed`` runs
                                            ``set_dino_topk_from_features`` with per_frame_topk,
                                            max_topk, include_first_frame, first_frame_stride
     patch_module.topk                      per-frame token top-k of dino_topk heads
@@ -18,7 +19,10 @@ Configuration (plain dict or attribute object, as the reference's addict ``model
     patch_module.topk_scope                "frame" (default) or "global" for block_topk heads
 The lazy indices are shared through one ``SelectionState`` per model instead of rebinding the
 aggregator forward: every dino_topk layer after the one holding the first correspondence head
-reads them, exactly the layers the reference copies them to.
+reads them, exactly the layers the reference copies them to. The non-lazy indices (and the DINO
+candidate of ``headprofile``) come from a forward hook on the aggregator's patch embedding, which sees
+the same post-norm patch tokens the reference's rebound ``Aggregator.forward`` reads
+(``patch_vggt.py:195-207, 226-240, 313-357``).
 """
 from __future__ import annotations
 
@@ -53,9 +57,11 @@ def patch_model(model, model_cfg):
     ptype = _get(pm, "type")
     if ptype == "headprofile":  # offline profiler writing the head-profile JSON (profiler.py)
         from .profiler import patch_model_profile
-        return patch_model_profile(model, model_cfg, HeadwiseSparseAttentionWrapper, NUM_SPECIAL_TOKENS,
-                                   model.aggregator.global_blocks[0].attn.num_heads,
-                                   len(model.aggregator.global_blocks), SelectionState())
+        model = patch_model_profile(model, model_cfg, HeadwiseSparseAttentionWrapper, NUM_SPECIAL_TOKENS,
+                                    model.aggregator.global_blocks[0].attn.num_heads,
+                                    len(model.aggregator.global_blocks), SelectionState())
+        install_feature_topk(model, model_cfg)
+        return model
     if ptype != "headsparse":
         raise NotImplementedError(f"patch_module.type={ptype!r}: only 'headsparse' and 'headprofile' are built")
     config = _load_config(model_cfg)
@@ -74,7 +80,34 @@ def patch_model(model, model_cfg):
             orig, layer_idx=i, dino_topk=_get(pm, "topk", 4), lazy_dino_topk=lazy, config=layer_config,
             block_topk=_get(pm, "block_topk", 4), topk_scope=_get(pm, "topk_scope", "frame"), shared=state)
     model.saf3r_selection_state = state
+    if has_dino and not lazy:
+        install_feature_topk(model, model_cfg)
     return model
+
+
+def install_feature_topk(model, model_cfg):
+    """Compute the non-lazy token top-k from the DINO patch tokens in every forward: a forward hook on
+    ``model.aggregator.patch_embed`` passes its post-norm patch tokens (``x_norm_patchtokens`` of the
+    DINOv2 output dict, or the token tensor of a plain patch embedding), [S, P, C] for the S frames of
+    the batch-1 input, to ``set_dino_topk_from_features``. ref: saf3r/patch/patch_vggt.py:195-207 and
+    :226-240 (the rebound aggregator forward of the non-lazy and profiling modes), :313-357 (its body).
+    Returns the hook handle, or None for a host without a patch embedding (such a host calls
+    ``set_dino_topk_from_features`` itself)."""
+    agg = getattr(model, "aggregator", None)
+    pe = getattr(agg, "patch_embed", None) if agg is not None else None
+    if pe is None:
+        return None
+    old = getattr(model, "saf3r_feature_topk_hook", None)
+    if old is not None:
+        old.remove()
+
+    def hook(module, inputs, output):
+        tokens = output["x_norm_patchtokens"] if isinstance(output, dict) else output
+        set_dino_topk_from_features(model, tokens, model_cfg)
+
+    handle = pe.register_forward_hook(hook)
+    model.saf3r_feature_topk_hook = handle
+    return handle
 
 
 def update_args_per_forward(model, img_h, img_w):

@@ -7,6 +7,10 @@ ref: saf3r/patch/wrapper.py:112-205 (BaseSparseAttentionProfiler: per head, ever
      :521-566 (save_profile_results: per head the candidate with the lowest mean error, grouped per
      layer, the first dino_topk head marked is_first_dino).
 
+The dino_topk candidate reads the DINO-feature top-k of the forward, which the forward hook installed on
+``aggregator.patch_embed`` computes (``patch_vggt.install_feature_topk``), as the reference's rebound
+aggregator forward does; it is scored for every profiled head, as in the reference.
+
 Every candidate runs through the same kernels as the sparse model: the profiled heads of a layer
 take the candidate's mode together (one sparse-attention launch per candidate), the other heads are
 skipped, and the layer returns full attention, as the reference profiler does.
@@ -88,7 +92,9 @@ class SparseAttentionProfiler(nn.Module):
         energy = (ref ** 2).mean(dim=(0, 2)) + 1e-10
         for i, (cfg, w) in enumerate(zip(self.cfgs, self.candidates)):
             if cfg["mode"] == "dino_topk" and self.shared.est_topk_idx is None:
-                continue  # no DINO-feature indices in this forward
+                raise RuntimeError("headprofile scores the dino_topk candidate from DINO-feature indices: run the "
+                                   "model through aggregator.patch_embed (the forward hook computes them) or call "
+                                   "set_dino_topk_from_features before this layer")
             out = w.compute_multihead_attention_packed(qkv, p, geom).float().reshape(N, self.num_heads, HEAD_DIM)
             mse = ((out - ref) ** 2).mean(dim=(0, 2)) / energy
             for h in self.heads:

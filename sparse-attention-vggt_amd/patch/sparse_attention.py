@@ -8,7 +8,9 @@ Reference modes          kernel pattern
   global_to_frame        FRAME_LOCAL
   all_to_first           ANCHOR
   skip                   SKIP
-  dino_topk              TOKEN_DYNAMIC (special rows dense, image rows gather-attend est_topk_idx)
+  dino_topk              TOKEN_DYNAMIC (special rows dense, image rows gather-attend est_topk_idx);
+                         with dino_sp2sp_stride s != 1 TOKEN_DYNAMIC_KEYSET (special rows over keys
+                         0, s, 2s, ...)
 Block patterns (same JSON format, new mode names)
   dense                  DENSE
   frame_local            FRAME_LOCAL
@@ -20,15 +22,16 @@ Block patterns (same JSON format, new mode names)
                          best mean-query scores, plus frame 0 and the specials with include_as
                          (default False))
   broadcast_first        BROADCAST (frame 0's attention map applied to every frame's V, :110-131)
-Reference option without a kernel in this package: q_probe_topk with q_sample_ratio != 1
--> NotImplementedError.
+q_probe_topk with q_sample_ratio < 1 takes the mean query over the reference's linspace-sampled rows
+(``:154-157``); dino_topk with dino_sp2sp_stride != 1 lets its special rows attend every s-th key
+(``:199-204``, pattern TOKEN_DYNAMIC_STRIDED over a strided key set).
 """
 from __future__ import annotations
 
 import torch
 
 from ..ops import (ANCHOR, ANCHOR_LOCAL, BLOCK_DYNAMIC, BROADCAST, DENSE, FRAME_LOCAL, KEYSET, KEYSET_STRIDE,
-                   KEYSET_TOPK, SKIP, TOKEN_DYNAMIC, KeySetSpec)
+                   KEYSET_TOPK, SKIP, TOKEN_DYNAMIC, TOKEN_DYNAMIC_KEYSET, KeySetSpec)
 
 MODE_TO_PATTERN = {
     "full": DENSE,
@@ -49,6 +52,8 @@ UNBUILT_MODES = ()
 
 def pattern_of(cfg: dict) -> int:
     mode = cfg["mode"]
+    if mode == "dino_topk" and int(cfg.get("dino_sp2sp_stride", 1)) != 1:
+        return TOKEN_DYNAMIC_KEYSET
     if mode in MODE_TO_PATTERN:
         return MODE_TO_PATTERN[mode]
     if mode in UNBUILT_MODES:
@@ -64,13 +69,17 @@ def keyset_spec(cfg: dict, head: int, num_tokens: int) -> KeySetSpec:
         start = head % stride if cfg.get("shift", False) else 0
         return KeySetSpec(head, KEYSET_STRIDE, stride, start, bool(cfg.get("include_as", True)))
     if mode == "q_probe_topk":
-        if cfg.get("q_sample_ratio", 1) != 1:
-            raise NotImplementedError("q_probe_topk with q_sample_ratio != 1 has no kernel in this package")
         if "stride" in cfg:
             k = max(1, num_tokens // int(cfg["stride"]))
         else:
             k = min(int(cfg.get("topk", 1024)), num_tokens)
-        return KeySetSpec(head, KEYSET_TOPK, k, 0, bool(cfg.get("include_as", False)))
+        return KeySetSpec(head, KEYSET_TOPK, k, 0, bool(cfg.get("include_as", False)),
+                          float(cfg.get("q_sample_ratio", 1)))
+    if mode == "dino_topk":  # special rows over k[::s] (``sparse_attention.py:199-204``)
+        stride = int(cfg.get("dino_sp2sp_stride", 1))
+        if stride < 1:
+            raise ValueError("dino_sp2sp_stride must be >= 1")
+        return KeySetSpec(head, KEYSET_STRIDE, stride, 0, False)
     raise ValueError(f"mode {mode!r} has no key set")
 
 

@@ -72,19 +72,16 @@ class BaseHeadwiseSparseAttentionWrapper(nn.Module):
                 seen.add(h)
                 self.head_cfg[h].update(group)
         self.patterns = [pattern_of(c) for c in self.head_cfg]
-        for h, c in enumerate(self.head_cfg):
-            if self.patterns[h] == ops.TOKEN_DYNAMIC and c.get("dino_sp2sp_stride", 1) != 1:
-                raise NotImplementedError("dino_topk with dino_sp2sp_stride != 1 has no kernel in this build")
         ks = {int(c.get("topk", self.block_topk)) for c, p in zip(self.head_cfg, self.patterns)
               if p == ops.BLOCK_DYNAMIC}
         if len(ks) > 1:
             raise ValueError(f"block_topk heads of one layer must share one k, got {sorted(ks)}")
         self.layer_block_topk = ks.pop() if ks else self.block_topk
         self.dyn_heads = [h for h, p in enumerate(self.patterns) if p == ops.BLOCK_DYNAMIC]
-        self.keyset_heads = [h for h, p in enumerate(self.patterns) if p == ops.KEYSET]
+        self.keyset_heads = [h for h, p in enumerate(self.patterns) if p in ops.KEYSET_PATTERNS]
         self.broadcast_heads = [h for h, p in enumerate(self.patterns) if p == ops.BROADCAST]
         self.last_keysets = None
-        self.dino_heads = [h for h, p in enumerate(self.patterns) if p == ops.TOKEN_DYNAMIC]
+        self.dino_heads = [h for h, p in enumerate(self.patterns) if p in ops.TOKEN_PATTERNS]
         self.first_dino_head = next((h for h in self.dino_heads if self.head_cfg[h].get("is_first_dino", False)), None)
 
     # ------------------------------------------------------------------------------------
@@ -150,12 +147,17 @@ class BaseHeadwiseSparseAttentionWrapper(nn.Module):
         probe_rows = [i for i, s in enumerate(specs) if s.mode == ops.KEYSET_TOPK]
         scores = None
         if probe_rows:
-            _, sc = ops.probe_scores(qp, kp, geom, [specs[i].head for i in probe_rows])
-            if len(probe_rows) == len(specs):
-                scores = sc
-            else:
+            ratios = sorted({specs[i].sample_ratio for i in probe_rows})
+            if len(ratios) == 1 and len(probe_rows) == len(specs):
+                _, scores = ops.probe_scores(qp, kp, geom, [specs[i].head for i in probe_rows],
+                                             sample=ops.probe_sample(geom.tokens, ratios[0]))
+            else:  # one call per sample ratio; rows of stride heads stay unused zeros
                 scores = torch.zeros(len(specs), geom.tokens, dtype=torch.float32, device=qp.device)
-                scores[probe_rows] = sc
+                for r in ratios:
+                    rows_r = [i for i in probe_rows if specs[i].sample_ratio == r]
+                    _, sc = ops.probe_scores(qp, kp, geom, [specs[i].head for i in rows_r],
+                                             sample=ops.probe_sample(geom.tokens, r))
+                    scores[rows_r] = sc
         idx, count = ops.keyset_build(specs, geom, scores, qp.device)
         ks = ops.keyset_gather(kp, geom, specs, qkv[:, 2 * C:], qkv.stride(0), HEAD_DIM, idx, count)
         ks.scores = scores

@@ -24,7 +24,7 @@ def test_library_exports_every_declared_symbol(pkg):
     for n in names:
         assert hasattr(lib, n), n
     assert set(names) == set(lib_mod.EXPORTS)
-    assert lib.saf3r_abi_version() == lib_mod.ABI_VERSION == 4
+    assert lib.saf3r_abi_version() == lib_mod.ABI_VERSION == 5
 
 
 def test_packed_slots_matches_layout(pkg):
@@ -46,13 +46,17 @@ def test_invalid_arguments_fail_before_launch(pkg):
     rc = lib.saf3r_sparse_attn_fwd(None, None, None, 2, 100, 5, 2, pat, None, 0, 0.125, None, 128, None, None, None,
                                    0, None, None, None, None, None)
     assert rc == 1 and b"null" in lib.saf3r_last_error()
-    bad = (ctypes.c_int32 * 1)(9)
+    bad = (ctypes.c_int32 * 1)(10)
     dev = ctypes.c_void_p(16)
     rc = lib.saf3r_sparse_attn_fwd(dev, dev, dev, 2, 100, 5, 1, bad, None, 0, 0.125, dev, 64, None, None, None, 0,
                                    None, None, None, None, None)
     assert rc == 1 and b"unknown pattern" in lib.saf3r_last_error()
     ks = (ctypes.c_int32 * 1)(7)  # KEYSET without its buffers
     rc = lib.saf3r_sparse_attn_fwd(dev, dev, dev, 2, 100, 5, 1, ks, None, 0, 0.125, dev, 64, None, None, None, 0,
+                                   None, None, None, None, None)
+    assert rc == 1 and b"key-set" in lib.saf3r_last_error()
+    tks = (ctypes.c_int32 * 1)(9)  # strided dino special rows without the key-set buffers
+    rc = lib.saf3r_sparse_attn_fwd(dev, dev, dev, 2, 100, 5, 1, tks, None, 0, 0.125, dev, 64, None, None, None, 0,
                                    None, None, None, None, None)
     assert rc == 1 and b"key-set" in lib.saf3r_last_error()
     rc = lib.saf3r_sparse_attn_fwd(dev, dev, dev, 2, 100, 5, 1, ks, None, 0, 0.125, dev, 64, dev, dev, dev, 100,
@@ -81,8 +85,12 @@ def test_invalid_arguments_fail_before_launch(pkg):
     assert rc == 1 and b"candidate" in lib.saf3r_last_error()
     rc = lib.saf3r_frame_topk_scores(dev, 9000, 2, 2, 4500, 0, 0, 1, 4, 0, dev, 8, None, None, None)
     assert rc == 2  # frames beyond 4096 keys
-    rc = lib.saf3r_probe_scores(dev, dev, 2, 100, 5, dev, 1, 0.125, dev, dev, dev, 10, None)
+    rc = lib.saf3r_probe_scores(dev, dev, 2, 100, 5, dev, 1, None, 0, 0.125, dev, dev, dev, 10, None)
     assert rc == 1 and b"scores_stride" in lib.saf3r_last_error()
+    rc = lib.saf3r_probe_scores(dev, dev, 2, 100, 5, dev, 1, dev, 201, 0.125, dev, dev, dev, 200, None)
+    assert rc == 1 and b"n_samples" in lib.saf3r_last_error()
+    rc = lib.saf3r_probe_scores(dev, dev, 2, 100, 5, dev, 1, None, 0, 0.125, None, dev, dev, 200, None)
+    assert rc == 1 and b"workspace" in lib.saf3r_last_error()
     rc = lib.saf3r_block_select(ctypes.c_void_p(16), ctypes.c_void_p(16), 1, 4, 2, 2, 33, 0, ctypes.c_void_p(16), None)
     assert rc == 2  # k beyond the supported range
     rc = lib.saf3r_pack_qkv(None, None, None, 64, 64, 0, 10, 1, 1, None, None, None, None, 1e-5, 0, None, None,

@@ -1,0 +1,205 @@
+"""GPU parity of the plugin inside a full (reduced-size) VGGT-style aggregator forward: DINOv2 patch
+embedding, alternating frame / global blocks, global ``attn`` modules patched by ``patch_model``.
+
+Every global layer's input and output are captured with forward hooks during the aggregator forward
+and the output is checked against the oracle layer on that input (kernels' own packed q/k/v, oracle key
+sets / block lists / token lists, fp64 attention, projection): max-abs 2e-2, mean-abs 2e-3. The
+non-lazy dino_topk indices, which the patch-embedding hook computes inside the forward, are checked
+bit-exact against the oracle's selection of the same bf16 score block.
+"""
+import importlib
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import selection as OS
+from tests.layer_check import check_layer_output, err
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+PH, PW, FRAMES, DIM, HEADS = 6, 7, 3, 256, 4
+
+
+@pytest.fixture(scope="module")
+def mods(pkg):
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    return tuple(importlib.import_module(pkg.__name__ + m) for m in (".patch", ".aggregator", ".ops"))
+
+
+def _model(agg, seed, depth=2, frame_attention="saf3r"):
+    torch.manual_seed(seed)
+    m = agg.VGGTAggregatorModel(img_size=14 * PH, embed_dim=DIM, depth=depth, num_heads=HEADS, dino_depth=2,
+                                dino_dim=DIM, dino_heads=HEADS, frame_attention=frame_attention)
+    for b in m.aggregator.global_blocks:  # non-trivial LayerNorm affine parameters and layer scale
+        for n in (b.attn.q_norm, b.attn.k_norm):
+            torch.nn.init.uniform_(n.weight, 0.5, 1.5)
+            torch.nn.init.normal_(n.bias, std=0.1)
+    for b in list(m.aggregator.global_blocks) + list(m.aggregator.frame_blocks):
+        torch.nn.init.uniform_(b.ls1.gamma, 0.5, 1.0)
+        torch.nn.init.uniform_(b.ls2.gamma, 0.5, 1.0)
+    return m
+
+
+def _capture(m):
+    """Forward hooks recording (x, pos, y) of every global attn module and the patch tokens."""
+    rec = {"layers": {}, "patch": None}
+    hooks = []
+    for i, b in enumerate(m.aggregator.global_blocks):
+        def hook(mod, args, kwargs, out, i=i):
+            x = args[0]
+            pos = kwargs.get("pos", args[1] if len(args) > 1 else None)
+            rec["layers"][i] = (x.detach().clone(), pos.detach().clone(), out.detach().clone())
+        hooks.append(b.attn.register_forward_hook(hook, with_kwargs=True))
+
+    def phook(mod, args, out):
+        rec["patch"] = out["x_norm_patchtokens"].detach().clone()
+    hooks.append(m.aggregator.patch_embed.register_forward_hook(phook))
+    return rec, hooks
+
+
+def _images(agg, frames=FRAMES, w_patches=PW):
+    x = agg.blurred_frames(frames, size=14 * max(PH, w_patches), sigma=1.5, seed=3)
+    return x[..., : 14 * PH, : 14 * w_patches].contiguous()
+
+
+def _run(m, plug, images):
+    plug.update_args_per_forward(m, "vggt", images.shape[-2], images.shape[-1])
+    with torch.no_grad():
+        return m(images.to(DEV).to(torch.bfloat16))
+
+
+def test_aggregator_all_full_matches_unpatched(mods, pkg):
+    """Every head 'full': each patched global layer equals the unpatched module computed in fp32 on the
+    CPU from the layer's captured input, and the whole forward stays finite with the expected shapes."""
+    plug, agg, ops = mods
+    m = _model(agg, 0)
+    ref_layers = [b.attn for b in _model(agg, 0).aggregator.global_blocks]  # same weights, fp32, CPU
+    m = m.to(DEV).to(torch.bfloat16)
+    plug.patch_model(m, "vggt", {"patch_module": {"type": "headsparse"}, "sparse_config": {"0": [], "1": []}})
+    rec, hooks = _capture(m)
+    imgs = _images(agg)
+    outs, start = _run(m, plug, imgs)
+    for h in hooks:
+        h.remove()
+    T = PH * PW + 5
+    assert start == 5 and len(outs) == 2 and outs[0].shape == (1, FRAMES, T, 2 * DIM)
+    assert all(torch.isfinite(o.float()).all() for o in outs)
+    for li, (x, pos, y) in rec["layers"].items():
+        with torch.no_grad():
+            yref = ref_layers[li](x.float().cpu(), pos.cpu().long())
+        mx, mean = err(y[0].cpu(), yref[0])
+        print(f"layer {li} all-full vs unpatched fp32: max {mx:.3g} mean {mean:.3g}", flush=True)
+        assert mx <= 2e-2 and mean <= 2e-3
+
+
+def test_aggregator_mixed_modes_match_oracle(mods, pkg):
+    """Block top-k, key-set, frame patterns and lazily shared dino_topk heads inside the forward."""
+    plug, agg, ops = mods
+    m = _model(agg, 1).to(DEV).to(torch.bfloat16)
+    cfg = {"patch_module": {"type": "headsparse", "topk_mode": "token", "lazy_dino_topk": True, "topk": 3,
+                            "block_topk": 2},
+           "sparse_config": {
+               "0": [{"mode": "dino_topk", "head_ids": [0], "is_first_dino": True},
+                     {"mode": "block_topk", "head_ids": [1]}, {"mode": "q_probe_topk", "head_ids": [2], "stride": 4},
+                     {"mode": "global_to_frame", "head_ids": [3]}],
+               "1": [{"mode": "dino_topk", "head_ids": [1, 2]}, {"mode": "stride", "head_ids": [0], "stride": 8},
+                     {"mode": "anchor_local", "head_ids": [3]}]}}
+    plug.patch_model(m, "vggt", cfg)
+    rec, hooks = _capture(m)
+    _run(m, plug, _images(agg))
+    for h in hooks:
+        h.remove()
+    geom = pkg.Geometry(FRAMES, PH * PW + 5, 5)
+    with torch.no_grad():
+        for li, (x, pos, y) in rec["layers"].items():
+            check_layer_output(m.aggregator.global_blocks[li].attn, x, pos, y[0], geom, ops, li)
+
+
+def test_aggregator_non_lazy_dino_topk(mods, pkg):
+    """lazy_dino_topk False: the indices come from the patch-embedding hook inside the forward (no
+    manual call), match the oracle selection of the same bf16 scores, and feed every dino_topk layer."""
+    plug, agg, ops = mods
+    m = _model(agg, 2).to(DEV).to(torch.bfloat16)
+    topk = 4
+    cfg = {"patch_module": {"type": "headsparse", "topk_mode": "token", "lazy_dino_topk": False, "topk": topk,
+                            "per_frame_topk": True, "max_topk": 2048, "include_first_frame": False},
+           "sparse_config": {"0": [{"mode": "dino_topk", "head_ids": [0, 3]}, {"mode": "block_topk", "head_ids": [1]}],
+                             "1": [{"mode": "dino_topk", "head_ids": [2]}]}}
+    plug.patch_model(m, "vggt", cfg)
+    rec, hooks = _capture(m)
+    _run(m, plug, _images(agg))
+    for h in hooks:
+        h.remove()
+    P = PH * PW
+    est = m.saf3r_selection_state.est_topk_idx
+    assert est is not None and est.shape == (FRAMES * P, FRAMES * topk)
+    # the same bf16 score block the selection read, then the oracle's selection
+    feat = torch.nn.functional.normalize(rec["patch"].reshape(1, FRAMES * P, DIM), p=2, dim=-1)
+    fb = feat[0].to(torch.bfloat16)  # the score block exactly as the selection computes it (same GEMM shape)
+    nk8 = -(-fb.shape[0] // 8) * 8
+    kt = torch.zeros(DIM, nk8, dtype=torch.bfloat16, device=fb.device)
+    kt[:, :fb.shape[0]] = fb.t()
+    scores = torch.matmul(fb, kt)[:, :fb.shape[0]].cpu()
+    bits = scores.contiguous().view(torch.int16).numpy().view(np.uint16)
+    ref = OS.token_topk_from_scores(bits, FRAMES, P, topk, per_frame_mode=True)
+    assert np.array_equal(est.cpu().numpy(), ref)
+    geom = pkg.Geometry(FRAMES, P + 5, 5)
+    with torch.no_grad():
+        for li, (x, pos, y) in rec["layers"].items():
+            w = m.aggregator.global_blocks[li].attn
+            assert torch.equal(w.est_topk_idx, est)
+            check_layer_output(w, x, pos, y[0], geom, ops, li)
+
+
+def test_aggregator_headprofile_scores_dino_candidate(mods, pkg, tmp_path):
+    """headprofile on the aggregator: the hook supplies the DINO-feature indices, so every profiled head
+    records every candidate, the dino_topk one included, and the profile JSON lists each head once."""
+    import json
+    plug, agg, ops = mods
+    m = _model(agg, 3).to(DEV).to(torch.bfloat16)
+    cfg = {"patch_module": {"type": "headprofile", "topk": 4, "per_frame_topk": True, "max_topk": 2048,
+                            "include_first_frame": False, "verbose": False}}
+    plug.patch_model(m, "vggt", cfg)
+    _run(m, plug, _images(agg))
+    for b in m.aggregator.global_blocks:
+        prof = b.attn
+        n = len(prof.cfgs)
+        assert prof.cfgs[-1]["mode"] == "dino_topk"
+        for h in range(HEADS):
+            assert sorted(prof.head_errors[h]) == list(range(n)), (prof.layer_idx, h)
+            assert all(np.isfinite(r["mse"][0]) for r in prof.head_errors[h].values())
+    path = tmp_path / "profile.json"
+    res = plug.save_profile_results(m, str(path))
+    saved = json.loads(path.read_text())
+    assert set(saved) == {"0", "1"}
+    for li, groups in res.items():
+        heads = sorted(h for g in groups for h in g["head_ids"])
+        assert heads == list(range(HEADS))
+
+
+def test_aggregator_non_square_input_and_sdpa_frames(mods, pkg):
+    """A 6 x 8 patch grid (position embedding interpolated) with the frame blocks on torch's fused SDPA
+    kernels: the patched global layers still match the oracle."""
+    plug, agg, ops = mods
+    m = _model(agg, 4, frame_attention="sdpa").to(DEV).to(torch.bfloat16)
+    cfg = {"patch_module": {"type": "headsparse", "block_topk": 2},
+           "sparse_config": {"0": [{"mode": "block_topk", "head_ids": [0, 1]}, {"mode": "frame_local", "head_ids": [2]}],
+                             "1": [{"mode": "dense", "head_ids": [0]}, {"mode": "anchor_local", "head_ids": [1, 2]}]}}
+    plug.patch_model(m, "vggt", cfg)
+    rec, hooks = _capture(m)
+    imgs = _images(agg, w_patches=8)
+    try:
+        _run(m, plug, imgs)
+    except RuntimeError as e:  # this torch build has no fused SDPA kernel for the shape
+        if "No available kernel" in str(e):
+            pytest.skip(f"fused SDPA unavailable: {e}")
+        raise
+    finally:
+        for h in hooks:
+            h.remove()
+    geom = pkg.Geometry(FRAMES, PH * 8 + 5, 5)
+    with torch.no_grad():
+        for li, (x, pos, y) in rec["layers"].items():
+            check_layer_output(m.aggregator.global_blocks[li].attn, x, pos, y[0], geom, ops, li)

@@ -50,6 +50,27 @@ def test_probe_scores_bit_exact(ops, pkg, F, T, ns):
         assert np.array_equal(scores[i].cpu().numpy().view(np.uint32), want_s.view(np.uint32)), f"scores head {h}"
 
 
+@pytest.mark.parametrize("F,T,ns,ratio", [(3, 155, 5, 0.1), (4, 1374, 5, 0.3), (2, 64, 0, 0.5), (1, 70, 5, 0.001)])
+def test_probe_scores_sampled_rows_bit_exact(ops, pkg, F, T, ns, ratio):
+    """q_sample_ratio < 1: the mean query over the reference's linspace rows (sparse_attention.py:154-157)."""
+    geom = pkg.Geometry(F, T, ns)
+    H = 2
+    q, k, v = _qkv(H, geom.tokens, seed=F * T + 1, scale=2.0)
+    qp, kp, vp = ops.pack_heads(q.to(DEV), k.to(DEV), v.to(DEV), geom)
+    rows = ops.probe_sample(geom.tokens, ratio)
+    assert rows is not None and len(rows) == max(1, int(geom.tokens * ratio))
+    qbar, scores = ops.probe_scores(qp, kp, geom, [1, 0], sample=rows)
+    torch.cuda.synchronize()
+    for i, h in enumerate([1, 0]):
+        want_q = OS.probe_mean(_bits(q[h][rows]))
+        assert np.array_equal(qbar[i].cpu().numpy().view(np.uint32), want_q.view(np.uint32)), f"qbar head {h}"
+        want_s = OS.probe_scores(want_q, _bits(k[h]))
+        assert np.array_equal(scores[i].cpu().numpy().view(np.uint32), want_s.view(np.uint32)), f"scores head {h}"
+    # the sampled mean is the fp64 mean of those rows to fp32 accuracy, and not the all-row mean
+    ref = q[0][rows].double().mean(0).float()
+    assert torch.allclose(qbar[1].cpu(), ref, atol=1e-5)
+
+
 @pytest.mark.parametrize("F,T,ns", [(3, 155, 5), (4, 1374, 5), (2, 64, 0)])
 def test_keyset_build_bit_exact(ops, pkg, F, T, ns):
     geom = pkg.Geometry(F, T, ns)

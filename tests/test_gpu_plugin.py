@@ -7,6 +7,7 @@ import torch
 
 from oracle import attention as OA
 from oracle import selection as OS
+from tests.layer_check import check_layer, err, make_stack
 from tests.layout_ref import slot_tokens, unpack_rows, unpack_v
 
 pytestmark = pytest.mark.gpu
@@ -20,19 +21,8 @@ def mods(pkg):
     return tuple(importlib.import_module(pkg.__name__ + m) for m in (".patch", ".vggt", ".ops", ".synth"))
 
 
-def _err(a, b):
-    e = (a.float() - b.float()).abs()
-    return e.max().item(), e.mean().item()
-
-
-def _make(vggt, depth, dim, heads, seed=0):
-    torch.manual_seed(seed)
-    m = vggt.GlobalAttentionStack(depth=depth, dim=dim, num_heads=heads)
-    for b in m.aggregator.global_blocks:  # non-trivial LayerNorm affine parameters
-        for n in (b.attn.q_norm, b.attn.k_norm):
-            torch.nn.init.uniform_(n.weight, 0.5, 1.5)
-            torch.nn.init.normal_(n.bias, std=0.1)
-    return m
+_err = err
+_make = make_stack
 
 
 def test_layer_matches_oracle_all_modes(mods, pkg):
@@ -146,56 +136,7 @@ def test_autocast_fp32_module(mods, pkg):
     assert _err(y, y32)[0] < 5e-2
 
 
-def _oracle_keysets(w, q, k, og, ops):
-    """Key sets of the wrapper's stride / q_probe_topk heads from the oracle on the packed q / k."""
-    from importlib import import_module
-    spa = import_module(type(w).__module__.rsplit(".", 1)[0] + ".sparse_attention")
-    out = {}
-    for h in w.keyset_heads:
-        s = spa.keyset_spec(w.head_cfg[h], h, og.tokens)
-        scores = None
-        if s.mode == ops.KEYSET_TOPK:
-            qb = OS.probe_mean(OS.bf16_bits(q[h].float().numpy()))
-            scores = OS.probe_scores(qb, OS.bf16_bits(k[h].float().numpy()))
-        out[h] = torch.from_numpy(OS.keyset(scores, og.tokens, og.tokens_per_frame, og.num_special, s.mode, s.param,
-                                            s.start, s.include))
-    return out
-
-
-def _check_layer(w, x, pos, geom, ops, li, est_ok=True):
-    """Runs one wrapper and checks it against the oracle layer on the kernels' own packed q/k/v."""
-    N, dim, H = geom.tokens, w.orig_module.qkv.in_features, w.num_heads
-    y = w(x, pos)
-    torch.cuda.synchronize()
-    om = w.orig_module
-    qkv = om.qkv(x).reshape(N, 3 * dim).contiguous()
-    qp, kp, vp = ops.pack_qkv(qkv, qkv[:, dim:], qkv[:, 2 * dim:], 3 * dim, 64, geom, H,
-                              ln_q=(om.q_norm.weight, om.q_norm.bias), ln_k=(om.k_norm.weight, om.k_norm.bias),
-                              pos=pos[0], rope_base=100.0)
-    torch.cuda.synchronize()
-    toks = slot_tokens(geom.frames, geom.tokens_per_frame, geom.num_special)
-    q, _ = unpack_rows(qp.cpu(), toks, N)
-    k, _ = unpack_rows(kp.cpu(), toks, N)
-    v, _ = unpack_v(vp.cpu(), toks, N)
-    og = OA.Geometry(geom.frames, geom.tokens_per_frame, geom.num_special)
-    sel = _oracle_keysets(w, q, k, og, ops)
-    if w.keyset_heads:  # the kernels' key sets are the oracle's, member for member
-        ks = w.last_keysets
-        for i, h in enumerate(w.keyset_heads):
-            c = int(ks.count[i])
-            assert torch.equal(ks.idx[i, :c].cpu(), sel[h].to(torch.int32)), f"layer {li} head {h} key set"
-    for h in w.dyn_heads:
-        sel[h] = torch.from_numpy(OS.block_select(OS.bf16_bits(q[h].float().numpy()),
-                                                  OS.bf16_bits(k[h].float().numpy()), geom.frames,
-                                                  geom.tokens_per_frame, geom.num_special, w.layer_block_topk))
-    est = w.est_topk_idx.cpu() if w.dino_heads else None
-    heads = OA.head_outputs(q.float(), k.float(), v.float(), list(w.patterns), og, sel, est_topk_idx=est,
-                            dtype=torch.float64)
-    attn = heads.permute(1, 0, 2).reshape(N, dim).to(torch.bfloat16).float()
-    yref = attn @ om.proj.weight.float().cpu().T + om.proj.bias.float().cpu()
-    mx, mean = _err(y[0].cpu(), yref)
-    print(f"layer {li}: max {mx:.3g} mean {mean:.3g}", flush=True)
-    assert mx <= 2e-2 and mean <= 2e-3
+_check_layer = check_layer
 
 
 def test_layer_keyset_modes(mods, pkg):
@@ -220,6 +161,36 @@ def test_layer_keyset_modes(mods, pkg):
     pos = synth.vggt_positions(F_, ph, pw).to(DEV)[None]
     with torch.no_grad():
         _check_layer(m.aggregator.global_blocks[0].attn, x, pos, geom, ops, 0)
+
+
+def test_layer_sampled_probe_and_strided_dino(mods, pkg):
+    """q_probe_topk with q_sample_ratio < 1 and dino_topk with dino_sp2sp_stride != 1 (special rows over
+    keys 0, s, 2s, ...; sparse_attention.py:154-157, 199-204) against the oracle layer."""
+    plug, vggt, ops, synth = mods
+    ph, pw, F_, H = 7, 9, 4, 8
+    dim = 64 * H
+    m = _make(vggt, 2, dim, H, seed=9).to(DEV).to(torch.bfloat16)
+    cfg = {"patch_module": {"type": "headsparse", "topk_mode": "token", "lazy_dino_topk": True, "topk": 3},
+           "sparse_config": {"0": [
+               {"mode": "dino_topk", "head_ids": [0], "is_first_dino": True, "dino_sp2sp_stride": 1},
+               {"mode": "dino_topk", "head_ids": [1], "dino_sp2sp_stride": 4},
+               {"mode": "q_probe_topk", "head_ids": [2], "stride": 4, "q_sample_ratio": 0.25},
+               {"mode": "q_probe_topk", "head_ids": [3], "topk": 50, "q_sample_ratio": 0.05, "include_as": True},
+               {"mode": "q_probe_topk", "head_ids": [4], "stride": 8},
+               {"mode": "stride", "head_ids": [5], "stride": 16}],
+               "1": [{"mode": "dino_topk", "head_ids": [2, 6], "dino_sp2sp_stride": 3},
+                     {"mode": "dino_topk", "head_ids": [7]}]}}
+    plug.patch_model(m, "vggt", cfg)
+    plug.update_args_per_forward(m, "vggt", ph * 14, pw * 14)
+    geom = pkg.Geometry(F_, ph * pw + 5, 5)
+    g = torch.Generator().manual_seed(10)
+    x = torch.randn(1, geom.tokens, dim, generator=g).to(torch.bfloat16).to(DEV)
+    pos = synth.vggt_positions(F_, ph, pw).to(DEV)[None]
+    w0 = m.aggregator.global_blocks[0].attn
+    assert w0.patterns[1] == ops.TOKEN_DYNAMIC_KEYSET and w0.patterns[0] == ops.TOKEN_DYNAMIC
+    with torch.no_grad():
+        for li in range(2):
+            _check_layer(m.aggregator.global_blocks[li].attn, x, pos, geom, ops, li)
 
 
 def test_reference_profile_layers(mods, pkg):

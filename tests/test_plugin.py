@@ -122,8 +122,16 @@ def test_reference_vggt_profile_fixture(plug, vggt):
     assert (qp.mode, qp.param, qp.include) == (ops.KEYSET_TOPK, n // 4, False)
     assert spa.keyset_spec({"mode": "q_probe_topk"}, 0, n).param == 1024
     assert spa.keyset_spec({"mode": "stride", "stride": 3, "shift": True}, 7, n).start == 1
-    with pytest.raises(NotImplementedError, match="q_sample_ratio"):
-        spa.keyset_spec({"mode": "q_probe_topk", "q_sample_ratio": 0.5}, 0, n)
+    assert spa.keyset_spec({"mode": "q_probe_topk", "q_sample_ratio": 0.5}, 0, n).sample_ratio == 0.5
+    # q_sample_ratio < 1: the reference's linspace rows (sparse_attention.py:154-157)
+    rows = ops.probe_sample(1000, 0.1)
+    assert rows.tolist() == torch.linspace(0, 999, steps=100).long().tolist() and rows[0] == 0 and rows[-1] == 999
+    assert ops.probe_sample(1000, 1) is None and ops.probe_sample(5, 0.01).tolist() == [0]
+    # dino_topk with dino_sp2sp_stride != 1: special rows over keys 0, s, 2s, ... (:199-204)
+    sd = spa.keyset_spec({"mode": "dino_topk", "dino_sp2sp_stride": 3}, 2, n)
+    assert (sd.mode, sd.param, sd.start, sd.include) == (ops.KEYSET_STRIDE, 3, 0, False)
+    assert spa.pattern_of({"mode": "dino_topk", "dino_sp2sp_stride": 3}) == ops.TOKEN_DYNAMIC_KEYSET
+    assert spa.pattern_of({"mode": "dino_topk", "dino_sp2sp_stride": 1}) == ops.TOKEN_DYNAMIC
     m = _model(vggt, depth=1, dim=128, heads=2)
     plug.patch_model(m, "vggt", {"patch_module": {"type": "headsparse"},
                                  "sparse_config": {"0": [{"mode": "broadcast_first", "head_ids": [0]}]}})
