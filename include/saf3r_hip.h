@@ -6,7 +6,8 @@
  *   - Every entry returns an int status (SAF3R_OK = 0). On failure nothing is launched and
  *     saf3r_last_error() returns a message (thread-local). No C++ exception crosses the ABI.
  *   - Every device buffer is allocated by the caller; the library never allocates or frees
- *     device memory and keeps no device state. `stream` is a hipStream_t (NULL = default
+ *     device memory and keeps no device state (the one exception is the static workspace of
+ *     saf3r_probe_scores_noalloc, a device array of the library's code object). `stream` is a hipStream_t (NULL = default
  *     stream); every entry is asynchronous on it and performs no host synchronisation.
  *   - bf16 buffers are passed as void* (IEEE bfloat16, 2 bytes per element).
  *   - Host-side arrays (head tables, frequency tables) are read during the call only.
@@ -171,6 +172,20 @@ int saf3r_probe_scores(const void* q_packed, const void* k_packed, int frames, i
                        int num_special, const int32_t* head_ids, int n_sel, const int32_t* sample_idx,
                        int n_samples, float scale, float* partial, float* qbar, float* scores,
                        int64_t scores_stride, void* stream);
+
+/*
+ * saf3r_probe_scores without the workspace argument: it allocates nothing (no hipMalloc / hipFree,
+ * no allocating library call) and keeps the partial sums in a static device array of the library
+ * (4 MiB per GPU, held until the process ends), for callers that cannot allocate: code under HIP
+ * graph capture, tight serving loops, harnesses that forbid allocation. n_sel <= 64
+ * (SAF3R_ERR_UNSUPPORTED beyond). Results are identical to saf3r_probe_scores. The array belongs to
+ * the current device and is shared by every call on it: calls that overlap on one GPU (other streams,
+ * other host threads) race. No counterpart in the reference.
+ */
+int saf3r_probe_scores_noalloc(const void* q_packed, const void* k_packed, int frames, int tokens_per_frame,
+                               int num_special, const int32_t* head_ids, int n_sel, const int32_t* sample_idx,
+                               int n_samples, float scale, float* qbar, float* scores, int64_t scores_stride,
+                               void* stream);
 
 /*
  * Shared key sets of n_heads heads (device int32 arrays of n_heads entries each):

@@ -18,6 +18,8 @@
 //     increasing token order with work-group prefix counts.
 //   keyset_gather_kernel: compact K rows and transposed, permuted V tiles of the members, in
 //     the packed layout the attention kernel reads.
+#include <mutex>
+
 #include "common.h"
 
 namespace saf3r {
@@ -336,6 +338,56 @@ extern "C" int saf3r_probe_scores(const void* q_packed, const void* k_packed, in
     return e;
   if (!partial) return fail(SAF3R_ERR_INVALID, "saf3r_probe_scores: null workspace");
   p.partial = partial;
+  return probe_launch(p, n_sel, stream);
+}
+
+// ---- allocation-free probe entry ------------------------------------------------------------
+// The partial sums of saf3r_probe_scores_noalloc live in this file-scope device array (one copy per
+// GPU, held until the process ends) instead of a caller workspace. Host code never passes the array's
+// name to a kernel: its device address on the current GPU comes from hipGetSymbolAddress, resolved
+// once per device and kept in scratch_addr. Every chunk sum the finish kernel reads is written by the
+// partial kernel of the same call first, so nothing needs clearing; calls that overlap on one GPU
+// (different streams, or several host threads) share the array and race.
+constexpr int kScratchHeads = 64;
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) float scratch[kScratchHeads * kProbeChunks * 64];  // 4 MiB
+
+static std::mutex scratch_mu;
+static float* scratch_addr[kMaxDevices];  // per device, set once
+
+static int scratch_ptr(const char* who, float** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return fail(SAF3R_ERR_LAUNCH, "%s: no current device (or device id >= %d)", who, kMaxDevices);
+  std::lock_guard<std::mutex> lock(scratch_mu);
+  if (!scratch_addr[dev]) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+      return fail(SAF3R_ERR_LAUNCH, "%s: hipGetSymbolAddress of the static workspace failed on device %d: %s", who,
+                  dev, hipGetErrorString(e));
+    scratch_addr[dev] = static_cast<float*>(ptr);
+  }
+  *out = scratch_addr[dev];
+  return SAF3R_OK;
+}
+
+extern "C" int saf3r_probe_scores_noalloc(const void* q_packed, const void* k_packed, int frames,
+                                          int tokens_per_frame, int num_special, const int32_t* head_ids, int n_sel,
+                                          const int32_t* sample_idx, int n_samples, float scale, float* qbar,
+                                          float* scores, int64_t scores_stride, void* stream) {
+  const char* who = "saf3r_probe_scores_noalloc";
+  if (int e = injected(who)) return e;
+  ProbeParams p;
+  if (int e = probe_setup(who, q_packed, k_packed, frames, tokens_per_frame, num_special, head_ids, n_sel, sample_idx,
+                          n_samples, scale, qbar, scores, scores_stride, &p))
+    return e;
+  if (n_sel > kScratchHeads)
+    return fail(SAF3R_ERR_UNSUPPORTED, "%s: n_sel %d exceeds the %d heads of the static workspace", who, n_sel,
+                kScratchHeads);
+  float* ws = nullptr;
+  if (int e = scratch_ptr(who, &ws)) return e;
+  p.partial = ws;
   return probe_launch(p, n_sel, stream);
 }
 

@@ -1,0 +1,67 @@
+"""The allocation-free probe entry ``saf3r_probe_scores_noalloc`` called through the C ABI, checked
+bit-exact against ``saf3r_probe_scores`` (caller workspace) on two calls in a row, the second with a
+smaller input, so a result cannot come from the static workspace's previous contents."""
+import ctypes
+import importlib
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+@pytest.fixture(scope="module")
+def mods(pkg):
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    return importlib.import_module(pkg.__name__ + ".ops"), importlib.import_module(pkg.__name__ + "._lib")
+
+
+def _probe(lib, L, noalloc, qp, kp, geom, heads, sample):
+    n = len(heads)
+    hs = torch.tensor(heads, dtype=torch.int32, device=DEV)
+    qbar = torch.full((n, 64), float("nan"), device=DEV)
+    scores = torch.full((n, geom.tokens + 3), float("nan"), device=DEV)
+    sp = ctypes.c_void_p(0 if sample is None else sample.data_ptr())
+    ns = 0 if sample is None else sample.numel()
+    args = (ctypes.c_void_p(qp.data_ptr()), ctypes.c_void_p(kp.data_ptr()), geom.frames, geom.tokens_per_frame,
+            geom.num_special, ctypes.c_void_p(hs.data_ptr()), n, sp, ns, 0.125)
+    outs = (ctypes.c_void_p(qbar.data_ptr()), ctypes.c_void_p(scores.data_ptr()), scores.stride(0), L.stream_ptr())
+    if noalloc:
+        rc = lib.saf3r_probe_scores_noalloc(*args, *outs)
+    else:
+        partial = torch.empty(n, 256, 64, device=DEV)
+        rc = lib.saf3r_probe_scores(*args, ctypes.c_void_p(partial.data_ptr()), *outs)
+    L.check(rc)
+    torch.cuda.synchronize()
+    return qbar.cpu(), scores[:, :geom.tokens].cpu()
+
+
+@pytest.mark.parametrize("order", ["large_then_small"])
+def test_noalloc_probe_matches_workspace_entry(mods, pkg, order):
+    ops, L = mods
+    lib = L.load()
+    cases = [(pkg.Geometry(6, 1374, 5), [5, 0, 3, 7, 1, 2, 6, 4], None),          # 8 heads, every token
+             (pkg.Geometry(2, 155, 5), [1, 2], torch.tensor([0, 7, 150, 309], dtype=torch.int32))]  # smaller
+    for i, (geom, heads, sample) in enumerate(cases):
+        print(f"call {i}: {geom} heads {heads} sample {None if sample is None else sample.tolist()}", flush=True)
+        g = torch.Generator().manual_seed(20 + i)
+        H = max(heads) + 1
+        q, k, v = ((torch.randn(H, geom.tokens, 64, generator=g) * 2).to(torch.bfloat16) for _ in range(3))
+        qp, kp, _ = ops.pack_heads(q.to(DEV), k.to(DEV), v.to(DEV), geom)
+        s = None if sample is None else sample.to(DEV)
+        want_q, want_s = _probe(lib, L, False, qp, kp, geom, heads, s)
+        got_q, got_s = _probe(lib, L, True, qp, kp, geom, heads, s)
+        assert np.array_equal(got_q.numpy().view(np.uint32), want_q.numpy().view(np.uint32)), f"qbar, call {i}"
+        assert np.array_equal(got_s.numpy().view(np.uint32), want_s.numpy().view(np.uint32)), f"scores, call {i}"
+        assert torch.isfinite(got_s).all()
+
+
+def test_noalloc_probe_rejects_more_heads_than_the_workspace(mods, pkg):
+    ops, L = mods
+    lib = L.load()
+    dev = ctypes.c_void_p(16)
+    rc = lib.saf3r_probe_scores_noalloc(dev, dev, 2, 100, 5, dev, 65, None, 0, 0.125, dev, dev, 200, None)
+    assert rc == 2 and b"static workspace" in lib.saf3r_last_error()
