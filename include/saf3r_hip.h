@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define SAF3R_ABI_VERSION 5
+#define SAF3R_ABI_VERSION 6
 
 enum saf3r_status {
   SAF3R_OK = 0,
@@ -68,6 +68,11 @@ enum saf3r_pattern {
                               head's key set (keys 0, s, 2s, ...: a SAF3R_KEYSET_STRIDE set with start 0
                               and no include), served from the key-set buffers like a KEYSET head;
                               patch rows go through saf3r_gather_attn_fwd. ref: sparse_attention.py:197-208 */
+};
+
+/* Flags of saf3r_sparse_attn_fwd. */
+enum saf3r_attn_flags {
+  SAF3R_ATTN_FIXED_ORDER = 1 /* every key walk starts at its first tile: run-to-run identical output */
 };
 
 /* Key-set kinds of saf3r_keyset_build. */
@@ -238,6 +243,16 @@ int saf3r_keyset_gather(const void* k_packed, int frames, int tokens_per_frame, 
  *   token_order: host uint8 [num_heads] or NULL: DENSE heads packed in token order by
  *        saf3r_pack_qkv (the flag is an error on any other pattern). Their key and query tiles
  *        then cover the F*T tokens without padding.
+ *   flags: 0 or SAF3R_ATTN_FIXED_ORDER. Without it, every key walk starts at the position the
+ *        device's wall clock divided by the walk's step time points to, so that the work-groups
+ *        resident at one moment read nearby key tiles (cache reuse); the summation order, and so the
+ *        last bits of the output, then vary from run to run (always within the bf16 tolerance).
+ *        With it, every walk starts at its first tile and the output is run-to-run identical.
+ *   pace, pace_seq: the walks' step times. pace is NULL (default step times) or a caller-owned
+ *        device array of 12 uint64, zero-filled once and passed to every call, with pace_seq
+ *        counting the calls (0, 1, 2, ...): each call measures its walks' mean step time into the
+ *        array and the next call starts its walks from that measurement. Calls on other streams that
+ *        share one array only disturb the measurement, never results. Ignored with FIXED_ORDER.
  * Replaces: the per-head loop saf3r/patch/wrapper.py:94-106 and the mode implementations of
  *           saf3r/patch/sparse_attention.py:12-90 for full / global_to_frame / all_to_first / skip /
  *           stride / q_probe_topk (over their key sets) / broadcast_first, the dense special rows of
@@ -248,7 +263,8 @@ int saf3r_sparse_attn_fwd(const void* q_packed, const void* k_packed, const void
                           const int32_t* sel, int sel_width, float scale, void* out, int64_t out_row_stride,
                           const void* keyset_k, const void* keyset_v, const int32_t* keyset_count,
                           int64_t keyset_capacity, const void* bcast_q, const void* bcast_k,
-                          const void* bcast_v, const uint8_t* token_order, void* stream);
+                          const void* bcast_v, const uint8_t* token_order, int flags, unsigned long long* pace,
+                          unsigned int pace_seq, void* stream);
 
 /*
  * Gather attention: out[r] = sum_j softmax_j(q[r] . k[idx[r][j]] * scale) v[idx[r][j]], fp32

@@ -59,8 +59,12 @@ struct AttnParams {
   int sel_width;
   float c;  // softmax scale * log2(e)
   uint32_t nsmagic;  // ceil(2^32 / ns): frame of a special slot = umulhi(slot, nsmagic); 0 for ns <= 1
-  uint64_t phase_dense;  // wall-clock ticks per key-tile step of a dense walk (0: fixed order)
-  uint64_t phase_split;  // wall-clock ticks per list position of a split-mode wave (0: fixed order)
+  uint64_t phase_dense;  // default wall-clock ticks per key-tile step of a dense walk (0: fixed order)
+  uint64_t phase_split;  // default wall-clock ticks per list position of a split-mode wave (0: fixed order)
+  unsigned long long* pace;  // caller's pacing state [2 kinds][3 slots][ticks, steps] (may be null)
+  int pace_read;             // slot measured by the previous call: its step time paces this launch
+  int pace_acc;              // slot this launch's walks add their (ticks, steps) to
+  int pace_zero;             // slot cleared for the next call
   const __bf16* kc;      // KEYSET heads: compact K [set][cap][64]
   const __bf16* vc;      // KEYSET heads: compact transposed V tiles [set][cap/64][64][64]
   const int32_t* ks_count;
@@ -494,10 +498,42 @@ __device__ inline void store_rows(const AttnParams& p, const Acc& A, const int64
   }
 }
 
+// ---- walk pacing ------------------------------------------------------------------------------
+// A walk starts at the position the wall clock divided by the step time points to. The step time of
+// walk kind k (0: single-range walks, 1: split-mode waves) is the mean measured by the previous call:
+// finishing walks add their elapsed ticks and steps to the caller's pace state (slot pace_acc), the
+// next call reads them (slot pace_read) and clears the slot the call after it accumulates into.
+// Reads and updates are vector atomics through L2; the state only steers walk starts, never results.
+constexpr uint64_t kPaceMinSteps = 256;  // measured steps below this: use the default step time
+constexpr int kPaceMinWalk = 16;         // walks shorter than this do not contribute
+#ifndef SAF3R_PACE_SCALE_PCT
+#define SAF3R_PACE_SCALE_PCT 100         // phase = measured mean step time * this / 100
+#endif
+
+__device__ inline uint64_t pace_phase(const AttnParams& p, int kind) {
+  const uint64_t def = kind ? p.phase_split : p.phase_dense;
+  if (!p.pace) return def;
+  unsigned long long* s = p.pace + kind * 6 + p.pace_read * 2;
+  const uint64_t ticks = __hip_atomic_load(s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const uint64_t steps = __hip_atomic_load(s + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (steps < kPaceMinSteps) return def;
+  const uint64_t ph = ticks * SAF3R_PACE_SCALE_PCT / (steps * 100);
+  return ph > 0 ? ph : 1;
+}
+
+__device__ inline void pace_add(const AttnParams& p, int kind, uint64_t t0, int steps) {
+  if (!p.pace || steps < kPaceMinWalk) return;
+  const uint64_t dt = __builtin_amdgcn_s_memrealtime() - t0;
+  unsigned long long* s = p.pace + kind * 6 + p.pace_acc * 2;
+  __hip_atomic_fetch_add(s, (unsigned long long)dt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_fetch_add(s + 1, (unsigned long long)steps, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
   __shared__ __align__(16) char ring[kRing];
   __shared__ int list[kMaxList];
   __shared__ int wcnt[4];
+  __shared__ uint64_t t_start;
 
   const Geom& g = p.g;
   // the id builtins, not threadIdx / blockIdx: in a kernel this large the latter stay calls, whose
@@ -507,6 +543,10 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
   const int lane = tid & 63, half = lane >> 5, col = lane & 31;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, uniform
   const int bid = __builtin_amdgcn_workgroup_id_x();
+  if (bid == 0 && tid < 4 && p.pace) {  // the slot the next call accumulates into starts at zero
+    unsigned long long* z = p.pace + (tid >> 1) * 6 + p.pace_zero * 2 + (tid & 1);
+    __hip_atomic_store(z, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
 
   // ---- decode the work item (uniform) ----
   int oh = 0;
@@ -682,9 +722,15 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
     }
     const int count = wk.count;
     int rot = 0;
-    if (eff == SAF3R_DENSE && p.phase_dense > 0 && count > 0) {
-      // one clock reading per work-group: the four waves share the ring and must agree
-      if (tid == 0) wcnt[0] = (int)((__builtin_amdgcn_s_memrealtime() / p.phase_dense) % (uint64_t)count);
+    const bool paced = eff == SAF3R_DENSE && p.phase_dense > 0 && count > 0;
+    if (paced) {
+      // one clock reading per work-group: the four waves share the ring and must agree; the start
+      // time waits in LDS for the pace update at the end (no registers held through the walk)
+      if (tid == 0) {
+        const uint64_t t = __builtin_amdgcn_s_memrealtime();
+        t_start = t;
+        wcnt[0] = (int)((t / pace_phase(p, 0)) % (uint64_t)count);
+      }
       __syncthreads();
       rot = __builtin_amdgcn_readfirstlane(wcnt[0]);  // an LDS value, uniform: keep the walk scalar
     }
@@ -837,6 +883,7 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
           A.o[dh][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[j][dh], pc[1][j], A.o[dh][1], 0, 0, 0);
         }
       if (!rel_patch) {
+        if (tid == 0 && paced) pace_add(p, 0, t_start, cnt);
         store(A);
         return;
       }
@@ -906,7 +953,11 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
     // frames together
     const int nw = total > w ? (total - w + 3) >> 2 : 0;
     int i0 = 0;
-    if (p.phase_split > 0 && nw > 0) i0 = (int)((__builtin_amdgcn_s_memrealtime() / p.phase_split) % (uint64_t)nw);
+    uint64_t t_split = 0;
+    if (p.phase_split > 0 && nw > 0) {
+      t_split = __builtin_amdgcn_s_memrealtime();
+      i0 = (int)((t_split / pace_phase(p, 1)) % (uint64_t)nw);
+    }
     i0 = __builtin_amdgcn_readfirstlane(i0);
     auto entry = [&](int i) {
       int ii = i + i0;
@@ -1035,6 +1086,7 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
         e1 = e2;
         e2 = ent(t + 3);
       }
+      if (lane == 0 && t_split) pace_add(p, 1, t_split, nw);
       // PV of the last block's second half
       wait_vm<0>();
       load_vh(slots + 8192 + 4096, vf);
@@ -1161,31 +1213,22 @@ static int head_segments(int h, int pat, bool tokord, int ntt, const Geom& g, in
   return n;
 }
 
-// Clock phases of the key walks. Defaults come from sweeps at the 128-frame VGGT shape (dense
-// walks hardly depend on it). The split value sits at the long end of the plateau of best
-// block-dynamic throughput and L2 reuse (2100-2250 ns on a fast device, 2200-2300 ns on a slower
-// one): a phase shorter than the walk's real step time scatters the work-groups over the key frames
-// (-8% at 2100 ns on the slower device), a longer one costs little; SAF3R_ATTN_PHASE="off" keeps the fixed walk order
-// (run-to-run identical output), and SAF3R_ATTN_PHASE="<dense ns>,<split ns>" overrides them.
-static void set_phase(AttnParams* p) {
-  double dense_ns = 2600.0, split_ns = 2250.0;
-  if (const char* e = getenv("SAF3R_ATTN_PHASE")) {
-    if (strcmp(e, "off") == 0) dense_ns = split_ns = 0.0;
-    else if (sscanf(e, "%lf,%lf", &dense_ns, &split_ns) != 2) dense_ns = split_ns = 0.0;
-  }
-  static int rate_khz[64];  // per device; 0 = not queried yet, -1 = unavailable
+// Default step times of the key walks (the first call on a pace state, or without one), from sweeps
+// at the 128-frame VGGT shape: the split value sits at the long end of the plateau of best
+// block-dynamic throughput (a phase shorter than the walk's real step time scatters the work-groups
+// over the key frames, a longer one costs little). Converted to wall-clock ticks with the device's
+// clock rate, queried on every call (no cached state).
+static void set_phase(AttnParams* p, bool fixed_order) {
+  p->phase_dense = p->phase_split = 0;
+  if (fixed_order) return;
+  const double dense_ns = 2600.0, split_ns = 2250.0;
   int dev = 0, khz = 0;
-  if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64) {
-    if (rate_khz[dev] == 0) {
-      int r = 0;
-      rate_khz[dev] = hipDeviceGetAttribute(&r, hipDeviceAttributeWallClockRate, dev) == hipSuccess && r > 0 ? r : -1;
-    }
-    khz = rate_khz[dev] > 0 ? rate_khz[dev] : 0;
-  }
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev) != hipSuccess ||
+      khz <= 0)
+    return;  // no wall clock: fixed order
   const double ticks_per_ns = khz * 1e-6;
-  p->phase_dense = dense_ns > 0.0 ? (uint64_t)fmax(1.0, dense_ns * ticks_per_ns) : 0;
-  p->phase_split = split_ns > 0.0 ? (uint64_t)fmax(1.0, split_ns * ticks_per_ns) : 0;
-  if (khz == 0) p->phase_dense = p->phase_split = 0;
+  p->phase_dense = (uint64_t)fmax(1.0, dense_ns * ticks_per_ns);
+  p->phase_split = (uint64_t)fmax(1.0, split_ns * ticks_per_ns);
 }
 
 }  // namespace saf3r
@@ -1198,7 +1241,7 @@ extern "C" int saf3r_sparse_attn_fwd(const void* q_packed, const void* k_packed,
                                      void* out, int64_t out_row_stride, const void* keyset_k, const void* keyset_v,
                                      const int32_t* keyset_count, int64_t keyset_capacity, const void* bcast_q,
                                      const void* bcast_k, const void* bcast_v, const uint8_t* token_order,
-                                     void* stream) {
+                                     int flags, unsigned long long* pace, unsigned int pace_seq, void* stream) {
   if (int e = injected("saf3r_sparse_attn_fwd")) return e;
   AttnParams p;
   if (!make_geom(frames, tokens_per_frame, num_special, &p.g))
@@ -1273,7 +1316,14 @@ extern "C" int saf3r_sparse_attn_fwd(const void* q_packed, const void* k_packed,
     return fail(SAF3R_ERR_UNSUPPORTED, "saf3r_sparse_attn_fwd: too many special tokens");
   // ceil(2^32 / ns) fits 32 bits for ns >= 2 only: ns = 1 is magic 0, which the kernel tests for
   p.nsmagic = p.g.ns > 1 ? (uint32_t)((0x100000000ull + (uint64_t)p.g.ns - 1) / (uint64_t)p.g.ns) : 0u;
-  set_phase(&p);
+  if (flags & ~SAF3R_ATTN_FIXED_ORDER) return fail(SAF3R_ERR_INVALID, "saf3r_sparse_attn_fwd: unknown flags 0x%x", flags);
+  if ((uintptr_t)pace % 8) return fail(SAF3R_ERR_INVALID, "saf3r_sparse_attn_fwd: pace must be 8-byte aligned");
+  const bool fixed = (flags & SAF3R_ATTN_FIXED_ORDER) != 0;
+  set_phase(&p, fixed);
+  p.pace = fixed ? nullptr : pace;
+  p.pace_read = (int)(pace_seq % 3u);
+  p.pace_acc = (int)((pace_seq + 1u) % 3u);
+  p.pace_zero = (int)((pace_seq + 2u) % 3u);
   Seg segs[kMaxSegs];
   int nseg = 0;
   for (int h = 0; h < num_heads; ++h)

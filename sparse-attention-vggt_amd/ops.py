@@ -23,11 +23,42 @@ PATTERN_NAMES = {
     BLOCK_DYNAMIC: "block_topk", TOKEN_DYNAMIC: "dino_topk", ANCHOR: "all_to_first", SKIP: "skip",
     KEYSET: "keyset", BROADCAST: "broadcast_first", TOKEN_DYNAMIC_KEYSET: "dino_topk_strided",
 }
+FIXED_ORDER = 1  # saf3r_attn_flags
 KEYSET_PATTERNS = (KEYSET, TOKEN_DYNAMIC_KEYSET)  # heads served from the key-set buffers
 TOKEN_PATTERNS = (TOKEN_DYNAMIC, TOKEN_DYNAMIC_KEYSET)  # heads whose patch rows gather-attend est_topk_idx
 
 
 _recorder = None
+
+# Key-walk order of saf3r_sparse_attn_fwd: "paced" (walks start where the measured step time and the
+# wall clock point, for cache reuse; the last output bits vary run to run) or "fixed" (every walk from
+# its first tile: run-to-run identical output).
+_walk_order = "paced"
+_pace_state = {}  # device index -> [int64 tensor of 12 (the library's pacing state), call counter]
+
+
+def set_walk_order(order: str) -> None:
+    """Default key-walk order of ``sparse_attn_fwd``: "paced" or "fixed"."""
+    global _walk_order
+    if order not in ("paced", "fixed"):
+        raise ValueError(f"walk order {order!r}: 'paced' or 'fixed'")
+    _walk_order = order
+
+
+def walk_order() -> str:
+    return _walk_order
+
+
+def _pace(device):
+    """(pointer, sequence number) of the per-device pacing state; the counter advances per call."""
+    idx = torch.device(device).index or 0
+    st = _pace_state.get(idx)
+    if st is None:
+        st = [torch.zeros(12, dtype=torch.int64, device=device), 0]
+        _pace_state[idx] = st
+    seq = st[1]
+    st[1] = (seq + 1) & 0xFFFFFFFF
+    return st[0], seq
 
 
 def set_event_recorder(recorder) -> None:
@@ -210,11 +241,12 @@ def block_select(pooled_q: torch.Tensor, pooled_k: torch.Tensor, frames: int, bl
 def sparse_attn_fwd(qp, kp, vp, geom: Geometry, patterns: Sequence[int], sel: torch.Tensor | None = None,
                     scale: float | None = None, out: torch.Tensor | None = None,
                     keysets: "KeySets | None" = None, broadcast: "Broadcast | None" = None,
-                    token_order: Sequence[bool] | None = None) -> torch.Tensor:
+                    token_order: Sequence[bool] | None = None, order: str | None = None) -> torch.Tensor:
     """All heads in one launch. Returns (or fills) ``out`` bf16 [N, H*64] in natural token order.
     ``keysets`` carries the compact K/V of the KEYSET heads and ``broadcast`` the frame-0 / per-frame
     buffers of the BROADCAST heads (each in increasing head order); ``token_order`` flags the
-    DENSE heads that ``pack_qkv`` packed in token order."""
+    DENSE heads that ``pack_qkv`` packed in token order. ``order`` ("paced" / "fixed", default
+    ``walk_order()``) chooses the key-walk order (see ``set_walk_order``)."""
     _need_cuda(qp, kp, vp)
     lib = _lib.load()
     H = qp.shape[0]
@@ -252,11 +284,20 @@ def sparse_attn_fwd(qp, kp, vp, geom: Geometry, patterns: Sequence[int], sel: to
             raise ValueError(f"{n_bc} BROADCAST heads need {n_bc} gathered frame-0 / per-frame buffers")
         bq, bk, bv = broadcast.q, broadcast.k, broadcast.v
     pat = _i32_array(patterns)
+    order = _walk_order if order is None else order
+    if order == "fixed":
+        flags, pace, seq = FIXED_ORDER, None, 0
+    elif order == "paced":
+        flags = 0
+        pace, seq = _pace(qp.device)
+    else:
+        raise ValueError(f"walk order {order!r}: 'paced' or 'fixed'")
     _mark("sparse_attn", "start")
     _lib.check(lib.saf3r_sparse_attn_fwd(
         _ptr(qp), _ptr(kp), _ptr(vp), geom.frames, geom.tokens_per_frame, geom.num_special, H,
         pat, _ptr(sel), width, float(scale), _ptr(out), out.stride(0), _ptr(ks_k), _ptr(ks_v), _ptr(ks_n),
-        ks_cap, _ptr(bq), _ptr(bk), _ptr(bv), _u8_flags(token_order, H), _lib.stream_ptr()))
+        ks_cap, _ptr(bq), _ptr(bk), _ptr(bv), _u8_flags(token_order, H), flags, _ptr(pace), seq,
+        _lib.stream_ptr()))
     _mark("sparse_attn", "end")
     return out
 

@@ -192,14 +192,12 @@ def test_sparse_attention_token_order_dense(ops, pkg, F, T, ns):
         _check_close(got[h], ref, f"token order F{F} T{T} ns{ns} head {h} pattern {pat}")
 
 
-@pytest.mark.parametrize("phase", ["off", None])
-def test_sparse_attention_outrun_reference(ops, pkg, monkeypatch, phase):
+@pytest.mark.parametrize("phase", ["fixed", "paced"])
+def test_sparse_attention_outrun_reference(ops, pkg, phase):
     """Keys whose scores exceed the lazily moved reference maximum by more than 2^64 in P (and one
     beyond the fp32 exponent range) must take the exact path: rescale O and l, recompute P. Every
-    pattern must still match the oracle. With the walk phase off every walk starts at its first
+    pattern must still match the oracle. In the fixed walk order every walk starts at its first
     tile, so the outliers (last frame) are met late."""
-    if phase is not None:
-        monkeypatch.setenv("SAF3R_ATTN_PHASE", phase)
     geom = pkg.Geometry(3, 155, 5)
     patterns = [ops.DENSE, ops.DENSE, ops.BLOCK_DYNAMIC, ops.FRAME_LOCAL, ops.ANCHOR_LOCAL]
     H = len(patterns)
@@ -215,7 +213,7 @@ def test_sparse_attention_outrun_reference(ops, pkg, monkeypatch, phase):
     qp, kp, vp = ops.pack_heads(q.to(DEV), k.to(DEV), v.to(DEV), geom, token_order=flags)
     pq, pk = ops.block_pool(qp, kp, geom, [2])
     sel = ops.block_select(pq, pk, geom.frames, geom.blocks_per_frame, 2)
-    out = ops.sparse_attn_fwd(qp, kp, vp, geom, patterns, sel, token_order=flags)
+    out = ops.sparse_attn_fwd(qp, kp, vp, geom, patterns, sel, token_order=flags, order=phase)
     torch.cuda.synchronize()
     og = OA.Geometry(3, 155, 5)
     got = out.float().cpu().reshape(N, H, 64).permute(1, 0, 2)
@@ -224,6 +222,39 @@ def test_sparse_attention_outrun_reference(ops, pkg, monkeypatch, phase):
         ref = OA.sparse_attention_gathered(q[h].float(), k[h].float(), v[h].float(), pat, og,
                                            sel[0].cpu() if h == 2 else None, dtype=torch.float64)
         _check_close(got[h], ref, f"outrun phase={phase} head {h} pattern {pat}")
+
+
+def test_walk_order_paced_and_fixed(ops, pkg):
+    """The paced walk order (the product default: walks start where the measured step time and the
+    wall clock point) matches the oracle on every pattern over repeated calls, whose pace state
+    carries a measured step time from the second call on; the fixed order is bitwise reproducible."""
+    geom = pkg.Geometry(24, 1374, 5)
+    patterns = [ops.DENSE, ops.BLOCK_DYNAMIC, ops.FRAME_LOCAL, ops.ANCHOR_LOCAL, ops.BLOCK_DYNAMIC, ops.DENSE]
+    H = len(patterns)
+    q, k, v = _qkv(H, geom.tokens, seed=99, scale=1.5)
+    flags = ops.token_order_heads(patterns)
+    qp, kp, vp = ops.pack_heads(q.to(DEV), k.to(DEV), v.to(DEV), geom, token_order=flags)
+    dyn = [1, 4]
+    pq, pk = ops.block_pool(qp, kp, geom, dyn)
+    sel = ops.block_select(pq, pk, geom.frames, geom.blocks_per_frame, 4)
+    outs = [ops.sparse_attn_fwd(qp, kp, vp, geom, patterns, sel, token_order=flags, order="paced").clone()
+            for _ in range(4)]
+    fixed = [ops.sparse_attn_fwd(qp, kp, vp, geom, patterns, sel, token_order=flags, order="fixed").clone()
+             for _ in range(2)]
+    torch.cuda.synchronize()
+    assert torch.equal(fixed[0], fixed[1])
+    pace = ops._pace_state[0][0].cpu()
+    assert int(pace[1::2].sum()) > 0  # the walks measured their step times
+    og = OA.Geometry(geom.frames, geom.tokens_per_frame, geom.num_special)
+    rows = torch.cat([torch.arange(0, 200), torch.arange(geom.tokens - 1500, geom.tokens, 7),
+                      torch.randint(0, geom.tokens, (300,), generator=torch.Generator().manual_seed(1))])
+    for h, pat in enumerate(patterns):
+        s = sel[dyn.index(h)].cpu() if h in dyn else None
+        m = OA.allowed_mask(pat, rows, og, s)
+        ref = OA.masked_attention(q[h][rows].float(), k[h].float(), v[h].float(), m)
+        for i, o in enumerate(outs + fixed):
+            got = o[rows.to(DEV)].float().cpu().reshape(len(rows), H, 64)[:, h]
+            _check_close(got, ref, f"walk order call {i} head {h} pattern {pat}")
 
 
 def test_sparse_attention_selection_edge_cases(ops, pkg):
