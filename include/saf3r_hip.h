@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define SAF3R_ABI_VERSION 6
+#define SAF3R_ABI_VERSION 7
 
 enum saf3r_status {
   SAF3R_OK = 0,
@@ -112,6 +112,11 @@ int64_t saf3r_packed_slots(int frames, int tokens_per_frame, int num_special);
  *   token_order: host uint8 [num_heads] or NULL. A head h < 64 with token_order[h] != 0 is packed
  *            in token order instead: slot t holds token t (t < F*T), no special or per-frame
  *            padding (the layout saf3r_sparse_attn_fwd reads for a DENSE head flagged the same way).
+ *   fp32_heads: host uint8 [num_heads] or NULL. Heads h < 64 flagged here also get their fp32 q and k
+ *            (after LayerNorm and RoPE, before the bf16 rounding) in qk32: the s-th flagged head (in
+ *            increasing head order) at qk32[((s*2 + 0|1) * F*T + t) * 64 + d] for q|k of token t.
+ *            (Under autocast the reference keeps q/k in fp32 after LayerNorm/RoPE; its q_probe_topk
+ *            mean / scores and its dino_topk gather read those fp32 values.)
  * Replaces: saf3r/patch/patch_vggt.py:577-583 (qkv reshape, q_norm/k_norm, rope) and
  *           saf3r/models/official_vggt/layers/rope.py:154-188.
  */
@@ -120,7 +125,8 @@ int saf3r_pack_qkv(const void* q, const void* k, const void* v, int64_t tok_stri
                    const float* q_ln_weight, const float* q_ln_bias, const float* k_ln_weight,
                    const float* k_ln_bias, float ln_eps, int apply_ln,
                    const int32_t* pos, const float* rope_cos, const float* rope_sin, int rope_positions,
-                   void* q_packed, void* k_packed, void* v_packed, const uint8_t* token_order, void* stream);
+                   void* q_packed, void* k_packed, void* v_packed, const uint8_t* token_order,
+                   const uint8_t* fp32_heads, float* qk32, void* stream);
 
 /*
  * Pooled patch-block means (fp32) of the packed Q and K of the listed heads.
@@ -160,23 +166,23 @@ int saf3r_block_select(const float* pooled_q, const float* pooled_k, int n, int 
                        int blocks_per_frame, int k, int scope, int32_t* idx, void* stream);
 
 /*
- * Mean query and probe scores of the q_probe_topk key set, for n_sel heads (head_ids, device
- * int32) of the packed Q/K.
- *   sample_idx: device int32 [n_samples] token ids in [0, N) (entries outside are clamped), or NULL
- *               for every token (n_samples ignored). The reference's q_sample_ratio < 1 samples
- *               torch.linspace(0, N-1, n).long() tokens; the caller passes that list.
- *   qbar[s][d]: mean over the sampled rows (all N = frames*tokens_per_frame tokens without a list):
- *               chunks of ceil(M/256) rows (M rows in list order) summed sequentially, chunk sums
- *               added in order, one division by M.
- *   scores[s][t] (row stride scores_stride >= N, token order): sequential fmaf over d of
+ * Mean query and probe scores of the q_probe_topk key set, for n_sel heads, from their fp32 q / k
+ * rows (the saf3r_pack_qkv qk32 rows: row t of slot s at q32 + s*slot_stride + 64 t, k32 likewise).
+ *   slots: device int32 [n_sel]; n_tokens: rows per slot (F*T); slot_stride >= 64 * n_tokens.
+ *   sample_idx: device int32 [n_samples] token ids in [0, n_tokens) (entries outside are clamped),
+ *               or NULL for every token (n_samples ignored). The reference's q_sample_ratio < 1
+ *               samples torch.linspace(0, N-1, n).long() tokens; the caller passes that list.
+ *   qbar[s][d]: mean over the sampled rows (all tokens without a list): chunks of ceil(M/256) rows
+ *               (M rows in list order) summed sequentially, chunk sums added in order, one division
+ *               by M.
+ *   scores[s][t] (row stride scores_stride >= n_tokens, token order): sequential fmaf over d of
  *               qbar[d] * k[t][d], times scale (1/8 for head_dim 64).
  *   partial: device workspace of n_sel * 256 * 64 floats.
- * Replaces: saf3r/patch/sparse_attention.py:150-168 (query sampling, q_bar and the probe scores).
+ * Replaces: saf3r/patch/sparse_attention.py:150-168 (query sampling, q_bar and the fp32 probe scores).
  */
-int saf3r_probe_scores(const void* q_packed, const void* k_packed, int frames, int tokens_per_frame,
-                       int num_special, const int32_t* head_ids, int n_sel, const int32_t* sample_idx,
-                       int n_samples, float scale, float* partial, float* qbar, float* scores,
-                       int64_t scores_stride, void* stream);
+int saf3r_probe_scores(const float* q32, const float* k32, int64_t slot_stride, int n_tokens, const int32_t* slots,
+                       int n_sel, const int32_t* sample_idx, int n_samples, float scale, float* partial,
+                       float* qbar, float* scores, int64_t scores_stride, void* stream);
 
 /*
  * saf3r_probe_scores without the workspace argument: it allocates nothing (no hipMalloc / hipFree,
@@ -187,10 +193,9 @@ int saf3r_probe_scores(const void* q_packed, const void* k_packed, int frames, i
  * the current device and is shared by every call on it: calls that overlap on one GPU (other streams,
  * other host threads) race. No counterpart in the reference.
  */
-int saf3r_probe_scores_noalloc(const void* q_packed, const void* k_packed, int frames, int tokens_per_frame,
-                               int num_special, const int32_t* head_ids, int n_sel, const int32_t* sample_idx,
-                               int n_samples, float scale, float* qbar, float* scores, int64_t scores_stride,
-                               void* stream);
+int saf3r_probe_scores_noalloc(const float* q32, const float* k32, int64_t slot_stride, int n_tokens,
+                               const int32_t* slots, int n_sel, const int32_t* sample_idx, int n_samples,
+                               float scale, float* qbar, float* scores, int64_t scores_stride, void* stream);
 
 /*
  * Shared key sets of n_heads heads (device int32 arrays of n_heads entries each):
@@ -268,13 +273,15 @@ int saf3r_sparse_attn_fwd(const void* q_packed, const void* k_packed, const void
 
 /*
  * Gather attention: out[r] = sum_j softmax_j(q[r] . k[idx[r][j]] * scale) v[idx[r][j]], fp32
- * accumulation, bf16 in/out, head_dim 64; idx entries < 0 or >= num_keys are skipped.
+ * accumulation, head_dim 64; idx entries < 0 or >= num_keys are skipped.
+ *   q, k: bf16 rows, or fp32 rows with qk_fp32 = 1 (row strides in elements of that type);
+ *   v, out: bf16 rows.
  *   idx: int32 [n][topk] (row stride topk, or 0 to share one list across rows).
  * Replaces: saf3r/triton/sparse_topk_attention.py:115-166 (fused_sparse_topk_attention) and
  *           :261-286 (the TopK > 2048 variant).
  */
 int saf3r_gather_attn_fwd(const saf3r_rows* q, const saf3r_rows* k, const saf3r_rows* v, const int32_t* idx,
-                          int64_t idx_row_stride, int n, int topk, int64_t num_keys, float scale,
+                          int64_t idx_row_stride, int n, int topk, int64_t num_keys, float scale, int qk_fp32,
                           const saf3r_rows* out, void* stream);
 
 /*

@@ -167,12 +167,13 @@ def gather_attention(q, k, v, idx, scale=None, dtype=torch.float32):
 
 
 def token_dynamic_attention(q, k, v, est_topk_idx, g: Geometry, sp2sp_stride=1, dtype=torch.float64,
-                            spec_keys=None):
+                            spec_keys=None, gather_qk=None):
     """Reference ``dino_topk_attention`` (``saf3r/patch/sparse_attention.py:189-231``).
 
     Special rows attend keys 0, s, 2s, ... (s = ``sp2sp_stride``; or the token list ``spec_keys``);
     image rows attend the image tokens ``est_topk_idx[i]`` (indices into the image-token list) and
-    never special keys.
+    never special keys. ``gather_qk`` = (q, k) gives the image rows' gather its own q / k (the fp32
+    values the reference's gather kernel reads under autocast); by default it uses ``q`` / ``k``.
     """
     frame, special, _ = token_info(g)
     out = torch.empty(g.tokens, v.shape[1], dtype=dtype)
@@ -181,7 +182,8 @@ def token_dynamic_attention(q, k, v, est_topk_idx, g: Geometry, sp2sp_stride=1, 
     m = torch.ones(len(spec), len(keys), dtype=torch.bool)
     out[spec] = masked_attention(q[spec], k[keys], v[keys], m, dtype=dtype)
     img = image_token_ids(g)
-    out[img] = gather_attention(q[img], k[img], v[img], est_topk_idx, dtype=dtype)
+    gq, gk = (q, k) if gather_qk is None else gather_qk
+    out[img] = gather_attention(gq[img], gk[img], v[img], est_topk_idx, dtype=dtype)
     return out
 
 
@@ -311,15 +313,17 @@ def qkv_prologue(qkv: torch.Tensor, num_heads: int, ln_q, ln_k, pos, eps=1e-5, r
 
 
 def head_outputs(q, k, v, patterns, g: Geometry, sel_by_head=None, est_topk_idx=None,
-                 dtype=torch.float32, gathered=True):
-    """Per-head attention of a layer: q/k/v [H, N, d] -> [H, N, d]."""
+                 dtype=torch.float32, gathered=True, gather_qk_by_head=None):
+    """Per-head attention of a layer: q/k/v [H, N, d] -> [H, N, d]. ``gather_qk_by_head`` {h: (q, k)}
+    gives the image-row gather of token-dynamic heads its own q / k."""
     outs = []
     for h, pat in enumerate(patterns):
         sel = None if sel_by_head is None else sel_by_head.get(h)
+        gqk = None if gather_qk_by_head is None else gather_qk_by_head.get(h)
         if pat == TOKEN_DYNAMIC:
-            o = token_dynamic_attention(q[h], k[h], v[h], est_topk_idx, g, dtype=dtype)
+            o = token_dynamic_attention(q[h], k[h], v[h], est_topk_idx, g, dtype=dtype, gather_qk=gqk)
         elif pat == TOKEN_DYNAMIC_KEYSET:  # sel: the special rows' key list
-            o = token_dynamic_attention(q[h], k[h], v[h], est_topk_idx, g, dtype=dtype, spec_keys=sel)
+            o = token_dynamic_attention(q[h], k[h], v[h], est_topk_idx, g, dtype=dtype, spec_keys=sel, gather_qk=gqk)
         elif pat == BROADCAST:
             o = broadcast_attention(q[h], k[h], v[h], g, dtype=dtype)
         elif gathered:
@@ -328,3 +332,126 @@ def head_outputs(q, k, v, patterns, g: Geometry, sel_by_head=None, est_topk_idx=
             o = pattern_attention(q[h], k[h], v[h], pat, g, sel, dtype=dtype)
         outs.append(o)
     return torch.stack(outs)
+
+
+# ----------------------------------------------------------------------------------------
+# The patched layer at the reference's own rounding points (autocast bf16)
+# ----------------------------------------------------------------------------------------
+
+def _bf16(x):
+    return x.to(torch.bfloat16).to(torch.float64)
+
+
+def reference_layer(x, w_qkv, b_qkv, ln_q, ln_k, w_proj, b_proj, pos, head_cfg, g: Geometry, lazy_topk: int = 4,
+                    eps: float = 1e-5, rope_base: float = 100.0, est_topk_idx=None):
+    """One patched global layer computed the way the reference computes it under ``autocast(bf16)``
+    (``saf3r/patch/patch_vggt.py:575-590``, ``saf3r/patch/wrapper.py:94-106``,
+    ``saf3r/patch/sparse_attention.py:12-273``), in fp64 with the reference's rounding points:
+
+    - qkv and proj Linear layers: bf16 inputs and weights, result rounded to bf16;
+    - q/k LayerNorm and RoPE in fp32 (autocast runs layer_norm in fp32; RoPE keeps the token dtype);
+    - SDPA modes (full, global_to_frame, all_to_first, stride, the q_probe_topk attention, the special
+      rows of dino_topk) attend on bf16-rounded q/k/v (autocast casts SDPA inputs);
+    - q_probe_topk: mean query and probe scores from the fp32 q/k (``:160-166``), rounded to fp32;
+      top-k ties to the lower token;
+    - dino_topk image rows: the gather kernel reads the fp32 q/k and the bf16 v
+      (``saf3r/triton/sparse_topk_attention.py:74-80``);
+    - lazy dino indices: per-frame top-``lazy_topk`` of bf16 q . bf16 k of the first correspondence head
+      (``fused_qk_topk.py:175-176``), ties to the lower key;
+    - broadcast_first: bf16 matmuls, fp32 softmax (``:110-131``);
+    - the head outputs are rounded to bf16 before the projection.
+
+    x [N, C] (bf16 values), head_cfg: one dict per head. Returns (y [N, C] fp64, info) where info
+    holds the key sets ({head: token list}) and the lazy indices used."""
+    with torch.no_grad():
+        return _reference_layer(x, w_qkv, b_qkv, ln_q, ln_k, w_proj, b_proj, pos, head_cfg, g, lazy_topk, eps,
+                                rope_base, est_topk_idx)
+
+
+def _reference_layer(x, w_qkv, b_qkv, ln_q, ln_k, w_proj, b_proj, pos, head_cfg, g, lazy_topk, eps, rope_base,
+                     est_topk_idx):
+    N, C = x.shape
+    H = len(head_cfg)
+    d = C // H
+    xd = _bf16(x.float())
+    qkv = _bf16(xd @ _bf16(w_qkv.float()).T + _bf16(b_qkv.float()))
+    qkv = qkv.reshape(N, 3, H, d).permute(1, 2, 0, 3)  # [3, H, N, d]
+    q32 = torch.nn.functional.layer_norm(qkv[0], (d,), ln_q[0].double(), ln_q[1].double(), eps).float()
+    k32 = torch.nn.functional.layer_norm(qkv[1], (d,), ln_k[0].double(), ln_k[1].double(), eps).float()
+    if pos is not None:
+        q32 = rope2d(q32, pos, rope_base)
+        k32 = rope2d(k32, pos, rope_base)
+    v = qkv[2]  # bf16 values in fp64
+    qb, kb = _bf16(q32), _bf16(k32)
+    scale = 1.0 / math.sqrt(d)
+    T, F = g.tokens_per_frame, g.frames
+    info = {"keysets": {}, "est_topk_idx": est_topk_idx}
+    img = image_token_ids(g)
+    _, special, _ = token_info(g)
+    spec = special.nonzero().flatten()
+
+    def sdpa(rows, keys, h):
+        s = (qb[h][rows] @ kb[h][keys].T) * scale
+        return torch.softmax(s, dim=-1) @ v[h][keys]
+
+    if est_topk_idx is None:
+        first = next((h for h, c in enumerate(head_cfg) if c["mode"] == "dino_topk" and c.get("is_first_dino")), None)
+        if first is not None:
+            s = (qb[first][img] @ kb[first][img].T).float().numpy()
+            from . import selection as OS
+            info["est_topk_idx"] = torch.from_numpy(OS.frame_topk(s, F, lazy_topk))
+    outs = []
+    for h, cfg in enumerate(head_cfg):
+        mode = cfg["mode"]
+        o = torch.empty(N, d, dtype=torch.float64)
+        if mode == "full":
+            o = sdpa(slice(0, N), slice(0, N), h)
+        elif mode == "skip":
+            o = torch.zeros(N, d, dtype=torch.float64)
+        elif mode == "global_to_frame":
+            for f in range(F):
+                r = slice(f * T, (f + 1) * T)
+                o[r] = sdpa(r, r, h)
+        elif mode == "all_to_first":
+            o = sdpa(slice(0, N), slice(0, T), h)
+        elif mode == "broadcast_first":
+            a = torch.softmax(_bf16((qb[h][:T] @ kb[h][:T].T) * scale).float(), dim=-1).double()
+            o = _bf16(_bf16(a) @ v[h].reshape(F, T, d)).reshape(N, d)
+        elif mode in ("stride", "q_probe_topk"):
+            include = cfg.get("include_as", mode == "stride")
+            if mode == "stride":
+                st = int(cfg.get("stride", 4))
+                start = h % st if cfg.get("shift", False) else 0
+                sel = torch.arange(start, N, st)
+            else:
+                k_top = max(1, N // int(cfg["stride"])) if "stride" in cfg else min(int(cfg.get("topk", 1024)), N)
+                ratio = cfg.get("q_sample_ratio", 1)
+                rows = torch.arange(N)
+                if ratio < 1:
+                    rows = torch.linspace(0, N - 1, steps=max(1, int(N * ratio))).long()
+                qbar = q32[h][rows].double().mean(0).float().double()
+                scores = ((qbar @ k32[h].double().T) / math.sqrt(d)).float().double()
+                order = sorted(range(N), key=lambda t: (-float(scores[t]), t))
+                sel = torch.tensor(order[:k_top], dtype=torch.long)
+            if include:
+                sel = torch.cat([sel, torch.arange(T), spec])
+            keys = torch.unique(sel)
+            info["keysets"][h] = keys
+            o = sdpa(slice(0, N), keys, h)
+        elif mode == "dino_topk":
+            st = int(cfg.get("dino_sp2sp_stride", 1))
+            o[spec] = sdpa(spec, torch.arange(0, N, st), h)
+            idx = info["est_topk_idx"].long()
+            valid = idx >= 0
+            kk = k32[h][img].double()[idx.clamp(min=0)]  # [P, W, d] fp32 keys
+            s = torch.einsum("rd,rwd->rw", q32[h][img].double(), kk) * scale
+            s = s.masked_fill(~valid, float("-inf"))
+            p = torch.softmax(s, dim=-1)
+            o[img] = torch.einsum("rw,rwd->rd", p, v[h][img][idx.clamp(min=0)])
+        else:
+            raise ValueError(f"mode {mode!r} has no reference-semantics restatement")
+        outs.append(_bf16(o))
+    info["heads"] = torch.stack(outs)  # [H, N, d] head outputs (bf16 values) before the projection
+    attn = info["heads"].permute(1, 0, 2).reshape(N, C)
+    y = attn @ _bf16(w_proj.float()).T + _bf16(b_proj.float())
+    return y, info

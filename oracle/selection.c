@@ -178,18 +178,19 @@ int oracle_global_topk(const float* scores, int NQ, int NC, int k, int32_t* out)
 /* Tokens per partial sum of the mean query: the N tokens split into at most 256 chunks. */
 int oracle_probe_chunk(int N) { return (N + 255) / 256; }
 
-/* Mean query of one head. q: bf16 bits, natural token order, row stride `row_stride`.
- * For each feature: each chunk of R = oracle_probe_chunk(N) consecutive tokens is summed
- * sequentially (fp32 adds, token order), the chunk sums are added sequentially in chunk
+/* Mean query of one head. q: fp32 rows in the order the mean visits them (token order, or the
+ * sampled rows in list order), row stride `row_stride`.
+ * For each feature: each chunk of R = oracle_probe_chunk(N) consecutive rows is summed
+ * sequentially (fp32 adds, row order), the chunk sums are added sequentially in chunk
  * order, and the total is divided once by N. */
-void oracle_probe_mean(const uint16_t* q, int64_t row_stride, int N, int D, float* out) {
+void oracle_probe_mean(const float* q, int64_t row_stride, int N, int D, float* out) {
     const int R = oracle_probe_chunk(N);
     for (int d = 0; d < D; ++d) {
         float total = 0.0f;
         for (int c0 = 0; c0 < N; c0 += R) {
             float part = 0.0f;
             const int c1 = c0 + R < N ? c0 + R : N;
-            for (int t = c0; t < c1; ++t) part = part + bf16_to_f32(q[(int64_t)t * row_stride + d]);
+            for (int t = c0; t < c1; ++t) part = part + q[(int64_t)t * row_stride + d];
             total = total + part;
         }
         out[d] = total / (float)N;
@@ -197,12 +198,13 @@ void oracle_probe_mean(const uint16_t* q, int64_t row_stride, int N, int D, floa
 }
 
 /* Probe scores of one head: score[t] = (sequential fmaf over d of qbar[d] * k[t][d]) * scale,
- * with scale = 1/sqrt(D) (a power of two for D = 64, so the product is exact). */
-void oracle_probe_scores(const float* qbar, const uint16_t* k, int64_t row_stride, int N, int D, float scale,
+ * k fp32 rows in token order, with scale = 1/sqrt(D) (a power of two for D = 64, so the product
+ * is exact). */
+void oracle_probe_scores(const float* qbar, const float* k, int64_t row_stride, int N, int D, float scale,
                          float* out) {
     for (int t = 0; t < N; ++t) {
         float acc = 0.0f;
-        for (int d = 0; d < D; ++d) acc = fmaf(qbar[d], bf16_to_f32(k[(int64_t)t * row_stride + d]), acc);
+        for (int d = 0; d < D; ++d) acc = fmaf(qbar[d], k[(int64_t)t * row_stride + d], acc);
         out[t] = acc * scale;
     }
 }

@@ -148,19 +148,28 @@ def probe_chunk(n: int) -> int:
     return int(_load().oracle_probe_chunk(n))
 
 
-def probe_mean(q_bf16: np.ndarray) -> np.ndarray:
-    """Mean query of one head over all tokens; ``q_bf16`` uint16 [N, D] in token order."""
-    q = np.ascontiguousarray(q_bf16, dtype=np.uint16)
+def _as_f32_rows(x: np.ndarray) -> np.ndarray:
+    """fp32 rows from fp32 values or bf16 bit patterns (uint16, converted exactly)."""
+    x = np.asarray(x)
+    if x.dtype == np.uint16:
+        return bf16_to_f32(x)
+    return np.ascontiguousarray(x, dtype=np.float32)
+
+
+def probe_mean(q: np.ndarray) -> np.ndarray:
+    """Mean query of one head over the given rows [N, D] (fp32 values or bf16 bits), in row order."""
+    q = np.ascontiguousarray(_as_f32_rows(q))
     n, d = q.shape
     out = np.zeros(d, dtype=np.float32)
     _load().oracle_probe_mean(_ptr(q), d, n, d, _ptr(out))
     return out
 
 
-def probe_scores(qbar: np.ndarray, k_bf16: np.ndarray, scale: float | None = None) -> np.ndarray:
-    """score[t] = sequential-fmaf(qbar . k[t]) * scale (scale defaults to 1/sqrt(D))."""
+def probe_scores(qbar: np.ndarray, k: np.ndarray, scale: float | None = None) -> np.ndarray:
+    """score[t] = sequential-fmaf(qbar . k[t]) * scale (scale defaults to 1/sqrt(D)); k [N, D] fp32 values
+    or bf16 bits."""
     qb = np.ascontiguousarray(qbar, dtype=np.float32)
-    k = np.ascontiguousarray(k_bf16, dtype=np.uint16)
+    k = np.ascontiguousarray(_as_f32_rows(k))
     n, d = k.shape
     out = np.zeros(n, dtype=np.float32)
     sc = float(np.float32(1.0 / np.sqrt(d))) if scale is None else float(scale)

@@ -6,17 +6,18 @@
 //      shares one list across rows), :173-258 (online-softmax variant for TopK > 2048).
 // Here one wave owns one query row and walks its list in chunks of 64 keys (one key per lane)
 // with an fp32 online softmax, so any list length is handled by the same kernel. Entries < 0 or
-// >= num_keys are skipped.
+// >= num_keys are skipped. q and k are bf16 or fp32 rows (the reference's kernel upcasts either).
 #include "common.h"
 
 namespace saf3r {
 
 struct RowsDev {
-  const __bf16* ptr;
+  const void* ptr;
   int64_t row_stride, base_row, rows_per_frame, frame_row_stride;
-  __device__ inline const __bf16* row(int64_t r) const {
+  template <typename T = __bf16>
+  __device__ inline const T* row(int64_t r) const {
     int64_t f = r / rows_per_frame;
-    return ptr + (base_row + f * frame_row_stride + (r - f * rows_per_frame)) * row_stride;
+    return static_cast<const T*>(ptr) + (base_row + f * frame_row_stride + (r - f * rows_per_frame)) * row_stride;
   }
 };
 
@@ -40,17 +41,23 @@ __device__ inline float wave_sum(float x) {
   return x;
 }
 
-// 2 waves per workgroup, one query row per wave.
+// 2 waves per workgroup, one query row per wave. QK32: q and k rows are fp32 (the reference's gather
+// reads the fp32 q / k of the autocast forward and multiplies in fp32); otherwise bf16.
+template <bool QK32>
 __global__ __launch_bounds__(128) void gather_attn_kernel(GatherParams p) {
   __shared__ float red[2][64][65];
+  __shared__ __align__(16) float qs[2][64];
   const int lane = tid_x() & 63, w = tid_x() >> 6;
   const int64_t r = (int64_t)bid_x() * 2 + w;
   const bool active = r < p.n;
   const int64_t rr = active ? r : 0;
 
-  // q row, packed bf16 pairs, identical in every lane
+  // q row: bf16 pairs in registers, identical in every lane; fp32 in LDS (read as broadcasts)
   uint32_t qw[32];
-  {
+  if constexpr (QK32) {
+    qs[w][lane] = p.q.row<float>(rr)[lane];
+    __syncthreads();
+  } else {
     const u32x4* q4 = reinterpret_cast<const u32x4*>(p.q.row(rr));
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
@@ -74,21 +81,34 @@ __global__ __launch_bounds__(128) void gather_attn_kernel(GatherParams p) {
     float s = -__builtin_inff();
     uint32_t vw[32];
     if (id >= 0) {
-      const u32x4* k4 = reinterpret_cast<const u32x4*>(p.k.row(id));
       const u32x4* v4 = reinterpret_cast<const u32x4*>(p.v.row(id));
       float dot = 0.f;
+      if constexpr (QK32) {
+        const f32x4* k4 = reinterpret_cast<const f32x4*>(p.k.row<float>(id));
+        const f32x4* q4 = reinterpret_cast<const f32x4*>(qs[w]);
+#pragma unroll
+        for (int t = 0; t < 16; ++t) {
+          const f32x4 kx = k4[t], qx = q4[t];
+          dot = __builtin_fmaf(qx[0], kx[0], dot);
+          dot = __builtin_fmaf(qx[1], kx[1], dot);
+          dot = __builtin_fmaf(qx[2], kx[2], dot);
+          dot = __builtin_fmaf(qx[3], kx[3], dot);
+        }
+      }
 #pragma unroll
       for (int t = 0; t < 8; ++t) {
-        const u32x4 kx = k4[t];
         const u32x4 vx = v4[t];
-        // elements are copied to scalars before the bf16x2 bit_cast: a bit_cast applied directly to
-        // a vector element (kx[e]) was lowered to element 0 for every e by this compiler
-        const uint32_t kw[4] = {kx.x, kx.y, kx.z, kx.w};
+        if constexpr (!QK32) {
+          const u32x4 kx = reinterpret_cast<const u32x4*>(p.k.row(id))[t];
+          // elements are copied to scalars before the bf16x2 bit_cast: a bit_cast applied directly to
+          // a vector element (kx[e]) was lowered to element 0 for every e by this compiler
+          const uint32_t kw[4] = {kx.x, kx.y, kx.z, kx.w};
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const uint32_t kk = kw[e], qq = qw[4 * t + e];
-          dot = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, kk), __builtin_bit_cast(bf16x2, qq), dot,
-                                                false);
+          for (int e = 0; e < 4; ++e) {
+            const uint32_t kk = kw[e], qq = qw[4 * t + e];
+            dot = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, kk), __builtin_bit_cast(bf16x2, qq),
+                                                  dot, false);
+          }
         }
         vw[4 * t + 0] = vx.x;
         vw[4 * t + 1] = vx.y;
@@ -122,17 +142,17 @@ __global__ __launch_bounds__(128) void gather_attn_kernel(GatherParams p) {
   for (int j = 0; j < 64; ++j) o += red[w][j][lane];
   if (active) {
     const float inv = l_run > 0.f ? 1.0f / l_run : 0.f;
-    __bf16* orow = const_cast<__bf16*>(p.out.row(r));
+    __bf16* orow = const_cast<__bf16*>(p.out.row<__bf16>(r));
     orow[lane] = (__bf16)(o * inv);
   }
 }
 
-static bool to_dev(const saf3r_rows* s, RowsDev* d, const char* name) {
+static bool to_dev(const saf3r_rows* s, RowsDev* d, const char* name, bool fp32 = false) {
   if (!s || !s->ptr) return fail(SAF3R_ERR_INVALID, "saf3r_gather_attn_fwd: null %s", name), false;
-  if (s->row_stride % 8 || ((uintptr_t)s->ptr % 16) || s->rows_per_frame <= 0 || s->base_row < 0)
-    return fail(SAF3R_ERR_INVALID, "saf3r_gather_attn_fwd: %s must be 16-byte aligned, row stride %% 8, rows_per_frame > 0",
-                name), false;
-  d->ptr = (const __bf16*)s->ptr;
+  if (s->row_stride % (fp32 ? 4 : 8) || ((uintptr_t)s->ptr % 16) || s->rows_per_frame <= 0 || s->base_row < 0)
+    return fail(SAF3R_ERR_INVALID, "saf3r_gather_attn_fwd: %s must be 16-byte aligned, row stride %% %d, rows_per_frame > 0",
+                name, fp32 ? 4 : 8), false;
+  d->ptr = s->ptr;
   d->row_stride = s->row_stride;
   d->base_row = s->base_row;
   d->rows_per_frame = s->rows_per_frame;
@@ -146,10 +166,13 @@ using namespace saf3r;
 
 extern "C" int saf3r_gather_attn_fwd(const saf3r_rows* q, const saf3r_rows* k, const saf3r_rows* v,
                                      const int32_t* idx, int64_t idx_row_stride, int n, int topk,
-                                     int64_t num_keys, float scale, const saf3r_rows* out, void* stream) {
+                                     int64_t num_keys, float scale, int qk_fp32, const saf3r_rows* out,
+                                     void* stream) {
   if (int e = injected("saf3r_gather_attn_fwd")) return e;
   GatherParams p;
-  if (!to_dev(q, &p.q, "q") || !to_dev(k, &p.k, "k") || !to_dev(v, &p.v, "v") || !to_dev(out, &p.out, "out"))
+  if (qk_fp32 != 0 && qk_fp32 != 1) return fail(SAF3R_ERR_INVALID, "saf3r_gather_attn_fwd: qk_fp32 must be 0 or 1");
+  if (!to_dev(q, &p.q, "q", qk_fp32) || !to_dev(k, &p.k, "k", qk_fp32) || !to_dev(v, &p.v, "v") ||
+      !to_dev(out, &p.out, "out"))
     return SAF3R_ERR_INVALID;
   if (!idx || n < 0 || topk <= 0 || idx_row_stride < 0 || num_keys <= 0 || num_keys > 0x7fffffff)
     return fail(SAF3R_ERR_INVALID, "saf3r_gather_attn_fwd: bad index list");
@@ -160,6 +183,9 @@ extern "C" int saf3r_gather_attn_fwd(const saf3r_rows* q, const saf3r_rows* k, c
   p.topk = topk;
   p.nk = num_keys;
   p.c = scale * 1.4426950408889634f;
-  hipLaunchKernelGGL(gather_attn_kernel, dim3((unsigned)((n + 1) / 2)), dim3(128), 0, (hipStream_t)stream, p);
+  if (qk_fp32)
+    hipLaunchKernelGGL(gather_attn_kernel<true>, dim3((unsigned)((n + 1) / 2)), dim3(128), 0, (hipStream_t)stream, p);
+  else
+    hipLaunchKernelGGL(gather_attn_kernel<false>, dim3((unsigned)((n + 1) / 2)), dim3(128), 0, (hipStream_t)stream, p);
   return check_launch("saf3r_gather_attn_fwd");
 }

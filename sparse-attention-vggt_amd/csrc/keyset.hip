@@ -35,37 +35,29 @@ __device__ inline int64_t token_slot(const Geom& g, int64_t t) {
 }
 
 struct ProbeParams {
-  const __bf16* q;
-  const __bf16* k;
-  Geom g;
-  int n;       // tokens F * T
+  const float* q;  // fp32 q rows of slot s at q + s * slot_stride, token t at + 64 t
+  const float* k;  // fp32 k rows, same layout
+  int64_t slot_stride;
+  int n;       // tokens
   int n_samp;  // rows of the mean: every token (sample == nullptr) or the listed ones
   const int32_t* sample;
   int chunk;
   int nchunks;
-  const int32_t* head_ids;
-  float* partial;  // [n_sel][kProbeChunks][64]
-  float* qbar;     // [n_sel][64]
-  float* scores;   // [n_sel][scores_stride]
+  const int32_t* slots;  // [n_sel] slots of the selected heads
+  float* partial;        // [n_sel][kProbeChunks][64]
+  float* qbar;           // [n_sel][64]
+  float* scores;         // [n_sel][scores_stride]
   int64_t scores_stride;
   float scale;
 };
-
-// Packed slot of token t < 2^31 in 32-bit arithmetic (t and the slot are uniform in the callers).
-__device__ inline int64_t token_slot32(const Geom& g, int t) {
-  const int f = t / g.T, r = t - f * g.T;
-  if (r < g.ns) return (int64_t)f * g.ns + r;
-  return (int64_t)g.Sp + (int64_t)f * g.Pp + (r - g.ns);
-}
 
 // grid (nchunks, n_sel), 64 threads: feature d of chunk c, summed over the chunk's rows in order.
 // Rows are read 16 at a time (independent loads in flight) and added in order, so the sum is the
 // sequential one.
 __global__ __launch_bounds__(64) void probe_partial_kernel(ProbeParams p) {
   const int c = bid_x(), hs = bid_y(), d = tid_x();
-  const int h = p.head_ids[hs];
+  const float* base = p.q + (int64_t)p.slots[hs] * p.slot_stride + d;
   const int i0 = c * p.chunk, i1 = min(p.n_samp, i0 + p.chunk);
-  const __bf16* base = p.q + (int64_t)h * p.g.L * 64 + d;
   float acc = 0.f;
   int i = i0;
   for (; i + 16 <= i1; i += 16) {
@@ -73,14 +65,14 @@ __global__ __launch_bounds__(64) void probe_partial_kernel(ProbeParams p) {
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
       const int t = p.sample ? min(max(p.sample[i + j], 0), p.n - 1) : i + j;
-      x[j] = (float)base[token_slot32(p.g, t) * 64];
+      x[j] = base[(int64_t)t * 64];
     }
 #pragma unroll
     for (int j = 0; j < 16; ++j) acc = acc + x[j];
   }
   for (; i < i1; ++i) {
     const int t = p.sample ? min(max(p.sample[i], 0), p.n - 1) : i;
-    acc = acc + (float)base[token_slot32(p.g, t) * 64];
+    acc = acc + base[(int64_t)t * 64];
   }
   p.partial[((int64_t)hs * kProbeChunks + c) * 64 + d] = acc;
 }
@@ -96,21 +88,20 @@ __global__ __launch_bounds__(64) void probe_finish_kernel(ProbeParams p) {
 // grid (ceil(N / 256), n_sel), 256 threads: one token per thread
 __global__ __launch_bounds__(256) void probe_scores_kernel(ProbeParams p) {
   __shared__ float qb[64];
-  const int hs = bid_y(), h = p.head_ids[hs];
+  const int hs = bid_y();
   if (tid_x() < 64) qb[tid_x()] = p.qbar[hs * 64 + tid_x()];
   __syncthreads();
   const int t = bid_x() * 256 + tid_x();
   if (t >= p.n) return;
-  const u32x4* row = reinterpret_cast<const u32x4*>(p.k + ((int64_t)h * p.g.L + token_slot32(p.g, t)) * 64);
+  const f32x4* row = reinterpret_cast<const f32x4*>(p.k + (int64_t)p.slots[hs] * p.slot_stride + (int64_t)t * 64);
   float acc = 0.f;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const u32x4 w = row[j];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      acc = __builtin_fmaf(qb[8 * j + 2 * e], bf16_lo(w[e]), acc);
-      acc = __builtin_fmaf(qb[8 * j + 2 * e + 1], bf16_hi(w[e]), acc);
-    }
+  for (int j = 0; j < 16; ++j) {
+    const f32x4 w = row[j];
+    acc = __builtin_fmaf(qb[4 * j], w[0], acc);
+    acc = __builtin_fmaf(qb[4 * j + 1], w[1], acc);
+    acc = __builtin_fmaf(qb[4 * j + 2], w[2], acc);
+    acc = __builtin_fmaf(qb[4 * j + 3], w[3], acc);
   }
   p.scores[hs * p.scores_stride + t] = acc * p.scale;
 }
@@ -288,29 +279,28 @@ __global__ __launch_bounds__(256) void keyset_gather_kernel(GatherKParams p) {
 using namespace saf3r;
 
 // Checks the arguments of both probe entries and fills everything but the workspace pointer.
-static int probe_setup(const char* who, const void* q_packed, const void* k_packed, int frames, int tokens_per_frame,
-                       int num_special, const int32_t* head_ids, int n_sel, const int32_t* sample_idx,
-                       int n_samples, float scale, float* qbar, float* scores, int64_t scores_stride,
-                       ProbeParams* pp) {
+// Checks the arguments of both probe entries and fills everything but the workspace pointer.
+static int probe_setup(const char* who, const float* q32, const float* k32, int64_t slot_stride, int n_tokens,
+                       const int32_t* slots, int n_sel, const int32_t* sample_idx, int n_samples, float scale,
+                       float* qbar, float* scores, int64_t scores_stride, ProbeParams* pp) {
   ProbeParams& p = *pp;
-  if (!make_geom(frames, tokens_per_frame, num_special, &p.g)) return fail(SAF3R_ERR_INVALID, "%s: invalid geometry", who);
-  const int64_t n = (int64_t)frames * tokens_per_frame;
-  if (n > 0x7fffffff) return fail(SAF3R_ERR_UNSUPPORTED, "%s: too many tokens", who);
-  if (!q_packed || !k_packed || !head_ids || !qbar || !scores) return fail(SAF3R_ERR_INVALID, "%s: null pointer", who);
-  if (n_sel <= 0 || n_sel > 65535 || scores_stride < n)
-    return fail(SAF3R_ERR_INVALID, "%s: bad n_sel %d or scores_stride", who, n_sel);
-  if (sample_idx && (n_samples <= 0 || n_samples > n))
-    return fail(SAF3R_ERR_INVALID, "%s: n_samples must be in [1, %lld]", who, (long long)n);
-  if (((uintptr_t)q_packed | (uintptr_t)k_packed) % 16)
-    return fail(SAF3R_ERR_INVALID, "%s: packed inputs must be 16-byte aligned", who);
-  p.q = (const __bf16*)q_packed;
-  p.k = (const __bf16*)k_packed;
-  p.n = (int)n;
+  if (!q32 || !k32 || !slots || !qbar || !scores) return fail(SAF3R_ERR_INVALID, "%s: null pointer", who);
+  if (n_tokens <= 0) return fail(SAF3R_ERR_INVALID, "%s: n_tokens must be positive", who);
+  if (n_sel <= 0 || n_sel > 65535 || scores_stride < n_tokens || slot_stride < (int64_t)n_tokens * 64)
+    return fail(SAF3R_ERR_INVALID, "%s: bad n_sel %d, slot_stride or scores_stride", who, n_sel);
+  if (sample_idx && (n_samples <= 0 || n_samples > n_tokens))
+    return fail(SAF3R_ERR_INVALID, "%s: n_samples must be in [1, %d]", who, n_tokens);
+  if (((uintptr_t)q32 | (uintptr_t)k32) % 16 || slot_stride % 4)
+    return fail(SAF3R_ERR_INVALID, "%s: fp32 rows must be 16-byte aligned (slot_stride %% 4)", who);
+  p.q = q32;
+  p.k = k32;
+  p.slot_stride = slot_stride;
+  p.n = n_tokens;
   p.sample = sample_idx;
-  p.n_samp = sample_idx ? n_samples : (int)n;
+  p.n_samp = sample_idx ? n_samples : n_tokens;
   p.chunk = (p.n_samp + kProbeChunks - 1) / kProbeChunks;
   p.nchunks = (p.n_samp + p.chunk - 1) / p.chunk;
-  p.head_ids = head_ids;
+  p.slots = slots;
   p.partial = nullptr;
   p.qbar = qbar;
   p.scores = scores;
@@ -327,14 +317,14 @@ static int probe_launch(const ProbeParams& p, int n_sel, void* stream) {
   return check_launch("saf3r_probe_scores");
 }
 
-extern "C" int saf3r_probe_scores(const void* q_packed, const void* k_packed, int frames, int tokens_per_frame,
-                                  int num_special, const int32_t* head_ids, int n_sel, const int32_t* sample_idx,
-                                  int n_samples, float scale, float* partial, float* qbar, float* scores,
-                                  int64_t scores_stride, void* stream) {
+extern "C" int saf3r_probe_scores(const float* q32, const float* k32, int64_t slot_stride, int n_tokens,
+                                  const int32_t* slots, int n_sel, const int32_t* sample_idx, int n_samples,
+                                  float scale, float* partial, float* qbar, float* scores, int64_t scores_stride,
+                                  void* stream) {
   if (int e = injected("saf3r_probe_scores")) return e;
   ProbeParams p;
-  if (int e = probe_setup("saf3r_probe_scores", q_packed, k_packed, frames, tokens_per_frame, num_special, head_ids,
-                          n_sel, sample_idx, n_samples, scale, qbar, scores, scores_stride, &p))
+  if (int e = probe_setup("saf3r_probe_scores", q32, k32, slot_stride, n_tokens, slots, n_sel, sample_idx, n_samples,
+                          scale, qbar, scores, scores_stride, &p))
     return e;
   if (!partial) return fail(SAF3R_ERR_INVALID, "saf3r_probe_scores: null workspace");
   p.partial = partial;
@@ -372,15 +362,15 @@ static int scratch_ptr(const char* who, float** out) {
   return SAF3R_OK;
 }
 
-extern "C" int saf3r_probe_scores_noalloc(const void* q_packed, const void* k_packed, int frames,
-                                          int tokens_per_frame, int num_special, const int32_t* head_ids, int n_sel,
-                                          const int32_t* sample_idx, int n_samples, float scale, float* qbar,
-                                          float* scores, int64_t scores_stride, void* stream) {
+extern "C" int saf3r_probe_scores_noalloc(const float* q32, const float* k32, int64_t slot_stride, int n_tokens,
+                                          const int32_t* slots, int n_sel, const int32_t* sample_idx, int n_samples,
+                                          float scale, float* qbar, float* scores, int64_t scores_stride,
+                                          void* stream) {
   const char* who = "saf3r_probe_scores_noalloc";
   if (int e = injected(who)) return e;
   ProbeParams p;
-  if (int e = probe_setup(who, q_packed, k_packed, frames, tokens_per_frame, num_special, head_ids, n_sel, sample_idx,
-                          n_samples, scale, qbar, scores, scores_stride, &p))
+  if (int e = probe_setup(who, q32, k32, slot_stride, n_tokens, slots, n_sel, sample_idx, n_samples, scale, qbar,
+                          scores, scores_stride, &p))
     return e;
   if (n_sel > kScratchHeads)
     return fail(SAF3R_ERR_UNSUPPORTED, "%s: n_sel %d exceeds the %d heads of the static workspace", who, n_sel,

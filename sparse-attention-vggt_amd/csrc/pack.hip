@@ -7,6 +7,9 @@
 // Under autocast(bf16) the reference runs LayerNorm and RoPE in fp32 and hands bf16 q/k/v to
 // attention; this kernel does the same and rounds once, to nearest-even bf16. The cos/sin tables
 // come from the caller, computed as the reference does (fp32 angles = position * inv_freq).
+// Heads flagged for fp32 rows also get their fp32 q and k (after LayerNorm and RoPE, before the
+// rounding) in token order: the reference reads those fp32 values in the q_probe_topk mean and scores
+// (saf3r/patch/sparse_attention.py:160-166) and in the dino_topk gather (sparse_topk_attention.py:74-80).
 #include "common.h"
 
 namespace saf3r {
@@ -32,6 +35,9 @@ struct PackParams {
   __bf16* vp;
   Geom g;
   uint64_t tok_order;  // heads (bit h) packed in token order: slot = token, no special/frame padding
+  float* qk32;         // fp32 q and k rows of the flagged heads: [slot][q, k][F*T tokens][64]
+  uint64_t f32_heads;  // heads (bit h) whose fp32 q / k rows are also written
+  int8_t f32slot[64];  // slot of a flagged head in qk32
 };
 
 // One 256-thread workgroup per (64-slot tile, head). Four threads own one slot row, 16 features
@@ -117,6 +123,11 @@ __global__ __launch_bounds__(256) void pack_qkv_kernel(PackParams p) {
     if (tok < 0) {
 #pragma unroll
       for (int j = 0; j < 16; ++j) x[j] = 0.f;
+    } else if (h < 64 && ((p.f32_heads >> h) & 1)) {
+      // the fp32 values before the bf16 rounding, in token order (the probe and gather inputs)
+      f32x4* d32 = reinterpret_cast<f32x4*>(p.qk32 + (((int64_t)p.f32slot[h] * 2 + which) * ntok + tok) * 64 + 16 * c);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) d32[j] = f32x4{x[4 * j], x[4 * j + 1], x[4 * j + 2], x[4 * j + 3]};
     }
     u32x4 o0, o1;
 #pragma unroll
@@ -173,7 +184,8 @@ extern "C" int saf3r_pack_qkv(const void* q, const void* k, const void* v, int64
                               const float* q_ln_weight, const float* q_ln_bias, const float* k_ln_weight,
                               const float* k_ln_bias, float ln_eps, int apply_ln, const int32_t* pos,
                               const float* rope_cos, const float* rope_sin, int rope_positions, void* q_packed,
-                              void* k_packed, void* v_packed, const uint8_t* token_order, void* stream) {
+                              void* k_packed, void* v_packed, const uint8_t* token_order, const uint8_t* fp32_heads,
+                              float* qk32, void* stream) {
   if (int e = injected("saf3r_pack_qkv")) return e;
   PackParams p;
   if (!make_geom(frames, tokens_per_frame, num_special, &p.g))
@@ -216,6 +228,19 @@ extern "C" int saf3r_pack_qkv(const void* q, const void* k, const void* v, int64
       if (h >= 64) return fail(SAF3R_ERR_UNSUPPORTED, "saf3r_pack_qkv: token order is supported for heads 0..63");
       p.tok_order |= 1ull << h;
     }
+  }
+  p.qk32 = qk32;
+  p.f32_heads = 0;
+  if (fp32_heads) {
+    int n32 = 0;
+    for (int h = 0; h < num_heads; ++h) {
+      if (!fp32_heads[h]) continue;
+      if (h >= 64) return fail(SAF3R_ERR_UNSUPPORTED, "saf3r_pack_qkv: fp32 rows are supported for heads 0..63");
+      p.f32_heads |= 1ull << h;
+      p.f32slot[h] = (int8_t)n32++;
+    }
+    if (n32 > 0 && (!qk32 || (uintptr_t)qk32 % 16))
+      return fail(SAF3R_ERR_INVALID, "saf3r_pack_qkv: fp32 heads need a 16-byte aligned qk32 buffer");
   }
   dim3 grid(p.g.NT, num_heads);
   hipLaunchKernelGGL(pack_qkv_kernel, grid, dim3(256), 0, (hipStream_t)stream, p);

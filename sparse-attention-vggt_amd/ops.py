@@ -135,19 +135,27 @@ def packed_buffers(geom: Geometry, num_heads: int, device) -> tuple[torch.Tensor
 
 def pack_qkv(q, k, v, tok_stride: int, head_stride: int, geom: Geometry, num_heads: int,
              ln_q=None, ln_k=None, ln_eps: float = 1e-5, pos=None, rope_base=None, rope_positions=None, out=None,
-             token_order: Sequence[bool] | None = None):
+             token_order: Sequence[bool] | None = None, fp32_heads: Sequence[bool] | None = None):
     """QK-LayerNorm + RoPE-2D + packing (``saf3r_pack_qkv``). ``q``/``k``/``v`` are tensors (or
     views) whose element (t, h, d) is at ``data_ptr + t*tok_stride + h*head_stride + d``.
     RoPE is applied when ``rope_base`` is given; ``rope_positions`` is the table length
     (default: max position + 1, which costs one device-to-host read). Heads flagged in
-    ``token_order`` are packed in token order (see ``token_order_heads``)."""
+    ``token_order`` are packed in token order (see ``token_order_heads``). With ``fp32_heads``
+    the call returns a fourth tensor, fp32 [n_flagged, 2, N, 64]: the fp32 q (index 0) and k (1) of
+    the flagged heads after LayerNorm / RoPE, in token order and increasing head order."""
     _need_cuda(q, k, v)
     lib = _lib.load()
     qp, kp, vp = out if out is not None else packed_buffers(geom, num_heads, q.device)
+    qk32 = None
+    if fp32_heads is not None and any(fp32_heads):
+        qk32 = torch.empty(sum(1 for f in fp32_heads if f), 2, geom.tokens, HEAD_DIM, dtype=torch.float32,
+                           device=q.device)
     apply_ln = ln_q is not None
-    if apply_ln:
-        qw, qb = (t.detach().float().contiguous() for t in ln_q)
-        kw, kb = (t.detach().float().contiguous() for t in ln_k)
+    if apply_ln:  # fp32 device copies (the kernel reads them as device arrays of 64 floats)
+        qw, qb = (t.detach().to(device=q.device, dtype=torch.float32).contiguous() for t in ln_q)
+        kw, kb = (t.detach().to(device=q.device, dtype=torch.float32).contiguous() for t in ln_k)
+        if any(t.numel() != HEAD_DIM for t in (qw, qb, kw, kb)):
+            raise ValueError("LayerNorm weight and bias must hold 64 values each")
     else:
         qw = qb = kw = kb = None
     rc = rs = None
@@ -162,7 +170,10 @@ def pack_qkv(q, k, v, tok_stride: int, head_stride: int, geom: Geometry, num_hea
         _ptr(q), _ptr(k), _ptr(v), tok_stride, head_stride, geom.frames, geom.tokens_per_frame, geom.num_special,
         num_heads, _ptr(qw), _ptr(qb), _ptr(kw), _ptr(kb), float(ln_eps), int(apply_ln),
         _ptr(pos) if rc is not None else None, _ptr(rc), _ptr(rs), npos, _ptr(qp), _ptr(kp), _ptr(vp),
-        _u8_flags(token_order, num_heads), _lib.stream_ptr()))
+        _u8_flags(token_order, num_heads), _u8_flags(fp32_heads, num_heads) if qk32 is not None else None,
+        _ptr(qk32), _lib.stream_ptr()))
+    if fp32_heads is not None:
+        return qp, kp, vp, qk32
     return qp, kp, vp
 
 
@@ -264,6 +275,7 @@ def sparse_attn_fwd(qp, kp, vp, geom: Geometry, patterns: Sequence[int], sel: to
     if n_dyn:
         if sel is None:
             raise ValueError("block-dynamic heads need a selection list")
+        _need_cuda(sel)
         sel = sel.to(torch.int32).contiguous()
         if sel.dim() != 3 or sel.shape[0] != n_dyn or sel.shape[1] != geom.num_blocks:
             raise ValueError(f"sel must be [{n_dyn}, {geom.num_blocks}, W], got {tuple(sel.shape)}")
@@ -304,37 +316,42 @@ def sparse_attn_fwd(qp, kp, vp, geom: Geometry, patterns: Sequence[int], sel: to
 
 def rows(t: torch.Tensor, row_stride: int | None = None, base_row: int = 0, rows_per_frame: int | None = None,
          frame_row_stride: int = 0, offset: int = 0) -> _lib.Rows:
-    """Row descriptor over a bf16 tensor (``offset`` in elements from its data pointer)."""
+    """Row descriptor over a bf16 or fp32 tensor (``offset`` and strides in elements of its dtype)."""
     rs = t.stride(-2) if row_stride is None else row_stride
     rpf = (1 << 62) if rows_per_frame is None else rows_per_frame
-    return _lib.Rows(t.data_ptr() + 2 * offset, rs, base_row, rpf, frame_row_stride)
+    return _lib.Rows(t.data_ptr() + t.element_size() * offset, rs, base_row, rpf, frame_row_stride)
 
 
 def gather_attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, idx: torch.Tensor,
                     scale: float | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
     """``fused_sparse_topk_attention`` (``saf3r/triton/sparse_topk_attention.py:115-166``):
-    q [N, 64], k/v [Nk, 64] bf16, idx int32 [N, TopK] (a stride-0 row view shares one list)."""
+    q [N, 64], k/v [Nk, 64], idx int32 [N, TopK] (a stride-0 row view shares one list). fp32 q and k
+    are read as fp32 (as the reference's kernel upcasts them); other dtypes are taken as bf16."""
     _need_cuda(q, k, v, idx)
     n, d = q.shape
     if d != HEAD_DIM:
         raise ValueError("head_dim must be 64")
-    q, k, v = (t.to(torch.bfloat16).contiguous() for t in (q, k, v))
+    f32 = q.dtype == torch.float32 and k.dtype == torch.float32
+    qk_t = torch.float32 if f32 else torch.bfloat16
+    q, k = (t.to(qk_t).contiguous() for t in (q, k))
+    v = v.to(torch.bfloat16).contiguous()
     if idx.stride(-1) != 1:
         idx = idx.contiguous()
     idx = idx.to(torch.int32)
     if out is None:
         out = torch.empty(n, v.shape[1], dtype=torch.bfloat16, device=q.device)
     return gather_attn_rows(rows(q), rows(k), rows(v), idx, idx.stride(0), n, idx.shape[1], k.shape[0], scale,
-                            rows(out), out)
+                            rows(out), out, qk_fp32=f32)
 
 
-def gather_attn_rows(qr, kr, vr, idx, idx_row_stride, n, topk, num_keys, scale, outr, keep=None):
+def gather_attn_rows(qr, kr, vr, idx, idx_row_stride, n, topk, num_keys, scale, outr, keep=None, qk_fp32=False):
+    """``saf3r_gather_attn_fwd`` on row descriptors; ``qk_fp32``: q and k rows are fp32."""
     lib = _lib.load()
     scale = 1.0 / math.sqrt(HEAD_DIM) if scale is None else scale
     _mark("gather_attn", "start")
     _lib.check(lib.saf3r_gather_attn_fwd(ctypes.byref(qr), ctypes.byref(kr), ctypes.byref(vr), _ptr(idx),
-                                         idx_row_stride, n, topk, num_keys, float(scale), ctypes.byref(outr),
-                                         _lib.stream_ptr()))
+                                         idx_row_stride, n, topk, num_keys, float(scale), int(bool(qk_fp32)),
+                                         ctypes.byref(outr), _lib.stream_ptr()))
     _mark("gather_attn", "end")
     return keep
 
@@ -406,30 +423,40 @@ class KeySets:
     qbar: torch.Tensor | None = None
 
 
-def probe_scores(qp: torch.Tensor, kp: torch.Tensor, geom: Geometry, head_ids: Sequence[int],
-                 scale: float | None = None, sample: torch.Tensor | None = None):
-    """Mean query and probe scores of ``head_ids`` (``saf3r/patch/sparse_attention.py:150-168``):
-    returns (qbar fp32 [n][64], scores fp32 [n][N] in token order). ``sample`` (int tokens) restricts
-    the mean to those query rows, in list order (the reference's ``q_sample_ratio < 1``)."""
-    _need_cuda(qp, kp)
+def probe_scores(qk32: torch.Tensor, slots: Sequence[int], scale: float | None = None,
+                 sample: torch.Tensor | None = None, noalloc: bool = False):
+    """Mean query and probe scores (``saf3r/patch/sparse_attention.py:150-168``) of the heads stored at
+    ``slots`` of ``qk32`` (fp32 [n, 2, N, 64], q and k rows in token order, as ``pack_qkv`` writes them
+    for ``fp32_heads``): returns (qbar fp32 [n_sel][64], scores fp32 [n_sel][N]). ``sample`` (int tokens)
+    restricts the mean to those query rows, in list order (the reference's ``q_sample_ratio < 1``).
+    ``noalloc`` uses the allocation-free entry (its partial sums in the library's static workspace)."""
+    _need_cuda(qk32)
     lib = _lib.load()
-    _check_packed(qp, kp, None, geom)
-    n = len(head_ids)
-    dev = qp.device
-    hs = torch.tensor(list(head_ids), dtype=torch.int32, device=dev)
-    partial = torch.empty(n, 256, HEAD_DIM, dtype=torch.float32, device=dev)
+    if qk32.dtype != torch.float32 or qk32.dim() != 4 or qk32.shape[1] != 2 or qk32.shape[3] != HEAD_DIM \
+            or not qk32.is_contiguous():
+        raise ValueError("qk32 must be a contiguous fp32 [n, 2, N, 64] tensor")
+    N = qk32.shape[2]
+    n = len(slots)
+    dev = qk32.device
+    hs = torch.tensor(list(slots), dtype=torch.int32, device=dev)
     qbar = torch.empty(n, HEAD_DIM, dtype=torch.float32, device=dev)
-    scores = torch.empty(n, geom.tokens, dtype=torch.float32, device=dev)
+    scores = torch.empty(n, N, dtype=torch.float32, device=dev)
     scale = 1.0 / math.sqrt(HEAD_DIM) if scale is None else scale
     if sample is not None:
         sample = sample.to(device=dev, dtype=torch.int32).contiguous()
-        if sample.dim() != 1 or not 1 <= sample.numel() <= geom.tokens:
+        if sample.dim() != 1 or not 1 <= sample.numel() <= N:
             raise ValueError("sample must list between 1 and N tokens")
+    stride = qk32.stride(0)
+    args = (_ptr(qk32), ctypes.c_void_p(qk32.data_ptr() + 4 * qk32.stride(1)), stride, N, _ptr(hs), n, _ptr(sample),
+            0 if sample is None else sample.numel(), float(scale))
     _mark("probe", "start")
-    _lib.check(lib.saf3r_probe_scores(_ptr(qp), _ptr(kp), geom.frames, geom.tokens_per_frame, geom.num_special,
-                                      _ptr(hs), n, _ptr(sample), 0 if sample is None else sample.numel(),
-                                      float(scale), _ptr(partial), _ptr(qbar), _ptr(scores), scores.stride(0),
-                                      _lib.stream_ptr()))
+    if noalloc:
+        _lib.check(lib.saf3r_probe_scores_noalloc(*args, _ptr(qbar), _ptr(scores), scores.stride(0),
+                                                  _lib.stream_ptr()))
+    else:
+        partial = torch.empty(n, 256, HEAD_DIM, dtype=torch.float32, device=dev)
+        _lib.check(lib.saf3r_probe_scores(*args, _ptr(partial), _ptr(qbar), _ptr(scores), scores.stride(0),
+                                          _lib.stream_ptr()))
     _mark("probe", "end")
     return qbar, scores
 
@@ -456,6 +483,7 @@ def keyset_build(specs: Sequence[KeySetSpec], geom: Geometry, scores: torch.Tens
     idx = torch.empty(n, geom.tokens, dtype=torch.int32, device=device)
     count = torch.empty(n, dtype=torch.int32, device=device)
     if scores is not None:
+        _need_cuda(scores)
         if scores.dtype != torch.float32 or scores.shape[0] != n or scores.shape[1] < geom.tokens:
             raise ValueError("scores must be fp32 [n_specs, >= N]")
         scores = scores.contiguous()

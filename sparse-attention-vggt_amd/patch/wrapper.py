@@ -59,6 +59,10 @@ class BaseHeadwiseSparseAttentionWrapper(nn.Module):
         self.topk_scope = kwargs.get("topk_scope", "frame")
         self.shared = kwargs.get("shared", None) or SelectionState()
         self.last_selection = None
+        # keep_attention: hold the pre-projection attention output [N, H*64] of the last forward in
+        # last_attention (for inspection and tests; off by default, it keeps the tensor alive)
+        self.keep_attention = False
+        self.last_attention = None
 
         cfg = kwargs.get("config", [])
         self.head_cfg = [{"mode": "full"} for _ in range(num_heads)]
@@ -83,6 +87,12 @@ class BaseHeadwiseSparseAttentionWrapper(nn.Module):
         self.last_keysets = None
         self.dino_heads = [h for h, p in enumerate(self.patterns) if p in ops.TOKEN_PATTERNS]
         self.first_dino_head = next((h for h in self.dino_heads if self.head_cfg[h].get("is_first_dino", False)), None)
+        # heads whose fp32 q / k (after LayerNorm / RoPE) the kernels read, as the reference reads its fp32
+        # values under autocast: the q_probe_topk mean and scores (sparse_attention.py:160-166) and the
+        # dino_topk gather (sparse_topk_attention.py:74-80)
+        probe = {h for h in self.keyset_heads if self.head_cfg[h]["mode"] == "q_probe_topk"}
+        self.fp32_heads = sorted(probe | set(self.dino_heads))
+        self.fp32_slot = {h: i for i, h in enumerate(self.fp32_heads)}
 
     # ------------------------------------------------------------------------------------
     def geometry(self, num_tokens: int) -> Geometry:
@@ -111,8 +121,11 @@ class BaseHeadwiseSparseAttentionWrapper(nn.Module):
             # table length: the patch grid bounds every position ((y+1, x+1) with specials at 0)
             npos = max(self.patch_height, self.patch_width) + 1 if self.patch_height else None
         tord = ops.token_order_heads(self.patterns)  # dense heads: unpadded token-order tiles
-        qp, kp, vp = ops.pack_qkv(qkv, qkv[:, C:], qkv[:, 2 * C:], 3 * C, HEAD_DIM, geom, H, ln_q=ln_q, ln_k=ln_k,
-                                  ln_eps=eps, pos=p2, rope_base=base, rope_positions=npos, token_order=tord)
+        f32 = [h in self.fp32_slot for h in range(H)] if self.fp32_heads else None
+        packed = ops.pack_qkv(qkv, qkv[:, C:], qkv[:, 2 * C:], 3 * C, HEAD_DIM, geom, H, ln_q=ln_q, ln_k=ln_k,
+                              ln_eps=eps, pos=p2, rope_base=base, rope_positions=npos, token_order=tord, fp32_heads=f32)
+        qp, kp, vp = packed[:3]
+        qk32 = packed[3] if f32 is not None else None
         sel = None
         if self.dyn_heads:
             pq, pk = ops.block_pool(qp, kp, geom, self.dyn_heads)
@@ -122,43 +135,46 @@ class BaseHeadwiseSparseAttentionWrapper(nn.Module):
             self._lazy_token_topk(qp, kp, geom)
         keysets = None
         if self.keyset_heads:
-            keysets = self._keysets(qp, kp, qkv, geom, C)
+            keysets = self._keysets(qk32, kp, qkv, geom, C)
         self.last_keysets = keysets
         bcast = None
         if self.broadcast_heads:  # broadcast_first: frame 0's Q/K rows and every frame's V tiles
             bcast = ops.broadcast_gather(qp, kp, geom, self.broadcast_heads, qkv[:, 2 * C:], qkv.stride(0), HEAD_DIM)
         out = ops.sparse_attn_fwd(qp, kp, vp, geom, self.patterns, sel, keysets=keysets, broadcast=bcast,
                                   token_order=tord)
-        if self.dino_heads:
+        if self.dino_heads:  # image rows: gather attention over est_topk_idx with the fp32 q / k
             est = self.est_topk_idx
-            P, W = geom.patches, est.shape[1]
+            P, W, T, ns = geom.patches, est.shape[1], geom.tokens_per_frame, geom.num_special
             for h in self.dino_heads:
-                qr = ops.rows(qp[h], 64, geom.special_slots, P, geom.padded_patches)
-                kr = ops.rows(kp[h], 64, geom.special_slots, P, geom.padded_patches)
-                vr = ops.rows(qkv, 3 * C, geom.num_special, P, geom.tokens_per_frame, offset=2 * C + h * HEAD_DIM)
-                orr = ops.rows(out, C, geom.num_special, P, geom.tokens_per_frame, offset=h * HEAD_DIM)
-                ops.gather_attn_rows(qr, kr, vr, est, W, geom.frames * P, W, geom.frames * P, None, orr)
+                s = self.fp32_slot[h]
+                qr = ops.rows(qk32[s, 0], 64, ns, P, T)
+                kr = ops.rows(qk32[s, 1], 64, ns, P, T)
+                vr = ops.rows(qkv, 3 * C, ns, P, T, offset=2 * C + h * HEAD_DIM)
+                orr = ops.rows(out, C, ns, P, T, offset=h * HEAD_DIM)
+                ops.gather_attn_rows(qr, kr, vr, est, W, geom.frames * P, W, geom.frames * P, None, orr, qk_fp32=True)
+        self.last_attention = out if self.keep_attention else None
         return out
 
-    def _keysets(self, qp, kp, qkv, geom: Geometry, C: int):
+    def _keysets(self, qk32, kp, qkv, geom: Geometry, C: int):
         """Shared key sets of the stride / q_probe_topk heads (``sparse_attention.py:143-186, 256-273``):
-        probe scores of the top-k heads, members in token order, then the compact K / V they attend."""
+        probe scores of the top-k heads from their fp32 q / k, members in token order, then the compact
+        K / V they attend."""
         specs = [keyset_spec(self.head_cfg[h], h, geom.tokens) for h in self.keyset_heads]
         probe_rows = [i for i, s in enumerate(specs) if s.mode == ops.KEYSET_TOPK]
         scores = None
         if probe_rows:
             ratios = sorted({specs[i].sample_ratio for i in probe_rows})
             if len(ratios) == 1 and len(probe_rows) == len(specs):
-                _, scores = ops.probe_scores(qp, kp, geom, [specs[i].head for i in probe_rows],
+                _, scores = ops.probe_scores(qk32, [self.fp32_slot[specs[i].head] for i in probe_rows],
                                              sample=ops.probe_sample(geom.tokens, ratios[0]))
             else:  # one call per sample ratio; rows of stride heads stay unused zeros
-                scores = torch.zeros(len(specs), geom.tokens, dtype=torch.float32, device=qp.device)
+                scores = torch.zeros(len(specs), geom.tokens, dtype=torch.float32, device=kp.device)
                 for r in ratios:
                     rows_r = [i for i in probe_rows if specs[i].sample_ratio == r]
-                    _, sc = ops.probe_scores(qp, kp, geom, [specs[i].head for i in rows_r],
+                    _, sc = ops.probe_scores(qk32, [self.fp32_slot[specs[i].head] for i in rows_r],
                                              sample=ops.probe_sample(geom.tokens, r))
                     scores[rows_r] = sc
-        idx, count = ops.keyset_build(specs, geom, scores, qp.device)
+        idx, count = ops.keyset_build(specs, geom, scores, kp.device)
         ks = ops.keyset_gather(kp, geom, specs, qkv[:, 2 * C:], qkv.stride(0), HEAD_DIM, idx, count)
         ks.scores = scores
         return ks

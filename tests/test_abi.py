@@ -24,7 +24,7 @@ def test_library_exports_every_declared_symbol(pkg):
     for n in names:
         assert hasattr(lib, n), n
     assert set(names) == set(lib_mod.EXPORTS)
-    assert lib.saf3r_abi_version() == lib_mod.ABI_VERSION == 6
+    assert lib.saf3r_abi_version() == lib_mod.ABI_VERSION == 7
 
 
 def test_packed_slots_matches_layout(pkg):
@@ -92,21 +92,40 @@ def test_invalid_arguments_fail_before_launch(pkg):
     assert rc == 1 and b"candidate" in lib.saf3r_last_error()
     rc = lib.saf3r_frame_topk_scores(dev, 9000, 2, 2, 4500, 0, 0, 1, 4, 0, dev, 8, None, None, None)
     assert rc == 2  # frames beyond 4096 keys
-    rc = lib.saf3r_probe_scores(dev, dev, 2, 100, 5, dev, 1, None, 0, 0.125, dev, dev, dev, 10, None)
+    rc = lib.saf3r_probe_scores(dev, dev, 200 * 64, 200, dev, 1, None, 0, 0.125, dev, dev, dev, 10, None)
     assert rc == 1 and b"scores_stride" in lib.saf3r_last_error()
-    rc = lib.saf3r_probe_scores(dev, dev, 2, 100, 5, dev, 1, dev, 201, 0.125, dev, dev, dev, 200, None)
+    rc = lib.saf3r_probe_scores(dev, dev, 100 * 64, 200, dev, 1, None, 0, 0.125, dev, dev, dev, 200, None)
+    assert rc == 1 and b"slot_stride" in lib.saf3r_last_error()
+    rc = lib.saf3r_probe_scores(dev, dev, 200 * 64, 200, dev, 1, dev, 201, 0.125, dev, dev, dev, 200, None)
     assert rc == 1 and b"n_samples" in lib.saf3r_last_error()
-    rc = lib.saf3r_probe_scores(dev, dev, 2, 100, 5, dev, 1, None, 0, 0.125, None, dev, dev, 200, None)
+    rc = lib.saf3r_probe_scores(dev, dev, 200 * 64, 200, dev, 1, None, 0, 0.125, None, dev, dev, 200, None)
     assert rc == 1 and b"workspace" in lib.saf3r_last_error()
+    rc = lib.saf3r_probe_scores_noalloc(dev, dev, 200 * 64, 200, dev, 65, None, 0, 0.125, dev, dev, 200, None)
+    assert rc == 2 and b"static workspace" in lib.saf3r_last_error()
+    rows = L.Rows(16, 64, 0, 1 << 40, 0)
+    rc = lib.saf3r_gather_attn_fwd(ctypes.byref(rows), ctypes.byref(rows), ctypes.byref(rows), dev, 4, 1, 4, 10, 0.125,
+                                   2, ctypes.byref(rows), None)
+    assert rc == 1 and b"qk_fp32" in lib.saf3r_last_error()
+    rows6 = L.Rows(16, 6, 0, 1 << 40, 0)  # fp32 rows need a row stride % 4, bf16 rows % 8
+    rc = lib.saf3r_gather_attn_fwd(ctypes.byref(rows6), ctypes.byref(rows6), ctypes.byref(rows), dev, 4, 1, 4, 10,
+                                   0.125, 1, ctypes.byref(rows), None)
+    assert rc == 1 and b"row stride % 4" in lib.saf3r_last_error()
     rc = lib.saf3r_block_select(ctypes.c_void_p(16), ctypes.c_void_p(16), 1, 4, 2, 2, 33, 0, ctypes.c_void_p(16), None)
     assert rc == 2  # k beyond the supported range
     rc = lib.saf3r_pack_qkv(None, None, None, 64, 64, 0, 10, 1, 1, None, None, None, None, 1e-5, 0, None, None,
-                            None, 0, None, None, None, None, 0, None, 0, None)
+                            None, 0, None, None, None, None, None, None, None)
     assert rc == 1 and b"geometry" in lib.saf3r_last_error()
     flags = (ctypes.c_uint8 * 65)(*([0] * 64 + [1]))  # token order beyond head 63
     rc = lib.saf3r_pack_qkv(dev, dev, dev, 64, 64, 2, 100, 5, 65, None, None, None, None, 1e-5, 0, None, None,
-                            None, 0, dev, dev, dev, flags, None)
+                            None, 0, dev, dev, dev, flags, None, None, None)
     assert rc == 2 and b"token order" in lib.saf3r_last_error()
+    rc = lib.saf3r_pack_qkv(dev, dev, dev, 64, 64, 2, 100, 5, 65, None, None, None, None, 1e-5, 0, None, None,
+                            None, 0, dev, dev, dev, None, flags, dev, None)
+    assert rc == 2 and b"fp32 rows" in lib.saf3r_last_error()
+    one = (ctypes.c_uint8 * 2)(0, 1)
+    rc = lib.saf3r_pack_qkv(dev, dev, dev, 64, 64, 2, 100, 5, 2, None, None, None, None, 1e-5, 0, None, None,
+                            None, 0, dev, dev, dev, None, one, None, None)
+    assert rc == 1 and b"qk32" in lib.saf3r_last_error()
     with pytest.raises(L.Saf3rError):
         L.check(1)
 

@@ -162,8 +162,10 @@ def test_keysets_128_frames(mods):
     patterns = [ops.KEYSET, ops.KEYSET, ops.DENSE, ops.KEYSET, ops.FRAME_LOCAL, ops.KEYSET]
     specs = [ops.KeySetSpec(0, ops.KEYSET_STRIDE, 4, 0, True), ops.KeySetSpec(1, ops.KEYSET_TOPK, n // 4, 0, False),
              ops.KeySetSpec(3, ops.KEYSET_TOPK, 1024, 0, True), ops.KeySetSpec(5, ops.KEYSET_STRIDE, 4, 1, False)]
-    qp, kp, vp = ops.pack_heads(q.to(DEV), k.to(DEV), v.to(DEV), geom)
-    _, sc = ops.probe_scores(qp, kp, geom, [1, 3])
+    qp, kp, vp, qk32 = ops.pack_heads(q.to(DEV), k.to(DEV), v.to(DEV), geom,
+                                      fp32_heads=[h in (1, 3) for h in range(len(patterns))])
+    _, sc = ops.probe_scores(qk32, [0, 1])  # fp32 rows of bf16 inputs: the bf16 values exactly
+    del qk32
     scores = torch.zeros(len(specs), n, device=DEV)
     scores[1], scores[2] = sc[0], sc[1]
     idx, count = ops.keyset_build(specs, geom, scores, DEV)

@@ -312,6 +312,25 @@ def test_gather_attention(ops, n, nk, topk):
     _check_close(got.cpu(), ref, f"gather n{n} topk{topk}")
 
 
+@pytest.mark.parametrize("n,nk,topk", [(100, 300, 7), (64, 5000, 512), (5, 3000, 2100)])
+def test_gather_attention_fp32_qk(ops, n, nk, topk):
+    """fp32 q / k rows (the reference's gather reads fp32 q / k under autocast): the scores are fp32 dot
+    products of the fp32 values, which bf16 rounding of q / k would move."""
+    g = torch.Generator().manual_seed(n + topk + 1)
+    q, k = (3.0 * torch.randn(m, 64, generator=g) for m in (n, nk))
+    v = torch.randn(nk, 64, generator=g).to(torch.bfloat16)
+    idx = torch.randint(0, nk, (n, topk), generator=g, dtype=torch.int32)
+    idx[0, :3] = -1
+    got = ops.gather_attn_fwd(q.to(DEV), k.to(DEV), v.to(DEV), idx.to(DEV))
+    torch.cuda.synchronize()
+    ref = OA.gather_attention(q.double(), k.double(), v.float(), idx, dtype=torch.float64)
+    _check_close(got.cpu(), ref, f"gather fp32 q/k n{n} topk{topk}")
+    ref_bf = OA.gather_attention(q.to(torch.bfloat16).float(), k.to(torch.bfloat16).float(), v.float(), idx,
+                                 dtype=torch.float64)
+    if topk <= 512:  # concentrated softmax: bf16-rounded q / k would be much further off than the kernel is
+        assert (ref_bf - ref).abs().max() > 2 * (got.cpu().float() - ref).abs().max()
+
+
 def test_gather_attention_shared_list(ops):
     g = torch.Generator().manual_seed(3)
     q, k, v = (torch.randn(m, 64, generator=g).to(torch.bfloat16) for m in (50, 400, 400))

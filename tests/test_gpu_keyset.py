@@ -34,41 +34,70 @@ def _bits(x: torch.Tensor) -> np.ndarray:
     return x.contiguous().view(torch.int16).numpy().view(np.uint16)
 
 
-@pytest.mark.parametrize("F,T,ns", [(3, 155, 5), (4, 1374, 5), (2, 64, 0), (1, 70, 5)])
-def test_probe_scores_bit_exact(ops, pkg, F, T, ns):
-    geom = pkg.Geometry(F, T, ns)
-    H = 3
-    q, k, v = _qkv(H, geom.tokens, seed=F + T, scale=2.0)
-    qp, kp, vp = ops.pack_heads(q.to(DEV), k.to(DEV), v.to(DEV), geom)
-    heads = [2, 0]
-    qbar, scores = ops.probe_scores(qp, kp, geom, heads)
-    torch.cuda.synchronize()
-    for i, h in enumerate(heads):
-        want_q = OS.probe_mean(_bits(q[h]))
-        assert np.array_equal(qbar[i].cpu().numpy().view(np.uint32), want_q.view(np.uint32)), f"qbar head {h}"
-        want_s = OS.probe_scores(want_q, _bits(k[h]))
-        assert np.array_equal(scores[i].cpu().numpy().view(np.uint32), want_s.view(np.uint32)), f"scores head {h}"
+def _qk32(H, N, seed, scale=2.0):
+    """fp32 q / k rows [H, 2, N, 64] in the layout pack_qkv writes for fp32 heads (not bf16-exact values)."""
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(H, 2, N, 64, generator=g) * scale + 0.3
 
 
-@pytest.mark.parametrize("F,T,ns,ratio", [(3, 155, 5, 0.1), (4, 1374, 5, 0.3), (2, 64, 0, 0.5), (1, 70, 5, 0.001)])
-def test_probe_scores_sampled_rows_bit_exact(ops, pkg, F, T, ns, ratio):
+@pytest.mark.parametrize("N", [3 * 155, 4 * 1374, 128, 70])
+def test_probe_scores_bit_exact(ops, pkg, N):
+    """The mean query and probe scores from fp32 q / k rows, both probe entries, against the oracle."""
+    qk = _qk32(3, N, seed=N)
+    qk_dev = qk.to(DEV).contiguous()
+    slots = [2, 0]
+    for noalloc in (False, True):
+        qbar, scores = ops.probe_scores(qk_dev, slots, noalloc=noalloc)
+        torch.cuda.synchronize()
+        for i, h in enumerate(slots):
+            want_q = OS.probe_mean(qk[h, 0].numpy())
+            assert np.array_equal(qbar[i].cpu().numpy().view(np.uint32), want_q.view(np.uint32)), f"qbar slot {h}"
+            want_s = OS.probe_scores(want_q, qk[h, 1].numpy())
+            assert np.array_equal(scores[i].cpu().numpy().view(np.uint32), want_s.view(np.uint32)), f"scores {h}"
+
+
+@pytest.mark.parametrize("N,ratio", [(3 * 155, 0.1), (4 * 1374, 0.3), (128, 0.5), (70, 0.001)])
+def test_probe_scores_sampled_rows_bit_exact(ops, pkg, N, ratio):
     """q_sample_ratio < 1: the mean query over the reference's linspace rows (sparse_attention.py:154-157)."""
-    geom = pkg.Geometry(F, T, ns)
-    H = 2
-    q, k, v = _qkv(H, geom.tokens, seed=F * T + 1, scale=2.0)
-    qp, kp, vp = ops.pack_heads(q.to(DEV), k.to(DEV), v.to(DEV), geom)
-    rows = ops.probe_sample(geom.tokens, ratio)
-    assert rows is not None and len(rows) == max(1, int(geom.tokens * ratio))
-    qbar, scores = ops.probe_scores(qp, kp, geom, [1, 0], sample=rows)
+    qk = _qk32(2, N, seed=N + 1)
+    rows = ops.probe_sample(N, ratio)
+    assert rows is not None and len(rows) == max(1, int(N * ratio))
+    qbar, scores = ops.probe_scores(qk.to(DEV).contiguous(), [1, 0], sample=rows)
     torch.cuda.synchronize()
     for i, h in enumerate([1, 0]):
-        want_q = OS.probe_mean(_bits(q[h][rows]))
-        assert np.array_equal(qbar[i].cpu().numpy().view(np.uint32), want_q.view(np.uint32)), f"qbar head {h}"
-        want_s = OS.probe_scores(want_q, _bits(k[h]))
-        assert np.array_equal(scores[i].cpu().numpy().view(np.uint32), want_s.view(np.uint32)), f"scores head {h}"
+        want_q = OS.probe_mean(qk[h, 0][rows].numpy())
+        assert np.array_equal(qbar[i].cpu().numpy().view(np.uint32), want_q.view(np.uint32)), f"qbar slot {h}"
+        want_s = OS.probe_scores(want_q, qk[h, 1].numpy())
+        assert np.array_equal(scores[i].cpu().numpy().view(np.uint32), want_s.view(np.uint32)), f"scores slot {h}"
     # the sampled mean is the fp64 mean of those rows to fp32 accuracy, and not the all-row mean
-    ref = q[0][rows].double().mean(0).float()
+    ref = qk[0, 0][rows].double().mean(0).float()
     assert torch.allclose(qbar[1].cpu(), ref, atol=1e-5)
+
+
+def test_pack_writes_fp32_rows_of_flagged_heads(ops, pkg):
+    """pack_qkv's fp32 rows (after LayerNorm / RoPE, before the bf16 rounding): token order, flagged heads
+    in increasing head order, and they round to exactly the packed bf16 rows."""
+    geom = pkg.Geometry(3, 5 + 6 * 7, 5)
+    H, N = 4, geom.tokens
+    C = 64 * H
+    g = torch.Generator().manual_seed(31)
+    qkv = torch.randn(N, 3 * C, generator=g).to(torch.bfloat16).to(DEV)
+    ln = (torch.rand(64, generator=g) + 0.5, 0.1 * torch.randn(64, generator=g))
+    pos = OA.vggt_positions(3, 6, 7)
+    qp, kp, vp, qk32 = ops.pack_qkv(qkv, qkv[:, C:], qkv[:, 2 * C:], 3 * C, 64, geom, H, ln_q=ln, ln_k=ln,
+                                    pos=pos.to(DEV), rope_base=100.0, fp32_heads=[False, True, False, True])
+    torch.cuda.synchronize()
+    toks = slot_tokens(geom.frames, geom.tokens_per_frame, geom.num_special)
+    q, _ = unpack_rows(qp.cpu(), toks, N)
+    k, _ = unpack_rows(kp.cpu(), toks, N)
+    assert tuple(qk32.shape) == (2, 2, N, 64)
+    qr, kr, _ = OA.qkv_prologue(qkv.cpu(), H, (ln[0], ln[1]), (ln[0], ln[1]), pos)
+    for s, h in enumerate((1, 3)):
+        assert torch.equal(qk32[s, 0].cpu().to(torch.bfloat16), q[h]) and torch.equal(qk32[s, 1].cpu().to(torch.bfloat16), k[h])
+        # the fp32 values themselves: the oracle prologue's fp32 LayerNorm + RoPE within fp32 rounding
+        ref_q = OA.rope2d(torch.nn.functional.layer_norm(qkv.cpu().float().reshape(N, 3, H, 64)[:, 0, h], (64,),
+                                                         ln[0], ln[1], 1e-5), pos)
+        assert torch.allclose(qk32[s, 0].cpu(), ref_q, rtol=1e-5, atol=1e-5)
 
 
 @pytest.mark.parametrize("F,T,ns", [(3, 155, 5), (4, 1374, 5), (2, 64, 0)])
@@ -123,10 +152,10 @@ def test_keyset_attention_in_one_launch(ops, pkg, F, T, ns):
     patterns = [ops.KEYSET, ops.DENSE, ops.KEYSET, ops.FRAME_LOCAL, ops.KEYSET, ops.ANCHOR]
     H = len(patterns)
     q, k, v = _qkv(H, n, seed=F * 3 + T, scale=1.5)
-    qp, kp, vp = ops.pack_heads(q.to(DEV), k.to(DEV), v.to(DEV), geom)
+    qp, kp, vp, qk32 = ops.pack_heads(q.to(DEV), k.to(DEV), v.to(DEV), geom, fp32_heads=[h == 2 for h in range(H)])
     specs = [ops.KeySetSpec(0, ops.KEYSET_STRIDE, 4, 0, True), ops.KeySetSpec(2, ops.KEYSET_TOPK, max(1, n // 4)),
              ops.KeySetSpec(4, ops.KEYSET_STRIDE, 128, 0, True)]
-    _, sc = ops.probe_scores(qp, kp, geom, [2])
+    _, sc = ops.probe_scores(qk32, [0])
     scores = torch.zeros(3, n, device=DEV)
     scores[1] = sc[0]
     idx, count = ops.keyset_build(specs, geom, scores, DEV)

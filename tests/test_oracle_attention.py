@@ -186,3 +186,90 @@ def test_broadcast_first_pins():
     # the gathered entry point dispatches to it
     torch.testing.assert_close(A.sparse_attention_gathered(q, k, v, A.BROADCAST, G, dtype=torch.float64), got)
 
+
+
+# ---- the layer at the reference's rounding points (oracle.attention.reference_layer) ----------
+
+def _layer_inputs(ph=3, pw=4, frames=2, H=4, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    C = 64 * H
+    G2 = A.Geometry(frames=frames, tokens_per_frame=5 + ph * pw)
+    x = torch.randn(G2.tokens, C, generator=g).to(torch.bfloat16).float()
+    w_qkv = torch.randn(3 * C, C, generator=g) / math.sqrt(C)
+    b_qkv = 0.1 * torch.randn(3 * C, generator=g)
+    ln = (1 + 0.2 * torch.randn(64, generator=g), 0.1 * torch.randn(64, generator=g))
+    w_p = torch.randn(C, C, generator=g) / math.sqrt(C)
+    b_p = 0.1 * torch.randn(C, generator=g)
+    pos = A.vggt_positions(frames, ph, pw)
+    return G2, x, w_qkv, b_qkv, ln, w_p, b_p, pos
+
+
+def test_reference_layer_all_full_is_the_unpatched_module():
+    """Every head 'full': the restatement equals an independent module (torch SDPA, its own RoPE)
+    run in fp64 on the same bf16 weights, within the bf16 rounding of q/k/v and head outputs."""
+    import importlib
+    import __graft_entry__
+    vggt = importlib.import_module(__graft_entry__.package().__name__ + ".vggt")
+    G2, x, w_qkv, b_qkv, ln, w_p, b_p, pos = _layer_inputs()
+    C = x.shape[1]
+    m = vggt.Attention(C, 4, qkv_bias=True, proj_bias=True, qk_norm=True, rope=vggt.RotaryPositionEmbedding2D(100.0))
+    with torch.no_grad():
+        m.qkv.weight.copy_(w_qkv.to(torch.bfloat16).float())
+        m.qkv.bias.copy_(b_qkv.to(torch.bfloat16).float())
+        m.proj.weight.copy_(w_p.to(torch.bfloat16).float())
+        m.proj.bias.copy_(b_p.to(torch.bfloat16).float())
+        for n in (m.q_norm, m.k_norm):
+            n.weight.copy_(ln[0])
+            n.bias.copy_(ln[1])
+        m = m.double()
+        exp = m(x.double()[None], pos[None])[0]
+    y, _ = A.reference_layer(x, w_qkv, b_qkv, ln, ln, w_p, b_p, pos, [{"mode": "full"}] * 4, G2)
+    torch.testing.assert_close(y, exp, rtol=0, atol=3e-2)
+    assert (y - exp).abs().mean() < 3e-3
+    # a transposed head split or a dropped RoPE term is far outside that bound
+    y2, _ = A.reference_layer(x, w_qkv, b_qkv, ln, ln, w_p, b_p, torch.zeros_like(pos), [{"mode": "full"}] * 4, G2)
+    assert (y2 - exp).abs().max() > 0.1
+
+
+def test_reference_layer_mode_identities():
+    """Key sets that cover every key reduce to 'full'; frame-local rows ignore other frames;
+    a skipped head contributes nothing but the projection bias; broadcast_first on one frame is
+    'full' up to its bf16 score rounding; dino rows over every image token exclude only specials."""
+    G2, x, w_qkv, b_qkv, ln, w_p, b_p, pos = _layer_inputs()
+    N, T = G2.tokens, G2.tokens_per_frame
+    args = (x, w_qkv, b_qkv, ln, ln, w_p, b_p, pos)
+    full, _ = A.reference_layer(*args, [{"mode": "full"}] * 4, G2)
+    cover = [{"mode": "stride", "stride": 1}, {"mode": "q_probe_topk", "topk": N},
+             {"mode": "q_probe_topk", "stride": 1, "include_as": True}, {"mode": "full"}]
+    y, info = A.reference_layer(*args, cover, G2)
+    torch.testing.assert_close(y, full, rtol=0, atol=1e-12)
+    assert all(len(info["keysets"][h]) == N for h in range(3))
+    # the probe key set is the top-k of the fp32 mean-query scores
+    few = [{"mode": "q_probe_topk", "topk": 7}] + [{"mode": "full"}] * 3
+    _, inf2 = A.reference_layer(*args, few, G2)
+    assert len(inf2["keysets"][0]) == 7
+    # skip: the head's columns of attn are zero, so y differs from full by that head's share only
+    sk = [{"mode": "skip"}] + [{"mode": "full"}] * 3
+    ys, _ = A.reference_layer(*args, sk, G2)
+    assert (ys - full).abs().max() > 1e-3
+    # frame-local rows of frame 1 do not depend on frame 0's tokens
+    fl = [{"mode": "global_to_frame"}] * 4
+    y1, _ = A.reference_layer(*args, fl, G2)
+    x2 = x.clone()
+    x2[:T] = torch.randn(T, x.shape[1]).to(torch.bfloat16).float()
+    y2, _ = A.reference_layer(x2, *args[1:], fl, G2)
+    torch.testing.assert_close(y1[T:], y2[T:], rtol=0, atol=1e-12)
+    # broadcast_first with one frame is full attention (bf16 scores and P)
+    G1 = A.Geometry(frames=1, tokens_per_frame=T)
+    b1, _ = A.reference_layer(x[:T], *args[1:-1], pos[:T], [{"mode": "broadcast_first"}] * 4, G1)
+    f1, _ = A.reference_layer(x[:T], *args[1:-1], pos[:T], [{"mode": "full"}] * 4, G1)
+    torch.testing.assert_close(b1, f1, rtol=0, atol=5e-2)
+    # dino rows listing every image token: image rows attend all image tokens (fp32 q/k), specials all keys
+    P = G2.patches
+    est = torch.arange(G2.frames * P, dtype=torch.int32)[None].repeat(G2.frames * P, 1)
+    dn = [{"mode": "dino_topk"}] * 4
+    yd, _ = A.reference_layer(*args, dn, G2, est_topk_idx=est)
+    yf, _ = A.reference_layer(*args, [{"mode": "full"}] * 4, G2)
+    spec = torch.tensor([f * T + i for f in range(G2.frames) for i in range(5)])
+    torch.testing.assert_close(yd[spec], yf[spec], rtol=0, atol=1e-12)
+    assert (yd - yf).abs().max() > 1e-4  # image rows exclude the special keys

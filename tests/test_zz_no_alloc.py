@@ -19,15 +19,16 @@ def mods(pkg):
     return importlib.import_module(pkg.__name__ + ".ops"), importlib.import_module(pkg.__name__ + "._lib")
 
 
-def _probe(lib, L, noalloc, qp, kp, geom, heads, sample):
-    n = len(heads)
-    hs = torch.tensor(heads, dtype=torch.int32, device=DEV)
+def _probe(lib, L, noalloc, qk32, slots, sample):
+    """Both probe entries through ctypes on fp32 q / k rows qk32 [n, 2, N, 64]."""
+    n, N = len(slots), qk32.shape[2]
+    hs = torch.tensor(slots, dtype=torch.int32, device=DEV)
     qbar = torch.full((n, 64), float("nan"), device=DEV)
-    scores = torch.full((n, geom.tokens + 3), float("nan"), device=DEV)
+    scores = torch.full((n, N + 3), float("nan"), device=DEV)
     sp = ctypes.c_void_p(0 if sample is None else sample.data_ptr())
     ns = 0 if sample is None else sample.numel()
-    args = (ctypes.c_void_p(qp.data_ptr()), ctypes.c_void_p(kp.data_ptr()), geom.frames, geom.tokens_per_frame,
-            geom.num_special, ctypes.c_void_p(hs.data_ptr()), n, sp, ns, 0.125)
+    args = (ctypes.c_void_p(qk32.data_ptr()), ctypes.c_void_p(qk32[:, 1].data_ptr()), qk32.stride(0), N,
+            ctypes.c_void_p(hs.data_ptr()), n, sp, ns, 0.125)
     outs = (ctypes.c_void_p(qbar.data_ptr()), ctypes.c_void_p(scores.data_ptr()), scores.stride(0), L.stream_ptr())
     if noalloc:
         rc = lib.saf3r_probe_scores_noalloc(*args, *outs)
@@ -36,24 +37,22 @@ def _probe(lib, L, noalloc, qp, kp, geom, heads, sample):
         rc = lib.saf3r_probe_scores(*args, ctypes.c_void_p(partial.data_ptr()), *outs)
     L.check(rc)
     torch.cuda.synchronize()
-    return qbar.cpu(), scores[:, :geom.tokens].cpu()
+    return qbar.cpu(), scores[:, :N].cpu()
 
 
 @pytest.mark.parametrize("order", ["large_then_small"])
 def test_noalloc_probe_matches_workspace_entry(mods, pkg, order):
     ops, L = mods
     lib = L.load()
-    cases = [(pkg.Geometry(6, 1374, 5), [5, 0, 3, 7, 1, 2, 6, 4], None),          # 8 heads, every token
-             (pkg.Geometry(2, 155, 5), [1, 2], torch.tensor([0, 7, 150, 309], dtype=torch.int32))]  # smaller
-    for i, (geom, heads, sample) in enumerate(cases):
-        print(f"call {i}: {geom} heads {heads} sample {None if sample is None else sample.tolist()}", flush=True)
+    cases = [(6 * 1374, [5, 0, 3, 7, 1, 2, 6, 4], None),                          # 8 heads, every token
+             (2 * 155, [1, 2], torch.tensor([0, 7, 150, 309], dtype=torch.int32))]  # smaller, sampled rows
+    for i, (N, slots, sample) in enumerate(cases):
+        print(f"call {i}: N {N} slots {slots} sample {None if sample is None else sample.tolist()}", flush=True)
         g = torch.Generator().manual_seed(20 + i)
-        H = max(heads) + 1
-        q, k, v = ((torch.randn(H, geom.tokens, 64, generator=g) * 2).to(torch.bfloat16) for _ in range(3))
-        qp, kp, _ = ops.pack_heads(q.to(DEV), k.to(DEV), v.to(DEV), geom)
+        qk32 = (torch.randn(max(slots) + 1, 2, N, 64, generator=g) * 2).to(DEV)
         s = None if sample is None else sample.to(DEV)
-        want_q, want_s = _probe(lib, L, False, qp, kp, geom, heads, s)
-        got_q, got_s = _probe(lib, L, True, qp, kp, geom, heads, s)
+        want_q, want_s = _probe(lib, L, False, qk32, slots, s)
+        got_q, got_s = _probe(lib, L, True, qk32, slots, s)
         assert np.array_equal(got_q.numpy().view(np.uint32), want_q.numpy().view(np.uint32)), f"qbar, call {i}"
         assert np.array_equal(got_s.numpy().view(np.uint32), want_s.numpy().view(np.uint32)), f"scores, call {i}"
         assert torch.isfinite(got_s).all()
@@ -63,5 +62,5 @@ def test_noalloc_probe_rejects_more_heads_than_the_workspace(mods, pkg):
     ops, L = mods
     lib = L.load()
     dev = ctypes.c_void_p(16)
-    rc = lib.saf3r_probe_scores_noalloc(dev, dev, 2, 100, 5, dev, 65, None, 0, 0.125, dev, dev, 200, None)
+    rc = lib.saf3r_probe_scores_noalloc(dev, dev, 200 * 64, 200, dev, 65, None, 0, 0.125, dev, dev, 200, None)
     assert rc == 2 and b"static workspace" in lib.saf3r_last_error()
