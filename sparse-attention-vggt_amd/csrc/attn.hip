@@ -98,21 +98,9 @@ __device__ inline float partner_sum(float x) {
   return __builtin_bit_cast(float, (uint32_t)r[0]) + __builtin_bit_cast(float, (uint32_t)r[1]);
 }
 
-__device__ inline void barrier_only() {
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
-
-// XOR swizzles of the 16-byte chunk index. 128-byte rows (8 chunks): rows r and r ^ 8 get
-// different masks, so 16 lanes reading 16 consecutive rows at one logical chunk hit 16 distinct
-// 16-byte bank groups whether the LDS serves 8 lanes over 32 banks or 16 lanes over 64 banks.
-// 64-byte rows (4 chunks) use the analogous mask.
 // high word of a 32 x 32-bit product as one multiply instruction (the __umulhi library routine is
 // an out-of-line call here, with the call's register saves, once per use)
 __device__ __forceinline__ uint32_t mulhi_u32(uint32_t a, uint32_t b) { return (uint32_t)(((uint64_t)a * b) >> 32); }
-
-__device__ inline int swz8(int r) { return (r & 7) ^ ((r >> 3) & 1); }
-__device__ inline int swz4(int r) { return ((r >> 1) & 3) ^ ((r >> 3) & 1); }
 
 struct Acc {
   f32x16 o[2][2];  // [dh][gq]: O^T rows 32*dh + (16*half + a), query 32*gq + col

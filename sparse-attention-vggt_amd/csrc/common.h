@@ -30,6 +30,25 @@ __device__ __forceinline__ int bid_z() { return (int)__builtin_amdgcn_workgroup_
 // LDS pointer type of the LDS-DMA loads (__builtin_amdgcn_global_load_lds)
 typedef __attribute__((address_space(3))) void lds_void;
 
+// 32-bit LDS address of a __shared__ object
+__device__ inline uint32_t lds_addr(const void* p) { return (uint32_t)(uintptr_t)(const lds_void*)p; }
+
+// LDS-DMA load of 16 bytes per lane: lane i's bytes at global src land at LDS lds_base + 16 i
+// (lds_base wave-uniform). Written as inline assembly so that the compiler does not see an LDS
+// write: after __builtin_amdgcn_global_load_lds it treats every later LDS read of the kernel as
+// possibly aliasing the DMA destination and waits for vmcnt(0) before it, which drains a load
+// ring every step. The caller orders reads of the destination itself (wait_vm, then a barrier).
+__device__ inline void dma16(const void* src, uint32_t lds_base) {
+  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(lds_base) : "memory");
+}
+// The same in the scalar-base form: wave-uniform base, per-lane 32-bit byte offset, and an
+// immediate IMM that moves the global and the LDS address alike.
+template <int IMM = 0>
+__device__ inline void dma16s(const void* base, uint32_t off, uint32_t lds_base) {
+  asm volatile("global_load_lds_dwordx4 %0, %1 offset:%2" ::"v"(off), "s"(base), "i"(IMM), "{m0}"(lds_base)
+               : "memory");
+}
+
 // s_waitcnt on vmcnt only (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14]),
 // followed by a compiler barrier so no LDS read is hoisted above it.
 template <int N>
@@ -37,6 +56,21 @@ __device__ inline void wait_vm() {
   __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
   asm volatile("" ::: "memory");
 }
+
+// s_barrier without the workgroup fences of __syncthreads(): those make the compiler wait for
+// every outstanding LDS-DMA load (vmcnt(0)) before the barrier, which serialises a load ring. The
+// caller waits for what it needs (wait_vm) first; the clobber keeps LDS accesses on their side.
+__device__ inline void barrier_only() {
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// XOR swizzles of the 16-byte chunk index. 128-byte rows (8 chunks): rows r and r ^ 8 get
+// different masks, so 16 lanes reading 16 consecutive rows at one logical chunk hit 16 distinct
+// 16-byte bank groups whether the LDS serves 8 lanes over 32 banks or 16 lanes over 64 banks.
+// 64-byte rows (4 chunks) use the analogous mask.
+__device__ inline int swz8(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+__device__ inline int swz4(int r) { return ((r >> 1) & 3) ^ ((r >> 3) & 1); }
 
 constexpr int kHeadDim = 64;
 constexpr int kBlock = 64;

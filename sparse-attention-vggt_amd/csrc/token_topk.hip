@@ -6,9 +6,9 @@
 //      :120-217 (API: q [B, Nq, D], k [B, Nk, D], Nk = frames * num_toks_per_img, output
 //      int32 [B, Nq, frames * min(topk, num_toks_per_img)] of key indices).
 // A 256-thread workgroup owns 128 queries (32 per wave). Key tiles of 64 keys are staged in LDS,
-// scored with v_mfma_f32_32x32x16_bf16 (S^T = K . Q^T), and every lane keeps a running top-k of
-// the 32 keys of the tile it holds; the two lane halves of a query merge their lists when the
-// frame ends.
+// scored with v_mfma_f32_32x32x16_bf16 (S^T = K . Q^T); a lane holds one query and 32 keys of each
+// tile, and keeps a running top-k of the keys of its half; the two lane halves of a query merge
+// their lists when the frame ends. Each frame is scored twice (see token_topk_kernel).
 #include <type_traits>
 
 #include "common.h"
@@ -22,6 +22,7 @@ struct TopkParams {
   int64_t k_rs, k_base, k_rpf, k_frs;
   int nq, F, P, ke;
   int kmode;  // key row of (frame f, token j): 1 = frame f row j (rows_per_frame == P), 0 = flat row f*P + j, 2 = general
+  int64_t k_fst;  // kmode 0 and 1: rows from frame f to frame f + 1 (P or frame_row_stride)
   int32_t* idx;
 };
 
@@ -42,10 +43,53 @@ __device__ inline uint64_t partner_u64(uint64_t x) {
   return ((uint64_t)phi << 32) | plo;
 }
 
+// Candidate buffer of pass 2: per lane up to kCand candidates (float bits << 32 | key index), entry i
+// of thread tid at cbuf[i * 256 + tid] (a lane's entries all sit in its own bank pair: no conflicts
+// whatever the fill levels), emptied into the lane's running top-K at the end of each frame. A lane
+// with more candidates than that in one frame (ties on a large scale) loses the rest and has its
+// frame recomputed directly at the frame's end (see token_topk_kernel).
 template <int K>
-__global__ __launch_bounds__(256) void token_topk_kernel(TopkParams p) {
-  __shared__ __align__(16) char kbuf[2][8192];
-  const int tid = tid_x(), lane = tid & 63, w = tid >> 6, half = lane >> 5, col = lane & 31;
+constexpr int cand_cap() { return K <= 8 ? 12 : 24; }
+constexpr int kStages = 3;  // K tiles in flight: the tile of step t + 2 loads while step t computes
+
+// K-th largest of the running float list t (descending, -inf = empty) after inserting x.
+template <int K>
+__device__ inline void fmax_insert(float (&t)[K], float x) {
+  bool c[K];
+#pragma unroll
+  for (int i = 0; i < K; ++i) c[i] = x > t[i];
+#pragma unroll
+  for (int i = K - 1; i > 0; --i) t[i] = c[i - 1] ? t[i - 1] : (c[i] ? x : t[i]);
+  t[0] = c[0] ? x : t[0];
+}
+
+// Two passes per key frame over the same bf16 MFMA scores (the score of a (query, key) pair is the
+// same sequence of MFMAs in both, so the same fp32 value):
+//   pass 1: every lane keeps the maximum of G groups of its candidates; the K-th largest of the 2G
+//           group maxima of a query (its two lane halves) is a lower bound tau of the query's K-th
+//           best score in the frame (they are 2G >= K distinct candidates);
+//   pass 2: only candidates with score >= tau (or unordered: a NaN never drops out) are appended to
+//           the lane's LDS buffer; a candidate costs one compare and a wave-uniform branch unless
+//           some lane of the wave keeps it. A lane whose buffer overflowed in the frame is served
+//           at the frame's end by a direct pass of its wave over the frame's key rows in global
+//           memory (same MFMAs, so the same scores) that inserts every candidate >= tau.
+// A few candidates per query and frame pass (about 3 of 1369 for top-4 of N(0,1) scores), so the
+// composite-key insertion that dominates a one-pass selection runs a few times per frame instead
+// of for every candidate. Key tiles stream through a 3-stage LDS ring filled by LDS-DMA loads
+// issued two steps ahead (rows past the frame's end load a valid row; their scores are masked).
+// Step t reads its K fragments, selects over the scores of step t - 1 while those reads are in
+// flight, then issues its MFMAs into the same registers; the two waves of a SIMD alternate their
+// VALU and MFMA phases.
+template <int K, bool FLAT>
+__global__ __launch_bounds__(256, K <= 8 ? 3 : 2) void token_topk_kernel(TopkParams p) {
+  // groups per lane (2G >= K maxima per query): more groups give a tighter tau for larger K, so that
+  // the candidates of a lane fit its buffer
+  constexpr int G = K <= 4 ? 4 : 2 * K;
+  __shared__ __align__(16) char ring[kStages][8192];
+  constexpr int kCand = cand_cap<K>();
+  __shared__ uint64_t cbuf[(kCand + 1) * 256];
+  const int tid = tid_x(), lane = tid & 63, half = lane >> 5, col = lane & 31;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t q0 = (int64_t)bid_x() * 128;
   const int64_t qi = q0 + 32 * w + col;
   const bool qvalid = qi < p.nq;
@@ -59,111 +103,224 @@ __global__ __launch_bounds__(256) void token_topk_kernel(TopkParams p) {
   }
 
   const int tiles_pf = (p.P + 63) / 64;
-  const int total = p.F * tiles_pf;
-  u32x4 kreg[2];
-  auto load_tile = [&](int f, int u) {
+  const int total = p.F * 2 * tiles_pf;  // frame f: pass 1 over its tiles, then pass 2
+  // LDS chunk position P = 256 j + 64 w + lane of a tile (instruction j of wave w) holds key row
+  // P / 8, global 16-byte chunk (P % 8) ^ swz8(row): the swizzle that makes the MFMA fragment
+  // reads conflict-free is applied on the load side
+  int rowj[2], chj[2];
 #pragma unroll
-    for (int e = 0; e < 2; ++e) {
-      const int id = tid + 256 * e, r = id >> 3, ch = id & 7;
-      const int pp = 64 * u + r;
-      if (pp < p.P) {
-        // the frame / row split of the key row without a 64-bit division where the layout allows
-        const __bf16* row = p.kmode == 1   ? p.kptr + (p.k_base + (int64_t)f * p.k_frs + pp) * p.k_rs
-                            : p.kmode == 0 ? p.kptr + (p.k_base + (int64_t)f * p.P + pp) * p.k_rs
-                                           : rows_at(p.kptr, p.k_rs, p.k_base, p.k_rpf, p.k_frs, (int64_t)f * p.P + pp);
-        const u32x4* src = reinterpret_cast<const u32x4*>(row);
-        kreg[e] = src[ch];
-      } else {
-        kreg[e] = u32x4{0, 0, 0, 0};
+  for (int j = 0; j < 2; ++j) {
+    const int P = 256 * j + 64 * w + lane;
+    rowj[j] = P >> 3;
+    chj[j] = (P & 7) ^ swz8(rowj[j]);
+  }
+  int iu = 0, ips = 0;  // tile and pass of the next step to issue
+  int64_t ifr = 0;      // its frame
+  // FLAT (kmode 0 and 1): frame f's rows are k_fst rows apart, so a tile's address is a uniform
+  // base plus a fixed 32-bit lane offset (the last tile of a frame clamps its rows to the frame's
+  // last row: its own offsets); otherwise every row goes through the general row mapping
+  const char* kb0 = reinterpret_cast<const char*>(p.kptr + p.k_base * p.k_rs);
+  const int64_t fbytes = p.k_fst * p.k_rs * 2, tbytes = 64 * p.k_rs * 2;
+  uint32_t lo[2], lo_last[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    lo[j] = (uint32_t)(rowj[j] * p.k_rs * 2 + 16 * chj[j]);
+    const int rl = min(64 * (tiles_pf - 1) + rowj[j], p.P - 1) - 64 * (tiles_pf - 1);
+    lo_last[j] = (uint32_t)(rl * p.k_rs * 2 + 16 * chj[j]);
+  }
+  // the tile of sequence step `step` (the next one) into its stage; past the last step the last
+  // frame's last tile is loaded again into a stage nobody reads, so every step waits on the same
+  // count of loads
+  auto issue = [&](int step) __attribute__((always_inline)) {
+    char* st = ring[step % kStages];
+    if constexpr (FLAT) {
+      const char* tb = kb0 + ifr * fbytes + iu * tbytes;
+      const bool last = iu == tiles_pf - 1;
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        dma16s(tb, last ? lo_last[j] : lo[j], __builtin_amdgcn_readfirstlane(lds_addr(st + 4096 * j + 1024 * w)));
+    } else {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int pp = min(64 * iu + rowj[j], p.P - 1);
+        const __bf16* row = rows_at(p.kptr, p.k_rs, p.k_base, p.k_rpf, p.k_frs, ifr * p.P + pp);
+        dma16(row + 8 * chj[j], __builtin_amdgcn_readfirstlane(lds_addr(st + 4096 * j + 1024 * w)));
       }
     }
-  };
-  auto store_tile = [&](int buf) {
-#pragma unroll
-    for (int e = 0; e < 2; ++e) {
-      const int id = tid + 256 * e, r = id >> 3, ch = id & 7;
-      *reinterpret_cast<u32x4*>(&kbuf[buf][r * 128 + ((ch ^ (r & 7)) << 4)]) = kreg[e];
+    if (step + 1 < total && ++iu == tiles_pf) {
+      iu = 0;
+      ifr += ips;
+      ips ^= 1;
     }
   };
 
-  // running top-k of the lane's even and of its odd candidates of the frame: two independent
-  // branch-free insertion chains whose instructions interleave (one chain alone waits on the
-  // compare-to-select hazards); keys are distinct, so merging the two lists loses nothing
-  uint64_t a[K], b2[K];
+  uint64_t a[K];  // the lane's running top-K of its half of the frame (composite keys, 0 = empty)
 #pragma unroll
-  for (int t = 0; t < K; ++t) a[t] = b2[t] = 0;
-
-  load_tile(0, 0);
-  store_tile(0);
-  __syncthreads();
-  int f = 0, u = 0;  // frame and tile of step t
-  for (int t = 0; t < total; ++t) {
-    const int cur = t & 1;
-    const int un = u + 1 == tiles_pf ? 0 : u + 1, fn = u + 1 == tiles_pf ? f + 1 : f;
-    if (t + 1 < total) load_tile(fn, un);
-    f32x16 s0 = {}, s1 = {};
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const int chn = 4 * half + s;
-      const int r0 = col, r1 = 32 + col;
-      bf16x8 ka = *reinterpret_cast<const bf16x8*>(&kbuf[cur][r0 * 128 + ((chn ^ (r0 & 7)) << 4)]);
-      bf16x8 kb = *reinterpret_cast<const bf16x8*>(&kbuf[cur][r1 * 128 + ((chn ^ (r1 & 7)) << 4)]);
-      s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qfrag[s], s0, 0, 0, 0);
-      s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kb, qfrag[s], s1, 0, 0, 0);
+  for (int t = 0; t < K; ++t) a[t] = 0;
+  float gmax[G];
+  float tau = -__builtin_inff();
+  int cnt = 0;  // candidates of this lane in the frame so far (entries held: min(cnt, kCand))
+  auto flush = [&]() __attribute__((always_inline)) {
+    const int n = min(cnt, kCand);
+    for (int i = 0; i < n; ++i) {
+      const uint64_t ent = cbuf[i * 256 + tid];
+      topk_insert<K>(a, ckey(__builtin_bit_cast(float, (uint32_t)(ent >> 32)), (uint32_t)ent));
     }
-    // candidates of this lane (key 0 stands for a padding position: it never enters a list); only
-    // a frame's last tile can hold padding, so the other tiles skip the test
-    auto scan = [&](auto padded) {
-#pragma unroll
-      for (int e = 0; e < 32; e += 2) {
-        uint64_t x[2];
-#pragma unroll
-        for (int o = 0; o < 2; ++o) {
-          const float sv = e + o < 16 ? s0[e + o] : s1[e + o - 16];
-          const int r = (e + o) & 15;
-          const int key = 32 * ((e + o) >> 4) + 8 * (r >> 2) + 4 * half + (r & 3);
-          const int pp = 64 * u + key;
-          x[o] = ckey(sv, (uint32_t)pp);
-          if constexpr (decltype(padded)::value) x[o] = pp < p.P ? x[o] : 0ull;
-        }
-        topk_insert<K>(a, x[0]);
-        topk_insert<K>(b2, x[1]);
-      }
-    };
-    if (64 * u + 64 <= p.P) scan(std::false_type{});
-    else scan(std::true_type{});
-    if (u == tiles_pf - 1) {
-      // merge the odd list and the partner half's list, then flush this frame
-#pragma unroll
-      for (int e = 0; e < K; ++e) {
-        topk_insert<K>(a, b2[e]);
-        b2[e] = 0;
-      }
-      uint64_t b[K];
-#pragma unroll
-      for (int e = 0; e < K; ++e) b[e] = partner_u64(a[e]);
-#pragma unroll
-      for (int e = 0; e < K; ++e)
-        if (b[e] > a[K - 1]) topk_insert<K>(a, b[e]);
-      if (qvalid && half == 0) {
-        int32_t* o = p.idx + qi * ((int64_t)p.F * p.ke) + (int64_t)f * p.ke;
-#pragma unroll
-        for (int e = 0; e < K; ++e)
-          if (e < p.ke) o[e] = a[e] ? (int32_t)(f * p.P + ckey_index(a[e])) : -1;
-      }
+    cnt = 0;
+  };
+  // candidate e of this lane: key 32*(e>>4) + 8*((e&15)>>2) + 4*half + (e&3) of the tile
+  auto kpos = [](int e) { return 32 * (e >> 4) + 8 * ((e & 15) >> 2) + (e & 3); };
+  int f = 0, ps = 0, u = 0;  // frame, pass and tile of the step being selected
+  // Frame f again, for the lanes flagged `over`: every candidate >= tau goes straight into a[]. K
+  // fragments come from global memory (this lane's rows col and 32 + col of each tile, chunks
+  // 4 half .. 4 half + 3), the MFMAs run as in the main loop on the whole wave.
+  auto direct = [&](bool over) __attribute__((always_inline)) {
+    if (over) {
 #pragma unroll
       for (int e = 0; e < K; ++e) a[e] = 0;
     }
-    if (t + 1 < total) store_tile(cur ^ 1);
-    __syncthreads();
-    f = fn;
-    u = un;
+    for (int h2 = 0; h2 < 2 * tiles_pf; ++h2) {  // 32 keys at a time: rows 32 h2 + col
+      const int r = min(32 * h2 + col, p.P - 1);
+      const __bf16* row;
+      if constexpr (FLAT) row = reinterpret_cast<const __bf16*>(kb0 + f * fbytes) + (int64_t)r * p.k_rs;
+      else row = rows_at(p.kptr, p.k_rs, p.k_base, p.k_rpf, p.k_frs, (int64_t)f * p.P + r);
+      const u32x4* src = reinterpret_cast<const u32x4*>(row + 32 * half);
+      bf16x8 fa[4];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) fa[s] = __builtin_bit_cast(bf16x8, src[s]);
+      f32x16 d = {};
+#pragma unroll
+      for (int s = 0; s < 4; ++s) d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[s], qfrag[s], d, 0, 0, 0);
+      const int pb = 32 * h2 + 4 * half;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int pp = pb + kpos(e);
+        if (over && !(d[e] < tau) && pp < p.P) topk_insert<K>(a, ckey(d[e], (uint32_t)pp));
+      }
+    }
+  };
+  // PADDED: the frame's last tile holds positions past the frame's end, which never count
+  auto select = [&](auto padded_tag, const f32x16& s0, const f32x16& s1) __attribute__((always_inline)) {
+    constexpr bool PADDED = decltype(padded_tag)::value;
+    const int pbase = 64 * u + 4 * half;
+    const int lim = p.P - pbase;  // candidate e is a key of the frame when kpos(e) < lim
+    auto sc = [&](int e) { return e < 16 ? s0[e] : s1[e - 16]; };
+    if (ps == 0) {
+      if (u == 0) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) gmax[g] = -__builtin_inff();
+      }
+#pragma unroll
+      for (int e = 0; e < 32; ++e)
+        gmax[e % G] = fmaxf(gmax[e % G], (!PADDED || kpos(e) < lim) ? sc(e) : -__builtin_inff());
+      if (u == tiles_pf - 1) {
+        // K-th largest of this query's 2G group maxima (this lane's and its partner half's)
+        float top[K];
+#pragma unroll
+        for (int i = 0; i < K; ++i) top[i] = -__builtin_inff();
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          uint32_t b = __builtin_bit_cast(uint32_t, gmax[g]);
+          auto r = __builtin_amdgcn_permlane32_swap(b, b, false, false);
+          const float other = __builtin_bit_cast(float, (uint32_t)(half ? r[0] : r[1]));
+          fmax_insert<K>(top, gmax[g]);
+          fmax_insert<K>(top, other);
+        }
+        tau = top[K - 1];
+      }
+    } else {
+#pragma unroll
+      for (int e0 = 0; e0 < 32; e0 += 8) {
+        // the wave masks of 8 candidates first, then one uniform branch each: the compares' latency
+        // is paid once per 8
+        uint64_t bm[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i)  // >= tau, or unordered
+          bm[i] = __builtin_amdgcn_ballot_w64(!(sc(e0 + i) < tau) && (!PADDED || kpos(e0 + i) < lim));
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          if (bm[i]) {
+            // lanes that drop the candidate, or whose buffer is full, write the spare row kCand
+            const int e = e0 + i;
+            const bool keep = (bm[i] >> lane) & 1;
+            cbuf[(keep && cnt < kCand ? cnt : kCand) * 256 + tid] =
+                ((uint64_t)__builtin_bit_cast(uint32_t, sc(e)) << 32) | (uint32_t)(pbase + kpos(e));
+            cnt += keep;
+          }
+        }
+      }
+      if (u == tiles_pf - 1) {
+        // empty the buffer (or recompute an overflowed lane), merge the partner half's list, then
+        // write this frame's indices
+        const bool over = cnt > kCand;
+        if (__builtin_amdgcn_ballot_w64(over)) direct(over);
+        if (over) cnt = 0;
+        flush();
+        uint64_t b[K];
+#pragma unroll
+        for (int e = 0; e < K; ++e) b[e] = partner_u64(a[e]);
+#pragma unroll
+        for (int e = 0; e < K; ++e)
+          if (b[e] > a[K - 1]) topk_insert<K>(a, b[e]);
+        if (qvalid && half == 0) {
+          int32_t* o = p.idx + qi * ((int64_t)p.F * p.ke) + (int64_t)f * p.ke;
+#pragma unroll
+          for (int e = 0; e < K; ++e)
+            if (e < p.ke) o[e] = a[e] ? (int32_t)(f * p.P + ckey_index(a[e])) : -1;
+        }
+#pragma unroll
+        for (int e = 0; e < K; ++e) a[e] = 0;
+        tau = -__builtin_inff();
+      }
+    }
+    if (++u == tiles_pf) {
+      u = 0;
+      if (ps) ++f;
+      ps ^= 1;
+    }
+  };
+
+  wait_vm<0>();  // q fragments landed; from here vmcnt counts ring loads only
+  for (int s = 0; s < kStages - 1; ++s) issue(s);
+  f32x16 s0 = {}, s1 = {};  // scores of the previous step
+  for (int t = 0; t <= total; ++t) {
+    bf16x8 ka[4], kbf[4];
+    if (t < total) {
+      wait_vm<2 * (kStages - 2)>();  // tile t landed: only the loads of step t + 1 are pending
+      barrier_only();                // every wave's share of tile t is in LDS; every wave is done with tile t-1
+      issue(t + kStages - 1);
+      const char* kb = ring[t % kStages];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int chn = 4 * half + s;
+        const int r0 = col, r1 = 32 + col;
+        ka[s] = *reinterpret_cast<const bf16x8*>(&kb[r0 * 128 + ((chn ^ swz8(r0)) << 4)]);
+        kbf[s] = *reinterpret_cast<const bf16x8*>(&kb[r1 * 128 + ((chn ^ swz8(r1)) << 4)]);
+      }
+    }
+    if (t > 0) {
+      if (64 * u + 64 > p.P) select(std::true_type{}, s0, s1);
+      else select(std::false_type{}, s0, s1);
+    }
+    if (t < total) {
+      // S^T = K . Q^T over the staged tile: keys 0..31 in s0, 32..63 in s1
+      s0 = f32x16{};
+      s1 = f32x16{};
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[s], qfrag[s], s0, 0, 0, 0);
+        s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kbf[s], qfrag[s], s1, 0, 0, 0);
+      }
+    }
   }
+  wait_vm<0>();  // the trailing loads into unread stages land before the work-group's LDS is released
 }
 
 template <int K>
 static int launch_topk(const TopkParams& p, hipStream_t st) {
-  hipLaunchKernelGGL(token_topk_kernel<K>, dim3((unsigned)((p.nq + 127) / 128)), dim3(256), 0, st, p);
+  const dim3 grid((unsigned)((p.nq + 127) / 128));
+  if (p.kmode == 2) hipLaunchKernelGGL((token_topk_kernel<K, false>), grid, dim3(256), 0, st, p);
+  else hipLaunchKernelGGL((token_topk_kernel<K, true>), grid, dim3(256), 0, st, p);
   return check_launch("saf3r_token_topk");
 }
 
@@ -193,6 +350,9 @@ extern "C" int saf3r_token_topk(const saf3r_rows* q, const saf3r_rows* k, int n_
   p.k_rpf = k->rows_per_frame;
   p.k_frs = k->frame_row_stride;
   p.kmode = k->rows_per_frame == per_frame ? 1 : k->rows_per_frame >= (int64_t)frames * per_frame ? 0 : 2;
+  p.k_fst = p.kmode == 1 ? k->frame_row_stride : per_frame;
+  // the flat form addresses a frame's rows with 32-bit lane offsets from a tile base
+  if (p.kmode != 2 && ((int64_t)per_frame + 64) * k->row_stride * 2 >= ((int64_t)1 << 31)) p.kmode = 2;
   p.nq = n_q;
   p.F = frames;
   p.P = per_frame;

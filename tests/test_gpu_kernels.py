@@ -361,6 +361,23 @@ def test_token_topk_key_row_layouts(ops, layout):
     assert torch.equal(got, want)
 
 
+@pytest.mark.parametrize("topk", [1, 4, 16])
+def test_token_topk_mass_ties(ops, topk):
+    """Key frames made of three repeated rows: a third of a frame's scores tie exactly at the
+    frame's best value, so far more candidates than fit a lane's buffer reach the threshold; the
+    lowest indices of the best value win, as in the reference's composite key."""
+    frames, P, nq = 3, 700, 260
+    g = torch.Generator().manual_seed(5)
+    base = torch.randn(3, 64, generator=g).to(torch.bfloat16)
+    k = base[torch.randint(0, 3, (frames * P,), generator=g)]
+    q = torch.randn(nq, 64, generator=g).to(torch.bfloat16)
+    got = ops.token_topk(q.to(DEV), k.to(DEV), frames, P, topk).cpu()
+    torch.cuda.synchronize()
+    s = (q.double() @ k.double().T).float().numpy()
+    ref = OS.frame_topk(s, frames, topk)
+    assert np.array_equal(got.numpy(), ref)
+
+
 @pytest.mark.parametrize("frames,P,topk", [(4, 1369, 4), (3, 100, 8), (2, 30, 16), (5, 64, 1)])
 def test_token_topk(ops, frames, P, topk):
     g = torch.Generator().manual_seed(frames * P)
