@@ -84,7 +84,7 @@ template <int K, bool FLAT>
 __global__ __launch_bounds__(256, K <= 8 ? 3 : 2) void token_topk_kernel(TopkParams p) {
   // groups per lane (2G >= K maxima per query): more groups give a tighter tau for larger K, so that
   // the candidates of a lane fit its buffer
-  constexpr int G = K <= 4 ? 4 : 2 * K;
+  constexpr int G = K <= 4 ? 8 : 2 * K;
   __shared__ __align__(16) char ring[kStages][8192];
   constexpr int kCand = cand_cap<K>();
   __shared__ uint64_t cbuf[(kCand + 1) * 256];
@@ -160,6 +160,10 @@ __global__ __launch_bounds__(256, K <= 8 ? 3 : 2) void token_topk_kernel(TopkPar
   float gmax[G];
   float tau = -__builtin_inff();
   int cnt = 0;  // candidates of this lane in the frame so far (entries held: min(cnt, kCand))
+  // LDS byte address of this lane's next entry: row min(cnt, kCand) (row kCand is the spare row
+  // that absorbs writes past the buffer's end)
+  const uint32_t wa0 = lds_addr(cbuf) + 8 * tid, wspare = wa0 + 2048 * kCand;
+  uint32_t wa = wa0;
   auto flush = [&]() __attribute__((always_inline)) {
     const int n = min(cnt, kCand);
     for (int i = 0; i < n; ++i) {
@@ -167,6 +171,7 @@ __global__ __launch_bounds__(256, K <= 8 ? 3 : 2) void token_topk_kernel(TopkPar
       topk_insert<K>(a, ckey(__builtin_bit_cast(float, (uint32_t)(ent >> 32)), (uint32_t)ent));
     }
     cnt = 0;
+    wa = wa0;
   };
   // candidate e of this lane: key 32*(e>>4) + 8*((e&15)>>2) + 4*half + (e&3) of the tile
   auto kpos = [](int e) { return 32 * (e >> 4) + 8 * ((e & 15) >> 2) + (e & 3); };
@@ -240,11 +245,13 @@ __global__ __launch_bounds__(256, K <= 8 ? 3 : 2) void token_topk_kernel(TopkPar
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
           if (bm[i]) {
-            // lanes that drop the candidate, or whose buffer is full, write the spare row kCand
+            // every lane writes its next entry; only the lanes that keep the candidate advance (a
+            // full buffer stays on the spare row)
             const int e = e0 + i;
-            const bool keep = (bm[i] >> lane) & 1;
-            cbuf[(keep && cnt < kCand ? cnt : kCand) * 256 + tid] =
-                ((uint64_t)__builtin_bit_cast(uint32_t, sc(e)) << 32) | (uint32_t)(pbase + kpos(e));
+            const bool keep = !(sc(e) < tau) && (!PADDED || kpos(e) < lim);
+            const uint64_t ent = ((uint64_t)__builtin_bit_cast(uint32_t, sc(e)) << 32) | (uint32_t)(pbase + kpos(e));
+            *reinterpret_cast<__attribute__((address_space(3))) uint64_t*>(wa) = ent;
+            wa = min(wa + (keep ? 2048u : 0u), wspare);
             cnt += keep;
           }
         }
