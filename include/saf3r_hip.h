@@ -288,7 +288,9 @@ int saf3r_gather_attn_fwd(const saf3r_rows* q, const saf3r_rows* k, const saf3r_
  * Per-frame token top-k of q.k (bf16 inputs, fp32 MFMA accumulation).
  *   q: n_q rows; k: frames*per_frame rows (frame f = rows [f*per_frame, (f+1)*per_frame));
  *   idx: int32 [n_q][frames*min(topk, per_frame)] global key rows, frame-major, score descending,
- *   ties to the lower index. 1 <= topk <= 16.
+ *   ties to the lower index. topk >= 1 and min(topk, per_frame) <= 128 (the reference's limit);
+ *   above 16 per_frame <= 4096, and the call takes a stream-ordered workspace of at most 1 GiB
+ *   (hipMallocAsync / hipFreeAsync on `stream`) for the scores of a chunk of queries.
  * Replaces: saf3r/triton/fused_qk_topk.py:120-217 (compute_qk_topk_indices_fused).
  */
 int saf3r_token_topk(const saf3r_rows* q, const saf3r_rows* k, int n_q, int frames, int per_frame, int topk,

@@ -38,14 +38,18 @@ __device__ inline uint32_t lds_addr(const void* p) { return (uint32_t)(uintptr_t
 // write: after __builtin_amdgcn_global_load_lds it treats every later LDS read of the kernel as
 // possibly aliasing the DMA destination and waits for vmcnt(0) before it, which drains a load
 // ring every step. The caller orders reads of the destination itself (wait_vm, then a barrier).
+// A scalar write of M0 needs a wait state before a global load with LDS destination reads it; the
+// compiler writes M0 (the LDS base) just ahead of the statement but its hazard checks do not see
+// into it, so the statement starts with the wait states itself.
 __device__ inline void dma16(const void* src, uint32_t lds_base) {
-  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(lds_base) : "memory");
+  asm volatile("s_nop 1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(lds_base) : "memory");
 }
 // The same in the scalar-base form: wave-uniform base, per-lane 32-bit byte offset, and an
 // immediate IMM that moves the global and the LDS address alike.
 template <int IMM = 0>
 __device__ inline void dma16s(const void* base, uint32_t off, uint32_t lds_base) {
-  asm volatile("global_load_lds_dwordx4 %0, %1 offset:%2" ::"v"(off), "s"(base), "i"(IMM), "{m0}"(lds_base)
+  asm volatile("s_nop 1\n\tglobal_load_lds_dwordx4 %0, %1 offset:%2" ::"v"(off), "s"(base), "i"(IMM),
+               "{m0}"(lds_base)
                : "memory");
 }
 

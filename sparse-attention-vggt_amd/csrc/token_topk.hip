@@ -24,6 +24,11 @@ struct TopkParams {
   int kmode;  // key row of (frame f, token j): 1 = frame f row j (rows_per_frame == P), 0 = flat row f*P + j, 2 = general
   int64_t k_fst;  // kmode 0 and 1: rows from frame f to frame f + 1 (P or frame_row_stride)
   int32_t* idx;
+  // score dump (k > 16): queries q_begin .. nq - 1, score of (query qi, frame f, key j) at
+  // ws[(qi - q_begin) * F * ppad + f * ppad + j], ppad = frame length rounded up to 64
+  float* ws;
+  int64_t q_begin;
+  int ppad;
 };
 
 __device__ inline const __bf16* rows_at(const __bf16* ptr, int64_t rs, int64_t base, int64_t rpf, int64_t frs,
@@ -80,7 +85,7 @@ __device__ inline void fmax_insert(float (&t)[K], float x) {
 // Step t reads its K fragments, selects over the scores of step t - 1 while those reads are in
 // flight, then issues its MFMAs into the same registers; the two waves of a SIMD alternate their
 // VALU and MFMA phases.
-template <int K, bool FLAT>
+template <int K, bool FLAT, bool DUMP>
 __global__ __launch_bounds__(256, K <= 8 ? 3 : 2) void token_topk_kernel(TopkParams p) {
   // groups per lane (2G >= K maxima per query): more groups give a tighter tau for larger K, so that
   // the candidates of a lane fit its buffer
@@ -90,7 +95,7 @@ __global__ __launch_bounds__(256, K <= 8 ? 3 : 2) void token_topk_kernel(TopkPar
   __shared__ uint64_t cbuf[(kCand + 1) * 256];
   const int tid = tid_x(), lane = tid & 63, half = lane >> 5, col = lane & 31;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int64_t q0 = (int64_t)bid_x() * 128;
+  const int64_t q0 = p.q_begin + (int64_t)bid_x() * 128;
   const int64_t qi = q0 + 32 * w + col;
   const bool qvalid = qi < p.nq;
 
@@ -103,7 +108,9 @@ __global__ __launch_bounds__(256, K <= 8 ? 3 : 2) void token_topk_kernel(TopkPar
   }
 
   const int tiles_pf = (p.P + 63) / 64;
-  const int total = p.F * 2 * tiles_pf;  // frame f: pass 1 over its tiles, then pass 2
+  // frame f: pass 1 over its tiles, then pass 2; DUMP: one pass over frame bid_y that stores the
+  // scores (a work-group per 128 queries and frame)
+  const int total = DUMP ? tiles_pf : p.F * 2 * tiles_pf;
   // LDS chunk position P = 256 j + 64 w + lane of a tile (instruction j of wave w) holds key row
   // P / 8, global 16-byte chunk (P % 8) ^ swz8(row): the swizzle that makes the MFMA fragment
   // reads conflict-free is applied on the load side
@@ -115,7 +122,7 @@ __global__ __launch_bounds__(256, K <= 8 ? 3 : 2) void token_topk_kernel(TopkPar
     chj[j] = (P & 7) ^ swz8(rowj[j]);
   }
   int iu = 0, ips = 0;  // tile and pass of the next step to issue
-  int64_t ifr = 0;      // its frame
+  int64_t ifr = DUMP ? bid_y() : 0;  // its frame
   // FLAT (kmode 0 and 1): frame f's rows are k_fst rows apart, so a tile's address is a uniform
   // base plus a fixed 32-bit lane offset (the last tile of a frame clamps its rows to the frame's
   // last row: its own offsets); otherwise every row goes through the general row mapping
@@ -149,7 +156,7 @@ __global__ __launch_bounds__(256, K <= 8 ? 3 : 2) void token_topk_kernel(TopkPar
     }
     if (step + 1 < total && ++iu == tiles_pf) {
       iu = 0;
-      ifr += ips;
+      ifr += DUMP ? 1 : ips;
       ips ^= 1;
     }
   };
@@ -175,7 +182,7 @@ __global__ __launch_bounds__(256, K <= 8 ? 3 : 2) void token_topk_kernel(TopkPar
   };
   // candidate e of this lane: key 32*(e>>4) + 8*((e&15)>>2) + 4*half + (e&3) of the tile
   auto kpos = [](int e) { return 32 * (e >> 4) + 8 * ((e & 15) >> 2) + (e & 3); };
-  int f = 0, ps = 0, u = 0;  // frame, pass and tile of the step being selected
+  int f = DUMP ? bid_y() : 0, ps = 0, u = 0;  // frame, pass and tile of the step being selected
   // Frame f again, for the lanes flagged `over`: every candidate >= tau goes straight into a[]. K
   // fragments come from global memory (this lane's rows col and 32 + col of each tile, chunks
   // 4 half .. 4 half + 3), the MFMAs run as in the main loop on the whole wave.
@@ -210,7 +217,21 @@ __global__ __launch_bounds__(256, K <= 8 ? 3 : 2) void token_topk_kernel(TopkPar
     const int pbase = 64 * u + 4 * half;
     const int lim = p.P - pbase;  // candidate e is a key of the frame when kpos(e) < lim
     auto sc = [&](int e) { return e < 16 ? s0[e] : s1[e - 16]; };
-    if (ps == 0) {
+    if constexpr (DUMP) {
+      // keys pbase + kpos(4 i) .. + 3 are consecutive: one 16-byte store each (the rows past the
+      // frame's end land in the row's padding)
+      if (qvalid) {
+        float* o = p.ws + (qi - p.q_begin) * ((int64_t)p.F * p.ppad) + (int64_t)f * p.ppad + pbase;
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          *reinterpret_cast<f32x4*>(o + kpos(4 * i)) = f32x4{sc(4 * i), sc(4 * i + 1), sc(4 * i + 2), sc(4 * i + 3)};
+      }
+      if (++u == tiles_pf) {
+        u = 0;
+        ++f;
+      }
+      return;
+    } else if (ps == 0) {
       if (u == 0) {
 #pragma unroll
         for (int g = 0; g < G; ++g) gmax[g] = -__builtin_inff();
@@ -326,9 +347,149 @@ __global__ __launch_bounds__(256, K <= 8 ? 3 : 2) void token_topk_kernel(TopkPar
 template <int K>
 static int launch_topk(const TopkParams& p, hipStream_t st) {
   const dim3 grid((unsigned)((p.nq + 127) / 128));
-  if (p.kmode == 2) hipLaunchKernelGGL((token_topk_kernel<K, false>), grid, dim3(256), 0, st, p);
-  else hipLaunchKernelGGL((token_topk_kernel<K, true>), grid, dim3(256), 0, st, p);
+  if (p.kmode == 2) hipLaunchKernelGGL((token_topk_kernel<K, false, false>), grid, dim3(256), 0, st, p);
+  else hipLaunchKernelGGL((token_topk_kernel<K, true, false>), grid, dim3(256), 0, st, p);
   return check_launch("saf3r_token_topk");
+}
+
+// ---- per-frame top-k for 16 < k <= 128 (the reference's range): scores, then a selection ----
+constexpr int kLargeMaxP = 4096;  // frame length of that path (values of a segment held by one wave)
+
+// One wave per (query row, frame) segment of P <= 64 NV stored scores. The ke-th largest composite
+// key (sortable float key << 32 | reversed index, the order of the reference's fused top-k) is
+// found by a radix select over the float keys, eight 4-bit digits from the top: every lane counts
+// its own keys into its own 16 LDS bins (bin b of lane l at word 64 b + l: no two lanes share a
+// bank or a word, so the adds never contend), then the wave sums each bin and picks the digit.
+// Keys above the threshold value all count, keys equal to it count from the lowest index on. Each
+// selected key's position is the number of selected keys above it.
+template <int NV>
+__global__ __launch_bounds__(256) void topk_large_kernel(const float* __restrict__ ws, int64_t q_begin, int64_t q_end,
+                                                          int F, int P, int ppad, int ke, int32_t* __restrict__ idx) {
+  __shared__ uint32_t hist[4][16 * 64];
+  __shared__ uint64_t sel[4][128];
+  const int lane = tid_x() & 63, w = tid_x() >> 6;
+  const int64_t seg = (int64_t)bid_x() * 4 + w;
+  if (seg >= (q_end - q_begin) * F) return;  // a whole wave leaves; no work-group barrier follows
+  const int64_t r = seg / F;
+  const int f = (int)(seg - r * F);
+  const float* src = ws + r * ((int64_t)F * ppad) + (int64_t)f * ppad;
+  uint32_t key[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int j = lane + 64 * i;
+    key[i] = j < P ? fkey(src[j]) : 0;
+  }
+  uint32_t* hw = hist[w];
+  uint32_t prefix = 0, mask = 0;
+  int need = ke;  // keys still to take at or below the current prefix
+  const int b = lane & 15, g = lane >> 4;  // the bin this lane sums, and its quarter of the lanes
+#pragma unroll 1
+  for (int sh = 28; sh >= 0; sh -= 4) {
+#pragma unroll
+    for (int t = 0; t < 16; ++t) hw[64 * t + lane] = 0;
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+      if (lane + 64 * i < P && (key[i] & mask) == prefix) atomicAdd(&hw[64 * ((key[i] >> sh) & 15) + lane], 1u);
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this lane's counts are in
+    __builtin_amdgcn_wave_barrier();
+    // total of bin b: lanes 16 g .. 16 g + 15 here, the other quarters through two exchanges
+    const u32x4* hb = reinterpret_cast<const u32x4*>(hw + 64 * b + 16 * g);
+    uint32_t tot = 0;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const u32x4 x = hb[t];
+      tot += x[0] + x[1] + x[2] + x[3];
+    }
+    tot += __shfl_xor(tot, 16);
+    tot += __shfl_xor(tot, 32);
+    // keys in bins above b (lanes b + 1 .. 15 of the first quarter hold them)
+    uint32_t incl = tot;
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) {
+      const uint32_t y = __shfl_down(incl, o, 16);
+      if (b + o < 16) incl += y;
+    }
+    const uint32_t above = incl - tot;
+    const bool hit = lane < 16 && above < (uint32_t)need && (uint32_t)need <= incl;
+    const uint64_t m = __ballot(hit);
+    const int src_lane = (int)__builtin_ctzll(m);
+    const int digit = __shfl(b, src_lane);
+    need -= (int)__shfl(above, src_lane);
+    prefix |= (uint32_t)digit << sh;
+    mask |= 0xFu << sh;
+    __builtin_amdgcn_wave_barrier();
+  }
+  // selected: keys above the threshold value, and the first `need` keys equal to it, by index
+  int cnt = 0, eqseen = 0;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int j = lane + 64 * i;
+    const bool valid = j < P;
+    const bool gt = valid && key[i] > prefix, eq = valid && key[i] == prefix;
+    const uint64_t meq = __ballot(eq);
+    const int req = eqseen + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(meq >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)meq, 0));
+    const bool take = gt || (eq && req < need);
+    const uint64_t mt = __ballot(take);
+    const int pos = cnt + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mt >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mt, 0));
+    if (take) sel[w][pos] = ((uint64_t)key[i] << 32) | (uint64_t)(0xFFFFFFFEu - (uint32_t)j);
+    cnt += __popcll(mt);
+    eqseen += __popcll(meq);
+  }
+  __builtin_amdgcn_s_waitcnt(0xc07f);
+  __builtin_amdgcn_wave_barrier();
+  int32_t* o = idx + (q_begin + r) * ((int64_t)F * ke) + (int64_t)f * ke;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int e = lane + 64 * h;
+    if (e < ke) {
+      const uint64_t x = sel[w][e];
+      int rank = 0;
+      for (int t = 0; t < ke; ++t) rank += sel[w][t] > x;
+      o[rank] = f * P + (int)ckey_index(x);
+    }
+  }
+}
+
+static int token_topk_large(TopkParams p, int n_q, hipStream_t st) {
+  const int tiles = (p.P + 63) / 64;
+  p.ppad = 64 * tiles;
+  const int64_t row_bytes = (int64_t)p.F * p.ppad * 4;
+  // queries per chunk: a workspace of at most 1 GiB, whole work-groups of 128
+  int64_t nqc = ((int64_t)1 << 30) / row_bytes / 128 * 128;
+  if (nqc < 128) nqc = 128;
+  if (nqc > n_q) nqc = n_q;
+  void* ws = nullptr;
+  if (hipMallocAsync(&ws, (size_t)(nqc * row_bytes), st) != hipSuccess)
+    return fail(SAF3R_ERR_LAUNCH, "saf3r_token_topk: workspace of %lld bytes not available", (long long)(nqc * row_bytes));
+  p.ws = static_cast<float*>(ws);
+  const int nv = tiles <= 4 ? 4 : tiles <= 8 ? 8 : tiles <= 12 ? 12 : tiles <= 16 ? 16 : tiles <= 24 ? 24
+                 : tiles <= 32 ? 32 : tiles <= 48 ? 48 : 64;
+  int rc = SAF3R_OK;
+  for (int64_t q0 = 0; q0 < n_q && rc == SAF3R_OK; q0 += nqc) {
+    const int64_t q1 = q0 + nqc < n_q ? q0 + nqc : n_q;
+    p.q_begin = q0;
+    p.nq = (int)q1;
+    const dim3 g1((unsigned)((q1 - q0 + 127) / 128), (unsigned)p.F);
+    if (p.kmode == 2) hipLaunchKernelGGL((token_topk_kernel<1, false, true>), g1, dim3(256), 0, st, p);
+    else hipLaunchKernelGGL((token_topk_kernel<1, true, true>), g1, dim3(256), 0, st, p);
+    rc = check_launch("saf3r_token_topk");
+    if (rc != SAF3R_OK) break;
+    const dim3 g2((unsigned)(((q1 - q0) * p.F + 3) / 4));
+    switch (nv) {
+      case 4: hipLaunchKernelGGL(topk_large_kernel<4>, g2, dim3(256), 0, st, p.ws, q0, q1, p.F, p.P, p.ppad, p.ke, p.idx); break;
+      case 8: hipLaunchKernelGGL(topk_large_kernel<8>, g2, dim3(256), 0, st, p.ws, q0, q1, p.F, p.P, p.ppad, p.ke, p.idx); break;
+      case 12: hipLaunchKernelGGL(topk_large_kernel<12>, g2, dim3(256), 0, st, p.ws, q0, q1, p.F, p.P, p.ppad, p.ke, p.idx); break;
+      case 16: hipLaunchKernelGGL(topk_large_kernel<16>, g2, dim3(256), 0, st, p.ws, q0, q1, p.F, p.P, p.ppad, p.ke, p.idx); break;
+      case 24: hipLaunchKernelGGL(topk_large_kernel<24>, g2, dim3(256), 0, st, p.ws, q0, q1, p.F, p.P, p.ppad, p.ke, p.idx); break;
+      case 32: hipLaunchKernelGGL(topk_large_kernel<32>, g2, dim3(256), 0, st, p.ws, q0, q1, p.F, p.P, p.ppad, p.ke, p.idx); break;
+      case 48: hipLaunchKernelGGL(topk_large_kernel<48>, g2, dim3(256), 0, st, p.ws, q0, q1, p.F, p.P, p.ppad, p.ke, p.idx); break;
+      default: hipLaunchKernelGGL(topk_large_kernel<64>, g2, dim3(256), 0, st, p.ws, q0, q1, p.F, p.P, p.ppad, p.ke, p.idx); break;
+    }
+    rc = check_launch("saf3r_token_topk");
+  }
+  if (hipFreeAsync(ws, st) != hipSuccess && rc == SAF3R_OK)
+    rc = fail(SAF3R_ERR_LAUNCH, "saf3r_token_topk: workspace release failed");
+  return rc;
 }
 
 }  // namespace saf3r
@@ -340,7 +501,12 @@ extern "C" int saf3r_token_topk(const saf3r_rows* q, const saf3r_rows* k, int n_
   if (int e = injected("saf3r_token_topk")) return e;
   if (!q || !k || !q->ptr || !k->ptr || !idx) return fail(SAF3R_ERR_INVALID, "saf3r_token_topk: null pointer");
   if (n_q < 0 || frames <= 0 || per_frame <= 0) return fail(SAF3R_ERR_INVALID, "saf3r_token_topk: bad shape");
-  if (topk < 1 || topk > 16) return fail(SAF3R_ERR_UNSUPPORTED, "saf3r_token_topk: topk must be in [1, 16]");
+  if (topk < 1) return fail(SAF3R_ERR_INVALID, "saf3r_token_topk: topk must be >= 1");
+  const int ke = topk < per_frame ? topk : per_frame;
+  if (ke > 128) return fail(SAF3R_ERR_UNSUPPORTED, "saf3r_token_topk: min(topk, per_frame) must be <= 128 (got %d)", ke);
+  if (ke > 16 && (per_frame > kLargeMaxP || frames > 65535))
+    return fail(SAF3R_ERR_UNSUPPORTED, "saf3r_token_topk: topk > 16 needs per_frame <= %d and frames <= 65535",
+                kLargeMaxP);
   if (q->row_stride % 8 || k->row_stride % 8 || ((uintptr_t)q->ptr | (uintptr_t)k->ptr) % 16 ||
       q->rows_per_frame <= 0 || k->rows_per_frame <= 0)
     return fail(SAF3R_ERR_INVALID, "saf3r_token_topk: rows must be 16-byte aligned, row stride %% 8");
@@ -363,9 +529,13 @@ extern "C" int saf3r_token_topk(const saf3r_rows* q, const saf3r_rows* k, int n_
   p.nq = n_q;
   p.F = frames;
   p.P = per_frame;
-  p.ke = topk < per_frame ? topk : per_frame;
+  p.ke = ke;
   p.idx = idx;
+  p.ws = nullptr;
+  p.q_begin = 0;
+  p.ppad = 0;
   hipStream_t st = (hipStream_t)stream;
+  if (ke > 16) return token_topk_large(p, n_q, st);
   if (p.ke <= 1) return launch_topk<1>(p, st);
   if (p.ke <= 2) return launch_topk<2>(p, st);
   if (p.ke <= 4) return launch_topk<4>(p, st);

@@ -378,6 +378,69 @@ def test_token_topk_mass_ties(ops, topk):
     assert np.array_equal(got.numpy(), ref)
 
 
+@pytest.mark.parametrize("frames,P,topk", [(3, 1369, 128), (2, 200, 100), (4, 70, 17), (2, 50, 300)])
+def test_token_topk_large_k(ops, frames, P, topk):
+    """16 < min(topk, P) <= 128 (the reference's range): scores of a chunk of queries, then a radix
+    selection per (query, frame); also topk > P (every key of a frame, best first)."""
+    g = torch.Generator().manual_seed(frames * P + topk)
+    nq = 300
+    q = torch.randn(nq, 64, generator=g).to(torch.bfloat16)
+    k = torch.randn(frames * P, 64, generator=g).to(torch.bfloat16)
+    got = ops.token_topk(q.to(DEV), k.to(DEV), frames, P, topk).cpu()
+    torch.cuda.synchronize()
+    s = (q.double() @ k.double().T).float().numpy()
+    ref = OS.frame_topk(s, frames, topk)
+    assert got.shape == ref.shape
+    gs = np.take_along_axis(s, got.numpy().astype(np.int64), axis=1)
+    rs = np.take_along_axis(s, ref.astype(np.int64), axis=1)
+    assert np.allclose(gs, rs, atol=1e-4, rtol=0), "selected scores differ beyond rounding noise"
+    assert (got.numpy() == ref).mean() >= 0.99
+    # within a frame: distinct keys of that frame, scores non-increasing
+    ke = min(topk, P)
+    gi = got.numpy().reshape(nq, frames, ke)
+    for f in range(frames):
+        blk = gi[:, f]
+        assert ((blk >= f * P) & (blk < (f + 1) * P)).all()
+        assert all(len(set(row)) == ke for row in blk)
+
+
+def test_token_topk_large_k_ties_and_layout(ops):
+    """Mass ties (three repeated key rows) at k = 64 through the general row map: bit-exact with the
+    oracle, lowest indices first among equal scores."""
+    frames, P, topk, pad = 4, 150, 64, 5
+    g = torch.Generator().manual_seed(8)
+    base = torch.randn(3, 64, generator=g).to(torch.bfloat16)
+    k = base[torch.randint(0, 3, (frames * P,), generator=g)]
+    q = torch.randn(130, 64, generator=g).to(torch.bfloat16)
+    store = torch.zeros(frames * P // (2 * P), pad + 2 * P, 64, dtype=torch.bfloat16)
+    store[:, pad:] = k.view(-1, 2 * P, 64)
+    store = store.to(DEV)  # kept alive: the row descriptor holds a raw pointer
+    kr = ops.rows(store.view(-1, 64), base_row=pad, rows_per_frame=2 * P, frame_row_stride=pad + 2 * P)
+    got = ops.token_topk(q.to(DEV), None, frames, P, topk, krows=kr).cpu()
+    torch.cuda.synchronize()
+    s = (q.double() @ k.double().T).float().numpy()
+    assert np.array_equal(got.numpy(), OS.frame_topk(s, frames, topk))
+
+
+def test_token_topk_large_k_chunks(ops):
+    """128 frames x 1369 keys, top-32 for 3000 queries: the score workspace (1 GiB at most) takes
+    the queries in three chunks; sampled rows at the chunk edges against the oracle."""
+    frames, P, topk, nq = 128, 1369, 32, 3000
+    g = torch.Generator().manual_seed(21)
+    q = torch.randn(nq, 64, generator=g).to(torch.bfloat16)
+    k = torch.randn(frames * P, 64, generator=g).to(torch.bfloat16)
+    got = ops.token_topk(q.to(DEV), k.to(DEV), frames, P, topk).cpu()
+    torch.cuda.synchronize()
+    rows = [0, 1, 1407, 1408, 1409, 2815, 2816, 2999]
+    s = (q[rows].double() @ k.double().T).float().numpy()
+    ref = OS.frame_topk(s, frames, topk)
+    g_ = got[rows].numpy()
+    gs = np.take_along_axis(s, g_.astype(np.int64), axis=1)
+    rs = np.take_along_axis(s, ref.astype(np.int64), axis=1)
+    assert np.allclose(gs, rs, atol=1e-4, rtol=0)
+    assert (g_ == ref).mean() >= 0.99
+
+
 @pytest.mark.parametrize("frames,P,topk", [(4, 1369, 4), (3, 100, 8), (2, 30, 16), (5, 64, 1)])
 def test_token_topk(ops, frames, P, topk):
     g = torch.Generator().manual_seed(frames * P)
