@@ -4,9 +4,15 @@
 //      fp32 scores, exact max-subtracted softmax, fp32 P.V, output in v.dtype), :115-166 (API:
 //      q [N, D], k/v [Nk, D], kv_indices [N, TopK], scale default 1/sqrt(D); a stride-0 index view
 //      shares one list across rows), :173-258 (online-softmax variant for TopK > 2048).
-// Here one wave owns one query row and walks its list in chunks of 64 keys (one key per lane)
-// with an fp32 online softmax, so any list length is handled by the same kernel. Entries < 0 or
-// >= num_keys are skipped. q and k are bf16 or fp32 rows (the reference's kernel upcasts either).
+// The work is one gathered K row and one V row per (query, listed key): bound by the cache
+// bandwidth of those row reads, not by arithmetic (a list is one query's own, so there is no
+// matrix product to share between queries). One wave owns one query row and walks its list in
+// chunks of 64 keys with an fp32 online softmax, so any list length is handled by the same
+// kernel. Lane l serves key slot ks = l / 8 of every group of 8 keys and dims 8 dg .. 8 dg + 7
+// (dg = l % 8): 8 lanes read a K or V row together (32 bytes each of an fp32 K row, 16 of a bf16
+// row), so one load instruction moves 8 whole rows, and the 8 partial dot products of a row are
+// summed by three DPP steps inside the 8 lanes. Entries < 0 or >= num_keys are skipped. q and k
+// are bf16 or fp32 rows (the reference's kernel upcasts either).
 #include "common.h"
 
 namespace saf3r {
@@ -30,120 +36,130 @@ struct GatherParams {
   float c;  // scale * log2(e)
 };
 
-__device__ inline float wave_max(float x) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
+// sum of x over the 8 lanes of this lane's group (quad swaps, then the mirrored quad of the group)
+__device__ inline float sum8(float x) {
+  x += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0xB1, 0xF, 0xF, true));
+  x += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x4E, 0xF, 0xF, true));
+  x += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x141, 0xF, 0xF, true));
   return x;
 }
-__device__ inline float wave_sum(float x) {
+// reductions over the 8 key slots (lanes dg, dg + 8, ..., dg + 56)
+__device__ inline float slots_max(float x) {
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
+  for (int o = 8; o < 64; o <<= 1) x = fmaxf(x, __shfl_xor(x, o));
+  return x;
+}
+__device__ inline float slots_sum(float x) {
+#pragma unroll
+  for (int o = 8; o < 64; o <<= 1) x += __shfl_xor(x, o);
   return x;
 }
 
-// 2 waves per workgroup, one query row per wave. QK32: q and k rows are fp32 (the reference's gather
+// 4 waves per workgroup, one query row per wave. QK32: q and k rows are fp32 (the reference's gather
 // reads the fp32 q / k of the autocast forward and multiplies in fp32); otherwise bf16.
 template <bool QK32>
-__global__ __launch_bounds__(128) void gather_attn_kernel(GatherParams p) {
-  __shared__ float red[2][64][65];
-  __shared__ __align__(16) float qs[2][64];
-  const int lane = tid_x() & 63, w = tid_x() >> 6;
-  const int64_t r = (int64_t)bid_x() * 2 + w;
-  const bool active = r < p.n;
-  const int64_t rr = active ? r : 0;
+__global__ __launch_bounds__(256) void gather_attn_kernel(GatherParams p) {
+  const int lane = tid_x() & 63, w = tid_x() >> 6, ks = lane >> 3, dg = lane & 7;
+  const int64_t r = (int64_t)bid_x() * 4 + w;
+  if (r >= p.n) return;  // a whole wave leaves; the kernel has no barrier
 
-  // q row: bf16 pairs in registers, identical in every lane; fp32 in LDS (read as broadcasts)
-  uint32_t qw[32];
+  // this lane's 8 dims of q: fp32 values (QK32) or bf16 pairs
+  float qv[8];
+  uint32_t qw[4];
   if constexpr (QK32) {
-    qs[w][lane] = p.q.row<float>(rr)[lane];
-    __syncthreads();
-  } else {
-    const u32x4* q4 = reinterpret_cast<const u32x4*>(p.q.row(rr));
+    const f32x4* q4 = reinterpret_cast<const f32x4*>(p.q.row<float>(r) + 8 * dg);
+    const f32x4 a = q4[0], b = q4[1];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      u32x4 x = q4[j];
-      qw[4 * j] = x[0];
-      qw[4 * j + 1] = x[1];
-      qw[4 * j + 2] = x[2];
-      qw[4 * j + 3] = x[3];
+    for (int e = 0; e < 4; ++e) {
+      qv[e] = a[e];
+      qv[4 + e] = b[e];
     }
+  } else {
+    const u32x4 x = *reinterpret_cast<const u32x4*>(p.q.row(r) + 8 * dg);
+    qw[0] = x.x;
+    qw[1] = x.y;
+    qw[2] = x.z;
+    qw[3] = x.w;
   }
-  float acc[64];
+  float acc[8];
 #pragma unroll
-  for (int d = 0; d < 64; ++d) acc[d] = 0.f;
+  for (int d = 0; d < 8; ++d) acc[d] = 0.f;
   float m_run = -__builtin_inff(), l_run = 0.f;
-  const int32_t* il = p.idx + rr * p.idx_stride;
+  const int32_t* il = p.idx + r * p.idx_stride;
 
   for (int c0 = 0; c0 < p.topk; c0 += 64) {
-    const int j = c0 + lane;
-    int id = (active && j < p.topk) ? il[j] : -1;
-    if (id >= p.nk) id = -1;
-    float s = -__builtin_inff();
-    uint32_t vw[32];
-    if (id >= 0) {
-      const u32x4* v4 = reinterpret_cast<const u32x4*>(p.v.row(id));
-      float dot = 0.f;
+    int myid = c0 + lane < p.topk ? il[c0 + lane] : -1;  // entry c0 + l of the list, in lane l
+    if (myid >= p.nk) myid = -1;
+    // key c0 + 8 it + ks: its score and its V dims
+    float s[8];
+    uint32_t vw[8][4];
+#pragma unroll
+    for (int it = 0; it < 8; ++it) {
+      const int id = __shfl(myid, 8 * it + ks);
+      const int64_t rid = id >= 0 ? id : 0;  // a masked entry reads row 0; its score is dropped
+      float part = 0.f;
       if constexpr (QK32) {
-        const f32x4* k4 = reinterpret_cast<const f32x4*>(p.k.row<float>(id));
-        const f32x4* q4 = reinterpret_cast<const f32x4*>(qs[w]);
+        const f32x4* k4 = reinterpret_cast<const f32x4*>(p.k.row<float>(rid) + 8 * dg);
+        const f32x4 a = k4[0], b = k4[1];
 #pragma unroll
-        for (int t = 0; t < 16; ++t) {
-          const f32x4 kx = k4[t], qx = q4[t];
-          dot = __builtin_fmaf(qx[0], kx[0], dot);
-          dot = __builtin_fmaf(qx[1], kx[1], dot);
-          dot = __builtin_fmaf(qx[2], kx[2], dot);
-          dot = __builtin_fmaf(qx[3], kx[3], dot);
-        }
+        for (int e = 0; e < 4; ++e) part = __builtin_fmaf(qv[e], a[e], part);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) part = __builtin_fmaf(qv[4 + e], b[e], part);
+      } else {
+        const u32x4 kx = *reinterpret_cast<const u32x4*>(p.k.row(rid) + 8 * dg);
+        // elements are copied to scalars before the bf16x2 bit_cast: a bit_cast applied directly to
+        // a vector element (kx[e]) was lowered to element 0 for every e by this compiler
+        const uint32_t kw[4] = {kx.x, kx.y, kx.z, kx.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          part = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, kw[e]), __builtin_bit_cast(bf16x2, qw[e]),
+                                                 part, false);
       }
-#pragma unroll
-      for (int t = 0; t < 8; ++t) {
-        const u32x4 vx = v4[t];
-        if constexpr (!QK32) {
-          const u32x4 kx = reinterpret_cast<const u32x4*>(p.k.row(id))[t];
-          // elements are copied to scalars before the bf16x2 bit_cast: a bit_cast applied directly to
-          // a vector element (kx[e]) was lowered to element 0 for every e by this compiler
-          const uint32_t kw[4] = {kx.x, kx.y, kx.z, kx.w};
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const uint32_t kk = kw[e], qq = qw[4 * t + e];
-            dot = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, kk), __builtin_bit_cast(bf16x2, qq),
-                                                  dot, false);
-          }
-        }
-        vw[4 * t + 0] = vx.x;
-        vw[4 * t + 1] = vx.y;
-        vw[4 * t + 2] = vx.z;
-        vw[4 * t + 3] = vx.w;
-      }
-      s = dot;
-    } else {
-#pragma unroll
-      for (int t = 0; t < 32; ++t) vw[t] = 0;
+      const u32x4 vx = *reinterpret_cast<const u32x4*>(p.v.row(rid) + 8 * dg);
+      vw[it][0] = vx.x;
+      vw[it][1] = vx.y;
+      vw[it][2] = vx.z;
+      vw[it][3] = vx.w;
+      part = sum8(part);
+      s[it] = id >= 0 ? part : -__builtin_inff();
     }
-    const float mx = wave_max(s);
+    float mx = s[0];
+#pragma unroll
+    for (int it = 1; it < 8; ++it) mx = fmaxf(mx, s[it]);
+    mx = slots_max(mx);
     const float m_new = fmaxf(m_run, mx);
     const float m_use = m_new == -__builtin_inff() ? 0.f : m_new;
     const float alpha = __builtin_amdgcn_exp2f((m_run - m_use) * p.c);
-    const float pj = __builtin_amdgcn_exp2f(__builtin_fmaf(s, p.c, -m_use * p.c));
-    l_run = l_run * alpha + wave_sum(pj);
-    m_run = m_new;
 #pragma unroll
-    for (int t = 0; t < 32; ++t) {
-      acc[2 * t] = __builtin_fmaf(pj, bf16_lo(vw[t]), acc[2 * t] * alpha);
-      acc[2 * t + 1] = __builtin_fmaf(pj, bf16_hi(vw[t]), acc[2 * t + 1] * alpha);
+    for (int d = 0; d < 8; ++d) acc[d] *= alpha;
+    float lsum = 0.f;
+#pragma unroll
+    for (int it = 0; it < 8; ++it) {
+      const float pj = __builtin_amdgcn_exp2f(__builtin_fmaf(s[it], p.c, -m_use * p.c));
+      lsum += pj;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        acc[2 * e] = __builtin_fmaf(pj, bf16_lo(vw[it][e]), acc[2 * e]);
+        acc[2 * e + 1] = __builtin_fmaf(pj, bf16_hi(vw[it][e]), acc[2 * e + 1]);
+      }
     }
+    l_run = l_run * alpha + slots_sum(lsum);
+    m_run = m_new;
   }
 
-  // column sums of acc over the 64 lanes through LDS
+  // sum the 8 key slots' partial outputs; lanes of slot 0 store dims 8 dg .. 8 dg + 7
 #pragma unroll
-  for (int d = 0; d < 64; ++d) red[w][lane][d] = acc[d];
-  __syncthreads();
-  float o = 0.f;
-  for (int j = 0; j < 64; ++j) o += red[w][j][lane];
-  if (active) {
+  for (int d = 0; d < 8; ++d) acc[d] = slots_sum(acc[d]);
+  if (ks == 0) {
     const float inv = l_run > 0.f ? 1.0f / l_run : 0.f;
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const bf16x2 pr = {(__bf16)(acc[2 * e] * inv), (__bf16)(acc[2 * e + 1] * inv)};
+      o[e] = __builtin_bit_cast(uint32_t, pr);
+    }
     __bf16* orow = const_cast<__bf16*>(p.out.row<__bf16>(r));
-    orow[lane] = (__bf16)(o * inv);
+    *reinterpret_cast<u32x4*>(orow + 8 * dg) = u32x4{o[0], o[1], o[2], o[3]};
   }
 }
 
@@ -183,9 +199,8 @@ extern "C" int saf3r_gather_attn_fwd(const saf3r_rows* q, const saf3r_rows* k, c
   p.topk = topk;
   p.nk = num_keys;
   p.c = scale * 1.4426950408889634f;
-  if (qk_fp32)
-    hipLaunchKernelGGL(gather_attn_kernel<true>, dim3((unsigned)((n + 1) / 2)), dim3(128), 0, (hipStream_t)stream, p);
-  else
-    hipLaunchKernelGGL(gather_attn_kernel<false>, dim3((unsigned)((n + 1) / 2)), dim3(128), 0, (hipStream_t)stream, p);
+  const dim3 grid((unsigned)((n + 3) / 4));
+  if (qk_fp32) hipLaunchKernelGGL(gather_attn_kernel<true>, grid, dim3(256), 0, (hipStream_t)stream, p);
+  else hipLaunchKernelGGL(gather_attn_kernel<false>, grid, dim3(256), 0, (hipStream_t)stream, p);
   return check_launch("saf3r_gather_attn_fwd");
 }
