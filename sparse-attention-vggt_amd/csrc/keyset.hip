@@ -52,23 +52,24 @@ struct ProbeParams {
 };
 
 // grid (nchunks, n_sel), 64 threads: feature d of chunk c, summed over the chunk's rows in order.
-// Rows are read 16 at a time (independent loads in flight) and added in order, so the sum is the
-// sequential one.
+// Rows are read 64 at a time (independent loads in flight: the chain of adds is cheap, the load
+// latency is not) and added in order, so the sum is the sequential one.
+constexpr int kProbeBatch = 64;
 __global__ __launch_bounds__(64) void probe_partial_kernel(ProbeParams p) {
   const int c = bid_x(), hs = bid_y(), d = tid_x();
   const float* base = p.q + (int64_t)p.slots[hs] * p.slot_stride + d;
   const int i0 = c * p.chunk, i1 = min(p.n_samp, i0 + p.chunk);
   float acc = 0.f;
   int i = i0;
-  for (; i + 16 <= i1; i += 16) {
-    float x[16];
+  for (; i + kProbeBatch <= i1; i += kProbeBatch) {
+    float x[kProbeBatch];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
+    for (int j = 0; j < kProbeBatch; ++j) {
       const int t = p.sample ? min(max(p.sample[i + j], 0), p.n - 1) : i + j;
       x[j] = base[(int64_t)t * 64];
     }
 #pragma unroll
-    for (int j = 0; j < 16; ++j) acc = acc + x[j];
+    for (int j = 0; j < kProbeBatch; ++j) acc = acc + x[j];
   }
   for (; i < i1; ++i) {
     const int t = p.sample ? min(max(p.sample[i], 0), p.n - 1) : i;
@@ -77,11 +78,21 @@ __global__ __launch_bounds__(64) void probe_partial_kernel(ProbeParams p) {
   p.partial[((int64_t)hs * kProbeChunks + c) * 64 + d] = acc;
 }
 
-// grid (n_sel), 64 threads: chunk sums in chunk order, then one correctly rounded division
+// grid (n_sel), 64 threads: chunk sums in chunk order (read 64 at a time), then one correctly
+// rounded division
 __global__ __launch_bounds__(64) void probe_finish_kernel(ProbeParams p) {
   const int hs = bid_x(), d = tid_x();
+  const float* part = p.partial + (int64_t)hs * kProbeChunks * 64 + d;
   float total = 0.f;
-  for (int c = 0; c < p.nchunks; ++c) total = total + p.partial[((int64_t)hs * kProbeChunks + c) * 64 + d];
+  int c = 0;
+  for (; c + kProbeBatch <= p.nchunks; c += kProbeBatch) {
+    float x[kProbeBatch];
+#pragma unroll
+    for (int j = 0; j < kProbeBatch; ++j) x[j] = part[(int64_t)(c + j) * 64];
+#pragma unroll
+    for (int j = 0; j < kProbeBatch; ++j) total = total + x[j];
+  }
+  for (; c < p.nchunks; ++c) total = total + part[(int64_t)c * 64];
   p.qbar[hs * 64 + d] = __fdiv_rn(total, (float)p.n_samp);
 }
 
