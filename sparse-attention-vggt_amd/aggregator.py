@@ -151,12 +151,25 @@ class DinoPatchEmbed(nn.Module):
         patch = patch.permute(0, 2, 3, 1).reshape(1, gh * gw, dim)
         return torch.cat([pe[:, :1], patch], dim=1).to(dtype)
 
+    def patchify(self, images: torch.Tensor) -> torch.Tensor:
+        """``self.proj`` (a 14x14 convolution with stride 14) as one GEMM over the non-overlapping
+        patches: the same weights and the same products, [n, gh*gw, C]. (The convolution path picked a
+        direct kernel that took 50 ms for 64 bf16 frames of 518 x 518 on this stack.)"""
+        n, c, h, w = images.shape
+        p = self.patch_size
+        gh, gw = h // p, w // p
+        patches = images.reshape(n, c, gh, p, gw, p).permute(0, 2, 4, 1, 3, 5).reshape(n, gh * gw, c * p * p)
+        weight = self.proj.weight.reshape(self.proj.out_channels, c * p * p)
+        if torch.is_autocast_enabled(patches.device.type):  # autocast casts the operands as for the conv
+            return F.linear(patches, weight, self.proj.bias)
+        return F.linear(patches, weight.to(patches.dtype), self.proj.bias.to(patches.dtype))
+
     def forward(self, images: torch.Tensor):
         n, _, h, w = images.shape
         p = self.patch_size
         if h % p or w % p:
             raise AssertionError(f"image size {h}x{w} is not a multiple of the patch size {p}")
-        x = self.proj(images).flatten(2).transpose(1, 2)  # [n, gh*gw, C]
+        x = self.patchify(images)  # [n, gh*gw, C]
         x = torch.cat([self.cls_token.expand(n, -1, -1).to(x.dtype), x], dim=1)
         x = x + self.position_embedding(h // p, w // p, x.dtype)
         x = torch.cat([x[:, :1], self.register_tokens.expand(n, -1, -1).to(x.dtype), x[:, 1:]], dim=1)
