@@ -29,6 +29,7 @@ struct TopkParams {
   float* ws;
   int64_t q_begin;
   int ppad;
+  int fgroups;  // frame groups of the selection launch (grid.y)
 };
 
 __device__ inline const __bf16* rows_at(const __bf16* ptr, int64_t rs, int64_t base, int64_t rpf, int64_t frs,
@@ -108,9 +109,12 @@ __global__ __launch_bounds__(256, K <= 8 ? 3 : 2) void token_topk_kernel(TopkPar
   }
 
   const int tiles_pf = (p.P + 63) / 64;
-  // frame f: pass 1 over its tiles, then pass 2; DUMP: one pass over frame bid_y that stores the
-  // scores (a work-group per 128 queries and frame)
-  const int total = DUMP ? tiles_pf : p.F * 2 * tiles_pf;
+  // frame f: pass 1 over its tiles, then pass 2, for the frames [f_lo, f_hi) of this work-group's
+  // frame group (bid_y of p.fgroups: the split only evens out the tail of the launch); DUMP: one
+  // pass over frame bid_y that stores the scores (a work-group per 128 queries and frame)
+  const int f_lo = __builtin_amdgcn_readfirstlane(DUMP ? bid_y() : p.F * bid_y() / p.fgroups);
+  const int f_hi = __builtin_amdgcn_readfirstlane(DUMP ? f_lo + 1 : p.F * (bid_y() + 1) / p.fgroups);
+  const int total = (f_hi - f_lo) * (DUMP ? 1 : 2) * tiles_pf;
   // LDS chunk position P = 256 j + 64 w + lane of a tile (instruction j of wave w) holds key row
   // P / 8, global 16-byte chunk (P % 8) ^ swz8(row): the swizzle that makes the MFMA fragment
   // reads conflict-free is applied on the load side
@@ -122,7 +126,7 @@ __global__ __launch_bounds__(256, K <= 8 ? 3 : 2) void token_topk_kernel(TopkPar
     chj[j] = (P & 7) ^ swz8(rowj[j]);
   }
   int iu = 0, ips = 0;  // tile and pass of the next step to issue
-  int64_t ifr = DUMP ? bid_y() : 0;  // its frame
+  int64_t ifr = f_lo;  // its frame
   // FLAT (kmode 0 and 1): frame f's rows are k_fst rows apart, so a tile's address is a uniform
   // base plus a fixed 32-bit lane offset (the last tile of a frame clamps its rows to the frame's
   // last row: its own offsets); otherwise every row goes through the general row mapping
@@ -182,7 +186,7 @@ __global__ __launch_bounds__(256, K <= 8 ? 3 : 2) void token_topk_kernel(TopkPar
   };
   // candidate e of this lane: key 32*(e>>4) + 8*((e&15)>>2) + 4*half + (e&3) of the tile
   auto kpos = [](int e) { return 32 * (e >> 4) + 8 * ((e & 15) >> 2) + (e & 3); };
-  int f = DUMP ? bid_y() : 0, ps = 0, u = 0;  // frame, pass and tile of the step being selected
+  int f = f_lo, ps = 0, u = 0;  // frame, pass and tile of the step being selected
   // Frame f again, for the lanes flagged `over`: every candidate >= tau goes straight into a[]. K
   // fragments come from global memory (this lane's rows col and 32 + col of each tile, chunks
   // 4 half .. 4 half + 3), the MFMAs run as in the main loop on the whole wave.
@@ -345,8 +349,29 @@ __global__ __launch_bounds__(256, K <= 8 ? 3 : 2) void token_topk_kernel(TopkPar
 }
 
 template <int K>
-static int launch_topk(const TopkParams& p, hipStream_t st) {
-  const dim3 grid((unsigned)((p.nq + 127) / 128));
+static int launch_topk(TopkParams p, hipStream_t st) {
+  // Frame groups: every work-group walks all frames of its queries in 2 passes, so with few, long
+  // work-groups the launch ends with a partly idle last round. Splitting the frames into g groups
+  // (one work-group per 128 queries and group, at least 2 frames each) picks the g whose rounds of
+  // resident work-groups (K <= 8: 3 per CU, else 2) are fullest.
+  const int64_t nb = (p.nq + 127) / 128;
+  int cus = 0, dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      cus <= 0)
+    cus = 256;
+  const int64_t slots = (int64_t)cus * (K <= 8 ? 3 : 2);
+  int best = 1;
+  double best_eff = 0.0;
+  for (int g = 1; g <= 8 && (g == 1 || p.F / g >= 2); ++g) {
+    const int64_t wgs = nb * g, rounds = (wgs + slots - 1) / slots;
+    const double eff = (double)wgs / (double)(rounds * slots);
+    if (eff > best_eff + 0.02) {
+      best_eff = eff;
+      best = g;
+    }
+  }
+  p.fgroups = best;
+  const dim3 grid((unsigned)nb, (unsigned)best);
   if (p.kmode == 2) hipLaunchKernelGGL((token_topk_kernel<K, false, false>), grid, dim3(256), 0, st, p);
   else hipLaunchKernelGGL((token_topk_kernel<K, true, false>), grid, dim3(256), 0, st, p);
   return check_launch("saf3r_token_topk");
@@ -534,6 +559,7 @@ extern "C" int saf3r_token_topk(const saf3r_rows* q, const saf3r_rows* k, int n_
   p.ws = nullptr;
   p.q_begin = 0;
   p.ppad = 0;
+  p.fgroups = 1;
   hipStream_t st = (hipStream_t)stream;
   if (ke > 16) return token_topk_large(p, n_q, st);
   if (p.ke <= 1) return launch_topk<1>(p, st);
