@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define SAF3R_ABI_VERSION 7
+#define SAF3R_ABI_VERSION 8
 
 enum saf3r_status {
   SAF3R_OK = 0,
@@ -117,6 +117,10 @@ int64_t saf3r_packed_slots(int frames, int tokens_per_frame, int num_special);
  *            increasing head order) at qk32[((s*2 + 0|1) * F*T + t) * 64 + d] for q|k of token t.
  *            (Under autocast the reference keeps q/k in fp32 after LayerNorm/RoPE; its q_probe_topk
  *            mean / scores and its dino_topk gather read those fp32 values.)
+ *   q_scaled, q_scale: host uint8 [num_heads] or NULL, and a factor. The packed Q of a head h < 64
+ *            flagged here is q * q_scale (fp32, after LayerNorm and RoPE), rounded once to bf16;
+ *            its qk32 rows stay unscaled. With q_scale = softmax scale * log2(e) this is the
+ *            prescaled Q that saf3r_sparse_attn_fwd takes for heads flagged in its q_scaled.
  * Replaces: saf3r/patch/patch_vggt.py:577-583 (qkv reshape, q_norm/k_norm, rope) and
  *           saf3r/models/official_vggt/layers/rope.py:154-188.
  */
@@ -126,7 +130,8 @@ int saf3r_pack_qkv(const void* q, const void* k, const void* v, int64_t tok_stri
                    const float* k_ln_bias, float ln_eps, int apply_ln,
                    const int32_t* pos, const float* rope_cos, const float* rope_sin, int rope_positions,
                    void* q_packed, void* k_packed, void* v_packed, const uint8_t* token_order,
-                   const uint8_t* fp32_heads, float* qk32, void* stream);
+                   const uint8_t* fp32_heads, float* qk32, const uint8_t* q_scaled, float q_scale,
+                   void* stream);
 
 /*
  * Pooled patch-block means (fp32) of the packed Q and K of the listed heads.
@@ -248,6 +253,11 @@ int saf3r_keyset_gather(const void* k_packed, int frames, int tokens_per_frame, 
  *   token_order: host uint8 [num_heads] or NULL: DENSE heads packed in token order by
  *        saf3r_pack_qkv (the flag is an error on any other pattern). Their key and query tiles
  *        then cover the F*T tokens without padding.
+ *   q_scaled: host uint8 [num_heads] or NULL: heads h < 64 whose Q rows (and BROADCAST Q buffer)
+ *        hold q * scale * log2(e) rounded once to bf16 (saf3r_pack_qkv's q_scaled with that
+ *        q_scale). Their walks take exp2 of the score MFMA results directly, without a running
+ *        maximum, while every partial row sum stays within [2^-64, 2^64]; a walk that leaves that
+ *        range is walked again with the exact maximum. Same results within the bf16 tolerance.
  *   flags: 0 or SAF3R_ATTN_FIXED_ORDER. Without it, every key walk starts at the position the
  *        device's wall clock divided by the walk's step time points to, so that the work-groups
  *        resident at one moment read nearby key tiles (cache reuse); the summation order, and so the
@@ -268,8 +278,8 @@ int saf3r_sparse_attn_fwd(const void* q_packed, const void* k_packed, const void
                           const int32_t* sel, int sel_width, float scale, void* out, int64_t out_row_stride,
                           const void* keyset_k, const void* keyset_v, const int32_t* keyset_count,
                           int64_t keyset_capacity, const void* bcast_q, const void* bcast_k,
-                          const void* bcast_v, const uint8_t* token_order, int flags, unsigned long long* pace,
-                          unsigned int pace_seq, void* stream);
+                          const void* bcast_v, const uint8_t* token_order, const uint8_t* q_scaled, int flags,
+                          unsigned long long* pace, unsigned int pace_seq, void* stream);
 
 /*
  * Gather attention: out[r] = sum_j softmax_j(q[r] . k[idx[r][j]] * scale) v[idx[r][j]], fp32

@@ -19,7 +19,7 @@ EXPORTS = (
     "saf3r_token_topk", "saf3r_probe_scores", "saf3r_keyset_build", "saf3r_keyset_gather",
     "saf3r_frame_topk_scores", "saf3r_probe_scores_noalloc",
 )
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 _lib = None
 
@@ -57,12 +57,12 @@ def load():
         "saf3r_last_error": ([], ctypes.c_char_p),
         "saf3r_packed_slots": ([i32, i32, i32], i64),
         "saf3r_pack_qkv": ([p, p, p, i64, i64, i32, i32, i32, i32, p, p, p, p, f32, i32, p, p, p, i32, p, p, p, p, p,
-                            p, p], i32),
+                            p, p, f32, p], i32),
         "saf3r_block_pool": ([p, p, i32, i32, i32, i32, p, i32, p, p, p], i32),
         "saf3r_topk_from_scores": ([p, i32, i32, i32, i32, i32, p, p], i32),
         "saf3r_block_select": ([p, p, i32, i32, i32, i32, i32, i32, p, p], i32),
-        "saf3r_sparse_attn_fwd": ([p, p, p, i32, i32, i32, i32, p, p, i32, f32, p, i64, p, p, p, i64, p, p, p, p, i32,
-                                   p, ctypes.c_uint, p], i32),
+        "saf3r_sparse_attn_fwd": ([p, p, p, i32, i32, i32, i32, p, p, i32, f32, p, i64, p, p, p, i64, p, p, p, p, p,
+                                   i32, p, ctypes.c_uint, p], i32),
         "saf3r_gather_attn_fwd": ([rows, rows, rows, p, i64, i32, i32, i64, f32, i32, rows, p], i32),
         "saf3r_token_topk": ([rows, rows, i32, i32, i32, i32, p, p], i32),
         "saf3r_probe_scores": ([p, p, i64, i32, p, i32, p, i32, f32, p, p, p, i64, p], i32),

@@ -74,6 +74,9 @@ struct AttnParams {
   const __bf16* bv;      // BROADCAST heads: V tiles [head][frame][bcap/64][64][64]
   int bcap;              // ceil(T/64)*64
   uint64_t tok_order;    // DENSE heads (bit h) packed in token order: tile t = tokens 64t .. 64t+63
+  uint64_t q_pre;        // heads (bit h) whose Q rows hold q * scale * log2(e)
+  int n_items;           // fixup launch: items in the segments, work-groups of the launch
+  int fix_groups;
   int ntok;              // F*T tokens
   int ntt;               // ceil(F*T/64) token-order tiles
   // work items in segments of one head each (a head has at most two: special-row and patch-row
@@ -301,11 +304,14 @@ __device__ __forceinline__ float exps_half(const f32x16& s, float c, float mc, b
 }
 
 // The block of half step h: O += V(h-1) P(h-1), sn = K(h+1) Q^T, pn = P(h) from s with row sums ts.
+// FAST: the head's Q rows carry the softmax scale and the walk keeps no reference maximum, so
+// P = exp2(s) with no per-score arithmetic before the exponential (see walk_unsafe).
+template <bool FAST>
 __device__ __forceinline__ void half_block(const bf16x8 (&kf)[4], const bf16x8 (&vf)[2][2],
                                            const bf16x8 (&qfrag)[2][4], const f32x16 (&s)[2], f32x16 (&sn)[2],
                                            const bf16x8 (&p)[2][2], bf16x8 (&pn)[2][2], float (&ts)[2], Acc& A,
                                            float c) {
-  const float mc0 = ref_mc(A.m[0], c), mc1 = ref_mc(A.m[1], c);
+  const float mc0 = FAST ? 0.f : ref_mc(A.m[0], c), mc1 = FAST ? 0.f : ref_mc(A.m[1], c);
   sn[0] = sn[1] = f32x16{};
   auto matrix = [&](int i) {
     if (i < 8) {
@@ -319,8 +325,8 @@ __device__ __forceinline__ void half_block(const bf16x8 (&kf)[4], const bf16x8 (
   auto vector = [&](int i) {
     const int g2 = i >> 3, u = 2 * (i & 7);
     const float mc = g2 ? mc1 : mc0;
-    const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[g2][u], c, -mc));
-    const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[g2][u + 1], c, -mc));
+    const float e0 = __builtin_amdgcn_exp2f(FAST ? s[g2][u] : __builtin_fmaf(s[g2][u], c, -mc));
+    const float e1 = __builtin_amdgcn_exp2f(FAST ? s[g2][u + 1] : __builtin_fmaf(s[g2][u + 1], c, -mc));
     const bf16x2 pr = {(__bf16)e0, (__bf16)e1};
     pn[g2][u >> 3][u & 7] = pr[0];
     pn[g2][u >> 3][(u & 7) + 1] = pr[1];
@@ -359,7 +365,15 @@ __device__ __forceinline__ void half_block(const bf16x8 (&kf)[4], const bf16x8 (
 // a row with an unmasked key, whose m is still -inf, always does): values up to 2^64 keep every
 // bf16 P, fp32 sum and O finite, so no per-step maximum is needed. The exact path takes the row
 // maximum of s, rescales O (which then holds every step before h) and l, and recomputes P(h).
-__device__ __forceinline__ void exact_fix(const f32x16 (&s)[2], bf16x8 (&pn)[2][2], float (&ts)[2], Acc& A, float c) {
+// FAST walks (reference fixed at 0) only record that a step went past 2^64 (or was not finite):
+// the work-group then walks the item again without FAST.
+template <bool FAST>
+__device__ __forceinline__ void exact_fix(const f32x16 (&s)[2], bf16x8 (&pn)[2][2], float (&ts)[2], Acc& A, float c,
+                                          bool& unsafe) {
+  if constexpr (FAST) {
+    if (__ballot(!(ts[0] <= 0x1p64f) || !(ts[1] <= 0x1p64f)) != 0) unsafe = true;
+    return;
+  }
   if (__ballot(ts[0] > 0x1p64f || ts[1] > 0x1p64f) == 0) return;
 #pragma unroll
   for (int gq = 0; gq < 2; ++gq) {
@@ -517,10 +531,77 @@ __device__ inline void pace_add(const AttnParams& p, int kind, uint64_t t0, int 
   __hip_atomic_fetch_add(s + 1, (unsigned long long)steps, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-__global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
+// A work item: head, pattern, item index within the head, first query tile, waves with a tile of
+// their own, walk kind, and (BROADCAST) the frame whose rows it writes.
+struct Item {
+  int h, pat, it, qt0, nw, kind, bfr;
+  bool tokord;
+};
+
+__device__ inline Item decode_item(const AttnParams& p, int item) {
+  const Geom& g = p.g;
+  Item d;
+  int oh = 0;
+  while (oh + 1 < p.n_order && item >= p.item_start[oh + 1]) ++oh;
+  d.h = p.order[oh];
+  d.pat = p.pattern[d.h];
+  d.it = item - p.item_start[oh] + p.item_base[oh];
+  d.bfr = 0;
+  const int pat = d.pat, it = d.it;
+  const int ns4 = (g.nst + 3) >> 2;
+  const int groups_pf = (g.NBf + 3) >> 2;
+  d.tokord = pat == SAF3R_DENSE && ((p.tok_order >> d.h) & 1);
+  if (pat == SAF3R_DENSE || pat == SAF3R_SKIP || pat == SAF3R_KEYSET) {
+    d.qt0 = 4 * it;
+    d.nw = min(4, (d.tokord ? p.ntt : g.NT) - d.qt0);
+    d.kind = pat == SAF3R_SKIP ? kSkip : kShared;
+  } else if (pat == SAF3R_BROADCAST) {
+    // query tile qt of frame 0's compact rows, written for frame bfr
+    const int nq = p.bcap / 64, gpf = (nq + 3) >> 2;
+    d.bfr = it / gpf;
+    d.qt0 = 4 * (it - d.bfr * gpf);
+    d.nw = min(4, nq - d.qt0);
+    d.kind = kShared;
+  } else if (pat == SAF3R_TOKEN_DYNAMIC || pat == SAF3R_TOKEN_DYNAMIC_KEYSET || (pat == SAF3R_BLOCK_DYNAMIC && it < ns4)) {
+    d.qt0 = 4 * it;
+    d.nw = min(4, g.nst - d.qt0);
+    d.kind = kShared;
+  } else if (pat == SAF3R_BLOCK_DYNAMIC) {
+    d.qt0 = g.nst + (it - ns4);
+    d.nw = 4;  // four waves on one query tile
+    d.kind = kSplit;
+  } else if (it < g.nst) {
+    d.qt0 = it;
+    d.nw = 1;
+    d.kind = kShared;
+  } else {
+    const int j = it - g.nst, f = j / groups_pf, gg = j % groups_pf;
+    d.qt0 = g.nst + f * g.NBf + 4 * gg;
+    d.nw = min(4, g.NBf - 4 * gg);
+    d.kind = kShared;
+  }
+  return d;
+}
+
+// FAST marker of an item: feature 0 of row 0 of its first query tile (a row that always exists)
+__device__ inline uint16_t* item_marker(const AttnParams& p, const Item& d) {
+  const Geom& g = p.g;
+  int64_t t0;
+  if (d.pat == SAF3R_BROADCAST) t0 = (int64_t)d.bfr * g.T + d.qt0 * 64;
+  else if (d.tokord) t0 = (int64_t)d.qt0 * 64;
+  else if (d.qt0 < g.nst) t0 = (int64_t)(d.qt0 * 64 / g.ns) * g.T + (d.qt0 * 64) % g.ns;
+  else t0 = (int64_t)((d.qt0 - g.nst) / g.NBf) * g.T + g.ns + ((d.qt0 - g.nst) % g.NBf) * 64;
+  return reinterpret_cast<uint16_t*>(p.out + t0 * p.out_stride + (int64_t)d.h * 64);
+}
+
+// The kernel body for work item `item` (uniform). FIXUP: walked again, exactly, because the main
+// launch marked it.
+template <bool FIXUP>
+__device__ __forceinline__ void attn_body(const AttnParams& p, const int item) {
   __shared__ __align__(16) char ring[kRing];
   __shared__ int list[kMaxList];
   __shared__ int wcnt[4];
+  __shared__ int uflag[4];
   __shared__ uint64_t t_start;
 
   const Geom& g = p.g;
@@ -530,52 +611,16 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
   const int tid = __builtin_amdgcn_workitem_id_x();
   const int lane = tid & 63, half = lane >> 5, col = lane & 31;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, uniform
-  const int bid = __builtin_amdgcn_workgroup_id_x();
-  if (bid == 0 && tid < 4 && p.pace) {  // the slot the next call accumulates into starts at zero
+  if (!FIXUP && item == 0 && tid < 4 && p.pace) {  // the slot the next call accumulates into starts at zero
     unsigned long long* z = p.pace + (tid >> 1) * 6 + p.pace_zero * 2 + (tid & 1);
     __hip_atomic_store(z, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 
   // ---- decode the work item (uniform) ----
-  int oh = 0;
-  while (oh + 1 < p.n_order && bid >= p.item_start[oh + 1]) ++oh;
-  const int h = p.order[oh];
-  const int pat = p.pattern[h];
-  const int it = bid - p.item_start[oh] + p.item_base[oh];
-  const int ns4 = (g.nst + 3) >> 2;
-  const int groups_pf = (g.NBf + 3) >> 2;
-  int qt0, nw, kind;
-  int bfr = 0;  // BROADCAST: the frame whose rows the item writes
-  const bool tokord = pat == SAF3R_DENSE && ((p.tok_order >> h) & 1);
-  if (pat == SAF3R_DENSE || pat == SAF3R_SKIP || pat == SAF3R_KEYSET) {
-    qt0 = 4 * it;
-    nw = min(4, (tokord ? p.ntt : g.NT) - qt0);
-    kind = pat == SAF3R_SKIP ? kSkip : kShared;
-  } else if (pat == SAF3R_BROADCAST) {
-    // query tile qt of frame 0's compact rows, written for frame bfr
-    const int nq = p.bcap / 64, gpf = (nq + 3) >> 2;
-    bfr = it / gpf;
-    qt0 = 4 * (it - bfr * gpf);
-    nw = min(4, nq - qt0);
-    kind = kShared;
-  } else if (pat == SAF3R_TOKEN_DYNAMIC || pat == SAF3R_TOKEN_DYNAMIC_KEYSET || (pat == SAF3R_BLOCK_DYNAMIC && it < ns4)) {
-    qt0 = 4 * it;
-    nw = min(4, g.nst - qt0);
-    kind = kShared;
-  } else if (pat == SAF3R_BLOCK_DYNAMIC) {
-    qt0 = g.nst + (it - ns4);
-    nw = 4;  // four waves on one query tile
-    kind = kSplit;
-  } else if (it < g.nst) {
-    qt0 = it;
-    nw = 1;
-    kind = kShared;
-  } else {
-    const int j = it - g.nst, f = j / groups_pf, gg = j % groups_pf;
-    qt0 = g.nst + f * g.NBf + 4 * gg;
-    nw = min(4, g.NBf - 4 * gg);
-    kind = kShared;
-  }
+  const Item d = decode_item(p, item);
+  const int h = d.h, pat = d.pat, qt0 = d.qt0, nw = d.nw, kind = d.kind;
+  const int bfr = d.bfr;  // BROADCAST: the frame whose rows the item writes
+  const bool tokord = d.tokord;
   const bool wactive = w < nw;
   const int qt = kind == kSplit ? qt0 : qt0 + (wactive ? w : 0);
   const bool qspecial = pat != SAF3R_BROADCAST && !tokord && qt < g.nst;
@@ -634,6 +679,17 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
     return;
   }
 
+  // Heads whose Q rows carry the softmax scale (q * scale * log2 e, rounded once when packed) walk
+  // in those units (c = 1) and without a reference maximum (FAST: P = exp2(s)) as long as every
+  // partial row sum stays within [2^-64, 2^64] (scores within about 64 units of 0). A FAST item that
+  // leaves that range stores nothing but a marker, 0xFFFF (a NaN, which finite inputs never give) in
+  // feature 0 of its first row, and the launch that follows (FIXUP) walks the marked items again
+  // with the exact reference maximum.
+  const bool qpre = h < 64 && ((p.q_pre >> h) & 1);
+  const bool fast = qpre && !FIXUP;
+  const float c = qpre ? 1.f : p.c;
+  // (the marker address is recomputed where it is used rather than held through the walk)
+  auto marker = [&]() { return item_marker(p, d); };
   // ---- Q fragments: lane holds features 32*half .. 32*half+31 of rows 32*gq + col ----
   bf16x8 qfrag[2][4];
   const __bf16* qrows = pat == SAF3R_BROADCAST ? p.bq + (int64_t)p.slot[h] * p.bcap * 64 : p.q + head_base * 64;
@@ -645,18 +701,45 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
   }
 
   Acc A;
+  auto init_acc = [&](bool fast) {
 #pragma unroll
-  for (int a = 0; a < 2; ++a) {
-    A.o[a][0] = A.o[a][1] = f32x16{};
-    A.m[a] = -__builtin_inff();
-    A.l[a] = 0.f;
-  }
-  const float c = p.c;
+    for (int a = 0; a < 2; ++a) {
+      A.o[a][0] = A.o[a][1] = f32x16{};
+      A.m[a] = fast ? 0.f : -__builtin_inff();
+      A.l[a] = 0.f;
+    }
+  };
+  // FAST end of a walk: true (work-group uniform) when the item must be walked again exactly
+  auto walk_unsafe = [&](bool unsafe) -> bool {
+    int64_t qtok[2];
+    int frow[2];
+    row_info(qtok, frow);
+    bool low = false;
+#pragma unroll
+    for (int gq = 0; gq < 2; ++gq) low |= qtok[gq] >= 0 && !(partner_sum(A.l[gq]) >= 0x1p-64f);
+    const bool bad = unsafe || __ballot(low) != 0;
+    if (lane == 0) uflag[w] = bad ? 1 : 0;
+    __syncthreads();
+    return (uflag[0] | uflag[1] | uflag[2] | uflag[3]) != 0;
+  };
 
   if (kind == kShared) {
     // The shared-mode walk, instantiated separately for KEYSET heads (compact key-set tiles) and
     // for every other pattern, so neither carries the other's state in registers.
-    auto shared_walk = [&](auto ks_tag) {
+    auto shared_walk = [&](auto ks_tag, auto fast_tag) {
+    constexpr bool FAST = decltype(fast_tag)::value;
+    bool unsafe = false;
+    init_acc(FAST);
+    // stores the rows, or (FAST, unsafe) marks the item for the exact walk
+    auto finish = [&]() {
+      if constexpr (FAST) {
+        if (walk_unsafe(unsafe)) {
+          if (tid == 0) *marker() = 0xFFFFu;
+          return;
+        }
+      }
+      store(A);
+    };
     // ---- key-tile sequence (uniform) ----
     Walk wk;
     bool frame_rel = false, rel_patch = false;
@@ -840,9 +923,9 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
           // half step 2t: PV of tile t-1 keys 32..63, scores of tile t keys 32..63
           if (v > 0 || t0 > 0) load_v(ring + ((v + 3) & 3) * 16384 + 8192, 1, vf, half, col);
           load_k(ring + v * 16384, 1, kf, half, col);
-          half_block(kf, vf, qfrag, s_cur, s_nxt, pc, pn, ts, A, c);
+          half_block<FAST>(kf, vf, qfrag, s_cur, s_nxt, pc, pn, ts, A, c);
           if (kv_cur < 64) mask_valid(s_nxt, kv_cur, 32, half);
-          exact_fix(s_cur, pn, ts, A, c);
+          exact_fix<FAST>(s_cur, pn, ts, A, c, unsafe);
           A.l[0] += ts[0];
           A.l[1] += ts[1];
           advance();
@@ -854,9 +937,9 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
           // half step 2t+1: PV of tile t keys 0..31, scores of tile t + 1 keys 0..31
           load_v(ring + v * 16384 + 8192, 0, vf, half, col);
           load_k(ring + ((v + 1) & 3) * 16384, 0, kf, half, col);
-          half_block(kf, vf, qfrag, s_nxt, s_cur, pn, pc, ts, A, c);
+          half_block<FAST>(kf, vf, qfrag, s_nxt, s_cur, pn, pc, ts, A, c);
           if (kv_nxt < 64) mask_valid(s_cur, kv_nxt, 0, half);
-          exact_fix(s_nxt, pc, ts, A, c);
+          exact_fix<FAST>(s_nxt, pc, ts, A, c, unsafe);
           A.l[0] += ts[0];
           A.l[1] += ts[1];
           kv_cur = kv_nxt;
@@ -872,7 +955,7 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
         }
       if (!rel_patch) {
         if (tid == 0 && paced) pace_add(p, 0, t_start, cnt);
-        store(A);
+        finish();
         return;
       }
       __syncthreads();  // every wave is done with the ring before the frame-relative walk reuses it
@@ -907,11 +990,15 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
         }
       }
     }
-    store(A);
+    finish();
+    };
+    auto run = [&](auto ks_tag) {
+      if (fast) shared_walk(ks_tag, std::true_type{});
+      else shared_walk(ks_tag, std::false_type{});
     };
     if (pat == SAF3R_KEYSET || pat == SAF3R_TOKEN_DYNAMIC_KEYSET || pat == SAF3R_BROADCAST || tokord)
-      shared_walk(std::true_type{});
-    else shared_walk(std::false_type{});
+      run(std::true_type{});
+    else run(std::false_type{});
     return;
   }
 
@@ -1018,6 +1105,12 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
         }
     };
 
+    // the wave's walk over its list positions; FAST: true when the wave must walk them again exactly
+    // (each wave's partial result is merged with its own reference maximum below)
+    auto split_walk = [&](auto fast_tag) -> bool {
+    constexpr bool FAST = decltype(fast_tag)::value;
+    bool unsafe = false;
+    init_acc(FAST);
     wait_vm<0>();
     if (nw > 0) {
       const auto ent = [&](int i) { return entry(min(i, nw - 1)); };
@@ -1050,24 +1143,24 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
         wait_vm<8>();
         if (t > 0) load_vh(slots + 8192 + 4096, vf);
         load_k(slots + 8192, 0, kf, half, col);
-        half_block(kf, vf, qfrag, s_cur, s_nxt, pc, pn, ts, A, c);
+        half_block<FAST>(kf, vf, qfrag, s_cur, s_nxt, pc, pn, ts, A, c);
         issue_k(e1, 1);
         issue_v(e0, 1);
         const int kv0 = e0 & 127;
         if (kv0 < 64) mask_valid(s_nxt, kv0, 32, half);
-        exact_fix(s_cur, pn, ts, A, c);
+        exact_fix<FAST>(s_cur, pn, ts, A, c, unsafe);
         A.l[0] += ts[0];
         A.l[1] += ts[1];
         // half step 2t+1: PV of block t half 0, scores of block t+1 half 0, softmax of block t half 1
         wait_vm<8>();
         load_vh(slots + 4096, vf);
         load_k(slots, 0, kf, half, col);
-        half_block(kf, vf, qfrag, s_nxt, s_cur, pn, pc, ts, A, c);
+        half_block<FAST>(kf, vf, qfrag, s_nxt, s_cur, pn, pc, ts, A, c);
         issue_k(e2, 0);
         issue_v(e1, 0);
         const int kv1 = e1 & 127;
         if (kv1 < 32) mask_valid(s_cur, kv1, 0, half);
-        exact_fix(s_nxt, pc, ts, A, c);
+        exact_fix<FAST>(s_nxt, pc, ts, A, c, unsafe);
         A.l[0] += ts[0];
         A.l[1] += ts[1];
         e0 = e1;
@@ -1085,12 +1178,26 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
           A.o[dh][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[j][dh], pc[0][j], A.o[dh][0], 0, 0, 0);
           A.o[dh][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[j][dh], pc[1][j], A.o[dh][1], 0, 0, 0);
         }
+      if constexpr (FAST) {
+        bool low = false;
+#pragma unroll
+        for (int gq = 0; gq < 2; ++gq) low |= !(partner_sum(A.l[gq]) >= 0x1p-64f);
+        return unsafe || __ballot(low) != 0;
+      }
     }
+    return false;
+    };
+    const bool unsafe = fast ? split_walk(std::true_type{}) : split_walk(std::false_type{});
 
     // ---- merge the four partial results through LDS ----
 #pragma unroll
     for (int gq = 0; gq < 2; ++gq) A.l[gq] = partner_sum(A.l[gq]);
+    if (lane == 0) uflag[w] = unsafe ? 1 : 0;
     __syncthreads();  // every wave is done with its slots and with the list
+    if (uflag[0] | uflag[1] | uflag[2] | uflag[3]) {  // a FAST wave left the range: the tile is walked again
+      if (tid == 0) *marker() = 0xFFFFu;
+      return;
+    }
     float* obuf = reinterpret_cast<float*>(ring) + w * 4096;  // [64 rows][64 d] fp32 per wave
     float* mls = reinterpret_cast<float*>(list);                // m[4][64], l[4][64]
 #pragma unroll
@@ -1154,6 +1261,41 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
       u32x4* o4 = reinterpret_cast<u32x4*>(p.out + tok * p.out_stride + (int64_t)h * 64 + d0);
       o4[0] = u32x4{wv[0], wv[1], wv[2], wv[3]};
       o4[1] = u32x4{wv[4], wv[5], wv[6], wv[7]};
+    }
+  }
+}
+
+__global__ __launch_bounds__(256, 2) void sparse_attn_kernel(AttnParams p) {
+  attn_body<false>(p, __builtin_amdgcn_workgroup_id_x());
+}
+
+// Work-group g reads the markers of items g, g + G, g + 2G, ... (G = fix_groups), 64 at a time on
+// wave 0's lanes, and walks the marked ones exactly, one after the other.
+__global__ __launch_bounds__(256, 2) void sparse_attn_fixup_kernel(AttnParams p) {
+  __shared__ uint64_t marked;
+  const int tid = __builtin_amdgcn_workitem_id_x();
+  const int G = p.fix_groups;
+  for (int base = __builtin_amdgcn_workgroup_id_x(); base < p.n_items; base += 64 * G) {
+    if (tid < 64) {
+      const int item = base + G * tid;
+      bool m = false;
+      if (item < p.n_items) {
+        const Item d = decode_item(p, item);
+        m = d.kind != kSkip && *reinterpret_cast<const volatile uint16_t*>(item_marker(p, d)) == 0xFFFFu;
+      }
+      const uint64_t b = __ballot(m);
+      if (tid == 0) marked = b;
+    }
+    __syncthreads();
+    uint64_t b = marked;
+    b = ((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32)) << 32) |
+        (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b);
+    __syncthreads();  // every wave has read the mask before the next batch writes it
+    while (b) {
+      const int l = __builtin_ctzll(b);
+      b &= b - 1;
+      attn_body<true>(p, base + G * l);
+      __syncthreads();  // the next item reuses the LDS
     }
   }
 }
@@ -1229,7 +1371,8 @@ extern "C" int saf3r_sparse_attn_fwd(const void* q_packed, const void* k_packed,
                                      void* out, int64_t out_row_stride, const void* keyset_k, const void* keyset_v,
                                      const int32_t* keyset_count, int64_t keyset_capacity, const void* bcast_q,
                                      const void* bcast_k, const void* bcast_v, const uint8_t* token_order,
-                                     int flags, unsigned long long* pace, unsigned int pace_seq, void* stream) {
+                                     const uint8_t* q_scaled, int flags, unsigned long long* pace,
+                                     unsigned int pace_seq, void* stream) {
   if (int e = injected("saf3r_sparse_attn_fwd")) return e;
   AttnParams p;
   if (!make_geom(frames, tokens_per_frame, num_special, &p.g))
@@ -1292,6 +1435,10 @@ extern "C" int saf3r_sparse_attn_fwd(const void* q_packed, const void* k_packed,
       p.tok_order |= 1ull << h;
     }
   }
+  p.q_pre = 0;
+  if (q_scaled)
+    for (int h = 0; h < num_heads; ++h)
+      if (q_scaled[h]) p.q_pre |= 1ull << h;
   p.q = (const __bf16*)q_packed;
   p.k = (const __bf16*)k_packed;
   p.v = (const __bf16*)v_packed;
@@ -1338,5 +1485,30 @@ extern "C" int saf3r_sparse_attn_fwd(const void* q_packed, const void* k_packed,
   p.item_start[p.n_order] = (int)total;
   if (total == 0) return SAF3R_OK;
   hipLaunchKernelGGL(sparse_attn_kernel, dim3((unsigned)total), dim3(256), 0, (hipStream_t)stream, p);
+  if (int e = check_launch("saf3r_sparse_attn_fwd")) return e;
+  // the exact walk of the items that left the FAST range: the same items of the prescaled heads,
+  // in the fixed order; every other item returns after reading its marker
+  AttnParams f = p;
+  f.pace = nullptr;
+  f.phase_dense = f.phase_split = 0;
+  int64_t ftotal = 0;
+  f.n_order = 0;
+  for (int i = 0; i < nseg; ++i) {
+    if (!((p.q_pre >> segs[i].h) & 1) || p.pattern[segs[i].h] == SAF3R_SKIP) continue;
+    f.order[f.n_order] = (int16_t)segs[i].h;
+    f.item_start[f.n_order] = (int)ftotal;
+    f.item_base[f.n_order] = segs[i].base;
+    ftotal += segs[i].items;
+    ++f.n_order;
+  }
+  f.item_start[f.n_order] = (int)ftotal;
+  if (ftotal == 0) return SAF3R_OK;
+  int cus = 0, dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    cus = 256;
+  f.n_items = (int)ftotal;
+  f.fix_groups = (int)std::min<int64_t>(ftotal, 2 * (int64_t)cus);  // one resident round
+  hipLaunchKernelGGL(sparse_attn_fixup_kernel, dim3((unsigned)f.fix_groups), dim3(256), 0, (hipStream_t)stream, f);
   return check_launch("saf3r_sparse_attn_fwd");
 }

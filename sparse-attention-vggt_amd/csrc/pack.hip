@@ -38,6 +38,8 @@ struct PackParams {
   float* qk32;         // fp32 q and k rows of the flagged heads: [slot][q, k][F*T tokens][64]
   uint64_t f32_heads;  // heads (bit h) whose fp32 q / k rows are also written
   int8_t f32slot[64];  // slot of a flagged head in qk32
+  uint64_t q_scaled;   // heads (bit h) whose packed Q is q * q_scale
+  float q_scale;
 };
 
 // One 256-thread workgroup per (64-slot tile, head). Four threads own one slot row, 16 features
@@ -129,6 +131,10 @@ __global__ __launch_bounds__(256) void pack_qkv_kernel(PackParams p) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) d32[j] = f32x4{x[4 * j], x[4 * j + 1], x[4 * j + 2], x[4 * j + 3]};
     }
+    if (which == 0 && h < 64 && ((p.q_scaled >> h) & 1)) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) x[j] *= p.q_scale;
+    }
     u32x4 o0, o1;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -185,7 +191,7 @@ extern "C" int saf3r_pack_qkv(const void* q, const void* k, const void* v, int64
                               const float* k_ln_bias, float ln_eps, int apply_ln, const int32_t* pos,
                               const float* rope_cos, const float* rope_sin, int rope_positions, void* q_packed,
                               void* k_packed, void* v_packed, const uint8_t* token_order, const uint8_t* fp32_heads,
-                              float* qk32, void* stream) {
+                              float* qk32, const uint8_t* q_scaled, float q_scale, void* stream) {
   if (int e = injected("saf3r_pack_qkv")) return e;
   PackParams p;
   if (!make_geom(frames, tokens_per_frame, num_special, &p.g))
@@ -241,6 +247,17 @@ extern "C" int saf3r_pack_qkv(const void* q, const void* k, const void* v, int64
     }
     if (n32 > 0 && (!qk32 || (uintptr_t)qk32 % 16))
       return fail(SAF3R_ERR_INVALID, "saf3r_pack_qkv: fp32 heads need a 16-byte aligned qk32 buffer");
+  }
+  p.q_scaled = 0;
+  p.q_scale = q_scale;
+  if (q_scaled) {
+    for (int h = 0; h < num_heads; ++h) {
+      if (!q_scaled[h]) continue;
+      if (h >= 64) return fail(SAF3R_ERR_UNSUPPORTED, "saf3r_pack_qkv: scaled Q is supported for heads 0..63");
+      p.q_scaled |= 1ull << h;
+    }
+    if (p.q_scaled && !(q_scale > 0.f && q_scale < 3.0e38f))
+      return fail(SAF3R_ERR_INVALID, "saf3r_pack_qkv: q_scale must be positive and finite");
   }
   dim3 grid(p.g.NT, num_heads);
   hipLaunchKernelGGL(pack_qkv_kernel, grid, dim3(256), 0, (hipStream_t)stream, p);

@@ -24,6 +24,7 @@ PATTERN_NAMES = {
     KEYSET: "keyset", BROADCAST: "broadcast_first", TOKEN_DYNAMIC_KEYSET: "dino_topk_strided",
 }
 FIXED_ORDER = 1  # saf3r_attn_flags
+LOG2E = 1.4426950408889634
 KEYSET_PATTERNS = (KEYSET, TOKEN_DYNAMIC_KEYSET)  # heads served from the key-set buffers
 TOKEN_PATTERNS = (TOKEN_DYNAMIC, TOKEN_DYNAMIC_KEYSET)  # heads whose patch rows gather-attend est_topk_idx
 
@@ -133,16 +134,25 @@ def packed_buffers(geom: Geometry, num_heads: int, device) -> tuple[torch.Tensor
     return q, k, v
 
 
+def prescale_factor(scale: float | None = None) -> float:
+    """The factor ``pack_qkv(q_scaled=...)`` applies to Q for ``sparse_attn_fwd(q_scaled=...)``:
+    softmax scale (default 1/sqrt(64)) times log2(e)."""
+    return (1.0 / math.sqrt(HEAD_DIM) if scale is None else scale) * LOG2E
+
+
 def pack_qkv(q, k, v, tok_stride: int, head_stride: int, geom: Geometry, num_heads: int,
              ln_q=None, ln_k=None, ln_eps: float = 1e-5, pos=None, rope_base=None, rope_positions=None, out=None,
-             token_order: Sequence[bool] | None = None, fp32_heads: Sequence[bool] | None = None):
+             token_order: Sequence[bool] | None = None, fp32_heads: Sequence[bool] | None = None,
+             q_scaled: Sequence[bool] | None = None, q_scale: float | None = None):
     """QK-LayerNorm + RoPE-2D + packing (``saf3r_pack_qkv``). ``q``/``k``/``v`` are tensors (or
     views) whose element (t, h, d) is at ``data_ptr + t*tok_stride + h*head_stride + d``.
     RoPE is applied when ``rope_base`` is given; ``rope_positions`` is the table length
     (default: max position + 1, which costs one device-to-host read). Heads flagged in
     ``token_order`` are packed in token order (see ``token_order_heads``). With ``fp32_heads``
     the call returns a fourth tensor, fp32 [n_flagged, 2, N, 64]: the fp32 q (index 0) and k (1) of
-    the flagged heads after LayerNorm / RoPE, in token order and increasing head order."""
+    the flagged heads after LayerNorm / RoPE, in token order and increasing head order. Heads flagged
+    in ``q_scaled`` get their packed Q multiplied by ``q_scale`` (default ``prescale_factor()``) in
+    fp32 before the one bf16 rounding; pass the same flags to ``sparse_attn_fwd``."""
     _need_cuda(q, k, v)
     lib = _lib.load()
     qp, kp, vp = out if out is not None else packed_buffers(geom, num_heads, q.device)
@@ -171,7 +181,8 @@ def pack_qkv(q, k, v, tok_stride: int, head_stride: int, geom: Geometry, num_hea
         num_heads, _ptr(qw), _ptr(qb), _ptr(kw), _ptr(kb), float(ln_eps), int(apply_ln),
         _ptr(pos) if rc is not None else None, _ptr(rc), _ptr(rs), npos, _ptr(qp), _ptr(kp), _ptr(vp),
         _u8_flags(token_order, num_heads), _u8_flags(fp32_heads, num_heads) if qk32 is not None else None,
-        _ptr(qk32), _lib.stream_ptr()))
+        _ptr(qk32), _u8_flags(q_scaled, num_heads), float(prescale_factor() if q_scale is None else q_scale),
+        _lib.stream_ptr()))
     if fp32_heads is not None:
         return qp, kp, vp, qk32
     return qp, kp, vp
@@ -252,12 +263,15 @@ def block_select(pooled_q: torch.Tensor, pooled_k: torch.Tensor, frames: int, bl
 def sparse_attn_fwd(qp, kp, vp, geom: Geometry, patterns: Sequence[int], sel: torch.Tensor | None = None,
                     scale: float | None = None, out: torch.Tensor | None = None,
                     keysets: "KeySets | None" = None, broadcast: "Broadcast | None" = None,
-                    token_order: Sequence[bool] | None = None, order: str | None = None) -> torch.Tensor:
+                    token_order: Sequence[bool] | None = None, order: str | None = None,
+                    q_scaled: Sequence[bool] | None = None) -> torch.Tensor:
     """All heads in one launch. Returns (or fills) ``out`` bf16 [N, H*64] in natural token order.
     ``keysets`` carries the compact K/V of the KEYSET heads and ``broadcast`` the frame-0 / per-frame
     buffers of the BROADCAST heads (each in increasing head order); ``token_order`` flags the
-    DENSE heads that ``pack_qkv`` packed in token order. ``order`` ("paced" / "fixed", default
-    ``walk_order()``) chooses the key-walk order (see ``set_walk_order``)."""
+    DENSE heads that ``pack_qkv`` packed in token order; ``q_scaled`` the heads whose packed Q
+    carries ``prescale_factor(scale)`` (``pack_qkv(q_scaled=...)``), which then skip the running
+    maximum. ``order`` ("paced" / "fixed", default ``walk_order()``) chooses the key-walk order
+    (see ``set_walk_order``)."""
     _need_cuda(qp, kp, vp)
     lib = _lib.load()
     H = qp.shape[0]
@@ -308,8 +322,8 @@ def sparse_attn_fwd(qp, kp, vp, geom: Geometry, patterns: Sequence[int], sel: to
     _lib.check(lib.saf3r_sparse_attn_fwd(
         _ptr(qp), _ptr(kp), _ptr(vp), geom.frames, geom.tokens_per_frame, geom.num_special, H,
         pat, _ptr(sel), width, float(scale), _ptr(out), out.stride(0), _ptr(ks_k), _ptr(ks_v), _ptr(ks_n),
-        ks_cap, _ptr(bq), _ptr(bk), _ptr(bv), _u8_flags(token_order, H), flags, _ptr(pace), seq,
-        _lib.stream_ptr()))
+        ks_cap, _ptr(bq), _ptr(bk), _ptr(bv), _u8_flags(token_order, H), _u8_flags(q_scaled, H), flags,
+        _ptr(pace), seq, _lib.stream_ptr()))
     _mark("sparse_attn", "end")
     return out
 

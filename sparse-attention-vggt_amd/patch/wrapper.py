@@ -93,6 +93,16 @@ class BaseHeadwiseSparseAttentionWrapper(nn.Module):
         probe = {h for h in self.keyset_heads if self.head_cfg[h]["mode"] == "q_probe_topk"}
         self.fp32_heads = sorted(probe | set(self.dino_heads))
         self.fp32_slot = {h: i for i, h in enumerate(self.fp32_heads)}
+        # pack Q with the softmax scale folded in (one bf16 rounding of the fp32 q * scale * log2 e), so
+        # that the attention walks skip the running maximum; off for tests that compare the plain layout
+        self.prescale_q = True
+
+    def q_scaled_heads(self) -> list[bool]:
+        """Heads whose packed Q carries ``ops.prescale_factor()``: every head except the first
+        correspondence head of a lazy dino_topk layer, whose packed Q the token top-k reads as the
+        reference's q (``fused_qk_topk.py:120-217``)."""
+        skip = self.first_dino_head if self.lazy_dino_topk else None
+        return [self.prescale_q and h != skip for h in range(self.num_heads)]
 
     # ------------------------------------------------------------------------------------
     def geometry(self, num_tokens: int) -> Geometry:
@@ -122,8 +132,10 @@ class BaseHeadwiseSparseAttentionWrapper(nn.Module):
             npos = max(self.patch_height, self.patch_width) + 1 if self.patch_height else None
         tord = ops.token_order_heads(self.patterns)  # dense heads: unpadded token-order tiles
         f32 = [h in self.fp32_slot for h in range(H)] if self.fp32_heads else None
+        qs = self.q_scaled_heads()
         packed = ops.pack_qkv(qkv, qkv[:, C:], qkv[:, 2 * C:], 3 * C, HEAD_DIM, geom, H, ln_q=ln_q, ln_k=ln_k,
-                              ln_eps=eps, pos=p2, rope_base=base, rope_positions=npos, token_order=tord, fp32_heads=f32)
+                              ln_eps=eps, pos=p2, rope_base=base, rope_positions=npos, token_order=tord, fp32_heads=f32,
+                              q_scaled=qs, q_scale=ops.prescale_factor(getattr(om, "scale", None)))
         qp, kp, vp = packed[:3]
         qk32 = packed[3] if f32 is not None else None
         sel = None
@@ -140,8 +152,8 @@ class BaseHeadwiseSparseAttentionWrapper(nn.Module):
         bcast = None
         if self.broadcast_heads:  # broadcast_first: frame 0's Q/K rows and every frame's V tiles
             bcast = ops.broadcast_gather(qp, kp, geom, self.broadcast_heads, qkv[:, 2 * C:], qkv.stride(0), HEAD_DIM)
-        out = ops.sparse_attn_fwd(qp, kp, vp, geom, self.patterns, sel, keysets=keysets, broadcast=bcast,
-                                  token_order=tord)
+        out = ops.sparse_attn_fwd(qp, kp, vp, geom, self.patterns, sel, scale=getattr(om, "scale", None),
+                                  keysets=keysets, broadcast=bcast, token_order=tord, q_scaled=qs)
         if self.dino_heads:  # image rows: gather attention over est_topk_idx with the fp32 q / k
             est = self.est_topk_idx
             P, W, T, ns = geom.patches, est.shape[1], geom.tokens_per_frame, geom.num_special

@@ -49,15 +49,16 @@ def oracle_keysets(w, qk32, og, ops):
 
 
 def packed_qkv(w, x, pos, geom, ops):
-    """The q / k / v [H, N, 64] (bf16, natural token order) the wrapper's kernels consumed for input x,
-    and {head: (q, k)} fp32 [N, 64] rows of its fp32 heads (probe and dino heads)."""
+    """The q / k / v [H, N, 64] (bf16, natural token order) the wrapper's kernels consumed for input x
+    (Q of the heads in ``w.q_scaled_heads()`` with ``ops.prescale_factor()`` folded in, as packed), and
+    {head: (q, k)} fp32 [N, 64] rows of its fp32 heads (probe and dino heads)."""
     N, dim, H = geom.tokens, w.orig_module.qkv.in_features, w.num_heads
     om = w.orig_module
     qkv = om.qkv(x).reshape(N, 3 * dim).to(torch.bfloat16).contiguous()
     f32 = [h in w.fp32_slot for h in range(H)]
     qp, kp, vp, qk32 = ops.pack_qkv(qkv, qkv[:, dim:], qkv[:, 2 * dim:], 3 * dim, 64, geom, H,
                                     ln_q=(om.q_norm.weight, om.q_norm.bias), ln_k=(om.k_norm.weight, om.k_norm.bias),
-                                    pos=pos[0], rope_base=100.0, fp32_heads=f32)
+                                    pos=pos[0], rope_base=100.0, fp32_heads=f32, q_scaled=w.q_scaled_heads())
     torch.cuda.synchronize()
     toks = slot_tokens(geom.frames, geom.tokens_per_frame, geom.num_special)
     q, _ = unpack_rows(qp.cpu(), toks, N)
@@ -73,8 +74,13 @@ def check_layer_output(w, x, pos, y, geom, ops, li, tol=(2e-2, 2e-3)):
     om = w.orig_module
     q, k, v, rows32 = packed_qkv(w, x, pos, geom, ops)
     og = OA.Geometry(geom.frames, geom.tokens_per_frame, geom.num_special)
+    c = ops.prescale_factor()
+    qs = w.q_scaled_heads()
     for h, (q32, k32) in rows32.items():  # the fp32 rows round to the bf16 ones the attention read
-        assert torch.equal(q32.to(torch.bfloat16), q[h]) and torch.equal(k32.to(torch.bfloat16), k[h])
+        assert torch.equal((q32 * c if qs[h] else q32).to(torch.bfloat16), q[h])
+        assert torch.equal(k32.to(torch.bfloat16), k[h])
+    # the attention's q: a prescaled head's packed values divided by the factor, in fp32
+    q_att = torch.stack([q[h].float() / c if qs[h] else q[h].float() for h in range(w.num_heads)])
     sel = oracle_keysets(w, rows32, og, ops)
     if w.keyset_heads:  # the kernels' key sets are the oracle's, member for member
         ks = w.last_keysets
@@ -89,7 +95,7 @@ def check_layer_output(w, x, pos, y, geom, ops, li, tol=(2e-2, 2e-3)):
         assert torch.equal(w.last_selection.cpu(), torch.stack([sel[h] for h in w.dyn_heads]).to(torch.int32))
     est = w.est_topk_idx.cpu() if w.dino_heads else None
     gqk = {h: rows32[h] for h in w.dino_heads}
-    heads = OA.head_outputs(q.float(), k.float(), v.float(), list(w.patterns), og, sel, est_topk_idx=est,
+    heads = OA.head_outputs(q_att, k.float(), v.float(), list(w.patterns), og, sel, est_topk_idx=est,
                             dtype=torch.float64, gather_qk_by_head=gqk)
     attn = heads.permute(1, 0, 2).reshape(N, dim).to(torch.bfloat16).float()
     if w.last_attention is not None:  # the attention output itself, at the attention tolerance

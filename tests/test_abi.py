@@ -24,7 +24,7 @@ def test_library_exports_every_declared_symbol(pkg):
     for n in names:
         assert hasattr(lib, n), n
     assert set(names) == set(lib_mod.EXPORTS)
-    assert lib.saf3r_abi_version() == lib_mod.ABI_VERSION == 7
+    assert lib.saf3r_abi_version() == lib_mod.ABI_VERSION == 8
 
 
 def test_packed_slots_matches_layout(pkg):
@@ -44,39 +44,39 @@ def test_invalid_arguments_fail_before_launch(pkg):
     lib = L.load()
     pat = (ctypes.c_int32 * 2)(0, 0)
     rc = lib.saf3r_sparse_attn_fwd(None, None, None, 2, 100, 5, 2, pat, None, 0, 0.125, None, 128, None, None, None,
-                                   0, None, None, None, None, 0, None, 0, None)
+                                   0, None, None, None, None, None, 0, None, 0, None)
     assert rc == 1 and b"null" in lib.saf3r_last_error()
     bad = (ctypes.c_int32 * 1)(10)
     dev = ctypes.c_void_p(16)
     rc = lib.saf3r_sparse_attn_fwd(dev, dev, dev, 2, 100, 5, 1, bad, None, 0, 0.125, dev, 64, None, None, None, 0,
-                                   None, None, None, None, 0, None, 0, None)
+                                   None, None, None, None, None, 0, None, 0, None)
     assert rc == 1 and b"unknown pattern" in lib.saf3r_last_error()
     ks = (ctypes.c_int32 * 1)(7)  # KEYSET without its buffers
     rc = lib.saf3r_sparse_attn_fwd(dev, dev, dev, 2, 100, 5, 1, ks, None, 0, 0.125, dev, 64, None, None, None, 0,
-                                   None, None, None, None, 0, None, 0, None)
+                                   None, None, None, None, None, 0, None, 0, None)
     assert rc == 1 and b"key-set" in lib.saf3r_last_error()
     tks = (ctypes.c_int32 * 1)(9)  # strided dino special rows without the key-set buffers
     rc = lib.saf3r_sparse_attn_fwd(dev, dev, dev, 2, 100, 5, 1, tks, None, 0, 0.125, dev, 64, None, None, None, 0,
-                                   None, None, None, None, 0, None, 0, None)
+                                   None, None, None, None, None, 0, None, 0, None)
     assert rc == 1 and b"key-set" in lib.saf3r_last_error()
     rc = lib.saf3r_sparse_attn_fwd(dev, dev, dev, 2, 100, 5, 1, ks, None, 0, 0.125, dev, 64, dev, dev, dev, 100,
-                                   None, None, None, None, 0, None, 0, None)
+                                   None, None, None, None, None, 0, None, 0, None)
     assert rc == 1 and b"multiple of 64" in lib.saf3r_last_error()
     bc = (ctypes.c_int32 * 1)(8)  # BROADCAST without its buffers
     rc = lib.saf3r_sparse_attn_fwd(dev, dev, dev, 2, 100, 5, 1, bc, None, 0, 0.125, dev, 64, None, None, None, 0,
-                                   None, dev, dev, None, 0, None, 0, None)
+                                   None, dev, dev, None, None, 0, None, 0, None)
     assert rc == 1 and b"BROADCAST" in lib.saf3r_last_error()
     fl = (ctypes.c_int32 * 1)(1)  # token order on a FRAME_LOCAL head
     tord = (ctypes.c_uint8 * 1)(1)
     rc = lib.saf3r_sparse_attn_fwd(dev, dev, dev, 2, 100, 5, 1, fl, None, 0, 0.125, dev, 64, None, None, None, 0,
-                                   None, None, None, tord, 0, None, 0, None)
+                                   None, None, None, tord, None, 0, None, 0, None)
     assert rc == 1 and b"only DENSE" in lib.saf3r_last_error()
     dn = (ctypes.c_int32 * 1)(0)
     rc = lib.saf3r_sparse_attn_fwd(dev, dev, dev, 2, 100, 5, 1, dn, None, 0, 0.125, dev, 64, None, None, None, 0,
-                                   None, None, None, None, 6, None, 0, None)
+                                   None, None, None, None, None, 6, None, 0, None)
     assert rc == 1 and b"unknown flags" in lib.saf3r_last_error()
     rc = lib.saf3r_sparse_attn_fwd(dev, dev, dev, 2, 100, 5, 1, dn, None, 0, 0.125, dev, 64, None, None, None, 0,
-                                   None, None, None, None, 0, ctypes.c_void_p(20), 0, None)
+                                   None, None, None, None, None, 0, ctypes.c_void_p(20), 0, None)
     assert rc == 1 and b"8-byte" in lib.saf3r_last_error()
     rc = lib.saf3r_keyset_build(None, 0, 1, dev, dev, dev, dev, 2, 100, 5, dev, 50, dev, None)
     assert rc == 1 and b"idx_stride" in lib.saf3r_last_error()
@@ -113,19 +113,26 @@ def test_invalid_arguments_fail_before_launch(pkg):
     rc = lib.saf3r_block_select(ctypes.c_void_p(16), ctypes.c_void_p(16), 1, 4, 2, 2, 33, 0, ctypes.c_void_p(16), None)
     assert rc == 2  # k beyond the supported range
     rc = lib.saf3r_pack_qkv(None, None, None, 64, 64, 0, 10, 1, 1, None, None, None, None, 1e-5, 0, None, None,
-                            None, 0, None, None, None, None, None, None, None)
+                            None, 0, None, None, None, None, None, None, None, 1.0, None)
     assert rc == 1 and b"geometry" in lib.saf3r_last_error()
     flags = (ctypes.c_uint8 * 65)(*([0] * 64 + [1]))  # token order beyond head 63
     rc = lib.saf3r_pack_qkv(dev, dev, dev, 64, 64, 2, 100, 5, 65, None, None, None, None, 1e-5, 0, None, None,
-                            None, 0, dev, dev, dev, flags, None, None, None)
+                            None, 0, dev, dev, dev, flags, None, None, None, 1.0, None)
     assert rc == 2 and b"token order" in lib.saf3r_last_error()
     rc = lib.saf3r_pack_qkv(dev, dev, dev, 64, 64, 2, 100, 5, 65, None, None, None, None, 1e-5, 0, None, None,
-                            None, 0, dev, dev, dev, None, flags, dev, None)
+                            None, 0, dev, dev, dev, None, flags, dev, None, 1.0, None)
     assert rc == 2 and b"fp32 rows" in lib.saf3r_last_error()
     one = (ctypes.c_uint8 * 2)(0, 1)
     rc = lib.saf3r_pack_qkv(dev, dev, dev, 64, 64, 2, 100, 5, 2, None, None, None, None, 1e-5, 0, None, None,
-                            None, 0, dev, dev, dev, None, one, None, None)
+                            None, 0, dev, dev, dev, None, one, None, None, 1.0, None)
     assert rc == 1 and b"qk32" in lib.saf3r_last_error()
+    rc = lib.saf3r_pack_qkv(dev, dev, dev, 64, 64, 2, 100, 5, 65, None, None, None, None, 1e-5, 0, None, None,
+                            None, 0, dev, dev, dev, None, None, None, flags, 0.18, None)
+    assert rc == 2 and b"scaled Q" in lib.saf3r_last_error()
+    for bad_scale in (0.0, -1.0, float("inf")):
+        rc = lib.saf3r_pack_qkv(dev, dev, dev, 64, 64, 2, 100, 5, 2, None, None, None, None, 1e-5, 0, None, None,
+                                None, 0, dev, dev, dev, None, None, None, one, bad_scale, None)
+        assert rc == 1 and b"q_scale" in lib.saf3r_last_error()
     with pytest.raises(L.Saf3rError):
         L.check(1)
 

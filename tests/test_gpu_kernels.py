@@ -224,6 +224,77 @@ def test_sparse_attention_outrun_reference(ops, pkg, phase):
         _check_close(got[h], ref, f"outrun phase={phase} head {h} pattern {pat}")
 
 
+def _prescaled_run(ops, pkg, geom, q, k, v, patterns, flags, order=None, k_sel=2):
+    """Packs every head with the softmax scale folded into Q and runs the attention on it; returns the
+    output, the block lists, and the q the kernels consumed in unscaled units (fp32: packed / factor)."""
+    c = ops.prescale_factor()
+    H = len(patterns)
+    tord = ops.token_order_heads(patterns)
+    qp, kp, vp = ops.pack_heads(q.to(DEV), k.to(DEV), v.to(DEV), geom, token_order=tord, q_scaled=flags)
+    dyn = [h for h, p in enumerate(patterns) if p == ops.BLOCK_DYNAMIC]
+    sel = None
+    if dyn:
+        pq, pk = ops.block_pool(qp, kp, geom, dyn)
+        sel = ops.block_select(pq, pk, geom.frames, geom.blocks_per_frame, k_sel)
+    out = ops.sparse_attn_fwd(qp, kp, vp, geom, patterns, sel, token_order=tord, q_scaled=flags, order=order)
+    torch.cuda.synchronize()
+    # the packed Q of a flagged head is bf16(q * c) (one rounding of the fp32 product)
+    q_used = torch.stack([(q[h].float() * c).to(torch.bfloat16).float() / c if flags[h] else q[h].float()
+                          for h in range(H)])
+    return out, sel, dyn, q_used
+
+
+@pytest.mark.parametrize("F,T,ns", [(3, 155, 5), (4, 1374, 5), (2, 64, 0), (3, 65, 1)])
+def test_sparse_attention_prescaled_q(ops, pkg, F, T, ns):
+    """Heads packed with the softmax scale in Q walk without a running maximum (exp2 of the MFMA
+    result); every pattern and both layouts of DENSE heads match the oracle on the q they consumed,
+    next to unflagged heads in the same launch."""
+    geom = pkg.Geometry(F, T, ns)
+    patterns = [ops.DENSE, ops.FRAME_LOCAL, ops.ANCHOR_LOCAL, ops.BLOCK_DYNAMIC, ops.ANCHOR, ops.SKIP,
+                ops.DENSE, ops.FRAME_LOCAL]
+    flags = [True, True, True, True, True, True, False, False]
+    H = len(patterns)
+    q, k, v = _qkv(H, geom.tokens, seed=F * 19 + T, scale=1.5)
+    out, sel, dyn, q_used = _prescaled_run(ops, pkg, geom, q, k, v, patterns, flags)
+    og = OA.Geometry(F, T, ns)
+    got = out.float().cpu().reshape(geom.tokens, H, 64).permute(1, 0, 2)
+    for h, pat in enumerate(patterns):
+        ref = OA.sparse_attention_gathered(q_used[h], k[h].float(), v[h].float(), pat, og,
+                                           sel[dyn.index(h)].cpu() if h in dyn else None, dtype=torch.float64)
+        _check_close(got[h], ref, f"prescaled F{F} T{T} ns{ns} head {h} pattern {pat}")
+
+
+@pytest.mark.parametrize("phase", ["fixed", "paced"])
+def test_sparse_attention_prescaled_out_of_range(ops, pkg, phase):
+    """Prescaled heads whose scores leave the range of the walk without a running maximum: keys 69
+    and 173 log2 units above the rest (partial row sums beyond 2^64), and rows whose every score lies
+    more than 64 units below 0 (row sums below 2^-64). The main launch marks those items and the
+    launch after it walks them with the exact maximum; every row matches the oracle."""
+    geom = pkg.Geometry(3, 155, 5)
+    patterns = [ops.DENSE, ops.DENSE, ops.BLOCK_DYNAMIC, ops.FRAME_LOCAL, ops.ANCHOR_LOCAL, ops.DENSE]
+    H = len(patterns)
+    g = torch.Generator().manual_seed(6)
+    N = geom.tokens
+    q = (0.5 + 0.1 * torch.randn(H, N, 64, generator=g)).to(torch.bfloat16)
+    k = (0.3 * torch.randn(H, N, 64, generator=g)).to(torch.bfloat16)
+    v = torch.randn(H, N, 64, generator=g).to(torch.bfloat16)
+    last = (geom.frames - 1) * geom.tokens_per_frame
+    k[:5, last + 40] = 12.0   # heads 0-4: outliers in the last frame (overflow)
+    k[:5, last + 100] = 30.0
+    # head 5: q.k about -400, about -72 log2 units after the scale, for every pair (underflow)
+    q[5] = (2.5 + 0.05 * torch.randn(N, 64, generator=g)).to(torch.bfloat16)
+    k[5] = (-2.5 + 0.05 * torch.randn(N, 64, generator=g)).to(torch.bfloat16)
+    flags = [True] * H
+    out, sel, dyn, q_used = _prescaled_run(ops, pkg, geom, q, k, v, patterns, flags, order=phase)
+    og = OA.Geometry(3, 155, 5)
+    got = out.float().cpu().reshape(N, H, 64).permute(1, 0, 2)
+    assert torch.isfinite(got).all()
+    for h, pat in enumerate(patterns):
+        ref = OA.sparse_attention_gathered(q_used[h], k[h].float(), v[h].float(), pat, og,
+                                           sel[0].cpu() if h == 2 else None, dtype=torch.float64)
+        _check_close(got[h], ref, f"prescaled out of range phase={phase} head {h} pattern {pat}")
+
+
 def test_walk_order_paced_and_fixed(ops, pkg):
     """The paced walk order (the product default: walks start where the measured step time and the
     wall clock point) matches the oracle on every pattern over repeated calls, whose pace state

@@ -169,9 +169,10 @@ def test_wired_layer_128_frames_sampled_rows(mods, pkg):
         y = w(x, pos)
         qkv = om.qkv(x).reshape(N, 3 * dim).contiguous()
         tord = ops.token_order_heads(w.patterns)
+        qs = w.q_scaled_heads()  # Q as the wrapper packed it (softmax scale folded in)
         qp, kp, vp = ops.pack_qkv(qkv, qkv[:, dim:], qkv[:, 2 * dim:], 3 * dim, 64, geom, H,
                                   ln_q=(om.q_norm.weight, om.q_norm.bias), ln_k=(om.k_norm.weight, om.k_norm.bias),
-                                  pos=pos[0], rope_base=100.0)  # every head in the padded layout, for reading back
+                                  pos=pos[0], rope_base=100.0, q_scaled=qs)  # every head padded, for reading back
         torch.cuda.synchronize()
     print("128-frame wired layer ran", flush=True)
     # block lists: bit-exact against the oracle's selection from the same packed q/k
@@ -192,8 +193,9 @@ def test_wired_layer_128_frames_sampled_rows(mods, pkg):
     og = OA.Geometry(F_, T, 5)
     attn = torch.empty(len(rows), H, 64, dtype=torch.float64)
     vnat = qkv[:, 2 * dim:].reshape(N, H, 64)
+    c = ops.prescale_factor()
     for h, pat in enumerate(w.patterns):
-        qh = _rows_of(qp, geom, rows, h)
+        qh = _rows_of(qp, geom, rows, h) / (c if qs[h] else 1.0)
         kh = _rows_of(kp, geom, toks_all, h)
         vh = vnat[:, h].float().cpu()
         mask = OA.allowed_mask(pat, rows, og, sel_of.get(h))
