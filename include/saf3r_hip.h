@@ -256,8 +256,8 @@ int saf3r_keyset_gather(const void* k_packed, int frames, int tokens_per_frame, 
  *   q_scaled: host uint8 [num_heads] or NULL: heads h < 64 whose Q rows (and BROADCAST Q buffer)
  *        hold q * scale * log2(e) rounded once to bf16 (saf3r_pack_qkv's q_scaled with that
  *        q_scale). Their walks take exp2 of the score MFMA results directly, without a running
- *        maximum, while every partial row sum stays within [2^-64, 2^64]; a walk that leaves that
- *        range is walked again with the exact maximum. Same results within the bf16 tolerance.
+ *        maximum; an item whose row sums do not end within [2^-64, 2^64] is walked again with
+ *        the exact maximum. Same results within the bf16 tolerance.
  *   flags: 0 or SAF3R_ATTN_FIXED_ORDER. Without it, every key walk starts at the position the
  *        device's wall clock divided by the walk's step time points to, so that the work-groups
  *        resident at one moment read nearby key tiles (cache reuse); the summation order, and so the

@@ -365,15 +365,16 @@ __device__ __forceinline__ void half_block(const bf16x8 (&kf)[4], const bf16x8 (
 // a row with an unmasked key, whose m is still -inf, always does): values up to 2^64 keep every
 // bf16 P, fp32 sum and O finite, so no per-step maximum is needed. The exact path takes the row
 // maximum of s, rescales O (which then holds every step before h) and l, and recomputes P(h).
-// FAST walks (reference fixed at 0) only record that a step went past 2^64 (or was not finite):
-// the work-group then walks the item again without FAST.
+// The row sums a FAST walk (reference maximum fixed at 0) may end with: within [2^-64, 2^64] every
+// P of the row is at most 2^64 and the row's largest P at least 2^-64 / n (no NaN passes).
+__device__ __forceinline__ bool in_fast_range(float l) { return l >= 0x1p-64f && l <= 0x1p64f; }
+
+// FAST walks (reference fixed at 0) check nothing per step: every P is non-negative, so a row sum
+// that ends within [2^-64, 2^64] bounds every P of the row, and the end of the walk tests that.
 template <bool FAST>
-__device__ __forceinline__ void exact_fix(const f32x16 (&s)[2], bf16x8 (&pn)[2][2], float (&ts)[2], Acc& A, float c,
-                                          bool& unsafe) {
-  if constexpr (FAST) {
-    if (__ballot(!(ts[0] <= 0x1p64f) || !(ts[1] <= 0x1p64f)) != 0) unsafe = true;
-    return;
-  }
+__device__ __forceinline__ void exact_fix(const f32x16 (&s)[2], bf16x8 (&pn)[2][2], float (&ts)[2], Acc& A,
+                                          float c) {
+  if constexpr (FAST) return;
   if (__ballot(ts[0] > 0x1p64f || ts[1] > 0x1p64f) == 0) return;
 #pragma unroll
   for (int gq = 0; gq < 2; ++gq) {
@@ -680,9 +681,9 @@ __device__ __forceinline__ void attn_body(const AttnParams& p, const int item) {
   }
 
   // Heads whose Q rows carry the softmax scale (q * scale * log2 e, rounded once when packed) walk
-  // in those units (c = 1) and without a reference maximum (FAST: P = exp2(s)) as long as every
-  // partial row sum stays within [2^-64, 2^64] (scores within about 64 units of 0). A FAST item that
-  // leaves that range stores nothing but a marker, 0xFFFF (a NaN, which finite inputs never give) in
+  // in those units (c = 1) and without a reference maximum (FAST: P = exp2(s)) when every stored
+  // row's sum ends within [2^-64, 2^64] (scores within about 64 units of 0). A FAST item whose rows
+  // do not stores nothing but a marker, 0xFFFF (a NaN, which finite inputs never give) in
   // feature 0 of its first row, and the launch that follows (FIXUP) walks the marked items again
   // with the exact reference maximum.
   const bool qpre = h < 64 && ((p.q_pre >> h) & 1);
@@ -693,9 +694,13 @@ __device__ __forceinline__ void attn_body(const AttnParams& p, const int item) {
   // ---- Q fragments: lane holds features 32*half .. 32*half+31 of rows 32*gq + col ----
   bf16x8 qfrag[2][4];
   const __bf16* qrows = pat == SAF3R_BROADCAST ? p.bq + (int64_t)p.slot[h] * p.bcap * 64 : p.q + head_base * 64;
+  // the tile index through an empty asm: the row numbers computed here must not be kept for the
+  // output rows after the walk (a 64-bit value held through the key loops was spilled in them)
+  int qtq = qt;
+  asm volatile("" : "+s"(qtq));
 #pragma unroll
   for (int gq = 0; gq < 2; ++gq) {
-    const u32x4* qsrc = reinterpret_cast<const u32x4*>(qrows + ((int64_t)qt * 64 + 32 * gq + col) * 64 + 32 * half);
+    const u32x4* qsrc = reinterpret_cast<const u32x4*>(qrows + ((int64_t)qtq * 64 + 32 * gq + col) * 64 + 32 * half);
 #pragma unroll
     for (int s = 0; s < 4; ++s) qfrag[gq][s] = __builtin_bit_cast(bf16x8, qsrc[s]);
   }
@@ -710,14 +715,14 @@ __device__ __forceinline__ void attn_body(const AttnParams& p, const int item) {
     }
   };
   // FAST end of a walk: true (work-group uniform) when the item must be walked again exactly
-  auto walk_unsafe = [&](bool unsafe) -> bool {
+  auto walk_unsafe = [&]() -> bool {
     int64_t qtok[2];
     int frow[2];
     row_info(qtok, frow);
     bool low = false;
 #pragma unroll
-    for (int gq = 0; gq < 2; ++gq) low |= qtok[gq] >= 0 && !(partner_sum(A.l[gq]) >= 0x1p-64f);
-    const bool bad = unsafe || __ballot(low) != 0;
+    for (int gq = 0; gq < 2; ++gq) low |= qtok[gq] >= 0 && !in_fast_range(partner_sum(A.l[gq]));
+    const bool bad = __ballot(low) != 0;
     if (lane == 0) uflag[w] = bad ? 1 : 0;
     __syncthreads();
     return (uflag[0] | uflag[1] | uflag[2] | uflag[3]) != 0;
@@ -728,12 +733,11 @@ __device__ __forceinline__ void attn_body(const AttnParams& p, const int item) {
     // for every other pattern, so neither carries the other's state in registers.
     auto shared_walk = [&](auto ks_tag, auto fast_tag) {
     constexpr bool FAST = decltype(fast_tag)::value;
-    bool unsafe = false;
     init_acc(FAST);
-    // stores the rows, or (FAST, unsafe) marks the item for the exact walk
+    // stores the rows, or (FAST, out of range) marks the item for the exact walk
     auto finish = [&]() {
       if constexpr (FAST) {
-        if (walk_unsafe(unsafe)) {
+        if (walk_unsafe()) {
           if (tid == 0) *marker() = 0xFFFFu;
           return;
         }
@@ -925,7 +929,7 @@ __device__ __forceinline__ void attn_body(const AttnParams& p, const int item) {
           load_k(ring + v * 16384, 1, kf, half, col);
           half_block<FAST>(kf, vf, qfrag, s_cur, s_nxt, pc, pn, ts, A, c);
           if (kv_cur < 64) mask_valid(s_nxt, kv_cur, 32, half);
-          exact_fix<FAST>(s_cur, pn, ts, A, c, unsafe);
+          exact_fix<FAST>(s_cur, pn, ts, A, c);
           A.l[0] += ts[0];
           A.l[1] += ts[1];
           advance();
@@ -939,7 +943,7 @@ __device__ __forceinline__ void attn_body(const AttnParams& p, const int item) {
           load_k(ring + ((v + 1) & 3) * 16384, 0, kf, half, col);
           half_block<FAST>(kf, vf, qfrag, s_nxt, s_cur, pn, pc, ts, A, c);
           if (kv_nxt < 64) mask_valid(s_cur, kv_nxt, 0, half);
-          exact_fix<FAST>(s_nxt, pc, ts, A, c, unsafe);
+          exact_fix<FAST>(s_nxt, pc, ts, A, c);
           A.l[0] += ts[0];
           A.l[1] += ts[1];
           kv_cur = kv_nxt;
@@ -1109,7 +1113,6 @@ __device__ __forceinline__ void attn_body(const AttnParams& p, const int item) {
     // (each wave's partial result is merged with its own reference maximum below)
     auto split_walk = [&](auto fast_tag) -> bool {
     constexpr bool FAST = decltype(fast_tag)::value;
-    bool unsafe = false;
     init_acc(FAST);
     wait_vm<0>();
     if (nw > 0) {
@@ -1148,7 +1151,7 @@ __device__ __forceinline__ void attn_body(const AttnParams& p, const int item) {
         issue_v(e0, 1);
         const int kv0 = e0 & 127;
         if (kv0 < 64) mask_valid(s_nxt, kv0, 32, half);
-        exact_fix<FAST>(s_cur, pn, ts, A, c, unsafe);
+        exact_fix<FAST>(s_cur, pn, ts, A, c);
         A.l[0] += ts[0];
         A.l[1] += ts[1];
         // half step 2t+1: PV of block t half 0, scores of block t+1 half 0, softmax of block t half 1
@@ -1160,7 +1163,7 @@ __device__ __forceinline__ void attn_body(const AttnParams& p, const int item) {
         issue_v(e1, 0);
         const int kv1 = e1 & 127;
         if (kv1 < 32) mask_valid(s_cur, kv1, 0, half);
-        exact_fix<FAST>(s_nxt, pc, ts, A, c, unsafe);
+        exact_fix<FAST>(s_nxt, pc, ts, A, c);
         A.l[0] += ts[0];
         A.l[1] += ts[1];
         e0 = e1;
@@ -1181,8 +1184,8 @@ __device__ __forceinline__ void attn_body(const AttnParams& p, const int item) {
       if constexpr (FAST) {
         bool low = false;
 #pragma unroll
-        for (int gq = 0; gq < 2; ++gq) low |= !(partner_sum(A.l[gq]) >= 0x1p-64f);
-        return unsafe || __ballot(low) != 0;
+        for (int gq = 0; gq < 2; ++gq) low |= !in_fast_range(partner_sum(A.l[gq]));
+        return __ballot(low) != 0;
       }
     }
     return false;
