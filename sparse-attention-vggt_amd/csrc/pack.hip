@@ -55,6 +55,19 @@ __global__ __launch_bounds__(256) void pack_qkv_kernel(PackParams p) {
   const int64_t src = tok * p.tok_stride + (int64_t)h * p.head_stride + 16 * c;
   const int64_t dst = ((int64_t)h * g.L + slot) * 64 + 16 * c;
 
+  // every load of the row first (q, k, v: 32 bytes each), so that they are in flight together
+  // (the stores of q's result would otherwise keep the k and v loads behind them)
+  u32x4 raw[3][2];
+#pragma unroll
+  for (int m = 0; m < 3; ++m) {
+    raw[m][0] = raw[m][1] = u32x4{0, 0, 0, 0};
+    if (tok >= 0) {
+      const u32x4* s4 = reinterpret_cast<const u32x4*>((m == 0 ? p.q : m == 1 ? p.k : p.v) + src);
+      raw[m][0] = s4[0];
+      raw[m][1] = s4[1];
+    }
+  }
+
   float cs[16], sn[16];
   if (p.apply_rope && tok >= 0) {
     const int pv = min(max(p.pos[tok * 2 + (c >> 1)], 0), p.rpos - 1);
@@ -76,21 +89,16 @@ __global__ __launch_bounds__(256) void pack_qkv_kernel(PackParams p) {
 
 #pragma unroll
   for (int which = 0; which < 2; ++which) {
-    const __bf16* in = which == 0 ? p.q : p.k;
     __bf16* outp = which == 0 ? p.qp : p.kp;
     float x[16];
-    if (tok >= 0) {
-      const u32x4* s4 = reinterpret_cast<const u32x4*>(in + src);
-      u32x4 a = s4[0], b = s4[1];
+    {
+      const u32x4 a = raw[which][0], b = raw[which][1];
       uint32_t w[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         x[2 * j] = bf16_lo(w[j]);
         x[2 * j + 1] = bf16_hi(w[j]);
       }
-    } else {
-#pragma unroll
-      for (int j = 0; j < 16; ++j) x[j] = 0.f;
     }
     if (p.apply_ln) {
       float s = 0.f;
@@ -150,15 +158,9 @@ __global__ __launch_bounds__(256) void pack_qkv_kernel(PackParams p) {
 
   // V: stage the tile's 64 rows, then write the transposed, permuted tile.
   {
-    u32x4 a = {0, 0, 0, 0}, b = {0, 0, 0, 0};
-    if (tok >= 0) {
-      const u32x4* s4 = reinterpret_cast<const u32x4*>(p.v + src);
-      a = s4[0];
-      b = s4[1];
-    }
     u32x4* l4 = reinterpret_cast<u32x4*>(vs + row * 72 + 16 * c);
-    l4[0] = a;
-    l4[1] = b;
+    l4[0] = raw[2][0];
+    l4[1] = raw[2][1];
   }
   __syncthreads();
   {
