@@ -42,144 +42,127 @@ struct PackParams {
   float q_scale;
 };
 
-// One 256-thread workgroup per (64-slot tile, head). Four threads own one slot row, 16 features
-// each; LayerNorm reduces across the four, RoPE pairs feature d with d +- 16 (partner thread ^ 1).
-__global__ __launch_bounds__(256) void pack_qkv_kernel(PackParams p) {
+// One 512-thread workgroup per (64-slot tile, head). Eight threads own one slot row, 8 features
+// each (thread c8 of a row: features 8 c8 .. 8 c8 + 7); LayerNorm reduces across the eight, RoPE
+// pairs feature d with d +- 16 (partner thread c8 ^ 2). Every load of a row is issued before any
+// processing, so the q, k and v loads are in flight together.
+__global__ __launch_bounds__(512) void pack_qkv_kernel(PackParams p) {
   __shared__ __align__(16) __bf16 vs[64 * 72];  // V rows of the tile, 144-byte row pitch
   const Geom& g = p.g;
   const int tile = bid_x(), h = bid_y();
-  const int t = tid_x(), row = t >> 2, c = t & 3;
+  const int t = tid_x(), row = t >> 3, c8 = t & 7;
   const int64_t slot = (int64_t)tile * 64 + row;
   const int64_t ntok = (int64_t)g.F * g.T;
   const int64_t tok = (h < 64 && ((p.tok_order >> h) & 1)) ? (slot < ntok ? slot : -1) : slot_token(g, slot);
-  const int64_t src = tok * p.tok_stride + (int64_t)h * p.head_stride + 16 * c;
-  const int64_t dst = ((int64_t)h * g.L + slot) * 64 + 16 * c;
+  const int64_t src = tok * p.tok_stride + (int64_t)h * p.head_stride + 8 * c8;
+  const int64_t dst = ((int64_t)h * g.L + slot) * 64 + 8 * c8;
 
-  // every load of the row first (q, k, v: 32 bytes each), so that they are in flight together
-  // (the stores of q's result would otherwise keep the k and v loads behind them)
-  u32x4 raw[3][2];
+  u32x4 raw[3];
 #pragma unroll
   for (int m = 0; m < 3; ++m) {
-    raw[m][0] = raw[m][1] = u32x4{0, 0, 0, 0};
-    if (tok >= 0) {
-      const u32x4* s4 = reinterpret_cast<const u32x4*>((m == 0 ? p.q : m == 1 ? p.k : p.v) + src);
-      raw[m][0] = s4[0];
-      raw[m][1] = s4[1];
-    }
+    raw[m] = u32x4{0, 0, 0, 0};
+    if (tok >= 0) raw[m] = *reinterpret_cast<const u32x4*>((m == 0 ? p.q : m == 1 ? p.k : p.v) + src);
   }
 
-  float cs[16], sn[16];
+  // RoPE: features 0..31 turn with the y position, 32..63 with x; feature e of a 32-half takes
+  // angle index e % 16 and, for e < 16, -t[e + 16] (else +t[e - 16]) as its partner term
+  float cs[8], sn[8];
   if (p.apply_rope && tok >= 0) {
-    const int pv = min(max(p.pos[tok * 2 + (c >> 1)], 0), p.rpos - 1);
-    const f32x4* c4 = reinterpret_cast<const f32x4*>(p.rcos + pv * 16);
-    const f32x4* s4 = reinterpret_cast<const f32x4*>(p.rsin + pv * 16);
+    const int pv = min(max(p.pos[tok * 2 + (c8 >> 2)], 0), p.rpos - 1);
+    const f32x4* c4 = reinterpret_cast<const f32x4*>(p.rcos + pv * 16 + 8 * (c8 & 1));
+    const f32x4* s4 = reinterpret_cast<const f32x4*>(p.rsin + pv * 16 + 8 * (c8 & 1));
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < 2; ++j) {
       const f32x4 cv = c4[j], sv = s4[j];
-      cs[4 * j] = cv[0];
-      cs[4 * j + 1] = cv[1];
-      cs[4 * j + 2] = cv[2];
-      cs[4 * j + 3] = cv[3];
-      sn[4 * j] = sv[0];
-      sn[4 * j + 1] = sv[1];
-      sn[4 * j + 2] = sv[2];
-      sn[4 * j + 3] = sv[3];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        cs[4 * j + e] = cv[e];
+        sn[4 * j + e] = sv[e];
+      }
     }
   }
 
 #pragma unroll
   for (int which = 0; which < 2; ++which) {
     __bf16* outp = which == 0 ? p.qp : p.kp;
-    float x[16];
-    {
-      const u32x4 a = raw[which][0], b = raw[which][1];
-      uint32_t w[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+    float x[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        x[2 * j] = bf16_lo(w[j]);
-        x[2 * j + 1] = bf16_hi(w[j]);
-      }
+    for (int j = 0; j < 4; ++j) {
+      x[2 * j] = bf16_lo(raw[which][j]);
+      x[2 * j + 1] = bf16_hi(raw[which][j]);
     }
     if (p.apply_ln) {
       float s = 0.f;
 #pragma unroll
-      for (int j = 0; j < 16; ++j) s += x[j];
+      for (int j = 0; j < 8; ++j) s += x[j];
       s += __shfl_xor(s, 1);
       s += __shfl_xor(s, 2);
+      s += __shfl_xor(s, 4);
       const float mean = s * (1.0f / 64.0f);
       float v2 = 0.f;
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
+      for (int j = 0; j < 8; ++j) {
         float dlt = x[j] - mean;
         v2 += dlt * dlt;
       }
       v2 += __shfl_xor(v2, 1);
       v2 += __shfl_xor(v2, 2);
+      v2 += __shfl_xor(v2, 4);
       const float rstd = 1.0f / sqrtf(v2 * (1.0f / 64.0f) + p.eps);
       const float* w = which == 0 ? p.qw : p.kw;
       const float* b = which == 0 ? p.qb : p.kb;
 #pragma unroll
-      for (int j = 0; j < 16; ++j) x[j] = (x[j] - mean) * rstd * w[16 * c + j] + b[16 * c + j];
+      for (int j = 0; j < 8; ++j) x[j] = (x[j] - mean) * rstd * w[8 * c8 + j] + b[8 * c8 + j];
     }
     if (p.apply_rope) {
-      float y[16];
+      float y[8];
 #pragma unroll
-      for (int j = 0; j < 16; ++j) y[j] = __shfl_xor(x[j], 1);
-      // even thread holds t1 (features 0..15 of its half), odd thread holds t2 (16..31)
-      const float sg = (c & 1) ? 1.0f : -1.0f;
+      for (int j = 0; j < 8; ++j) y[j] = __shfl_xor(x[j], 2);
+      const float sg = (c8 & 2) ? 1.0f : -1.0f;
 #pragma unroll
-      for (int j = 0; j < 16; ++j) x[j] = x[j] * cs[j] + sg * y[j] * sn[j];
+      for (int j = 0; j < 8; ++j) x[j] = x[j] * cs[j] + sg * y[j] * sn[j];
     }
     if (tok < 0) {
 #pragma unroll
-      for (int j = 0; j < 16; ++j) x[j] = 0.f;
+      for (int j = 0; j < 8; ++j) x[j] = 0.f;
     } else if (h < 64 && ((p.f32_heads >> h) & 1)) {
       // the fp32 values before the bf16 rounding, in token order (the probe and gather inputs)
-      f32x4* d32 = reinterpret_cast<f32x4*>(p.qk32 + (((int64_t)p.f32slot[h] * 2 + which) * ntok + tok) * 64 + 16 * c);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) d32[j] = f32x4{x[4 * j], x[4 * j + 1], x[4 * j + 2], x[4 * j + 3]};
+      f32x4* d32 = reinterpret_cast<f32x4*>(p.qk32 + (((int64_t)p.f32slot[h] * 2 + which) * ntok + tok) * 64 + 8 * c8);
+      d32[0] = f32x4{x[0], x[1], x[2], x[3]};
+      d32[1] = f32x4{x[4], x[5], x[6], x[7]};
     }
     if (which == 0 && h < 64 && ((p.q_scaled >> h) & 1)) {
 #pragma unroll
-      for (int j = 0; j < 16; ++j) x[j] *= p.q_scale;
+      for (int j = 0; j < 8; ++j) x[j] *= p.q_scale;
     }
-    u32x4 o0, o1;
+    u32x4 o;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      bf16x2 a = {(__bf16)x[2 * j], (__bf16)x[2 * j + 1]};
-      bf16x2 b = {(__bf16)x[8 + 2 * j], (__bf16)x[8 + 2 * j + 1]};
-      o0[j] = __builtin_bit_cast(uint32_t, a);
-      o1[j] = __builtin_bit_cast(uint32_t, b);
+      const bf16x2 a = {(__bf16)x[2 * j], (__bf16)x[2 * j + 1]};
+      o[j] = __builtin_bit_cast(uint32_t, a);
     }
-    u32x4* d4 = reinterpret_cast<u32x4*>(outp + dst);
-    d4[0] = o0;
-    d4[1] = o1;
+    *reinterpret_cast<u32x4*>(outp + dst) = o;
   }
 
   // V: stage the tile's 64 rows, then write the transposed, permuted tile.
-  {
-    u32x4* l4 = reinterpret_cast<u32x4*>(vs + row * 72 + 16 * c);
-    l4[0] = raw[2][0];
-    l4[1] = raw[2][1];
-  }
+  *reinterpret_cast<u32x4*>(vs + row * 72 + 8 * c8) = raw[2];
   __syncthreads();
   {
-    const int i = t >> 2;                               // tile row (d after permutation)
+    const int i = t >> 3;                               // tile row (d after permutation)
     const int ii = i & 31;
     const int d = 32 * (i >> 5) + 16 * ((ii >> 2) & 1) + 4 * (ii >> 3) + (ii & 3);  // phi
-    uint32_t w[8];
+    uint32_t w[4];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      int c0 = 16 * c + 2 * j, c1 = c0 + 1;
+    for (int j = 0; j < 4; ++j) {
+      int c0 = 8 * c8 + 2 * j, c1 = c0 + 1;
       int k0 = (c0 & ~12) | ((c0 & 4) << 1) | ((c0 & 8) >> 1);  // kappa
       int k1 = (c1 & ~12) | ((c1 & 4) << 1) | ((c1 & 8) >> 1);
       uint16_t lo = __builtin_bit_cast(uint16_t, vs[k0 * 72 + d]);
       uint16_t hi = __builtin_bit_cast(uint16_t, vs[k1 * 72 + d]);
       w[j] = (uint32_t)lo | ((uint32_t)hi << 16);
     }
-    u32x4* d4 = reinterpret_cast<u32x4*>(p.vp + ((int64_t)h * g.L + (int64_t)tile * 64) * 64 + i * 64 + 16 * c);
-    d4[0] = u32x4{w[0], w[1], w[2], w[3]};
-    d4[1] = u32x4{w[4], w[5], w[6], w[7]};
+    *reinterpret_cast<u32x4*>(p.vp + ((int64_t)h * g.L + (int64_t)tile * 64) * 64 + i * 64 + 8 * c8) =
+        u32x4{w[0], w[1], w[2], w[3]};
   }
 }
 
@@ -262,6 +245,6 @@ extern "C" int saf3r_pack_qkv(const void* q, const void* k, const void* v, int64
       return fail(SAF3R_ERR_INVALID, "saf3r_pack_qkv: q_scale must be positive and finite");
   }
   dim3 grid(p.g.NT, num_heads);
-  hipLaunchKernelGGL(pack_qkv_kernel, grid, dim3(256), 0, (hipStream_t)stream, p);
+  hipLaunchKernelGGL(pack_qkv_kernel, grid, dim3(512), 0, (hipStream_t)stream, p);
   return check_launch("saf3r_pack_qkv");
 }
