@@ -171,18 +171,17 @@ __global__ __launch_bounds__(256, K <= 8 ? 3 : 2) void token_topk_kernel(TopkPar
   for (int t = 0; t < K; ++t) a[t] = 0;
   float gmax[G];
   float tau = -__builtin_inff();
-  int cnt = 0;  // candidates of this lane in the frame so far (entries held: min(cnt, kCand))
-  // LDS byte address of this lane's next entry: row min(cnt, kCand) (row kCand is the spare row
-  // that absorbs writes past the buffer's end)
+  // LDS byte address of this lane's next entry, row n for n candidates so far in the frame (rows
+  // from kCand on are written to row kCand, the spare row that absorbs writes past the buffer)
   const uint32_t wa0 = lds_addr(cbuf) + 8 * tid, wspare = wa0 + 2048 * kCand;
   uint32_t wa = wa0;
+  auto count = [&]() { return (int)((wa - wa0) >> 11); };
   auto flush = [&]() __attribute__((always_inline)) {
-    const int n = min(cnt, kCand);
+    const int n = min(count(), kCand);
     for (int i = 0; i < n; ++i) {
       const uint64_t ent = cbuf[i * 256 + tid];
       topk_insert<K>(a, ckey(__builtin_bit_cast(float, (uint32_t)(ent >> 32)), (uint32_t)ent));
     }
-    cnt = 0;
     wa = wa0;
   };
   // candidate e of this lane: key 32*(e>>4) + 8*((e&15)>>2) + 4*half + (e&3) of the tile
@@ -276,18 +275,17 @@ __global__ __launch_bounds__(256, K <= 8 ? 3 : 2) void token_topk_kernel(TopkPar
             const int e = e0 + i;
             const bool keep = !(sc(e) < tau) && (!PADDED || kpos(e) < lim);
             const uint64_t ent = ((uint64_t)__builtin_bit_cast(uint32_t, sc(e)) << 32) | (uint32_t)(pbase + kpos(e));
-            *reinterpret_cast<__attribute__((address_space(3))) uint64_t*>(wa) = ent;
-            wa = min(wa + (keep ? 2048u : 0u), wspare);
-            cnt += keep;
+            *reinterpret_cast<__attribute__((address_space(3))) uint64_t*>(min(wa, wspare)) = ent;
+            wa += keep ? 2048u : 0u;
           }
         }
       }
       if (u == tiles_pf - 1) {
         // empty the buffer (or recompute an overflowed lane), merge the partner half's list, then
         // write this frame's indices
-        const bool over = cnt > kCand;
+        const bool over = count() > kCand;
         if (__builtin_amdgcn_ballot_w64(over)) direct(over);
-        if (over) cnt = 0;
+        if (over) wa = wa0;
         flush();
         uint64_t b[K];
 #pragma unroll
