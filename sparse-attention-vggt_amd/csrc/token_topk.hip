@@ -143,10 +143,14 @@ __global__ __launch_bounds__(256, K <= 8 ? 3 : 2) void token_topk_kernel(TopkPar
   // the tile of sequence step `step` (the next one) into its stage; past the last step the last
   // frame's last tile is loaded again into a stage nobody reads, so every step waits on the same
   // count of loads
+  // tile address of the next step to issue (FLAT), advanced by additions; stage of that step
+  const char* itb = kb0 + f_lo * fbytes;
+  int ist = 0;
   auto issue = [&](int step) __attribute__((always_inline)) {
-    char* st = ring[step % kStages];
+    char* st = ring[ist];
+    ist = ist == kStages - 1 ? 0 : ist + 1;
     if constexpr (FLAT) {
-      const char* tb = kb0 + ifr * fbytes + iu * tbytes;
+      const char* tb = itb;
       const bool last = iu == tiles_pf - 1;
 #pragma unroll
       for (int j = 0; j < 2; ++j)
@@ -159,10 +163,16 @@ __global__ __launch_bounds__(256, K <= 8 ? 3 : 2) void token_topk_kernel(TopkPar
         dma16(row + 8 * chj[j], __builtin_amdgcn_readfirstlane(lds_addr(st + 4096 * j + 1024 * w)));
       }
     }
-    if (step + 1 < total && ++iu == tiles_pf) {
-      iu = 0;
-      ifr += DUMP ? 1 : ips;
-      ips ^= 1;
+    if (step + 1 < total) {
+      itb += tbytes;
+      if (++iu == tiles_pf) {
+        iu = 0;
+        const int adv = DUMP ? 1 : ips;
+        ifr += adv;
+        itb -= tiles_pf * tbytes;
+        if (adv) itb += fbytes;
+        ips ^= 1;
+      }
     }
   };
 
@@ -314,13 +324,15 @@ __global__ __launch_bounds__(256, K <= 8 ? 3 : 2) void token_topk_kernel(TopkPar
   wait_vm<0>();  // q fragments landed; from here vmcnt counts ring loads only
   for (int s = 0; s < kStages - 1; ++s) issue(s);
   f32x16 s0 = {}, s1 = {};  // scores of the previous step
+  int rst = 0;  // stage of step t
   for (int t = 0; t <= total; ++t) {
     bf16x8 ka[4], kbf[4];
     if (t < total) {
       wait_vm<2 * (kStages - 2)>();  // tile t landed: only the loads of step t + 1 are pending
       barrier_only();                // every wave's share of tile t is in LDS; every wave is done with tile t-1
       issue(t + kStages - 1);
-      const char* kb = ring[t % kStages];
+      const char* kb = ring[rst];
+      rst = rst == kStages - 1 ? 0 : rst + 1;
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
         const int chn = 4 * half + s;
