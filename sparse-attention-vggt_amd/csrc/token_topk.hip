@@ -179,7 +179,9 @@ __global__ __launch_bounds__(256, K <= 8 ? 3 : 2) void token_topk_kernel(TopkPar
   uint64_t a[K];  // the lane's running top-K of its half of the frame (composite keys, 0 = empty)
 #pragma unroll
   for (int t = 0; t < K; ++t) a[t] = 0;
-  float gmax[G];
+  float gmax[G];  // this lane's group maxima over the tiles of pass 1 so far
+#pragma unroll
+  for (int g = 0; g < G; ++g) gmax[g] = -__builtin_inff();
   float tau = -__builtin_inff();
   // LDS byte address of this lane's next entry, row n for n candidates so far in the frame (rows
   // from kCand on are written to row kCand, the spare row that absorbs writes past the buffer)
@@ -246,10 +248,6 @@ __global__ __launch_bounds__(256, K <= 8 ? 3 : 2) void token_topk_kernel(TopkPar
       }
       return;
     } else if (ps == 0) {
-      if (u == 0) {
-#pragma unroll
-        for (int g = 0; g < G; ++g) gmax[g] = -__builtin_inff();
-      }
 #pragma unroll
       for (int e = 0; e < 32; ++e)
         gmax[e % G] = fmaxf(gmax[e % G], (!PADDED || kpos(e) < lim) ? sc(e) : -__builtin_inff());
@@ -265,6 +263,7 @@ __global__ __launch_bounds__(256, K <= 8 ? 3 : 2) void token_topk_kernel(TopkPar
           const float other = __builtin_bit_cast(float, (uint32_t)(half ? r[0] : r[1]));
           fmax_insert<K>(top, gmax[g]);
           fmax_insert<K>(top, other);
+          gmax[g] = -__builtin_inff();
         }
         tau = top[K - 1];
       }
@@ -284,9 +283,11 @@ __global__ __launch_bounds__(256, K <= 8 ? 3 : 2) void token_topk_kernel(TopkPar
             // full buffer stays on the spare row)
             const int e = e0 + i;
             const bool keep = !(sc(e) < tau) && (!PADDED || kpos(e) < lim);
-            const uint64_t ent = ((uint64_t)__builtin_bit_cast(uint32_t, sc(e)) << 32) | (uint32_t)(pbase + kpos(e));
-            *reinterpret_cast<__attribute__((address_space(3))) uint64_t*>(min(wa, wspare)) = ent;
+            const uint32_t at = min(wa, wspare);
             wa += keep ? 2048u : 0u;
+            auto* ew = reinterpret_cast<__attribute__((address_space(3))) uint32_t*>(at);
+            ew[0] = (uint32_t)(pbase + kpos(e));
+            ew[1] = __builtin_bit_cast(uint32_t, sc(e));
           }
         }
       }
