@@ -28,6 +28,15 @@
  *         kappa(c) swaps bits 2 and 3 of c, and phi(i) = 16*((i>>2)&1) + 4*(i>>3) + (i&3).
  *         (These permutations match the register layout of the MFMA 32x32x16 bf16 operands so
  *         that every LDS read in the attention kernel is a 16-byte vector.)
+ *
+ * Per-head layout variants (saf3r_layout, chosen per head by the token_order flags of saf3r_pack_qkv and
+ * saf3r_sparse_attn_fwd; the same Q, K, V buffers and tile formats):
+ *   SAF3R_LAYOUT_TOKEN  (DENSE heads): slot t holds token t (t < F*T), no special or per-frame padding.
+ *   SAF3R_LAYOUT_FRAMED (FRAME_LOCAL, ANCHOR_LOCAL, ANCHOR heads): with NBT = ceil(T/64), frame f's T
+ *         tokens, special ones included, in token order at slots f*NBT*64 .. f*NBT*64 + T - 1, zeros in
+ *         the rest of its NBT tiles. Needs F*NBT*64 <= L, true when the special tokens fit the padding
+ *         of the frame's last patch tile (NBT == NBf) or num_special == 0; every key set of these
+ *         patterns is then whole frames, walked with prefix masks only.
  */
 #ifndef SAF3R_HIP_H
 #define SAF3R_HIP_H
@@ -38,7 +47,7 @@
 extern "C" {
 #endif
 
-#define SAF3R_ABI_VERSION 8
+#define SAF3R_ABI_VERSION 9
 
 enum saf3r_status {
   SAF3R_OK = 0,
@@ -68,6 +77,13 @@ enum saf3r_pattern {
                               head's key set (keys 0, s, 2s, ...: a SAF3R_KEYSET_STRIDE set with start 0
                               and no include), served from the key-set buffers like a KEYSET head;
                               patch rows go through saf3r_gather_attn_fwd. ref: sparse_attention.py:197-208 */
+};
+
+/* Per-head layouts of the token_order arrays (see "Per-head layout variants" above). */
+enum saf3r_layout {
+  SAF3R_LAYOUT_PACKED = 0, /* the packed layout */
+  SAF3R_LAYOUT_TOKEN = 1,  /* token order, DENSE heads */
+  SAF3R_LAYOUT_FRAMED = 2  /* frame-padded token order, FRAME_LOCAL / ANCHOR_LOCAL / ANCHOR heads */
 };
 
 /* Flags of saf3r_sparse_attn_fwd. */
@@ -109,9 +125,10 @@ int64_t saf3r_packed_slots(int frames, int tokens_per_frame, int num_special);
  *   rope_cos, rope_sin: device fp32 [rope_positions][16] tables, cos / sin of
  *            position * inv_freq[i] (inv_freq[i] = 1 / base^(2i/32)); NULL disables RoPE.
  *            Positions are clamped to [0, rope_positions - 1].
- *   token_order: host uint8 [num_heads] or NULL. A head h < 64 with token_order[h] != 0 is packed
- *            in token order instead: slot t holds token t (t < F*T), no special or per-frame
- *            padding (the layout saf3r_sparse_attn_fwd reads for a DENSE head flagged the same way).
+ *   token_order: host uint8 [num_heads] or NULL: saf3r_layout per head (heads h < 64 only; 0 =
+ *            packed). SAF3R_LAYOUT_TOKEN packs slot t = token t, SAF3R_LAYOUT_FRAMED frame f's tokens
+ *            at tile f*ceil(T/64) (SAF3R_ERR_UNSUPPORTED where it does not fit): the layouts
+ *            saf3r_sparse_attn_fwd reads for heads flagged the same way.
  *   fp32_heads: host uint8 [num_heads] or NULL. Heads h < 64 flagged here also get their fp32 q and k
  *            (after LayerNorm and RoPE, before the bf16 rounding) in qk32: the s-th flagged head (in
  *            increasing head order) at qk32[((s*2 + 0|1) * F*T + t) * 64 + d] for q|k of token t.
@@ -250,9 +267,10 @@ int saf3r_keyset_gather(const void* k_packed, int frames, int tokens_per_frame, 
  *          bcast_v: bf16 [n_broadcast][F][C/64] key-set V tiles (saf3r_keyset_gather layout) of
  *                   frame f's tokens f*T .. f*T+T-1.
  *        NULL when no head is BROADCAST.
- *   token_order: host uint8 [num_heads] or NULL: DENSE heads packed in token order by
- *        saf3r_pack_qkv (the flag is an error on any other pattern). Their key and query tiles
- *        then cover the F*T tokens without padding.
+ *   token_order: host uint8 [num_heads] or NULL: the saf3r_layout saf3r_pack_qkv packed each head
+ *        in. SAF3R_LAYOUT_TOKEN is for DENSE heads (key and query tiles then cover the F*T tokens
+ *        without padding), SAF3R_LAYOUT_FRAMED for FRAME_LOCAL / ANCHOR_LOCAL / ANCHOR heads (each
+ *        query tile then walks whole frames: its own, frame 0, or both); any other pairing is an error.
  *   q_scaled: host uint8 [num_heads] or NULL: heads h < 64 whose Q rows (and BROADCAST Q buffer)
  *        hold q * scale * log2(e) rounded once to bf16 (saf3r_pack_qkv's q_scaled with that
  *        q_scale). Their walks take exp2 of the score MFMA results directly, without a running

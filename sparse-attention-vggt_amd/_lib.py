@@ -19,7 +19,7 @@ EXPORTS = (
     "saf3r_token_topk", "saf3r_probe_scores", "saf3r_keyset_build", "saf3r_keyset_gather",
     "saf3r_frame_topk_scores", "saf3r_probe_scores_noalloc",
 )
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 _lib = None
 

@@ -94,7 +94,8 @@ def executed_tile_flops(patterns, geom: Geometry, sel: torch.Tensor | None = Non
     """FLOP of the 64 x 64 (query tile, key tile) pairs the attention kernel walks, 4 * d * 64 * 64 per
     pair, padding and masked positions included: set against the algorithmic FLOP it shows the padding
     and masking waste. Query tiles: the special region (ceil(F*ns/64) tiles) and NBf patch tiles per
-    frame, or ceil(F*T/64) token-order tiles for DENSE heads packed in token order. Key tiles per query
+    frame, or ceil(F*T/64) token-order tiles for DENSE heads packed in token order, or ceil(T/64) tiles
+    per frame for frame-relative heads in the framed layout (``token_order`` value 2). Key tiles per query
     tile follow each pattern's walk: the special tiles holding the needed frames' special tokens plus
     those frames' patch tiles for the frame-relative patterns, the listed blocks for block-dynamic
     patch rows, ceil(count/64) compact tiles for key sets, ceil(T/64) for broadcast_first."""
@@ -122,12 +123,18 @@ def executed_tile_flops(patterns, geom: Geometry, sel: torch.Tensor | None = Non
             total += NBf * keys
         return total
 
+    nbt = geom.frame_tiles
     tiles = 0
     j = jk = 0
     for h, p in enumerate(patterns):
-        tok = bool(token_order[h]) if token_order is not None else False
+        lay = int(token_order[h]) if token_order is not None else 0
         if p == DENSE:
-            tiles += ntt * ntt if tok else NT * NT
+            tiles += ntt * ntt if lay else NT * NT
+        elif lay == 2 and p in (FRAME_LOCAL, ANCHOR_LOCAL, ANCHOR):
+            # framed layout: NBT query tiles per frame, each walking one frame (two for the
+            # anchor+local rows of frames 1 .. F-1)
+            frames_walked = F + (F - 1) if p == ANCHOR_LOCAL else F
+            tiles += nbt * nbt * frames_walked
         elif p == FRAME_LOCAL:
             tiles += frame_rel(False, True)
         elif p == ANCHOR_LOCAL:

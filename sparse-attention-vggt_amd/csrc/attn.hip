@@ -74,6 +74,7 @@ struct AttnParams {
   const __bf16* bv;      // BROADCAST heads: V tiles [head][frame][bcap/64][64][64]
   int bcap;              // ceil(T/64)*64
   uint64_t tok_order;    // DENSE heads (bit h) packed in token order: tile t = tokens 64t .. 64t+63
+  uint64_t framed;       // frame-relative heads (bit h) in the framed layout: frame f = tiles f*NBT ..
   uint64_t q_pre;        // heads (bit h) whose Q rows hold q * scale * log2(e)
   int n_items;           // fixup launch: items in the segments, work-groups of the launch
   int fix_groups;
@@ -536,7 +537,7 @@ __device__ inline void pace_add(const AttnParams& p, int kind, uint64_t t0, int 
 // their own, walk kind, and (BROADCAST) the frame whose rows it writes.
 struct Item {
   int h, pat, it, qt0, nw, kind, bfr;
-  bool tokord;
+  bool tokord, framed;
 };
 
 __device__ inline Item decode_item(const AttnParams& p, int item) {
@@ -552,7 +553,14 @@ __device__ inline Item decode_item(const AttnParams& p, int item) {
   const int ns4 = (g.nst + 3) >> 2;
   const int groups_pf = (g.NBf + 3) >> 2;
   d.tokord = pat == SAF3R_DENSE && ((p.tok_order >> d.h) & 1);
-  if (pat == SAF3R_DENSE || pat == SAF3R_SKIP || pat == SAF3R_KEYSET) {
+  d.framed = d.h < 64 && ((p.framed >> d.h) & 1);
+  if (d.framed) {
+    // four consecutive query tiles of one frame (the frame's last item may hold fewer)
+    const int gpf = (g.NBT + 3) >> 2, f = it / gpf, gg = it - f * gpf;
+    d.qt0 = f * g.NBT + 4 * gg;
+    d.nw = min(4, g.NBT - 4 * gg);
+    d.kind = kShared;
+  } else if (pat == SAF3R_DENSE || pat == SAF3R_SKIP || pat == SAF3R_KEYSET) {
     d.qt0 = 4 * it;
     d.nw = min(4, (d.tokord ? p.ntt : g.NT) - d.qt0);
     d.kind = pat == SAF3R_SKIP ? kSkip : kShared;
@@ -590,6 +598,7 @@ __device__ inline uint16_t* item_marker(const AttnParams& p, const Item& d) {
   int64_t t0;
   if (d.pat == SAF3R_BROADCAST) t0 = (int64_t)d.bfr * g.T + d.qt0 * 64;
   else if (d.tokord) t0 = (int64_t)d.qt0 * 64;
+  else if (d.framed) t0 = (int64_t)(d.qt0 / g.NBT) * g.T + (d.qt0 % g.NBT) * 64;
   else if (d.qt0 < g.nst) t0 = (int64_t)(d.qt0 * 64 / g.ns) * g.T + (d.qt0 * 64) % g.ns;
   else t0 = (int64_t)((d.qt0 - g.nst) / g.NBf) * g.T + g.ns + ((d.qt0 - g.nst) % g.NBf) * 64;
   return reinterpret_cast<uint16_t*>(p.out + t0 * p.out_stride + (int64_t)d.h * 64);
@@ -621,12 +630,13 @@ __device__ __forceinline__ void attn_body(const AttnParams& p, const int item) {
   const Item d = decode_item(p, item);
   const int h = d.h, pat = d.pat, qt0 = d.qt0, nw = d.nw, kind = d.kind;
   const int bfr = d.bfr;  // BROADCAST: the frame whose rows the item writes
-  const bool tokord = d.tokord;
+  const bool tokord = d.tokord, framed = d.framed;
   const bool wactive = w < nw;
   const int qt = kind == kSplit ? qt0 : qt0 + (wactive ? w : 0);
-  const bool qspecial = pat != SAF3R_BROADCAST && !tokord && qt < g.nst;
-  const int qf = qspecial ? 0 : (qt - g.nst) / g.NBf;
-  const int qb = qspecial ? 0 : (qt - g.nst) % g.NBf;
+  const bool qspecial = pat != SAF3R_BROADCAST && !tokord && !framed && qt < g.nst;
+  // query frame and the tile's position within it (framed: every wave's tile is in qt0's frame)
+  const int qf = framed ? qt0 / g.NBT : qspecial ? 0 : (qt - g.nst) / g.NBf;
+  const int qb = framed ? qt - qf * g.NBT : qspecial ? 0 : (qt - g.nst) % g.NBf;
   const bool writer = kind == kSplit ? true : wactive;
 
   // output token (or -1) and frame of the lane's two query rows; evaluated where they are used
@@ -643,6 +653,10 @@ __device__ __forceinline__ void attn_body(const AttnParams& p, const int item) {
         const int i = qt * 64 + r;
         qtok[gq] = (writer && i < p.ntok) ? (int64_t)i : -1;
         frow[gq] = 0;
+      } else if (framed) {
+        const int i = qb * 64 + r;
+        qtok[gq] = (writer && i < g.T) ? (int64_t)qf * g.T + i : -1;
+        frow[gq] = qf;
       } else if (qspecial) {
         const int64_t sl = (int64_t)qt * 64 + r;
         qtok[gq] = (writer && sl < g.S) ? (sl / g.ns) * g.T + sl % g.ns : -1;
@@ -760,10 +774,15 @@ __device__ __forceinline__ void attn_body(const AttnParams& p, const int item) {
       ks_keys = __builtin_amdgcn_readfirstlane(pat == SAF3R_BROADCAST ? g.T
                                                : tokord               ? p.ntok
                                                                       : min(p.ks_count[p.slot[h]], (int)p.ks_cap));
+    // framed heads: frame 0's tiles (ANCHOR, and first for ANCHOR_LOCAL), then the query frame's
+    // (FRAME_LOCAL, and ANCHOR_LOCAL from frame 1 on), each frame NBT tiles with only its last partial
+    const bool two = framed && pat == SAF3R_ANCHOR_LOCAL && qf != 0;
     if constexpr (keyset) {
       wk.init(0, (ks_keys + 63) / 64, 0, 0, 0, 0, 0, 0);
     } else if (eff == SAF3R_DENSE) {
       wk.init(0, g.NT, 0, 0, 0, 0, 0, 0);
+    } else if (framed) {
+      wk.init(pat == SAF3R_FRAME_LOCAL ? qf * g.NBT : 0, g.NBT, two ? qf * g.NBT : 0, two ? g.NBT : 0, 0, 0, 0, 0);
     } else {
       frame_rel = true;
       int f0, f1;
@@ -850,7 +869,7 @@ __device__ __forceinline__ void attn_body(const AttnParams& p, const int item) {
       wi.next(g);
     };
 
-    if (keyset || eff == SAF3R_DENSE || rel_patch) {
+    if (keyset || eff == SAF3R_DENSE || rel_patch || framed) {
       // ---- single-range walk: tiles rot, rot + 1, ... (mod count), only partial tiles masked ----
       // (dense and key-set walks: tiles 0 .. count-1 entered at rot; patch-row items of
       // frame-relative heads: their own frame's patch tiles, then the frame-relative walk below)
@@ -858,19 +877,22 @@ __device__ __forceinline__ void attn_body(const AttnParams& p, const int item) {
       // that every stage offset is a constant, waves without a query tile of their own compute
       // on a duplicate (their rows are not stored), and the tile position and its valid-key
       // count advance without branches.
-      const int nst = g.nst, NBf = g.NBf;
-      const int lastv = g.P - 64 * (NBf - 1);  // valid keys in the last patch tile of a frame
-      const int sbeg = rel_patch ? seg_s : 0;
+      // (framed heads: no special tiles, NBT tiles per frame, T - 64 (NBT - 1) valid keys in the last)
+      const int nst = framed ? 0 : g.nst, NBf = framed ? g.NBT : g.NBf;
+      const int lastv = framed ? g.T - 64 * (NBf - 1) : g.P - 64 * (NBf - 1);  // valid keys, last tile of a frame
+      const int sbeg = rel_patch ? seg_s : framed ? wk.s0 : 0;
       const int cnt = rel_patch ? seg_l : count;
-      const int send = sbeg + cnt;
-      int kt = rel_patch ? sbeg : rot, bk = -1;  // consumed tile and its block within its frame
+      // the tile after which the walk continues at jto: the end of the range (wrapping to its start),
+      // or for a framed two-frame walk the end of frame 0 (continuing at the query frame)
+      const int jfrom = two ? g.NBT : sbeg + cnt, jto = two ? wk.s1 : sbeg;
+      int kt = (rel_patch || framed) ? sbeg : rot, bk = -1;  // consumed tile and its block within its frame
       if constexpr (!keyset) bk = kt >= nst ? (kt - nst) % NBf : -1;
       auto kvalid_of = [&]() -> int {
         if constexpr (keyset) return min(64, ks_keys - 64 * kt);
         else return kt < nst ? min(64, g.S - 64 * kt) : (bk == NBf - 1 ? lastv : 64);
       };
       auto advance = [&]() {
-        kt = kt + 1 == send ? sbeg : kt + 1;
+        kt = kt + 1 == jfrom ? jto : kt + 1;
         if constexpr (!keyset) bk = kt < nst ? -1 : (kt == nst || bk + 1 == NBf ? 0 : bk + 1);
       };
       int kti = kt;  // next tile to load
@@ -887,7 +909,7 @@ __device__ __forceinline__ void attn_body(const AttnParams& p, const int item) {
           __builtin_amdgcn_global_load_lds((const void*)(bk + o), (lds_void*)(st + 4096 * u), 16, 0, 0);
           __builtin_amdgcn_global_load_lds((const void*)(bv + o), (lds_void*)(st + 8192 + 4096 * u), 16, 0, 0);
         }
-        kti = kti + 1 == send ? sbeg : kti + 1;
+        kti = kti + 1 == jfrom ? jto : kti + 1;
       };
       if (cnt == 0) {
         store(A);
@@ -1311,13 +1333,17 @@ struct Seg {
   int64_t steps;
 };
 
-static int head_segments(int h, int pat, bool tokord, int ntt, const Geom& g, int sel_width, int64_t ks_cap,
-                         Seg* out) {
+static int head_segments(int h, int pat, bool tokord, bool framed, int ntt, const Geom& g, int sel_width,
+                         int64_t ks_cap, Seg* out) {
   const int ns4 = (g.nst + 3) / 4, groups_pf = (g.NBf + 3) / 4;
   int n = 0;
   auto add = [&](int base, int items, int64_t steps) {
     if (items > 0) out[n++] = Seg{h, base, items, steps};
   };
+  if (framed) {  // four query tiles of one frame per item; one or two frames of key tiles
+    add(0, g.F * ((g.NBT + 3) / 4), (int64_t)g.NBT * (pat == SAF3R_ANCHOR_LOCAL ? 2 : 1));
+    return n;
+  }
   switch (pat) {
     case SAF3R_DENSE:
       if (tokord) add(0, (ntt + 3) / 4, ntt);
@@ -1425,17 +1451,29 @@ extern "C" int saf3r_sparse_attn_fwd(const void* q_packed, const void* k_packed,
       return fail(SAF3R_ERR_UNSUPPORTED, "saf3r_sparse_attn_fwd: sel_width must be in [1, %d] (got %d)", kMaxList,
                   sel_width);
   }
-  p.tok_order = 0;
+  p.tok_order = p.framed = 0;
   if ((int64_t)frames * tokens_per_frame > 0x7fffffc0ll)
     return fail(SAF3R_ERR_UNSUPPORTED, "saf3r_sparse_attn_fwd: too many tokens");
   p.ntok = frames * tokens_per_frame;
   p.ntt = (p.ntok + 63) / 64;
   if (token_order) {
     for (int h = 0; h < num_heads; ++h) {
-      if (!token_order[h]) continue;
-      if (p.pattern[h] != SAF3R_DENSE)
-        return fail(SAF3R_ERR_INVALID, "saf3r_sparse_attn_fwd: head %d: only DENSE heads take the token-order layout", h);
-      p.tok_order |= 1ull << h;
+      const int lay = token_order[h], pt = p.pattern[h];
+      if (!lay) continue;
+      if (lay == SAF3R_LAYOUT_TOKEN) {
+        if (pt != SAF3R_DENSE)
+          return fail(SAF3R_ERR_INVALID, "saf3r_sparse_attn_fwd: head %d: only DENSE heads take the token-order layout", h);
+        p.tok_order |= 1ull << h;
+      } else if (lay == SAF3R_LAYOUT_FRAMED) {
+        if (pt != SAF3R_FRAME_LOCAL && pt != SAF3R_ANCHOR_LOCAL && pt != SAF3R_ANCHOR)
+          return fail(SAF3R_ERR_INVALID,
+                      "saf3r_sparse_attn_fwd: head %d: only FRAME_LOCAL / ANCHOR_LOCAL / ANCHOR heads take the framed layout", h);
+        if (!framed_fits(p.g))
+          return fail(SAF3R_ERR_UNSUPPORTED, "saf3r_sparse_attn_fwd: the framed layout does not fit this geometry");
+        p.framed |= 1ull << h;
+      } else {
+        return fail(SAF3R_ERR_INVALID, "saf3r_sparse_attn_fwd: head %d: unknown layout %d", h, lay);
+      }
     }
   }
   p.q_pre = 0;
@@ -1465,8 +1503,8 @@ extern "C" int saf3r_sparse_attn_fwd(const void* q_packed, const void* k_packed,
   Seg segs[kMaxSegs];
   int nseg = 0;
   for (int h = 0; h < num_heads; ++h)
-    nseg += head_segments(h, p.pattern[h], (p.tok_order >> h) & 1, p.ntt, p.g, sel_width, keyset_capacity,
-                          segs + nseg);
+    nseg += head_segments(h, p.pattern[h], (p.tok_order >> h) & 1, (p.framed >> h) & 1, p.ntt, p.g, sel_width,
+                          keyset_capacity, segs + nseg);
   for (int i = 1; i < nseg; ++i) {  // stable: longest item first
     const Seg x = segs[i];
     int j = i;

@@ -105,6 +105,7 @@ struct Geom {
   int nst;    // special tiles (Sp / 64)
   int NT;     // tiles per head (L / 64)
   int64_t L;  // slots per head
+  int NBT;    // framed layout: tiles per frame (ceil(T / 64)), frame f at tiles f*NBT .. f*NBT + NBT - 1
 };
 
 inline bool make_geom(int F, int T, int ns, Geom* g) {
@@ -121,7 +122,17 @@ inline bool make_geom(int F, int T, int ns, Geom* g) {
   g->L = (int64_t)g->Sp + (int64_t)F * g->Pp;
   if (g->L / kBlock > (int64_t)0x7fffffff) return false;
   g->NT = (int)(g->L / kBlock);
+  g->NBT = (T + kBlock - 1) / kBlock;
   return true;
+}
+
+// Framed layout (heads of the frame-relative patterns): frame f's T tokens in token order at slots
+// f*NBT*64 .. f*NBT*64 + T - 1, the rest of its NBT tiles zero. It fits the L slots of a head when the
+// special tokens fit the padding of the last patch tile (NBT == NBf) or there are no special tokens.
+inline bool framed_fits(const Geom& g) { return (int64_t)g.F * g.NBT * kBlock <= g.L; }
+__host__ __device__ inline int64_t framed_token(const Geom& g, int64_t slot) {
+  const int64_t tp = (int64_t)g.NBT * kBlock, f = slot / tp, t = slot - f * tp;
+  return (f < g.F && t < g.T) ? f * g.T + t : -1;
 }
 
 // Token index of a packed slot, or -1 for padding.

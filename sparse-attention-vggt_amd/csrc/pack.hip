@@ -35,6 +35,7 @@ struct PackParams {
   __bf16* vp;
   Geom g;
   uint64_t tok_order;  // heads (bit h) packed in token order: slot = token, no special/frame padding
+  uint64_t framed;     // heads (bit h) packed in the framed layout: frame f's tokens in order at tile f*NBT
   float* qk32;         // fp32 q and k rows of the flagged heads: [slot][q, k][F*T tokens][64]
   uint64_t f32_heads;  // heads (bit h) whose fp32 q / k rows are also written
   int8_t f32slot[64];  // slot of a flagged head in qk32
@@ -53,7 +54,9 @@ __global__ __launch_bounds__(512) void pack_qkv_kernel(PackParams p) {
   const int t = tid_x(), row = t >> 3, c8 = t & 7;
   const int64_t slot = (int64_t)tile * 64 + row;
   const int64_t ntok = (int64_t)g.F * g.T;
-  const int64_t tok = (h < 64 && ((p.tok_order >> h) & 1)) ? (slot < ntok ? slot : -1) : slot_token(g, slot);
+  const int64_t tok = (h < 64 && ((p.tok_order >> h) & 1)) ? (slot < ntok ? slot : -1)
+                      : (h < 64 && ((p.framed >> h) & 1)) ? framed_token(g, slot)
+                                                           : slot_token(g, slot);
   const int64_t src = tok * p.tok_stride + (int64_t)h * p.head_stride + 8 * c8;
   const int64_t dst = ((int64_t)h * g.L + slot) * 64 + 8 * c8;
 
@@ -212,12 +215,21 @@ extern "C" int saf3r_pack_qkv(const void* q, const void* k, const void* v, int64
   p.qp = (__bf16*)q_packed;
   p.kp = (__bf16*)k_packed;
   p.vp = (__bf16*)v_packed;
-  p.tok_order = 0;
+  p.tok_order = p.framed = 0;
   if (token_order) {
     for (int h = 0; h < num_heads; ++h) {
-      if (!token_order[h]) continue;
+      const int lay = token_order[h];
+      if (!lay) continue;
       if (h >= 64) return fail(SAF3R_ERR_UNSUPPORTED, "saf3r_pack_qkv: token order is supported for heads 0..63");
-      p.tok_order |= 1ull << h;
+      if (lay == SAF3R_LAYOUT_TOKEN) {
+        p.tok_order |= 1ull << h;
+      } else if (lay == SAF3R_LAYOUT_FRAMED) {
+        if (!framed_fits(p.g))
+          return fail(SAF3R_ERR_UNSUPPORTED, "saf3r_pack_qkv: the framed layout needs ceil(T/64) = ceil(P/64) here");
+        p.framed |= 1ull << h;
+      } else {
+        return fail(SAF3R_ERR_INVALID, "saf3r_pack_qkv: head %d: unknown layout %d", h, lay);
+      }
     }
   }
   p.qk32 = qk32;

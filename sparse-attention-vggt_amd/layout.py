@@ -4,7 +4,9 @@ Frame f holds tokens [f*T, (f+1)*T); the first ``num_special`` are special (came
 ``saf3r/patch/sparse_attention.py:93-107``), the other P = T - num_special are patch tokens, cut
 into NBf = ceil(P/64) blocks per frame. The packed layout puts all special tokens first
 (padded to a multiple of 64 slots) and then every frame's patch tokens padded to NBf*64 slots,
-so every 64-slot tile belongs to one frame (or to the special region).
+so every 64-slot tile belongs to one frame (or to the special region). Two per-head variants
+use the same buffers: token order (DENSE heads, slot t = token t) and the framed layout
+(frame-relative heads, frame f's T tokens in token order at tile f*ceil(T/64)).
 """
 from __future__ import annotations
 
@@ -62,3 +64,14 @@ class Geometry:
     @property
     def tiles(self) -> int:
         return self.slots // BLOCK
+
+    @property
+    def frame_tiles(self) -> int:
+        """Tiles per frame in the framed layout (NBT = ceil(T/64))."""
+        return -(-self.tokens_per_frame // BLOCK)
+
+    @property
+    def framed_fits(self) -> bool:
+        """The framed layout (frame f's T tokens in token order at tile f*NBT) fits the L slots of a
+        head: the special tokens fit the padding of a frame's last patch tile, or there are none."""
+        return self.frames * self.frame_tiles * BLOCK <= self.slots

@@ -24,6 +24,7 @@ PATTERN_NAMES = {
     KEYSET: "keyset", BROADCAST: "broadcast_first", TOKEN_DYNAMIC_KEYSET: "dino_topk_strided",
 }
 FIXED_ORDER = 1  # saf3r_attn_flags
+LAYOUT_PACKED, LAYOUT_TOKEN, LAYOUT_FRAMED = 0, 1, 2  # saf3r_layout: per-head layouts (token_order arrays)
 LOG2E = 1.4426950408889634
 KEYSET_PATTERNS = (KEYSET, TOKEN_DYNAMIC_KEYSET)  # heads served from the key-set buffers
 TOKEN_PATTERNS = (TOKEN_DYNAMIC, TOKEN_DYNAMIC_KEYSET)  # heads whose patch rows gather-attend est_topk_idx
@@ -100,10 +101,30 @@ def _u8_flags(flags: Sequence[bool] | None, n: int):
     return (ctypes.c_uint8 * n)(*[1 if f else 0 for f in flags])
 
 
-def token_order_heads(patterns: Sequence[int]) -> list[bool]:
-    """Heads that take the token-order packed layout: the DENSE ones (no special or per-frame
-    padding, so none of their query or key tiles is partly empty)."""
-    return [int(p) == DENSE for p in patterns]
+def _u8_layouts(layouts: Sequence[int] | None, n: int):
+    """Host uint8 [n] array of per-head layouts (``LAYOUT_*``; True counts as ``LAYOUT_TOKEN``)."""
+    if layouts is None:
+        return None
+    layouts = [int(x) for x in layouts]
+    if len(layouts) != n:
+        raise ValueError(f"one layout per head: got {len(layouts)} for {n} heads")
+    if any(x not in (LAYOUT_PACKED, LAYOUT_TOKEN, LAYOUT_FRAMED) for x in layouts):
+        raise ValueError(f"unknown layout in {layouts}")
+    return (ctypes.c_uint8 * n)(*layouts)
+
+
+FRAMED_PATTERNS = (FRAME_LOCAL, ANCHOR_LOCAL, ANCHOR)  # heads that can take the framed layout
+
+
+def token_order_heads(patterns: Sequence[int], geom: Geometry | None = None) -> list[int]:
+    """Per-head layout for ``pack_qkv`` / ``sparse_attn_fwd`` (``token_order``): DENSE heads take token
+    order (no special or per-frame padding, so none of their query or key tiles is partly empty);
+    with ``geom`` given and ``geom.framed_fits``, the frame-relative heads take the framed layout
+    (each frame's tokens, special ones included, in whole tiles of their own, so every query tile
+    walks whole frames with prefix masks only); every other head the packed layout."""
+    framed = geom is not None and geom.framed_fits
+    return [LAYOUT_TOKEN if int(p) == DENSE else LAYOUT_FRAMED if (framed and int(p) in FRAMED_PATTERNS)
+            else LAYOUT_PACKED for p in patterns]
 
 
 def rope_inv_freq(base: float = 100.0, feature_dim: int = 32) -> torch.Tensor:
@@ -142,13 +163,13 @@ def prescale_factor(scale: float | None = None) -> float:
 
 def pack_qkv(q, k, v, tok_stride: int, head_stride: int, geom: Geometry, num_heads: int,
              ln_q=None, ln_k=None, ln_eps: float = 1e-5, pos=None, rope_base=None, rope_positions=None, out=None,
-             token_order: Sequence[bool] | None = None, fp32_heads: Sequence[bool] | None = None,
+             token_order: Sequence[int] | None = None, fp32_heads: Sequence[bool] | None = None,
              q_scaled: Sequence[bool] | None = None, q_scale: float | None = None):
     """QK-LayerNorm + RoPE-2D + packing (``saf3r_pack_qkv``). ``q``/``k``/``v`` are tensors (or
     views) whose element (t, h, d) is at ``data_ptr + t*tok_stride + h*head_stride + d``.
     RoPE is applied when ``rope_base`` is given; ``rope_positions`` is the table length
-    (default: max position + 1, which costs one device-to-host read). Heads flagged in
-    ``token_order`` are packed in token order (see ``token_order_heads``). With ``fp32_heads``
+    (default: max position + 1, which costs one device-to-host read). ``token_order`` gives each
+    head's layout (``LAYOUT_*``, see ``token_order_heads``; True = token order). With ``fp32_heads``
     the call returns a fourth tensor, fp32 [n_flagged, 2, N, 64]: the fp32 q (index 0) and k (1) of
     the flagged heads after LayerNorm / RoPE, in token order and increasing head order. Heads flagged
     in ``q_scaled`` get their packed Q multiplied by ``q_scale`` (default ``prescale_factor()``) in
@@ -180,7 +201,7 @@ def pack_qkv(q, k, v, tok_stride: int, head_stride: int, geom: Geometry, num_hea
         _ptr(q), _ptr(k), _ptr(v), tok_stride, head_stride, geom.frames, geom.tokens_per_frame, geom.num_special,
         num_heads, _ptr(qw), _ptr(qb), _ptr(kw), _ptr(kb), float(ln_eps), int(apply_ln),
         _ptr(pos) if rc is not None else None, _ptr(rc), _ptr(rs), npos, _ptr(qp), _ptr(kp), _ptr(vp),
-        _u8_flags(token_order, num_heads), _u8_flags(fp32_heads, num_heads) if qk32 is not None else None,
+        _u8_layouts(token_order, num_heads), _u8_flags(fp32_heads, num_heads) if qk32 is not None else None,
         _ptr(qk32), _u8_flags(q_scaled, num_heads), float(prescale_factor() if q_scale is None else q_scale),
         _lib.stream_ptr()))
     if fp32_heads is not None:
@@ -263,12 +284,12 @@ def block_select(pooled_q: torch.Tensor, pooled_k: torch.Tensor, frames: int, bl
 def sparse_attn_fwd(qp, kp, vp, geom: Geometry, patterns: Sequence[int], sel: torch.Tensor | None = None,
                     scale: float | None = None, out: torch.Tensor | None = None,
                     keysets: "KeySets | None" = None, broadcast: "Broadcast | None" = None,
-                    token_order: Sequence[bool] | None = None, order: str | None = None,
+                    token_order: Sequence[int] | None = None, order: str | None = None,
                     q_scaled: Sequence[bool] | None = None) -> torch.Tensor:
     """All heads in one launch. Returns (or fills) ``out`` bf16 [N, H*64] in natural token order.
     ``keysets`` carries the compact K/V of the KEYSET heads and ``broadcast`` the frame-0 / per-frame
-    buffers of the BROADCAST heads (each in increasing head order); ``token_order`` flags the
-    DENSE heads that ``pack_qkv`` packed in token order; ``q_scaled`` the heads whose packed Q
+    buffers of the BROADCAST heads (each in increasing head order); ``token_order`` gives the layout
+    ``pack_qkv`` packed each head in (``token_order_heads``); ``q_scaled`` the heads whose packed Q
     carries ``prescale_factor(scale)`` (``pack_qkv(q_scaled=...)``), which then skip the running
     maximum. ``order`` ("paced" / "fixed", default ``walk_order()``) chooses the key-walk order
     (see ``set_walk_order``)."""
@@ -322,7 +343,7 @@ def sparse_attn_fwd(qp, kp, vp, geom: Geometry, patterns: Sequence[int], sel: to
     _lib.check(lib.saf3r_sparse_attn_fwd(
         _ptr(qp), _ptr(kp), _ptr(vp), geom.frames, geom.tokens_per_frame, geom.num_special, H,
         pat, _ptr(sel), width, float(scale), _ptr(out), out.stride(0), _ptr(ks_k), _ptr(ks_v), _ptr(ks_n),
-        ks_cap, _ptr(bq), _ptr(bk), _ptr(bv), _u8_flags(token_order, H), _u8_flags(q_scaled, H), flags,
+        ks_cap, _ptr(bq), _ptr(bk), _ptr(bv), _u8_layouts(token_order, H), _u8_flags(q_scaled, H), flags,
         _ptr(pace), seq, _lib.stream_ptr()))
     _mark("sparse_attn", "end")
     return out

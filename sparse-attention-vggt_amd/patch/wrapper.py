@@ -130,7 +130,8 @@ class BaseHeadwiseSparseAttentionWrapper(nn.Module):
             p2 = pos.reshape(-1, 2)
             # table length: the patch grid bounds every position ((y+1, x+1) with specials at 0)
             npos = max(self.patch_height, self.patch_width) + 1 if self.patch_height else None
-        tord = ops.token_order_heads(self.patterns)  # dense heads: unpadded token-order tiles
+        # dense heads: unpadded token-order tiles; frame-relative heads: whole frames per tile run
+        tord = ops.token_order_heads(self.patterns, geom)
         f32 = [h in self.fp32_slot for h in range(H)] if self.fp32_heads else None
         qs = self.q_scaled_heads()
         packed = ops.pack_qkv(qkv, qkv[:, C:], qkv[:, 2 * C:], 3 * C, HEAD_DIM, geom, H, ln_q=ln_q, ln_k=ln_k,

@@ -19,6 +19,19 @@ def slot_tokens(frames, tokens_per_frame, num_special):
     return torch.tensor(toks, dtype=torch.long)
 
 
+def framed_slot_tokens(frames, tokens_per_frame, num_special):
+    """Token id of every slot of a head in the framed layout (-1 for padding), over the same number of
+    slots as the packed layout: frame f's tokens in order from slot 64 * ceil(T/64) * f."""
+    T = tokens_per_frame
+    nslots = len(slot_tokens(frames, tokens_per_frame, num_special))
+    tp = -(-T // 64) * 64
+    toks = [-1] * nslots
+    for f in range(frames):
+        for t in range(T):
+            toks[f * tp + t] = f * T + t
+    return torch.tensor(toks, dtype=torch.long)
+
+
 def kappa(c):
     return (c & ~12) | ((c & 4) << 1) | ((c & 8) >> 1)
 

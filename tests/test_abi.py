@@ -24,7 +24,7 @@ def test_library_exports_every_declared_symbol(pkg):
     for n in names:
         assert hasattr(lib, n), n
     assert set(names) == set(lib_mod.EXPORTS)
-    assert lib.saf3r_abi_version() == lib_mod.ABI_VERSION == 8
+    assert lib.saf3r_abi_version() == lib_mod.ABI_VERSION == 9
 
 
 def test_packed_slots_matches_layout(pkg):
@@ -72,6 +72,17 @@ def test_invalid_arguments_fail_before_launch(pkg):
                                    None, None, None, tord, None, 0, None, 0, None)
     assert rc == 1 and b"only DENSE" in lib.saf3r_last_error()
     dn = (ctypes.c_int32 * 1)(0)
+    framed = (ctypes.c_uint8 * 1)(2)  # the framed layout on a DENSE head
+    rc = lib.saf3r_sparse_attn_fwd(dev, dev, dev, 2, 100, 5, 1, dn, None, 0, 0.125, dev, 64, None, None, None, 0,
+                                   None, None, None, framed, None, 0, None, 0, None)
+    assert rc == 1 and b"framed layout" in lib.saf3r_last_error()
+    # the framed layout where the special tokens do not fit a frame's last patch tile (P = 64, ns = 5)
+    rc = lib.saf3r_sparse_attn_fwd(dev, dev, dev, 2, 69, 5, 1, fl, None, 0, 0.125, dev, 64, None, None, None, 0,
+                                   None, None, None, framed, None, 0, None, 0, None)
+    assert rc == 2 and b"does not fit" in lib.saf3r_last_error()
+    rc = lib.saf3r_sparse_attn_fwd(dev, dev, dev, 2, 100, 5, 1, fl, None, 0, 0.125, dev, 64, None, None, None, 0,
+                                   None, None, None, (ctypes.c_uint8 * 1)(3), None, 0, None, 0, None)
+    assert rc == 1 and b"unknown layout" in lib.saf3r_last_error()
     rc = lib.saf3r_sparse_attn_fwd(dev, dev, dev, 2, 100, 5, 1, dn, None, 0, 0.125, dev, 64, None, None, None, 0,
                                    None, None, None, None, None, 6, None, 0, None)
     assert rc == 1 and b"unknown flags" in lib.saf3r_last_error()
@@ -119,6 +130,12 @@ def test_invalid_arguments_fail_before_launch(pkg):
     rc = lib.saf3r_pack_qkv(dev, dev, dev, 64, 64, 2, 100, 5, 65, None, None, None, None, 1e-5, 0, None, None,
                             None, 0, dev, dev, dev, flags, None, None, None, 1.0, None)
     assert rc == 2 and b"token order" in lib.saf3r_last_error()
+    rc = lib.saf3r_pack_qkv(dev, dev, dev, 64, 64, 2, 69, 5, 1, None, None, None, None, 1e-5, 0, None, None,
+                            None, 0, dev, dev, dev, framed, None, None, None, 1.0, None)
+    assert rc == 2 and b"framed layout" in lib.saf3r_last_error()
+    rc = lib.saf3r_pack_qkv(dev, dev, dev, 64, 64, 2, 100, 5, 1, None, None, None, None, 1e-5, 0, None, None,
+                            None, 0, dev, dev, dev, (ctypes.c_uint8 * 1)(7), None, None, None, 1.0, None)
+    assert rc == 1 and b"unknown layout" in lib.saf3r_last_error()
     rc = lib.saf3r_pack_qkv(dev, dev, dev, 64, 64, 2, 100, 5, 65, None, None, None, None, 1e-5, 0, None, None,
                             None, 0, dev, dev, dev, None, flags, dev, None, 1.0, None)
     assert rc == 2 and b"fp32 rows" in lib.saf3r_last_error()
@@ -151,6 +168,11 @@ def test_fault_injection_is_reported(pkg, monkeypatch):
 def test_geometry_derived_sizes(pkg):
     g = pkg.Geometry(128, 1374, 5)
     assert (g.patches, g.blocks_per_frame, g.num_blocks, g.tokens) == (1369, 22, 2816, 175872)
+    # framed layout: 22 tiles per frame (25 patches + 5 specials in the last), inside the 2826 packed tiles
+    assert (g.frame_tiles, g.framed_fits, g.tiles) == (22, True, 2826)
+    assert pkg.Geometry(2, 69, 5).framed_fits is False  # 64 patches fill their tile: no room for the specials
+    assert pkg.Geometry(3, 64, 0).framed_fits is True
+    assert pkg.Geometry(96, 1301, 5).framed_fits is True  # DA3 504^2: 1296 % 64 = 16, + 5
     g5 = pkg.Geometry(96, 1301, 5)
     assert (g5.blocks_per_frame, g5.num_blocks, g5.tokens) == (21, 2016, 124896)
     with pytest.raises(ValueError):

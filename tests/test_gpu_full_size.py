@@ -64,23 +64,27 @@ def _check_rows(out, q, k, v, patterns, og, sel_of, rows, what):
         assert err.max().item() <= ATOL_MAX and err.mean().item() <= ATOL_MEAN, f"{what} head {h}"
 
 
-def _run_selected_layer(ops, geom, q, k, v, patterns, k_sel):
-    qp, kp, vp = ops.pack_heads(q.to(DEV), k.to(DEV), v.to(DEV), geom)
+def _run_selected_layer(ops, geom, q, k, v, patterns, k_sel, layouts=False):
+    """One layer over packed heads; ``layouts``: the per-head layouts the plugin uses (token order for
+    dense heads, the framed layout for frame-relative heads), else every head in the packed layout."""
+    tord = ops.token_order_heads(patterns, geom) if layouts else None
+    qp, kp, vp = ops.pack_heads(q.to(DEV), k.to(DEV), v.to(DEV), geom, token_order=tord)
     dyn = [h for h, p in enumerate(patterns) if p == ops.BLOCK_DYNAMIC]
     pq, pk = ops.block_pool(qp, kp, geom, dyn)
     sel = ops.block_select(pq, pk, geom.frames, geom.blocks_per_frame, k_sel)
-    out = ops.sparse_attn_fwd(qp, kp, vp, geom, patterns, sel)
+    out = ops.sparse_attn_fwd(qp, kp, vp, geom, patterns, sel, token_order=tord)
     torch.cuda.synchronize()
     return out, sel.cpu(), dyn
 
 
-def _structured_layer(ops, synth, frames, heads, tokens_per_frame, patterns, k_sel, seed, n_random):
+def _structured_layer(ops, synth, frames, heads, tokens_per_frame, patterns, k_sel, seed, n_random, layouts):
     wl = synth.structured_qkv(frames=frames, heads=heads, tokens_per_frame=tokens_per_frame, seed=0)
     geom = wl.geom
     q, k, v = (t.to(torch.bfloat16) for t in (wl.q, wl.k, wl.v))
     del wl
-    out, sel, dyn = _run_selected_layer(ops, geom, q, k, v, patterns, k_sel)
-    print(f"F{frames} T{tokens_per_frame} H{heads}: layer ran, checking {len(dyn)} block lists", flush=True)
+    out, sel, dyn = _run_selected_layer(ops, geom, q, k, v, patterns, k_sel, layouts)
+    print(f"F{frames} T{tokens_per_frame} H{heads} layouts={layouts}: layer ran, checking {len(dyn)} block lists",
+          flush=True)
     for i, h in enumerate(dyn):
         want = OS.block_select(_bits(q[h]), _bits(k[h]), geom.frames, geom.tokens_per_frame, geom.num_special, k_sel)
         assert np.array_equal(sel[i].numpy(), want), f"block list of head {h}"
@@ -92,22 +96,27 @@ def _structured_layer(ops, synth, frames, heads, tokens_per_frame, patterns, k_s
 
 def test_layer_32_frames(mods):
     ops, synth = mods
-    _structured_layer(ops, synth, 32, 16, 1374, synth.seeded_patterns(16, seed=1), 4, seed=32, n_random=256)
+    _structured_layer(ops, synth, 32, 16, 1374, synth.seeded_patterns(16, seed=1), 4, seed=32, n_random=256,
+                      layouts=False)
 
 
 def test_layer_128_frames(mods):
     ops, synth = mods
-    _structured_layer(ops, synth, 128, 16, 1374, synth.seeded_patterns(16, seed=1), 4, seed=128, n_random=192)
+    _structured_layer(ops, synth, 128, 16, 1374, synth.seeded_patterns(16, seed=1), 4, seed=128, n_random=192,
+                      layouts=True)
 
 
 def test_layer_da3_shape(mods):
     ops, synth = mods
-    _structured_layer(ops, synth, 96, 24, 1301, synth.da3_patterns(24, seed=1), 8, seed=96, n_random=128)
+    _structured_layer(ops, synth, 96, 24, 1301, synth.da3_patterns(24, seed=1), 8, seed=96, n_random=128,
+                      layouts=True)
 
 
-@pytest.mark.parametrize("frames,tokens_per_frame,k_sel", [(128, 1374, 4), (96, 1301, 8)])
-def test_uniform_weights_every_row(mods, pkg, frames, tokens_per_frame, k_sel):
-    """Q = K = 0: each output row is the plain mean of V over the keys its pattern allows."""
+@pytest.mark.parametrize("frames,tokens_per_frame,k_sel,layouts",
+                         [(128, 1374, 4, True), (96, 1301, 8, True), (128, 1374, 4, False)])
+def test_uniform_weights_every_row(mods, pkg, frames, tokens_per_frame, k_sel, layouts):
+    """Q = K = 0: each output row is the plain mean of V over the keys its pattern allows (with the
+    plugin's per-head layouts, and with every head in the packed layout)."""
     ops, synth = mods
     geom = pkg.Geometry(frames, tokens_per_frame, 5)
     patterns = [ops.DENSE, ops.FRAME_LOCAL, ops.ANCHOR_LOCAL, ops.BLOCK_DYNAMIC, ops.ANCHOR, ops.SKIP,
@@ -116,7 +125,7 @@ def test_uniform_weights_every_row(mods, pkg, frames, tokens_per_frame, k_sel):
     g = torch.Generator().manual_seed(frames)
     v = torch.randn(H, N, 64, generator=g).to(torch.bfloat16)
     zero = torch.zeros(H, N, 64, dtype=torch.bfloat16)
-    out, sel, dyn = _run_selected_layer(ops, geom, zero, zero, v, patterns, k_sel)
+    out, sel, dyn = _run_selected_layer(ops, geom, zero, zero, v, patterns, k_sel, layouts)
     nbf = geom.blocks_per_frame
     kb = min(k_sel, nbf)
     lowest = (torch.arange(frames)[:, None] * nbf + torch.arange(kb)[None, :]).reshape(-1).to(torch.int32)
@@ -145,8 +154,8 @@ def test_uniform_weights_every_row(mods, pkg, frames, tokens_per_frame, k_sel):
         else:
             want = torch.zeros(frames, T, 64, dtype=torch.float64)
         err = (got[:, :, h].double() - want).abs()
-        print(f"uniform F{frames} head {h} pattern {pat}: max {err.max().item():.3g} mean {err.mean().item():.3g}",
-              flush=True)
+        print(f"uniform F{frames} layouts={layouts} head {h} pattern {pat}: max {err.max().item():.3g} "
+              f"mean {err.mean().item():.3g}", flush=True)
         assert err.max().item() <= ATOL_MAX and err.mean().item() <= ATOL_MEAN, f"head {h}"
 
 

@@ -12,7 +12,7 @@ import torch
 
 from oracle import attention as OA
 from oracle import selection as OS
-from tests.layout_ref import slot_tokens, unpack_rows, unpack_v
+from tests.layout_ref import framed_slot_tokens, slot_tokens, unpack_rows, unpack_v
 
 pytestmark = pytest.mark.gpu
 ATOL_MAX, ATOL_MEAN = 2e-2, 2e-3
@@ -69,6 +69,29 @@ def test_pack_token_order_bit_exact(ops, pkg, F, T, ns):
     tokord = torch.tensor([t if t < geom.tokens else -1 for t in range(geom.slots)])
     for h, fl in enumerate(flags):
         toks = tokord if fl else padded
+        for src, pk in ((q, qp), (k, kp)):
+            nat, pad = unpack_rows(pk[h:h + 1].cpu(), toks, geom.tokens)
+            assert torch.equal(nat[0], src[h]) and (pad == 0).all()
+        nat, pad = unpack_v(vp[h:h + 1].cpu(), toks, geom.tokens)
+        assert torch.equal(nat[0], v[h]) and (pad == 0).all()
+
+
+@pytest.mark.parametrize("F,T,ns", GEOMS)
+def test_pack_framed_bit_exact(ops, pkg, F, T, ns):
+    """Framed heads: frame f's tokens in order from tile f*ceil(T/64), zeros elsewhere; the other heads
+    keep their layouts. Where the framed layout does not fit the head, packing it is refused."""
+    geom = pkg.Geometry(F, T, ns)
+    H = 3
+    q, k, v = _qkv(H, geom.tokens, seed=F * 7 + T)
+    lay = [ops.LAYOUT_FRAMED, ops.LAYOUT_PACKED, ops.LAYOUT_TOKEN]
+    if not geom.framed_fits:
+        with pytest.raises(RuntimeError, match="framed layout"):
+            ops.pack_heads(q.to(DEV), k.to(DEV), v.to(DEV), geom, token_order=lay)
+        return
+    qp, kp, vp = ops.pack_heads(q.to(DEV), k.to(DEV), v.to(DEV), geom, token_order=lay)
+    torch.cuda.synchronize()
+    tokord = torch.tensor([t if t < geom.tokens else -1 for t in range(geom.slots)])
+    for h, toks in enumerate((framed_slot_tokens(F, T, ns), slot_tokens(F, T, ns), tokord)):
         for src, pk in ((q, qp), (k, kp)):
             nat, pad = unpack_rows(pk[h:h + 1].cpu(), toks, geom.tokens)
             assert torch.equal(nat[0], src[h]) and (pad == 0).all()
@@ -192,8 +215,40 @@ def test_sparse_attention_token_order_dense(ops, pkg, F, T, ns):
         _check_close(got[h], ref, f"token order F{F} T{T} ns{ns} head {h} pattern {pat}")
 
 
+@pytest.mark.parametrize("F,T,ns", GEOMS)
+@pytest.mark.parametrize("prescaled", [False, True])
+def test_sparse_attention_framed(ops, pkg, F, T, ns, prescaled):
+    """Frame-relative heads in the framed layout (the plugin's layouts: token order for dense heads),
+    with packed-layout heads in the same launch, against the oracle. Where the framed layout does not
+    fit, token_order_heads leaves those heads packed and the same check covers that path."""
+    geom = pkg.Geometry(F, T, ns)
+    patterns = [ops.FRAME_LOCAL, ops.ANCHOR_LOCAL, ops.DENSE, ops.ANCHOR, ops.BLOCK_DYNAMIC, ops.FRAME_LOCAL,
+                ops.ANCHOR_LOCAL]
+    H = len(patterns)
+    q, k, v = _qkv(H, geom.tokens, seed=F * 19 + T, scale=1.5)
+    tord = ops.token_order_heads(patterns, geom)
+    want_lay = ops.LAYOUT_FRAMED if geom.framed_fits else ops.LAYOUT_PACKED
+    assert [tord[h] for h in (0, 1, 3, 5, 6)] == [want_lay] * 5 and tord[2] == ops.LAYOUT_TOKEN
+    flags = [prescaled] * H
+    qp, kp, vp = ops.pack_heads(q.to(DEV), k.to(DEV), v.to(DEV), geom, token_order=tord, q_scaled=flags)
+    pq, pk = ops.block_pool(qp, kp, geom, [4])
+    sel = ops.block_select(pq, pk, geom.frames, geom.blocks_per_frame, 2)
+    og = OA.Geometry(F, T, ns)
+    c = ops.prescale_factor()
+    for order in ("fixed", "paced"):
+        out = ops.sparse_attn_fwd(qp, kp, vp, geom, patterns, sel, token_order=tord, q_scaled=flags, order=order)
+        torch.cuda.synchronize()
+        got = out.float().cpu().reshape(geom.tokens, H, 64).permute(1, 0, 2)
+        for h, pat in enumerate(patterns):
+            qh = (q[h].float() * c).to(torch.bfloat16).float() / c if prescaled else q[h].float()
+            ref = OA.sparse_attention_gathered(qh, k[h].float(), v[h].float(), pat, og,
+                                               sel[0].cpu() if h == 4 else None, dtype=torch.float64)
+            _check_close(got[h], ref, f"framed F{F} T{T} ns{ns} prescaled={prescaled} {order} head {h} pattern {pat}")
+
+
 @pytest.mark.parametrize("phase", ["fixed", "paced"])
-def test_sparse_attention_outrun_reference(ops, pkg, phase):
+@pytest.mark.parametrize("framed", [False, True])
+def test_sparse_attention_outrun_reference(ops, pkg, phase, framed):
     """Keys whose scores exceed the lazily moved reference maximum by more than 2^64 in P (and one
     beyond the fp32 exponent range) must take the exact path: rescale O and l, recompute P. Every
     pattern must still match the oracle. In the fixed walk order every walk starts at its first
@@ -209,7 +264,9 @@ def test_sparse_attention_outrun_reference(ops, pkg, phase):
     last = (geom.frames - 1) * geom.tokens_per_frame
     k[:, last + 40] = 12.0   # q.k ~ 384: about 69 log2 units above the first steps
     k[:, last + 100] = 30.0  # about 173 log2 units: exp2 overflows fp32 in the fast pass
-    flags = [True, False, False, False, False]  # dense head 0 token order, head 1 padded
+    # dense head 0 token order, head 1 packed; the frame-relative heads packed or framed
+    F2 = ops.LAYOUT_FRAMED if framed else ops.LAYOUT_PACKED
+    flags = [ops.LAYOUT_TOKEN, ops.LAYOUT_PACKED, ops.LAYOUT_PACKED, F2, F2]
     qp, kp, vp = ops.pack_heads(q.to(DEV), k.to(DEV), v.to(DEV), geom, token_order=flags)
     pq, pk = ops.block_pool(qp, kp, geom, [2])
     sel = ops.block_select(pq, pk, geom.frames, geom.blocks_per_frame, 2)
@@ -221,15 +278,16 @@ def test_sparse_attention_outrun_reference(ops, pkg, phase):
     for h, pat in enumerate(patterns):
         ref = OA.sparse_attention_gathered(q[h].float(), k[h].float(), v[h].float(), pat, og,
                                            sel[0].cpu() if h == 2 else None, dtype=torch.float64)
-        _check_close(got[h], ref, f"outrun phase={phase} head {h} pattern {pat}")
+        _check_close(got[h], ref, f"outrun phase={phase} framed={framed} head {h} pattern {pat}")
 
 
-def _prescaled_run(ops, pkg, geom, q, k, v, patterns, flags, order=None, k_sel=2):
+def _prescaled_run(ops, pkg, geom, q, k, v, patterns, flags, order=None, k_sel=2, framed=False):
     """Packs every head with the softmax scale folded into Q and runs the attention on it; returns the
-    output, the block lists, and the q the kernels consumed in unscaled units (fp32: packed / factor)."""
+    output, the block lists, and the q the kernels consumed in unscaled units (fp32: packed / factor).
+    ``framed``: frame-relative heads in the framed layout."""
     c = ops.prescale_factor()
     H = len(patterns)
-    tord = ops.token_order_heads(patterns)
+    tord = ops.token_order_heads(patterns, geom if framed else None)
     qp, kp, vp = ops.pack_heads(q.to(DEV), k.to(DEV), v.to(DEV), geom, token_order=tord, q_scaled=flags)
     dyn = [h for h, p in enumerate(patterns) if p == ops.BLOCK_DYNAMIC]
     sel = None
@@ -265,7 +323,8 @@ def test_sparse_attention_prescaled_q(ops, pkg, F, T, ns):
 
 
 @pytest.mark.parametrize("phase", ["fixed", "paced"])
-def test_sparse_attention_prescaled_out_of_range(ops, pkg, phase):
+@pytest.mark.parametrize("framed", [False, True])
+def test_sparse_attention_prescaled_out_of_range(ops, pkg, phase, framed):
     """Prescaled heads whose scores leave the range of the walk without a running maximum: keys 69
     and 173 log2 units above the rest (partial row sums beyond 2^64), and rows whose every score lies
     more than 64 units below 0 (row sums below 2^-64). The main launch marks those items and the
@@ -285,14 +344,14 @@ def test_sparse_attention_prescaled_out_of_range(ops, pkg, phase):
     q[5] = (2.5 + 0.05 * torch.randn(N, 64, generator=g)).to(torch.bfloat16)
     k[5] = (-2.5 + 0.05 * torch.randn(N, 64, generator=g)).to(torch.bfloat16)
     flags = [True] * H
-    out, sel, dyn, q_used = _prescaled_run(ops, pkg, geom, q, k, v, patterns, flags, order=phase)
+    out, sel, dyn, q_used = _prescaled_run(ops, pkg, geom, q, k, v, patterns, flags, order=phase, framed=framed)
     og = OA.Geometry(3, 155, 5)
     got = out.float().cpu().reshape(N, H, 64).permute(1, 0, 2)
     assert torch.isfinite(got).all()
     for h, pat in enumerate(patterns):
         ref = OA.sparse_attention_gathered(q_used[h], k[h].float(), v[h].float(), pat, og,
                                            sel[0].cpu() if h == 2 else None, dtype=torch.float64)
-        _check_close(got[h], ref, f"prescaled out of range phase={phase} head {h} pattern {pat}")
+        _check_close(got[h], ref, f"prescaled out of range phase={phase} framed={framed} head {h} pattern {pat}")
 
 
 def test_walk_order_paced_and_fixed(ops, pkg):
@@ -303,7 +362,7 @@ def test_walk_order_paced_and_fixed(ops, pkg):
     patterns = [ops.DENSE, ops.BLOCK_DYNAMIC, ops.FRAME_LOCAL, ops.ANCHOR_LOCAL, ops.BLOCK_DYNAMIC, ops.DENSE]
     H = len(patterns)
     q, k, v = _qkv(H, geom.tokens, seed=99, scale=1.5)
-    flags = ops.token_order_heads(patterns)
+    flags = ops.token_order_heads(patterns, geom)  # the plugin's layouts
     qp, kp, vp = ops.pack_heads(q.to(DEV), k.to(DEV), v.to(DEV), geom, token_order=flags)
     dyn = [1, 4]
     pq, pk = ops.block_pool(qp, kp, geom, dyn)
