@@ -165,6 +165,48 @@ def test_block_select_bit_exact(ops, frames, nbf, k, scope):
         assert np.array_equal(got[h], ref)
 
 
+def _pooled_case(case, n, rows, rng):
+    x = rng.standard_normal((n, rows, 64)).astype(np.float32) * np.float32(0.2)
+    if case == "zeros":  # every score 0: no order is certain, every pair takes the sequential path
+        x[:] = 0
+    elif case == "wide":  # magnitudes 1e-30 .. 1e30 across rows and features
+        x *= (10.0 ** rng.uniform(-30, 30, size=(n, rows, 64))).astype(np.float32)
+    elif case == "tiny":  # values at and below the fp32 / bf16 normal range
+        x *= np.float32(1e-37)
+        x[:, ::3] *= np.float32(1e-3)
+    elif case == "nonfinite":
+        x.reshape(-1)[rng.integers(0, x.size, 40)] = np.inf
+        x.reshape(-1)[rng.integers(0, x.size, 40)] = -np.inf
+        x.reshape(-1)[rng.integers(0, x.size, 40)] = np.nan
+    return x
+
+
+_ADV_CASES = ["normal", "ties", "zeros", "wide", "tiny", "nonfinite"]
+
+
+@pytest.mark.parametrize("frames,nbf,k,case",
+                         [(f, b, kk, c) for (f, b, kk) in [(4, 22, 4), (5, 32, 8), (3, 1, 1), (6, 21, 3), (2, 7, 8),
+                                                          (9, 17, 2)] for c in _ADV_CASES]
+                         + [(128, 22, 4, "normal")])
+def test_block_select_adversarial_bit_exact(ops, frames, nbf, k, case):
+    """Block selection against the oracle on pooled inputs that stress the order: exact ties (equal
+    candidates, equal query blocks, 1-ulp neighbours), all-zero scores, 60 decades of magnitude,
+    values below the normal range, infinities and NaNs."""
+    rng = np.random.default_rng(frames * 7 + nbf * 3 + k + len(case))
+    n, nb = 2, frames * nbf
+    pq = _pooled_case(case, n, nb, rng)
+    pk = _pooled_case(case, n, nb, rng)
+    if case == "ties":
+        pk[:, 1::nbf] = pk[:, 0::nbf][:, :pk[:, 1::nbf].shape[1]]
+        pq[:, 1::2] = pq[:, 0::2][:, :pq[:, 1::2].shape[1]]
+        if nbf > 3:
+            pk[0, 2::nbf] = np.nextafter(pk[0, 3::nbf], np.float32(np.inf))
+    got = ops.block_select(torch.from_numpy(pq).to(DEV), torch.from_numpy(pk).to(DEV), frames, nbf, k).cpu().numpy()
+    for h in range(n):
+        ref = OS.frame_topk(OS.block_scores(pq[h], pk[h]), frames, k)
+        assert np.array_equal(got[h], ref), f"{case}: head {h} differs from the oracle"
+
+
 def _run_layer(ops, pkg, geom, q, k, v, patterns, k_sel=2):
     qp, kp, vp = ops.pack_heads(q.to(DEV), k.to(DEV), v.to(DEV), geom)
     dyn = [h for h, p in enumerate(patterns) if p == ops.BLOCK_DYNAMIC]
@@ -408,26 +450,35 @@ def test_sparse_attention_selection_edge_cases(ops, pkg):
         _check_close(got[h], ref, f"edge head {h}")
 
 
-def test_sparse_attention_structured_c1(ops, pkg):
-    """The 4-frame VGGT shape with the structured generator and round-robin patterns."""
+@pytest.mark.parametrize("layouts", [False, True])
+def test_sparse_attention_structured_c1(ops, pkg, layouts):
+    """The 4-frame VGGT shape (5,496 tokens, 16 heads) with the structured generator and round-robin
+    patterns: every head in the packed layout, or with the plugin's layouts and prescaled Q."""
     synth = importlib.import_module(pkg.__name__ + ".synth")
-    wl = synth.structured_qkv(frames=4, heads=4, seed=0)
+    H = 16
+    wl = synth.structured_qkv(frames=4, heads=H, seed=0)
     geom = wl.geom
-    patterns = synth.round_robin_patterns(4)
+    patterns = synth.round_robin_patterns(H)
     q, k, v = (t.to(torch.bfloat16) for t in (wl.q, wl.k, wl.v))
-    out, sel, dyn = _run_layer(ops, pkg, geom, q, k, v, patterns, k_sel=4)
+    if layouts:
+        out, sel, dyn, q_used = _prescaled_run(ops, pkg, geom, q, k, v, patterns, [True] * H, k_sel=4, framed=True)
+    else:
+        out, sel, dyn = _run_layer(ops, pkg, geom, q, k, v, patterns, k_sel=4)
+        q_used = q.float()
     og = OA.Geometry(geom.frames, geom.tokens_per_frame, geom.num_special)
-    got = out.float().cpu().reshape(geom.tokens, 4, 64).permute(1, 0, 2)
-    # the selection is bit-exact against the oracle pipeline
+    got = out.float().cpu().reshape(geom.tokens, H, 64).permute(1, 0, 2)
+    # the selection is bit-exact against the oracle pipeline on the packed Q (prescaled: bf16(q * c))
+    c = ops.prescale_factor()
     for i, h in enumerate(dyn):
-        ref_sel = OS.block_select(OS.bf16_bits(q[h].float().numpy()), OS.bf16_bits(k[h].float().numpy()),
+        qsel = (q[h].float() * c).to(torch.bfloat16) if layouts else q[h]
+        ref_sel = OS.block_select(OS.bf16_bits(qsel.float().numpy()), OS.bf16_bits(k[h].float().numpy()),
                                   geom.frames, geom.tokens_per_frame, geom.num_special, 4)
         assert np.array_equal(sel[i].cpu().numpy(), ref_sel)
     sel_by_head = {h: sel[i].cpu() for i, h in enumerate(dyn)}
     for h, pat in enumerate(patterns):
-        ref = OA.sparse_attention_gathered(q[h].float(), k[h].float(), v[h].float(), pat, og, sel_by_head.get(h),
+        ref = OA.sparse_attention_gathered(q_used[h], k[h].float(), v[h].float(), pat, og, sel_by_head.get(h),
                                            dtype=torch.float64)
-        _check_close(got[h], ref, f"C1 head {h} pattern {pat}")
+        _check_close(got[h], ref, f"C1 layouts={layouts} head {h} pattern {pat}")
 
 
 @pytest.mark.parametrize("n,nk,topk", [(100, 300, 7), (37, 64, 64), (64, 5000, 512), (5, 3000, 2100)])
