@@ -332,6 +332,50 @@ def calibrate_copy():
                       "write_bytes": dst.numel() * 4, "launches": 3}), flush=True)
 
 
+def per_pattern(pkg, frames, reps=5):
+    """The attention launch alone, per pattern: 16 heads of one pattern (dense in token order, block
+    top-4, frame-local / anchor+local / anchor in the framed layout) and the bench's 16-head mix (seed 1),
+    over N(0,1) q / k / v at ``frames`` x 1374 tokens, every head with the softmax scale packed into Q,
+    walks paced; 2 warm-up launches, the median of ``reps`` (stream events around each launch)."""
+    import importlib
+    ops = importlib.import_module(pkg.__name__ + ".ops")
+    acc = importlib.import_module(pkg.__name__ + ".accounting")
+    synth = importlib.import_module(pkg.__name__ + ".synth")
+    dev = torch.device("cuda:0")
+    H = 16
+    geom = pkg.Geometry(frames, 1374, 5)
+    g = torch.Generator(device=dev).manual_seed(0)
+    q, k, v = (torch.randn(H, geom.tokens, 64, generator=g, device=dev).to(torch.bfloat16) for _ in range(3))
+    sets = {"dense": [ops.DENSE] * H, "block_topk": [ops.BLOCK_DYNAMIC] * H, "frame_local": [ops.FRAME_LOCAL] * H,
+            "anchor_local": [ops.ANCHOR_LOCAL] * H, "anchor": [ops.ANCHOR] * H, "mix": synth.seeded_patterns(H, seed=1)}
+    res = {"shape": f"{frames} x 1374 tokens, {H} heads", "reps": reps}
+    out = torch.empty(geom.tokens, H * 64, dtype=torch.bfloat16, device=dev)
+    for name, pats in sets.items():
+        lay = ops.token_order_heads(pats, geom)
+        qs = [True] * H
+        qp, kp, vp = ops.pack_heads(q, k, v, geom, token_order=lay, q_scaled=qs)
+        dyn = [h for h, p in enumerate(pats) if p == ops.BLOCK_DYNAMIC]
+        sel = None
+        if dyn:
+            pq, pk = ops.block_pool(qp, kp, geom, dyn)
+            sel = ops.block_select(pq, pk, frames, geom.blocks_per_frame, 4)
+        for _ in range(2):
+            ops.sparse_attn_fwd(qp, kp, vp, geom, pats, sel, out=out, token_order=lay, q_scaled=qs)
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(reps):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            ops.sparse_attn_fwd(qp, kp, vp, geom, pats, sel, out=out, token_order=lay, q_scaled=qs)
+            e1.record()
+            torch.cuda.synchronize()
+            ts.append(e0.elapsed_time(e1))
+        ms = statistics.median(ts)
+        res[name] = {"ms": round(ms, 3), "tflops": round(acc.attention_flops(pats, geom, sel) / (ms * 1e-3) / 1e12, 1)}
+        del qp, kp, vp
+    return res
+
+
 def measured_traffic(kernel="sparse_attn_kernel"):
     """HBM bytes per launch of the attention kernel at this workload, as recorded from the
     FETCH_SIZE and WRITE_SIZE counter runs (scaled by the copy calibration) in the committed
@@ -360,6 +404,8 @@ def main():
                     help="also time the non-lazy DINO-feature token selection at the full frame count")
     ap.add_argument("--aggregator-frames", type=int, default=64,
                     help="frames of the full-aggregator forward leg (0 skips it)")
+    ap.add_argument("--per-pattern", action="store_true",
+                    help="run only the per-pattern attention timing (16 heads of each pattern, and the head mix)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only a plain copy kernel of known size (reads 1 GiB, writes 1 GiB), for scaling "
                          "the FETCH_SIZE / WRITE_SIZE counters of a profiling run")
@@ -371,6 +417,9 @@ def main():
 
     if args.calibrate_copy:
         calibrate_copy()
+        return
+    if args.per_pattern:
+        print(json.dumps({"per_pattern": per_pattern(__graft_entry__.package(), args.frames)}), flush=True)
         return
 
     import importlib
