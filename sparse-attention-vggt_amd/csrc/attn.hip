@@ -16,7 +16,8 @@
 // need one cross-half exchange (v_permlane32_swap). Softmax uses base-2 exponentials against a
 // lazily moved reference maximum: no per-tile maximum is taken; the reference (and O, l) move only
 // when a tile's partial row sum exceeds 2^64. Row sums are dot2 products of the bf16 P values
-// that feed the PV product.
+// that feed the PV product; walks without a reference maximum (FAST) sum the same P values on the
+// matrix core instead (v_mfma_f32_4x4x4_16b_bf16 against a 0/1 selector, next to the PV product).
 //
 // Shared mode (dense, frame-local, anchor+local, anchor, special rows of the dynamic patterns):
 // a workgroup of four waves owns up to four consecutive query tiles with one key sequence. Full
@@ -110,7 +111,30 @@ struct Acc {
   f32x16 o[2][2];  // [dh][gq]: O^T rows 32*dh + (16*half + a), query 32*gq + col
   float m[2];      // reference maximum (raw score units) per query group
   float l[2];      // partial row sum over this lane's keys
+  f32x4 ls;        // FAST walks: element gq = this lane's row sum of group gq from the matrix core
+  s16x4 sel[2];    // 0/1 selector operands of those row sums (bf16 1.0 in the lanes of row gq)
 };
+
+// FAST row sums on the matrix core: v_mfma_f32_4x4x4_16b_bf16 computes, in each of its 16 blocks
+// of four lanes, D[i][j] = sum_k A[i][k] B[k][j], with A row i held by lane 4b+i, B column j and D
+// column j by lane 4b+j, and D row i in accumulator element i. With B = four P values of a lane
+// and A = sel[gq] (ones in row gq only) the lane's own accumulator element gq gains the sum of its
+// four values; two instructions take a P fragment (eight values). The P values are the bf16 ones
+// that feed the PV product, as with the dot2 sums.
+__device__ __forceinline__ void rowsum_mfma(Acc& A, const bf16x8& pf, int gq) {
+  const u32x4 w = __builtin_bit_cast(u32x4, pf);
+  const s16x4 lo = __builtin_bit_cast(s16x4, u32x2{w[0], w[1]});
+  const s16x4 hi = __builtin_bit_cast(s16x4, u32x2{w[2], w[3]});
+  A.ls = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(A.sel[gq], lo, A.ls, 0, 0, 0);
+  A.ls = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(A.sel[gq], hi, A.ls, 0, 0, 0);
+}
+
+// end of a FAST pipelined walk: the matrix-core row sums join the lane's partial sums
+__device__ __forceinline__ void fold_rowsums(Acc& A) {
+  A.l[0] += A.ls[0];
+  A.l[1] += A.ls[1];
+  A.ls = f32x4{};
+}
 
 struct TileMask {
   bool need;     // some element of the tile is masked
@@ -318,6 +342,8 @@ __device__ __forceinline__ void half_block(const bf16x8 (&kf)[4], const bf16x8 (
     if (i < 8) {
       const int j = i >> 2, dh = (i >> 1) & 1, gq = i & 1;
       A.o[dh][gq] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[j][dh], p[gq][j], A.o[dh][gq], 0, 0, 0);
+      if constexpr (FAST)
+        if (dh == 1) rowsum_mfma(A, p[gq][j], gq);  // each P fragment once, after its second PV
     } else {
       const int k = i - 8, st = k >> 1, gq = k & 1;
       sn[gq] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[st], qfrag[gq][st], sn[gq], 0, 0, 0);
@@ -343,21 +369,27 @@ __device__ __forceinline__ void half_block(const bf16x8 (&kf)[4], const bf16x8 (
     __builtin_amdgcn_sched_barrier(0);
   }
   // row sums of the rounded P (so l and O agree), as one burst of dot2 at the end: each dot2
-  // waits for the matrix pipe, so spread between the MFMAs they would stall every one of them
-  const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
-  ts[0] = ts[1] = 0.f;
+  // waits for the matrix pipe, so spread between the MFMAs they would stall every one of them.
+  // FAST walks summed P(h-1) on the matrix core above and never read ts.
+  if constexpr (!FAST) {
+    const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
+    ts[0] = ts[1] = 0.f;
 #pragma unroll
-  for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
-    for (int u = 0; u < 8; u += 2)
+      for (int u = 0; u < 8; u += 2)
 #pragma unroll
-      for (int g = 0; g < 2; ++g) {
-        const bf16x2 pr = {pn[g][j][u], pn[g][j][u + 1]};
-        ts[g] = __builtin_amdgcn_fdot2_f32_bf16(pr, ones, ts[g], false);
-      }
+        for (int g = 0; g < 2; ++g) {
+          const bf16x2 pr = {pn[g][j][u], pn[g][j][u + 1]};
+          ts[g] = __builtin_amdgcn_fdot2_f32_bf16(pr, ones, ts[g], false);
+        }
+    asm volatile("" : "+v"(ts[0]), "+v"(ts[1]));
+  } else {
+    asm volatile("" : "+v"(A.ls));
+  }
   // every result is due here: otherwise the compiler sinks the softmax (and MFMAs) past the
   // masking branch that follows, into blocks of their own, and nothing overlaps any more
-  asm volatile("" : "+v"(pn[0][0]), "+v"(pn[0][1]), "+v"(pn[1][0]), "+v"(pn[1][1]), "+v"(ts[0]), "+v"(ts[1]));
+  asm volatile("" : "+v"(pn[0][0]), "+v"(pn[0][1]), "+v"(pn[1][0]), "+v"(pn[1][1]));
   asm volatile("" : "+v"(sn[0]), "+v"(sn[1]));
   asm volatile("" : "+v"(A.o[0][0]), "+v"(A.o[0][1]), "+v"(A.o[1][0]), "+v"(A.o[1][1]));
 }
@@ -368,7 +400,13 @@ __device__ __forceinline__ void half_block(const bf16x8 (&kf)[4], const bf16x8 (
 // maximum of s, rescales O (which then holds every step before h) and l, and recomputes P(h).
 // The row sums a FAST walk (reference maximum fixed at 0) may end with: within [2^-64, 2^64] every
 // P of the row is at most 2^64 and the row's largest P at least 2^-64 / n (no NaN passes).
-__device__ __forceinline__ bool in_fast_range(float l) { return l >= 0x1p-64f && l <= 0x1p64f; }
+// The test runs on the bits: for l >= 0 their order is the order of the values, and a NaN (which
+// the matrix-core row sums give where a selector zero meets an infinite P, and which comparisons
+// compiled without NaN semantics would not see) lies above 2^64 there, as does -0.
+__device__ __forceinline__ bool in_fast_range(float l) {
+  const uint32_t b = __builtin_bit_cast(uint32_t, l);
+  return b >= 0x1F800000u && b <= 0x5F800000u;  // 2^-64, 2^64
+}
 
 // FAST walks (reference fixed at 0) check nothing per step: every P is non-negative, so a row sum
 // that ends within [2^-64, 2^64] bounds every P of the row, and the end of the walk tests that.
@@ -726,7 +764,10 @@ __device__ __forceinline__ void attn_body(const AttnParams& p, const int item) {
       A.o[a][0] = A.o[a][1] = f32x16{};
       A.m[a] = fast ? 0.f : -__builtin_inff();
       A.l[a] = 0.f;
+      const short one = (lane & 3) == a ? (short)0x3F80 : (short)0;  // bf16 1.0 in row a's lanes
+      A.sel[a] = s16x4{one, one, one, one};
     }
+    A.ls = f32x4{};
   };
   // FAST end of a walk: true (work-group uniform) when the item must be walked again exactly
   auto walk_unsafe = [&]() -> bool {
@@ -952,8 +993,10 @@ __device__ __forceinline__ void attn_body(const AttnParams& p, const int item) {
           half_block<FAST>(kf, vf, qfrag, s_cur, s_nxt, pc, pn, ts, A, c);
           if (kv_cur < 64) mask_valid(s_nxt, kv_cur, 32, half);
           exact_fix<FAST>(s_cur, pn, ts, A, c);
-          A.l[0] += ts[0];
-          A.l[1] += ts[1];
+          if constexpr (!FAST) {
+            A.l[0] += ts[0];
+            A.l[1] += ts[1];
+          }
           advance();
           const int kv_nxt = kvalid_of();  // tile t + 1 (past the end: never read)
           if (t + 2 < cnt) wait_vm<4>();
@@ -966,8 +1009,10 @@ __device__ __forceinline__ void attn_body(const AttnParams& p, const int item) {
           half_block<FAST>(kf, vf, qfrag, s_nxt, s_cur, pn, pc, ts, A, c);
           if (kv_nxt < 64) mask_valid(s_cur, kv_nxt, 0, half);
           exact_fix<FAST>(s_nxt, pc, ts, A, c);
-          A.l[0] += ts[0];
-          A.l[1] += ts[1];
+          if constexpr (!FAST) {
+            A.l[0] += ts[0];
+            A.l[1] += ts[1];
+          }
           kv_cur = kv_nxt;
         }
       }
@@ -979,6 +1024,14 @@ __device__ __forceinline__ void attn_body(const AttnParams& p, const int item) {
           A.o[dh][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[j][dh], pc[0][j], A.o[dh][0], 0, 0, 0);
           A.o[dh][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[j][dh], pc[1][j], A.o[dh][1], 0, 0, 0);
         }
+      if constexpr (FAST) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          rowsum_mfma(A, pc[0][j], 0);
+          rowsum_mfma(A, pc[1][j], 1);
+        }
+        fold_rowsums(A);
+      }
       if (!rel_patch) {
         if (tid == 0 && paced) pace_add(p, 0, t_start, cnt);
         finish();
@@ -1174,8 +1227,10 @@ __device__ __forceinline__ void attn_body(const AttnParams& p, const int item) {
         const int kv0 = e0 & 127;
         if (kv0 < 64) mask_valid(s_nxt, kv0, 32, half);
         exact_fix<FAST>(s_cur, pn, ts, A, c);
-        A.l[0] += ts[0];
-        A.l[1] += ts[1];
+        if constexpr (!FAST) {
+          A.l[0] += ts[0];
+          A.l[1] += ts[1];
+        }
         // half step 2t+1: PV of block t half 0, scores of block t+1 half 0, softmax of block t half 1
         wait_vm<8>();
         load_vh(slots + 4096, vf);
@@ -1186,8 +1241,10 @@ __device__ __forceinline__ void attn_body(const AttnParams& p, const int item) {
         const int kv1 = e1 & 127;
         if (kv1 < 32) mask_valid(s_cur, kv1, 0, half);
         exact_fix<FAST>(s_nxt, pc, ts, A, c);
-        A.l[0] += ts[0];
-        A.l[1] += ts[1];
+        if constexpr (!FAST) {
+          A.l[0] += ts[0];
+          A.l[1] += ts[1];
+        }
         e0 = e1;
         e1 = e2;
         e2 = ent(t + 3);
@@ -1204,6 +1261,12 @@ __device__ __forceinline__ void attn_body(const AttnParams& p, const int item) {
           A.o[dh][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[j][dh], pc[1][j], A.o[dh][1], 0, 0, 0);
         }
       if constexpr (FAST) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          rowsum_mfma(A, pc[0][j], 0);
+          rowsum_mfma(A, pc[1][j], 1);
+        }
+        fold_rowsums(A);
         bool low = false;
 #pragma unroll
         for (int gq = 0; gq < 2; ++gq) low |= !in_fast_range(partner_sum(A.l[gq]));
