@@ -5,9 +5,10 @@
  * Conventions
  *   - Every entry returns an int status (SAF3R_OK = 0). On failure nothing is launched and
  *     saf3r_last_error() returns a message (thread-local). No C++ exception crosses the ABI.
- *   - Every device buffer is allocated by the caller; the library never allocates or frees
- *     device memory and keeps no device state (the one exception is the static workspace of
- *     saf3r_probe_scores_noalloc, a device array of the library's code object). `stream` is a hipStream_t (NULL = default
+ *   - Every device buffer, workspaces included, is allocated by the caller (entries that need a
+ *     workspace have a size query); the library never allocates or frees device memory and keeps
+ *     no device state (the one exception is the static workspace of saf3r_probe_scores_noalloc, a
+ *     device array of the library's code object). `stream` is a hipStream_t (NULL = default
  *     stream); every entry is asynchronous on it and performs no host synchronisation.
  *   - bf16 buffers are passed as void* (IEEE bfloat16, 2 bytes per element).
  *   - Host-side arrays (head tables, frequency tables) are read during the call only.
@@ -47,7 +48,7 @@
 extern "C" {
 #endif
 
-#define SAF3R_ABI_VERSION 9
+#define SAF3R_ABI_VERSION 10
 
 enum saf3r_status {
   SAF3R_OK = 0,
@@ -89,6 +90,13 @@ enum saf3r_layout {
 /* Flags of saf3r_sparse_attn_fwd. */
 enum saf3r_attn_flags {
   SAF3R_ATTN_FIXED_ORDER = 1 /* every key walk starts at its first tile: run-to-run identical output */
+};
+
+/* dtype_flags of saf3r_gather_attn_fwd: rows are bf16 unless flagged fp32. */
+enum saf3r_gather_dtype {
+  SAF3R_GATHER_QK_FP32 = 1, /* q and k rows are fp32 */
+  SAF3R_GATHER_V_FP32 = 2,  /* v rows are fp32 */
+  SAF3R_GATHER_OUT_FP32 = 4 /* out rows are fp32 (the accumulator itself, not rounded) */
 };
 
 /* Key-set kinds of saf3r_keyset_build. */
@@ -211,9 +219,10 @@ int saf3r_probe_scores(const float* q32, const float* k32, int64_t slot_stride, 
  * no allocating library call) and keeps the partial sums in a static device array of the library
  * (4 MiB per GPU, held until the process ends), for callers that cannot allocate: code under HIP
  * graph capture, tight serving loops, harnesses that forbid allocation. n_sel <= 64
- * (SAF3R_ERR_UNSUPPORTED beyond). Results are identical to saf3r_probe_scores. The array belongs to
- * the current device and is shared by every call on it: calls that overlap on one GPU (other streams,
- * other host threads) race. No counterpart in the reference.
+ * (SAF3R_ERR_UNSUPPORTED beyond). Results are identical to saf3r_probe_scores. The array used is
+ * the one of the device of `stream` (the current device for the NULL stream), shared by every call
+ * on that device: calls that overlap on one GPU (other streams, other host threads) race. No
+ * counterpart in the reference.
  */
 int saf3r_probe_scores_noalloc(const float* q32, const float* k32, int64_t slot_stride, int n_tokens,
                                const int32_t* slots, int n_sel, const int32_t* sample_idx, int n_samples,
@@ -301,28 +310,42 @@ int saf3r_sparse_attn_fwd(const void* q_packed, const void* k_packed, const void
 
 /*
  * Gather attention: out[r] = sum_j softmax_j(q[r] . k[idx[r][j]] * scale) v[idx[r][j]], fp32
- * accumulation, head_dim 64; idx entries < 0 or >= num_keys are skipped.
- *   q, k: bf16 rows, or fp32 rows with qk_fp32 = 1 (row strides in elements of that type);
- *   v, out: bf16 rows.
+ * scores and accumulation, head_dim 64 (q, k, v and out rows of 64 elements); idx entries < 0 or
+ * >= num_keys are skipped; a row with no valid entry is written as zeros.
+ *   q, k: bf16 rows, or fp32 rows with SAF3R_GATHER_QK_FP32 in dtype_flags;
+ *   v: bf16 rows, or fp32 rows with SAF3R_GATHER_V_FP32; out: bf16 rows (the fp32 result rounded
+ *   once), or fp32 rows with SAF3R_GATHER_OUT_FP32. Row strides are in elements of the row's type.
+ *   (The reference upcasts q, k and v to fp32 and stores out in v.dtype: fp16 inputs are passed
+ *   upcast to fp32 exactly, with an fp32 out rounded to fp16 by the caller.)
  *   idx: int32 [n][topk] (row stride topk, or 0 to share one list across rows).
  * Replaces: saf3r/triton/sparse_topk_attention.py:115-166 (fused_sparse_topk_attention) and
  *           :261-286 (the TopK > 2048 variant).
  */
 int saf3r_gather_attn_fwd(const saf3r_rows* q, const saf3r_rows* k, const saf3r_rows* v, const int32_t* idx,
-                          int64_t idx_row_stride, int n, int topk, int64_t num_keys, float scale, int qk_fp32,
+                          int64_t idx_row_stride, int n, int topk, int64_t num_keys, float scale, int dtype_flags,
                           const saf3r_rows* out, void* stream);
 
 /*
- * Per-frame token top-k of q.k (bf16 inputs, fp32 MFMA accumulation).
+ * Per-frame token top-k of q.k (bf16 inputs, fp32 MFMA accumulation), one batch element per call
+ * (the reference's batch dimension B is a loop of calls over q[b], k[b], idx[b]).
  *   q: n_q rows; k: frames*per_frame rows (frame f = rows [f*per_frame, (f+1)*per_frame));
  *   idx: int32 [n_q][frames*min(topk, per_frame)] global key rows, frame-major, score descending,
  *   ties to the lower index. topk >= 1 and min(topk, per_frame) <= 128 (the reference's limit);
- *   above 16 per_frame <= 4096, and the call takes a stream-ordered workspace of at most 1 GiB
- *   (hipMallocAsync / hipFreeAsync on `stream`) for the scores of a chunk of queries.
+ *   above 16 per_frame <= 4096.
+ *   workspace / workspace_bytes: caller-owned device memory for the scores of a chunk of queries,
+ *   used when min(topk, per_frame) > 16 (NULL / 0 otherwise). saf3r_token_topk_workspace_bytes
+ *   gives the size that runs every query in one chunk (at most about 1 GiB); any size of at least
+ *   the scores of 128 queries (frames * roundup(per_frame, 64) * 4 * 128 bytes) works, in more
+ *   chunks. Calls that share a workspace must be ordered (one stream).
  * Replaces: saf3r/triton/fused_qk_topk.py:120-217 (compute_qk_topk_indices_fused).
  */
 int saf3r_token_topk(const saf3r_rows* q, const saf3r_rows* k, int n_q, int frames, int per_frame, int topk,
-                     int32_t* idx, void* stream);
+                     int32_t* idx, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Workspace bytes saf3r_token_topk takes for these sizes in one chunk: 0 when
+ * min(topk, per_frame) <= 16, -1 for sizes saf3r_token_topk rejects. No counterpart in the
+ * reference (its Triton kernel keeps each query's list in registers). */
+int64_t saf3r_token_topk_workspace_bytes(int n_q, int frames, int per_frame, int topk);
 
 /*
  * Token top-k from blocks of bf16 scores: the selection of the non-lazy DINO-feature path.

@@ -12,7 +12,8 @@
 // (dg = l % 8): 8 lanes read a K or V row together (32 bytes each of an fp32 K row, 16 of a bf16
 // row), so one load instruction moves 8 whole rows, and the 8 partial dot products of a row are
 // summed by three DPP steps inside the 8 lanes. Entries < 0 or >= num_keys are skipped. q and k
-// are bf16 or fp32 rows (the reference's kernel upcasts either).
+// are bf16 or fp32 rows (the reference's kernel upcasts either); v and out are bf16 or fp32 rows
+// (the reference writes out in v.dtype from its fp32 accumulator).
 #include "common.h"
 
 namespace saf3r {
@@ -56,8 +57,9 @@ __device__ inline float slots_sum(float x) {
 }
 
 // 4 waves per workgroup, one query row per wave. QK32: q and k rows are fp32 (the reference's gather
-// reads the fp32 q / k of the autocast forward and multiplies in fp32); otherwise bf16.
-template <bool QK32>
+// reads the fp32 q / k of the autocast forward and multiplies in fp32); otherwise bf16. V32 / O32:
+// v / out rows are fp32; otherwise bf16.
+template <bool QK32, bool V32, bool O32>
 __global__ __launch_bounds__(256) void gather_attn_kernel(GatherParams p) {
   const int lane = tid_x() & 63, w = tid_x() >> 6, ks = lane >> 3, dg = lane & 7;
   const int64_t r = (int64_t)bid_x() * 4 + w;
@@ -92,7 +94,8 @@ __global__ __launch_bounds__(256) void gather_attn_kernel(GatherParams p) {
     if (myid >= p.nk) myid = -1;
     // key c0 + 8 it + ks: its score and its V dims
     float s[8];
-    uint32_t vw[8][4];
+    float vf[8][8];     // V32: the V dims of key slot it
+    uint32_t vw[8][4];  // otherwise the same dims as bf16 pairs
 #pragma unroll
     for (int it = 0; it < 8; ++it) {
       const int id = __shfl(myid, 8 * it + ks);
@@ -115,11 +118,21 @@ __global__ __launch_bounds__(256) void gather_attn_kernel(GatherParams p) {
           part = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, kw[e]), __builtin_bit_cast(bf16x2, qw[e]),
                                                  part, false);
       }
-      const u32x4 vx = *reinterpret_cast<const u32x4*>(p.v.row(rid) + 8 * dg);
-      vw[it][0] = vx.x;
-      vw[it][1] = vx.y;
-      vw[it][2] = vx.z;
-      vw[it][3] = vx.w;
+      if constexpr (V32) {
+        const f32x4* v4 = reinterpret_cast<const f32x4*>(p.v.row<float>(rid) + 8 * dg);
+        const f32x4 a = v4[0], b = v4[1];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          vf[it][e] = a[e];
+          vf[it][4 + e] = b[e];
+        }
+      } else {
+        const u32x4 vx = *reinterpret_cast<const u32x4*>(p.v.row(rid) + 8 * dg);
+        vw[it][0] = vx.x;
+        vw[it][1] = vx.y;
+        vw[it][2] = vx.z;
+        vw[it][3] = vx.w;
+      }
       part = sum8(part);
       s[it] = id >= 0 ? part : -__builtin_inff();
     }
@@ -137,10 +150,15 @@ __global__ __launch_bounds__(256) void gather_attn_kernel(GatherParams p) {
     for (int it = 0; it < 8; ++it) {
       const float pj = __builtin_amdgcn_exp2f(__builtin_fmaf(s[it], p.c, -m_use * p.c));
       lsum += pj;
+      if constexpr (V32) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        acc[2 * e] = __builtin_fmaf(pj, bf16_lo(vw[it][e]), acc[2 * e]);
-        acc[2 * e + 1] = __builtin_fmaf(pj, bf16_hi(vw[it][e]), acc[2 * e + 1]);
+        for (int d = 0; d < 8; ++d) acc[d] = __builtin_fmaf(pj, vf[it][d], acc[d]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          acc[2 * e] = __builtin_fmaf(pj, bf16_lo(vw[it][e]), acc[2 * e]);
+          acc[2 * e + 1] = __builtin_fmaf(pj, bf16_hi(vw[it][e]), acc[2 * e + 1]);
+        }
       }
     }
     l_run = l_run * alpha + slots_sum(lsum);
@@ -152,14 +170,20 @@ __global__ __launch_bounds__(256) void gather_attn_kernel(GatherParams p) {
   for (int d = 0; d < 8; ++d) acc[d] = slots_sum(acc[d]);
   if (ks == 0) {
     const float inv = l_run > 0.f ? 1.0f / l_run : 0.f;
-    uint32_t o[4];
+    if constexpr (O32) {
+      float* orow = const_cast<float*>(p.out.row<float>(r)) + 8 * dg;
+      *reinterpret_cast<f32x4*>(orow) = f32x4{acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv};
+      *reinterpret_cast<f32x4*>(orow + 4) = f32x4{acc[4] * inv, acc[5] * inv, acc[6] * inv, acc[7] * inv};
+    } else {
+      uint32_t o[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const bf16x2 pr = {(__bf16)(acc[2 * e] * inv), (__bf16)(acc[2 * e + 1] * inv)};
-      o[e] = __builtin_bit_cast(uint32_t, pr);
+      for (int e = 0; e < 4; ++e) {
+        const bf16x2 pr = {(__bf16)(acc[2 * e] * inv), (__bf16)(acc[2 * e + 1] * inv)};
+        o[e] = __builtin_bit_cast(uint32_t, pr);
+      }
+      __bf16* orow = const_cast<__bf16*>(p.out.row<__bf16>(r));
+      *reinterpret_cast<u32x4*>(orow + 8 * dg) = u32x4{o[0], o[1], o[2], o[3]};
     }
-    __bf16* orow = const_cast<__bf16*>(p.out.row<__bf16>(r));
-    *reinterpret_cast<u32x4*>(orow + 8 * dg) = u32x4{o[0], o[1], o[2], o[3]};
   }
 }
 
@@ -180,15 +204,24 @@ static bool to_dev(const saf3r_rows* s, RowsDev* d, const char* name, bool fp32 
 
 using namespace saf3r;
 
+template <bool QK32, bool V32>
+static void launch_gather(const GatherParams& p, bool o32, dim3 grid, hipStream_t st) {
+  if (o32) hipLaunchKernelGGL((gather_attn_kernel<QK32, V32, true>), grid, dim3(256), 0, st, p);
+  else hipLaunchKernelGGL((gather_attn_kernel<QK32, V32, false>), grid, dim3(256), 0, st, p);
+}
+
 extern "C" int saf3r_gather_attn_fwd(const saf3r_rows* q, const saf3r_rows* k, const saf3r_rows* v,
                                      const int32_t* idx, int64_t idx_row_stride, int n, int topk,
-                                     int64_t num_keys, float scale, int qk_fp32, const saf3r_rows* out,
+                                     int64_t num_keys, float scale, int dtype_flags, const saf3r_rows* out,
                                      void* stream) {
   if (int e = injected("saf3r_gather_attn_fwd")) return e;
   GatherParams p;
-  if (qk_fp32 != 0 && qk_fp32 != 1) return fail(SAF3R_ERR_INVALID, "saf3r_gather_attn_fwd: qk_fp32 must be 0 or 1");
-  if (!to_dev(q, &p.q, "q", qk_fp32) || !to_dev(k, &p.k, "k", qk_fp32) || !to_dev(v, &p.v, "v") ||
-      !to_dev(out, &p.out, "out"))
+  if (dtype_flags & ~(SAF3R_GATHER_QK_FP32 | SAF3R_GATHER_V_FP32 | SAF3R_GATHER_OUT_FP32))
+    return fail(SAF3R_ERR_INVALID, "saf3r_gather_attn_fwd: unknown dtype flags 0x%x", dtype_flags);
+  const bool qk32 = dtype_flags & SAF3R_GATHER_QK_FP32, v32 = dtype_flags & SAF3R_GATHER_V_FP32,
+             o32 = dtype_flags & SAF3R_GATHER_OUT_FP32;
+  if (!to_dev(q, &p.q, "q", qk32) || !to_dev(k, &p.k, "k", qk32) || !to_dev(v, &p.v, "v", v32) ||
+      !to_dev(out, &p.out, "out", o32))
     return SAF3R_ERR_INVALID;
   if (!idx || n < 0 || topk <= 0 || idx_row_stride < 0 || num_keys <= 0 || num_keys > 0x7fffffff)
     return fail(SAF3R_ERR_INVALID, "saf3r_gather_attn_fwd: bad index list");
@@ -200,7 +233,13 @@ extern "C" int saf3r_gather_attn_fwd(const saf3r_rows* q, const saf3r_rows* k, c
   p.nk = num_keys;
   p.c = scale * 1.4426950408889634f;
   const dim3 grid((unsigned)((n + 3) / 4));
-  if (qk_fp32) hipLaunchKernelGGL(gather_attn_kernel<true>, grid, dim3(256), 0, (hipStream_t)stream, p);
-  else hipLaunchKernelGGL(gather_attn_kernel<false>, grid, dim3(256), 0, (hipStream_t)stream, p);
+  hipStream_t st = (hipStream_t)stream;
+  if (qk32) {
+    if (v32) launch_gather<true, true>(p, o32, grid, st);
+    else launch_gather<true, false>(p, o32, grid, st);
+  } else {
+    if (v32) launch_gather<false, true>(p, o32, grid, st);
+    else launch_gather<false, false>(p, o32, grid, st);
+  }
   return check_launch("saf3r_gather_attn_fwd");
 }

@@ -345,8 +345,8 @@ extern "C" int saf3r_probe_scores(const float* q32, const float* k32, int64_t sl
 // ---- allocation-free probe entry ------------------------------------------------------------
 // The partial sums of saf3r_probe_scores_noalloc live in this file-scope device array (one copy per
 // GPU, held until the process ends) instead of a caller workspace. Host code never passes the array's
-// name to a kernel: its device address on the current GPU comes from hipGetSymbolAddress, resolved
-// once per device and kept in scratch_addr. Every chunk sum the finish kernel reads is written by the
+// name to a kernel: its device address on the GPU of the call's stream comes from
+// hipGetSymbolAddress, resolved once per device and kept in scratch_addr. Every chunk sum the finish kernel reads is written by the
 // partial kernel of the same call first, so nothing needs clearing; calls that overlap on one GPU
 // (different streams, or several host threads) share the array and race.
 constexpr int kScratchHeads = 64;
@@ -356,14 +356,28 @@ static __device__ __align__(256) float scratch[kScratchHeads * kProbeChunks * 64
 static std::mutex scratch_mu;
 static float* scratch_addr[kMaxDevices];  // per device, set once
 
-static int scratch_ptr(const char* who, float** out) {
-  int dev = -1;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
-    return fail(SAF3R_ERR_LAUNCH, "%s: no current device (or device id >= %d)", who, kMaxDevices);
+// The array of the device `stream` belongs to (the current device for the NULL stream): each GPU
+// holds its own copy at its own address, which hipGetSymbolAddress reports for the current device,
+// so the lookup runs with that device current and restores the caller's device afterwards.
+static int scratch_ptr(const char* who, hipStream_t stream, float** out) {
+  int cur = -1, dev = -1;
+  if (hipGetDevice(&cur) != hipSuccess || cur < 0)
+    return fail(SAF3R_ERR_LAUNCH, "%s: no current device", who);
+  dev = cur;
+  if (stream) {
+    hipDevice_t sd = -1;
+    if (hipStreamGetDevice(stream, &sd) != hipSuccess || sd < 0)
+      return fail(SAF3R_ERR_INVALID, "%s: the stream's device could not be determined", who);
+    dev = (int)sd;
+  }
+  if (dev >= kMaxDevices) return fail(SAF3R_ERR_UNSUPPORTED, "%s: device id %d >= %d", who, dev, kMaxDevices);
   std::lock_guard<std::mutex> lock(scratch_mu);
   if (!scratch_addr[dev]) {
+    if (dev != cur && hipSetDevice(dev) != hipSuccess)
+      return fail(SAF3R_ERR_LAUNCH, "%s: cannot make device %d current", who, dev);
     void* ptr = nullptr;
     const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (dev != cur) (void)hipSetDevice(cur);
     if (e != hipSuccess || !ptr)
       return fail(SAF3R_ERR_LAUNCH, "%s: hipGetSymbolAddress of the static workspace failed on device %d: %s", who,
                   dev, hipGetErrorString(e));
@@ -387,7 +401,7 @@ extern "C" int saf3r_probe_scores_noalloc(const float* q32, const float* k32, in
     return fail(SAF3R_ERR_UNSUPPORTED, "%s: n_sel %d exceeds the %d heads of the static workspace", who, n_sel,
                 kScratchHeads);
   float* ws = nullptr;
-  if (int e = scratch_ptr(who, &ws)) return e;
+  if (int e = scratch_ptr(who, (hipStream_t)stream, &ws)) return e;
   p.partial = ws;
   return probe_launch(p, n_sel, stream);
 }

@@ -492,30 +492,41 @@ __global__ __launch_bounds__(256) void topk_large_kernel(const float* __restrict
   }
 }
 
-static int token_topk_large(TopkParams p, int n_q, hipStream_t st) {
+// Bytes of one query's stored scores (frames x frame length rounded up to 64, fp32).
+static int64_t large_row_bytes(int frames, int per_frame) { return (int64_t)frames * (64 * ((per_frame + 63) / 64)) * 4; }
+
+// Queries per chunk: a workspace of at most 1 GiB in whole work-groups of 128 queries (at least one).
+static int64_t large_chunk_rows(int n_q, int frames, int per_frame) {
+  int64_t nqc = ((int64_t)1 << 30) / large_row_bytes(frames, per_frame) / 128 * 128;
+  if (nqc < 128) nqc = 128;
+  const int64_t nq128 = ((int64_t)n_q + 127) / 128 * 128;
+  return nqc < nq128 ? nqc : nq128;
+}
+
+// The caller's workspace holds the scores of `nqc` queries at a time (whole work-groups of 128);
+// chunks run one after another on the stream, so one workspace serves every chunk.
+static int token_topk_large(TopkParams p, int n_q, void* workspace, int64_t workspace_bytes, hipStream_t st) {
   const int tiles = (p.P + 63) / 64;
   p.ppad = 64 * tiles;
-  const int64_t row_bytes = (int64_t)p.F * p.ppad * 4;
-  // queries per chunk: a workspace of at most 1 GiB, whole work-groups of 128
-  int64_t nqc = ((int64_t)1 << 30) / row_bytes / 128 * 128;
-  if (nqc < 128) nqc = 128;
+  const int64_t row_bytes = large_row_bytes(p.F, p.P);
+  int64_t nqc = workspace_bytes / row_bytes / 128 * 128;
+  if (!workspace || nqc < 128)
+    return fail(SAF3R_ERR_INVALID,
+                "saf3r_token_topk: min(topk, per_frame) > 16 needs a workspace of at least %lld bytes "
+                "(saf3r_token_topk_workspace_bytes), got %lld",
+                (long long)(128 * row_bytes), (long long)(workspace ? workspace_bytes : 0));
   if (nqc > n_q) nqc = n_q;
-  void* ws = nullptr;
-  if (hipMallocAsync(&ws, (size_t)(nqc * row_bytes), st) != hipSuccess)
-    return fail(SAF3R_ERR_LAUNCH, "saf3r_token_topk: workspace of %lld bytes not available", (long long)(nqc * row_bytes));
-  p.ws = static_cast<float*>(ws);
+  p.ws = static_cast<float*>(workspace);
   const int nv = tiles <= 4 ? 4 : tiles <= 8 ? 8 : tiles <= 12 ? 12 : tiles <= 16 ? 16 : tiles <= 24 ? 24
                  : tiles <= 32 ? 32 : tiles <= 48 ? 48 : 64;
-  int rc = SAF3R_OK;
-  for (int64_t q0 = 0; q0 < n_q && rc == SAF3R_OK; q0 += nqc) {
+  for (int64_t q0 = 0; q0 < n_q; q0 += nqc) {
     const int64_t q1 = q0 + nqc < n_q ? q0 + nqc : n_q;
     p.q_begin = q0;
     p.nq = (int)q1;
     const dim3 g1((unsigned)((q1 - q0 + 127) / 128), (unsigned)p.F);
     if (p.kmode == 2) hipLaunchKernelGGL((token_topk_kernel<1, false, true>), g1, dim3(256), 0, st, p);
     else hipLaunchKernelGGL((token_topk_kernel<1, true, true>), g1, dim3(256), 0, st, p);
-    rc = check_launch("saf3r_token_topk");
-    if (rc != SAF3R_OK) break;
+    if (int rc = check_launch("saf3r_token_topk")) return rc;
     const dim3 g2((unsigned)(((q1 - q0) * p.F + 3) / 4));
     switch (nv) {
       case 4: hipLaunchKernelGGL(topk_large_kernel<4>, g2, dim3(256), 0, st, p.ws, q0, q1, p.F, p.P, p.ppad, p.ke, p.idx); break;
@@ -527,28 +538,40 @@ static int token_topk_large(TopkParams p, int n_q, hipStream_t st) {
       case 48: hipLaunchKernelGGL(topk_large_kernel<48>, g2, dim3(256), 0, st, p.ws, q0, q1, p.F, p.P, p.ppad, p.ke, p.idx); break;
       default: hipLaunchKernelGGL(topk_large_kernel<64>, g2, dim3(256), 0, st, p.ws, q0, q1, p.F, p.P, p.ppad, p.ke, p.idx); break;
     }
-    rc = check_launch("saf3r_token_topk");
+    if (int rc = check_launch("saf3r_token_topk")) return rc;
   }
-  if (hipFreeAsync(ws, st) != hipSuccess && rc == SAF3R_OK)
-    rc = fail(SAF3R_ERR_LAUNCH, "saf3r_token_topk: workspace release failed");
-  return rc;
+  return SAF3R_OK;
 }
 
 }  // namespace saf3r
 
 using namespace saf3r;
 
+// Shape checks shared by saf3r_token_topk and its workspace query.
+static int topk_shape(const char* who, int n_q, int frames, int per_frame, int topk) {
+  if (n_q < 0 || frames <= 0 || per_frame <= 0) return fail(SAF3R_ERR_INVALID, "%s: bad shape", who);
+  if (topk < 1) return fail(SAF3R_ERR_INVALID, "%s: topk must be >= 1", who);
+  const int ke = topk < per_frame ? topk : per_frame;
+  if (ke > 128) return fail(SAF3R_ERR_UNSUPPORTED, "%s: min(topk, per_frame) must be <= 128 (got %d)", who, ke);
+  if (ke > 16 && (per_frame > kLargeMaxP || frames > 65535))
+    return fail(SAF3R_ERR_UNSUPPORTED, "%s: topk > 16 needs per_frame <= %d and frames <= 65535", who, kLargeMaxP);
+  return SAF3R_OK;
+}
+
+extern "C" int64_t saf3r_token_topk_workspace_bytes(int n_q, int frames, int per_frame, int topk) {
+  if (topk_shape("saf3r_token_topk_workspace_bytes", n_q, frames, per_frame, topk)) return -1;
+  const int ke = topk < per_frame ? topk : per_frame;
+  if (ke <= 16 || n_q == 0) return 0;
+  return large_chunk_rows(n_q, frames, per_frame) * large_row_bytes(frames, per_frame);
+}
+
 extern "C" int saf3r_token_topk(const saf3r_rows* q, const saf3r_rows* k, int n_q, int frames, int per_frame,
-                                int topk, int32_t* idx, void* stream) {
+                                int topk, int32_t* idx, void* workspace, int64_t workspace_bytes, void* stream) {
   if (int e = injected("saf3r_token_topk")) return e;
   if (!q || !k || !q->ptr || !k->ptr || !idx) return fail(SAF3R_ERR_INVALID, "saf3r_token_topk: null pointer");
-  if (n_q < 0 || frames <= 0 || per_frame <= 0) return fail(SAF3R_ERR_INVALID, "saf3r_token_topk: bad shape");
-  if (topk < 1) return fail(SAF3R_ERR_INVALID, "saf3r_token_topk: topk must be >= 1");
+  if (int e = topk_shape("saf3r_token_topk", n_q, frames, per_frame, topk)) return e;
   const int ke = topk < per_frame ? topk : per_frame;
-  if (ke > 128) return fail(SAF3R_ERR_UNSUPPORTED, "saf3r_token_topk: min(topk, per_frame) must be <= 128 (got %d)", ke);
-  if (ke > 16 && (per_frame > kLargeMaxP || frames > 65535))
-    return fail(SAF3R_ERR_UNSUPPORTED, "saf3r_token_topk: topk > 16 needs per_frame <= %d and frames <= 65535",
-                kLargeMaxP);
+  if (workspace_bytes < 0) return fail(SAF3R_ERR_INVALID, "saf3r_token_topk: negative workspace size");
   if (q->row_stride % 8 || k->row_stride % 8 || ((uintptr_t)q->ptr | (uintptr_t)k->ptr) % 16 ||
       q->rows_per_frame <= 0 || k->rows_per_frame <= 0)
     return fail(SAF3R_ERR_INVALID, "saf3r_token_topk: rows must be 16-byte aligned, row stride %% 8");
@@ -578,7 +601,7 @@ extern "C" int saf3r_token_topk(const saf3r_rows* q, const saf3r_rows* k, int n_
   p.ppad = 0;
   p.fgroups = 1;
   hipStream_t st = (hipStream_t)stream;
-  if (ke > 16) return token_topk_large(p, n_q, st);
+  if (ke > 16) return token_topk_large(p, n_q, workspace, workspace_bytes, st);
   if (p.ke <= 1) return launch_topk<1>(p, st);
   if (p.ke <= 2) return launch_topk<2>(p, st);
   if (p.ke <= 4) return launch_topk<4>(p, st);

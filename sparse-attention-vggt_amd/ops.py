@@ -360,57 +360,109 @@ def rows(t: torch.Tensor, row_stride: int | None = None, base_row: int = 0, rows
 def gather_attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, idx: torch.Tensor,
                     scale: float | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
     """``fused_sparse_topk_attention`` (``saf3r/triton/sparse_topk_attention.py:115-166``):
-    q [N, 64], k/v [Nk, 64], idx int32 [N, TopK] (a stride-0 row view shares one list). fp32 q and k
-    are read as fp32 (as the reference's kernel upcasts them); other dtypes are taken as bf16."""
+    q [N, 64], k [Nk, 64], v [Nk, 64], idx int32 [N, TopK] (a stride-0 row view shares one list)
+    -> out [N, 64] in ``v.dtype``. As the reference's kernel, q, k and v are used as fp32 (upcast
+    exactly) and the fp32 result is rounded once to ``v.dtype``; bf16 rows are read as they are.
+    head_dim and the value dim must be 64 (the reference autotunes any D; this build raises)."""
     _need_cuda(q, k, v, idx)
+    if q.dim() != 2 or k.dim() != 2 or v.dim() != 2 or idx.dim() != 2:
+        raise ValueError("q, k, v and kv_indices must be 2-D")
     n, d = q.shape
-    if d != HEAD_DIM:
-        raise ValueError("head_dim must be 64")
-    f32 = q.dtype == torch.float32 and k.dtype == torch.float32
-    qk_t = torch.float32 if f32 else torch.bfloat16
+    if d != HEAD_DIM or k.shape[1] != HEAD_DIM or v.shape[1] != HEAD_DIM:
+        raise ValueError(f"head_dim and value dim must be {HEAD_DIM} (got q {d}, k {k.shape[1]}, v {v.shape[1]})")
+    if k.shape[0] != v.shape[0]:
+        raise ValueError("k and v must hold the same number of rows")
+    if idx.shape[0] != n:
+        raise ValueError("kv_indices must have one row per query")
+    floats = (torch.float32, torch.float16, torch.bfloat16)
+    if q.dtype not in floats or k.dtype not in floats or v.dtype not in floats:
+        raise TypeError("q, k and v must be float32, float16 or bfloat16")
+    qk32 = not (q.dtype == torch.bfloat16 and k.dtype == torch.bfloat16)
+    qk_t = torch.float32 if qk32 else torch.bfloat16
     q, k = (t.to(qk_t).contiguous() for t in (q, k))
-    v = v.to(torch.bfloat16).contiguous()
+    out_dtype = v.dtype
+    v32 = out_dtype != torch.bfloat16  # fp32 rows (fp16 upcast exactly), fp32 result rounded here
+    res_t = torch.float32 if v32 else torch.bfloat16
+    v = v.to(res_t).contiguous()
     if idx.stride(-1) != 1:
         idx = idx.contiguous()
     idx = idx.to(torch.int32)
-    if out is None:
-        out = torch.empty(n, v.shape[1], dtype=torch.bfloat16, device=q.device)
-    return gather_attn_rows(rows(q), rows(k), rows(v), idx, idx.stride(0), n, idx.shape[1], k.shape[0], scale,
-                            rows(out), out, qk_fp32=f32)
+    direct = out is not None and out.dtype == res_t and out.shape == (n, HEAD_DIM) and out.stride(-1) == 1
+    res = out if direct else torch.empty(n, HEAD_DIM, dtype=res_t, device=q.device)
+    flags = ((_lib.GATHER_QK_FP32 if qk32 else 0) | (_lib.GATHER_V_FP32 | _lib.GATHER_OUT_FP32 if v32 else 0))
+    gather_attn_rows(rows(q), rows(k), rows(v), idx, idx.stride(0), n, idx.shape[1], k.shape[0], scale, rows(res),
+                     dtype_flags=flags)
+    if out is not None and not direct:
+        out.copy_(res)
+        return out
+    return res if res.dtype == out_dtype else res.to(out_dtype)
 
 
-def gather_attn_rows(qr, kr, vr, idx, idx_row_stride, n, topk, num_keys, scale, outr, keep=None, qk_fp32=False):
-    """``saf3r_gather_attn_fwd`` on row descriptors; ``qk_fp32``: q and k rows are fp32."""
+def gather_attn_rows(qr, kr, vr, idx, idx_row_stride, n, topk, num_keys, scale, outr, keep=None, qk_fp32=False,
+                     dtype_flags=None):
+    """``saf3r_gather_attn_fwd`` on row descriptors; ``qk_fp32``: q and k rows are fp32 (or give the
+    full ``dtype_flags``)."""
     lib = _lib.load()
     scale = 1.0 / math.sqrt(HEAD_DIM) if scale is None else scale
+    flags = (_lib.GATHER_QK_FP32 if qk_fp32 else 0) if dtype_flags is None else dtype_flags
     _mark("gather_attn", "start")
     _lib.check(lib.saf3r_gather_attn_fwd(ctypes.byref(qr), ctypes.byref(kr), ctypes.byref(vr), _ptr(idx),
-                                         idx_row_stride, n, topk, num_keys, float(scale), int(bool(qk_fp32)),
+                                         idx_row_stride, n, topk, num_keys, float(scale), int(flags),
                                          ctypes.byref(outr), _lib.stream_ptr()))
     _mark("gather_attn", "end")
     return keep
 
 
+def token_topk_workspace_bytes(n_q: int, frames: int, per_frame: int, topk: int) -> int:
+    """Bytes of the score workspace ``saf3r_token_topk`` takes for these sizes (0 for top-k <= 16)."""
+    nbytes = _lib.load().saf3r_token_topk_workspace_bytes(n_q, frames, per_frame, topk)
+    if nbytes < 0:
+        _lib.check(_lib.SAF3R_ERR_INVALID)  # raises with the library's message
+    return int(nbytes)
+
+
 def token_topk(q: torch.Tensor, k: torch.Tensor, frames: int, per_frame: int, topk: int,
-               qrows: _lib.Rows | None = None, krows: _lib.Rows | None = None, n_q: int | None = None):
-    """``compute_qk_topk_indices_fused`` (``saf3r/triton/fused_qk_topk.py:120-217``) for one batch:
-    q [Nq, 64], k [frames*per_frame, 64] bf16 -> int32 [Nq, frames*min(topk, per_frame)]."""
-    _need_cuda(q, k)
+               qrows: _lib.Rows | None = None, krows: _lib.Rows | None = None, n_q: int | None = None,
+               workspace: torch.Tensor | None = None):
+    """``compute_qk_topk_indices_fused`` (``saf3r/triton/fused_qk_topk.py:120-217``):
+    q [Nq, 64], k [frames*per_frame, 64] -> int32 [Nq, frames*min(topk, per_frame)], or with a batch
+    dimension q [B, Nq, 64], k [B, frames*per_frame, 64] -> [B, Nq, frames*min(topk, per_frame)]
+    (one call per batch element, as the reference's grid dimension 1 runs them; ``:187``). q and k
+    are rounded to bf16, as the reference's kernel multiplies bf16 tiles. Above top-16 the score
+    workspace is a torch allocation of ``token_topk_workspace_bytes`` (or ``workspace``)."""
+    _need_cuda(q, k) if qrows is None or krows is None else _need_cuda(q)
+    if qrows is None and krows is None and q.dim() == 3:
+        if k is None or k.dim() != 3 or k.shape[0] != q.shape[0]:
+            raise ValueError("batched q needs k of the same batch size")
+        ws = workspace
+        if ws is None:
+            nbytes = token_topk_workspace_bytes(q.shape[1], frames, per_frame, topk)
+            ws = torch.empty(nbytes, dtype=torch.uint8, device=q.device) if nbytes else None
+        return torch.stack([token_topk(q[b], k[b], frames, per_frame, topk, workspace=ws)
+                            for b in range(q.shape[0])])
     lib = _lib.load()
     if qrows is None:
+        if q.dim() != 2 or q.shape[-1] != HEAD_DIM:
+            raise ValueError(f"q must be [Nq, {HEAD_DIM}] or [B, Nq, {HEAD_DIM}]")
         q = q.to(torch.bfloat16).contiguous()
         qrows = rows(q)
         n_q = q.shape[0]
     if krows is None:
+        if k.dim() != 2 or k.shape[-1] != HEAD_DIM:
+            raise ValueError(f"k must be [Nk, {HEAD_DIM}] like q")
         k = k.to(torch.bfloat16).contiguous()
         if k.shape[0] != frames * per_frame:
             raise ValueError("k must hold frames * per_frame rows")
         krows = rows(k)
     ke = min(topk, per_frame)
     idx = torch.empty(n_q, frames * ke, dtype=torch.int32, device=q.device)
+    if workspace is None:
+        nbytes = token_topk_workspace_bytes(n_q, frames, per_frame, topk)
+        workspace = torch.empty(nbytes, dtype=torch.uint8, device=q.device) if nbytes else None
     _mark("token_topk", "start")
     _lib.check(lib.saf3r_token_topk(ctypes.byref(qrows), ctypes.byref(krows), n_q, frames, per_frame, topk,
-                                    _ptr(idx), _lib.stream_ptr()))
+                                    _ptr(idx), _ptr(workspace), 0 if workspace is None else workspace.numel(),
+                                    _lib.stream_ptr()))
     _mark("token_topk", "end")
     return idx
 

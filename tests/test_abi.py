@@ -24,7 +24,7 @@ def test_library_exports_every_declared_symbol(pkg):
     for n in names:
         assert hasattr(lib, n), n
     assert set(names) == set(lib_mod.EXPORTS)
-    assert lib.saf3r_abi_version() == lib_mod.ABI_VERSION == 9
+    assert lib.saf3r_abi_version() == lib_mod.ABI_VERSION == 10
 
 
 def test_packed_slots_matches_layout(pkg):
@@ -115,14 +115,32 @@ def test_invalid_arguments_fail_before_launch(pkg):
     assert rc == 2 and b"static workspace" in lib.saf3r_last_error()
     rows = L.Rows(16, 64, 0, 1 << 40, 0)
     rc = lib.saf3r_gather_attn_fwd(ctypes.byref(rows), ctypes.byref(rows), ctypes.byref(rows), dev, 4, 1, 4, 10, 0.125,
-                                   2, ctypes.byref(rows), None)
-    assert rc == 1 and b"qk_fp32" in lib.saf3r_last_error()
+                                   8, ctypes.byref(rows), None)
+    assert rc == 1 and b"dtype flags" in lib.saf3r_last_error()
+    # fp32 V / out rows (dtype flags 2 and 4) need a row stride % 4
+    rc = lib.saf3r_gather_attn_fwd(ctypes.byref(rows), ctypes.byref(rows), ctypes.byref(rows6 := L.Rows(16, 6, 0, 1 << 40, 0)),
+                                   dev, 4, 1, 4, 10, 0.125, 2, ctypes.byref(rows), None)
+    assert rc == 1 and b"v must be" in lib.saf3r_last_error()
+    rc = lib.saf3r_gather_attn_fwd(ctypes.byref(rows), ctypes.byref(rows), ctypes.byref(rows), dev, 4, 1, 4, 10, 0.125,
+                                   4, ctypes.byref(rows6), None)
+    assert rc == 1 and b"out must be" in lib.saf3r_last_error()
     rows6 = L.Rows(16, 6, 0, 1 << 40, 0)  # fp32 rows need a row stride % 4, bf16 rows % 8
     rc = lib.saf3r_gather_attn_fwd(ctypes.byref(rows6), ctypes.byref(rows6), ctypes.byref(rows), dev, 4, 1, 4, 10,
                                    0.125, 1, ctypes.byref(rows), None)
     assert rc == 1 and b"row stride % 4" in lib.saf3r_last_error()
     rc = lib.saf3r_block_select(ctypes.c_void_p(16), ctypes.c_void_p(16), 1, 4, 2, 2, 33, 0, ctypes.c_void_p(16), None)
     assert rc == 2  # k beyond the supported range
+    # token top-k above k = 16 takes the caller's workspace: none, or one too small for 128 queries, fails
+    krows = L.Rows(16, 64, 0, 1 << 40, 0)
+    rc = lib.saf3r_token_topk(ctypes.byref(krows), ctypes.byref(krows), 100, 2, 50, 32, dev, None, 0, None)
+    assert rc == 1 and b"workspace" in lib.saf3r_last_error()
+    rc = lib.saf3r_token_topk(ctypes.byref(krows), ctypes.byref(krows), 100, 2, 50, 32, dev, dev, 2 * 64 * 4 * 127,
+                              None)
+    assert rc == 1 and b"at least 65536 bytes" in lib.saf3r_last_error()
+    rc = lib.saf3r_token_topk(ctypes.byref(krows), ctypes.byref(krows), 100, 2, 50, 32, dev, dev, -1, None)
+    assert rc == 1 and b"negative" in lib.saf3r_last_error()
+    rc = lib.saf3r_token_topk(ctypes.byref(krows), ctypes.byref(krows), 100, 2, 200, 129, dev, None, 0, None)
+    assert rc == 2 and b"128" in lib.saf3r_last_error()
     rc = lib.saf3r_pack_qkv(None, None, None, 64, 64, 0, 10, 1, 1, None, None, None, None, 1e-5, 0, None, None,
                             None, 0, None, None, None, None, None, None, None, 1.0, None)
     assert rc == 1 and b"geometry" in lib.saf3r_last_error()
@@ -154,6 +172,26 @@ def test_invalid_arguments_fail_before_launch(pkg):
         L.check(1)
 
 
+def test_token_topk_workspace_size_query(pkg):
+    """The score workspace of the top-k > 16 path: rows of frames x roundup(per_frame, 64) fp32
+    scores for whole work-groups of 128 queries, at most 1 GiB (one chunk), 0 for top-k <= 16."""
+    from importlib import import_module
+    lib = import_module(pkg.__name__ + "._lib").load()
+    ws = lib.saf3r_token_topk_workspace_bytes
+    row = 128 * 1408 * 4  # 128 frames x 1369 patches, padded to 1408
+    assert ws(175232, 128, 1369, 4) == 0
+    assert ws(175232, 128, 1369, 16) == 0
+    assert ws(175232, 128, 1369, 17) == (2 ** 30 // row // 128 * 128) * row == 1408 * row
+    assert ws(175232, 128, 1369, 17) <= 2 ** 30
+    assert ws(100, 2, 50, 32) == 128 * 2 * 64 * 4  # min(32, 50) > 16: one work-group of 128 queries
+    assert ws(100, 2, 10, 32) == 0  # min(32, 10) = 10 <= 16
+    assert ws(300, 3, 100, 64) == 384 * 3 * 128 * 4
+    assert ws(0, 3, 100, 64) == 0
+    assert ws(100, 2, 200, 129) == -1  # beyond the reference's limit of 128
+    assert ws(100, 2, 5000, 32) == -1  # frames above 4096 keys on the k > 16 path
+    assert ws(-1, 2, 50, 4) == -1
+
+
 def test_fault_injection_is_reported(pkg, monkeypatch):
     from importlib import import_module
     lib = import_module(pkg.__name__ + "._lib").load()
@@ -177,3 +215,19 @@ def test_geometry_derived_sizes(pkg):
     assert (g5.blocks_per_frame, g5.num_blocks, g5.tokens) == (21, 2016, 124896)
     with pytest.raises(ValueError):
         pkg.Geometry.from_tokens(100, 30)
+
+
+def test_kernel_binding_validates_before_any_gpu_call(pkg):
+    """The reference-signature binding raises ValueError for CPU tensors and malformed shapes."""
+    from importlib import import_module
+    import torch
+    kb = import_module(pkg.__name__ + ".kernel_binding")
+    q = torch.randn(4, 64)
+    with pytest.raises(ValueError, match="GPU"):
+        kb.fused_sparse_topk_attention(q, q, q, torch.zeros(4, 2, dtype=torch.int32))
+    with pytest.raises(ValueError, match="num_toks_per_img"):
+        kb.compute_qk_topk_indices_fused(q[None], q[None], 2, None)
+    with pytest.raises(ValueError, match="agree"):
+        kb.compute_qk_topk_indices_fused(q[None], q[None].expand(2, 4, 64), 2, 2)
+    with pytest.raises(ValueError, match="GPU"):
+        kb.compute_qk_topk_indices_fused(q[None], q[None], 2, 2)
