@@ -6,6 +6,7 @@ attention in fp64 and the output projection, and compares the layer output the w
 """
 import importlib
 
+import numpy as np
 import torch
 
 from oracle import attention as OA
@@ -109,6 +110,71 @@ def check_layer_output(w, x, pos, y, geom, ops, li, tol=(2e-2, 2e-3)):
     print(f"layer {li}: max {mx:.3g} mean {mean:.3g} (|y| max {ymax:.3g}, mean {ymean:.3g})", flush=True)
     assert mx <= tol[0] + ymax * 2 ** -8 and mean <= tol[1] + ymean * 2 ** -8, (li, mx, mean)
     return mx, mean
+
+
+def rows_of(packed, geom, tokens, head):
+    """Rows of ``tokens`` of one head from packed [H, L, 64] Q or K (the padded layout)."""
+    slot = torch.full((geom.tokens,), -1, dtype=torch.long)
+    toks = slot_tokens(geom.frames, geom.tokens_per_frame, geom.num_special)
+    valid = toks >= 0
+    slot[toks[valid]] = torch.arange(len(toks))[valid]
+    return packed[head][slot[tokens].to(packed.device)].float().cpu()
+
+
+def sample_rows(geom, n_random, seed):
+    """Query rows for a sampled check: frame 0's specials, the end of frame 0 and the start of frame 1
+    (special and patch rows), the first 70 rows of the last frame, and ``n_random`` random rows."""
+    T, N = geom.tokens_per_frame, geom.tokens
+    rng = torch.Generator().manual_seed(seed)
+    return torch.unique(torch.cat([torch.arange(5), torch.arange(T - 64, T + 5), torch.arange(N - T, N - T + 70),
+                                   torch.randint(0, N, (n_random,), generator=rng)]))
+
+
+def check_sampled_rows(w, x, pos, y, geom, ops, rows, what, tol=(2e-2, 2e-3)):
+    """A block-pattern layer (dense / frame-local / anchor+local / block top-k heads) at full size,
+    checked on sampled rows: q / k / v recomputed by the packing in the padded layout (deterministic),
+    every block list bit-exact against the oracle's selection from the same packed q / k, the attention
+    of ``rows`` against the oracle's masked fp64 attention, and y on those rows through the projection."""
+    N, dim, H = geom.tokens, w.orig_module.qkv.in_features, w.num_heads
+    om = w.orig_module
+    qkv = om.qkv(x).reshape(N, 3 * dim).contiguous()
+    qs = w.q_scaled_heads()  # Q as the wrapper packed it (softmax scale folded in)
+    qp, kp, _ = ops.pack_qkv(qkv, qkv[:, dim:], qkv[:, 2 * dim:], 3 * dim, 64, geom, H,
+                             ln_q=(om.q_norm.weight, om.q_norm.bias), ln_k=(om.k_norm.weight, om.k_norm.bias),
+                             pos=pos[0], rope_base=100.0, q_scaled=qs)  # every head padded, for reading back
+    torch.cuda.synchronize()
+    toks_all = torch.arange(N)
+    T, F_ = geom.tokens_per_frame, geom.frames
+    sel_of = {}
+    bits = lambda t: t.contiguous().view(torch.int16).numpy().view(np.uint16)
+    for i, h in enumerate(w.dyn_heads):
+        qh = rows_of(qp, geom, toks_all, h).to(torch.bfloat16)
+        kh = rows_of(kp, geom, toks_all, h).to(torch.bfloat16)
+        want = OS.block_select(bits(qh), bits(kh), F_, T, geom.num_special, w.layer_block_topk)
+        assert np.array_equal(w.last_selection[i].cpu().numpy(), want), f"{what}: block list of head {h}"
+        sel_of[h] = torch.from_numpy(want)
+    print(f"{what}: {len(sel_of)} block lists bit-exact", flush=True)
+    og = OA.Geometry(F_, T, geom.num_special)
+    attn = torch.empty(len(rows), H, 64, dtype=torch.float64)
+    vnat = qkv[:, 2 * dim:].reshape(N, H, 64)
+    c = ops.prescale_factor()
+    for h, pat in enumerate(w.patterns):
+        qh = rows_of(qp, geom, rows, h) / (c if qs[h] else 1.0)
+        kh = rows_of(kp, geom, toks_all, h)
+        vh = vnat[:, h].float().cpu()
+        mask = OA.allowed_mask(pat, rows, og, sel_of.get(h))
+        attn[:, h] = OA.masked_attention(qh, kh, vh, mask, dtype=torch.float64)
+    got_attn = w.last_attention[rows.to(x.device)].float().cpu().reshape(len(rows), H, 64)
+    amx, amean = err(got_attn, attn)
+    print(f"{what}: attention on {len(rows)} rows: max {amx:.3g} mean {amean:.3g}", flush=True)
+    assert amx <= tol[0] and amean <= tol[1], (what, amx, amean)
+    a = attn.reshape(len(rows), dim).to(torch.bfloat16).double()
+    yref = a @ om.proj.weight.double().cpu().T + om.proj.bias.double().cpu()
+    mx, mean = err(y[rows.to(x.device)].cpu(), yref)
+    ymax, ymean = yref.abs().max().item(), yref.abs().mean().item()
+    print(f"{what}: y on {len(rows)} rows: max {mx:.3g} mean {mean:.3g} (|y| max {ymax:.3g})", flush=True)
+    assert mx <= tol[0] + ymax * 2 ** -8 and mean <= tol[1] + ymean * 2 ** -8, (what, mx, mean)
+    return amx, amean
 
 
 def check_layer(w, x, pos, geom, ops, li):

@@ -203,3 +203,47 @@ def test_aggregator_non_square_input_and_sdpa_frames(mods, pkg):
     with torch.no_grad():
         for li, (x, pos, y) in rec["layers"].items():
             check_layer_output(m.aggregator.global_blocks[li].attn, x, pos, y[0], geom, ops, li)
+
+
+def test_aggregator_vggt1b_width_4_frames(mods, pkg):
+    """The aggregator at VGGT-1B width (dim 1024, 16 heads, 518 x 518 frames: 37 x 37 patches, 1374 tokens
+    per frame), 4 frames blurred with sigma 4 as the benchmark's aggregator leg, depth 2 (DINO depth 2),
+    every global-attention mode across the two layers (lazy dino top-4 first computed in layer 0 and
+    shared with layer 1): each global layer's output inside the forward against the oracle layer."""
+    plug, agg, ops = mods
+    torch.manual_seed(5)
+    m = agg.VGGTAggregatorModel(img_size=518, embed_dim=1024, depth=2, num_heads=16, dino_depth=2, dino_dim=1024,
+                                dino_heads=16, frame_attention="saf3r")
+    for b in m.aggregator.global_blocks:
+        for n in (b.attn.q_norm, b.attn.k_norm):
+            torch.nn.init.uniform_(n.weight, 0.5, 1.5)
+            torch.nn.init.normal_(n.bias, std=0.1)
+    m = m.to(DEV).to(torch.bfloat16)
+    cfg = {"patch_module": {"type": "headsparse", "topk_mode": "token", "lazy_dino_topk": True, "topk": 4,
+                            "block_topk": 4},
+           "sparse_config": {
+               "0": [{"mode": "dino_topk", "head_ids": [0], "is_first_dino": True},
+                     {"mode": "block_topk", "head_ids": [1, 2, 3, 4]}, {"mode": "frame_local", "head_ids": [5]},
+                     {"mode": "anchor_local", "head_ids": [6]}, {"mode": "dense", "head_ids": [7]},
+                     {"mode": "q_probe_topk", "head_ids": [8], "stride": 4},
+                     {"mode": "stride", "head_ids": [9], "stride": 8, "include_as": True},
+                     {"mode": "global_to_frame", "head_ids": [10]}, {"mode": "all_to_first", "head_ids": [11]},
+                     {"mode": "broadcast_first", "head_ids": [12]}, {"mode": "skip", "head_ids": [13]}],
+               "1": [{"mode": "dino_topk", "head_ids": [0, 1, 2]}, {"mode": "block_topk", "head_ids": [3, 4, 5]},
+                     {"mode": "q_probe_topk", "head_ids": [6], "topk": 600, "include_as": True},
+                     {"mode": "anchor_local", "head_ids": [7, 8]}, {"mode": "frame_local", "head_ids": [9]}]}}
+    plug.patch_model(m, "vggt", cfg)
+    rec, hooks = _capture(m)
+    imgs = agg.blurred_frames(4, size=518, sigma=4.0, seed=6)
+    try:
+        outs, start = _run(m, plug, imgs)
+    finally:
+        for h in hooks:
+            h.remove()
+    assert start == 5 and outs[0].shape == (1, 4, 1374, 2048)
+    geom = pkg.Geometry(4, 1374, 5)
+    with torch.no_grad():
+        for li, (x, pos, y) in rec["layers"].items():
+            w = m.aggregator.global_blocks[li].attn
+            print(f"VGGT-1B-width aggregator, global layer {li}", flush=True)
+            check_layer_output(w, x, pos, y[0], geom, ops, li)

@@ -211,3 +211,53 @@ def test_broadcast_first_in_one_launch(ops, pkg, F, T, ns):
         print(f"F{F} T{T} head {h} pattern {pat}: max {err.max().item():.3g} mean {err.mean().item():.3g}", flush=True)
         assert err.max().item() <= ATOL_MAX and err.mean().item() <= ATOL_MEAN
 
+
+
+@pytest.mark.parametrize("phase", ["fixed", "paced"])
+def test_keyset_broadcast_prescaled_out_of_range(ops, pkg, phase):
+    """KEYSET, BROADCAST and TOKEN_DYNAMIC_KEYSET heads with the softmax scale packed into Q, whose
+    scores leave the range of the walk without a running maximum: outlier keys 69 and 173 log2 units
+    above the rest in frame 0 (heads 0-2: a partial row sum beyond 2^64), and every score about 72 units
+    below 0 (heads 3-5: row sums below 2^-64). The fixup launch must find the marked items of these
+    walks too; every written row matches the oracle in both walk orders."""
+    geom = pkg.Geometry(3, 155, 5)
+    P = ops
+    patterns = [P.KEYSET, P.BROADCAST, P.TOKEN_DYNAMIC_KEYSET, P.KEYSET, P.BROADCAST, P.TOKEN_DYNAMIC_KEYSET]
+    H, N, T = len(patterns), geom.tokens, geom.tokens_per_frame
+    g = torch.Generator().manual_seed(16)
+    q = (0.5 + 0.1 * torch.randn(H, N, 64, generator=g)).to(torch.bfloat16)
+    k = (0.3 * torch.randn(H, N, 64, generator=g)).to(torch.bfloat16)
+    v = torch.randn(H, N, 64, generator=g).to(torch.bfloat16)
+    k[:3, 40] = 12.0   # frame-0 tokens 40 and 100: members of every key set below (stride 4 from 0, or frame 0)
+    k[:3, 100] = 30.0
+    q[3:] = (2.5 + 0.05 * torch.randn(3, N, 64, generator=g)).to(torch.bfloat16)
+    k[3:] = (-2.5 + 0.05 * torch.randn(3, N, 64, generator=g)).to(torch.bfloat16)
+    flags = [True] * H
+    qp, kp, vp = ops.pack_heads(q.to(DEV), k.to(DEV), v.to(DEV), geom, q_scaled=flags)
+    specs = [ops.KeySetSpec(0, ops.KEYSET_STRIDE, 3, 1, True), ops.KeySetSpec(2, ops.KEYSET_STRIDE, 4, 0, False),
+             ops.KeySetSpec(3, ops.KEYSET_STRIDE, 3, 1, True), ops.KeySetSpec(5, ops.KEYSET_STRIDE, 4, 0, False)]
+    idx, count = ops.keyset_build(specs, geom, None, DEV)
+    vnat = v.permute(1, 0, 2).contiguous().to(DEV)
+    ks = ops.keyset_gather(kp, geom, specs, vnat, H * 64, 64, idx, count)
+    bc = ops.broadcast_gather(qp, kp, geom, [1, 4], vnat, H * 64, 64)
+    out = torch.zeros(N, H * 64, dtype=torch.bfloat16, device=DEV)
+    for _ in range(2 if phase == "paced" else 1):  # paced: the second call paces by measured step times
+        ops.sparse_attn_fwd(qp, kp, vp, geom, patterns, keysets=ks, broadcast=bc, out=out, q_scaled=flags,
+                            order=phase)
+    torch.cuda.synchronize()
+    c = ops.prescale_factor()
+    q_used = (q.float() * c).to(torch.bfloat16).float() / c  # the packed Q in unscaled units
+    og = OA.Geometry(3, 155, 5)
+    got = out.float().cpu().reshape(N, H, 64).permute(1, 0, 2)
+    assert torch.isfinite(got).all()
+    ks_of = {s.head: idx[i, :int(count[i])].cpu() for i, s in enumerate(specs)}
+    assert all(40 in ks_of[h].tolist() and 100 in ks_of[h].tolist() for h in (0, 2))
+    special = torch.tensor([f * T + s for f in range(3) for s in range(5)])
+    for h, pat in enumerate(patterns):
+        ref_pat = P.KEYSET if pat == P.TOKEN_DYNAMIC_KEYSET else pat
+        ref = OA.sparse_attention_gathered(q_used[h], k[h].float(), v[h].float(), ref_pat, og, ks_of.get(h),
+                                           dtype=torch.float64)
+        rows = special if pat == P.TOKEN_DYNAMIC_KEYSET else torch.arange(N)  # its patch rows are the gather's
+        e = (got[h][rows] - ref[rows].float()).abs()
+        print(f"{phase} head {h} pattern {pat}: max {e.max().item():.3g} mean {e.mean().item():.3g}", flush=True)
+        assert e.max().item() <= ATOL_MAX and e.mean().item() <= ATOL_MEAN

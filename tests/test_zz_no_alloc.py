@@ -59,8 +59,39 @@ def test_noalloc_probe_matches_workspace_entry(mods, pkg, order):
 
 
 def test_noalloc_probe_rejects_more_heads_than_the_workspace(mods, pkg):
+    """65 heads exceed the static workspace's 64: rejected before any launch. Every buffer is a real
+    device tensor of the size the call describes, so that a rejection that stopped working would show
+    as a wrong status, not as an access to an invalid address."""
     ops, L = mods
     lib = L.load()
-    dev = ctypes.c_void_p(16)
-    rc = lib.saf3r_probe_scores_noalloc(dev, dev, 200 * 64, 200, dev, 65, None, 0, 0.125, dev, dev, 200, None)
+    n_sel, n_tok = 65, 64
+    qk32 = torch.zeros(n_sel, 2, n_tok, 64, device=DEV)
+    slots = torch.arange(n_sel, dtype=torch.int32, device=DEV)
+    qbar = torch.zeros(n_sel, 64, device=DEV)
+    scores = torch.zeros(n_sel, n_tok, device=DEV)
+    torch.cuda.synchronize()
+    rc = lib.saf3r_probe_scores_noalloc(ctypes.c_void_p(qk32.data_ptr()), ctypes.c_void_p(qk32[:, 1].data_ptr()),
+                                        qk32.stride(0), n_tok, ctypes.c_void_p(slots.data_ptr()), n_sel, None, 0,
+                                        0.125, ctypes.c_void_p(qbar.data_ptr()), ctypes.c_void_p(scores.data_ptr()),
+                                        scores.stride(0), L.stream_ptr())
+    torch.cuda.synchronize()
     assert rc == 2 and b"static workspace" in lib.saf3r_last_error()
+    assert (qbar == 0).all() and (scores == 0).all()  # nothing was launched
+
+
+def test_noalloc_probe_on_a_side_stream(mods, pkg):
+    """On a non-default stream the entry resolves its workspace from the stream's device
+    (hipStreamGetDevice): the same results as the workspace entry on that stream."""
+    ops, L = mods
+    lib = L.load()
+    g = torch.Generator().manual_seed(31)
+    N, slots = 3 * 155, [2, 0]
+    qk32 = (torch.randn(3, 2, N, 64, generator=g) * 2).to(DEV)
+    side = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(side):
+        assert L.stream_ptr().value  # a real stream handle, not the NULL stream
+        want_q, want_s = _probe(lib, L, False, qk32, slots, None)
+        got_q, got_s = _probe(lib, L, True, qk32, slots, None)
+    assert np.array_equal(got_q.numpy().view(np.uint32), want_q.numpy().view(np.uint32))
+    assert np.array_equal(got_s.numpy().view(np.uint32), want_s.numpy().view(np.uint32))
