@@ -58,12 +58,14 @@ class EventRecorder:
         return {k: [a.elapsed_time(b) for a, b in v] for k, v in self.pairs.items()}
 
 
-def layer_config(layers, heads, seed_base, synth, ops):
+def layer_config(layers, heads, seed_base, synth, ops, table_fn=None):
+    """Head-profile config with one seeded block-pattern table per layer (seed ``seed_base + layer``)."""
     names = {ops.BLOCK_DYNAMIC: "block_topk", ops.FRAME_LOCAL: "frame_local", ops.ANCHOR_LOCAL: "anchor_local",
              ops.DENSE: "dense"}
+    table_fn = table_fn or synth.seeded_patterns
     cfg, tables = {}, []
     for li in range(layers):
-        table = synth.seeded_patterns(heads, seed=seed_base + li)
+        table = table_fn(heads, seed=seed_base + li)
         tables.append(table)
         groups = {}
         for h, p in enumerate(table):
@@ -389,6 +391,179 @@ def measured_traffic(kernel="sparse_attn_kernel"):
     return int(m.group(1)) if m else None
 
 
+def run_stack(pkg, frames, dim, heads, grid, layers, topk, table_fn, steps, warmup, sparse_cfg=None):
+    """The patched global-attention layers of a VGGT-style model on one GPU: ``layers`` layers of
+    GlobalAttentionStack(dim, heads) with random-init bf16 weights (seed 0), N(0,1) input tokens (seed 0)
+    of ``frames`` frames x (5 + grid^2) tokens, head tables ``table_fn(heads, seed=1 + layer)`` (or the
+    head-profile ``sparse_cfg``), block top-``topk``. One step = every layer on the same input, after
+    ``update_args_per_forward`` (a new forward). ``warmup`` untimed steps, then ``steps`` timed steps
+    between two device synchronisations; stream events bracket every kernel launch of the timed steps."""
+    import importlib
+    ops = importlib.import_module(pkg.__name__ + ".ops")
+    synth = importlib.import_module(pkg.__name__ + ".synth")
+    vggt = importlib.import_module(pkg.__name__ + ".vggt")
+    plug = importlib.import_module(pkg.__name__ + ".patch")
+    acc = importlib.import_module(pkg.__name__ + ".accounting")
+    dev = torch.device("cuda:0")
+    torch.manual_seed(0)
+    model = vggt.GlobalAttentionStack(depth=layers, dim=dim, num_heads=heads)
+    model = model.to(dev).to(torch.bfloat16).eval()
+    if sparse_cfg is not None:
+        plug.patch_model(model, "vggt", {"patch_module": {"type": "headsparse", "topk_mode": "token",
+                                                          "lazy_dino_topk": True, "topk": 4},
+                                         "sparse_config": sparse_cfg})
+    else:
+        cfg, _ = layer_config(layers, heads, 1, synth, ops, table_fn)
+        plug.patch_model(model, "vggt", {"patch_module": {"type": "headsparse", "topk_mode": "token",
+                                                          "block_topk": topk, "topk_scope": "frame"},
+                                         "sparse_config": cfg})
+    plug.update_args_per_forward(model, "vggt", grid * 14, grid * 14)
+    T = grid * grid + 5
+    N = frames * T
+    geom = pkg.Geometry(frames, T, 5)
+    g = torch.Generator(device=dev).manual_seed(0)
+    x = torch.randn(1, N, dim, generator=g, device=dev).to(torch.bfloat16)
+    pos = synth.vggt_positions(frames, grid, grid, device=dev)[None]
+    wrappers = [b.attn for b in model.aggregator.global_blocks]
+
+    def step():
+        plug.update_args_per_forward(model, "vggt", grid * 14, grid * 14)  # a new forward: lazy indices recomputed
+        for layer in wrappers:
+            layer(x, pos)
+
+    rec = EventRecorder()
+    ops.set_event_recorder(rec)
+    with torch.no_grad():
+        for _ in range(warmup):
+            step()
+        torch.cuda.synchronize()
+        rec.enabled = True
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            step()
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        rec.enabled = False
+    ops.set_event_recorder(None)
+    ms_step = (t1 - t0) * 1e3 / steps
+
+    # algorithmic work of every layer (selection lists and key sets of the last step); the attention
+    # kernel's own share excludes the image rows of dino_topk heads (done by the gather kernel)
+    def layer_work(w, full):
+        width = w.est_topk_idx.shape[1] if (full and w.dino_heads) else 0
+        counts = w.last_keysets.count.tolist() if w.keyset_heads else None
+        return acc.attention_flops(w.patterns, geom, w.last_selection, width, counts)
+
+    res = {
+        "ms_step": ms_step, "ms_layer": ms_step / layers, "dur": rec.durations_ms(), "layers": wrappers,
+        "geom": geom, "model": model,
+        "attn_flops": [layer_work(w, True) for w in wrappers],
+        "kernel_flops": [layer_work(w, False) for w in wrappers],
+        "exec_flops": [acc.executed_tile_flops(w.patterns, geom, w.last_selection,
+                                               w.last_keysets.count.tolist() if w.keyset_heads else None,
+                                               ops.token_order_heads(w.patterns)) for w in wrappers],
+    }
+    del x
+    return res
+
+
+def da3_leg(pkg, steps, warmup):
+    """The DA3-Giant-style shape through the plugin: 24 layers, dim 1536, 24 heads, 96 frames of
+    5 + 36 x 36 tokens (124,896), per-layer head tables of 12 block-top-8 / 4 frame-local / 4 anchor+local /
+    4 dense heads (seed 1 + layer), random-init bf16 weights, N(0,1) tokens."""
+    import importlib
+    synth = importlib.import_module(pkg.__name__ + ".synth")
+    acc = importlib.import_module(pkg.__name__ + ".accounting")
+    layers, dim = 24, 1536
+    run = run_stack(pkg, 96, dim, 24, 36, layers, 8, synth.da3_patterns, steps, warmup)
+    geom = run["geom"]
+    attn_ms = run["dur"].get("sparse_attn", [])
+    proj = acc.projection_flops(geom.tokens, dim)
+    layer_flops = sum(run["attn_flops"]) / layers + proj
+    attn_tflops = sum(run["kernel_flops"]) * steps / (sum(attn_ms) * 1e-3) / 1e12
+    res = {
+        "workload": (f"DA3-Giant-style global attention: {layers} layers x 96 frames x {geom.tokens_per_frame} "
+                     f"tokens ({geom.tokens}), 24 heads, d 64, dim 1536, head mix 12 block-top8 / 4 frame-local / "
+                     "4 anchor+local / 4 dense per layer (seed 1+layer), block 64"),
+        "steps": steps, "warmup": warmup,
+        "ms_per_layer": round(run["ms_layer"], 3),
+        "tokens_per_s": round(geom.tokens / (run["ms_layer"] * 1e-3), 1),
+        "layer_tflops": round(layer_flops / (run["ms_layer"] * 1e-3) / 1e12, 2),
+        "attn_ms_per_layer": round(statistics.fmean(attn_ms), 3),
+        "attn_tflops": round(attn_tflops, 2),
+        "roofline_frac": round(attn_tflops / PEAK_BF16_TFLOPS, 4),
+        "flop_per_layer": {"attention": round(sum(run["attn_flops"]) / layers), "projection": proj},
+        "other_kernels_ms": {k: round(statistics.fmean(v), 4) for k, v in run["dur"].items() if k != "sparse_attn"},
+    }
+    del run
+    torch.cuda.empty_cache()
+    return res
+
+
+def single_layer_leg(pkg, frames, reps=10):
+    """One global-attention layer on the structured Q/K/V generator (seed 0) at ``frames`` x 1374 tokens,
+    16 heads, head table of seed 1 (7 block-top-4 / 4 frame-local / 3 anchor+local / 2 dense): packing
+    (Q with the softmax scale, the plugin's layouts), block pooling and selection, and the attention
+    launch, as the wrapper runs them; 2 warm-up layers, the median of ``reps`` (stream events)."""
+    import importlib
+    ops = importlib.import_module(pkg.__name__ + ".ops")
+    synth = importlib.import_module(pkg.__name__ + ".synth")
+    acc = importlib.import_module(pkg.__name__ + ".accounting")
+    dev = torch.device("cuda:0")
+    H = 16
+    wl = synth.structured_qkv(frames=frames, heads=H, seed=0, device=dev)
+    geom = wl.geom
+    q, k, v = (t.to(torch.bfloat16) for t in (wl.q, wl.k, wl.v))
+    del wl
+    pats = synth.seeded_patterns(H, seed=1)
+    lay = ops.token_order_heads(pats, geom)
+    qs = [True] * H
+    dyn = [h for h, p in enumerate(pats) if p == ops.BLOCK_DYNAMIC]
+    out = torch.empty(geom.tokens, H * 64, dtype=torch.bfloat16, device=dev)
+
+    def layer():
+        qp, kp, vp = ops.pack_heads(q, k, v, geom, token_order=lay, q_scaled=qs)
+        pq, pk = ops.block_pool(qp, kp, geom, dyn)
+        sel = ops.block_select(pq, pk, frames, geom.blocks_per_frame, 4)
+        ops.sparse_attn_fwd(qp, kp, vp, geom, pats, sel, out=out, token_order=lay, q_scaled=qs)
+        return sel
+
+    rec = EventRecorder()
+    ops.set_event_recorder(rec)
+    for _ in range(2):
+        layer()
+    torch.cuda.synchronize()
+    layer_ms = []
+    rec.enabled = True
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        sel = layer()
+        e1.record()
+        torch.cuda.synchronize()
+        layer_ms.append(e0.elapsed_time(e1))
+    rec.enabled = False
+    ops.set_event_recorder(None)
+    dur = rec.durations_ms()
+    flops = acc.attention_flops(pats, geom, sel)
+    ms = statistics.median(layer_ms)
+    attn = statistics.median(dur["sparse_attn"])
+    return {
+        "workload": (f"one global-attention layer, {frames} frames x 1374 tokens ({geom.tokens}), 16 heads, d 64, "
+                     "structured Q/K/V (seed 0), head mix 7 block-top4 / 4 frame-local / 3 anchor+local / 2 dense "
+                     "(seed 1), block 64; packing + pooling + selection + attention, no projections"),
+        "reps": reps,
+        "ms_per_layer": round(ms, 3),
+        "tokens_per_s": round(geom.tokens / (ms * 1e-3), 1),
+        "layer_tflops": round(flops / (ms * 1e-3) / 1e12, 2),
+        "attn_ms": round(attn, 3),
+        "attn_tflops": round(flops / (attn * 1e-3) / 1e12, 2),
+        "roofline_frac": round(flops / (attn * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+        "algorithmic_flop": flops,
+        "other_kernels_ms": {k: round(statistics.median(v), 4) for k, v in dur.items() if k != "sparse_attn"},
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -406,6 +581,8 @@ def main():
                     help="frames of the full-aggregator forward leg (0 skips it)")
     ap.add_argument("--per-pattern", action="store_true",
                     help="run only the per-pattern attention timing (16 heads of each pattern, and the head mix)")
+    ap.add_argument("--no-extra-configs", dest="extra_configs", action="store_false",
+                    help="skip the 32-frame single-layer and the DA3-Giant-shape legs")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only a plain copy kernel of known size (reads 1 GiB, writes 1 GiB), for scaling "
                          "the FETCH_SIZE / WRITE_SIZE counters of a profiling run")
@@ -426,71 +603,18 @@ def main():
     pkg = __graft_entry__.package()
     ops = importlib.import_module(pkg.__name__ + ".ops")
     synth = importlib.import_module(pkg.__name__ + ".synth")
-    vggt = importlib.import_module(pkg.__name__ + ".vggt")
-    plug = importlib.import_module(pkg.__name__ + ".patch")
     acc = importlib.import_module(pkg.__name__ + ".accounting")
 
-    dev = torch.device("cuda:0")
-    dim, heads, ph, pw = 1024, 16, 37, 37
-    torch.manual_seed(0)
-    model = vggt.GlobalAttentionStack(depth=args.layers, dim=dim, num_heads=heads)
-    model = model.to(dev).to(torch.bfloat16).eval()
+    sparse_cfg = None
     if args.sparse_config:
         with open(args.sparse_config) as f:
-            cfg = {k: v for k, v in json.load(f).items() if int(k) < args.layers}
-        plug.patch_model(model, "vggt", {"patch_module": {"type": "headsparse", "topk_mode": "token",
-                                                          "lazy_dino_topk": True, "topk": 4}, "sparse_config": cfg})
-    else:
-        cfg, _ = layer_config(args.layers, heads, 1, synth, ops)
-        plug.patch_model(model, "vggt", {"patch_module": {"type": "headsparse", "topk_mode": "token",
-                                                          "block_topk": 4, "topk_scope": "frame"},
-                                         "sparse_config": cfg})
-    plug.update_args_per_forward(model, "vggt", ph * 14, pw * 14)
-    T = ph * pw + 5
-    N = args.frames * T
-    geom = pkg.Geometry(args.frames, T, 5)
-    g = torch.Generator(device=dev).manual_seed(0)
-    x = torch.randn(1, N, dim, generator=g, device=dev).to(torch.bfloat16)
-    pos = synth.vggt_positions(args.frames, ph, pw, device=dev)[None]
-    layers = [b.attn for b in model.aggregator.global_blocks]
-
+            sparse_cfg = {k: v for k, v in json.load(f).items() if int(k) < args.layers}
+    run = run_stack(pkg, args.frames, 1024, 16, 37, args.layers, 4, synth.seeded_patterns, args.steps, args.warmup,
+                    sparse_cfg)
+    ms_step, ms_layer, dur, layers, geom = run["ms_step"], run["ms_layer"], run["dur"], run["layers"], run["geom"]
+    N, T, dim, heads = geom.tokens, geom.tokens_per_frame, 1024, 16
     tables = [w.patterns for w in layers]
-
-    def step():
-        plug.update_args_per_forward(model, "vggt", ph * 14, pw * 14)  # a new forward: lazy indices recomputed
-        for layer in layers:
-            layer(x, pos)
-
-    rec = EventRecorder()
-    ops.set_event_recorder(rec)
-    with torch.no_grad():
-        for _ in range(args.warmup):
-            step()
-        torch.cuda.synchronize()
-        rec.enabled = True
-        t0 = time.perf_counter()
-        for _ in range(args.steps):
-            step()
-        torch.cuda.synchronize()
-        t1 = time.perf_counter()
-        rec.enabled = False
-    ops.set_event_recorder(None)
-    ms_step = (t1 - t0) * 1e3 / args.steps
-    ms_layer = ms_step / args.layers
-    dur = rec.durations_ms()
-
-    # algorithmic work of every layer (selection lists and key sets of the last step); the attention
-    # kernel's own share excludes the image rows of dino_topk heads (done by the gather kernel)
-    def layer_work(w, full):
-        width = w.est_topk_idx.shape[1] if (full and w.dino_heads) else 0
-        counts = w.last_keysets.count.tolist() if w.keyset_heads else None
-        return acc.attention_flops(w.patterns, geom, w.last_selection, width, counts)
-
-    attn_flops = [layer_work(w, True) for w in layers]
-    kernel_flops = [layer_work(w, False) for w in layers]
-    exec_flops = [acc.executed_tile_flops(w.patterns, geom, w.last_selection,
-                                          w.last_keysets.count.tolist() if w.keyset_heads else None,
-                                          ops.token_order_heads(w.patterns)) for w in layers]
+    attn_flops, kernel_flops, exec_flops = run["attn_flops"], run["kernel_flops"], run["exec_flops"]
     proj = acc.projection_flops(N, dim)
     layer_flops = sum(attn_flops) / args.layers + proj
     attn_ms = dur.get("sparse_attn", [])
@@ -566,8 +690,11 @@ def main():
     }
     if args.non_lazy_select:
         result["non_lazy_selection"] = non_lazy_selection(pkg, args.frames)
-    del layers, model, x
+    del layers, run
     torch.cuda.empty_cache()
+    if not args.sparse_config and args.extra_configs:
+        result["config_32_frames"] = single_layer_leg(pkg, 32)
+        result["config_da3_giant"] = da3_leg(pkg, max(1, args.steps // 4), 1)
     if args.aggregator_frames > 0 and not args.sparse_config:
         result["aggregator"] = aggregator_leg(pkg, args.aggregator_frames)
     if not args.no_cpu_baseline and not args.sparse_config:
