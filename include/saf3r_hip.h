@@ -48,7 +48,7 @@
 extern "C" {
 #endif
 
-#define SAF3R_ABI_VERSION 10
+#define SAF3R_ABI_VERSION 11
 
 enum saf3r_status {
   SAF3R_OK = 0,
@@ -146,6 +146,16 @@ int64_t saf3r_packed_slots(int frames, int tokens_per_frame, int num_special);
  *            flagged here is q * q_scale (fp32, after LayerNorm and RoPE), rounded once to bf16;
  *            its qk32 rows stay unscaled. With q_scale = softmax scale * log2(e) this is the
  *            prescaled Q that saf3r_sparse_attn_fwd takes for heads flagged in its q_scaled.
+ *   pool_heads, pool_mean, pool_split, pool_meta: host uint8 [num_heads] or NULL, and device buffers.
+ *            Heads h < 64 flagged here (packed layout only) also get the pooled block records of
+ *            saf3r_block_select_pooled, for the s-th flagged head (increasing head order), tensor
+ *            t = 0 (q) / 1 (k) and patch block b = f*NBf + j at record r = (s*2 + t)*F*NBf + b:
+ *              pool_mean[r*64 + d]:  the block mean of bf16(q) (q after LayerNorm and RoPE, without
+ *                                    q_scale) or of the packed bf16 k, each feature summed over the
+ *                                    block's patch tokens in order in fp32 and divided once by their
+ *                                    number (bit-identical to saf3r_block_pool on unscaled rows);
+ *              pool_split[r*128 ...]: fp16 bits of the mean's two-part split (saf3r_pooled_prepare);
+ *              pool_meta[r*2 ...]:    its norm bound and scale (saf3r_pooled_prepare).
  * Replaces: saf3r/patch/patch_vggt.py:577-583 (qkv reshape, q_norm/k_norm, rope) and
  *           saf3r/models/official_vggt/layers/rope.py:154-188.
  */
@@ -156,6 +166,7 @@ int saf3r_pack_qkv(const void* q, const void* k, const void* v, int64_t tok_stri
                    const int32_t* pos, const float* rope_cos, const float* rope_sin, int rope_positions,
                    void* q_packed, void* k_packed, void* v_packed, const uint8_t* token_order,
                    const uint8_t* fp32_heads, float* qk32, const uint8_t* q_scaled, float q_scale,
+                   const uint8_t* pool_heads, float* pool_mean, uint16_t* pool_split, float* pool_meta,
                    void* stream);
 
 /*
@@ -194,6 +205,36 @@ int saf3r_topk_from_scores(const float* scores, int n, int rows, int frames, int
  */
 int saf3r_block_select(const float* pooled_q, const float* pooled_k, int n, int nbq, int frames,
                        int blocks_per_frame, int k, int scope, int32_t* idx, void* stream);
+
+/*
+ * Split records of pooled rows for saf3r_block_select_pooled, from fp32 rows mean [rows][64]:
+ *   split[r*128 + d], split[r*128 + 64 + d]: fp16 bits of h1 = fp16(x * 2^s) and
+ *     h2 = fp16(x * 2^s - h1), x = mean[r*64 + d], s chosen so that the row's largest magnitude times
+ *     2^s lies in [2^14, 2^15) (s = 0 for a zero row);
+ *   meta[r*2]: an upper bound of the row's L2 norm, or +inf when the row has a non-finite value or a
+ *     largest magnitude outside [2^-50, 2^50] (such rows are always scored exactly);
+ *   meta[r*2 + 1]: 2^-s.
+ * No counterpart in the reference.
+ */
+int saf3r_pooled_prepare(const float* mean, int64_t rows, uint16_t* split, float* meta, void* stream);
+
+/*
+ * Per-frame block selection of the BLOCK_DYNAMIC pattern on the matrix cores, bit-identical to
+ * saf3r_block_select (scope 0) on the same means.
+ *   mean / split / meta: the pooled records of n heads (saf3r_pack_qkv pool_* or saf3r_pooled_prepare):
+ *     record (s*2 + t)*NB + b for head s, tensor t = 0 (query blocks) / 1 (key blocks), block b,
+ *     NB = frames * blocks_per_frame; mean [..][64] fp32, split [..][128] fp16 bits, meta [..][2].
+ *   idx: int32 [n][NB][frames*min(k, NBf)], frame-major, score descending, ties to the lower block.
+ *   score(i, j) = sequential fmaf over d = 0..63 of mean_q[i][d] * mean_k[j][d], as saf3r_block_select.
+ * Scores are approximated on the matrix cores from the split records with a proven error bound; a
+ * (query block, frame) whose best k + 1 approximations are separated by more than the bound is
+ * taken from them, every other one (near ties, rows flagged +inf) from the exact sequential scores.
+ * 1 <= k <= 32, blocks_per_frame <= 32 (k > 16 runs the sequential kernel on the means).
+ * Replaces: the block top-k of the dynamic pattern (no reference symbol; per-frame semantics of
+ *           saf3r/patch/wrapper.py:48 and saf3r/triton/fused_qk_topk.py:120-217 at block level).
+ */
+int saf3r_block_select_pooled(const float* mean, const uint16_t* split, const float* meta, int n, int frames,
+                              int blocks_per_frame, int k, int32_t* idx, void* stream);
 
 /*
  * Mean query and probe scores of the q_probe_topk key set, for n_sel heads, from their fp32 q / k

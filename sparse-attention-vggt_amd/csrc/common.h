@@ -179,6 +179,39 @@ __device__ inline void topk_insert(uint64_t (&a)[K], uint64_t x) {
   a[0] = c[0] ? x : a[0];
 }
 
+// ---------------------------------------------------------------------------------------
+// Split record of a pooled row for the matrix-core block scores. A wave holds the row's 64 fp32
+// values, one per lane. The row is scaled by 2^s (s chosen so that its largest magnitude lies in
+// [2^14, 2^15)) and written as two fp16 parts, x * 2^s = h1 + h2 + r with h1 = fp16(x * 2^s),
+// h2 = fp16(x * 2^s - h1) (the difference is exact in fp32) and |r| <= 2^-22 |x * 2^s| in fp16's normal
+// range. meta[0] is an upper bound of the row's L2 norm (+inf for a row outside the range the score
+// error bound covers: a non-finite value, or a largest magnitude outside [2^-50, 2^50] for a row
+// that is not all zero), meta[1] = 2^-s.
+// ---------------------------------------------------------------------------------------
+__device__ inline void pooled_split_row(float x, int lane, uint16_t* __restrict__ split, float* __restrict__ meta) {
+  float mx = fabsf(x), ss = x * x;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    mx = fmaxf(mx, __shfl_xor(mx, o));
+    ss += __shfl_xor(ss, o);
+  }
+  int e = 0;
+  (void)frexpf(mx, &e);  // mx = m * 2^e, m in [0.5, 1)
+  const bool zero = mx == 0.f;
+  const bool safe = zero || (mx >= 0x1p-50f && mx <= 0x1p50f);  // also false for inf / NaN
+  const int sc = zero ? 0 : 15 - e;                            // mx * 2^sc in [2^14, 2^15)
+  const float xs = ldexpf(x, sc);
+  const _Float16 h1 = (_Float16)xs;
+  const _Float16 h2 = (_Float16)(xs - (float)h1);
+  split[lane] = __builtin_bit_cast(uint16_t, h1);
+  split[64 + lane] = __builtin_bit_cast(uint16_t, h2);
+  if (lane == 0) {
+    // the fp32 sum of squares and the root are within 2^-17 of the exact norm: 2^-10 covers them
+    meta[0] = safe ? sqrtf(ss) * (1.0f + 0x1p-10f) : __builtin_inff();
+    meta[1] = ldexpf(1.0f, -sc);
+  }
+}
+
 __device__ inline float bf16_lo(uint32_t w) { return __builtin_bit_cast(float, w << 16); }
 __device__ inline float bf16_hi(uint32_t w) { return __builtin_bit_cast(float, w & 0xFFFF0000u); }
 

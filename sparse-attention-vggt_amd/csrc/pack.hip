@@ -41,14 +41,24 @@ struct PackParams {
   int8_t f32slot[64];  // slot of a flagged head in qk32
   uint64_t q_scaled;   // heads (bit h) whose packed Q is q * q_scale
   float q_scale;
+  uint64_t pool_heads;  // heads (bit h) whose patch-block means of bf16(q) and bf16(k) are written
+  int8_t pool_slot[64]; // slot of a pooled head in the pooled arrays
+  float* pool_mean;     // [slot][q, k][F*NBf][64]
+  uint16_t* pool_split; // [slot][q, k][F*NBf][2][64] fp16 bits (pooled_split_row)
+  float* pool_meta;     // [slot][q, k][F*NBf][2]
 };
 
 // One 512-thread workgroup per (64-slot tile, head). Eight threads own one slot row, 8 features
 // each (thread c8 of a row: features 8 c8 .. 8 c8 + 7); LayerNorm reduces across the eight, RoPE
 // pairs feature d with d +- 16 (partner thread c8 ^ 2). Every load of a row is issued before any
 // processing, so the q, k and v loads are in flight together.
+// Pooled heads: a patch tile of the packed layout is one selection block; its bf16(q) (without the
+// Q scale) and bf16(k) rows are staged in LDS and one thread per (tensor, feature) sums them in row
+// order and divides once by the block population (the block means of the block-dynamic pattern,
+// bit-identical to that definition), then each of those two waves writes its row's split record.
 __global__ __launch_bounds__(512) void pack_qkv_kernel(PackParams p) {
   __shared__ __align__(16) __bf16 vs[64 * 72];  // V rows of the tile, 144-byte row pitch
+  __shared__ __align__(16) __bf16 ps[2][64 * 64];  // pooled heads: bf16 q / k rows of the tile
   const Geom& g = p.g;
   const int tile = bid_x(), h = bid_y();
   const int t = tid_x(), row = t >> 3, c8 = t & 7;
@@ -59,6 +69,8 @@ __global__ __launch_bounds__(512) void pack_qkv_kernel(PackParams p) {
                                                            : slot_token(g, slot);
   const int64_t src = tok * p.tok_stride + (int64_t)h * p.head_stride + 8 * c8;
   const int64_t dst = ((int64_t)h * g.L + slot) * 64 + 8 * c8;
+  // a patch tile of a pooled head (pooled heads are packed in the padded layout: tile = block)
+  const bool pool = h < 64 && ((p.pool_heads >> h) & 1) && tile >= g.nst;
 
   u32x4 raw[3];
 #pragma unroll
@@ -134,6 +146,15 @@ __global__ __launch_bounds__(512) void pack_qkv_kernel(PackParams p) {
       d32[0] = f32x4{x[0], x[1], x[2], x[3]};
       d32[1] = f32x4{x[4], x[5], x[6], x[7]};
     }
+    if (pool) {  // the unscaled bf16 row (zeros past the block's population)
+      u32x4 o;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const bf16x2 a = {(__bf16)x[2 * j], (__bf16)x[2 * j + 1]};
+        o[j] = __builtin_bit_cast(uint32_t, a);
+      }
+      *reinterpret_cast<u32x4*>(&ps[which][row * 64 + 8 * c8]) = o;
+    }
     if (which == 0 && h < 64 && ((p.q_scaled >> h) & 1)) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) x[j] *= p.q_scale;
@@ -167,6 +188,19 @@ __global__ __launch_bounds__(512) void pack_qkv_kernel(PackParams p) {
     *reinterpret_cast<u32x4*>(p.vp + ((int64_t)h * g.L + (int64_t)tile * 64) * 64 + i * 64 + 8 * c8) =
         u32x4{w[0], w[1], w[2], w[3]};
   }
+  if (pool && t < 128) {  // waves 0 (q) and 1 (k): lane = feature
+    const int which = t >> 6, d = t & 63;
+    const int pt = tile - g.nst, b = pt % g.NBf;
+    const int cnt = min(64, g.P - 64 * b);
+    const __bf16* col = &ps[which][d];
+    float sum = 0.f;
+    for (int r = 0; r < cnt; ++r) sum = sum + (float)col[r * 64];
+    const float mean = sum / (float)cnt;
+    const int64_t nb = (int64_t)g.F * g.NBf;
+    const int64_t rec = ((int64_t)p.pool_slot[h] * 2 + which) * nb + pt;  // pt = f * NBf + b
+    p.pool_mean[rec * 64 + d] = mean;
+    pooled_split_row(mean, d, p.pool_split + rec * 128, p.pool_meta + rec * 2);
+  }
 }
 
 }  // namespace saf3r
@@ -179,7 +213,8 @@ extern "C" int saf3r_pack_qkv(const void* q, const void* k, const void* v, int64
                               const float* k_ln_bias, float ln_eps, int apply_ln, const int32_t* pos,
                               const float* rope_cos, const float* rope_sin, int rope_positions, void* q_packed,
                               void* k_packed, void* v_packed, const uint8_t* token_order, const uint8_t* fp32_heads,
-                              float* qk32, const uint8_t* q_scaled, float q_scale, void* stream) {
+                              float* qk32, const uint8_t* q_scaled, float q_scale, const uint8_t* pool_heads,
+                              float* pool_mean, uint16_t* pool_split, float* pool_meta, void* stream) {
   if (int e = injected("saf3r_pack_qkv")) return e;
   PackParams p;
   if (!make_geom(frames, tokens_per_frame, num_special, &p.g))
@@ -255,6 +290,24 @@ extern "C" int saf3r_pack_qkv(const void* q, const void* k, const void* v, int64
     }
     if (p.q_scaled && !(q_scale > 0.f && q_scale < 3.0e38f))
       return fail(SAF3R_ERR_INVALID, "saf3r_pack_qkv: q_scale must be positive and finite");
+  }
+  p.pool_heads = 0;
+  p.pool_mean = pool_mean;
+  p.pool_split = pool_split;
+  p.pool_meta = pool_meta;
+  if (pool_heads) {
+    int np = 0;
+    for (int h = 0; h < num_heads; ++h) {
+      if (!pool_heads[h]) continue;
+      if (h >= 64) return fail(SAF3R_ERR_UNSUPPORTED, "saf3r_pack_qkv: pooling is supported for heads 0..63");
+      if (((p.tok_order | p.framed) >> h) & 1)
+        return fail(SAF3R_ERR_INVALID, "saf3r_pack_qkv: pooled head %d must use the packed layout", h);
+      p.pool_heads |= 1ull << h;
+      p.pool_slot[h] = (int8_t)np++;
+    }
+    if (np > 0 && (!pool_mean || !pool_split || !pool_meta || ((uintptr_t)pool_mean | (uintptr_t)pool_split |
+                                                                (uintptr_t)pool_meta) % 16))
+      return fail(SAF3R_ERR_INVALID, "saf3r_pack_qkv: pooled heads need 16-byte aligned pool_mean / split / meta");
   }
   dim3 grid(p.g.NT, num_heads);
   hipLaunchKernelGGL(pack_qkv_kernel, grid, dim3(512), 0, (hipStream_t)stream, p);

@@ -161,10 +161,27 @@ def prescale_factor(scale: float | None = None) -> float:
     return (1.0 / math.sqrt(HEAD_DIM) if scale is None else scale) * LOG2E
 
 
+@dataclass
+class Pooled:
+    """Pooled block records of n heads (``saf3r_block_select_pooled``'s input): record
+    (s*2 + t)*NB + b for head s, tensor t (0 = q, 1 = k), block b. ``mean`` fp32 [n, 2, NB, 64],
+    ``split`` int16 [n, 2, NB, 2, 64] (fp16 bits), ``meta`` fp32 [n, 2, NB, 2]."""
+    mean: torch.Tensor
+    split: torch.Tensor
+    meta: torch.Tensor
+
+    @staticmethod
+    def empty(n: int, nb: int, device) -> "Pooled":
+        return Pooled(torch.empty(n, 2, nb, HEAD_DIM, dtype=torch.float32, device=device),
+                      torch.empty(n, 2, nb, 2, HEAD_DIM, dtype=torch.int16, device=device),
+                      torch.empty(n, 2, nb, 2, dtype=torch.float32, device=device))
+
+
 def pack_qkv(q, k, v, tok_stride: int, head_stride: int, geom: Geometry, num_heads: int,
              ln_q=None, ln_k=None, ln_eps: float = 1e-5, pos=None, rope_base=None, rope_positions=None, out=None,
              token_order: Sequence[int] | None = None, fp32_heads: Sequence[bool] | None = None,
-             q_scaled: Sequence[bool] | None = None, q_scale: float | None = None):
+             q_scaled: Sequence[bool] | None = None, q_scale: float | None = None,
+             pool_heads: Sequence[int] | None = None):
     """QK-LayerNorm + RoPE-2D + packing (``saf3r_pack_qkv``). ``q``/``k``/``v`` are tensors (or
     views) whose element (t, h, d) is at ``data_ptr + t*tok_stride + h*head_stride + d``.
     RoPE is applied when ``rope_base`` is given; ``rope_positions`` is the table length
@@ -173,10 +190,18 @@ def pack_qkv(q, k, v, tok_stride: int, head_stride: int, geom: Geometry, num_hea
     the call returns a fourth tensor, fp32 [n_flagged, 2, N, 64]: the fp32 q (index 0) and k (1) of
     the flagged heads after LayerNorm / RoPE, in token order and increasing head order. Heads flagged
     in ``q_scaled`` get their packed Q multiplied by ``q_scale`` (default ``prescale_factor()``) in
-    fp32 before the one bf16 rounding; pass the same flags to ``sparse_attn_fwd``."""
+    fp32 before the one bf16 rounding; pass the same flags to ``sparse_attn_fwd``. With
+    ``pool_heads`` (head ids, packed layout) the pack also writes those heads' pooled block records
+    (block means of bf16(q) without the scale and of bf16(k), and their split records) and the call
+    returns them last, as a :class:`Pooled`."""
     _need_cuda(q, k, v)
     lib = _lib.load()
     qp, kp, vp = out if out is not None else packed_buffers(geom, num_heads, q.device)
+    pooled, pool_flags = None, None
+    if pool_heads:
+        pool_heads = sorted(pool_heads)
+        pooled = Pooled.empty(len(pool_heads), geom.num_blocks, q.device)
+        pool_flags = [h in pool_heads for h in range(num_heads)]
     qk32 = None
     if fp32_heads is not None and any(fp32_heads):
         qk32 = torch.empty(sum(1 for f in fp32_heads if f), 2, geom.tokens, HEAD_DIM, dtype=torch.float32,
@@ -203,10 +228,10 @@ def pack_qkv(q, k, v, tok_stride: int, head_stride: int, geom: Geometry, num_hea
         _ptr(pos) if rc is not None else None, _ptr(rc), _ptr(rs), npos, _ptr(qp), _ptr(kp), _ptr(vp),
         _u8_layouts(token_order, num_heads), _u8_flags(fp32_heads, num_heads) if qk32 is not None else None,
         _ptr(qk32), _u8_flags(q_scaled, num_heads), float(prescale_factor() if q_scale is None else q_scale),
-        _lib.stream_ptr()))
-    if fp32_heads is not None:
-        return qp, kp, vp, qk32
-    return qp, kp, vp
+        _u8_flags(pool_flags, num_heads), _ptr(pooled.mean if pooled else None),
+        _ptr(pooled.split if pooled else None), _ptr(pooled.meta if pooled else None), _lib.stream_ptr()))
+    res = (qp, kp, vp) + ((qk32,) if fp32_heads is not None else ()) + ((pooled,) if pooled is not None else ())
+    return res
 
 
 def pack_heads(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, geom: Geometry, **kw):
@@ -242,6 +267,36 @@ def block_pool(qp: torch.Tensor, kp: torch.Tensor | None, geom: Geometry, heads:
                                     hs, n, _ptr(pq), _ptr(pk), _lib.stream_ptr()))
     _mark("block_pool", "end")
     return pq, pk
+
+
+def pooled_prepare(mean: torch.Tensor) -> Pooled:
+    """Split records of fp32 pooled means [n, 2, NB, 64] (``saf3r_pooled_prepare``)."""
+    _need_cuda(mean)
+    lib = _lib.load()
+    mean = mean.float().contiguous()
+    n, two, nb, d = mean.shape
+    if two != 2 or d != HEAD_DIM:
+        raise ValueError("pooled means must be [n, 2, NB, 64]")
+    res = Pooled(mean, torch.empty(n, 2, nb, 2, HEAD_DIM, dtype=torch.int16, device=mean.device),
+                 torch.empty(n, 2, nb, 2, dtype=torch.float32, device=mean.device))
+    _lib.check(lib.saf3r_pooled_prepare(_ptr(mean), n * 2 * nb, _ptr(res.split), _ptr(res.meta), _lib.stream_ptr()))
+    return res
+
+
+def block_select_pooled(pooled: Pooled, frames: int, blocks_per_frame: int, k: int) -> torch.Tensor:
+    """Per-frame block top-k on the matrix cores (``saf3r_block_select_pooled``), bit-identical to
+    ``block_select`` on ``pooled.mean``: int32 [n, NB, frames*min(k, NBf)] of global block ids."""
+    _need_cuda(pooled.mean, pooled.split, pooled.meta)
+    lib = _lib.load()
+    n, _, nb, _ = pooled.mean.shape
+    if nb != frames * blocks_per_frame:
+        raise ValueError("pooled records do not match frames * blocks_per_frame")
+    idx = torch.empty(n, nb, frames * min(k, blocks_per_frame), dtype=torch.int32, device=pooled.mean.device)
+    _mark("block_select", "start")
+    _lib.check(lib.saf3r_block_select_pooled(_ptr(pooled.mean), _ptr(pooled.split), _ptr(pooled.meta), n, frames,
+                                             blocks_per_frame, k, _ptr(idx), _lib.stream_ptr()))
+    _mark("block_select", "end")
+    return idx
 
 
 def topk_from_scores(scores: torch.Tensor, frames: int, k: int) -> torch.Tensor:

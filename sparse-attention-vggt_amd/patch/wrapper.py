@@ -6,8 +6,9 @@ ref: saf3r/patch/wrapper.py:8-106 (BaseHeadwiseSparseAttentionWrapper: head_cfg 
      every later layer), :575-590 (qkv -> q/k norm -> RoPE -> attention -> proj).
 
 One forward of a layer on the GPU:
-  qkv Linear (torch) -> saf3r_pack_qkv (LayerNorm + RoPE + packing) -> [block-dynamic heads:
-  saf3r_block_pool + saf3r_block_select] -> [lazy dino_topk: saf3r_token_topk once per forward]
+  qkv Linear (torch) -> saf3r_pack_qkv (LayerNorm + RoPE + packing; block means of the block-dynamic
+  heads) -> [block-dynamic heads: saf3r_block_select_pooled] -> [lazy dino_topk: saf3r_token_topk
+  once per forward]
   -> saf3r_sparse_attn_fwd (all heads, one launch) -> [dino_topk image rows: saf3r_gather_attn_fwd]
   -> proj Linear (torch).
 Instead of a Python loop over heads, every head runs in the single attention launch.
@@ -134,15 +135,21 @@ class BaseHeadwiseSparseAttentionWrapper(nn.Module):
         tord = ops.token_order_heads(self.patterns, geom)
         f32 = [h in self.fp32_slot for h in range(H)] if self.fp32_heads else None
         qs = self.q_scaled_heads()
+        # block_topk heads: the pack also writes their pooled block records (means of bf16 q / k)
         packed = ops.pack_qkv(qkv, qkv[:, C:], qkv[:, 2 * C:], 3 * C, HEAD_DIM, geom, H, ln_q=ln_q, ln_k=ln_k,
                               ln_eps=eps, pos=p2, rope_base=base, rope_positions=npos, token_order=tord, fp32_heads=f32,
-                              q_scaled=qs, q_scale=ops.prescale_factor(getattr(om, "scale", None)))
+                              q_scaled=qs, q_scale=ops.prescale_factor(getattr(om, "scale", None)),
+                              pool_heads=self.dyn_heads or None)
         qp, kp, vp = packed[:3]
         qk32 = packed[3] if f32 is not None else None
         sel = None
         if self.dyn_heads:
-            pq, pk = ops.block_pool(qp, kp, geom, self.dyn_heads)
-            sel = ops.block_select(pq, pk, geom.frames, geom.blocks_per_frame, self.layer_block_topk, self.topk_scope)
+            pooled = packed[-1]
+            if self.topk_scope == "frame":
+                sel = ops.block_select_pooled(pooled, geom.frames, geom.blocks_per_frame, self.layer_block_topk)
+            else:
+                sel = ops.block_select(pooled.mean[:, 0], pooled.mean[:, 1], geom.frames, geom.blocks_per_frame,
+                                       self.layer_block_topk, self.topk_scope)
         self.last_selection = sel  # block lists of the block_topk heads, in head order
         if self.dino_heads:
             self._lazy_token_topk(qp, kp, geom)

@@ -49,10 +49,11 @@ def oracle_keysets(w, qk32, og, ops):
     return out
 
 
-def packed_qkv(w, x, pos, geom, ops):
+def packed_qkv(w, x, pos, geom, ops, plain=False):
     """The q / k / v [H, N, 64] (bf16, natural token order) the wrapper's kernels consumed for input x
     (Q of the heads in ``w.q_scaled_heads()`` with ``ops.prescale_factor()`` folded in, as packed), and
-    {head: (q, k)} fp32 [N, 64] rows of its fp32 heads (probe and dino heads)."""
+    {head: (q, k)} fp32 [N, 64] rows of its fp32 heads (probe and dino heads). ``plain``: also the
+    bf16 q without the scale (the rows the block means of the block_topk heads are taken from)."""
     N, dim, H = geom.tokens, w.orig_module.qkv.in_features, w.num_heads
     om = w.orig_module
     qkv = om.qkv(x).reshape(N, 3 * dim).to(torch.bfloat16).contiguous()
@@ -66,14 +67,20 @@ def packed_qkv(w, x, pos, geom, ops):
     k, _ = unpack_rows(kp.cpu(), toks, N)
     v, _ = unpack_v(vp.cpu(), toks, N)
     rows32 = {h: (qk32[s, 0].cpu(), qk32[s, 1].cpu()) for h, s in w.fp32_slot.items()} if qk32 is not None else {}
-    return q, k, v, rows32
+    if not plain:
+        return q, k, v, rows32
+    qp0, _, _ = ops.pack_qkv(qkv, qkv[:, dim:], qkv[:, 2 * dim:], 3 * dim, 64, geom, H,
+                             ln_q=(om.q_norm.weight, om.q_norm.bias), ln_k=(om.k_norm.weight, om.k_norm.bias),
+                             pos=pos[0], rope_base=100.0)
+    q0, _ = unpack_rows(qp0.cpu(), toks, N)
+    return q, k, v, rows32, q0
 
 
 def check_layer_output(w, x, pos, y, geom, ops, li, tol=(2e-2, 2e-3)):
     """``y`` (the wrapper's output for input x) against the oracle layer on the kernels' own q/k/v."""
     N, dim = geom.tokens, w.orig_module.qkv.in_features
     om = w.orig_module
-    q, k, v, rows32 = packed_qkv(w, x, pos, geom, ops)
+    q, k, v, rows32, q_plain = packed_qkv(w, x, pos, geom, ops, plain=True)
     og = OA.Geometry(geom.frames, geom.tokens_per_frame, geom.num_special)
     c = ops.prescale_factor()
     qs = w.q_scaled_heads()
@@ -88,8 +95,8 @@ def check_layer_output(w, x, pos, y, geom, ops, li, tol=(2e-2, 2e-3)):
         for i, h in enumerate(w.keyset_heads):
             c = int(ks.count[i])
             assert torch.equal(ks.idx[i, :c].cpu(), sel[h].to(torch.int32)), f"layer {li} head {h} key set"
-    for h in w.dyn_heads:
-        sel[h] = torch.from_numpy(OS.block_select(OS.bf16_bits(q[h].float().numpy()),
+    for h in w.dyn_heads:  # block means of the unscaled bf16 q and of k
+        sel[h] = torch.from_numpy(OS.block_select(OS.bf16_bits(q_plain[h].float().numpy()),
                                                   OS.bf16_bits(k[h].float().numpy()), geom.frames,
                                                   geom.tokens_per_frame, geom.num_special, w.layer_block_topk))
     if w.dyn_heads:  # the kernels' block lists are the oracle's
@@ -139,16 +146,17 @@ def check_sampled_rows(w, x, pos, y, geom, ops, rows, what, tol=(2e-2, 2e-3)):
     om = w.orig_module
     qkv = om.qkv(x).reshape(N, 3 * dim).contiguous()
     qs = w.q_scaled_heads()  # Q as the wrapper packed it (softmax scale folded in)
-    qp, kp, _ = ops.pack_qkv(qkv, qkv[:, dim:], qkv[:, 2 * dim:], 3 * dim, 64, geom, H,
-                             ln_q=(om.q_norm.weight, om.q_norm.bias), ln_k=(om.k_norm.weight, om.k_norm.bias),
-                             pos=pos[0], rope_base=100.0, q_scaled=qs)  # every head padded, for reading back
+    pk = dict(ln_q=(om.q_norm.weight, om.q_norm.bias), ln_k=(om.k_norm.weight, om.k_norm.bias), pos=pos[0],
+              rope_base=100.0)  # every head padded, for reading back
+    qp, kp, _ = ops.pack_qkv(qkv, qkv[:, dim:], qkv[:, 2 * dim:], 3 * dim, 64, geom, H, q_scaled=qs, **pk)
+    qp0, _, _ = ops.pack_qkv(qkv, qkv[:, dim:], qkv[:, 2 * dim:], 3 * dim, 64, geom, H, **pk)  # unscaled q
     torch.cuda.synchronize()
     toks_all = torch.arange(N)
     T, F_ = geom.tokens_per_frame, geom.frames
     sel_of = {}
     bits = lambda t: t.contiguous().view(torch.int16).numpy().view(np.uint16)
-    for i, h in enumerate(w.dyn_heads):
-        qh = rows_of(qp, geom, toks_all, h).to(torch.bfloat16)
+    for i, h in enumerate(w.dyn_heads):  # block means of the unscaled bf16 q and of k
+        qh = rows_of(qp0, geom, toks_all, h).to(torch.bfloat16)
         kh = rows_of(kp, geom, toks_all, h).to(torch.bfloat16)
         want = OS.block_select(bits(qh), bits(kh), F_, T, geom.num_special, w.layer_block_topk)
         assert np.array_equal(w.last_selection[i].cpu().numpy(), want), f"{what}: block list of head {h}"

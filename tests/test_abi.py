@@ -24,7 +24,7 @@ def test_library_exports_every_declared_symbol(pkg):
     for n in names:
         assert hasattr(lib, n), n
     assert set(names) == set(lib_mod.EXPORTS)
-    assert lib.saf3r_abi_version() == lib_mod.ABI_VERSION == 10
+    assert lib.saf3r_abi_version() == lib_mod.ABI_VERSION == 11
 
 
 def test_packed_slots_matches_layout(pkg):
@@ -142,32 +142,50 @@ def test_invalid_arguments_fail_before_launch(pkg):
     rc = lib.saf3r_token_topk(ctypes.byref(krows), ctypes.byref(krows), 100, 2, 200, 129, dev, None, 0, None)
     assert rc == 2 and b"128" in lib.saf3r_last_error()
     rc = lib.saf3r_pack_qkv(None, None, None, 64, 64, 0, 10, 1, 1, None, None, None, None, 1e-5, 0, None, None,
-                            None, 0, None, None, None, None, None, None, None, 1.0, None)
+                            None, 0, None, None, None, None, None, None, None, 1.0, None, None, None, None, None)
     assert rc == 1 and b"geometry" in lib.saf3r_last_error()
     flags = (ctypes.c_uint8 * 65)(*([0] * 64 + [1]))  # token order beyond head 63
     rc = lib.saf3r_pack_qkv(dev, dev, dev, 64, 64, 2, 100, 5, 65, None, None, None, None, 1e-5, 0, None, None,
-                            None, 0, dev, dev, dev, flags, None, None, None, 1.0, None)
+                            None, 0, dev, dev, dev, flags, None, None, None, 1.0, None, None, None, None, None)
     assert rc == 2 and b"token order" in lib.saf3r_last_error()
     rc = lib.saf3r_pack_qkv(dev, dev, dev, 64, 64, 2, 69, 5, 1, None, None, None, None, 1e-5, 0, None, None,
-                            None, 0, dev, dev, dev, framed, None, None, None, 1.0, None)
+                            None, 0, dev, dev, dev, framed, None, None, None, 1.0, None, None, None, None, None)
     assert rc == 2 and b"framed layout" in lib.saf3r_last_error()
     rc = lib.saf3r_pack_qkv(dev, dev, dev, 64, 64, 2, 100, 5, 1, None, None, None, None, 1e-5, 0, None, None,
-                            None, 0, dev, dev, dev, (ctypes.c_uint8 * 1)(7), None, None, None, 1.0, None)
+                            None, 0, dev, dev, dev, (ctypes.c_uint8 * 1)(7), None, None, None, 1.0, None, None, None, None, None)
     assert rc == 1 and b"unknown layout" in lib.saf3r_last_error()
     rc = lib.saf3r_pack_qkv(dev, dev, dev, 64, 64, 2, 100, 5, 65, None, None, None, None, 1e-5, 0, None, None,
-                            None, 0, dev, dev, dev, None, flags, dev, None, 1.0, None)
+                            None, 0, dev, dev, dev, None, flags, dev, None, 1.0, None, None, None, None, None)
     assert rc == 2 and b"fp32 rows" in lib.saf3r_last_error()
     one = (ctypes.c_uint8 * 2)(0, 1)
     rc = lib.saf3r_pack_qkv(dev, dev, dev, 64, 64, 2, 100, 5, 2, None, None, None, None, 1e-5, 0, None, None,
-                            None, 0, dev, dev, dev, None, one, None, None, 1.0, None)
+                            None, 0, dev, dev, dev, None, one, None, None, 1.0, None, None, None, None, None)
     assert rc == 1 and b"qk32" in lib.saf3r_last_error()
     rc = lib.saf3r_pack_qkv(dev, dev, dev, 64, 64, 2, 100, 5, 65, None, None, None, None, 1e-5, 0, None, None,
-                            None, 0, dev, dev, dev, None, None, None, flags, 0.18, None)
+                            None, 0, dev, dev, dev, None, None, None, flags, 0.18, None, None, None, None, None)
     assert rc == 2 and b"scaled Q" in lib.saf3r_last_error()
     for bad_scale in (0.0, -1.0, float("inf")):
         rc = lib.saf3r_pack_qkv(dev, dev, dev, 64, 64, 2, 100, 5, 2, None, None, None, None, 1e-5, 0, None, None,
-                                None, 0, dev, dev, dev, None, None, None, one, bad_scale, None)
+                                None, 0, dev, dev, dev, None, None, None, one, bad_scale, None, None, None, None, None)
         assert rc == 1 and b"q_scale" in lib.saf3r_last_error()
+    one_pool = (ctypes.c_uint8 * 2)(1, 0)
+    rc = lib.saf3r_pack_qkv(dev, dev, dev, 64, 64, 2, 100, 5, 2, None, None, None, None, 1e-5, 0, None, None,
+                            None, 0, dev, dev, dev, (ctypes.c_uint8 * 2)(1, 0), None, None, None, 1.0, one_pool,
+                            dev, dev, dev, None)
+    assert rc == 1 and b"packed layout" in lib.saf3r_last_error()  # a pooled head in token order
+    rc = lib.saf3r_pack_qkv(dev, dev, dev, 64, 64, 2, 100, 5, 2, None, None, None, None, 1e-5, 0, None, None,
+                            None, 0, dev, dev, dev, None, None, None, None, 1.0, one_pool, dev, None, dev, None)
+    assert rc == 1 and b"pool_mean" in lib.saf3r_last_error()
+    rc = lib.saf3r_pooled_prepare(dev, 10, ctypes.c_void_p(24), dev, None)
+    assert rc == 1 and b"16-byte" in lib.saf3r_last_error()
+    rc = lib.saf3r_pooled_prepare(dev, -1, dev, dev, None)
+    assert rc == 1
+    rc = lib.saf3r_block_select_pooled(dev, dev, dev, 1, 4, 33, 4, dev, None)
+    assert rc == 2 and b"32 blocks" in lib.saf3r_last_error()
+    rc = lib.saf3r_block_select_pooled(dev, dev, dev, 1, 4, 22, 33, dev, None)
+    assert rc == 2 and b"k must be" in lib.saf3r_last_error()
+    rc = lib.saf3r_block_select_pooled(dev, None, dev, 1, 4, 22, 4, dev, None)
+    assert rc == 1 and b"null" in lib.saf3r_last_error()
     with pytest.raises(L.Saf3rError):
         L.check(1)
 

@@ -68,11 +68,15 @@ def _run_selected_layer(ops, geom, q, k, v, patterns, k_sel, layouts=False):
     """One layer over packed heads; ``layouts``: the per-head layouts the plugin uses (token order for
     dense heads, the framed layout for frame-relative heads), else every head in the packed layout."""
     tord = ops.token_order_heads(patterns, geom) if layouts else None
-    qp, kp, vp = ops.pack_heads(q.to(DEV), k.to(DEV), v.to(DEV), geom, token_order=tord)
     dyn = [h for h, p in enumerate(patterns) if p == ops.BLOCK_DYNAMIC]
-    pq, pk = ops.block_pool(qp, kp, geom, dyn)
-    sel = ops.block_select(pq, pk, geom.frames, geom.blocks_per_frame, k_sel)
+    # the plugin's selection path: block means written by the pack, matrix-core selection
+    qp, kp, vp, pooled = ops.pack_heads(q.to(DEV), k.to(DEV), v.to(DEV), geom, token_order=tord, pool_heads=dyn)
+    sel = ops.block_select_pooled(pooled, geom.frames, geom.blocks_per_frame, k_sel)
     out = ops.sparse_attn_fwd(qp, kp, vp, geom, patterns, sel, token_order=tord)
+    # the sequential path on the separately pooled packed rows selects the same blocks
+    pq, pk = ops.block_pool(qp, kp, geom, dyn)
+    assert torch.equal(pq, pooled.mean[:, 0]) and torch.equal(pk, pooled.mean[:, 1])
+    assert torch.equal(ops.block_select(pq, pk, geom.frames, geom.blocks_per_frame, k_sel), sel)
     torch.cuda.synchronize()
     return out, sel.cpu(), dyn
 

@@ -207,6 +207,106 @@ def test_block_select_adversarial_bit_exact(ops, frames, nbf, k, case):
         assert np.array_equal(got[h], ref), f"{case}: head {h} differs from the oracle"
 
 
+@pytest.mark.parametrize("frames,nbf,k,case",
+                         [(f, b, kk, c) for (f, b, kk) in [(4, 22, 4), (5, 32, 8), (3, 1, 1), (6, 21, 3), (2, 7, 8),
+                                                          (9, 17, 2)] for c in _ADV_CASES]
+                         + [(128, 22, 4, "normal"), (3, 5, 8, "ties"), (5, 4, 4, "normal"), (3, 3, 8, "ties"),
+                            (2, 32, 16, "normal"), (2, 9, 1, "ties"), (3, 22, 20, "normal")])
+def test_block_select_pooled_adversarial_bit_exact(ops, frames, nbf, k, case):
+    """The matrix-core block selection (split records, certified order, exact pass for the rest)
+    against the oracle's sequential scores on the adversarial pooled inputs, including k = NBf
+    (whole frames), k + 1 > NBf, 32 blocks per frame and k > 16 (the sequential kernel)."""
+    rng = np.random.default_rng(frames * 11 + nbf * 5 + k + len(case))
+    n, nb = 2, frames * nbf
+    pq = _pooled_case(case, n, nb, rng)
+    pk = _pooled_case(case, n, nb, rng)
+    if case == "ties":
+        pk[:, 1::nbf] = pk[:, 0::nbf][:, :pk[:, 1::nbf].shape[1]]
+        pq[:, 1::2] = pq[:, 0::2][:, :pq[:, 1::2].shape[1]]
+        if nbf > 3:
+            pk[0, 2::nbf] = np.nextafter(pk[0, 3::nbf], np.float32(np.inf))
+    mean = torch.from_numpy(np.stack([pq, pk], axis=1)).to(DEV)  # [n, 2, NB, 64]
+    pooled = ops.pooled_prepare(mean)
+    got = ops.block_select_pooled(pooled, frames, nbf, k).cpu().numpy()
+    for h in range(n):
+        ref = OS.frame_topk(OS.block_scores(pq[h], pk[h]), frames, k)
+        assert np.array_equal(got[h], ref), f"{case}: head {h} differs from the oracle"
+
+
+def test_block_select_pooled_128_frames(ops):
+    """128 frames x 22 blocks of N(0, 1/64)-like pooled means (the benchmark's scale), 3 heads: the
+    matrix-core selection is bit-identical to the oracle's sequential selection."""
+    rng = np.random.default_rng(77)
+    frames, nbf, n = 128, 22, 3
+    base = rng.standard_normal((n, 1, 64)).astype(np.float32) * np.float32(0.3)  # a shared component
+    mean = (base[:, None] + rng.standard_normal((n, 2, frames * nbf, 64)).astype(np.float32) * np.float32(0.12))
+    pooled = ops.pooled_prepare(torch.from_numpy(mean).to(DEV))
+    got = ops.block_select_pooled(pooled, frames, nbf, 4).cpu().numpy()
+    for h in range(n):
+        ref = OS.frame_topk(OS.block_scores(mean[h, 0], mean[h, 1]), frames, 4)
+        assert np.array_equal(got[h], ref), f"head {h}"
+
+
+def test_pooled_prepare_split_is_exact(ops):
+    """The split record: x * 2^s == h1 + h2 + r with |r| <= 2^-22 |x 2^s| (fp16 normal range), the row's
+    largest magnitude times 2^s in [2^14, 2^15), meta = (a norm bound >= the norm, 2^-s); rows outside
+    the covered range (non-finite, largest magnitude beyond [2^-50, 2^50]) carry +inf."""
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((1, 2, 6, 64)).astype(np.float32)
+    x[0, 0, 1] *= np.float32(1e-6)
+    x[0, 0, 2] = 0
+    x[0, 0, 3, 5] = np.inf
+    x[0, 1, 0] *= np.float32(1e20)  # largest magnitude above 2^50
+    x[0, 1, 1] *= np.float32(1e-20)  # below 2^-50
+    pooled = ops.pooled_prepare(torch.from_numpy(x).to(DEV))
+    split = pooled.split.cpu().numpy().view(np.float16).astype(np.float64)
+    meta = pooled.meta.cpu().numpy()
+    for t in range(2):
+        for r in range(6):
+            row = x[0, t, r].astype(np.float64)
+            norm, inv = meta[0, t, r]
+            finite = np.isfinite(row).all()
+            mx = np.abs(row).max() if finite else np.inf
+            safe = finite and (mx == 0 or 2.0 ** -50 <= mx <= 2.0 ** 50)
+            if not safe:
+                assert norm == np.inf, (t, r)
+                continue
+            assert norm >= np.sqrt((row ** 2).sum())
+            if mx == 0:
+                assert inv == 1 and (split[0, t, r] == 0).all()
+                continue
+            xs = row / inv
+            assert 2.0 ** 14 <= np.abs(xs).max() < 2.0 ** 15
+            h1, h2 = split[0, t, r, 0], split[0, t, r, 1]
+            assert np.array_equal(h1, xs.astype(np.float16).astype(np.float64))
+            resid = xs - h1 - h2
+            ok = np.abs(resid) <= 2.0 ** -22 * np.abs(xs) + 2.0 ** -25  # fp16 subnormal spacing / 2
+            assert ok.all(), (t, r, resid[~ok])
+
+
+def test_pack_pools_unscaled_rows_bit_exact(ops, pkg):
+    """Pooled records from the pack: the block means of bf16(q) (without the Q scale) and bf16(k) equal
+    the oracle's pooling of those rows bit for bit, the split records equal saf3r_pooled_prepare's of
+    the same means, and the selection from them equals the oracle's."""
+    geom = pkg.Geometry(3, 155, 5)
+    H = 4
+    q, k, v = _qkv(H, geom.tokens, seed=12, scale=1.3)
+    qs = [True, False, True, True]
+    qp, kp, vp, pooled = ops.pack_heads(q.to(DEV), k.to(DEV), v.to(DEV), geom, q_scaled=qs, pool_heads=[3, 1])
+    torch.cuda.synchronize()
+    for slot, h in enumerate([1, 3]):
+        for t, src in enumerate((q, k)):
+            ref = OS.block_pool(OS.bf16_bits(src[h].float().numpy()), geom.frames, geom.tokens_per_frame, 5)
+            assert np.array_equal(pooled.mean[slot, t].cpu().numpy().view(np.uint32), ref.view(np.uint32)), (h, t)
+    again = ops.pooled_prepare(pooled.mean.clone())
+    assert torch.equal(again.split, pooled.split) and torch.equal(again.meta, pooled.meta)
+    sel = ops.block_select_pooled(pooled, geom.frames, geom.blocks_per_frame, 2).cpu().numpy()
+    for slot, h in enumerate([1, 3]):
+        ref = OS.block_select(OS.bf16_bits(q[h].float().numpy()), OS.bf16_bits(k[h].float().numpy()),
+                              geom.frames, geom.tokens_per_frame, 5, 2)
+        assert np.array_equal(sel[slot], ref)
+
+
 def _run_layer(ops, pkg, geom, q, k, v, patterns, k_sel=2):
     qp, kp, vp = ops.pack_heads(q.to(DEV), k.to(DEV), v.to(DEV), geom)
     dyn = [h for h, p in enumerate(patterns) if p == ops.BLOCK_DYNAMIC]
