@@ -355,12 +355,10 @@ def per_pattern(pkg, frames, reps=5):
     for name, pats in sets.items():
         lay = ops.token_order_heads(pats, geom)
         qs = [True] * H
-        qp, kp, vp = ops.pack_heads(q, k, v, geom, token_order=lay, q_scaled=qs)
         dyn = [h for h, p in enumerate(pats) if p == ops.BLOCK_DYNAMIC]
-        sel = None
-        if dyn:
-            pq, pk = ops.block_pool(qp, kp, geom, dyn)
-            sel = ops.block_select(pq, pk, frames, geom.blocks_per_frame, 4)
+        packed = ops.pack_heads(q, k, v, geom, token_order=lay, q_scaled=qs, pool_heads=dyn)
+        qp, kp, vp = packed[:3]
+        sel = ops.block_select_pooled(packed[-1], frames, geom.blocks_per_frame, 4) if dyn else None
         for _ in range(2):
             ops.sparse_attn_fwd(qp, kp, vp, geom, pats, sel, out=out, token_order=lay, q_scaled=qs)
         torch.cuda.synchronize()
@@ -456,15 +454,37 @@ def run_stack(pkg, frames, dim, heads, grid, layers, topk, table_fn, steps, warm
 
     res = {
         "ms_step": ms_step, "ms_layer": ms_step / layers, "dur": rec.durations_ms(), "layers": wrappers,
-        "geom": geom, "model": model,
+        "geom": geom, "model": model, "x": x, "pos": pos,
         "attn_flops": [layer_work(w, True) for w in wrappers],
         "kernel_flops": [layer_work(w, False) for w in wrappers],
         "exec_flops": [acc.executed_tile_flops(w.patterns, geom, w.last_selection,
                                                w.last_keysets.count.tolist() if w.keyset_heads else None,
                                                ops.token_order_heads(w.patterns)) for w in wrappers],
     }
-    del x
     return res
+
+
+def pool_increment(run, reps=10):
+    """What pooling adds to the pack: the first layer's pack (LayerNorm, RoPE, layouts, scaled Q) with
+    and without the block records of its block_topk heads, alternated ``reps`` times, each launch
+    timed by its own stream events; medians in ms."""
+    w, x, pos, geom = run["layers"][0], run["x"], run["pos"], run["geom"]
+    ts = {True: [], False: []}
+    with torch.no_grad():
+        qkv = w.orig_module.qkv(x).reshape(geom.tokens, -1).contiguous()
+        for pool in (True, False):
+            w.pack(qkv, pos, geom, pool)
+        torch.cuda.synchronize()
+        for _ in range(reps):
+            for pool in (True, False):
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                w.pack(qkv, pos, geom, pool)
+                e1.record()
+                torch.cuda.synchronize()
+                ts[pool].append(e0.elapsed_time(e1))
+    del qkv
+    return statistics.median(ts[True]), statistics.median(ts[False])
 
 
 def da3_leg(pkg, steps, warmup):
@@ -503,7 +523,7 @@ def da3_leg(pkg, steps, warmup):
 def single_layer_leg(pkg, frames, reps=10):
     """One global-attention layer on the structured Q/K/V generator (seed 0) at ``frames`` x 1374 tokens,
     16 heads, head table of seed 1 (7 block-top-4 / 4 frame-local / 3 anchor+local / 2 dense): packing
-    (Q with the softmax scale, the plugin's layouts), block pooling and selection, and the attention
+    (Q with the softmax scale, the plugin's layouts, block means), block selection and the attention
     launch, as the wrapper runs them; 2 warm-up layers, the median of ``reps`` (stream events)."""
     import importlib
     ops = importlib.import_module(pkg.__name__ + ".ops")
@@ -522,9 +542,8 @@ def single_layer_leg(pkg, frames, reps=10):
     out = torch.empty(geom.tokens, H * 64, dtype=torch.bfloat16, device=dev)
 
     def layer():
-        qp, kp, vp = ops.pack_heads(q, k, v, geom, token_order=lay, q_scaled=qs)
-        pq, pk = ops.block_pool(qp, kp, geom, dyn)
-        sel = ops.block_select(pq, pk, frames, geom.blocks_per_frame, 4)
+        qp, kp, vp, pooled = ops.pack_heads(q, k, v, geom, token_order=lay, q_scaled=qs, pool_heads=dyn)
+        sel = ops.block_select_pooled(pooled, frames, geom.blocks_per_frame, 4)
         ops.sparse_attn_fwd(qp, kp, vp, geom, pats, sel, out=out, token_order=lay, q_scaled=qs)
         return sel
 
@@ -551,7 +570,7 @@ def single_layer_leg(pkg, frames, reps=10):
     return {
         "workload": (f"one global-attention layer, {frames} frames x 1374 tokens ({geom.tokens}), 16 heads, d 64, "
                      "structured Q/K/V (seed 0), head mix 7 block-top4 / 4 frame-local / 3 anchor+local / 2 dense "
-                     "(seed 1), block 64; packing + pooling + selection + attention, no projections"),
+                     "(seed 1), block 64; packing with block means + selection + attention, no projections"),
         "reps": reps,
         "ms_per_layer": round(ms, 3),
         "tokens_per_s": round(geom.tokens / (ms * 1e-3), 1),
@@ -628,16 +647,27 @@ def main():
         sel_extra_scores = {}
     width = args.frames * min(4, geom.blocks_per_frame)
     sb = acc.selection_bytes(geom, n_dyn, width)
-    pool_ms = dur.get("block_pool", [])
     sel_ms = dur.get("block_select", [])
     sel_extra = {}
-    if pool_ms and sel_ms:
+    if sel_ms:
+        pooled_ms, plain_ms = pool_increment(run)
+        inc = pooled_ms - plain_ms
+        sel_avg = statistics.fmean(sel_ms)
+        fused = max(inc, 0.0) + sel_avg
         sel_extra = {
-            "pool_ms": round(statistics.fmean(pool_ms), 4),
-            "select_ms": round(statistics.fmean(sel_ms), 4),
-            "pool_GBs": round(sb["pool"] / (statistics.fmean(pool_ms) * 1e-3) / 1e9, 1),
-            "select_GBs": round(sb["select"] / (statistics.fmean(sel_ms) * 1e-3) / 1e9, 1),
-            "fused_path_GBs": round(sb["fused_path"] / ((statistics.fmean(pool_ms) + statistics.fmean(sel_ms)) * 1e-3) / 1e9, 1),
+            "select_kernel": "block_select_mfma_kernel",
+            "select_ms": round(sel_avg, 4),
+            "pack_ms_with_pooling": round(pooled_ms, 4),
+            "pack_ms_without_pooling": round(plain_ms, 4),
+            "pool_increment_ms": round(inc, 4),
+            "fused_path_ms": round(fused, 4),
+            "fused_path_GBs": round(sb["fused_path"] / (fused * 1e-3) / 1e9, 1),
+            "fused_path_frac": round(sb["fused_path"] / (fused * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+            "fused_path_bytes": sb["fused_path"],
+            "fused_path_note": ("algorithmic bytes (read Q and K of the block_topk heads, write their lists) over the "
+                                "selection's added time: the pack's increment for the block means (median of "
+                                "alternating packs with / without them, negative values counted as 0) plus the "
+                                "selection kernel"),
             "heads": n_dyn,
         }
         sel_extra.update(sel_extra_scores)

@@ -228,13 +228,23 @@ int saf3r_pooled_prepare(const float* mean, int64_t rows, uint16_t* split, float
  *   score(i, j) = sequential fmaf over d = 0..63 of mean_q[i][d] * mean_k[j][d], as saf3r_block_select.
  * Scores are approximated on the matrix cores from the split records with a proven error bound; a
  * (query block, frame) whose best k + 1 approximations are separated by more than the bound is
- * taken from them, every other one (near ties, rows flagged +inf) from the exact sequential scores.
+ * taken from them, every other one (near ties, rows flagged +inf) from the exact sequential scores
+ * by a second kernel.
+ *   workspace / workspace_bytes: caller-owned device memory of at least
+ *     saf3r_block_select_pooled_workspace_bytes(n, frames, blocks_per_frame, k) bytes, 16-byte
+ *     aligned (the per-workgroup queues of the pairs taken exactly). Needs no clearing; calls that
+ *     share a workspace must be ordered (one stream).
  * 1 <= k <= 32, blocks_per_frame <= 32 (k > 16 runs the sequential kernel on the means).
  * Replaces: the block top-k of the dynamic pattern (no reference symbol; per-frame semantics of
  *           saf3r/patch/wrapper.py:48 and saf3r/triton/fused_qk_topk.py:120-217 at block level).
  */
 int saf3r_block_select_pooled(const float* mean, const uint16_t* split, const float* meta, int n, int frames,
-                              int blocks_per_frame, int k, int32_t* idx, void* stream);
+                              int blocks_per_frame, int k, int32_t* idx, void* workspace, int64_t workspace_bytes,
+                              void* stream);
+
+/* Workspace bytes of saf3r_block_select_pooled for these sizes (0 when k > 16 selects the sequential
+ * kernel), -1 for sizes it rejects. No counterpart in the reference. */
+int64_t saf3r_block_select_pooled_workspace_bytes(int n, int frames, int blocks_per_frame, int k);
 
 /*
  * Mean query and probe scores of the q_probe_topk key set, for n_sel heads, from their fp32 q / k

@@ -18,7 +18,7 @@ EXPORTS = (
     "saf3r_topk_from_scores", "saf3r_block_select", "saf3r_sparse_attn_fwd", "saf3r_gather_attn_fwd",
     "saf3r_token_topk", "saf3r_probe_scores", "saf3r_keyset_build", "saf3r_keyset_gather",
     "saf3r_frame_topk_scores", "saf3r_probe_scores_noalloc", "saf3r_token_topk_workspace_bytes",
-    "saf3r_pooled_prepare", "saf3r_block_select_pooled",
+    "saf3r_pooled_prepare", "saf3r_block_select_pooled", "saf3r_block_select_pooled_workspace_bytes",
 )
 ABI_VERSION = 11
 GATHER_QK_FP32, GATHER_V_FP32, GATHER_OUT_FP32 = 1, 2, 4  # enum saf3r_gather_dtype
@@ -62,7 +62,8 @@ def load():
         "saf3r_pack_qkv": ([p, p, p, i64, i64, i32, i32, i32, i32, p, p, p, p, f32, i32, p, p, p, i32, p, p, p, p, p,
                             p, p, f32, p, p, p, p, p], i32),
         "saf3r_pooled_prepare": ([p, i64, p, p, p], i32),
-        "saf3r_block_select_pooled": ([p, p, p, i32, i32, i32, i32, p, p], i32),
+        "saf3r_block_select_pooled": ([p, p, p, i32, i32, i32, i32, p, p, i64, p], i32),
+        "saf3r_block_select_pooled_workspace_bytes": ([i32, i32, i32, i32], i64),
         "saf3r_block_pool": ([p, p, i32, i32, i32, i32, p, i32, p, p, p], i32),
         "saf3r_topk_from_scores": ([p, i32, i32, i32, i32, i32, p, p], i32),
         "saf3r_block_select": ([p, p, i32, i32, i32, i32, i32, i32, p, p], i32),

@@ -179,6 +179,28 @@ __device__ inline void topk_insert(uint64_t (&a)[K], uint64_t x) {
   a[0] = c[0] ? x : a[0];
 }
 
+// Reductions over a whole wave without LDS: DPP within each row of 16 lanes (quad swaps, row
+// rotations by 4 and 8), then the row pairs and the halves through v_permlane16_swap /
+// v_permlane32_swap. Every lane receives the result.
+template <int CTL>
+__device__ inline float dpp_mov(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTL, 0xF, 0xF, false));
+}
+
+template <typename Op>
+__device__ inline float wave_reduce(float x, Op op) {
+  x = op(x, dpp_mov<0xB1>(x));   // quad_perm [1, 0, 3, 2]
+  x = op(x, dpp_mov<0x4E>(x));   // quad_perm [2, 3, 0, 1]
+  x = op(x, dpp_mov<0x124>(x));  // row_ror:4
+  x = op(x, dpp_mov<0x128>(x));  // row_ror:8
+  const uint32_t u = __builtin_bit_cast(uint32_t, x);
+  const auto r16 = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  x = op(__builtin_bit_cast(float, (uint32_t)r16[0]), __builtin_bit_cast(float, (uint32_t)r16[1]));
+  const uint32_t v = __builtin_bit_cast(uint32_t, x);
+  const auto r32 = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return op(__builtin_bit_cast(float, (uint32_t)r32[0]), __builtin_bit_cast(float, (uint32_t)r32[1]));
+}
+
 // ---------------------------------------------------------------------------------------
 // Split record of a pooled row for the matrix-core block scores. A wave holds the row's 64 fp32
 // values, one per lane. The row is scaled by 2^s (s chosen so that its largest magnitude lies in
@@ -189,16 +211,15 @@ __device__ inline void topk_insert(uint64_t (&a)[K], uint64_t x) {
 // that is not all zero), meta[1] = 2^-s.
 // ---------------------------------------------------------------------------------------
 __device__ inline void pooled_split_row(float x, int lane, uint16_t* __restrict__ split, float* __restrict__ meta) {
-  float mx = fabsf(x), ss = x * x;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    mx = fmaxf(mx, __shfl_xor(mx, o));
-    ss += __shfl_xor(ss, o);
-  }
+  const float mx = wave_reduce(fabsf(x), [](float a, float b) { return fmaxf(a, b); });
+  const float ss = wave_reduce(x * x, [](float a, float b) { return a + b; });
   int e = 0;
   (void)frexpf(mx, &e);  // mx = m * 2^e, m in [0.5, 1)
   const bool zero = mx == 0.f;
-  const bool safe = zero || (mx >= 0x1p-50f && mx <= 0x1p50f);  // also false for inf / NaN
+  // maxNum drops a NaN, the sum of squares does not: a row with an inf or a NaN has a non-finite ss
+  // and is not safe (tested on the bits, so that no NaN assumption of the compiler can drop it)
+  const bool safe = ((__builtin_bit_cast(uint32_t, ss) & 0x7F800000u) != 0x7F800000u) &&
+                    (zero || (mx >= 0x1p-50f && mx <= 0x1p50f));
   const int sc = zero ? 0 : 15 - e;                            // mx * 2^sc in [2^14, 2^15)
   const float xs = ldexpf(x, sc);
   const _Float16 h1 = (_Float16)xs;

@@ -194,7 +194,15 @@ __global__ __launch_bounds__(512) void pack_qkv_kernel(PackParams p) {
     const int cnt = min(64, g.P - 64 * b);
     const __bf16* col = &ps[which][d];
     float sum = 0.f;
-    for (int r = 0; r < cnt; ++r) sum = sum + (float)col[r * 64];
+    int r = 0;
+    for (; r + 8 <= cnt; r += 8) {  // eight reads in flight, then the additions in row order
+      float x[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) x[j] = (float)col[(r + j) * 64];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) sum = sum + x[j];
+    }
+    for (; r < cnt; ++r) sum = sum + (float)col[r * 64];
     const float mean = sum / (float)cnt;
     const int64_t nb = (int64_t)g.F * g.NBf;
     const int64_t rec = ((int64_t)p.pool_slot[h] * 2 + which) * nb + pt;  // pt = f * NBf + b

@@ -279,199 +279,6 @@ __global__ __launch_bounds__(256) void block_select_global_kernel(const float* _
 }
 
 
-// ---------------------------------------------------------------------------------------
-// Block select on the matrix cores, bit-identical to the sequential kernel above.
-//
-// Score of query block i and key block j: the sequential fmaf chain s_ij = q_i . k_j. The kernel
-// computes an approximation from the fp16 split records (pooled_split_row):
-//   A_ij = Q1 K1^T + (Q1 K2^T + Q2 K1^T)   (two fp32 accumulators on v_mfma_f32_32x32x16_f16),
-//   a_ij = A_ij 2^-(sq_i + sk_j).
-// Error bound (u = 2^-24; sums taken as any order of fp32 additions with relative error <= 2u):
-//   MFMA sums of 64 exact fp16 products: 63 * 2^-23 sum|q k|; the small accumulator: 2^-18 of that;
-//   the dropped terms (h2 h2', h r', r h'): 3 * 2^-22 sum|q k|; the fmaf chain of the oracle:
-//   63 * 2^-24 sum|q k|; fp16 values below the normal range: 2^-25 |q| |k|; the final additions and the
-//   score keys below: 2^-17 |q| |k|. In all less than 1.4e-5 |q| |k| (sum|q k| <= |q| |k|), so
-//   |a_ij - s_ij| <= E_ij = 2^-15 |q_i| |k_j| with a factor of 2 to spare.
-// A (query block, frame) is certified when its k + 1 best approximate scores (by a) are separated
-// pairwise by more than 2 E_max (E_max over the frame's key blocks): the exact scores then have
-// the same order, strictly, so the top-k and its order are those of a. Every other pair (near ties,
-// rows outside the bound's range: norm +inf, which makes the threshold +inf or NaN) is queued in LDS
-// and computed exactly at the end: all the frame's sequential fmaf scores, ranked by the composite
-// key (score key, lower index first), as the oracle does.
-//
-// Decomposition: a workgroup of 4 waves owns 128 query blocks (32 per wave) of one head and a
-// range of frames, walked by all four waves in the same order (a frame's key records are read by
-// the four waves together, one L2 read). Per frame a wave runs S^T = K . Q^T for the frame's key
-// blocks (padded to 32 rows) against its 32 queries: lane (col, half) holds query col and 16 key
-// rows 8 g + 4 half + r; each value's sortable key (fkey) carries the key index in its 5 low bits
-// (31 - index: integer keys, so no value flushes and no tag makes a NaN) and is inserted into a
-// sorted list of the KL best (one max and KL - 1 med3 per value), the two halves merge their lists
-// through v_permlane32_swap, and the gaps of the merged list decide the pair.
-// ---------------------------------------------------------------------------------------
-constexpr int kMfmaSelFrames = 32;  // frames per workgroup
-
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-
-struct SelMfmaParams {
-  const float* mean;      // [n][2][NB][64]
-  const uint16_t* split;  // [n][2][NB][2][64]
-  const float* meta;      // [n][2][NB][2]
-  int32_t* idx;           // [n][NB][F * ke]
-  int F, NBf, NB, ke;
-};
-
-__device__ inline uint32_t med3u(uint32_t a, uint32_t b, uint32_t c) {
-  return max(min(a, b), min(max(a, b), c));  // one v_med3_u32
-}
-
-// insert x into the descending list a: a[0] = max, a[t] = med3(old a[t-1], old a[t], x), every slot
-// from the old list (the slots do not depend on each other)
-template <int KL>
-__device__ inline void list_insert(uint32_t (&a)[KL], uint32_t x) {
-#pragma unroll
-  for (int t = KL - 1; t > 0; --t) a[t] = med3u(a[t - 1], a[t], x);
-  a[0] = max(a[0], x);
-}
-
-// the float a sortable key (fkey) came from
-__device__ inline float key_value(uint32_t k) {
-  return __builtin_bit_cast(float, (k & 0x80000000u) ? (k ^ 0x80000000u) : ~k);
-}
-
-template <int KL>
-__global__ __launch_bounds__(256) void block_select_mfma_kernel(SelMfmaParams p) {
-  __shared__ uint32_t queue[128 * kMfmaSelFrames];
-  __shared__ uint32_t qcount;
-  const int lane = tid_x() & 63, w = tid_x() >> 6, col = lane & 31, half = lane >> 5;
-  const int hs = bid_z();
-  const int f0 = bid_y() * kMfmaSelFrames, f1 = min(p.F, f0 + kMfmaSelFrames);
-  const int64_t NB = p.NB;
-  const int qloc = 32 * w + col;                 // query block within the workgroup
-  const int64_t qi = (int64_t)bid_x() * 128 + qloc;
-  const bool qvalid = qi < NB;
-  const int64_t qrec = (int64_t)hs * 2 * NB + (qvalid ? qi : NB - 1);           // tensor 0 = q
-  const int64_t krec0 = ((int64_t)hs * 2 + 1) * NB;                            // tensor 1 = k
-  if (tid_x() == 0) qcount = 0;
-
-  // Q fragments: lane (col, half) holds features 32 half + 8 st .. + 7 of its query, both fp16 parts
-  f16x8 qf[2][4];
-  {
-    const u32x4* src = reinterpret_cast<const u32x4*>(p.split + qrec * 128 + 32 * half);
-#pragma unroll
-    for (int pc = 0; pc < 2; ++pc)
-#pragma unroll
-      for (int st = 0; st < 4; ++st) qf[pc][st] = __builtin_bit_cast(f16x8, src[pc * 8 + st]);
-  }
-  const float2 qm = *reinterpret_cast<const float2*>(p.meta + qrec * 2);
-  // threshold factor in units of A 2^-sk: 2 E + the tag truncation (2^-17 |q| |k|), times 2^sq
-  const float cq = (0x1p-14f + 0x1p-17f) * qm.x / qm.y;
-  __syncthreads();
-
-  const int kr = col < p.NBf ? col : p.NBf - 1;  // this lane's key row (rows past the frame repeat the last)
-  for (int f = f0; f < f1; ++f) {
-    const int64_t krec = krec0 + (int64_t)f * p.NBf + kr;
-    f16x8 kf[2][4];
-    const u32x4* ksrc = reinterpret_cast<const u32x4*>(p.split + krec * 128 + 32 * half);
-#pragma unroll
-    for (int pc = 0; pc < 2; ++pc)
-#pragma unroll
-      for (int st = 0; st < 4; ++st) kf[pc][st] = __builtin_bit_cast(f16x8, ksrc[pc * 8 + st]);
-    const float2 km = *reinterpret_cast<const float2*>(p.meta + krec * 2);
-    f32x16 a1 = {}, a2 = {};
-#pragma unroll
-    for (int st = 0; st < 4; ++st) a1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[0][st], qf[0][st], a1, 0, 0, 0);
-#pragma unroll
-    for (int st = 0; st < 4; ++st) {
-      a2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[0][st], qf[1][st], a2, 0, 0, 0);
-      a2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[1][st], qf[0][st], a2, 0, 0, 0);
-    }
-    // the frame's largest key norm (+inf if any of its rows is outside the bound's range)
-    float nkmax = km.x;
-#pragma unroll
-    for (int o = 1; o < 32; o <<= 1) nkmax = fmaxf(nkmax, __shfl_xor(nkmax, o));
-    uint32_t lst[KL];
-#pragma unroll
-    for (int t = 0; t < KL; ++t) lst[t] = 0u;  // below every key of a real value
-#pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      const int key = 8 * (v >> 2) + 4 * half + (v & 3);
-      if (8 * (v >> 2) >= p.NBf) break;  // groups past the frame (uniform)
-      const float ks = __shfl(km.y, key);  // 2^-sk of that key row (lane key holds it)
-      const float av = (a1[v] + a2[v]) * ks;
-      const uint32_t x = (fkey(av) & ~31u) | (uint32_t)(31 - key);
-      list_insert<KL>(lst, key < p.NBf ? x : 0u);
-    }
-    // merge with the other half's list (lanes l and l + 32 hold the same query)
-#pragma unroll
-    for (int t = 0; t < KL; ++t) {
-      const auto r = __builtin_amdgcn_permlane32_swap(lst[t], lst[t], false, false);
-      list_insert<KL>(lst, (uint32_t)(half ? r[0] : r[1]));
-    }
-    // certification: k + 1 best pairwise separated by more than the threshold (an empty slot, key 0,
-    // is a NaN value: only reached when ke = NBf, where the last gap is not needed)
-    const float thr = cq * nkmax;
-    bool ok = true;
-#pragma unroll
-    for (int t = 0; t < KL - 1; ++t)
-      if (t < p.ke) ok = ok && (t + 1 == p.NBf || key_value(lst[t]) - key_value(lst[t + 1]) > thr);
-    if (half == 0 && qvalid) {
-      if (ok) {
-        int32_t* o = p.idx + ((int64_t)hs * NB + qi) * ((int64_t)p.F * p.ke) + (int64_t)f * p.ke;
-#pragma unroll
-        for (int t = 0; t < KL - 1; ++t)
-          if (t < p.ke) o[t] = f * p.NBf + (31 - (int)(lst[t] & 31u));
-      } else {
-        const uint32_t at = atomicAdd(&qcount, 1u);
-        queue[at] = ((uint32_t)qloc << 16) | (uint32_t)(f - f0);
-      }
-    }
-  }
-  __syncthreads();
-
-  // exact pass over the queued pairs: two per wave at a time, lane (half, j) scores key block j
-  const int n_q = (int)qcount;
-  const float* qmean = p.mean + (int64_t)hs * 2 * NB * 64;
-  const float* kmean = p.mean + ((int64_t)hs * 2 + 1) * NB * 64;
-  for (int e0 = 2 * w; e0 < n_q; e0 += 8) {
-    const int e = e0 + half;
-    const bool act = e < n_q;
-    const uint32_t ent = act ? queue[e] : queue[e0];
-    const int64_t i = (int64_t)bid_x() * 128 + (ent >> 16);
-    const int f = f0 + (int)(ent & 0xFFFF);
-    const int j = col < p.NBf ? col : p.NBf - 1;
-    const f32x4* qr = reinterpret_cast<const f32x4*>(qmean + i * 64);
-    const f32x4* kv = reinterpret_cast<const f32x4*>(kmean + ((int64_t)f * p.NBf + j) * 64);
-    float acc = 0.f;
-#pragma unroll
-    for (int d4 = 0; d4 < 16; ++d4) {
-      const f32x4 a = qr[d4], b = kv[d4];
-      acc = __builtin_fmaf(a[0], b[0], acc);
-      acc = __builtin_fmaf(a[1], b[1], acc);
-      acc = __builtin_fmaf(a[2], b[2], acc);
-      acc = __builtin_fmaf(a[3], b[3], acc);
-    }
-    const uint64_t key = col < p.NBf ? ckey(acc, (uint32_t)j) : 0;
-    const uint32_t klo = (uint32_t)key, khi = (uint32_t)(key >> 32);
-    int rank = 0;
-    for (int c = 0; c < p.NBf; ++c) {  // keys of the same half beat this one
-      const uint32_t lo = __shfl(klo, 32 * half + c), hi = __shfl(khi, 32 * half + c);
-      rank += (((uint64_t)hi << 32) | lo) > key;
-    }
-    if (act && col < p.NBf && rank < p.ke)
-      p.idx[((int64_t)hs * NB + i) * ((int64_t)p.F * p.ke) + (int64_t)f * p.ke + rank] = f * p.NBf + j;
-  }
-}
-
-// Split records of given fp32 pooled rows (one wave per row): the input of the matrix-core select
-// for means that did not come from saf3r_pack_qkv.
-__global__ __launch_bounds__(256) void pooled_prepare_kernel(const float* __restrict__ mean, int64_t rows,
-                                                             uint16_t* __restrict__ split, float* __restrict__ meta) {
-  const int64_t r = (int64_t)bid_x() * 4 + (tid_x() >> 6);
-  if (r >= rows) return;  // a whole wave leaves; no barrier follows
-  const int lane = tid_x() & 63;
-  pooled_split_row(mean[r * 64 + lane], lane, split + r * 128, meta + r * 2);
-}
-
 template <template <int> class Launcher, typename... Args>
 int dispatch_k(int k, Args... args) {
   if (k <= 1) return Launcher<1>::run(args...);
@@ -558,59 +365,6 @@ extern "C" int saf3r_topk_from_scores(const float* scores, int n, int rows, int 
   int ke = k < cands_per_frame ? k : cands_per_frame;
   return dispatch_k<TopkScoresLaunch>(ke, scores, (int64_t)n * rows, frames, cands_per_frame, ke, idx,
                                       (hipStream_t)stream);
-}
-
-extern "C" int saf3r_pooled_prepare(const float* mean, int64_t rows, uint16_t* split, float* meta, void* stream) {
-  if (int e = injected("saf3r_pooled_prepare")) return e;
-  if (!mean || !split || !meta || rows < 0) return fail(SAF3R_ERR_INVALID, "saf3r_pooled_prepare: bad arguments");
-  if (((uintptr_t)mean | (uintptr_t)split | (uintptr_t)meta) % 16)
-    return fail(SAF3R_ERR_INVALID, "saf3r_pooled_prepare: buffers must be 16-byte aligned");
-  if (rows == 0) return SAF3R_OK;
-  if ((rows + 3) / 4 > 0x7fffffff) return fail(SAF3R_ERR_INVALID, "saf3r_pooled_prepare: too many rows");
-  hipLaunchKernelGGL(pooled_prepare_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, (hipStream_t)stream, mean,
-                     rows, split, meta);
-  return check_launch("saf3r_pooled_prepare");
-}
-
-extern "C" int saf3r_block_select_pooled(const float* mean, const uint16_t* split, const float* meta, int n,
-                                         int frames, int blocks_per_frame, int k, int32_t* idx, void* stream) {
-  if (int e = injected("saf3r_block_select_pooled")) return e;
-  if (!mean || !split || !meta || !idx) return fail(SAF3R_ERR_INVALID, "saf3r_block_select_pooled: null pointer");
-  if (((uintptr_t)mean | (uintptr_t)split | (uintptr_t)meta) % 16)
-    return fail(SAF3R_ERR_INVALID, "saf3r_block_select_pooled: pooled buffers must be 16-byte aligned");
-  if (n <= 0 || n > 65535 || frames <= 0 || blocks_per_frame <= 0 ||
-      (int64_t)frames * blocks_per_frame > 0x7fffffff / 64)
-    return fail(SAF3R_ERR_INVALID, "saf3r_block_select_pooled: bad shape");
-  if (k < 1 || k > 32) return fail(SAF3R_ERR_UNSUPPORTED, "saf3r_block_select_pooled: k must be in [1, 32] (got %d)", k);
-  if (blocks_per_frame > 32)
-    return fail(SAF3R_ERR_UNSUPPORTED, "saf3r_block_select_pooled: at most 32 blocks per frame");
-  const int NBf = blocks_per_frame, ke = k < NBf ? k : NBf;
-  const int NB = frames * NBf;
-  hipStream_t st = (hipStream_t)stream;
-  if (ke > 16) {  // lists longer than the matrix-core path keeps: the sequential kernel, head by head
-    for (int h = 0; h < n; ++h) {
-      const float* pq = mean + (int64_t)h * 2 * NB * 64;
-      if (int rc = dispatch_k<SelectFrameLaunch>(ke, pq, pq + (int64_t)NB * 64, 1, NB, frames, NBf, ke,
-                                                 idx + (int64_t)h * NB * frames * ke, st))
-        return rc;
-    }
-    return SAF3R_OK;
-  }
-  SelMfmaParams p;
-  p.mean = mean;
-  p.split = split;
-  p.meta = meta;
-  p.idx = idx;
-  p.F = frames;
-  p.NBf = NBf;
-  p.NB = NB;
-  p.ke = ke;
-  const dim3 grid((unsigned)((NB + 127) / 128), (unsigned)((frames + kMfmaSelFrames - 1) / kMfmaSelFrames),
-                  (unsigned)n);
-  if (ke <= 4) hipLaunchKernelGGL(block_select_mfma_kernel<5>, grid, dim3(256), 0, st, p);
-  else if (ke <= 8) hipLaunchKernelGGL(block_select_mfma_kernel<9>, grid, dim3(256), 0, st, p);
-  else hipLaunchKernelGGL(block_select_mfma_kernel<17>, grid, dim3(256), 0, st, p);
-  return check_launch("saf3r_block_select_pooled");
 }
 
 extern "C" int saf3r_block_select(const float* pooled_q, const float* pooled_k, int n, int nbq, int frames,

@@ -1,0 +1,418 @@
+// Per-frame block selection of the dynamic pattern on the matrix cores, bit-identical to the
+// sequential selection (block_select_frame_kernel in select.hip, the oracle's definition).
+//
+// ref: saf3r/triton/fused_qk_topk.py:73-100 (composite key = sortable fp32 bits << 32 | reversed
+//      index, per-frame top-k, frame-major output in descending order), saf3r/patch/wrapper.py:48.
+//
+// Score of query block i and key block j: the sequential fmaf chain s_ij = q_i . k_j over the fp32
+// block means. The kernel computes an approximation from the fp16 split records (pooled_split_row
+// in common.h: x 2^s = h1 + h2 + r, |r| <= 2^-22 |x 2^s|):
+//   A_ij = Q1 K1^T + (Q1 K2^T + Q2 K1^T)   (two fp32 accumulators on v_mfma_f32_32x32x16_f16),
+//   a_ij = A_ij 2^-(sq_i + sk_j).
+// Error bound (u = 2^-24; sums taken as any order of fp32 additions with relative error <= 2u):
+//   MFMA sums of 64 exact fp16 products: 63 * 2^-23 sum|q k|; the small accumulator: 2^-18 of that;
+//   the dropped terms (h2 h2', h r', r h'): 3 * 2^-22 sum|q k|; the fmaf chain of the oracle:
+//   63 * 2^-24 sum|q k|; fp16 values below the normal range: 2^-25 |q| |k|; the final additions:
+//   2^-22 |q| |k|. In all less than 1.3e-5 |q| |k| (sum|q k| <= |q| |k|), so
+//   |a_ij - s_ij| <= E_ij = 2^-15 |q_i| |k_j| with a factor of 2 to spare.
+// A (query block, frame) is certified when its k + 1 best approximate scores (by a, each carrying
+// its key index in the 5 low mantissa bits: a change of at most 2^-18 |a|) are separated pairwise by
+// more than thr = 2 E_max + 2^-17 |q| |k|max (E_max over the frame's key blocks): the exact scores
+// then have the same order, strictly, so the top-k and its order are those of a. Every other pair
+// (near ties, rows outside the bound's range: norm +inf, which makes the threshold +inf or NaN) goes
+// to a list in the caller's workspace with its candidate keys: those whose tagged a is within thr
+// of the k-th best (the true top-k is among them: any other key's exact score is below the k-th
+// best's approximation minus E), or every key of the frame when the list's last entry is also
+// within thr (keys outside the list may then qualify) or the threshold is not finite.
+// block_select_exact_kernel ranks the candidates by their sequential fmaf scores and the composite
+// key (score key, lower index first), as the oracle does (about 1.3% of the pairs at 128 frames on
+// random-init weights).
+//
+// Decomposition: a workgroup of 4 waves owns 128 query blocks (32 per wave) of one head and a
+// range of frames. Each frame's key records (NBf rows of 256 bytes, contiguous) are copied once
+// per workgroup into a 3-stage LDS ring by LDS-DMA loads, two frames ahead, 16-byte chunks
+// XOR-swizzled by row so that the 32 rows a fragment read touches fall into 16 distinct chunk
+// columns. Per frame a wave runs S^T = K . Q^T for the frame's key blocks (padded to 32 rows)
+// against its 32 queries: lane (col, half) holds query col and 16 key rows 8 g + 4 half + r; each
+// tagged value is inserted into a sorted list of the KL best (one max and KL - 1 med3 per value),
+// the two halves merge their lists through v_permlane32_swap, and the gaps of the merged list
+// decide the pair. The key scales and the frames' largest key norms are staged in LDS once per
+// workgroup; the certified lists are kept in LDS and written after the frame loop, so that no
+// global store sits between the ring's loads and their waits. The file is compiled without NaN
+// semantics (no canonicalisation before max / med3): every value in a certified pair is finite, and
+// finiteness itself is tested on the bits.
+#include "common.h"
+
+namespace saf3r {
+
+constexpr int kSelRing = 3;          // LDS ring stages (frames)
+constexpr int kSelStage = 32 * 256;  // bytes per stage: 32 key rows of 256 bytes
+constexpr int kSelExactWGs = 2048;   // persistent grid of the exact pass
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+struct SelMfmaParams {
+  const float* mean;      // [n][2][NB][64]
+  const uint16_t* split;  // [n][2][NB][2][64]
+  const float* meta;      // [n][2][NB][2]
+  int32_t* idx;           // [n][NB][F * ke]
+  uint32_t* qcount;       // the number of listed pairs (cleared before the select kernel)
+  u32x4* queue;           // listed pairs: (head * NB + query block, frame, candidate key mask, 0)
+  int F, NBf, NB, ke;
+};
+
+// insert x into the descending list a: a[0] = max, a[t] = med3(old a[t-1], old a[t], x), every slot
+// from the old list (the slots do not depend on each other)
+template <int KL>
+__device__ inline void list_insert(float (&a)[KL], float x) {
+#pragma unroll
+  for (int t = KL - 1; t > 0; --t) a[t] = __builtin_amdgcn_fmed3f(a[t - 1], a[t], x);
+  a[0] = fmaxf(a[0], x);
+}
+
+__device__ inline int tag_key(float v) { return 31 - (int)(__builtin_bit_cast(uint32_t, v) & 31u); }
+
+// LDS byte offset of 16-byte chunk c of key row r in a ring stage
+__device__ inline int sel_chunk(int r, int c) { return (r * 16 + (c ^ (r & 15))) * 16; }
+
+// KL: list length (k + 1 rounded up: 5, 9, 17); NG: groups of 8 key blocks per frame (ceil(NBf / 8)).
+// FPW = 32 / (KL - 1) frames per workgroup; about 45 KB of LDS: three workgroups per CU.
+template <int KL, int NG>
+__global__ __launch_bounds__(256) void block_select_mfma_kernel(SelMfmaParams p) {
+  constexpr int FPW = 32 / (KL - 1);
+  __shared__ __align__(16) char ring[kSelRing * kSelStage];
+  __shared__ int32_t outb[128 * 33];  // [query][frame in group * ke + t], rows of 33: no bank conflicts
+  __shared__ __align__(16) float ksc[FPW][32];  // 2^-sk of the frame's key blocks (1 past NBf)
+  __shared__ float nkm[FPW];                    // the frame's largest key norm bound
+  __shared__ u32x2 queue[128 * FPW];            // (query in the group, frame in the group), candidate mask
+  __shared__ uint32_t qcount, gbase;
+  const int tid = tid_x(), lane = tid & 63, w = tid >> 6, col = lane & 31, half = lane >> 5;
+  const int hs = bid_z();
+  const int f0 = bid_y() * FPW, f1 = min(p.F, f0 + FPW);
+  const int nf = f1 - f0;
+  const int64_t NB = p.NB;
+  const int qloc = 32 * w + col;  // query block within the workgroup
+  const int64_t qi = (int64_t)bid_x() * 128 + qloc;
+  const bool qvalid = qi < NB;
+  const int64_t qrec = (int64_t)hs * 2 * NB + (qvalid ? qi : NB - 1);  // tensor 0 = q
+  const int64_t krec0 = ((int64_t)hs * 2 + 1) * NB;                   // tensor 1 = k
+
+  // Q fragments: lane (col, half) holds features 32 half + 8 st .. + 7 of its query, both fp16 parts
+  f16x8 qf[2][4];
+  {
+    const u32x4* src = reinterpret_cast<const u32x4*>(p.split + qrec * 128 + 32 * half);
+#pragma unroll
+    for (int pc = 0; pc < 2; ++pc)
+#pragma unroll
+      for (int st = 0; st < 4; ++st) qf[pc][st] = __builtin_bit_cast(f16x8, src[pc * 8 + st]);
+  }
+  const float2 qm = *reinterpret_cast<const float2*>(p.meta + qrec * 2);
+
+  // key meta of the workgroup's frames: the scale of every key block in LDS, and the frame's largest
+  // norm bound (the 32 threads of a frame's entries, a half wave, reduce it by shuffles)
+  if (tid == 0) qcount = 0;
+  for (int e0 = 0; e0 < FPW * 32; e0 += 256) {
+    const int e = e0 + tid, fl = e >> 5, j = e & 31;
+    float2 m = {0.f, 0.f};  // rows past the frame: no norm, no scale
+    if (fl < nf && j < p.NBf) m = *reinterpret_cast<const float2*>(p.meta + (krec0 + (int64_t)(f0 + fl) * p.NBf + j) * 2);
+    if (fl < FPW) ksc[fl][j] = m.y;
+    float mx = m.x;
+#pragma unroll
+    for (int o = 1; o < 32; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    if (j == 0 && fl < FPW) nkm[fl] = mx;
+  }
+  __syncthreads();
+
+  // ring fill: thread t copies LDS chunks t and 256 + t of the stage (row = chunk / 16, the global
+  // chunk through the swizzle; rows past NBf repeat the frame's last row)
+  const uint32_t ring_base = lds_addr(ring);
+  auto fill = [&](int f) {
+    const uint32_t st = ring_base + (uint32_t)(((f - f0) % kSelRing) * kSelStage);
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int pos = 256 * u + tid, r = pos >> 4, c = (pos & 15) ^ (r & 15);
+      const int rr = r < p.NBf ? r : p.NBf - 1;
+      const uint16_t* src = p.split + (krec0 + (int64_t)f * p.NBf + rr) * 128 + 8 * c;
+      dma16(src, st + (uint32_t)(4096 * u + 1024 * w));
+    }
+  };
+  for (int j = 0; j < kSelRing - 1; ++j)
+    if (j < nf) fill(f0 + j);
+
+  // threshold factor in units of A 2^-sk: 2 E + the tag truncation (2^-17 |q| |k|), times 2^sq
+  const float cq = (0x1p-14f + 0x1p-17f) * qm.x / qm.y;
+  const int kr = col < p.NBf ? col : p.NBf - 1;  // this lane's key row
+  uint32_t tagc[NG * 4];                         // 31 - key of every value this lane holds
+#pragma unroll
+  for (int v = 0; v < NG * 4; ++v) tagc[v] = (uint32_t)(31 - (8 * (v >> 2) + 4 * half + (v & 3)));
+  const uint32_t all_keys = p.NBf >= 32 ? 0xFFFFFFFFu : (1u << p.NBf) - 1u;
+
+  for (int f = f0; f < f1; ++f) {
+    const int fl = f - f0;
+    // frame f's copy landed (the next frame's copy may still be in flight: the loop issues no other
+    // vector memory operation), then every wave is past frame f - 1, whose stage the copy of frame
+    // f + 2 reuses
+    if (f + 1 < f1) wait_vm<2>();
+    else wait_vm<0>();
+    barrier_only();
+    if (f + kSelRing - 1 < f1) fill(f + kSelRing - 1);
+    const char* stg = ring + (fl % kSelRing) * kSelStage;
+    f16x8 kf[2][4];
+#pragma unroll
+    for (int pc = 0; pc < 2; ++pc)
+#pragma unroll
+      for (int st = 0; st < 4; ++st)
+        kf[pc][st] = *reinterpret_cast<const f16x8*>(stg + sel_chunk(kr, 8 * pc + 4 * half + st));
+    f32x16 a1 = {}, a2 = {};
+#pragma unroll
+    for (int st = 0; st < 4; ++st) a1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[0][st], qf[0][st], a1, 0, 0, 0);
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      a2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[0][st], qf[1][st], a2, 0, 0, 0);
+      a2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[1][st], qf[0][st], a2, 0, 0, 0);
+    }
+    // this lane's key blocks 8 g + 4 half + r: their scales (one 16-byte read per group of four)
+    float ks[NG][4];
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      const f32x4 x = *reinterpret_cast<const f32x4*>(&ksc[fl][8 * g + 4 * half]);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) ks[g][r] = x[r];
+    }
+    const float thr = cq * nkm[fl];
+    float lst[KL];
+#pragma unroll
+    for (int t = 0; t < KL; ++t) lst[t] = -__builtin_huge_valf();
+#pragma unroll
+    for (int g = 0; g < NG; ++g)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int v = 4 * g + r;
+        const float av = (a1[v] + a2[v]) * ks[g][r];
+        float x = __builtin_bit_cast(float, (__builtin_bit_cast(uint32_t, av) & ~31u) | tagc[v]);
+        if (g == NG - 1) x = 8 * g + 4 * half + r < p.NBf ? x : -__builtin_huge_valf();  // past the frame
+        list_insert<KL>(lst, x);
+      }
+    // merge with the other half's list (lanes l and l + 32 hold the same query): the whole partner
+    // list first, then the insertions (an entry exchanged after an insertion could be one's own)
+    float other[KL];
+#pragma unroll
+    for (int t = 0; t < KL; ++t) {
+      const uint32_t u = __builtin_bit_cast(uint32_t, lst[t]);
+      const auto rr = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+      other[t] = __builtin_bit_cast(float, (uint32_t)(half ? rr[0] : rr[1]));
+    }
+#pragma unroll
+    for (int t = 0; t < KL; ++t) list_insert<KL>(lst, other[t]);
+    // certification: a finite threshold (every row in the bound's range, so every value finite) and
+    // the k + 1 best pairwise separated by more than it (with ke = NBf the gap after the last is not
+    // needed)
+    const bool finite = (__builtin_bit_cast(uint32_t, thr) & 0x7F800000u) != 0x7F800000u;  // on the bits
+    bool ok = finite;
+#pragma unroll
+    for (int t = 0; t < KL - 1; ++t)
+      if (t < p.ke) ok = ok && (t + 1 == p.NBf || lst[t] - lst[t + 1] > thr);
+    if (half == 0) {
+      if (ok) {
+        int32_t* o = outb + qloc * 33 + fl * p.ke;
+#pragma unroll
+        for (int t = 0; t < KL - 1; ++t)
+          if (t < p.ke) o[t] = f * p.NBf + tag_key(lst[t]);
+      } else if (qvalid) {
+        // candidates: list entries within thr of the k-th best, or every key when an entry past the
+        // list could be one (the last entry is within thr too), the threshold is not finite, or the
+        // whole frame is selected
+        float kth = lst[0];
+#pragma unroll
+        for (int t = 1; t < KL; ++t)
+          if (t < p.ke) kth = lst[t];
+        uint32_t mask = 0;
+#pragma unroll
+        for (int t = 0; t < KL; ++t)
+          if (lst[t] >= kth - thr) mask |= 1u << tag_key(lst[t]);
+        if (!finite || p.ke >= p.NBf || lst[KL - 1] >= kth - thr) mask = all_keys;
+        const uint32_t at = atomicAdd(&qcount, 1u);
+        queue[at] = u32x2{((uint32_t)qloc << 16) | (uint32_t)fl, mask};
+      }
+    }
+  }
+  __syncthreads();
+  // the certified lists (listed pairs' slots hold stale values that the exact pass overwrites)
+  const int run = nf * p.ke;  // ints per query
+  for (int e = tid; e < 128 * run; e += 256) {
+    const int q = e / run, o = e - q * run;
+    const int64_t i = (int64_t)bid_x() * 128 + q;
+    if (i < NB) p.idx[((int64_t)hs * NB + i) * ((int64_t)p.F * p.ke) + (int64_t)f0 * p.ke + o] = outb[q * 33 + o];
+  }
+  // the listed pairs to the global list: one atomic per workgroup reserves its range
+  const uint32_t nq = qcount;
+  if (tid == 0) gbase = nq ? atomicAdd(p.qcount, nq) : 0u;
+  __syncthreads();
+  for (uint32_t e = tid; e < nq; e += 256) {
+    const u32x2 ent = queue[e];
+    p.queue[gbase + e] = u32x4{(uint32_t)((int64_t)hs * NB + (int64_t)bid_x() * 128 + (ent[0] >> 16)),
+                               (uint32_t)(f0 + (int)(ent[0] & 0xFFFF)), ent[1], 0u};
+  }
+}
+
+__global__ void select_clear_kernel(uint32_t* count) {
+  if (tid_x() == 0) *count = 0;
+}
+
+// The listed pairs, exactly: a persistent grid, one pair per half wave at a time. Lane (half, j)
+// computes the sequential fmaf score of key block j of the pair's frame when j is a candidate; the
+// candidates are ranked by the composite key through LDS (non-candidates hold key 0, below every
+// real key), and the k best written in order.
+__global__ __launch_bounds__(256) void block_select_exact_kernel(SelMfmaParams p) {
+  __shared__ __align__(16) uint64_t keys[8][32];
+  const int tid = tid_x(), lane = tid & 63, w = tid >> 6, col = lane & 31, half = lane >> 5;
+  const int slot = 2 * w + half;
+  const uint32_t nq = *p.qcount;
+  const int64_t NB = p.NB;
+  const int j = col < p.NBf ? col : p.NBf - 1;
+  const uint32_t stride = (uint32_t)gridDim.x * 8;
+  for (uint32_t e0 = (uint32_t)bid_x() * 8; e0 < nq; e0 += stride) {  // the same trips for every lane
+    const uint32_t e = e0 + (uint32_t)slot;
+    const bool act = e < nq;
+    const u32x4 ent = p.queue[act ? e : e0];
+    const int64_t hq = ent[0];  // head * NB + query block
+    const int64_t hs = hq / NB, i = hq - hs * NB;
+    const int f = (int)ent[1];
+    const bool cand = act && col < p.NBf && ((ent[2] >> col) & 1u);
+    uint64_t key = 0;
+    if (cand) {
+      const f32x4* qr = reinterpret_cast<const f32x4*>(p.mean + (hs * 2 * NB + i) * 64);
+      const f32x4* kv = reinterpret_cast<const f32x4*>(p.mean + ((hs * 2 + 1) * NB + (int64_t)f * p.NBf + j) * 64);
+      f32x4 qa[16], kb[16];  // both rows in flight at once, then the chain
+#pragma unroll
+      for (int d4 = 0; d4 < 16; ++d4) {
+        qa[d4] = qr[d4];
+        kb[d4] = kv[d4];
+      }
+      float acc = 0.f;
+#pragma unroll
+      for (int d4 = 0; d4 < 16; ++d4) {
+        acc = __builtin_fmaf(qa[d4][0], kb[d4][0], acc);
+        acc = __builtin_fmaf(qa[d4][1], kb[d4][1], acc);
+        acc = __builtin_fmaf(qa[d4][2], kb[d4][2], acc);
+        acc = __builtin_fmaf(qa[d4][3], kb[d4][3], acc);
+      }
+      key = ckey(acc, (uint32_t)j);
+    }
+    keys[slot][col] = key;
+    __builtin_amdgcn_wave_barrier();
+    asm volatile("" ::: "memory");
+    int rank = 0;  // every slot's key read at once
+#pragma unroll
+    for (int c = 0; c < 32; c += 2) {
+      const u32x4 kk = *reinterpret_cast<const u32x4*>(&keys[slot][c]);
+      rank += ((((uint64_t)kk[1] << 32) | kk[0]) > key) + ((((uint64_t)kk[3] << 32) | kk[2]) > key);
+    }
+    if (cand && rank < p.ke) p.idx[hq * ((int64_t)p.F * p.ke) + (int64_t)f * p.ke + rank] = f * p.NBf + j;
+    __builtin_amdgcn_wave_barrier();
+    asm volatile("" ::: "memory");
+  }
+}
+
+// Split records of given fp32 pooled rows (one wave per row): the input of the matrix-core select
+// for means that did not come from saf3r_pack_qkv.
+__global__ __launch_bounds__(256) void pooled_prepare_kernel(const float* __restrict__ mean, int64_t rows,
+                                                             uint16_t* __restrict__ split, float* __restrict__ meta) {
+  const int64_t r = (int64_t)bid_x() * 4 + (tid_x() >> 6);
+  if (r >= rows) return;  // a whole wave leaves; no barrier follows
+  const int lane = tid_x() & 63;
+  pooled_split_row(mean[r * 64 + lane], lane, split + r * 128, meta + r * 2);
+}
+
+template <int KL>
+static void launch_select_mfma(int ng, dim3 grid, hipStream_t st, const SelMfmaParams& p) {
+  switch (ng) {
+    case 1: hipLaunchKernelGGL((block_select_mfma_kernel<KL, 1>), grid, dim3(256), 0, st, p); break;
+    case 2: hipLaunchKernelGGL((block_select_mfma_kernel<KL, 2>), grid, dim3(256), 0, st, p); break;
+    case 3: hipLaunchKernelGGL((block_select_mfma_kernel<KL, 3>), grid, dim3(256), 0, st, p); break;
+    default: hipLaunchKernelGGL((block_select_mfma_kernel<KL, 4>), grid, dim3(256), 0, st, p); break;
+  }
+}
+
+// frames per workgroup of the matrix-core select for this k: 32 / (list length - 1)
+static int select_fpw(int ke) { return ke <= 4 ? 8 : ke <= 8 ? 4 : 2; }
+
+}  // namespace saf3r
+
+using namespace saf3r;
+
+extern "C" int saf3r_pooled_prepare(const float* mean, int64_t rows, uint16_t* split, float* meta, void* stream) {
+  if (int e = injected("saf3r_pooled_prepare")) return e;
+  if (!mean || !split || !meta || rows < 0) return fail(SAF3R_ERR_INVALID, "saf3r_pooled_prepare: bad arguments");
+  if (((uintptr_t)mean | (uintptr_t)split | (uintptr_t)meta) % 16)
+    return fail(SAF3R_ERR_INVALID, "saf3r_pooled_prepare: buffers must be 16-byte aligned");
+  if (rows == 0) return SAF3R_OK;
+  if ((rows + 3) / 4 > 0x7fffffff) return fail(SAF3R_ERR_INVALID, "saf3r_pooled_prepare: too many rows");
+  hipLaunchKernelGGL(pooled_prepare_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, (hipStream_t)stream, mean,
+                     rows, split, meta);
+  return check_launch("saf3r_pooled_prepare");
+}
+
+extern "C" int64_t saf3r_block_select_pooled_workspace_bytes(int n, int frames, int blocks_per_frame, int k) {
+  if (n <= 0 || n > 65535 || frames <= 0 || blocks_per_frame <= 0 || blocks_per_frame > 32 ||
+      (int64_t)frames * blocks_per_frame > 0x7fffffff / 64 || k < 1 || k > 32)
+    return -1;
+  const int ke = k < blocks_per_frame ? k : blocks_per_frame;
+  if (ke > 16) return 0;  // the sequential kernel: no workspace
+  // a 16-byte count slot, then one 16-byte entry per (query block, frame) pair: the worst case
+  return 16 + (int64_t)n * frames * blocks_per_frame * frames * 16;
+}
+
+extern "C" int saf3r_block_select_pooled(const float* mean, const uint16_t* split, const float* meta, int n,
+                                         int frames, int blocks_per_frame, int k, int32_t* idx, void* workspace,
+                                         int64_t workspace_bytes, void* stream) {
+  if (int e = injected("saf3r_block_select_pooled")) return e;
+  if (!mean || !split || !meta || !idx) return fail(SAF3R_ERR_INVALID, "saf3r_block_select_pooled: null pointer");
+  if (((uintptr_t)mean | (uintptr_t)split | (uintptr_t)meta) % 16)
+    return fail(SAF3R_ERR_INVALID, "saf3r_block_select_pooled: pooled buffers must be 16-byte aligned");
+  if (n <= 0 || n > 65535 || frames <= 0 || blocks_per_frame <= 0 ||
+      (int64_t)frames * blocks_per_frame > 0x7fffffff / 64)
+    return fail(SAF3R_ERR_INVALID, "saf3r_block_select_pooled: bad shape");
+  if (k < 1 || k > 32) return fail(SAF3R_ERR_UNSUPPORTED, "saf3r_block_select_pooled: k must be in [1, 32] (got %d)", k);
+  if (blocks_per_frame > 32)
+    return fail(SAF3R_ERR_UNSUPPORTED, "saf3r_block_select_pooled: at most 32 blocks per frame");
+  const int NBf = blocks_per_frame, ke = k < NBf ? k : NBf;
+  const int NB = frames * NBf;
+  hipStream_t st = (hipStream_t)stream;
+  if (ke > 16) {  // lists longer than the matrix-core path keeps: the sequential selection, head by head
+    for (int h = 0; h < n; ++h) {
+      const float* pq = mean + (int64_t)h * 2 * NB * 64;
+      if (int rc = saf3r_block_select(pq, pq + (int64_t)NB * 64, 1, NB, frames, NBf, k, 0,
+                                      idx + (int64_t)h * NB * frames * ke, stream))
+        return rc;
+    }
+    return SAF3R_OK;
+  }
+  const int64_t need = saf3r_block_select_pooled_workspace_bytes(n, frames, blocks_per_frame, k);
+  if (!workspace || workspace_bytes < need || (uintptr_t)workspace % 16)
+    return fail(SAF3R_ERR_INVALID,
+                "saf3r_block_select_pooled: needs a 16-byte aligned workspace of %lld bytes "
+                "(saf3r_block_select_pooled_workspace_bytes), got %lld",
+                (long long)need, (long long)(workspace ? workspace_bytes : 0));
+  const int fpw = select_fpw(ke);
+  const dim3 grid((unsigned)((NB + 127) / 128), (unsigned)((frames + fpw - 1) / fpw), (unsigned)n);
+  SelMfmaParams p;
+  p.mean = mean;
+  p.split = split;
+  p.meta = meta;
+  p.idx = idx;
+  p.qcount = static_cast<uint32_t*>(workspace);
+  p.queue = reinterpret_cast<u32x4*>(static_cast<char*>(workspace) + 16);
+  p.F = frames;
+  p.NBf = NBf;
+  p.NB = NB;
+  p.ke = ke;
+  const int ng = (NBf + 7) / 8;
+  hipLaunchKernelGGL(select_clear_kernel, dim3(1), dim3(64), 0, st, p.qcount);
+  if (ke <= 4) launch_select_mfma<5>(ng, grid, st, p);
+  else if (ke <= 8) launch_select_mfma<9>(ng, grid, st, p);
+  else launch_select_mfma<17>(ng, grid, st, p);
+  if (int rc = check_launch("saf3r_block_select_pooled")) return rc;
+  hipLaunchKernelGGL(block_select_exact_kernel, dim3(kSelExactWGs), dim3(256), 0, st, p);
+  return check_launch("saf3r_block_select_pooled");
+}

@@ -222,6 +222,7 @@ def pack_qkv(q, k, v, tok_stride: int, head_stride: int, geom: Geometry, num_hea
         pos = pos.to(device=q.device, dtype=torch.int32).contiguous()
         npos = int(rope_positions) if rope_positions is not None else int(pos.max().item()) + 1
         rc, rs = rope_tables(npos, rope_base, q.device)
+    _mark("pack_qkv", "start")
     _lib.check(lib.saf3r_pack_qkv(
         _ptr(q), _ptr(k), _ptr(v), tok_stride, head_stride, geom.frames, geom.tokens_per_frame, geom.num_special,
         num_heads, _ptr(qw), _ptr(qb), _ptr(kw), _ptr(kb), float(ln_eps), int(apply_ln),
@@ -230,6 +231,7 @@ def pack_qkv(q, k, v, tok_stride: int, head_stride: int, geom: Geometry, num_hea
         _ptr(qk32), _u8_flags(q_scaled, num_heads), float(prescale_factor() if q_scale is None else q_scale),
         _u8_flags(pool_flags, num_heads), _ptr(pooled.mean if pooled else None),
         _ptr(pooled.split if pooled else None), _ptr(pooled.meta if pooled else None), _lib.stream_ptr()))
+    _mark("pack_qkv", "end")
     res = (qp, kp, vp) + ((qk32,) if fp32_heads is not None else ()) + ((pooled,) if pooled is not None else ())
     return res
 
@@ -283,18 +285,31 @@ def pooled_prepare(mean: torch.Tensor) -> Pooled:
     return res
 
 
+_select_ws = {}  # (device, bytes) -> the selection's workspace, kept for the next call of the same size
+
+
 def block_select_pooled(pooled: Pooled, frames: int, blocks_per_frame: int, k: int) -> torch.Tensor:
     """Per-frame block top-k on the matrix cores (``saf3r_block_select_pooled``), bit-identical to
-    ``block_select`` on ``pooled.mean``: int32 [n, NB, frames*min(k, NBf)] of global block ids."""
+    ``block_select`` on ``pooled.mean``: int32 [n, NB, frames*min(k, NBf)] of global block ids. The
+    workspace (queues of the pairs taken exactly) is a torch allocation kept per device and size."""
     _need_cuda(pooled.mean, pooled.split, pooled.meta)
     lib = _lib.load()
     n, _, nb, _ = pooled.mean.shape
     if nb != frames * blocks_per_frame:
         raise ValueError("pooled records do not match frames * blocks_per_frame")
-    idx = torch.empty(n, nb, frames * min(k, blocks_per_frame), dtype=torch.int32, device=pooled.mean.device)
+    dev = pooled.mean.device
+    idx = torch.empty(n, nb, frames * min(k, blocks_per_frame), dtype=torch.int32, device=dev)
+    nbytes = lib.saf3r_block_select_pooled_workspace_bytes(n, frames, blocks_per_frame, k)
+    if nbytes < 0:
+        raise ValueError(f"unsupported block selection: {n} heads, {frames} frames x {blocks_per_frame} blocks, k {k}")
+    key = (dev.index, int(nbytes))
+    ws = _select_ws.get(key)
+    if ws is None and nbytes:
+        ws = _select_ws[key] = torch.empty(nbytes, dtype=torch.uint8, device=dev)
     _mark("block_select", "start")
     _lib.check(lib.saf3r_block_select_pooled(_ptr(pooled.mean), _ptr(pooled.split), _ptr(pooled.meta), n, frames,
-                                             blocks_per_frame, k, _ptr(idx), _lib.stream_ptr()))
+                                             blocks_per_frame, k, _ptr(idx), _ptr(ws), int(nbytes),
+                                             _lib.stream_ptr()))
     _mark("block_select", "end")
     return idx
 

@@ -112,8 +112,10 @@ class BaseHeadwiseSparseAttentionWrapper(nn.Module):
         T = self.patch_height * self.patch_width + self.num_special_tokens
         return Geometry.from_tokens(num_tokens, T, self.num_special_tokens)
 
-    def compute_multihead_attention_packed(self, qkv: torch.Tensor, pos, geom: Geometry) -> torch.Tensor:
-        """qkv: bf16 [N, 3*H*64] (the qkv Linear output). Returns bf16 [N, H*64]."""
+    def pack(self, qkv: torch.Tensor, pos, geom: Geometry, pool: bool = True):
+        """``saf3r_pack_qkv`` of this layer: QK-LayerNorm + RoPE-2D + the per-head layouts, Q with the
+        softmax scale where flagged, the fp32 rows of the probe / dino heads, and (``pool``) the block
+        means of the block_topk heads. Returns ``ops.pack_qkv``'s tuple."""
         om = self.orig_module
         H = self.num_heads
         C = H * HEAD_DIM
@@ -134,14 +136,22 @@ class BaseHeadwiseSparseAttentionWrapper(nn.Module):
         # dense heads: unpadded token-order tiles; frame-relative heads: whole frames per tile run
         tord = ops.token_order_heads(self.patterns, geom)
         f32 = [h in self.fp32_slot for h in range(H)] if self.fp32_heads else None
-        qs = self.q_scaled_heads()
         # block_topk heads: the pack also writes their pooled block records (means of bf16 q / k)
-        packed = ops.pack_qkv(qkv, qkv[:, C:], qkv[:, 2 * C:], 3 * C, HEAD_DIM, geom, H, ln_q=ln_q, ln_k=ln_k,
-                              ln_eps=eps, pos=p2, rope_base=base, rope_positions=npos, token_order=tord, fp32_heads=f32,
-                              q_scaled=qs, q_scale=ops.prescale_factor(getattr(om, "scale", None)),
-                              pool_heads=self.dyn_heads or None)
+        return ops.pack_qkv(qkv, qkv[:, C:], qkv[:, 2 * C:], 3 * C, HEAD_DIM, geom, H, ln_q=ln_q, ln_k=ln_k,
+                            ln_eps=eps, pos=p2, rope_base=base, rope_positions=npos, token_order=tord, fp32_heads=f32,
+                            q_scaled=self.q_scaled_heads(), q_scale=ops.prescale_factor(getattr(om, "scale", None)),
+                            pool_heads=(self.dyn_heads or None) if pool else None)
+
+    def compute_multihead_attention_packed(self, qkv: torch.Tensor, pos, geom: Geometry) -> torch.Tensor:
+        """qkv: bf16 [N, 3*H*64] (the qkv Linear output). Returns bf16 [N, H*64]."""
+        om = self.orig_module
+        H = self.num_heads
+        C = H * HEAD_DIM
+        tord = ops.token_order_heads(self.patterns, geom)
+        qs = self.q_scaled_heads()
+        packed = self.pack(qkv, pos, geom)
         qp, kp, vp = packed[:3]
-        qk32 = packed[3] if f32 is not None else None
+        qk32 = packed[3] if self.fp32_heads else None
         sel = None
         if self.dyn_heads:
             pooled = packed[-1]
