@@ -232,9 +232,11 @@ int saf3r_pooled_prepare(const float* mean, int64_t rows, uint16_t* split, float
  * by a second kernel.
  *   workspace / workspace_bytes: caller-owned device memory of at least
  *     saf3r_block_select_pooled_workspace_bytes(n, frames, blocks_per_frame, k) bytes, 16-byte
- *     aligned (the per-workgroup queues of the pairs taken exactly). Needs no clearing; calls that
- *     share a workspace must be ordered (one stream).
- * 1 <= k <= 32, blocks_per_frame <= 32 (k > 16 runs the sequential kernel on the means).
+ *     aligned: a count and the list of the pairs taken exactly (16 bytes per pair, room for every
+ *     pair). The call resets the count itself with a one-thread kernel on the stream (no memset), so
+ *     the workspace needs no clearing; calls that share a workspace must be ordered (one stream).
+ * 1 <= k <= 32, blocks_per_frame <= 32 (k > 16 runs the sequential kernel on the means), at most
+ * 2^32 (query block, frame) pairs over the n heads (SAF3R_ERR_UNSUPPORTED beyond).
  * Replaces: the block top-k of the dynamic pattern (no reference symbol; per-frame semantics of
  *           saf3r/patch/wrapper.py:48 and saf3r/triton/fused_qk_topk.py:120-217 at block level).
  */

@@ -224,7 +224,7 @@ static int cmp_u64_desc(const void* a, const void* b) {
  */
 int oracle_keyset(const float* scores, int N, int T, int ns, int mode, int param, int start, int include,
                   int32_t* out) {
-    if (N <= 0 || T <= 0 || param <= 0) return -1;
+    if (N <= 0 || T <= 0 || param <= 0 || (mode == 0 && start < 0)) return -1;
     unsigned char* in = (unsigned char*)calloc((size_t)N, 1);
     if (!in) return -2;
     if (mode == 0) {

@@ -112,19 +112,23 @@ struct Geom {
 
 inline bool make_geom(int F, int T, int ns, Geom* g) {
   if (F <= 0 || T <= 0 || ns < 0 || ns >= T) return false;
+  // sizes in 64 bits first: every count kept in 32 bits below must fit
+  const int64_t P = (int64_t)T - ns, NBf = (P + kBlock - 1) / kBlock, Pp = NBf * kBlock;
+  const int64_t S = (int64_t)F * ns, Sp = (S + kBlock - 1) / kBlock * kBlock;
+  const int64_t L = Sp + (int64_t)F * Pp;
+  if (Pp > 0x7fffffff || Sp > 0x7fffffff || L / kBlock > 0x7fffffff) return false;
   g->F = F;
   g->T = T;
   g->ns = ns;
-  g->P = T - ns;
-  g->NBf = (g->P + kBlock - 1) / kBlock;
-  g->Pp = g->NBf * kBlock;
-  g->S = F * ns;
-  g->Sp = (g->S + kBlock - 1) / kBlock * kBlock;
-  g->nst = g->Sp / kBlock;
-  g->L = (int64_t)g->Sp + (int64_t)F * g->Pp;
-  if (g->L / kBlock > (int64_t)0x7fffffff) return false;
-  g->NT = (int)(g->L / kBlock);
-  g->NBT = (T + kBlock - 1) / kBlock;
+  g->P = (int)P;
+  g->NBf = (int)NBf;
+  g->Pp = (int)Pp;
+  g->S = (int)S;
+  g->Sp = (int)Sp;
+  g->nst = (int)(Sp / kBlock);
+  g->L = L;
+  g->NT = (int)(L / kBlock);
+  g->NBT = (int)(((int64_t)T + kBlock - 1) / kBlock);
   return true;
 }
 

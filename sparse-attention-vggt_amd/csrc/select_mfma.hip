@@ -359,6 +359,8 @@ extern "C" int64_t saf3r_block_select_pooled_workspace_bytes(int n, int frames, 
     return -1;
   const int ke = k < blocks_per_frame ? k : blocks_per_frame;
   if (ke > 16) return 0;  // the sequential kernel: no workspace
+  // the list's count and its (head * NB + query block) entries are 32-bit
+  if ((int64_t)n * frames * blocks_per_frame * frames > 0xFFFFFFFFll) return -1;
   // a 16-byte count slot, then one 16-byte entry per (query block, frame) pair: the worst case
   return 16 + (int64_t)n * frames * blocks_per_frame * frames * 16;
 }
@@ -389,6 +391,8 @@ extern "C" int saf3r_block_select_pooled(const float* mean, const uint16_t* spli
     return SAF3R_OK;
   }
   const int64_t need = saf3r_block_select_pooled_workspace_bytes(n, frames, blocks_per_frame, k);
+  if (need < 0)
+    return fail(SAF3R_ERR_UNSUPPORTED, "saf3r_block_select_pooled: more than 2^32 (query block, frame) pairs");
   if (!workspace || workspace_bytes < need || (uintptr_t)workspace % 16)
     return fail(SAF3R_ERR_INVALID,
                 "saf3r_block_select_pooled: needs a 16-byte aligned workspace of %lld bytes "
