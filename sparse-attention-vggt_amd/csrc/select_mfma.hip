@@ -7,23 +7,23 @@
 // Score of query block i and key block j: the sequential fmaf chain s_ij = q_i . k_j over the fp32
 // block means. The kernel computes an approximation from the fp16 split records (pooled_split_row
 // in common.h: x 2^s = h1 + h2 + r, |r| <= 2^-22 |x 2^s|):
-//   A_ij = Q1 K1^T + (Q1 K2^T + Q2 K1^T)   (two fp32 accumulators on v_mfma_f32_32x32x16_f16),
+//   A_ij = Q1 K1^T, then + Q1 K2^T + Q2 K1^T   (one fp32 accumulator, 12 v_mfma_f32_32x32x16_f16),
 //   a_ij = A_ij 2^-(sq_i + sk_j).
 // Error bound (u = 2^-24; sums taken as any order of fp32 additions with relative error <= 2u):
-//   MFMA sums of 64 exact fp16 products: 63 * 2^-23 sum|q k|; the small accumulator: 2^-18 of that;
-//   the dropped terms (h2 h2', h r', r h'): 3 * 2^-22 sum|q k|; the fmaf chain of the oracle:
-//   63 * 2^-24 sum|q k|; fp16 values below the normal range: 2^-25 |q| |k|; the final additions:
-//   2^-22 |q| |k|. In all less than 1.3e-5 |q| |k| (sum|q k| <= |q| |k|), so
-//   |a_ij - s_ij| <= E_ij = 2^-15 |q_i| |k_j| with a factor of 2 to spare.
+//   the accumulator's 192 exact fp16 products: 191 * 2^-23 (1 + 2^-10) sum|q k|; the dropped terms
+//   (h2 h2', h r', r h'): 3 * 2^-22 sum|q k|; the fmaf chain of the oracle: 63 * 2^-24 sum|q k|;
+//   fp16 values below the normal range: 2^-25 |q| |k|; the scaling is exact. In all less than
+//   2.8e-5 |q| |k| (sum|q k| <= |q| |k|), so |a_ij - s_ij| <= E_ij = 2^-15 |q_i| |k_j| (3.05e-5).
 // A (query block, frame) is certified when its k + 1 best approximate scores (by a, each carrying
-// its key index in the 5 low mantissa bits: a change of at most 2^-18 |a|) are separated pairwise by
-// more than thr = 2 E_max + 2^-17 |q| |k|max (E_max over the frame's key blocks): the exact scores
-// then have the same order, strictly, so the top-k and its order are those of a. Every other pair
-// (near ties, rows outside the bound's range: norm +inf, which makes the threshold +inf or NaN) goes
-// to a list in the caller's workspace with its candidate keys: those whose tagged a is within thr
-// of the k-th best (the true top-k is among them: any other key's exact score is below the k-th
-// best's approximation minus E), or every key of the frame when the list's last entry is also
-// within thr (keys outside the list may then qualify) or the threshold is not finite.
+// a tag in the 5 low mantissa bits that names the key: a change of at most 2^-18 |a|) are separated
+// pairwise by more than thr = 2 E_max + 2^-17 |q| |k|max (E_max over the frame's key blocks): the
+// exact scores then have the same order, strictly, so the top-k and its order are those of a. Every
+// other pair (near ties, rows outside the bound's range: norm +inf, which makes the threshold +inf
+// or NaN; a zero threshold, where the tags alone would order exact ties) goes to a list in the caller's workspace with its candidate keys: those whose tagged a is
+// at least lo = (k-th best tagged a) - thr, which hold the true top-k (its members' exact scores are
+// at least the k-th best's approximation minus E). Each half wave's own list of its KL best tells
+// which of its keys qualify; when its last entry is at least lo, keys past it may too, and every
+// key of that half is a candidate (every key of the frame when the threshold is not finite or zero).
 // block_select_exact_kernel ranks the candidates by their sequential fmaf scores and the composite
 // key (score key, lower index first), as the oracle does (about 1.3% of the pairs at 128 frames on
 // random-init weights).
@@ -36,7 +36,9 @@
 // against its 32 queries: lane (col, half) holds query col and 16 key rows 8 g + 4 half + r; each
 // tagged value is inserted into a sorted list of the KL best (one max and KL - 1 med3 per value),
 // the two halves merge their lists through v_permlane32_swap, and the gaps of the merged list
-// decide the pair. The key scales and the frames' largest key norms are staged in LDS once per
+// decide the pair. A lane's own values carry tag v (its value index 4 g + r); entries taken from the
+// other half get tag bit 4 set, so a half-0 lane reads key 8 (t & 15) / 4 + 4 (t >> 4) + (t & 3)
+// back from tag t. The key scales and the frames' largest key norms are staged in LDS once per
 // workgroup; the certified lists are kept in LDS and written after the frame loop, so that no
 // global store sits between the ring's loads and their waits. The file is compiled without NaN
 // semantics (no canonicalisation before max / med3): every value in a certified pair is finite, and
@@ -45,9 +47,13 @@
 
 namespace saf3r {
 
-constexpr int kSelRing = 3;          // LDS ring stages (frames)
-constexpr int kSelStage = 32 * 256;  // bytes per stage: 32 key rows of 256 bytes
+constexpr int kSelRing = 5;          // LDS ring stages (frames): four frames in flight
 constexpr int kSelExactWGs = 2048;   // persistent grid of the exact pass
+constexpr int kSelQueue = 512;       // LDS queue entries per workgroup (listed pairs; more spill over)
+// empty list slots and key rows past the frame: the lowest finite float, whose low mantissa bits
+// are all set, so that tagging it (an OR into those bits) leaves it unchanged and never makes a NaN;
+// with k <= NBf such entries never take part in a certified order
+constexpr float kSelPad = -0x1.fffffep127f;
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
@@ -70,29 +76,47 @@ __device__ inline void list_insert(float (&a)[KL], float x) {
   a[0] = fmaxf(a[0], x);
 }
 
-__device__ inline int tag_key(float v) { return 31 - (int)(__builtin_bit_cast(uint32_t, v) & 31u); }
+// key block (within the frame) of a tagged value in a half-0 lane's merged list
+__device__ inline int tag_key(float v) {
+  const int t = (int)(__builtin_bit_cast(uint32_t, v) & 31u);
+  return 8 * ((t & 15) >> 2) + 4 * (t >> 4) + (t & 3);
+}
 
 // LDS byte offset of 16-byte chunk c of key row r in a ring stage
 __device__ inline int sel_chunk(int r, int c) { return (r * 16 + (c ^ (r & 15))) * 16; }
 
 // KL: list length (k + 1 rounded up: 5, 9, 17); NG: groups of 8 key blocks per frame (ceil(NBf / 8)).
-// FPW = 32 / (KL - 1) frames per workgroup; about 45 KB of LDS: three workgroups per CU.
+// FPW = 32 / (KL - 1) frames per workgroup (a workgroup's lists are staged in LDS, one byte per
+// entry); about 38 KB of LDS.
+//
+// Workgroup order (blockIdx.x = r + 8 (j + cm qt), cm = ceil(G / 8) for G frame groups): the
+// hardware hands workgroups to the 8 XCDs in turn, so r is the XCD, and XCD r takes the frame
+// groups g = r + 8 j only. Each XCD's L2 then holds the key records of 1/8 of the frames (about
+// 0.6 MB for 7 heads at 128 frames) for every query tile, instead of all of them.
 template <int KL, int NG>
 __global__ __launch_bounds__(256) void block_select_mfma_kernel(SelMfmaParams p) {
   constexpr int FPW = 32 / (KL - 1);
-  __shared__ __align__(16) char ring[kSelRing * kSelStage];
-  __shared__ int32_t outb[128 * 33];  // [query][frame in group * ke + t], rows of 33: no bank conflicts
-  __shared__ __align__(16) float ksc[FPW][32];  // 2^-sk of the frame's key blocks (1 past NBf)
+  constexpr int OPB = 36;  // bytes per query row of the staged lists (9 words: no bank conflicts)
+  constexpr int kStage = NG * 8 * 256;  // bytes per ring stage: 8 NG key rows of 256 bytes
+  __shared__ __align__(16) char ring[kSelRing * kStage];
+  // [query][frame in group * ke + t]: the key block in its frame; for a listed pair the first byte is
+  // kQueued (its entry is in the queue) or kSpilled (the queue was full: listed with every key)
+  __shared__ __align__(16) uint8_t outb[128 * OPB];
+  __shared__ __align__(16) float ksc[FPW][32];  // 2^-sk of the frame's key blocks (0 past NBf)
   __shared__ float nkm[FPW];                    // the frame's largest key norm bound
-  __shared__ u32x2 queue[128 * FPW];            // (query in the group, frame in the group), candidate mask
+  __shared__ u32x2 queue[kSelQueue];            // (query in the group, frame in the group), candidate mask
   __shared__ uint32_t qcount, gbase;
+  constexpr uint8_t kQueued = 0xFE, kSpilled = 0xFF;
   const int tid = tid_x(), lane = tid & 63, w = tid >> 6, col = lane & 31, half = lane >> 5;
   const int hs = bid_z();
-  const int f0 = bid_y() * FPW, f1 = min(p.F, f0 + FPW);
+  const int G = (p.F + FPW - 1) / FPW, cm = (G + 7) / 8;
+  const int xr = bid_x() & 7, xj = (bid_x() >> 3) % cm, qt = (bid_x() >> 3) / cm;
+  const int f0 = (xr + 8 * xj) * FPW, f1 = min(p.F, f0 + FPW);
+  if (f0 >= p.F) return;  // an empty slot of the XCD order: the whole workgroup leaves
   const int nf = f1 - f0;
   const int64_t NB = p.NB;
   const int qloc = 32 * w + col;  // query block within the workgroup
-  const int64_t qi = (int64_t)bid_x() * 128 + qloc;
+  const int64_t qi = (int64_t)qt * 128 + qloc;
   const bool qvalid = qi < NB;
   const int64_t qrec = (int64_t)hs * 2 * NB + (qvalid ? qi : NB - 1);  // tensor 0 = q
   const int64_t krec0 = ((int64_t)hs * 2 + 1) * NB;                   // tensor 1 = k
@@ -123,17 +147,21 @@ __global__ __launch_bounds__(256) void block_select_mfma_kernel(SelMfmaParams p)
   }
   __syncthreads();
 
-  // ring fill: thread t copies LDS chunks t and 256 + t of the stage (row = chunk / 16, the global
-  // chunk through the swizzle; rows past NBf repeat the frame's last row)
+  // ring fill: every thread issues two 16-byte copies per frame (the same count in every wave, which
+  // the waits below rely on): thread t copies LDS chunks (256 u + t) mod 128 NG of the stage (row =
+  // chunk / 16, the global chunk through the swizzle; rows past NBf repeat the frame's last row;
+  // with fewer than 512 chunks some copies repeat others, same data to the same place). 128 NG is a
+  // multiple of 64, so a wave's chunks stay contiguous from its base.
   const uint32_t ring_base = lds_addr(ring);
   auto fill = [&](int f) {
-    const uint32_t st = ring_base + (uint32_t)(((f - f0) % kSelRing) * kSelStage);
+    const uint32_t st = ring_base + (uint32_t)(((f - f0) % kSelRing) * kStage);
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-      const int pos = 256 * u + tid, r = pos >> 4, c = (pos & 15) ^ (r & 15);
+      const int base = (256 * u + 64 * w) % (NG * 128), pos = base + lane;
+      const int r = pos >> 4, c = (pos & 15) ^ (r & 15);
       const int rr = r < p.NBf ? r : p.NBf - 1;
       const uint16_t* src = p.split + (krec0 + (int64_t)f * p.NBf + rr) * 128 + 8 * c;
-      dma16(src, st + (uint32_t)(4096 * u + 1024 * w));
+      dma16(src, st + (uint32_t)(16 * base));
     }
   };
   for (int j = 0; j < kSelRing - 1; ++j)
@@ -142,35 +170,54 @@ __global__ __launch_bounds__(256) void block_select_mfma_kernel(SelMfmaParams p)
   // threshold factor in units of A 2^-sk: 2 E + the tag truncation (2^-17 |q| |k|), times 2^sq
   const float cq = (0x1p-14f + 0x1p-17f) * qm.x / qm.y;
   const int kr = col < p.NBf ? col : p.NBf - 1;  // this lane's key row
-  uint32_t tagc[NG * 4];                         // 31 - key of every value this lane holds
-#pragma unroll
-  for (int v = 0; v < NG * 4; ++v) tagc[v] = (uint32_t)(31 - (8 * (v >> 2) + 4 * half + (v & 3)));
   const uint32_t all_keys = p.NBf >= 32 ? 0xFFFFFFFFu : (1u << p.NBf) - 1u;
+  const uint32_t half0_keys = all_keys & 0x0F0F0F0Fu, half1_keys = all_keys & 0xF0F0F0F0u;
 
-  for (int f = f0; f < f1; ++f) {
-    const int fl = f - f0;
-    // frame f's copy landed (the next frame's copy may still be in flight: the loop issues no other
-    // vector memory operation), then every wave is past frame f - 1, whose stage the copy of frame
-    // f + 2 reuses
-    if (f + 1 < f1) wait_vm<2>();
-    else wait_vm<0>();
-    barrier_only();
-    if (f + kSelRing - 1 < f1) fill(f + kSelRing - 1);
-    const char* stg = ring + (fl % kSelRing) * kSelStage;
+  // wait until frame g's copy has landed, with `after` frames issued after it still in flight (two
+  // copies per frame: the loop issues no other vector memory operation)
+  static_assert(kSelRing == 5, "the waits below count up to kSelRing - 2 frames in flight");
+  auto wait_frame = [](int after) {
+    switch (after) {
+      case 3: wait_vm<6>(); break;
+      case 2: wait_vm<4>(); break;
+      case 1: wait_vm<2>(); break;
+      default: wait_vm<0>(); break;
+    }
+  };
+  // K fragments of frame g (ring stage g % kSelRing) and its 12 matrix products
+  auto products = [&](int gl) {
+    const char* stg = ring + (gl % kSelRing) * kStage;
     f16x8 kf[2][4];
 #pragma unroll
     for (int pc = 0; pc < 2; ++pc)
 #pragma unroll
       for (int st = 0; st < 4; ++st)
         kf[pc][st] = *reinterpret_cast<const f16x8*>(stg + sel_chunk(kr, 8 * pc + 4 * half + st));
-    f32x16 a1 = {}, a2 = {};
+    f32x16 a = {};
 #pragma unroll
-    for (int st = 0; st < 4; ++st) a1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[0][st], qf[0][st], a1, 0, 0, 0);
+    for (int st = 0; st < 4; ++st) a = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[0][st], qf[0][st], a, 0, 0, 0);
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
-      a2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[0][st], qf[1][st], a2, 0, 0, 0);
-      a2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[1][st], qf[0][st], a2, 0, 0, 0);
+      a = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[0][st], qf[1][st], a, 0, 0, 0);
+      a = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[1][st], qf[0][st], a, 0, 0, 0);
     }
+    return a;
+  };
+
+  // Software pipeline: the products of frame f + 1 are issued before the list work of frame f, so
+  // the matrix cores run them while the same wave works through the lists.
+  wait_frame(min(kSelRing - 2, f1 - 1 - f0));
+  barrier_only();
+  if (f0 + kSelRing - 1 < f1) fill(f0 + kSelRing - 1);
+  f32x16 acc = products(0);
+  for (int f = f0; f < f1; ++f) {
+    const int fl = f - f0;
+    // frame f + 1's copy landed, and every wave has read frame f's fragments (before this barrier),
+    // so frame f + kSelRing may take its stage; the last frame re-runs its own products (unused)
+    wait_frame(min(kSelRing - 2, f1 - 2 - f));
+    barrier_only();
+    if (f + kSelRing < f1) fill(f + kSelRing);
+    const f32x16 acc_next = products(f + 1 < f1 ? fl + 1 : fl);
     // this lane's key blocks 8 g + 4 half + r: their scales (one 16-byte read per group of four)
     float ks[NG][4];
 #pragma unroll
@@ -182,15 +229,15 @@ __global__ __launch_bounds__(256) void block_select_mfma_kernel(SelMfmaParams p)
     const float thr = cq * nkm[fl];
     float lst[KL];
 #pragma unroll
-    for (int t = 0; t < KL; ++t) lst[t] = -__builtin_huge_valf();
+    for (int t = 0; t < KL; ++t) lst[t] = kSelPad;
 #pragma unroll
     for (int g = 0; g < NG; ++g)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int v = 4 * g + r;
-        const float av = (a1[v] + a2[v]) * ks[g][r];
-        float x = __builtin_bit_cast(float, (__builtin_bit_cast(uint32_t, av) & ~31u) | tagc[v]);
-        if (g == NG - 1) x = 8 * g + 4 * half + r < p.NBf ? x : -__builtin_huge_valf();  // past the frame
+        const float av = acc[v] * ks[g][r];
+        float x = __builtin_bit_cast(float, (__builtin_bit_cast(uint32_t, av) & ~31u) | (uint32_t)v);
+        if (g == NG - 1) x = 8 * g + 4 * half + r < p.NBf ? x : kSelPad;  // past the frame
         list_insert<KL>(lst, x);
       }
     // merge with the other half's list (lanes l and l + 32 hold the same query): the whole partner
@@ -200,57 +247,80 @@ __global__ __launch_bounds__(256) void block_select_mfma_kernel(SelMfmaParams p)
     for (int t = 0; t < KL; ++t) {
       const uint32_t u = __builtin_bit_cast(uint32_t, lst[t]);
       const auto rr = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-      other[t] = __builtin_bit_cast(float, (uint32_t)(half ? rr[0] : rr[1]));
+      other[t] = __builtin_bit_cast(float, (uint32_t)(half ? rr[0] : rr[1]) | 16u);
     }
+    float own[KL];  // this half's list (its candidates, when the pair is listed)
+#pragma unroll
+    for (int t = 0; t < KL; ++t) own[t] = lst[t];
 #pragma unroll
     for (int t = 0; t < KL; ++t) list_insert<KL>(lst, other[t]);
     // certification: a finite threshold (every row in the bound's range, so every value finite) and
     // the k + 1 best pairwise separated by more than it (with ke = NBf the gap after the last is not
     // needed)
+    // (a zero threshold, from a zero query or a frame of zero keys, leaves only the tags to order
+    // exact ties: such pairs are listed with every key)
     const bool finite = (__builtin_bit_cast(uint32_t, thr) & 0x7F800000u) != 0x7F800000u;  // on the bits
-    bool ok = finite;
+    const bool usable = finite && thr > 0.f;
+    bool ok = usable;
 #pragma unroll
     for (int t = 0; t < KL - 1; ++t)
       if (t < p.ke) ok = ok && (t + 1 == p.NBf || lst[t] - lst[t + 1] > thr);
     if (half == 0) {
+      uint8_t* o = outb + qloc * OPB + fl * p.ke;
       if (ok) {
-        int32_t* o = outb + qloc * 33 + fl * p.ke;
 #pragma unroll
         for (int t = 0; t < KL - 1; ++t)
-          if (t < p.ke) o[t] = f * p.NBf + tag_key(lst[t]);
+          if (t < p.ke) o[t] = (uint8_t)tag_key(lst[t]);
       } else if (qvalid) {
-        // candidates: list entries within thr of the k-th best, or every key when an entry past the
-        // list could be one (the last entry is within thr too), the threshold is not finite, or the
-        // whole frame is selected
+        // candidates: each half's entries at least lo; every key of a half whose last entry is at
+        // least lo too (keys past its list may qualify), of the frame when the threshold is not
+        // finite or the whole frame is selected
         float kth = lst[0];
 #pragma unroll
         for (int t = 1; t < KL; ++t)
           if (t < p.ke) kth = lst[t];
+        const float lo = kth - thr;
         uint32_t mask = 0;
 #pragma unroll
-        for (int t = 0; t < KL; ++t)
-          if (lst[t] >= kth - thr) mask |= 1u << tag_key(lst[t]);
-        if (!finite || p.ke >= p.NBf || lst[KL - 1] >= kth - thr) mask = all_keys;
+        for (int t = 0; t < KL; ++t) {
+          if (own[t] >= lo) mask |= 1u << tag_key(own[t]);
+          if (other[t] >= lo) mask |= 1u << tag_key(other[t]);
+        }
+        if (own[KL - 1] >= lo) mask |= half0_keys;
+        if (other[KL - 1] >= lo) mask |= half1_keys;
+        if (!usable || p.ke >= p.NBf) mask = all_keys;
+        mask &= all_keys;
         const uint32_t at = atomicAdd(&qcount, 1u);
-        queue[at] = u32x2{((uint32_t)qloc << 16) | (uint32_t)fl, mask};
+        if (at < (uint32_t)kSelQueue) queue[at] = u32x2{((uint32_t)qloc << 16) | (uint32_t)fl, mask};
+        o[0] = at < (uint32_t)kSelQueue ? kQueued : kSpilled;
       }
     }
+    acc = acc_next;
   }
   __syncthreads();
-  // the certified lists (listed pairs' slots hold stale values that the exact pass overwrites)
-  const int run = nf * p.ke;  // ints per query
-  for (int e = tid; e < 128 * run; e += 256) {
-    const int q = e / run, o = e - q * run;
-    const int64_t i = (int64_t)bid_x() * 128 + q;
-    if (i < NB) p.idx[((int64_t)hs * NB + i) * ((int64_t)p.F * p.ke) + (int64_t)f0 * p.ke + o] = outb[q * 33 + o];
+  // the certified lists, one (query, frame) pair per thread at a time (a listed pair's slots get
+  // stale values that the exact pass overwrites); a spilled pair goes to the global list here
+  const int64_t row = (int64_t)p.F * p.ke;
+  for (int e = tid; e < 128 * nf; e += 256) {
+    const int q = e / nf, fl = e - q * nf;
+    const int64_t i = (int64_t)qt * 128 + q;
+    if (i >= NB) continue;
+    const uint8_t* o = outb + q * OPB + fl * p.ke;
+    int32_t* dst = p.idx + ((int64_t)hs * NB + i) * row + (int64_t)(f0 + fl) * p.ke;
+    const int fb = (f0 + fl) * p.NBf;
+    for (int t = 0; t < p.ke; ++t) dst[t] = fb + o[t];
+    if (o[0] == kSpilled) {
+      const uint32_t at = atomicAdd(p.qcount, 1u);
+      p.queue[at] = u32x4{(uint32_t)((int64_t)hs * NB + i), (uint32_t)(f0 + fl), all_keys, 0u};
+    }
   }
-  // the listed pairs to the global list: one atomic per workgroup reserves its range
-  const uint32_t nq = qcount;
+  // the queued pairs to the global list: one atomic per workgroup reserves its range
+  const uint32_t nq = min(qcount, (uint32_t)kSelQueue);
   if (tid == 0) gbase = nq ? atomicAdd(p.qcount, nq) : 0u;
   __syncthreads();
   for (uint32_t e = tid; e < nq; e += 256) {
     const u32x2 ent = queue[e];
-    p.queue[gbase + e] = u32x4{(uint32_t)((int64_t)hs * NB + (int64_t)bid_x() * 128 + (ent[0] >> 16)),
+    p.queue[gbase + e] = u32x4{(uint32_t)((int64_t)hs * NB + (int64_t)qt * 128 + (ent[0] >> 16)),
                                (uint32_t)(f0 + (int)(ent[0] & 0xFFFF)), ent[1], 0u};
   }
 }
@@ -398,8 +468,8 @@ extern "C" int saf3r_block_select_pooled(const float* mean, const uint16_t* spli
                 "saf3r_block_select_pooled: needs a 16-byte aligned workspace of %lld bytes "
                 "(saf3r_block_select_pooled_workspace_bytes), got %lld",
                 (long long)need, (long long)(workspace ? workspace_bytes : 0));
-  const int fpw = select_fpw(ke);
-  const dim3 grid((unsigned)((NB + 127) / 128), (unsigned)((frames + fpw - 1) / fpw), (unsigned)n);
+  const int fpw = select_fpw(ke), groups = (frames + fpw - 1) / fpw;
+  const dim3 grid((unsigned)(8 * ((groups + 7) / 8) * ((NB + 127) / 128)), 1u, (unsigned)n);
   SelMfmaParams p;
   p.mean = mean;
   p.split = split;
