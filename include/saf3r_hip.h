@@ -151,9 +151,8 @@ int64_t saf3r_packed_slots(int frames, int tokens_per_frame, int num_special);
  *            saf3r_block_select_pooled, for the s-th flagged head (increasing head order), tensor
  *            t = 0 (q) / 1 (k) and patch block b = f*NBf + j at record r = (s*2 + t)*F*NBf + b:
  *              pool_mean[r*64 + d]:  the block mean of bf16(q) (q after LayerNorm and RoPE, without
- *                                    q_scale) or of the packed bf16 k, each feature summed over the
- *                                    block's patch tokens in order in fp32 and divided once by their
- *                                    number (bit-identical to saf3r_block_pool on unscaled rows);
+ *                                    q_scale) or of the packed bf16 k, summed and divided as
+ *                                    saf3r_block_pool does (bit-identical to it on unscaled rows);
  *              pool_split[r*128 ...]: fp16 bits of the mean's two-part split (saf3r_pooled_prepare);
  *              pool_meta[r*2 ...]:    its norm bound and scale (saf3r_pooled_prepare).
  * Replaces: saf3r/patch/patch_vggt.py:577-583 (qkv reshape, q_norm/k_norm, rope) and
@@ -173,8 +172,9 @@ int saf3r_pack_qkv(const void* q, const void* k, const void* v, int64_t tok_stri
  * Pooled patch-block means (fp32) of the packed Q and K of the listed heads.
  *   head_ids: host int32 [n_heads_sel]; pooled_q / pooled_k: [n_heads_sel][F*NBf][64].
  *   k_packed / pooled_k may both be NULL (pool Q only).
- * Each column is summed sequentially over the block's patch tokens in order (fp32) and divided
- * once by the block population, so results are bit-identical to that definition.
+ * Each column is summed in fp32 in a fixed order: the block's patch tokens in groups of 16
+ * consecutive rows, each group in row order from +0.0, the group sums in group order from +0.0; then
+ * one division by the block population. Results are bit-identical to that definition.
  * Replaces: block pooling of the dynamic pattern (reference precedent
  *           saf3r/patch/adaptive_block_value.py:16-24).
  */

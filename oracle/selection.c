@@ -56,9 +56,14 @@ static float bf16_to_f32(uint16_t h) {
  * x: bf16 bits, natural token layout [F*T, D] with row stride `row_stride` (elements).
  * Frame f, patch p (0 <= p < P = T - nspec) is token f*T + nspec + p.
  * Block b of frame f covers patches [64b, min(64b+64, P)).
- * out: [F*NBf, D] fp32, row f*NBf + b. Each column is summed sequentially in patch order
- * (fp32 adds) and divided once by the population.
+ * out: [F*NBf, D] fp32, row f*NBf + b. Summation order of each column (fp32 adds): the block's
+ * rows in groups of ORACLE_POOL_GROUP consecutive rows; each group summed in row order from +0.0,
+ * the group sums added in group order from +0.0 (a group past the population adds +0.0, which
+ * changes nothing: a sum started at +0.0 is never -0.0); then one division by the population.
+ * (The order is this build's definition of the block mean; the reference's mean over a block has
+ * no fixed order.)
  */
+#define ORACLE_POOL_GROUP 16
 void oracle_block_pool(const uint16_t* x, int64_t row_stride, int F, int T, int nspec, int D,
                        int block, float* out) {
     int P = T - nspec;
@@ -70,9 +75,13 @@ void oracle_block_pool(const uint16_t* x, int64_t row_stride, int F, int T, int 
             float* o = out + ((int64_t)f * NBf + b) * D;
             for (int d = 0; d < D; ++d) {
                 float acc = 0.0f;
-                for (int r = 0; r < cnt; ++r) {
-                    int64_t tok = (int64_t)f * T + nspec + p0 + r;
-                    acc = acc + bf16_to_f32(x[tok * row_stride + d]);
+                for (int g0 = 0; g0 < cnt; g0 += ORACLE_POOL_GROUP) {
+                    float part = 0.0f;
+                    for (int r = g0; r < g0 + ORACLE_POOL_GROUP && r < cnt; ++r) {
+                        int64_t tok = (int64_t)f * T + nspec + p0 + r;
+                        part = part + bf16_to_f32(x[tok * row_stride + d]);
+                    }
+                    acc = acc + part;
                 }
                 o[d] = acc / (float)cnt;
             }

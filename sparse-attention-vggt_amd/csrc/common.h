@@ -81,6 +81,10 @@ __device__ inline int swz4(int r) { return ((r >> 1) & 3) ^ ((r >> 3) & 1); }
 constexpr int kHeadDim = 64;
 constexpr int kBlock = 64;
 constexpr int kMaxHeads = 64;
+// Block means (the pooled rows of the dynamic pattern) sum each feature in groups of kPoolGroup
+// consecutive rows, each group in row order from +0.0, then the group sums in group order from +0.0,
+// and divide once by the block's population.
+constexpr int kPoolGroup = 16;
 
 // ---------------------------------------------------------------------------------------
 // Error channel

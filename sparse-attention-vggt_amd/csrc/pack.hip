@@ -53,12 +53,15 @@ struct PackParams {
 // pairs feature d with d +- 16 (partner thread c8 ^ 2). Every load of a row is issued before any
 // processing, so the q, k and v loads are in flight together.
 // Pooled heads: a patch tile of the packed layout is one selection block; its bf16(q) (without the
-// Q scale) and bf16(k) rows are staged in LDS and one thread per (tensor, feature) sums them in row
-// order and divides once by the block population (the block means of the block-dynamic pattern,
-// bit-identical to that definition), then each of those two waves writes its row's split record.
+// Q scale) and bf16(k) rows are staged in LDS, every thread sums one (tensor, group of kPoolGroup
+// rows, feature) in row order, and one thread per (tensor, feature) adds the group sums in order
+// and divides once by the block population: the block means of the block-dynamic pattern,
+// bit-identical to that definition. Rows past the population hold +0.0, which changes no sum
+// started at +0.0. Each of those two waves then writes its row's split record.
 __global__ __launch_bounds__(512) void pack_qkv_kernel(PackParams p) {
   __shared__ __align__(16) __bf16 vs[64 * 72];  // V rows of the tile, 144-byte row pitch
   __shared__ __align__(16) __bf16 ps[2][64 * 64];  // pooled heads: bf16 q / k rows of the tile
+  __shared__ float pp[2][64 / kPoolGroup][64];     // pooled heads: group sums
   const Geom& g = p.g;
   const int tile = bid_x(), h = bid_y();
   const int t = tid_x(), row = t >> 3, c8 = t & 7;
@@ -188,21 +191,28 @@ __global__ __launch_bounds__(512) void pack_qkv_kernel(PackParams p) {
     *reinterpret_cast<u32x4*>(p.vp + ((int64_t)h * g.L + (int64_t)tile * 64) * 64 + i * 64 + 8 * c8) =
         u32x4{w[0], w[1], w[2], w[3]};
   }
+  if (pool) {  // uniform over the workgroup
+    static_assert(2 * (64 / kPoolGroup) * 64 == 512, "one thread per (tensor, group, feature)");
+    {
+      const int which = t >> 8, grp = (t >> 6) & 3, d = t & 63;
+      const __bf16* col = &ps[which][grp * kPoolGroup * 64 + d];
+      float x[kPoolGroup];  // every read in flight, then the additions in row order
+#pragma unroll
+      for (int i = 0; i < kPoolGroup; ++i) x[i] = (float)col[i * 64];
+      float part = 0.f;
+#pragma unroll
+      for (int i = 0; i < kPoolGroup; ++i) part = part + x[i];
+      pp[which][grp][d] = part;
+    }
+    __syncthreads();
+  }
   if (pool && t < 128) {  // waves 0 (q) and 1 (k): lane = feature
     const int which = t >> 6, d = t & 63;
     const int pt = tile - g.nst, b = pt % g.NBf;
     const int cnt = min(64, g.P - 64 * b);
-    const __bf16* col = &ps[which][d];
     float sum = 0.f;
-    int r = 0;
-    for (; r + 8 <= cnt; r += 8) {  // eight reads in flight, then the additions in row order
-      float x[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) x[j] = (float)col[(r + j) * 64];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) sum = sum + x[j];
-    }
-    for (; r < cnt; ++r) sum = sum + (float)col[r * 64];
+    for (int grp = 0; grp < 64 / kPoolGroup; ++grp) sum = sum + pp[which][grp][d];
     const float mean = sum / (float)cnt;
     const int64_t nb = (int64_t)g.F * g.NBf;
     const int64_t rec = ((int64_t)p.pool_slot[h] * 2 + which) * nb + pt;  // pt = f * NBf + b

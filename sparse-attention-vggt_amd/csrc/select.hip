@@ -5,8 +5,8 @@
 //      index, running top-k per frame, frame-major flush in descending order),
 //      saf3r/triton/topk_utils.py:26-29 (sortable key), saf3r/patch/wrapper.py:48 (top-k per frame),
 //      saf3r/patch/adaptive_block_value.py:16-24 (block mean over the real population).
-// Every fp32 result is produced in a fixed operation order (sequential sums, one division,
-// sequential fma), so it is bit-identical to that definition.
+// Every fp32 result is produced in a fixed operation order (block sums in groups of 16 rows, one
+// division, sequential fma), so it is bit-identical to that definition.
 #include <algorithm>
 
 #include "common.h"
@@ -15,7 +15,8 @@ namespace saf3r {
 
 // ---------------------------------------------------------------------------------------
 // Pooling: eight lanes per (head, patch block), each lane owning 8 features (16-byte loads), so a
-// wave streams eight blocks at once. Every feature is still summed sequentially in row order.
+// wave streams eight blocks at once. Every feature is summed in the block-mean order: groups of
+// kPoolGroup rows, each in row order from +0.0, the group sums added in order from +0.0.
 // ---------------------------------------------------------------------------------------
 struct PoolParams {
   const __bf16* q;
@@ -50,25 +51,36 @@ __global__ __launch_bounds__(256) void block_pool_kernel(PoolParams p) {
   float aq[8], ak[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) aq[e] = ak[e] = 0.f;
-  int r = 0;
-  for (; r + 4 <= cnt; r += 4) {
-    u32x4 xq[4], xk[4];
+  for (int g0 = 0; g0 < cnt; g0 += kPoolGroup) {
+    const int g1 = min(cnt, g0 + kPoolGroup);
+    float gq[8], gk[8];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) xq[j] = qs[(r + j) * 8];
-    if (ks) {
+    for (int e = 0; e < 8; ++e) gq[e] = gk[e] = 0.f;
+    int r = g0;
+    for (; r + 4 <= g1; r += 4) {
+      u32x4 xq[4], xk[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) xk[j] = ks[(r + j) * 8];
+      for (int j = 0; j < 4; ++j) xq[j] = qs[(r + j) * 8];
+      if (ks) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) xk[j] = ks[(r + j) * 8];
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) add_row8(gq, xq[j]);
+      if (ks) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) add_row8(gk, xk[j]);
+      }
+    }
+    for (; r < g1; ++r) {
+      add_row8(gq, qs[r * 8]);
+      if (ks) add_row8(gk, ks[r * 8]);
     }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) add_row8(aq, xq[j]);
-    if (ks) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) add_row8(ak, xk[j]);
+    for (int e = 0; e < 8; ++e) {
+      aq[e] = aq[e] + gq[e];
+      ak[e] = ak[e] + gk[e];
     }
-  }
-  for (; r < cnt; ++r) {
-    add_row8(aq, qs[r * 8]);
-    if (ks) add_row8(ak, ks[r * 8]);
   }
   const float fc = (float)cnt;
   const int64_t o = ((int64_t)hs * p.nb + bi) * 64 + 8 * sub;

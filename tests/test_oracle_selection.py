@@ -98,6 +98,32 @@ def test_block_pool_is_population_mean():
         assert np.array_equal(got[f * 3 + 2], (rows.sum(0) / np.float32(22)).astype(np.float32))
 
 
+def test_block_pool_summation_order_is_grouped_by_16_rows():
+    """The block mean's fp32 order: groups of 16 rows, each summed in row order, the group sums added
+    in group order. Closed forms on values where every other order rounds differently: 8 rows of
+    2^21 then ones (ulp 2 at 2^24, ties to even drop single ones)."""
+    F, T, ns, D = 1, 64, 0, 2
+    x = np.ones((64, D), np.float32)
+    x[:8] = 2.0 ** 21
+    got = sel.block_pool(sel.bf16_bits(x), F, T, ns)
+    # group 0: 2^24 (its 8 ones are each lost); groups 1..3: 16 each, added exactly
+    assert np.all(got == np.float32((2 ** 24 + 48) / 64))
+    # (sequential: 2^24 / 64; groups of 8: (2^24 + 56) / 64; groups of 32: (2^24 + 32) / 64)
+    assert got[0, 0] not in (np.float32(2 ** 24 / 64), np.float32((2 ** 24 + 56) / 64), np.float32((2 ** 24 + 32) / 64))
+    # group sums in order: 2^24 + 1 + 1 + 2 rounds to 2^24 + 2 (reversed it would be 2^24 + 4)
+    y = np.zeros((64, D), np.float32)
+    y[:8] = 2.0 ** 21
+    y[16], y[32], y[48] = 1.0, 1.0, 2.0
+    got = sel.block_pool(sel.bf16_bits(y), F, T, ns)
+    assert np.all(got == np.float32((2 ** 24 + 2) / 64))
+    # a partial block of 22 rows: 8 rows of 2^21, 14 ones -> group 0 = 2^24, group 1 = 6
+    F, T, ns = 1, 64 + 22 + 5, 5
+    z = np.ones((T, D), np.float32)
+    z[ns + 64:ns + 72] = 2.0 ** 21
+    got = sel.block_pool(sel.bf16_bits(z), F, T, ns)
+    assert np.all(got[1] == np.float32(np.float32(2 ** 24 + 6) / np.float32(22)))
+
+
 def test_block_scores_use_sequential_fma():
     rng = np.random.default_rng(2)
     q = rng.integers(-5, 6, size=(4, 64)).astype(np.float32)
