@@ -48,7 +48,7 @@
 extern "C" {
 #endif
 
-#define SAF3R_ABI_VERSION 11
+#define SAF3R_ABI_VERSION 12
 
 enum saf3r_status {
   SAF3R_OK = 0,
@@ -377,6 +377,26 @@ int saf3r_sparse_attn_fwd(const void* q_packed, const void* k_packed, const void
 int saf3r_gather_attn_fwd(const saf3r_rows* q, const saf3r_rows* k, const saf3r_rows* v, const int32_t* idx,
                           int64_t idx_row_stride, int n, int topk, int64_t num_keys, float scale, int dtype_flags,
                           const saf3r_rows* out, void* stream);
+/*
+ * saf3r_gather_attn_fwd in two passes, for many rows with long lists (the dino_topk image rows:
+ * 128 frames x 1369 rows, 512 keys each): every row's list is cut into 8 slices of consecutive
+ * entries; slice s is walked by work-groups the hardware places on XCD s (so each XCD's L2 holds
+ * the rows of 1/8 of the list positions, one frame range for frame-major lists), each writing the
+ * slice's partial softmax (maximum, sum of weights, unnormalised output) to the caller's workspace;
+ * a second kernel merges the 8 partials of a row. Same arguments and results as
+ * saf3r_gather_attn_fwd within fp32 rounding (the summation order differs).
+ *   workspace / workspace_bytes: caller-owned device memory of at least
+ *     saf3r_gather_attn_workspace_bytes(n, topk) bytes, 16-byte aligned; calls that share it must
+ *     be ordered (one stream).
+ * Replaces: as saf3r_gather_attn_fwd.
+ */
+int saf3r_gather_attn_fwd_sliced(const saf3r_rows* q, const saf3r_rows* k, const saf3r_rows* v, const int32_t* idx,
+                                 int64_t idx_row_stride, int n, int topk, int64_t num_keys, float scale,
+                                 int dtype_flags, const saf3r_rows* out, void* workspace, int64_t workspace_bytes,
+                                 void* stream);
+/* Workspace bytes of saf3r_gather_attn_fwd_sliced (n * 8 slices * 66 floats), -1 for invalid sizes.
+ * No counterpart in the reference (its kernel keeps each row's state in registers). */
+int64_t saf3r_gather_attn_workspace_bytes(int n, int topk);
 
 /*
  * Per-frame token top-k of q.k (bf16 inputs, fp32 MFMA accumulation), one batch element per call

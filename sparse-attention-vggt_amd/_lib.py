@@ -19,8 +19,9 @@ EXPORTS = (
     "saf3r_token_topk", "saf3r_probe_scores", "saf3r_keyset_build", "saf3r_keyset_gather",
     "saf3r_frame_topk_scores", "saf3r_probe_scores_noalloc", "saf3r_token_topk_workspace_bytes",
     "saf3r_pooled_prepare", "saf3r_block_select_pooled", "saf3r_block_select_pooled_workspace_bytes",
+    "saf3r_gather_attn_fwd_sliced", "saf3r_gather_attn_workspace_bytes",
 )
-ABI_VERSION = 11
+ABI_VERSION = 12
 GATHER_QK_FP32, GATHER_V_FP32, GATHER_OUT_FP32 = 1, 2, 4  # enum saf3r_gather_dtype
 SAF3R_OK, SAF3R_ERR_INVALID, SAF3R_ERR_UNSUPPORTED, SAF3R_ERR_LAUNCH, SAF3R_ERR_INJECTED = range(5)
 
@@ -70,6 +71,8 @@ def load():
         "saf3r_sparse_attn_fwd": ([p, p, p, i32, i32, i32, i32, p, p, i32, f32, p, i64, p, p, p, i64, p, p, p, p, p,
                                    i32, p, ctypes.c_uint, p], i32),
         "saf3r_gather_attn_fwd": ([rows, rows, rows, p, i64, i32, i32, i64, f32, i32, rows, p], i32),
+        "saf3r_gather_attn_fwd_sliced": ([rows, rows, rows, p, i64, i32, i32, i64, f32, i32, rows, p, i64, p], i32),
+        "saf3r_gather_attn_workspace_bytes": ([i32, i32], i64),
         "saf3r_token_topk": ([rows, rows, i32, i32, i32, i32, p, p, i64, p], i32),
         "saf3r_token_topk_workspace_bytes": ([i32, i32, i32, i32], i64),
         "saf3r_probe_scores": ([p, p, i64, i32, p, i32, p, i32, f32, p, p, p, i64, p], i32),

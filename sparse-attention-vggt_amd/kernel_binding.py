@@ -24,7 +24,7 @@ import ctypes
 
 import torch
 
-from . import _lib
+from . import _lib, ops
 
 HEAD_DIM = 64
 
@@ -75,9 +75,16 @@ def fused_sparse_topk_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tenso
         return out.to(out_dtype)
     flags = (_lib.GATHER_QK_FP32 if qk32 else 0) | (_lib.GATHER_V_FP32 | _lib.GATHER_OUT_FP32 if v32 else 0)
     lib = _lib.load()
-    _check(lib.saf3r_gather_attn_fwd(ctypes.byref(_rows(q)), ctypes.byref(_rows(k)), ctypes.byref(_rows(v)),
-                                     ctypes.c_void_p(idx.data_ptr()), idx.stride(0), N, idx.shape[1], k.shape[0],
-                                     float(scale), flags, ctypes.byref(_rows(out)), _stream()))
+    args = (ctypes.byref(_rows(q)), ctypes.byref(_rows(k)), ctypes.byref(_rows(v)), ctypes.c_void_p(idx.data_ptr()),
+            idx.stride(0), N, idx.shape[1], k.shape[0], float(scale), flags, ctypes.byref(_rows(out)))
+    if ops.gather_sliced(N, idx.shape[1]):  # many rows with long lists: the two-pass kernels
+        nbytes = lib.saf3r_gather_attn_workspace_bytes(N, idx.shape[1])
+        if nbytes < 0:
+            raise RuntimeError(lib.saf3r_last_error().decode(errors="replace"))
+        ws = torch.empty(nbytes, device=q.device, dtype=torch.uint8)
+        _check(lib.saf3r_gather_attn_fwd_sliced(*args, ctypes.c_void_p(ws.data_ptr()), nbytes, _stream()))
+    else:
+        _check(lib.saf3r_gather_attn_fwd(*args, _stream()))
     return out if out.dtype == out_dtype else out.to(out_dtype)
 
 

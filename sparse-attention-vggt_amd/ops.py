@@ -468,17 +468,42 @@ def gather_attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, idx: torc
     return res if res.dtype == out_dtype else res.to(out_dtype)
 
 
+_gather_ws = {}  # (device, bytes) -> the sliced gather's workspace, kept for the next call of the same size
+
+
+def gather_sliced(n: int, topk: int) -> bool:
+    """Whether a gather of ``n`` rows with ``topk``-entry lists takes the two-pass sliced kernels (many
+    rows with long lists, where the rows the lists touch exceed one XCD's L2)."""
+    return topk >= 128 and n * topk >= (1 << 22)
+
+
 def gather_attn_rows(qr, kr, vr, idx, idx_row_stride, n, topk, num_keys, scale, outr, keep=None, qk_fp32=False,
-                     dtype_flags=None):
+                     dtype_flags=None, sliced=None):
     """``saf3r_gather_attn_fwd`` on row descriptors; ``qk_fp32``: q and k rows are fp32 (or give the
-    full ``dtype_flags``)."""
+    full ``dtype_flags``). ``sliced`` (default: ``gather_sliced(n, topk)``) runs
+    ``saf3r_gather_attn_fwd_sliced`` with a workspace kept per device and size."""
     lib = _lib.load()
     scale = 1.0 / math.sqrt(HEAD_DIM) if scale is None else scale
     flags = (_lib.GATHER_QK_FP32 if qk_fp32 else 0) if dtype_flags is None else dtype_flags
+    if sliced is None:
+        sliced = gather_sliced(n, topk)
     _mark("gather_attn", "start")
-    _lib.check(lib.saf3r_gather_attn_fwd(ctypes.byref(qr), ctypes.byref(kr), ctypes.byref(vr), _ptr(idx),
-                                         idx_row_stride, n, topk, num_keys, float(scale), int(flags),
-                                         ctypes.byref(outr), _lib.stream_ptr()))
+    if sliced and n > 0:
+        nbytes = int(lib.saf3r_gather_attn_workspace_bytes(n, topk))
+        if nbytes < 0:
+            raise RuntimeError(lib.saf3r_last_error().decode(errors="replace"))
+        dev = torch.cuda.current_device()
+        ws = _gather_ws.get((dev, nbytes))
+        if ws is None:
+            _gather_ws.clear()  # one size at a time: the dino heads of a forward share one
+            ws = _gather_ws[(dev, nbytes)] = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        _lib.check(lib.saf3r_gather_attn_fwd_sliced(ctypes.byref(qr), ctypes.byref(kr), ctypes.byref(vr), _ptr(idx),
+                                                    idx_row_stride, n, topk, num_keys, float(scale), int(flags),
+                                                    ctypes.byref(outr), _ptr(ws), nbytes, _lib.stream_ptr()))
+    else:
+        _lib.check(lib.saf3r_gather_attn_fwd(ctypes.byref(qr), ctypes.byref(kr), ctypes.byref(vr), _ptr(idx),
+                                             idx_row_stride, n, topk, num_keys, float(scale), int(flags),
+                                             ctypes.byref(outr), _lib.stream_ptr()))
     _mark("gather_attn", "end")
     return keep
 

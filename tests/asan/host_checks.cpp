@@ -198,6 +198,16 @@ static void check_other_entries() {
   CHECK(rc == SAF3R_ERR_INVALID && last_error_has("dtype"));
   rc = saf3r_gather_attn_fwd(&rows, &rows, &rows, nullptr, 4, 10, 4, 100, 0.125f, 0, &rows, nullptr);
   CHECK(rc == SAF3R_ERR_INVALID && last_error_has("index list"));
+  CHECK(saf3r_gather_attn_workspace_bytes(100, 512) == int64_t(100) * 8 * 66 * 4);
+  CHECK(saf3r_gather_attn_workspace_bytes(-1, 512) == -1);
+  CHECK(saf3r_gather_attn_workspace_bytes(10, 0) == -1);
+  rc = saf3r_gather_attn_fwd_sliced(&rows, &rows, &rows, di, 4, 10, 4, 100, 0.125f, 0, &rows, nullptr, 0, nullptr);
+  CHECK(rc == SAF3R_ERR_INVALID && last_error_has("workspace"));
+  rc = saf3r_gather_attn_fwd_sliced(&rows, &rows, &rows, di, 4, 10, 4, 100, 0.125f, 0, &rows, d, 100, nullptr);
+  CHECK(rc == SAF3R_ERR_INVALID && last_error_has("workspace"));
+  rc = saf3r_gather_attn_fwd_sliced(&rows, &rows, &null_rows, di, 4, 10, 4, 100, 0.125f, 0, &rows, d, 1 << 20,
+                                    nullptr);
+  CHECK(rc == SAF3R_ERR_INVALID && last_error_has("null"));
 
   rc = saf3r_token_topk(&rows, &rows, 10, 4, 1369, 0, di, nullptr, 0, nullptr);
   CHECK(rc == SAF3R_ERR_INVALID && last_error_has("topk"));
@@ -235,6 +245,8 @@ static void check_fault_injection() {
   CHECK(saf3r_pooled_prepare(nullptr, -1, nullptr, nullptr, nullptr) == SAF3R_ERR_INJECTED);
   CHECK(saf3r_gather_attn_fwd(nullptr, nullptr, nullptr, nullptr, 0, 0, 0, 0, 0.f, 0, nullptr, nullptr) ==
         SAF3R_ERR_INJECTED);
+  CHECK(saf3r_gather_attn_fwd_sliced(nullptr, nullptr, nullptr, nullptr, 0, 0, 0, 0, 0.f, 0, nullptr, nullptr, 0,
+                                     nullptr) == SAF3R_ERR_INJECTED);
   setenv("SAF3R_FAULT_INJECT", "saf3r_keyset_build", 1);
   CHECK(saf3r_keyset_build(nullptr, 0, 0, nullptr, nullptr, nullptr, nullptr, 0, 0, 0, nullptr, 0, nullptr,
                            nullptr) == SAF3R_ERR_INJECTED);

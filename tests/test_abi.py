@@ -24,7 +24,7 @@ def test_library_exports_every_declared_symbol(pkg):
     for n in names:
         assert hasattr(lib, n), n
     assert set(names) == set(lib_mod.EXPORTS)
-    assert lib.saf3r_abi_version() == lib_mod.ABI_VERSION == 11
+    assert lib.saf3r_abi_version() == lib_mod.ABI_VERSION == 12
 
 
 def test_packed_slots_matches_layout(pkg):
@@ -214,6 +214,15 @@ def test_token_topk_workspace_size_query(pkg):
     assert ws(100, 2, 200, 129) == -1  # beyond the reference's limit of 128
     assert ws(100, 2, 5000, 32) == -1  # frames above 4096 keys on the k > 16 path
     assert ws(-1, 2, 50, 4) == -1
+
+
+def test_gather_workspace_size_query(pkg):
+    from importlib import import_module
+    lib = import_module(pkg.__name__ + "._lib").load()
+    assert lib.saf3r_gather_attn_workspace_bytes(175232, 512) == 175232 * 8 * 66 * 4  # 8 slices x 66 floats
+    assert lib.saf3r_gather_attn_workspace_bytes(0, 512) == 0
+    assert lib.saf3r_gather_attn_workspace_bytes(-1, 512) == -1
+    assert lib.saf3r_gather_attn_workspace_bytes(10, 0) == -1
 
 
 def test_fault_injection_is_reported(pkg, monkeypatch):

@@ -623,6 +623,46 @@ def test_gather_attention_shared_list(ops):
     _check_close(got.cpu(), ref, "gather shared list")
 
 
+@pytest.mark.parametrize("n,nk,topk,rpf", [(100, 300, 5, 300), (70, 3000, 300, 300), (3000, 40 * 137, 160, 137)])
+def test_gather_attention_sliced(ops, n, nk, topk, rpf):
+    """The two-pass sliced gather (lists cut into 8 slices, partial softmax merged): against the fp64
+    reference, and within fp32 rounding of the one-pass kernel. Covers slices left empty (topk 5 < 8),
+    masked and out-of-range entries, a row with no valid entry, fp32 q / k, and key rows addressed
+    frame by frame (rows_per_frame < the key count, skipping 3 junk rows per stored frame)."""
+    g = torch.Generator().manual_seed(n + topk + 7)
+    q = 3.0 * torch.randn(n, 64, generator=g)
+    k = 3.0 * torch.randn(nk, 64, generator=g)
+    v = torch.randn(nk, 64, generator=g).to(torch.bfloat16)
+    idx = torch.randint(0, nk, (n, topk), generator=g, dtype=torch.int32)
+    idx[0, :3] = -1
+    idx[1, :] = -1            # no valid entry: zeros
+    idx[2, -1] = nk + 5       # out of range: skipped
+    pad = 3
+    kst = torch.randn(nk // rpf, pad + rpf, 64, generator=g)
+    kst[:, pad:] = k.view(-1, rpf, 64)
+    vst = torch.randn(nk // rpf, pad + rpf, 64, generator=g).to(torch.bfloat16)
+    vst[:, pad:] = v.view(-1, rpf, 64)
+    qd, kd, vd, idd = q.to(DEV), kst.to(DEV).view(-1, 64), vst.to(DEV).view(-1, 64), idx.to(DEV)
+    kr = ops.rows(kd, base_row=pad, rows_per_frame=rpf, frame_row_stride=pad + rpf)
+    vr = ops.rows(vd, base_row=pad, rows_per_frame=rpf, frame_row_stride=pad + rpf)
+    outs = {}
+    for sliced in (True, False):
+        out = torch.full((n, 64), 7.0, dtype=torch.bfloat16, device=DEV)
+        ops.gather_attn_rows(ops.rows(qd), kr, vr, idd, topk, n, topk, nk, None, ops.rows(out), qk_fp32=True,
+                             sliced=sliced)
+        outs[sliced] = out.cpu()
+    torch.cuda.synchronize()
+    ref = OA.gather_attention(q.double(), k.double(), v.float(), idx.clamp(max=nk - 1).where(idx < nk, -1),
+                              dtype=torch.float64)
+    ref[1] = 0.0  # the reference's softmax over no entry is NaN; the kernels write zeros
+    _check_close(outs[True], ref, f"sliced gather n{n} topk{topk}")
+    assert torch.all(outs[True][1] == 0)
+    # the same sums in another order: one bf16 ulp (of the larger value) apart at most, beside values
+    # near zero that cancellation leaves (an absolute 1e-4, far below the outputs' scale of 1)
+    a, b = outs[True].float(), outs[False].float()
+    assert ((a - b).abs() <= torch.maximum(a.abs(), b.abs()) * 2 ** -7 + 1e-4).all(), (a - b).abs().max()
+
+
 @pytest.mark.parametrize("layout", ["framed", "paired"])
 def test_token_topk_key_row_layouts(ops, layout):
     """Key rows described frame by frame (rows_per_frame == per_frame: the plugin's packed layout)
