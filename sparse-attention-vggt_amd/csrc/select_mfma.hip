@@ -63,7 +63,7 @@ struct SelMfmaParams {
   const float* meta;      // [n][2][NB][2]
   int32_t* idx;           // [n][NB][F * ke]
   uint32_t* qcount;       // the number of listed pairs (cleared before the select kernel)
-  u32x4* queue;           // listed pairs: (head * NB + query block, frame, candidate key mask, 0)
+  u32x4* queue;           // listed pairs: (query block, frame, candidate key mask, head)
   int F, NBf, NB, ke;
 };
 
@@ -311,7 +311,7 @@ __global__ __launch_bounds__(256) void block_select_mfma_kernel(SelMfmaParams p)
     for (int t = 0; t < p.ke; ++t) dst[t] = fb + o[t];
     if (o[0] == kSpilled) {
       const uint32_t at = atomicAdd(p.qcount, 1u);
-      p.queue[at] = u32x4{(uint32_t)((int64_t)hs * NB + i), (uint32_t)(f0 + fl), all_keys, 0u};
+      p.queue[at] = u32x4{(uint32_t)i, (uint32_t)(f0 + fl), all_keys, (uint32_t)hs};
     }
   }
   // the queued pairs to the global list: one atomic per workgroup reserves its range
@@ -320,8 +320,8 @@ __global__ __launch_bounds__(256) void block_select_mfma_kernel(SelMfmaParams p)
   __syncthreads();
   for (uint32_t e = tid; e < nq; e += 256) {
     const u32x2 ent = queue[e];
-    p.queue[gbase + e] = u32x4{(uint32_t)((int64_t)hs * NB + (int64_t)qt * 128 + (ent[0] >> 16)),
-                               (uint32_t)(f0 + (int)(ent[0] & 0xFFFF)), ent[1], 0u};
+    p.queue[gbase + e] = u32x4{(uint32_t)((int64_t)qt * 128 + (ent[0] >> 16)),
+                               (uint32_t)(f0 + (int)(ent[0] & 0xFFFF)), ent[1], (uint32_t)hs};
   }
 }
 
@@ -345,8 +345,8 @@ __global__ __launch_bounds__(256) void block_select_exact_kernel(SelMfmaParams p
     const uint32_t e = e0 + (uint32_t)slot;
     const bool act = e < nq;
     const u32x4 ent = p.queue[act ? e : e0];
-    const int64_t hq = ent[0];  // head * NB + query block
-    const int64_t hs = hq / NB, i = hq - hs * NB;
+    const int64_t i = ent[0], hs = ent[3];  // query block, head
+    const int64_t hq = hs * NB + i;
     const int f = (int)ent[1];
     const bool cand = act && col < p.NBf && ((ent[2] >> col) & 1u);
     uint64_t key = 0;
@@ -429,7 +429,7 @@ extern "C" int64_t saf3r_block_select_pooled_workspace_bytes(int n, int frames, 
     return -1;
   const int ke = k < blocks_per_frame ? k : blocks_per_frame;
   if (ke > 16) return 0;  // the sequential kernel: no workspace
-  // the list's count and its (head * NB + query block) entries are 32-bit
+  // the list's count is 32-bit
   if ((int64_t)n * frames * blocks_per_frame * frames > 0xFFFFFFFFll) return -1;
   // a 16-byte count slot, then one 16-byte entry per (query block, frame) pair: the worst case
   return 16 + (int64_t)n * frames * blocks_per_frame * frames * 16;
