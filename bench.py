@@ -602,6 +602,9 @@ def main():
                     help="run only the per-pattern attention timing (16 heads of each pattern, and the head mix)")
     ap.add_argument("--no-extra-configs", dest="extra_configs", action="store_false",
                     help="skip the 32-frame single-layer and the DA3-Giant-shape legs")
+    ap.add_argument("--only-config", choices=["32-frames", "da3-giant"], default=None,
+                    help="run only one of the extra legs (the 32-frame single layer or the DA3-Giant shape) and "
+                         "print its JSON, for profiling that shape alone")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only a plain copy kernel of known size (reads 1 GiB, writes 1 GiB), for scaling "
                          "the FETCH_SIZE / WRITE_SIZE counters of a profiling run")
@@ -616,6 +619,12 @@ def main():
         return
     if args.per_pattern:
         print(json.dumps({"per_pattern": per_pattern(__graft_entry__.package(), args.frames)}), flush=True)
+        return
+    if args.only_config == "32-frames":
+        print(json.dumps({"config_32_frames": single_layer_leg(__graft_entry__.package(), 32)}), flush=True)
+        return
+    if args.only_config == "da3-giant":
+        print(json.dumps({"config_da3_giant": da3_leg(__graft_entry__.package(), args.steps, args.warmup)}), flush=True)
         return
 
     import importlib
