@@ -383,7 +383,8 @@ int saf3r_gather_attn_fwd(const saf3r_rows* q, const saf3r_rows* k, const saf3r_
  * entries; slice s is walked by work-groups the hardware places on XCD s (so each XCD's L2 holds
  * the rows of 1/8 of the list positions, one frame range for frame-major lists), each writing the
  * slice's partial softmax (maximum, sum of weights, unnormalised output) to the caller's workspace;
- * a second kernel merges the 8 partials of a row. Same arguments and results as
+ * a second kernel merges the 8 partials of a row. Rows run in chunks of 65536 (both kernels per
+ * chunk), so the workspace holds one chunk's partials. Same arguments and results as
  * saf3r_gather_attn_fwd within fp32 rounding (the summation order differs).
  *   workspace / workspace_bytes: caller-owned device memory of at least
  *     saf3r_gather_attn_workspace_bytes(n, topk) bytes, 16-byte aligned; calls that share it must
@@ -394,7 +395,8 @@ int saf3r_gather_attn_fwd_sliced(const saf3r_rows* q, const saf3r_rows* k, const
                                  int64_t idx_row_stride, int n, int topk, int64_t num_keys, float scale,
                                  int dtype_flags, const saf3r_rows* out, void* workspace, int64_t workspace_bytes,
                                  void* stream);
-/* Workspace bytes of saf3r_gather_attn_fwd_sliced (n * 8 slices * 66 floats), -1 for invalid sizes.
+/* Workspace bytes of saf3r_gather_attn_fwd_sliced (min(n, 65536) rows * 8 slices * 66 floats: at most
+ * 138 MB), -1 for invalid sizes.
  * No counterpart in the reference (its kernel keeps each row's state in registers). */
 int64_t saf3r_gather_attn_workspace_bytes(int n, int topk);
 

@@ -67,7 +67,8 @@ struct GatherParams {
   int64_t nk;
   float c;          // scale * log2(e)
   int64_t resident; // C: waves resident on the GPU at once (walk order only)
-  float* part;      // sliced mode: partial results [n][kGatherSlices][66]
+  float* part;      // sliced mode: partial results [n][kGatherSlices][66] of the rows of this launch
+  int64_t r0;       // sliced mode: the first row of this launch (rows r0 .. r0 + n - 1)
 };
 
 constexpr int kGatherSlices = 8;  // sliced mode: list slices, a multiple of the 8 XCDs
@@ -102,8 +103,9 @@ __global__ __launch_bounds__(256) void gather_attn_kernel(GatherParams p) {
   // (b % 8) + 8 (b / 8G): slice s runs on XCD s % 8, the XCD's slices one after the other
   const int64_t ng = (p.n + 3) / 4;
   const int slice = SLICED ? (int)(bid_x() % 8 + 8 * (bid_x() / (8 * ng))) : 0;
-  const int64_t r = (SLICED ? (int64_t)(bid_x() / 8) % ng : (int64_t)bid_x()) * 4 + w;
-  if (r >= p.n) return;  // a whole wave leaves; the kernel has no barrier
+  const int64_t rl = (SLICED ? (int64_t)(bid_x() / 8) % ng : (int64_t)bid_x()) * 4 + w;  // row of this launch
+  if (rl >= p.n) return;  // a whole wave leaves; the kernel has no barrier
+  const int64_t r = SLICED ? p.r0 + rl : rl;
 
   // this lane's 8 dims of q: fp32 values (QK32) or bf16 pairs
   float qv[8];
@@ -135,7 +137,7 @@ __global__ __launch_bounds__(256) void gather_attn_kernel(GatherParams p) {
 
   const int nsteps = max(1, (len + ENT - 1) / ENT);
   const int64_t res = SLICED ? max((int64_t)1, p.resident / kGatherSlices) : p.resident;
-  const int s0 = r < res ? 0 : (int)(((r - res) * nsteps / res) % nsteps);
+  const int s0 = rl < res ? 0 : (int)(((rl - res) * nsteps / res) % nsteps);
   // entry st * ENT + l of the part, in lane l < ENT (-1 past it or out of range)
   auto entry = [&](int st) {  // (range-checked where it is used)
     const int e = st * ENT + (lane & (ENT - 1));
@@ -223,7 +225,7 @@ __global__ __launch_bounds__(256) void gather_attn_kernel(GatherParams p) {
 #pragma unroll
   for (int d = 0; d < 8; ++d) acc[d] = slots_sum(acc[d]);
   if constexpr (SLICED) {  // the slice's unnormalised sum, its maximum and its sum of weights
-    float* pr = p.part + (r * kGatherSlices + slice) * 66;
+    float* pr = p.part + (rl * kGatherSlices + slice) * 66;
     if (ks == 0) {
       *reinterpret_cast<f32x4*>(pr + 8 * dg) = f32x4{acc[0], acc[1], acc[2], acc[3]};
       *reinterpret_cast<f32x4*>(pr + 8 * dg + 4) = f32x4{acc[4], acc[5], acc[6], acc[7]};
@@ -258,14 +260,14 @@ __global__ __launch_bounds__(256) void gather_attn_kernel(GatherParams p) {
 template <bool O32>
 __global__ __launch_bounds__(256) void gather_merge_kernel(GatherParams p) {
   const int lane = tid_x() & 63, w = tid_x() >> 6, sl = lane >> 3, dg = lane & 7;
-  const int64_t r = (int64_t)bid_x() * 4 + w;
-  if (r >= p.n) return;
+  const int64_t rl = (int64_t)bid_x() * 4 + w, r = p.r0 + rl;
+  if (rl >= p.n) return;
   constexpr int H = kGatherSlices / 8;  // slices per lane: sl, sl + 8, ...
   f32x4 a[H], b[H];
   float m[H], l[H], mx = -__builtin_inff();
 #pragma unroll
   for (int j = 0; j < H; ++j) {
-    const float* pr = p.part + (r * kGatherSlices + sl + 8 * j) * 66;
+    const float* pr = p.part + (rl * kGatherSlices + sl + 8 * j) * 66;
     a[j] = *reinterpret_cast<const f32x4*>(pr + 8 * dg);
     b[j] = *reinterpret_cast<const f32x4*>(pr + 8 * dg + 4);
     m[j] = pr[64];
@@ -322,6 +324,7 @@ static bool to_dev(const saf3r_rows* s, RowsDev* d, const char* name, bool fp32 
 
 constexpr int kGatherStep = 32;        // list entries per walk step
 constexpr int kGatherStepSliced = 16;  // the same in sliced mode (a slice's 64 entries in 4 steps)
+constexpr int64_t kGatherChunkRows = 65536;  // sliced mode: rows per pair of launches
 
 // waves of this kernel the device holds at once (for the walk order; 1 if unknown)
 template <typename K>
@@ -340,8 +343,16 @@ static void launch_gather_o(GatherParams p, bool sliced, hipStream_t st) {
   if (sliced) {
     auto kernel = gather_attn_kernel<QK32, V32, O32, kGatherStepSliced, true>;
     p.resident = resident_waves(kernel);
-    hipLaunchKernelGGL(kernel, dim3(rows4 * kGatherSlices), dim3(256), 0, st, p);
-    hipLaunchKernelGGL(gather_merge_kernel<O32>, dim3(rows4), dim3(256), 0, st, p);
+    // rows in chunks: one chunk's partial results (138 MB) stay in the memory-side cache between
+    // its two kernels, and the workspace holds one chunk
+    const int64_t n = p.n;
+    for (int64_t r0 = 0; r0 < n; r0 += kGatherChunkRows) {
+      p.r0 = r0;
+      p.n = (int)(n - r0 < kGatherChunkRows ? n - r0 : kGatherChunkRows);
+      const unsigned g4 = (unsigned)((p.n + 3) / 4);
+      hipLaunchKernelGGL(kernel, dim3(g4 * kGatherSlices), dim3(256), 0, st, p);
+      hipLaunchKernelGGL(gather_merge_kernel<O32>, dim3(g4), dim3(256), 0, st, p);
+    }
   } else {
     auto kernel = gather_attn_kernel<QK32, V32, O32, kGatherStep, false>;
     p.resident = resident_waves(kernel);
@@ -377,6 +388,7 @@ static int gather_run(const char* who, const saf3r_rows* q, const saf3r_rows* k,
   p.nk = num_keys;
   p.c = scale * 1.4426950408889634f;
   p.part = part;
+  p.r0 = 0;
   const bool sliced = part != nullptr;
   hipStream_t st = (hipStream_t)stream;
   if (qk32) {
@@ -404,7 +416,7 @@ extern "C" int saf3r_gather_attn_fwd(const saf3r_rows* q, const saf3r_rows* k, c
 
 extern "C" int64_t saf3r_gather_attn_workspace_bytes(int n, int topk) {
   if (n < 0 || topk <= 0) return -1;
-  return (int64_t)n * kGatherSlices * 66 * (int64_t)sizeof(float);
+  return (n < kGatherChunkRows ? (int64_t)n : kGatherChunkRows) * kGatherSlices * 66 * (int64_t)sizeof(float);
 }
 
 extern "C" int saf3r_gather_attn_fwd_sliced(const saf3r_rows* q, const saf3r_rows* k, const saf3r_rows* v,

@@ -219,7 +219,8 @@ def test_token_topk_workspace_size_query(pkg):
 def test_gather_workspace_size_query(pkg):
     from importlib import import_module
     lib = import_module(pkg.__name__ + "._lib").load()
-    assert lib.saf3r_gather_attn_workspace_bytes(175232, 512) == 175232 * 8 * 66 * 4  # 8 slices x 66 floats
+    assert lib.saf3r_gather_attn_workspace_bytes(175232, 512) == 65536 * 8 * 66 * 4  # one chunk: 8 slices x 66 floats
+    assert lib.saf3r_gather_attn_workspace_bytes(1000, 512) == 1000 * 8 * 66 * 4
     assert lib.saf3r_gather_attn_workspace_bytes(0, 512) == 0
     assert lib.saf3r_gather_attn_workspace_bytes(-1, 512) == -1
     assert lib.saf3r_gather_attn_workspace_bytes(10, 0) == -1

@@ -663,6 +663,31 @@ def test_gather_attention_sliced(ops, n, nk, topk, rpf):
     assert ((a - b).abs() <= torch.maximum(a.abs(), b.abs()) * 2 ** -7 + 1e-4).all(), (a - b).abs().max()
 
 
+def test_gather_attention_sliced_row_chunks(ops):
+    """The sliced gather runs rows in chunks of 65536 (both kernels per chunk, one chunk's partials in
+    the workspace): 2 chunks, the second partial. Every row against the one-pass kernel, and rows at
+    the chunk boundary and the ends against the fp64 reference."""
+    n, nk, topk = 65536 + 777, 4000, 24
+    g = torch.Generator().manual_seed(11)
+    q = 3.0 * torch.randn(n, 64, generator=g)
+    k = 3.0 * torch.randn(nk, 64, generator=g)
+    v = torch.randn(nk, 64, generator=g).to(torch.bfloat16)
+    idx = torch.randint(0, nk, (n, topk), generator=g, dtype=torch.int32)
+    qd, kd, vd, idd = q.to(DEV), k.to(DEV), v.to(DEV), idx.to(DEV)
+    outs = {}
+    for sliced in (True, False):
+        out = torch.full((n, 64), 7.0, dtype=torch.bfloat16, device=DEV)
+        ops.gather_attn_rows(ops.rows(qd), ops.rows(kd), ops.rows(vd), idd, topk, n, topk, nk, None, ops.rows(out),
+                             qk_fp32=True, sliced=sliced)
+        outs[sliced] = out.cpu()
+    torch.cuda.synchronize()
+    a, b = outs[True].float(), outs[False].float()
+    assert ((a - b).abs() <= torch.maximum(a.abs(), b.abs()) * 2 ** -7 + 1e-4).all(), (a - b).abs().max()
+    rows = torch.tensor([0, 1, 65534, 65535, 65536, 65537, n - 2, n - 1])
+    ref = OA.gather_attention(q[rows].double(), k.double(), v.float(), idx[rows], dtype=torch.float64)
+    _check_close(outs[True][rows], ref, "sliced gather across row chunks")
+
+
 @pytest.mark.parametrize("layout", ["framed", "paired"])
 def test_token_topk_key_row_layouts(ops, layout):
     """Key rows described frame by frame (rows_per_frame == per_frame: the plugin's packed layout)
