@@ -48,7 +48,7 @@
 extern "C" {
 #endif
 
-#define SAF3R_ABI_VERSION 12
+#define SAF3R_ABI_VERSION 13
 
 enum saf3r_status {
   SAF3R_OK = 0,
@@ -229,14 +229,10 @@ int saf3r_pooled_prepare(const float* mean, int64_t rows, uint16_t* split, float
  * Scores are approximated on the matrix cores from the split records with a proven error bound; a
  * (query block, frame) whose best k + 1 approximations are separated by more than the bound is
  * taken from them, every other one (near ties, rows flagged +inf) from the exact sequential scores
- * by a second kernel.
- *   workspace / workspace_bytes: caller-owned device memory of at least
- *     saf3r_block_select_pooled_workspace_bytes(n, frames, blocks_per_frame, k) bytes, 16-byte
- *     aligned: a count and the list of the pairs taken exactly (16 bytes per pair, room for every
- *     pair). The call resets the count itself with a one-thread kernel on the stream (no memset), so
- *     the workspace needs no clearing; calls that share a workspace must be ordered (one stream).
- * 1 <= k <= 32, blocks_per_frame <= 32 (k > 16 runs the sequential kernel on the means), at most
- * 2^32 (query block, frame) pairs over the n heads (SAF3R_ERR_UNSUPPORTED beyond).
+ * of its candidate keys, in the same kernel (one launch).
+ *   workspace / workspace_bytes: not used (saf3r_block_select_pooled_workspace_bytes returns 0);
+ *     NULL / 0 is accepted. They stay in the signature for callers built against ABI 12.
+ * 1 <= k <= 32, blocks_per_frame <= 32 (k > 16 runs the sequential kernel on the means).
  * Replaces: the block top-k of the dynamic pattern (no reference symbol; per-frame semantics of
  *           saf3r/patch/wrapper.py:48 and saf3r/triton/fused_qk_topk.py:120-217 at block level).
  */
@@ -244,8 +240,8 @@ int saf3r_block_select_pooled(const float* mean, const uint16_t* split, const fl
                               int blocks_per_frame, int k, int32_t* idx, void* workspace, int64_t workspace_bytes,
                               void* stream);
 
-/* Workspace bytes of saf3r_block_select_pooled for these sizes (0 when k > 16 selects the sequential
- * kernel), -1 for sizes it rejects. No counterpart in the reference. */
+/* Workspace bytes of saf3r_block_select_pooled for these sizes: 0 (the selection needs none), -1 for
+ * sizes it rejects. No counterpart in the reference. */
 int64_t saf3r_block_select_pooled_workspace_bytes(int n, int frames, int blocks_per_frame, int k);
 
 /*

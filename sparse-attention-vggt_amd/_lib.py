@@ -21,7 +21,7 @@ EXPORTS = (
     "saf3r_pooled_prepare", "saf3r_block_select_pooled", "saf3r_block_select_pooled_workspace_bytes",
     "saf3r_gather_attn_fwd_sliced", "saf3r_gather_attn_workspace_bytes",
 )
-ABI_VERSION = 12
+ABI_VERSION = 13
 GATHER_QK_FP32, GATHER_V_FP32, GATHER_OUT_FP32 = 1, 2, 4  # enum saf3r_gather_dtype
 SAF3R_OK, SAF3R_ERR_INVALID, SAF3R_ERR_UNSUPPORTED, SAF3R_ERR_LAUNCH, SAF3R_ERR_INJECTED = range(5)
 

@@ -24,13 +24,13 @@
 // at least the k-th best's approximation minus E). Each half wave's own list of its KL best tells
 // which of its keys qualify; when its last entry is at least lo, keys past it may too, and every
 // key of that half is a candidate (every key of the frame when the threshold is not finite or zero).
-// block_select_exact_kernel ranks the candidates by their sequential fmaf scores and the composite
-// key (score key, lower index first), as the oracle does (about 1.3% of the pairs at 128 frames on
-// random-init weights).
+// After its frames, the workgroup ranks the candidates of its listed pairs by their sequential fmaf
+// scores and the composite key (score key, lower index first), as the oracle does (about 1.3% of
+// the pairs at 128 frames on random-init weights).
 //
 // Decomposition: a workgroup of 4 waves owns 128 query blocks (32 per wave) of one head and a
 // range of frames. Each frame's key records (NBf rows of 256 bytes, contiguous) are copied once
-// per workgroup into a 3-stage LDS ring by LDS-DMA loads, two frames ahead, 16-byte chunks
+// per workgroup into a 4-stage LDS ring (3 stages for 32-block frames) by LDS-DMA loads, 16-byte chunks
 // XOR-swizzled by row so that the 32 rows a fragment read touches fall into 16 distinct chunk
 // columns. Per frame a wave runs S^T = K . Q^T for the frame's key blocks (padded to 32 rows)
 // against its 32 queries: lane (col, half) holds query col and 16 key rows 8 g + 4 half + r; each
@@ -40,16 +40,16 @@
 // other half get tag bit 4 set, so a half-0 lane reads key 8 (t & 15) / 4 + 4 (t >> 4) + (t & 3)
 // back from tag t. The key scales and the frames' largest key norms are staged in LDS once per
 // workgroup; the certified lists are kept in LDS and written after the frame loop, so that no
-// global store sits between the ring's loads and their waits. The file is compiled without NaN
+// global store sits between the ring's loads and their waits. The listed pairs wait in an LDS queue
+// with room for every pair of the workgroup, and the workgroup scores them exactly after its frames
+// (one pair per half wave at a time), so the selection is one kernel and needs no workspace. The file is compiled without NaN
 // semantics (no canonicalisation before max / med3): every value in a certified pair is finite, and
 // finiteness itself is tested on the bits.
 #include "common.h"
 
 namespace saf3r {
 
-constexpr int kSelRing = 5;          // LDS ring stages (frames): four frames in flight
-constexpr int kSelExactWGs = 2048;   // persistent grid of the exact pass
-constexpr int kSelQueue = 512;       // LDS queue entries per workgroup (listed pairs; more spill over)
+constexpr int kSelQueue = 1024;      // LDS queue entries per workgroup: every (query block, frame) pair of it
 // empty list slots and key rows past the frame: the lowest finite float, whose low mantissa bits
 // are all set, so that tagging it (an OR into those bits) leaves it unchanged and never makes a NaN;
 // with k <= NBf such entries never take part in a certified order
@@ -62,8 +62,6 @@ struct SelMfmaParams {
   const uint16_t* split;  // [n][2][NB][2][64]
   const float* meta;      // [n][2][NB][2]
   int32_t* idx;           // [n][NB][F * ke]
-  uint32_t* qcount;       // the number of listed pairs (cleared before the select kernel)
-  u32x4* queue;           // listed pairs: (query block, frame, candidate key mask, head)
   int F, NBf, NB, ke;
 };
 
@@ -87,26 +85,32 @@ __device__ inline int sel_chunk(int r, int c) { return (r * 16 + (c ^ (r & 15)))
 
 // KL: list length (k + 1 rounded up: 5, 9, 17); NG: groups of 8 key blocks per frame (ceil(NBf / 8)).
 // FPW = 32 / (KL - 1) frames per workgroup (a workgroup's lists are staged in LDS, one byte per
-// entry); about 38 KB of LDS.
+// entry); at most 38 KB of LDS (four workgroups per CU). For lists of up to 9 the compiler is held
+// to four waves per SIMD (at most 128 VGPRs; the exact pass's row loads would take more).
 //
 // Workgroup order (blockIdx.x = r + 8 (j + cm qt), cm = ceil(G / 8) for G frame groups): the
 // hardware hands workgroups to the 8 XCDs in turn, so r is the XCD, and XCD r takes the frame
 // groups g = r + 8 j only. Each XCD's L2 then holds the key records of 1/8 of the frames (about
 // 0.6 MB for 7 heads at 128 frames) for every query tile, instead of all of them.
 template <int KL, int NG>
-__global__ __launch_bounds__(256) void block_select_mfma_kernel(SelMfmaParams p) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KL <= 9 ? 4 : 1))) void block_select_mfma_kernel(
+    SelMfmaParams p) {
   constexpr int FPW = 32 / (KL - 1);
   constexpr int OPB = 36;  // bytes per query row of the staged lists (9 words: no bank conflicts)
   constexpr int kStage = NG * 8 * 256;  // bytes per ring stage: 8 NG key rows of 256 bytes
+  // LDS ring stages (frames): 4 (three frames in flight), 3 for 32-block frames, so that four
+  // workgroups fit a CU's LDS
+  constexpr int kSelRing = NG <= 3 ? 4 : 3;
   __shared__ __align__(16) char ring[kSelRing * kStage];
   // [query][frame in group * ke + t]: the key block in its frame; for a listed pair the first byte is
-  // kQueued (its entry is in the queue) or kSpilled (the queue was full: listed with every key)
+  // kQueued (its entry is in the queue)
   __shared__ __align__(16) uint8_t outb[128 * OPB];
   __shared__ __align__(16) float ksc[FPW][32];  // 2^-sk of the frame's key blocks (0 past NBf)
   __shared__ float nkm[FPW];                    // the frame's largest key norm bound
   __shared__ u32x2 queue[kSelQueue];            // (query in the group, frame in the group), candidate mask
-  __shared__ uint32_t qcount, gbase;
-  constexpr uint8_t kQueued = 0xFE, kSpilled = 0xFF;
+  __shared__ uint32_t qcount;
+  static_assert(128 * FPW <= kSelQueue, "the queue holds every pair of the workgroup");
+  constexpr uint8_t kQueued = 0xFE;
   const int tid = tid_x(), lane = tid & 63, w = tid >> 6, col = lane & 31, half = lane >> 5;
   const int hs = bid_z();
   const int G = (p.F + FPW - 1) / FPW, cm = (G + 7) / 8;
@@ -175,7 +179,7 @@ __global__ __launch_bounds__(256) void block_select_mfma_kernel(SelMfmaParams p)
 
   // wait until frame g's copy has landed, with `after` frames issued after it still in flight (two
   // copies per frame: the loop issues no other vector memory operation)
-  static_assert(kSelRing == 5, "the waits below count up to kSelRing - 2 frames in flight");
+  static_assert(kSelRing >= 3 && kSelRing <= 5, "the waits below count up to 3 frames in flight");
   auto wait_frame = [](int after) {
     switch (after) {
       case 3: wait_vm<6>(); break;
@@ -291,94 +295,72 @@ __global__ __launch_bounds__(256) void block_select_mfma_kernel(SelMfmaParams p)
         if (!usable || p.ke >= p.NBf) mask = all_keys;
         mask &= all_keys;
         const uint32_t at = atomicAdd(&qcount, 1u);
-        if (at < (uint32_t)kSelQueue) queue[at] = u32x2{((uint32_t)qloc << 16) | (uint32_t)fl, mask};
-        o[0] = at < (uint32_t)kSelQueue ? kQueued : kSpilled;
+        queue[at] = u32x2{((uint32_t)qloc << 16) | (uint32_t)fl, mask};
+        o[0] = kQueued;
       }
     }
     acc = acc_next;
   }
   __syncthreads();
-  // the certified lists, one (query, frame) pair per thread at a time (a listed pair's slots get
-  // stale values that the exact pass overwrites); a spilled pair goes to the global list here
+  // the certified lists, one (query, frame) pair per thread at a time (the listed pairs are written
+  // by the exact pass below)
   const int64_t row = (int64_t)p.F * p.ke;
   for (int e = tid; e < 128 * nf; e += 256) {
     const int q = e / nf, fl = e - q * nf;
     const int64_t i = (int64_t)qt * 128 + q;
     if (i >= NB) continue;
     const uint8_t* o = outb + q * OPB + fl * p.ke;
+    if (o[0] == kQueued) continue;
     int32_t* dst = p.idx + ((int64_t)hs * NB + i) * row + (int64_t)(f0 + fl) * p.ke;
     const int fb = (f0 + fl) * p.NBf;
     for (int t = 0; t < p.ke; ++t) dst[t] = fb + o[t];
-    if (o[0] == kSpilled) {
-      const uint32_t at = atomicAdd(p.qcount, 1u);
-      p.queue[at] = u32x4{(uint32_t)i, (uint32_t)(f0 + fl), all_keys, (uint32_t)hs};
-    }
   }
-  // the queued pairs to the global list: one atomic per workgroup reserves its range
-  const uint32_t nq = min(qcount, (uint32_t)kSelQueue);
-  if (tid == 0) gbase = nq ? atomicAdd(p.qcount, nq) : 0u;
-  __syncthreads();
-  for (uint32_t e = tid; e < nq; e += 256) {
-    const u32x2 ent = queue[e];
-    p.queue[gbase + e] = u32x4{(uint32_t)((int64_t)qt * 128 + (ent[0] >> 16)),
-                               (uint32_t)(f0 + (int)(ent[0] & 0xFFFF)), ent[1], (uint32_t)hs};
-  }
-}
-
-__global__ void select_clear_kernel(uint32_t* count) {
-  if (tid_x() == 0) *count = 0;
-}
-
-// The listed pairs, exactly: a persistent grid, one pair per half wave at a time. Lane (half, j)
-// computes the sequential fmaf score of key block j of the pair's frame when j is a candidate; the
-// candidates are ranked by the composite key through LDS (non-candidates hold key 0, below every
-// real key), and the k best written in order.
-__global__ __launch_bounds__(256) void block_select_exact_kernel(SelMfmaParams p) {
-  __shared__ __align__(16) uint64_t keys[8][32];
-  const int tid = tid_x(), lane = tid & 63, w = tid >> 6, col = lane & 31, half = lane >> 5;
+  // The listed pairs of this workgroup, exactly, one pair per half wave at a time: lane (half, j)
+  // computes the sequential fmaf score of key block j of the pair's frame when j is a candidate; the
+  // candidates are ranked by the composite key through LDS (non-candidates hold key 0, below every
+  // real key), and the k best written in order. The ring is free: every copy has landed and every
+  // wave has passed the barrier above.
+  uint64_t* keys = reinterpret_cast<uint64_t*>(ring);  // [8 slots][32]
   const int slot = 2 * w + half;
-  const uint32_t nq = *p.qcount;
-  const int64_t NB = p.NB;
-  const int j = col < p.NBf ? col : p.NBf - 1;
-  const uint32_t stride = (uint32_t)gridDim.x * 8;
-  for (uint32_t e0 = (uint32_t)bid_x() * 8; e0 < nq; e0 += stride) {  // the same trips for every lane
+  const uint32_t nq = qcount;
+  const int jk = col < p.NBf ? col : p.NBf - 1;
+  for (uint32_t e0 = 0; e0 < nq; e0 += 8) {  // the same trips for every lane
     const uint32_t e = e0 + (uint32_t)slot;
     const bool act = e < nq;
-    const u32x4 ent = p.queue[act ? e : e0];
-    const int64_t i = ent[0], hs = ent[3];  // query block, head
-    const int64_t hq = hs * NB + i;
-    const int f = (int)ent[1];
-    const bool cand = act && col < p.NBf && ((ent[2] >> col) & 1u);
+    const u32x2 ent = queue[act ? e : e0];
+    const int64_t i = (int64_t)qt * 128 + (ent[0] >> 16);
+    const int f = f0 + (int)(ent[0] & 0xFFFF);
+    const bool cand = act && col < p.NBf && ((ent[1] >> col) & 1u);
     uint64_t key = 0;
     if (cand) {
-      const f32x4* qr = reinterpret_cast<const f32x4*>(p.mean + (hs * 2 * NB + i) * 64);
-      const f32x4* kv = reinterpret_cast<const f32x4*>(p.mean + ((hs * 2 + 1) * NB + (int64_t)f * p.NBf + j) * 64);
+      const f32x4* qr = reinterpret_cast<const f32x4*>(p.mean + ((int64_t)hs * 2 * NB + i) * 64);
+      const f32x4* kv = reinterpret_cast<const f32x4*>(p.mean + (krec0 + (int64_t)f * p.NBf + jk) * 64);
       f32x4 qa[16], kb[16];  // both rows in flight at once, then the chain
 #pragma unroll
       for (int d4 = 0; d4 < 16; ++d4) {
         qa[d4] = qr[d4];
         kb[d4] = kv[d4];
       }
-      float acc = 0.f;
+      float a = 0.f;
 #pragma unroll
       for (int d4 = 0; d4 < 16; ++d4) {
-        acc = __builtin_fmaf(qa[d4][0], kb[d4][0], acc);
-        acc = __builtin_fmaf(qa[d4][1], kb[d4][1], acc);
-        acc = __builtin_fmaf(qa[d4][2], kb[d4][2], acc);
-        acc = __builtin_fmaf(qa[d4][3], kb[d4][3], acc);
+        a = __builtin_fmaf(qa[d4][0], kb[d4][0], a);
+        a = __builtin_fmaf(qa[d4][1], kb[d4][1], a);
+        a = __builtin_fmaf(qa[d4][2], kb[d4][2], a);
+        a = __builtin_fmaf(qa[d4][3], kb[d4][3], a);
       }
-      key = ckey(acc, (uint32_t)j);
+      key = ckey(a, (uint32_t)jk);
     }
-    keys[slot][col] = key;
+    keys[slot * 32 + col] = key;
     __builtin_amdgcn_wave_barrier();
     asm volatile("" ::: "memory");
     int rank = 0;  // every slot's key read at once
 #pragma unroll
     for (int c = 0; c < 32; c += 2) {
-      const u32x4 kk = *reinterpret_cast<const u32x4*>(&keys[slot][c]);
+      const u32x4 kk = *reinterpret_cast<const u32x4*>(&keys[slot * 32 + c]);
       rank += ((((uint64_t)kk[1] << 32) | kk[0]) > key) + ((((uint64_t)kk[3] << 32) | kk[2]) > key);
     }
-    if (cand && rank < p.ke) p.idx[hq * ((int64_t)p.F * p.ke) + (int64_t)f * p.ke + rank] = f * p.NBf + j;
+    if (cand && rank < p.ke) p.idx[((int64_t)hs * NB + i) * row + (int64_t)f * p.ke + rank] = f * p.NBf + jk;
     __builtin_amdgcn_wave_barrier();
     asm volatile("" ::: "memory");
   }
@@ -427,12 +409,7 @@ extern "C" int64_t saf3r_block_select_pooled_workspace_bytes(int n, int frames, 
   if (n <= 0 || n > 65535 || frames <= 0 || blocks_per_frame <= 0 || blocks_per_frame > 32 ||
       (int64_t)frames * blocks_per_frame > 0x7fffffff / 64 || k < 1 || k > 32)
     return -1;
-  const int ke = k < blocks_per_frame ? k : blocks_per_frame;
-  if (ke > 16) return 0;  // the sequential kernel: no workspace
-  // the list's count is 32-bit
-  if ((int64_t)n * frames * blocks_per_frame * frames > 0xFFFFFFFFll) return -1;
-  // a 16-byte count slot, then one 16-byte entry per (query block, frame) pair: the worst case
-  return 16 + (int64_t)n * frames * blocks_per_frame * frames * 16;
+  return 0;  // every pair is taken exactly inside its workgroup; the k > 16 kernel needs none either
 }
 
 extern "C" int saf3r_block_select_pooled(const float* mean, const uint16_t* split, const float* meta, int n,
@@ -460,14 +437,8 @@ extern "C" int saf3r_block_select_pooled(const float* mean, const uint16_t* spli
     }
     return SAF3R_OK;
   }
-  const int64_t need = saf3r_block_select_pooled_workspace_bytes(n, frames, blocks_per_frame, k);
-  if (need < 0)
-    return fail(SAF3R_ERR_UNSUPPORTED, "saf3r_block_select_pooled: more than 2^32 (query block, frame) pairs");
-  if (!workspace || workspace_bytes < need || (uintptr_t)workspace % 16)
-    return fail(SAF3R_ERR_INVALID,
-                "saf3r_block_select_pooled: needs a 16-byte aligned workspace of %lld bytes "
-                "(saf3r_block_select_pooled_workspace_bytes), got %lld",
-                (long long)need, (long long)(workspace ? workspace_bytes : 0));
+  (void)workspace;  // none is needed (the size query returns 0); kept for the entry's signature
+  (void)workspace_bytes;
   const int fpw = select_fpw(ke), groups = (frames + fpw - 1) / fpw;
   const dim3 grid((unsigned)(8 * ((groups + 7) / 8) * ((NB + 127) / 128)), 1u, (unsigned)n);
   SelMfmaParams p;
@@ -475,18 +446,13 @@ extern "C" int saf3r_block_select_pooled(const float* mean, const uint16_t* spli
   p.split = split;
   p.meta = meta;
   p.idx = idx;
-  p.qcount = static_cast<uint32_t*>(workspace);
-  p.queue = reinterpret_cast<u32x4*>(static_cast<char*>(workspace) + 16);
   p.F = frames;
   p.NBf = NBf;
   p.NB = NB;
   p.ke = ke;
   const int ng = (NBf + 7) / 8;
-  hipLaunchKernelGGL(select_clear_kernel, dim3(1), dim3(64), 0, st, p.qcount);
   if (ke <= 4) launch_select_mfma<5>(ng, grid, st, p);
   else if (ke <= 8) launch_select_mfma<9>(ng, grid, st, p);
   else launch_select_mfma<17>(ng, grid, st, p);
-  if (int rc = check_launch("saf3r_block_select_pooled")) return rc;
-  hipLaunchKernelGGL(block_select_exact_kernel, dim3(kSelExactWGs), dim3(256), 0, st, p);
   return check_launch("saf3r_block_select_pooled");
 }

@@ -285,13 +285,10 @@ def pooled_prepare(mean: torch.Tensor) -> Pooled:
     return res
 
 
-_select_ws = {}  # (device, bytes) -> the selection's workspace, kept for the next call of the same size
-
-
 def block_select_pooled(pooled: Pooled, frames: int, blocks_per_frame: int, k: int) -> torch.Tensor:
     """Per-frame block top-k on the matrix cores (``saf3r_block_select_pooled``), bit-identical to
-    ``block_select`` on ``pooled.mean``: int32 [n, NB, frames*min(k, NBf)] of global block ids. The
-    workspace (queues of the pairs taken exactly) is a torch allocation kept per device and size."""
+    ``block_select`` on ``pooled.mean``: int32 [n, NB, frames*min(k, NBf)] of global block ids (one
+    launch; no workspace)."""
     _need_cuda(pooled.mean, pooled.split, pooled.meta)
     lib = _lib.load()
     n, _, nb, _ = pooled.mean.shape
@@ -299,17 +296,11 @@ def block_select_pooled(pooled: Pooled, frames: int, blocks_per_frame: int, k: i
         raise ValueError("pooled records do not match frames * blocks_per_frame")
     dev = pooled.mean.device
     idx = torch.empty(n, nb, frames * min(k, blocks_per_frame), dtype=torch.int32, device=dev)
-    nbytes = lib.saf3r_block_select_pooled_workspace_bytes(n, frames, blocks_per_frame, k)
-    if nbytes < 0:
+    if lib.saf3r_block_select_pooled_workspace_bytes(n, frames, blocks_per_frame, k) < 0:
         raise ValueError(f"unsupported block selection: {n} heads, {frames} frames x {blocks_per_frame} blocks, k {k}")
-    key = (dev.index, int(nbytes))
-    ws = _select_ws.get(key)
-    if ws is None and nbytes:
-        ws = _select_ws[key] = torch.empty(nbytes, dtype=torch.uint8, device=dev)
     _mark("block_select", "start")
     _lib.check(lib.saf3r_block_select_pooled(_ptr(pooled.mean), _ptr(pooled.split), _ptr(pooled.meta), n, frames,
-                                             blocks_per_frame, k, _ptr(idx), _ptr(ws), int(nbytes),
-                                             _lib.stream_ptr()))
+                                             blocks_per_frame, k, _ptr(idx), None, 0, _lib.stream_ptr()))
     _mark("block_select", "end")
     return idx
 

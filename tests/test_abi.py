@@ -24,7 +24,7 @@ def test_library_exports_every_declared_symbol(pkg):
     for n in names:
         assert hasattr(lib, n), n
     assert set(names) == set(lib_mod.EXPORTS)
-    assert lib.saf3r_abi_version() == lib_mod.ABI_VERSION == 12
+    assert lib.saf3r_abi_version() == lib_mod.ABI_VERSION == 13
 
 
 def test_packed_slots_matches_layout(pkg):
@@ -186,12 +186,9 @@ def test_invalid_arguments_fail_before_launch(pkg):
     assert rc == 2 and b"k must be" in lib.saf3r_last_error()
     rc = lib.saf3r_block_select_pooled(dev, None, dev, 1, 4, 22, 4, dev, None, 0, None)
     assert rc == 1 and b"null" in lib.saf3r_last_error()
-    need = lib.saf3r_block_select_pooled_workspace_bytes(7, 128, 22, 4)
-    assert need == 16 + 7 * 128 * 22 * 128 * 16  # a count, then a 16-byte entry per (query block, frame)
+    assert lib.saf3r_block_select_pooled_workspace_bytes(7, 128, 22, 4) == 0  # the selection needs no workspace
     assert lib.saf3r_block_select_pooled_workspace_bytes(1, 4, 22, 20) == 0  # k > 16: the sequential kernel
     assert lib.saf3r_block_select_pooled_workspace_bytes(1, 4, 33, 4) == -1
-    rc = lib.saf3r_block_select_pooled(dev, dev, dev, 7, 128, 22, 4, dev, dev, need - 1, None)
-    assert rc == 1 and b"workspace" in lib.saf3r_last_error()
     with pytest.raises(L.Saf3rError):
         L.check(1)
 
