@@ -338,6 +338,8 @@ int saf3r_keyset_gather(const void* k_packed, int frames, int tokens_per_frame, 
  *        device's wall clock divided by the walk's step time points to, so that the work-groups
  *        resident at one moment read nearby key tiles (cache reuse); the summation order, and so the
  *        last bits of the output, then vary from run to run (always within the bf16 tolerance).
+ *        The block lists of BLOCK_DYNAMIC heads are walked that way only when those heads' K and V
+ *        rows exceed 256 MiB (the Infinity Cache); below, from their first position.
  *        With it, every walk starts at its first tile and the output is run-to-run identical.
  *   pace, pace_seq: the walks' step times. pace is NULL (default step times) or a caller-owned
  *        device array of 12 uint64, zero-filled once and passed to every call, with pace_seq

@@ -1440,6 +1440,9 @@ static int head_segments(int h, int pat, bool tokord, bool framed, int ntt, cons
 // block-dynamic throughput (a phase shorter than the walk's real step time scatters the work-groups
 // over the key frames, a longer one costs little). Converted to wall-clock ticks with the device's
 // clock rate, queried on every call (no cached state).
+// the K + V bytes of the block-dynamic heads from which split-mode walks are clock-paced
+constexpr int64_t kSplitPacedMinBytes = (int64_t)256 << 20;
+
 static void set_phase(AttnParams* p, bool fixed_order) {
   p->phase_dense = p->phase_split = 0;
   if (fixed_order) return;
@@ -1559,6 +1562,18 @@ extern "C" int saf3r_sparse_attn_fwd(const void* q_packed, const void* k_packed,
   if ((uintptr_t)pace % 8) return fail(SAF3R_ERR_INVALID, "saf3r_sparse_attn_fwd: pace must be 8-byte aligned");
   const bool fixed = (flags & SAF3R_ATTN_FIXED_ORDER) != 0;
   set_phase(&p, fixed);
+  // Split-mode walks start at their first list position when the K and V rows of the block-dynamic
+  // heads fit the 256 MiB Infinity Cache: work-groups that started at different times then read
+  // different frames, all served from that cache, and the clock-paced order (every resident
+  // work-group on the same frames) measured slower there: 16 block-top-4 heads at 32 / 48 frames
+  // (185 / 278 MB) ran 548 / 725 TFLOP/s paced against 753 / 782 in that order, at 64 / 96 frames
+  // (370 / 556 MB) 808 / 862 paced against 790 / 601.
+  {
+    int64_t split_bytes = 0;
+    for (int h = 0; h < num_heads; ++h)
+      if (p.pattern[h] == SAF3R_BLOCK_DYNAMIC) split_bytes += (int64_t)p.g.L * 256;  // K + V rows of 128 B
+    if (split_bytes <= kSplitPacedMinBytes) p.phase_split = 0;
+  }
   p.pace = fixed ? nullptr : pace;
   p.pace_read = (int)(pace_seq % 3u);
   p.pace_acc = (int)((pace_seq + 1u) % 3u);
