@@ -108,7 +108,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KL <= 9 ? 4
   __shared__ __align__(16) float ksc[FPW][32];  // 2^-sk of the frame's key blocks (0 past NBf)
   __shared__ float nkm[FPW];                    // the frame's largest key norm bound
   __shared__ u32x2 queue[kSelQueue];            // (query in the group, frame in the group), candidate mask
-  __shared__ uint32_t qcount;
+  __shared__ uint32_t qcount, wsum[4];
   static_assert(128 * FPW <= kSelQueue, "the queue holds every pair of the workgroup");
   constexpr uint8_t kQueued = 0xFE;
   const int tid = tid_x(), lane = tid & 63, w = tid >> 6, col = lane & 31, half = lane >> 5;
@@ -315,26 +315,72 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KL <= 9 ? 4
     const int fb = (f0 + fl) * p.NBf;
     for (int t = 0; t < p.ke; ++t) dst[t] = fb + o[t];
   }
-  // The listed pairs of this workgroup, exactly, one pair per half wave at a time: lane (half, j)
-  // computes the sequential fmaf score of key block j of the pair's frame when j is a candidate; the
-  // candidates are ranked by the composite key through LDS (non-candidates hold key 0, below every
-  // real key), and the k best written in order. The ring is free: every copy has landed and every
-  // wave has passed the barrier above.
-  uint64_t* keys = reinterpret_cast<uint64_t*>(ring);  // [8 slots][32]
-  const int slot = 2 * w + half;
+  // The listed pairs of this workgroup, exactly, one candidate key per thread: the candidates are
+  // numbered pair by pair (an exclusive prefix of the masks' popcounts), every thread computes the
+  // sequential fmaf score of one candidate from the fp32 means (one round of row loads for up to 256
+  // candidates), and a candidate's rank among its pair's candidates by the composite key (higher
+  // score, then lower block) places it among the k best. Pairs whose candidates exceed the LDS space
+  // run in batches. The ring is free: every copy has landed and every wave has passed the barrier
+  // above.
+  constexpr int kOffBytes = ((kSelQueue + 1) * 2 + 15) / 16 * 16;
+  constexpr int kCandMax = (kSelRing * kStage - kOffBytes) / 6 / 4 * 4;
+  static_assert(kCandMax >= 32, "the candidates of one pair fit");
+  uint16_t* coff = reinterpret_cast<uint16_t*>(ring);                                // [nq + 1]
+  float* csc = reinterpret_cast<float*>(ring + kOffBytes);                          // [kCandMax] scores
+  uint16_t* cid = reinterpret_cast<uint16_t*>(ring + kOffBytes + 4 * kCandMax);     // [kCandMax] pair << 5 | key
   const uint32_t nq = qcount;
-  const int jk = col < p.NBf ? col : p.NBf - 1;
-  for (uint32_t e0 = 0; e0 < nq; e0 += 8) {  // the same trips for every lane
-    const uint32_t e = e0 + (uint32_t)slot;
-    const bool act = e < nq;
-    const u32x2 ent = queue[act ? e : e0];
-    const int64_t i = (int64_t)qt * 128 + (ent[0] >> 16);
-    const int f = f0 + (int)(ent[0] & 0xFFFF);
-    const bool cand = act && col < p.NBf && ((ent[1] >> col) & 1u);
-    uint64_t key = 0;
-    if (cand) {
+  {
+    uint32_t cnt[4], tsum = 0;  // thread t counts the candidates of pairs 4t .. 4t + 3
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const uint32_t e = 4 * tid + u;
+      cnt[u] = e < nq ? (uint32_t)__builtin_popcount(queue[e][1]) : 0u;
+      tsum += cnt[u];
+    }
+    uint32_t inc = tsum;  // inclusive prefix within the wave
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint32_t y = __shfl_up(inc, o);
+      if (lane >= o) inc += y;
+    }
+    if (lane == 63) wsum[w] = inc;
+    __syncthreads();
+    uint32_t pre = inc - tsum;
+    for (int v = 0; v < w; ++v) pre += wsum[v];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const uint32_t e = 4 * tid + u;
+      if (e < nq) coff[e] = (uint16_t)pre;
+      pre += cnt[u];
+    }
+    if (tid == 0) coff[nq] = (uint16_t)(wsum[0] + wsum[1] + wsum[2] + wsum[3]);
+    __syncthreads();
+  }
+  for (uint32_t p0 = 0; p0 < nq;) {  // the same trips for every thread
+    // pairs p0 .. p1 - 1: the longest run from p0 whose candidates fit (one pair always does)
+    const uint32_t base = coff[p0];
+    uint32_t lo = p0 + 1, hi = nq;
+    while (lo < hi) {
+      const uint32_t mid = (lo + hi + 1) >> 1;
+      if (coff[mid] - base <= (uint32_t)kCandMax) lo = mid;
+      else hi = mid - 1;
+    }
+    const uint32_t p1 = lo, nc = coff[p1] - base;
+    for (uint32_t e = p0 + tid; e < p1; e += 256) {
+      uint32_t m = queue[e][1], o = coff[e] - base;
+      while (m) {
+        cid[o++] = (uint16_t)((e << 5) | (uint32_t)__builtin_ctz(m));
+        m &= m - 1;
+      }
+    }
+    __syncthreads();
+    for (uint32_t c = tid; c < nc; c += 256) {
+      const uint32_t v = cid[c], j = v & 31;
+      const u32x2 ent = queue[v >> 5];
+      const int64_t i = (int64_t)qt * 128 + (ent[0] >> 16);
+      const int f = f0 + (int)(ent[0] & 0xFFFF);
       const f32x4* qr = reinterpret_cast<const f32x4*>(p.mean + ((int64_t)hs * 2 * NB + i) * 64);
-      const f32x4* kv = reinterpret_cast<const f32x4*>(p.mean + (krec0 + (int64_t)f * p.NBf + jk) * 64);
+      const f32x4* kv = reinterpret_cast<const f32x4*>(p.mean + (krec0 + (int64_t)f * p.NBf + j) * 64);
       f32x4 qa[16], kb[16];  // both rows in flight at once, then the chain
 #pragma unroll
       for (int d4 = 0; d4 < 16; ++d4) {
@@ -349,20 +395,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KL <= 9 ? 4
         a = __builtin_fmaf(qa[d4][2], kb[d4][2], a);
         a = __builtin_fmaf(qa[d4][3], kb[d4][3], a);
       }
-      key = ckey(a, (uint32_t)jk);
+      csc[c] = a;
     }
-    keys[slot * 32 + col] = key;
-    __builtin_amdgcn_wave_barrier();
-    asm volatile("" ::: "memory");
-    int rank = 0;  // every slot's key read at once
-#pragma unroll
-    for (int c = 0; c < 32; c += 2) {
-      const u32x4 kk = *reinterpret_cast<const u32x4*>(&keys[slot * 32 + c]);
-      rank += ((((uint64_t)kk[1] << 32) | kk[0]) > key) + ((((uint64_t)kk[3] << 32) | kk[2]) > key);
+    __syncthreads();
+    for (uint32_t c = tid; c < nc; c += 256) {
+      const uint32_t v = cid[c], e = v >> 5, j = v & 31;
+      const uint64_t key = ckey(csc[c], j);
+      const uint32_t b0 = coff[e] - base, b1 = coff[e + 1] - base;
+      int rank = 0;
+      for (uint32_t c2 = b0; c2 < b1; ++c2) rank += ckey(csc[c2], cid[c2] & 31u) > key ? 1 : 0;
+      if (rank < p.ke) {
+        const u32x2 ent = queue[e];
+        const int64_t i = (int64_t)qt * 128 + (ent[0] >> 16);
+        const int f = f0 + (int)(ent[0] & 0xFFFF);
+        p.idx[((int64_t)hs * NB + i) * row + (int64_t)f * p.ke + rank] = f * p.NBf + (int)j;
+      }
     }
-    if (cand && rank < p.ke) p.idx[((int64_t)hs * NB + i) * row + (int64_t)f * p.ke + rank] = f * p.NBf + jk;
-    __builtin_amdgcn_wave_barrier();
-    asm volatile("" ::: "memory");
+    __syncthreads();  // the next batch overwrites the candidates
+    p0 = p1;
   }
 }
 
