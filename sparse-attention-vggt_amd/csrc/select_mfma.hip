@@ -19,7 +19,8 @@
 // pairwise by more than thr = 2 E_max + 2^-17 |q| |k|max (E_max over the frame's key blocks): the
 // exact scores then have the same order, strictly, so the top-k and its order are those of a. Every
 // other pair (near ties, rows outside the bound's range: norm +inf, which makes the threshold +inf
-// or NaN; a zero threshold, where the tags alone would order exact ties) goes to a list in the caller's workspace with its candidate keys: those whose tagged a is
+// or NaN; a zero threshold, where the tags alone would order exact ties) is listed with its
+// candidate keys: those whose tagged a is
 // at least lo = (k-th best tagged a) - thr, which hold the true top-k (its members' exact scores are
 // at least the k-th best's approximation minus E). Each half wave's own list of its KL best tells
 // which of its keys qualify; when its last entry is at least lo, keys past it may too, and every
@@ -41,10 +42,10 @@
 // back from tag t. The key scales and the frames' largest key norms are staged in LDS once per
 // workgroup; the certified lists are kept in LDS and written after the frame loop, so that no
 // global store sits between the ring's loads and their waits. The listed pairs wait in an LDS queue
-// with room for every pair of the workgroup, and the workgroup scores them exactly after its frames
-// (one pair per half wave at a time), so the selection is one kernel and needs no workspace. The file is compiled without NaN
-// semantics (no canonicalisation before max / med3): every value in a certified pair is finite, and
-// finiteness itself is tested on the bits.
+// with room for every pair of the workgroup, and the workgroup scores their candidates exactly after
+// its frames (one candidate key per thread), so the selection is one kernel and needs no workspace.
+// The file is compiled without NaN semantics (no canonicalisation before max / med3): every value
+// in a certified pair is finite, and finiteness itself is tested on the bits.
 #include "common.h"
 
 namespace saf3r {
