@@ -464,10 +464,11 @@ def run_stack(pkg, frames, dim, heads, grid, layers, topk, table_fn, steps, warm
     return res
 
 
-def pool_increment(run, reps=10):
+def pool_increment(run, reps=10, burst=4):
     """What pooling adds to the pack: the first layer's pack (LayerNorm, RoPE, layouts, scaled Q) with
-    and without the block records of its block_topk heads, alternated ``reps`` times, each launch
-    timed by its own stream events; medians in ms."""
+    and without the block records of its block_topk heads, alternated ``reps`` times; each time
+    ``burst`` packs run back to back between two stream events (the GPU stays busy, so the host's
+    launch work between the packs is not timed). Medians of the per-pack times, in ms."""
     w, x, pos, geom = run["layers"][0], run["x"], run["pos"], run["geom"]
     ts = {True: [], False: []}
     with torch.no_grad():
@@ -479,10 +480,11 @@ def pool_increment(run, reps=10):
             for pool in (True, False):
                 e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
                 e0.record()
-                w.pack(qkv, pos, geom, pool)
+                for _ in range(burst):
+                    w.pack(qkv, pos, geom, pool)
                 e1.record()
                 torch.cuda.synchronize()
-                ts[pool].append(e0.elapsed_time(e1))
+                ts[pool].append(e0.elapsed_time(e1) / burst)
     del qkv
     return statistics.median(ts[True]), statistics.median(ts[False])
 
@@ -674,9 +676,9 @@ def main():
             "fused_path_frac": round(sb["fused_path"] / (fused * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
             "fused_path_bytes": sb["fused_path"],
             "fused_path_note": ("algorithmic bytes (read Q and K of the block_topk heads, write their lists) over the "
-                                "selection's added time: the pack's increment for the block means (median of "
-                                "alternating packs with / without them, negative values counted as 0) plus the "
-                                "selection kernel"),
+                                "selection's added time: the pack's increment for the block means (medians of "
+                                "alternating bursts of 4 back-to-back packs with / without them, negative values "
+                                "counted as 0) plus the selection kernel"),
             "heads": n_dyn,
         }
         sel_extra.update(sel_extra_scores)
