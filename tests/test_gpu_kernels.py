@@ -233,6 +233,21 @@ def test_block_select_pooled_adversarial_bit_exact(ops, frames, nbf, k, case):
         assert np.array_equal(got[h], ref), f"{case}: head {h} differs from the oracle"
 
 
+@pytest.mark.parametrize("frames,nbf,k", [(24, 22, 4), (12, 21, 8), (9, 32, 4), (16, 6, 2)])
+def test_block_select_pooled_many_listed_pairs(ops, frames, nbf, k):
+    """Pooled means in {-1/4, 0, 1/4}: exact score ties everywhere, so about 4 in 5 (query block,
+    frame) pairs are listed and a work-group's exact pass holds more candidates than its LDS space
+    (several batches); bit-identical to the oracle's sequential selection."""
+    rng = np.random.default_rng(frames * 13 + nbf + k)
+    n, nb = 2, frames * nbf
+    mean = (rng.integers(-1, 2, size=(n, 2, nb, 64)).astype(np.float32) * np.float32(0.25))
+    pooled = ops.pooled_prepare(torch.from_numpy(mean).to(DEV))
+    got = ops.block_select_pooled(pooled, frames, nbf, k).cpu().numpy()
+    for h in range(n):
+        ref = OS.frame_topk(OS.block_scores(mean[h, 0], mean[h, 1]), frames, k)
+        assert np.array_equal(got[h], ref), f"head {h}"
+
+
 def test_block_select_pooled_128_frames(ops):
     """128 frames x 22 blocks of N(0, 1/64)-like pooled means (the benchmark's scale), 3 heads: the
     matrix-core selection is bit-identical to the oracle's sequential selection."""
