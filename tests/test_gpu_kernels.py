@@ -678,11 +678,12 @@ def test_gather_attention_sliced(ops, n, nk, topk, rpf):
     assert ((a - b).abs() <= torch.maximum(a.abs(), b.abs()) * 2 ** -7 + 1e-4).all(), (a - b).abs().max()
 
 
-def test_gather_attention_sliced_row_chunks(ops):
+@pytest.mark.parametrize("n", [65536 + 777, 2 * 65536 + 5])
+def test_gather_attention_sliced_row_chunks(ops, n):
     """The sliced gather runs rows in chunks of 65536 (both kernels per chunk, one chunk's partials in
-    the workspace): 2 chunks, the second partial. Every row against the one-pass kernel, and rows at
-    the chunk boundary and the ends against the fp64 reference."""
-    n, nk, topk = 65536 + 777, 4000, 24
+    the workspace): 2 and 3 chunks, the last one partial. Every row against the one-pass kernel, and
+    rows at the chunk boundaries and the ends against the fp64 reference."""
+    nk, topk = 4000, 24
     g = torch.Generator().manual_seed(11)
     q = 3.0 * torch.randn(n, 64, generator=g)
     k = 3.0 * torch.randn(nk, 64, generator=g)
@@ -698,7 +699,7 @@ def test_gather_attention_sliced_row_chunks(ops):
     torch.cuda.synchronize()
     a, b = outs[True].float(), outs[False].float()
     assert ((a - b).abs() <= torch.maximum(a.abs(), b.abs()) * 2 ** -7 + 1e-4).all(), (a - b).abs().max()
-    rows = torch.tensor([0, 1, 65534, 65535, 65536, 65537, n - 2, n - 1])
+    rows = torch.tensor(sorted({0, 1, 65534, 65535, 65536, 65537, 131071, 131072, n - 2, n - 1} & set(range(n))))
     ref = OA.gather_attention(q[rows].double(), k.double(), v.float(), idx[rows], dtype=torch.float64)
     _check_close(outs[True][rows], ref, "sliced gather across row chunks")
 
