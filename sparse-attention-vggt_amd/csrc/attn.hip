@@ -1435,14 +1435,14 @@ static int head_segments(int h, int pat, bool tokord, bool framed, int ntt, cons
   return n;
 }
 
+// the K + V bytes of the block-dynamic heads above which split-mode walks are clock-paced
+constexpr int64_t kSplitPacedMinBytes = (int64_t)256 << 20;
+
 // Default step times of the key walks (the first call on a pace state, or without one), from sweeps
 // at the 128-frame VGGT shape: the split value sits at the long end of the plateau of best
 // block-dynamic throughput (a phase shorter than the walk's real step time scatters the work-groups
 // over the key frames, a longer one costs little). Converted to wall-clock ticks with the device's
 // clock rate, queried on every call (no cached state).
-// the K + V bytes of the block-dynamic heads from which split-mode walks are clock-paced
-constexpr int64_t kSplitPacedMinBytes = (int64_t)256 << 20;
-
 static void set_phase(AttnParams* p, bool fixed_order) {
   p->phase_dense = p->phase_split = 0;
   if (fixed_order) return;
