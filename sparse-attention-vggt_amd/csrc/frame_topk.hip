@@ -115,7 +115,15 @@ __global__ __launch_bounds__(256) void frame_select_kernel(FrameTopkParams p) {
   const int64_t s0 = (int64_t)f * p.P;        // first key of the frame in the row
   const int64_t a0 = s0 & ~(int64_t)7;        // aligned span start
   const uint16_t* rowp = p.scores + (int64_t)row * p.srs;
-  uint32_t key[RC][8];  // 0xFFFFFFFF: no key
+  // order keys of the frame's scores; slots outside the frame hold 0, which no threshold of the
+  // search counts (its thresholds are >= 1; a real key 0, the lowest, only matters at t = 0)
+  uint32_t key[RC][8];
+  const int lo_e = (int)(s0 - a0);  // valid slot positions: lo_e <= 8 (lane + 64 r) + e < lo_e + P
+  auto valid = [&](int r, int e) {
+    const uint32_t pos = (uint32_t)(8 * (lane + 64 * r) + e - lo_e);
+    return pos < (uint32_t)p.P;
+  };
+  int nv = 0;
 #pragma unroll
   for (int r = 0; r < RC; ++r) {
     const int64_t e0 = a0 + 8 * (int64_t)(lane + 64 * r);
@@ -123,17 +131,18 @@ __global__ __launch_bounds__(256) void frame_select_kernel(FrameTopkParams p) {
     if (e0 < s0 + p.P) v = *reinterpret_cast<const u32x4*>(rowp + e0);
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const int64_t x = e0 + e;
       const uint16_t b = (uint16_t)(v[e >> 1] >> (16 * (e & 1)));
-      key[r][e] = (x >= s0 && x < s0 + p.P) ? sortable16(b) : 0xFFFFFFFFu;
+      const bool in = valid(r, e);
+      key[r][e] = in ? sortable16(b) : 0u;
+      nv += in ? 1 : 0;
     }
   }
-  auto count_ge = [&](uint32_t t) {  // valid keys >= t, wave-wide
+  auto count_ge = [&](uint32_t t) {  // keys >= t (t >= 1), wave-wide
     int c = 0;
 #pragma unroll
     for (int r = 0; r < RC; ++r)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) c += (key[r][e] != 0xFFFFFFFFu && key[r][e] >= t) ? 1 : 0;
+      for (int e = 0; e < 8; ++e) c += key[r][e] >= t ? 1 : 0;
     // per-lane counts summed by ballots of their bits (c <= 8 * RC <= 72)
     int sum = 0;
 #pragma unroll
@@ -141,14 +150,41 @@ __global__ __launch_bounds__(256) void frame_select_kernel(FrameTopkParams p) {
     return sum;
   };
   const int k = p.k;
-  uint32_t lo = 0, hi = 65535;  // count(key >= lo) >= k holds for lo = 0
+  // Bracket for the bisection: t is at most the largest key, and for k <= 64 at least the k-th
+  // largest of the lanes' largest keys (k distinct keys reach it), found by a bisection over one
+  // value per lane (a compare and a ballot per step).
+  uint32_t lmax = 0;
+#pragma unroll
+  for (int r = 0; r < RC; ++r)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) lmax = max(lmax, key[r][e]);
+  uint32_t hi = lmax;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) hi = max(hi, (uint32_t)__shfl_xor((int)hi, o));
+  uint32_t lo = 0;  // count(key >= lo) >= k holds for lo = 0
+  const bool any = nv > 0;
+  if (k <= 64 && __popcll(__ballot(any)) >= k) {
+    uint32_t a = 0, b = hi;  // count(lane maxima >= a) >= k
+    while (a < b) {
+      const uint32_t mid = (a + b + 1) >> 1;
+      if (__popcll(__ballot(any && lmax >= mid)) >= k) a = mid;
+      else b = mid - 1;
+    }
+    lo = a;
+  }
+  int c_above = 0;  // count(key >= hi + 1): 0 for the largest key, then the count of the last miss
   while (lo < hi) {
     const uint32_t mid = (lo + hi + 1) >> 1;
-    if (count_ge(mid) >= k) lo = mid;
-    else hi = mid - 1;
+    const int c = count_ge(mid);
+    if (c >= k) {
+      lo = mid;
+    } else {
+      hi = mid - 1;
+      c_above = c;
+    }
   }
   const uint32_t t = lo;
-  const int need_eq = k - (t < 65535 ? count_ge(t + 1) : 0);  // keys equal to t to keep, lowest first
+  const int need_eq = k - c_above;  // keys equal to t to keep, lowest first
   int32_t* o = p.out + (int64_t)row * p.ors + p.ocol + (int64_t)fs * k;
   uint16_t* ok = p.okey ? p.okey + (int64_t)row * p.ors + (int64_t)fs * k : nullptr;
   int base = 0, eq_seen = 0;
@@ -156,16 +192,16 @@ __global__ __launch_bounds__(256) void frame_select_kernel(FrameTopkParams p) {
   for (int r = 0; r < RC; ++r) {
     int neq = 0;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) neq += key[r][e] == t ? 1 : 0;
+    for (int e = 0; e < 8; ++e) neq += (valid(r, e) && key[r][e] == t) ? 1 : 0;
     int eq_tot;
     const int eq_pre = eq_seen + wave_prefix4(neq, &eq_tot);
     int nsel = 0, eq_run = 0;
     bool sel[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const bool valid = key[r][e] != 0xFFFFFFFFu;
-      const bool eq = valid && key[r][e] == t;
-      sel[e] = valid && (key[r][e] > t || (eq && eq_pre + eq_run < need_eq));
+      const bool in = valid(r, e);
+      const bool eq = in && key[r][e] == t;
+      sel[e] = in && (key[r][e] > t || (eq && eq_pre + eq_run < need_eq));
       eq_run += eq ? 1 : 0;
       nsel += sel[e] ? 1 : 0;
     }

@@ -32,6 +32,8 @@ CASES = [  # frames, per_frame, topk, per_frame_mode, exclude_first, first_strid
     (4, 70, 50, False, False, 1, 0),
     (3, 200, 90, False, True, 8, 40),
     (1, 9, 20, True, False, 1, 0),
+    (3, 1369, 64, True, False, 1, 0),
+    (2, 1369, 100, True, True, 2, 0),
 ]
 
 
