@@ -13,9 +13,9 @@
 //     R = ceil(N / 256) tokens summed sequentially, chunk sums added in order, one division).
 //   probe_scores_kernel: score[t] = sequential fmaf over d of qbar[d] k[t][d], times 1/sqrt(D).
 //   keyset_build_kernel: one work-group per head. Top-k by a 4-pass radix select on the
-//     sortable key (ties to the lower index), then one ordered pass over the tokens that marks
-//     members (top-k or strided, plus the anchor frame and specials) and compacts them in
-//     increasing token order with work-group prefix counts.
+//     sortable key (ties to the lower index), then the members (top-k or strided, plus the anchor
+//     frame and specials) in increasing token order: each wave marks a contiguous run of tokens
+//     in LDS masks, one prefix over the waves places the runs, and each wave writes its own.
 //   keyset_gather_kernel: compact K rows and transposed, permuted V tiles of the members, in
 //     the packed layout the attention kernel reads.
 #include <mutex>
@@ -130,29 +130,15 @@ struct BuildParams {
   int32_t* count;
 };
 
-// Exclusive prefix count of a per-thread flag over the work-group, and the total. wsum holds
-// one slot per wave; two barriers.
-__device__ inline int block_prefix(bool flag, int* wsum, int& total) {
-  const int lane = tid_x() & 63, w = tid_x() >> 6;
-  const uint64_t m = __ballot(flag);
-  const int pre = __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0));
-  if (lane == 0) wsum[w] = __popcll(m);
-  __syncthreads();
-  int before = 0, all = 0;
-  for (int i = 0; i < kBuildThreads / 64; ++i) {
-    const int v = wsum[i];
-    before += i < w ? v : 0;
-    all += v;
-  }
-  __syncthreads();
-  total = all;
-  return before + pre;
-}
-
 // grid (n_heads), kBuildThreads threads
 __global__ __launch_bounds__(kBuildThreads) void keyset_build_kernel(BuildParams p) {
+  constexpr int kWaves = kBuildThreads / 64;
+  constexpr int kSegChunks = 4096;  // chunks of 64 tokens whose member masks a segment holds
+  constexpr int kInFlight = 16;  // score reads per thread in flight in the radix passes
   __shared__ int hist[256];
-  __shared__ int wsum[kBuildThreads / 64];
+  __shared__ int wscan[4];
+  __shared__ uint64_t fmask[kSegChunks];
+  __shared__ int wcnt[kWaves], weq[kWaves];
   __shared__ uint32_t sh_prefix;
   __shared__ int sh_remaining;
   const int hh = bid_x(), tid = tid_x();
@@ -171,19 +157,43 @@ __global__ __launch_bounds__(kBuildThreads) void keyset_build_kernel(BuildParams
     for (int shift = 24; shift >= 0; shift -= 8) {
       if (tid < 256) hist[tid] = 0;
       __syncthreads();
-      for (int t = tid; t < p.n; t += kBuildThreads) {
-        const uint32_t key = fkey(sc[t]);
-        if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255], 1);
+      // kInFlight scores per thread read at once, then their counts
+      for (int t0 = tid; t0 < p.n; t0 += kInFlight * kBuildThreads) {
+        float v[kInFlight];
+#pragma unroll
+        for (int u = 0; u < kInFlight; ++u) {
+          const int t = t0 + u * kBuildThreads;
+          v[u] = t < p.n ? sc[t] : 0.f;
+        }
+#pragma unroll
+        for (int u = 0; u < kInFlight; ++u) {
+          const uint32_t key = fkey(v[u]);
+          if (t0 + u * kBuildThreads < p.n && (key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255], 1);
+        }
       }
       __syncthreads();
-      if (tid == 0) {
-        int above = 0, b = 255;
-        for (; b > 0; --b) {
-          if (above + hist[b] >= remaining) break;
-          above += hist[b];
+      // the bin of the remaining-th largest key: thread i < 256 holds bin 255 - i; inclusive sums
+      // from the top over the four waves of those threads, and the one thread whose bin reaches
+      // `remaining` first records it
+      int cnt = 0, inc = 0;
+      if (tid < 256) {
+        cnt = hist[255 - tid];
+        inc = cnt;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+          const int y = __shfl_up(inc, o);
+          if ((tid & 63) >= o) inc += y;
         }
-        sh_prefix = prefix | ((uint32_t)b << shift);
-        sh_remaining = remaining - above;
+        if ((tid & 63) == 63) wscan[tid >> 6] = inc;
+      }
+      __syncthreads();
+      if (tid < 256) {
+        for (int i = 0; i < (tid >> 6); ++i) inc += wscan[i];
+        const int excl = inc - cnt;
+        if (excl < remaining && inc >= remaining) {
+          sh_prefix = prefix | ((uint32_t)(255 - tid) << shift);
+          sh_remaining = remaining - excl;
+        }
       }
       __syncthreads();
       prefix = sh_prefix;
@@ -196,27 +206,104 @@ __global__ __launch_bounds__(kBuildThreads) void keyset_build_kernel(BuildParams
   }
 
   // ---- members in token order: select, union, compact ----
+  // Segments of up to kSegChunks chunks of 64 tokens; wave w takes a contiguous run of a segment's
+  // chunks. Top-k heads first count their keys equal to the threshold per wave (their ranks among
+  // those keys decide which are taken); then every wave computes its chunks' member masks into
+  // LDS and counts them, one prefix over the waves places each wave's members, and the wave writes
+  // them from its masks: three barriers per segment instead of two prefix steps per 1024 tokens.
   int32_t* out = p.idx + (int64_t)hh * p.idx_stride;
-  int run_eq = 0, run_out = 0;
-  for (int base = 0; base < p.n; base += kBuildThreads) {
-    const int t = base + tid;
-    const bool valid = t < p.n;
-    bool sel;
+  const int lane = tid & 63, w = tid >> 6;
+  int run_eq = 0, run_out = 0;  // equal keys and members before the segment
+  for (int seg0 = 0; seg0 < p.n; seg0 += kSegChunks * 64) {
+    const int nch = (min(p.n - seg0, kSegChunks * 64) + 63) / 64;
+    const int per = (nch + kWaves - 1) / kWaves;
+    const int c0 = min(nch, w * per), c1 = min(nch, c0 + per);
+    // the score of chunk c's token for this lane (0 outside the head's tokens)
+    auto key_at = [&](int c) {
+      const int t = seg0 + 64 * c + lane;
+      return t < p.n ? fkey(sc[t]) : 0u;
+    };
+    int eq_before = run_eq, seg_eq = 0;
     if (mode == 1) {
-      const uint32_t key = valid ? fkey(sc[t]) : 0u;
-      const bool eq = valid && key == thr;
-      int tot_eq;
-      const int rank = run_eq + block_prefix(eq, wsum, tot_eq);
-      run_eq += tot_eq;
-      sel = valid && param > 0 && (key > thr || (eq && rank < need_eq));
-    } else {
-      sel = valid && param > 0 && t >= start && (t - start) % param == 0;
+      int e = 0;
+      for (int c = c0; c < c1; c += 8) {  // eight chunks' scores in flight at once
+        uint32_t kk[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) kk[u] = c + u < c1 ? key_at(c + u) : 0u;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int t = seg0 + 64 * (c + u) + lane;
+          e += __popcll(__ballot(c + u < c1 && t < p.n && kk[u] == thr));
+        }
+      }
+      if (lane == 0) weq[w] = e;
+      __syncthreads();
+      for (int i = 0; i < kWaves; ++i) {
+        const int v = weq[i];
+        eq_before += i < w ? v : 0;
+        seg_eq += v;
+      }
     }
-    const bool flag = sel || (include && valid && (t < p.T || t % p.T < p.ns));
-    int tot;
-    const int pos = run_out + block_prefix(flag, wsum, tot);
-    if (flag) out[pos] = t;
-    run_out += tot;
+    int cnt = 0, eqr = eq_before;  // rank of the wave's next key equal to the threshold
+    // t mod T and (t - start) mod stride of the lane's token, stepped by 64 tokens per chunk (no
+    // division in the loop)
+    const int t_first = seg0 + 64 * c0 + lane;
+    int rT = t_first % p.T;
+    const int stepT = 64 % p.T;
+    const int stride = (mode == 0 && param > 0) ? param : 1;
+    int rS = t_first >= start ? (t_first - start) % stride : 0;
+    const int stepS = 64 % stride;
+    for (int c = c0; c < c1; c += 8) {
+      uint32_t kk[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) kk[u] = (mode == 1 && c + u < c1) ? key_at(c + u) : 0u;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        if (c + u >= c1) break;  // uniform
+        const int t = seg0 + 64 * (c + u) + lane;
+        const bool valid = t < p.n;
+        bool sel;
+        if (mode == 1) {
+          const bool eq = valid && kk[u] == thr;
+          const uint64_t meq = __ballot(eq);
+          const int rank = eqr + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(meq >> 32),
+                                                                __builtin_amdgcn_mbcnt_lo((uint32_t)meq, 0));
+          eqr += __popcll(meq);
+          sel = valid && param > 0 && (kk[u] > thr || (eq && rank < need_eq));
+        } else {
+          sel = valid && param > 0 && t >= start && rS == 0;
+        }
+        const bool flag = sel || (include && valid && (t < p.T || rT < p.ns));
+        const uint64_t m = __ballot(flag);
+        if (lane == 0) fmask[c + u] = m;
+        cnt += __popcll(m);
+        // the next chunk's token, t + 64 (below start the residue is not used)
+        rT += stepT;
+        if (rT >= p.T) rT -= p.T;
+        if (t + 64 >= start) {
+          rS = t >= start ? rS + stepS : (t + 64 - start) % stride;
+          if (rS >= stride) rS -= stride;
+        }
+      }
+    }
+    if (lane == 0) wcnt[w] = cnt;
+    __syncthreads();
+    int pos = run_out, seg_out = 0;
+    for (int i = 0; i < kWaves; ++i) {
+      const int v = wcnt[i];
+      pos += i < w ? v : 0;
+      seg_out += v;
+    }
+    for (int c = c0; c < c1; ++c) {
+      const uint64_t m = fmask[c];
+      if ((m >> lane) & 1)
+        out[pos + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0))] =
+            seg0 + 64 * c + lane;
+      pos += __popcll(m);
+    }
+    run_out += seg_out;
+    run_eq += seg_eq;
+    __syncthreads();  // the next segment rewrites the masks and the wave counts
   }
   if (tid == 0) p.count[hh] = run_out;
 }

@@ -100,8 +100,11 @@ def test_pack_writes_fp32_rows_of_flagged_heads(ops, pkg):
         assert torch.allclose(qk32[s, 0].cpu(), ref_q, rtol=1e-5, atol=1e-5)
 
 
-@pytest.mark.parametrize("F,T,ns", [(3, 155, 5), (4, 1374, 5), (2, 64, 0)])
+@pytest.mark.parametrize("F,T,ns", [(3, 155, 5), (4, 1374, 5), (2, 64, 0), (5, 37, 5), (200, 1374, 5)])
 def test_keyset_build_bit_exact(ops, pkg, F, T, ns):
+    """Key sets bit-exact against the oracle: stride sets (several starts and strides), top-k sets on
+    normal and heavily tied scores, k above the token count; frames shorter than 64 tokens, and
+    274,800 tokens (more than one 262,144-token segment of the build kernel)."""
     geom = pkg.Geometry(F, T, ns)
     n = geom.tokens
     rng = np.random.default_rng(n)
