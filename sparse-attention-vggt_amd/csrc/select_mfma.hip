@@ -108,9 +108,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KL <= 9 ? 4
   __shared__ __align__(16) uint8_t outb[128 * OPB];
   __shared__ __align__(16) float ksc[FPW][32];  // 2^-sk of the frame's key blocks (0 past NBf)
   __shared__ float nkm[FPW];                    // the frame's largest key norm bound
-  __shared__ u32x2 queue[kSelQueue];            // (query in the group, frame in the group), candidate mask
-  __shared__ uint32_t qcount, wsum[4];
-  static_assert(128 * FPW <= kSelQueue, "the queue holds every pair of the workgroup");
+  // listed pairs: (query in the group << 24 | frame in the group << 16 | first candidate), candidate mask
+  __shared__ u32x2 queue[kSelQueue];
+  // pairs << 16 | candidates: one atomic gives a listed pair its queue slot and its candidates' offset
+  __shared__ uint32_t qctr;
+  static_assert(128 * FPW <= kSelQueue && FPW <= 256 && kSelQueue * 32 <= 65536,
+                "the queue holds every pair of the workgroup; fields fit their bits");
   constexpr uint8_t kQueued = 0xFE;
   const int tid = tid_x(), lane = tid & 63, w = tid >> 6, col = lane & 31, half = lane >> 5;
   const int hs = bid_z();
@@ -126,6 +129,27 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KL <= 9 ? 4
   const int64_t qrec = (int64_t)hs * 2 * NB + (qvalid ? qi : NB - 1);  // tensor 0 = q
   const int64_t krec0 = ((int64_t)hs * 2 + 1) * NB;                   // tensor 1 = k
 
+  // ring fill: every thread issues two 16-byte copies per frame (the same count in every wave, which
+  // the waits below rely on): thread t copies LDS chunks (256 u + t) mod 128 NG of the stage (row =
+  // chunk / 16, the global chunk through the swizzle; rows past NBf repeat the frame's last row;
+  // with fewer than 512 chunks some copies repeat others, same data to the same place). 128 NG is a
+  // multiple of 64, so a wave's chunks stay contiguous from its base.
+  const uint32_t ring_base = lds_addr(ring);
+  auto fill = [&](int f) {
+    const uint32_t st = ring_base + ((uint32_t)(f - f0) % kSelRing) * kStage;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int base = (256 * u + 64 * w) % (NG * 128), pos = base + lane;
+      const int r = pos >> 4, c = (pos & 15) ^ (r & 15);
+      const int rr = r < p.NBf ? r : p.NBf - 1;
+      const uint16_t* src = p.split + (krec0 + (int64_t)f * p.NBf + rr) * 128 + 8 * c;
+      dma16(src, st + (uint32_t)(16 * base));
+    }
+  };
+  // the first frames' copies go out first, so that their latency overlaps that of the loads below
+  for (int j = 0; j < kSelRing - 1; ++j)
+    if (j < nf) fill(f0 + j);
+
   // Q fragments: lane (col, half) holds features 32 half + 8 st .. + 7 of its query, both fp16 parts
   f16x8 qf[2][4];
   {
@@ -139,7 +163,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KL <= 9 ? 4
 
   // key meta of the workgroup's frames: the scale of every key block in LDS, and the frame's largest
   // norm bound (the 32 threads of a frame's entries, a half wave, reduce it by shuffles)
-  if (tid == 0) qcount = 0;
+  if (tid == 0) qctr = 0;
   for (int e0 = 0; e0 < FPW * 32; e0 += 256) {
     const int e = e0 + tid, fl = e >> 5, j = e & 31;
     float2 m = {0.f, 0.f};  // rows past the frame: no norm, no scale
@@ -151,26 +175,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KL <= 9 ? 4
     if (j == 0 && fl < FPW) nkm[fl] = mx;
   }
   __syncthreads();
-
-  // ring fill: every thread issues two 16-byte copies per frame (the same count in every wave, which
-  // the waits below rely on): thread t copies LDS chunks (256 u + t) mod 128 NG of the stage (row =
-  // chunk / 16, the global chunk through the swizzle; rows past NBf repeat the frame's last row;
-  // with fewer than 512 chunks some copies repeat others, same data to the same place). 128 NG is a
-  // multiple of 64, so a wave's chunks stay contiguous from its base.
-  const uint32_t ring_base = lds_addr(ring);
-  auto fill = [&](int f) {
-    const uint32_t st = ring_base + (uint32_t)(((f - f0) % kSelRing) * kStage);
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int base = (256 * u + 64 * w) % (NG * 128), pos = base + lane;
-      const int r = pos >> 4, c = (pos & 15) ^ (r & 15);
-      const int rr = r < p.NBf ? r : p.NBf - 1;
-      const uint16_t* src = p.split + (krec0 + (int64_t)f * p.NBf + rr) * 128 + 8 * c;
-      dma16(src, st + (uint32_t)(16 * base));
-    }
-  };
-  for (int j = 0; j < kSelRing - 1; ++j)
-    if (j < nf) fill(f0 + j);
 
   // threshold factor in units of A 2^-sk: 2 E + the tag truncation (2^-17 |q| |k|), times 2^sq
   const float cq = (0x1p-14f + 0x1p-17f) * qm.x / qm.y;
@@ -266,16 +270,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KL <= 9 ? 4
     // exact ties: such pairs are listed with every key)
     const bool finite = (__builtin_bit_cast(uint32_t, thr) & 0x7F800000u) != 0x7F800000u;  // on the bits
     const bool usable = finite && thr > 0.f;
+    // (every term evaluated: no branches)
     bool ok = usable;
 #pragma unroll
-    for (int t = 0; t < KL - 1; ++t)
-      if (t < p.ke) ok = ok && (t + 1 == p.NBf || lst[t] - lst[t + 1] > thr);
+    for (int t = 0; t < KL - 1; ++t) ok = ok & ((t >= p.ke) | (t + 1 == p.NBf) | (lst[t] - lst[t + 1] > thr));
     if (half == 0) {
       uint8_t* o = outb + qloc * OPB + fl * p.ke;
       if (ok) {
+        if (p.ke == 4) {  // one aligned word (OPB and 4 fl are multiples of 4)
+          *reinterpret_cast<uint32_t*>(o) = (uint32_t)tag_key(lst[0]) | ((uint32_t)tag_key(lst[1]) << 8) |
+                                            ((uint32_t)tag_key(lst[2]) << 16) | ((uint32_t)tag_key(lst[3]) << 24);
+        } else {
 #pragma unroll
-        for (int t = 0; t < KL - 1; ++t)
-          if (t < p.ke) o[t] = (uint8_t)tag_key(lst[t]);
+          for (int t = 0; t < KL - 1; ++t)
+            if (t < p.ke) o[t] = (uint8_t)tag_key(lst[t]);
+        }
       } else if (qvalid) {
         // candidates: each half's entries at least lo; every key of a half whose last entry is at
         // least lo too (keys past its list may qualify), of the frame when the threshold is not
@@ -295,80 +304,78 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KL <= 9 ? 4
         if (other[KL - 1] >= lo) mask |= half1_keys;
         if (!usable || p.ke >= p.NBf) mask = all_keys;
         mask &= all_keys;
-        const uint32_t at = atomicAdd(&qcount, 1u);
-        queue[at] = u32x2{((uint32_t)qloc << 16) | (uint32_t)fl, mask};
+        uint32_t nc = (uint32_t)__builtin_popcount(mask);
+        if (nc < (uint32_t)p.ke) {  // cannot happen (the list's best k qualify); every key, to be safe
+          mask = all_keys;
+          nc = (uint32_t)__builtin_popcount(mask);
+        }
+        const uint32_t at = atomicAdd(&qctr, (1u << 16) | nc);  // slot at >> 16, candidates from at & 0xFFFF
+        queue[at >> 16] = u32x2{((uint32_t)qloc << 24) | ((uint32_t)fl << 16) | (at & 0xFFFFu), mask};
         o[0] = kQueued;
       }
     }
     acc = acc_next;
   }
   __syncthreads();
-  // the certified lists, one (query, frame) pair per thread at a time (the listed pairs are written
-  // by the exact pass below)
+  // the certified lists: two threads per query, frames of one parity each (the listed pairs are
+  // written by the exact pass below); k = 4 lists as one 16-byte store when the output is aligned
   const int64_t row = (int64_t)p.F * p.ke;
-  for (int e = tid; e < 128 * nf; e += 256) {
-    const int q = e / nf, fl = e - q * nf;
-    const int64_t i = (int64_t)qt * 128 + q;
-    if (i >= NB) continue;
-    const uint8_t* o = outb + q * OPB + fl * p.ke;
-    if (o[0] == kQueued) continue;
-    int32_t* dst = p.idx + ((int64_t)hs * NB + i) * row + (int64_t)(f0 + fl) * p.ke;
-    const int fb = (f0 + fl) * p.NBf;
-    for (int t = 0; t < p.ke; ++t) dst[t] = fb + o[t];
-  }
-  // The listed pairs of this workgroup, exactly, one candidate key per thread: the candidates are
-  // numbered pair by pair (an exclusive prefix of the masks' popcounts), every thread computes the
-  // sequential fmaf score of one candidate from the fp32 means (one round of row loads for up to 256
-  // candidates), and a candidate's rank among its pair's candidates by the composite key (higher
-  // score, then lower block) places it among the k best. Pairs whose candidates exceed the LDS space
-  // run in batches. The ring is free: every copy has landed and every wave has passed the barrier
-  // above.
-  constexpr int kOffBytes = ((kSelQueue + 1) * 2 + 15) / 16 * 16;
-  constexpr int kCandMax = (kSelRing * kStage - kOffBytes) / 6 / 4 * 4;
-  static_assert(kCandMax >= 32, "the candidates of one pair fit");
-  uint16_t* coff = reinterpret_cast<uint16_t*>(ring);                                // [nq + 1]
-  float* csc = reinterpret_cast<float*>(ring + kOffBytes);                          // [kCandMax] scores
-  uint16_t* cid = reinterpret_cast<uint16_t*>(ring + kOffBytes + 4 * kCandMax);     // [kCandMax] pair << 5 | key
-  const uint32_t nq = qcount;
   {
-    uint32_t cnt[4], tsum = 0;  // thread t counts the candidates of pairs 4t .. 4t + 3
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const uint32_t e = 4 * tid + u;
-      cnt[u] = e < nq ? (uint32_t)__builtin_popcount(queue[e][1]) : 0u;
-      tsum += cnt[u];
+    const int q = tid >> 1;
+    const int64_t i = (int64_t)qt * 128 + q;
+    const bool a16 = ((uintptr_t)p.idx & 15) == 0;
+    if (i < NB) {
+      int32_t* drow = p.idx + ((int64_t)hs * NB + i) * row;
+      for (int fl = tid & 1; fl < nf; fl += 2) {
+        const uint8_t* o = outb + q * OPB + fl * p.ke;
+        const int fb = (f0 + fl) * p.NBf;
+        int32_t* dst = drow + (int64_t)(f0 + fl) * p.ke;
+        if (p.ke == 4) {
+          const uint32_t wv = *reinterpret_cast<const uint32_t*>(o);
+          if ((wv & 0xFFu) == kQueued) continue;
+          const int v0 = fb + (int)(wv & 0xFFu), v1 = fb + (int)((wv >> 8) & 0xFFu);
+          const int v2 = fb + (int)((wv >> 16) & 0xFFu), v3 = fb + (int)(wv >> 24);
+          if (a16) {
+            *reinterpret_cast<u32x4*>(dst) = u32x4{(uint32_t)v0, (uint32_t)v1, (uint32_t)v2, (uint32_t)v3};
+          } else {
+            dst[0] = v0;
+            dst[1] = v1;
+            dst[2] = v2;
+            dst[3] = v3;
+          }
+        } else {
+          if (o[0] == kQueued) continue;
+          for (int t = 0; t < p.ke; ++t) dst[t] = fb + o[t];
+        }
+      }
     }
-    uint32_t inc = tsum;  // inclusive prefix within the wave
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const uint32_t y = __shfl_up(inc, o);
-      if (lane >= o) inc += y;
-    }
-    if (lane == 63) wsum[w] = inc;
-    __syncthreads();
-    uint32_t pre = inc - tsum;
-    for (int v = 0; v < w; ++v) pre += wsum[v];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const uint32_t e = 4 * tid + u;
-      if (e < nq) coff[e] = (uint16_t)pre;
-      pre += cnt[u];
-    }
-    if (tid == 0) coff[nq] = (uint16_t)(wsum[0] + wsum[1] + wsum[2] + wsum[3]);
-    __syncthreads();
   }
+  // The listed pairs of this workgroup, exactly, one candidate key per thread: each pair's candidates
+  // were numbered when it was listed (its first candidate's offset in its queue entry, its count the
+  // popcount of its mask), every thread computes the sequential fmaf score of one candidate from the
+  // fp32 means (one round of row loads for up to 256 candidates), and a candidate's rank among its
+  // pair's candidates by the composite key (higher score, then lower block) places it among the k
+  // best. Pairs whose candidates exceed the LDS space run in batches. The ring is free: every copy
+  // has landed and every wave has passed the barrier above.
+  constexpr int kCandMax = kSelRing * kStage / 6 / 4 * 4;
+  static_assert(kCandMax >= 32, "the candidates of one pair fit");
+  float* csc = reinterpret_cast<float*>(ring);                          // [kCandMax] scores
+  uint16_t* cid = reinterpret_cast<uint16_t*>(ring + 4 * kCandMax);     // [kCandMax] pair << 5 | key
+  const uint32_t ctr = qctr, nq = ctr >> 16, ntot = ctr & 0xFFFFu;
+  auto first = [&](uint32_t e) { return e < nq ? (queue[e][0] & 0xFFFFu) : ntot; };  // pair e's first candidate
   for (uint32_t p0 = 0; p0 < nq;) {  // the same trips for every thread
     // pairs p0 .. p1 - 1: the longest run from p0 whose candidates fit (one pair always does)
-    const uint32_t base = coff[p0];
+    const uint32_t base = first(p0);
     uint32_t lo = p0 + 1, hi = nq;
     while (lo < hi) {
       const uint32_t mid = (lo + hi + 1) >> 1;
-      if (coff[mid] - base <= (uint32_t)kCandMax) lo = mid;
+      if (first(mid) - base <= (uint32_t)kCandMax) lo = mid;
       else hi = mid - 1;
     }
-    const uint32_t p1 = lo, nc = coff[p1] - base;
+    const uint32_t p1 = lo, nc = first(p1) - base;
     for (uint32_t e = p0 + tid; e < p1; e += 256) {
-      uint32_t m = queue[e][1], o = coff[e] - base;
+      const u32x2 ent = queue[e];
+      uint32_t m = ent[1], o = (ent[0] & 0xFFFFu) - base;
       while (m) {
         cid[o++] = (uint16_t)((e << 5) | (uint32_t)__builtin_ctz(m));
         m &= m - 1;
@@ -378,8 +385,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KL <= 9 ? 4
     for (uint32_t c = tid; c < nc; c += 256) {
       const uint32_t v = cid[c], j = v & 31;
       const u32x2 ent = queue[v >> 5];
-      const int64_t i = (int64_t)qt * 128 + (ent[0] >> 16);
-      const int f = f0 + (int)(ent[0] & 0xFFFF);
+      const int64_t i = (int64_t)qt * 128 + (ent[0] >> 24);
+      const int f = f0 + (int)((ent[0] >> 16) & 0xFFu);
       const f32x4* qr = reinterpret_cast<const f32x4*>(p.mean + ((int64_t)hs * 2 * NB + i) * 64);
       const f32x4* kv = reinterpret_cast<const f32x4*>(p.mean + (krec0 + (int64_t)f * p.NBf + j) * 64);
       f32x4 qa[16], kb[16];  // both rows in flight at once, then the chain
@@ -402,13 +409,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KL <= 9 ? 4
     for (uint32_t c = tid; c < nc; c += 256) {
       const uint32_t v = cid[c], e = v >> 5, j = v & 31;
       const uint64_t key = ckey(csc[c], j);
-      const uint32_t b0 = coff[e] - base, b1 = coff[e + 1] - base;
+      const u32x2 ent = queue[e];
+      const uint32_t b0 = (ent[0] & 0xFFFFu) - base, b1 = b0 + (uint32_t)__builtin_popcount(ent[1]);
       int rank = 0;
       for (uint32_t c2 = b0; c2 < b1; ++c2) rank += ckey(csc[c2], cid[c2] & 31u) > key ? 1 : 0;
       if (rank < p.ke) {
-        const u32x2 ent = queue[e];
-        const int64_t i = (int64_t)qt * 128 + (ent[0] >> 16);
-        const int f = f0 + (int)(ent[0] & 0xFFFF);
+        const int64_t i = (int64_t)qt * 128 + (ent[0] >> 24);
+        const int f = f0 + (int)((ent[0] >> 16) & 0xFFu);
         p.idx[((int64_t)hs * NB + i) * row + (int64_t)f * p.ke + rank] = f * p.NBf + (int)j;
       }
     }

@@ -262,6 +262,28 @@ def test_block_select_pooled_128_frames(ops):
         assert np.array_equal(got[h], ref), f"head {h}"
 
 
+def test_block_select_pooled_unaligned_output(ops, pkg):
+    """The C entry takes any 4-byte aligned int32 output: lists written at an address 4 bytes past a
+    16-byte boundary (per-element stores in place of 16-byte ones) equal those of an aligned buffer,
+    and the words on either side stay untouched."""
+    from importlib import import_module
+    lib = import_module(pkg.__name__ + "._lib")
+    rng = np.random.default_rng(5)
+    frames, nbf, n, k = 12, 22, 2, 4
+    mean = rng.standard_normal((n, 2, frames * nbf, 64)).astype(np.float32) * np.float32(0.125)
+    pooled = ops.pooled_prepare(torch.from_numpy(mean).to(DEV))
+    want = ops.block_select_pooled(pooled, frames, nbf, k)
+    buf = torch.full((want.numel() + 8,), -7, dtype=torch.int32, device=DEV)
+    assert buf.data_ptr() % 16 == 0
+    L = lib.load()
+    rc = L.saf3r_block_select_pooled(pooled.mean.data_ptr(), pooled.split.data_ptr(), pooled.meta.data_ptr(), n,
+                                     frames, nbf, k, buf.data_ptr() + 4, None, 0, lib.stream_ptr())
+    assert rc == 0, lib.load().saf3r_last_error()
+    got = buf.cpu()
+    assert torch.equal(got[1:1 + want.numel()], want.flatten().cpu())
+    assert int(got[0]) == -7 and bool((got[1 + want.numel():] == -7).all())
+
+
 def test_pooled_prepare_split_is_exact(ops):
     """The split record: x * 2^s == h1 + h2 + r with |r| <= 2^-22 |x 2^s| (fp16 normal range), the row's
     largest magnitude times 2^s in [2^14, 2^15), meta = (a norm bound >= the norm, 2^-s); rows outside
