@@ -46,6 +46,9 @@
 // its frames (one candidate key per thread), so the selection is one kernel and needs no workspace.
 // The file is compiled without NaN semantics (no canonicalisation before max / med3): every value
 // in a certified pair is finite, and finiteness itself is tested on the bits.
+#include <algorithm>
+#include <atomic>
+
 #include "common.h"
 
 namespace saf3r {
@@ -64,6 +67,11 @@ struct SelMfmaParams {
   const float* meta;      // [n][2][NB][2]
   int32_t* idx;           // [n][NB][F * ke]
   int F, NBf, NB, ke;
+  int n;                  // heads
+  int fpg;                // frames per frame group (at most FPW; fewer for short clips, so that
+                          // all 8 XCDs get groups)
+  int slots;              // work-groups per XCD in one resident round
+  int pieces;             // 1: units cut into pieces (fewer units than slots)
 };
 
 // insert x into the descending list a: a[0] = max, a[t] = med3(old a[t-1], old a[t], x), every slot
@@ -89,10 +97,14 @@ __device__ inline int sel_chunk(int r, int c) { return (r * 16 + (c ^ (r & 15)))
 // entry); at most 38 KB of LDS (four workgroups per CU). For lists of up to 9 the compiler is held
 // to four waves per SIMD (at most 128 VGPRs; the exact pass's row loads would take more).
 //
-// Workgroup order (blockIdx.x = r + 8 (j + cm qt), cm = ceil(G / 8) for G frame groups): the
-// hardware hands workgroups to the 8 XCDs in turn, so r is the XCD, and XCD r takes the frame
-// groups g = r + 8 j only. Each XCD's L2 then holds the key records of 1/8 of the frames (about
-// 0.6 MB for 7 heads at 128 frames) for every query tile, instead of all of them.
+// Workgroup order (blockIdx.x = r + 8 i): the hardware hands workgroups to the 8 XCDs in turn, so r
+// is the XCD, and XCD r takes the frame groups g = r + 8 j only. Each XCD's L2 then holds the key
+// records of 1/8 of the frames (about 0.6 MB for 7 heads at 128 frames) for every query tile,
+// instead of all of them. A group holds fpg = min(FPW, ceil(F / 8)) frames, so that short clips
+// still give every XCD groups. Each (head, query tile, group) unit runs in one workgroup; when XCD 0
+// has fewer units than the S workgroups an XCD holds at once, each unit is cut into pieces of a few
+// frames so that all S slots work (a workgroup's fixed part, about 8 us of loads, list writes and
+// the exact pass, makes pieces lose once the units fill a round).
 template <int KL, int NG>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KL <= 9 ? 4 : 1))) void block_select_mfma_kernel(
     SelMfmaParams p) {
@@ -116,13 +128,45 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KL <= 9 ? 4
                 "the queue holds every pair of the workgroup; fields fit their bits");
   constexpr uint8_t kQueued = 0xFE;
   const int tid = tid_x(), lane = tid & 63, w = tid >> 6, col = lane & 31, half = lane >> 5;
-  const int hs = bid_z();
-  const int G = (p.F + FPW - 1) / FPW, cm = (G + 7) / 8;
-  const int xr = bid_x() & 7, xj = (bid_x() >> 3) % cm, qt = (bid_x() >> 3) / cm;
-  const int f0 = (xr + 8 * xj) * FPW, f1 = min(p.F, f0 + FPW);
-  if (f0 >= p.F) return;  // an empty slot of the XCD order: the whole workgroup leaves
-  const int nf = f1 - f0;
   const int64_t NB = p.NB;
+  const int G = (p.F + p.fpg - 1) / p.fpg;
+  const int xr = bid_x() & 7;
+  int hs, qt, g;
+  uint32_t piece = 0, m = 1;  // piece of m of the unit's frames
+  if (!p.pieces) {  // blockIdx = (xr + 8 (j + cm qt), 1, head), cm = ceil(G / 8): one unit each
+    const int cm = (G + 7) / 8, xq = bid_x() >> 3;
+    qt = xq / cm;
+    g = xr + 8 * (xq - qt * cm);
+    hs = bid_z();
+    if (g >= G) return;  // an empty slot of the XCD order: the whole workgroup leaves
+  } else {  // fewer units than slots: blockIdx.x = xr + 8 wi, XCD xr's units cut into S pieces
+    // (32-bit arithmetic: the entry keeps the units of an XCD at most 2^27)
+    const uint32_t nqt = (uint32_t)((NB + 127) / 128);
+    const uint32_t wi = bid_x() >> 3;
+    const uint32_t cnt = G > xr ? (uint32_t)(G - xr + 7) / 8u : 0u;  // frame groups of this XCD
+    const uint32_t Q = (uint32_t)p.n * nqt * cnt, S = (uint32_t)p.slots;
+    if (Q == 0 || wi >= S) return;
+    const uint32_t base = S / Q, extra = S - base * Q;  // m = base + 1 for the first extra units
+    uint32_t unit;
+    if (wi < extra * (base + 1)) {
+      m = base + 1;
+      unit = wi / m;
+      piece = wi - unit * m;
+    } else {
+      m = base;
+      const uint32_t t2 = wi - extra * (base + 1);
+      unit = extra + t2 / m;
+      piece = t2 - (unit - extra) * m;
+    }
+    const uint32_t pr = unit / cnt;
+    hs = (int)(pr / nqt);
+    qt = (int)(pr - (uint32_t)hs * nqt);
+    g = xr + 8 * (int)(unit - pr * cnt);
+  }
+  const int gnf = min(p.F - g * p.fpg, p.fpg);  // frames of group g
+  const int f0 = g * p.fpg + (int)(piece * (uint32_t)gnf / m), f1 = g * p.fpg + (int)((piece + 1) * (uint32_t)gnf / m);
+  if (f0 >= f1) return;  // an empty piece (more pieces than frames)
+  const int nf = f1 - f0;
   const int qloc = 32 * w + col;  // query block within the workgroup
   const int64_t qi = (int64_t)qt * 128 + qloc;
   const bool qvalid = qi < NB;
@@ -434,13 +478,44 @@ __global__ __launch_bounds__(256) void pooled_prepare_kernel(const float* __rest
   pooled_split_row(mean[r * 64 + lane], lane, split + r * 128, meta + r * 2);
 }
 
+// work-groups of the selection kernel the current device holds at once (1024 if unknown)
+template <int KL, int NG>
+static int64_t select_slots() {
+  static std::atomic<int64_t> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) dev = 0;
+  if (dev < 64) {
+    const int64_t v = cache[dev].load(std::memory_order_relaxed);
+    if (v > 0) return v;
+  }
+  int cus = 0, blocks = 0;
+  int64_t v = 1024;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, block_select_mfma_kernel<KL, NG>, 256, 0) == hipSuccess &&
+      cus > 0 && blocks > 0)
+    v = (int64_t)cus * blocks;
+  if (dev < 64) cache[dev].store(v, std::memory_order_relaxed);
+  return v;
+}
+
+// a workgroup per (head, query tile, frame group), or, when XCD 0 (the one with the most frame
+// groups) has fewer of them than it holds workgroups at once, a workgroup per slot and piece
+template <int KL, int NG>
+static void launch_select_one(hipStream_t st, SelMfmaParams p, int64_t units_xcd0) {
+  p.slots = (int)std::max<int64_t>(1, select_slots<KL, NG>() / 8);
+  p.pieces = units_xcd0 < p.slots ? 1 : 0;
+  const int64_t nqt = ((int64_t)p.NB + 127) / 128, cm = ((p.F + p.fpg - 1) / p.fpg + 7) / 8;
+  const dim3 grid = p.pieces ? dim3(8u * (unsigned)p.slots) : dim3((unsigned)(8 * cm * nqt), 1u, (unsigned)p.n);
+  hipLaunchKernelGGL((block_select_mfma_kernel<KL, NG>), grid, dim3(256), 0, st, p);
+}
+
 template <int KL>
-static void launch_select_mfma(int ng, dim3 grid, hipStream_t st, const SelMfmaParams& p) {
+static void launch_select_mfma(int ng, hipStream_t st, const SelMfmaParams& p, int64_t units_xcd0) {
   switch (ng) {
-    case 1: hipLaunchKernelGGL((block_select_mfma_kernel<KL, 1>), grid, dim3(256), 0, st, p); break;
-    case 2: hipLaunchKernelGGL((block_select_mfma_kernel<KL, 2>), grid, dim3(256), 0, st, p); break;
-    case 3: hipLaunchKernelGGL((block_select_mfma_kernel<KL, 3>), grid, dim3(256), 0, st, p); break;
-    default: hipLaunchKernelGGL((block_select_mfma_kernel<KL, 4>), grid, dim3(256), 0, st, p); break;
+    case 1: launch_select_one<KL, 1>(st, p, units_xcd0); break;
+    case 2: launch_select_one<KL, 2>(st, p, units_xcd0); break;
+    case 3: launch_select_one<KL, 3>(st, p, units_xcd0); break;
+    default: launch_select_one<KL, 4>(st, p, units_xcd0); break;
   }
 }
 
@@ -497,8 +572,7 @@ extern "C" int saf3r_block_select_pooled(const float* mean, const uint16_t* spli
   }
   (void)workspace;  // none is needed (the size query returns 0); kept for the entry's signature
   (void)workspace_bytes;
-  const int fpw = select_fpw(ke), groups = (frames + fpw - 1) / fpw;
-  const dim3 grid((unsigned)(8 * ((groups + 7) / 8) * ((NB + 127) / 128)), 1u, (unsigned)n);
+  const int fpg = std::max(1, std::min(select_fpw(ke), (frames + 7) / 8)), groups = (frames + fpg - 1) / fpg;
   SelMfmaParams p;
   p.mean = mean;
   p.split = split;
@@ -508,9 +582,16 @@ extern "C" int saf3r_block_select_pooled(const float* mean, const uint16_t* spli
   p.NBf = NBf;
   p.NB = NB;
   p.ke = ke;
+  p.n = n;
+  p.fpg = fpg;
+  p.slots = 1;
+  p.pieces = 0;
+  const int64_t units_xcd0 = (int64_t)n * ((NB + 127) / 128) * ((groups + 7) / 8);
+  if (units_xcd0 > ((int64_t)1 << 27))  // keeps the grids and the kernel's unit arithmetic in 32 bits
+    return fail(SAF3R_ERR_UNSUPPORTED, "saf3r_block_select_pooled: too many (head, query tile, frame group) units");
   const int ng = (NBf + 7) / 8;
-  if (ke <= 4) launch_select_mfma<5>(ng, grid, st, p);
-  else if (ke <= 8) launch_select_mfma<9>(ng, grid, st, p);
-  else launch_select_mfma<17>(ng, grid, st, p);
+  if (ke <= 4) launch_select_mfma<5>(ng, st, p, units_xcd0);
+  else if (ke <= 8) launch_select_mfma<9>(ng, st, p, units_xcd0);
+  else launch_select_mfma<17>(ng, st, p, units_xcd0);
   return check_launch("saf3r_block_select_pooled");
 }
