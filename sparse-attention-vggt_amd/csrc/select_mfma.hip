@@ -262,8 +262,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KL <= 9 ? 4
   wait_frame(min(kSelRing - 2, f1 - 1 - f0));
   barrier_only();
   if (f0 + kSelRing - 1 < f1) fill(f0 + kSelRing - 1);
-  f32x16 acc = products(0);
-  for (int f = f0; f < f1; ++f) {
+  // one frame: its list work on acc (its products), after issuing the next frame's products
+  auto step = [&](const int f, const f32x16& acc) -> f32x16 {
     const int fl = f - f0;
     // frame f + 1's copy landed, and every wave has read frame f's fragments (before this barrier),
     // so frame f + kSelRing may take its stage; the last frame re-runs its own products (unused)
@@ -294,17 +294,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KL <= 9 ? 4
         list_insert<KL>(lst, x);
       }
     // merge with the other half's list (lanes l and l + 32 hold the same query): the whole partner
-    // list first, then the insertions (an entry exchanged after an insertion could be one's own)
-    float other[KL];
+    // list first, then the insertions (an entry exchanged after an insertion could be one's own).
+    // One v_permlane32_swap of an entry with itself leaves [own, partner's] on a half-0 lane and
+    // [partner's, own] on a half-1 lane: every lane merges the second into the first, with tag bit 4
+    // on the second, so a half-0 lane (the only one whose merged list is used) keeps its own list
+    // and takes its partner's without a select.
+    float own[KL], other[KL];  // on half-0 lanes: this half's list (its candidates) and the partner's
 #pragma unroll
     for (int t = 0; t < KL; ++t) {
       const uint32_t u = __builtin_bit_cast(uint32_t, lst[t]);
       const auto rr = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-      other[t] = __builtin_bit_cast(float, (uint32_t)(half ? rr[0] : rr[1]) | 16u);
+      own[t] = __builtin_bit_cast(float, (uint32_t)rr[0]);
+      other[t] = __builtin_bit_cast(float, (uint32_t)rr[1] | 16u);
     }
-    float own[KL];  // this half's list (its candidates, when the pair is listed)
 #pragma unroll
-    for (int t = 0; t < KL; ++t) own[t] = lst[t];
+    for (int t = 0; t < KL; ++t) lst[t] = own[t];
 #pragma unroll
     for (int t = 0; t < KL; ++t) list_insert<KL>(lst, other[t]);
     // certification: a finite threshold (every row in the bound's range, so every value finite) and
@@ -358,8 +362,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KL <= 9 ? 4
         o[0] = kQueued;
       }
     }
-    acc = acc_next;
+    return acc_next;
+  };
+  // two frames per trip, so that the two accumulators alternate instead of being copied (lists of
+  // up to 5 and at most 24 blocks per frame; otherwise the second accumulator's registers spill or
+  // push scalar values out: one frame per trip)
+  f32x16 acc0 = products(0), acc1;
+  int fs = f0;
+  if constexpr (NG <= 3 && KL <= 5) {
+    for (; fs + 1 < f1; fs += 2) {
+      acc1 = step(fs, acc0);
+      acc0 = step(fs + 1, acc1);
+    }
   }
+  for (; fs < f1; ++fs) acc0 = step(fs, acc0);
   __syncthreads();
   // the certified lists: two threads per query, frames of one parity each (the listed pairs are
   // written by the exact pass below); k = 4 lists as one 16-byte store when the output is aligned
