@@ -48,6 +48,7 @@
 // in a certified pair is finite, and finiteness itself is tested on the bits.
 #include <algorithm>
 #include <atomic>
+#include <type_traits>
 
 #include "common.h"
 
@@ -178,21 +179,27 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KL <= 9 ? 4
   // chunk / 16, the global chunk through the swizzle; rows past NBf repeat the frame's last row;
   // with fewer than 512 chunks some copies repeat others, same data to the same place). 128 NG is a
   // multiple of 64, so a wave's chunks stay contiguous from its base.
+  // The copies take the scalar-base form: the frame's records as a uniform base, the lane's byte
+  // offset in them (foff) and the wave's LDS offset in the stage (fdst) fixed per thread.
   const uint32_t ring_base = lds_addr(ring);
-  auto fill = [&](int f) {
-    const uint32_t st = ring_base + ((uint32_t)(f - f0) % kSelRing) * kStage;
+  uint32_t foff[2], fdst[2];
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int base = (256 * u + 64 * w) % (NG * 128), pos = base + lane;
-      const int r = pos >> 4, c = (pos & 15) ^ (r & 15);
-      const int rr = r < p.NBf ? r : p.NBf - 1;
-      const uint16_t* src = p.split + (krec0 + (int64_t)f * p.NBf + rr) * 128 + 8 * c;
-      dma16(src, st + (uint32_t)(16 * base));
-    }
+  for (int u = 0; u < 2; ++u) {
+    const int base = (256 * u + 64 * w) % (NG * 128), pos = base + lane;
+    const int r = pos >> 4, c = (pos & 15) ^ (r & 15);
+    const int rr = r < p.NBf ? r : p.NBf - 1;
+    foff[u] = (uint32_t)(rr * 128 + 8 * c) * 2u;
+    fdst[u] = __builtin_amdgcn_readfirstlane((uint32_t)(16 * base));  // uniform: base depends on the wave only
+  }
+  auto fill = [&](int f, int stage) {  // frame f into ring stage `stage` ((f - f0) mod kSelRing)
+    const uint32_t st = ring_base + (uint32_t)(stage * kStage);
+    const uint16_t* frec = p.split + (krec0 + (int64_t)f * p.NBf) * 128;  // the frame's key records
+    dma16s(frec, foff[0], st + fdst[0]);
+    dma16s(frec, foff[1], st + fdst[1]);
   };
   // the first frames' copies go out first, so that their latency overlaps that of the loads below
   for (int j = 0; j < kSelRing - 1; ++j)
-    if (j < nf) fill(f0 + j);
+    if (j < nf) fill(f0 + j, j);
 
   // Q fragments: lane (col, half) holds features 32 half + 8 st .. + 7 of its query, both fp16 parts
   f16x8 qf[2][4];
@@ -238,8 +245,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KL <= 9 ? 4
     }
   };
   // K fragments of frame g (ring stage g % kSelRing) and its 12 matrix products
-  auto products = [&](int gl) {
-    const char* stg = ring + (gl % kSelRing) * kStage;
+  auto products = [&](int stage) {  // the frame in ring stage `stage`
+    const char* stg = ring + stage * kStage;
     f16x8 kf[2][4];
 #pragma unroll
     for (int pc = 0; pc < 2; ++pc)
@@ -261,16 +268,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KL <= 9 ? 4
   // the matrix cores run them while the same wave works through the lists.
   wait_frame(min(kSelRing - 2, f1 - 1 - f0));
   barrier_only();
-  if (f0 + kSelRing - 1 < f1) fill(f0 + kSelRing - 1);
-  // one frame: its list work on acc (its products), after issuing the next frame's products
-  auto step = [&](const int f, const f32x16& acc) -> f32x16 {
+  if (f0 + kSelRing - 1 < f1) fill(f0 + kSelRing - 1, kSelRing - 1);
+  // one frame: its list work on acc (its products), after issuing the next frame's products. ST:
+  // the frame's ring stage when the caller knows it at compile time (LDS reads then take it as an
+  // immediate offset), else -1
+  auto step = [&](auto stc, const int f, const f32x16& acc) -> f32x16 {
+    constexpr int ST = decltype(stc)::value;
     const int fl = f - f0;
+    const int stage = ST >= 0 ? ST : fl % kSelRing;
     // frame f + 1's copy landed, and every wave has read frame f's fragments (before this barrier),
-    // so frame f + kSelRing may take its stage; the last frame re-runs its own products (unused)
+    // so frame f + kSelRing may take its stage; after the last frame every copy has landed, and the
+    // next stage's products run on whatever it holds (unused)
     wait_frame(min(kSelRing - 2, f1 - 2 - f));
     barrier_only();
-    if (f + kSelRing < f1) fill(f + kSelRing);
-    const f32x16 acc_next = products(f + 1 < f1 ? fl + 1 : fl);
+    if (f + kSelRing < f1) fill(f + kSelRing, stage);
+    const f32x16 acc_next = products(stage + 1 == kSelRing ? 0 : stage + 1);
     // this lane's key blocks 8 g + 4 half + r: their scales (one 16-byte read per group of four)
     float ks[NG][4];
 #pragma unroll
@@ -364,18 +376,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KL <= 9 ? 4
     }
     return acc_next;
   };
-  // two frames per trip, so that the two accumulators alternate instead of being copied (lists of
-  // up to 5 and at most 24 blocks per frame; otherwise the second accumulator's registers spill or
-  // push scalar values out: one frame per trip)
+  // four frames per trip (one per ring stage), so that the two accumulators alternate instead of
+  // being copied and the stages are compile-time offsets (lists of up to 5 and at most 24 blocks
+  // per frame; otherwise the second accumulator's registers spill or push scalar values out: one
+  // frame per trip)
   f32x16 acc0 = products(0), acc1;
   int fs = f0;
   if constexpr (NG <= 3 && KL <= 5) {
-    for (; fs + 1 < f1; fs += 2) {
-      acc1 = step(fs, acc0);
-      acc0 = step(fs + 1, acc1);
+    static_assert(kSelRing == 4, "one trip walks the four stages");
+    for (; fs + 3 < f1; fs += 4) {
+      acc1 = step(std::integral_constant<int, 0>{}, fs, acc0);
+      acc0 = step(std::integral_constant<int, 1>{}, fs + 1, acc1);
+      acc1 = step(std::integral_constant<int, 2>{}, fs + 2, acc0);
+      acc0 = step(std::integral_constant<int, 3>{}, fs + 3, acc1);
     }
   }
-  for (; fs < f1; ++fs) acc0 = step(fs, acc0);
+  for (; fs < f1; ++fs) acc0 = step(std::integral_constant<int, -1>{}, fs, acc0);
   __syncthreads();
   // the certified lists: two threads per query, frames of one parity each (the listed pairs are
   // written by the exact pass below); k = 4 lists as one 16-byte store when the output is aligned
