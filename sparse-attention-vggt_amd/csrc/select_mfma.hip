@@ -245,14 +245,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KL <= 9 ? 4
     }
   };
   // K fragments of frame g (ring stage g % kSelRing) and its 12 matrix products
+  // LDS byte offsets of this lane's eight fragment chunks in a stage (one register each)
+  uint32_t koff[2][4];
+#pragma unroll
+  for (int pc = 0; pc < 2; ++pc)
+#pragma unroll
+    for (int st = 0; st < 4; ++st) koff[pc][st] = (uint32_t)sel_chunk(kr, 8 * pc + 4 * half + st);
   auto products = [&](int stage) {  // the frame in ring stage `stage`
     const char* stg = ring + stage * kStage;
     f16x8 kf[2][4];
 #pragma unroll
     for (int pc = 0; pc < 2; ++pc)
 #pragma unroll
-      for (int st = 0; st < 4; ++st)
-        kf[pc][st] = *reinterpret_cast<const f16x8*>(stg + sel_chunk(kr, 8 * pc + 4 * half + st));
+      for (int st = 0; st < 4; ++st) kf[pc][st] = *reinterpret_cast<const f16x8*>(stg + koff[pc][st]);
     f32x16 a = {};
 #pragma unroll
     for (int st = 0; st < 4; ++st) a = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[0][st], qf[0][st], a, 0, 0, 0);
@@ -442,7 +447,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KL <= 9 ? 4
   for (uint32_t p0 = 0; p0 < nq;) {  // the same trips for every thread
     // pairs p0 .. p1 - 1: the longest run from p0 whose candidates fit (one pair always does)
     const uint32_t base = first(p0);
-    uint32_t lo = p0 + 1, hi = nq;
+    uint32_t lo = ntot - base <= (uint32_t)kCandMax ? nq : p0 + 1, hi = nq;  // all the rest fit: no search
     while (lo < hi) {
       const uint32_t mid = (lo + hi + 1) >> 1;
       if (first(mid) - base <= (uint32_t)kCandMax) lo = mid;
