@@ -464,11 +464,12 @@ def run_stack(pkg, frames, dim, heads, grid, layers, topk, table_fn, steps, warm
     return res
 
 
-def pool_increment(run, reps=10, burst=4):
+def pool_increment(run, reps=30, burst=4):
     """What pooling adds to the pack: the first layer's pack (LayerNorm, RoPE, layouts, scaled Q) with
     and without the block records of its block_topk heads, alternated ``reps`` times; each time
     ``burst`` packs run back to back between two stream events (the GPU stays busy, so the host's
-    launch work between the packs is not timed). Medians of the per-pack times, in ms."""
+    launch work between the packs is not timed). Medians of the per-pack times and of the
+    differences of adjacent bursts (which drift of the clock between bursts affects least), in ms."""
     w, x, pos, geom = run["layers"][0], run["x"], run["pos"], run["geom"]
     ts = {True: [], False: []}
     with torch.no_grad():
@@ -486,7 +487,8 @@ def pool_increment(run, reps=10, burst=4):
                 torch.cuda.synchronize()
                 ts[pool].append(e0.elapsed_time(e1) / burst)
     del qkv
-    return statistics.median(ts[True]), statistics.median(ts[False])
+    diffs = [a - b for a, b in zip(ts[True], ts[False])]
+    return statistics.median(ts[True]), statistics.median(ts[False]), statistics.median(diffs)
 
 
 def da3_leg(pkg, steps, warmup):
@@ -661,8 +663,7 @@ def main():
     sel_ms = dur.get("block_select", [])
     sel_extra = {}
     if sel_ms:
-        pooled_ms, plain_ms = pool_increment(run)
-        inc = pooled_ms - plain_ms
+        pooled_ms, plain_ms, inc = pool_increment(run)
         sel_avg = statistics.fmean(sel_ms)
         fused = max(inc, 0.0) + sel_avg
         sel_extra = {
@@ -676,9 +677,9 @@ def main():
             "fused_path_frac": round(sb["fused_path"] / (fused * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
             "fused_path_bytes": sb["fused_path"],
             "fused_path_note": ("algorithmic bytes (read Q and K of the block_topk heads, write their lists) over the "
-                                "selection's added time: the pack's increment for the block means (medians of "
-                                "alternating bursts of 4 back-to-back packs with / without them, negative values "
-                                "counted as 0) plus the selection kernel"),
+                                "selection's added time: the pack's increment for the block means (median difference "
+                                "of 30 adjacent pairs of bursts of 4 back-to-back packs with / without them, a "
+                                "negative value counted as 0) plus the selection kernel"),
             "heads": n_dyn,
         }
         sel_extra.update(sel_extra_scores)
