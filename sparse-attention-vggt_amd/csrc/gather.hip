@@ -80,31 +80,44 @@ __device__ inline float sum8(float x) {
   x += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x141, 0xF, 0xF, true));
   return x;
 }
-// reductions over the 8 key slots (lanes dg, dg + 8, ..., dg + 56)
+// reductions over the key slots of a query's LANES lanes (lanes dg, dg + 8, ... of its group)
+template <int LANES = 64>
 __device__ inline float slots_max(float x) {
 #pragma unroll
-  for (int o = 8; o < 64; o <<= 1) x = fmaxf(x, __shfl_xor(x, o));
+  for (int o = 8; o < LANES; o <<= 1) x = fmaxf(x, __shfl_xor(x, o));
   return x;
 }
+template <int LANES = 64>
 __device__ inline float slots_sum(float x) {
 #pragma unroll
-  for (int o = 8; o < 64; o <<= 1) x += __shfl_xor(x, o);
+  for (int o = 8; o < LANES; o <<= 1) x += __shfl_xor(x, o);
   return x;
 }
 
-// 4 waves per workgroup, one query row per wave. QK32: q and k rows are fp32 (the reference's gather
-// reads the fp32 q / k of the autocast forward and multiplies in fp32); otherwise bf16. V32 / O32:
-// v / out rows are fp32; otherwise bf16.
-template <bool QK32, bool V32, bool O32, int ENT, bool SLICED>
+// 4 waves per workgroup, QPW query rows per wave (each on 64 / QPW lanes: its key slots are 8 / QPW
+// groups of 8 lanes). Two rows per wave put twice the rows of a walk step in flight at once, so the
+// L2 serves more reads of the step's key rows between two fetches of them. QK32: q and k rows are
+// fp32 (the reference's gather reads the fp32 q / k of the autocast forward and multiplies in fp32);
+// otherwise bf16. V32 / O32: v / out rows are fp32; otherwise bf16.
+template <bool QK32, bool V32, bool O32, int ENT, bool SLICED, int QPW>
 __global__ __launch_bounds__(256) void gather_attn_kernel(GatherParams p) {
-  constexpr int NIT = ENT / 8;  // groups of 8 keys per step
-  const int lane = tid_x() & 63, w = tid_x() >> 6, ks = lane >> 3, dg = lane & 7;
-  // sliced: workgroup b takes rows 4 g .. 4 g + 3, g = (b / 8) % G (G = ceil(n / 4)), of slice
-  // (b % 8) + 8 (b / 8G): slice s runs on XCD s % 8, the XCD's slices one after the other
-  const int64_t ng = (p.n + 3) / 4;
+  static_assert(QPW == 1 || QPW == 2, "one or two rows per wave");
+  constexpr int LANES = 64 / QPW;       // lanes of one row
+  constexpr int SLOTS = LANES / 8;      // key slots of one row
+  constexpr int NIT = ENT / SLOTS;      // groups of SLOTS keys per step
+  static_assert(ENT <= LANES && ENT % SLOTS == 0, "a step's entries sit in the row's lanes");
+  const int lane = tid_x() & 63, w = tid_x() >> 6, dg = lane & 7;
+  const int qh = lane / LANES, qbase = qh * LANES, ks = (lane - qbase) >> 3;
+  constexpr int RPW = 4 * QPW;  // rows per workgroup
+  // sliced: workgroup b takes rows RPW g .. RPW g + RPW - 1, g = (b / 8) % G (G = ceil(n / RPW)),
+  // of slice (b % 8) + 8 (b / 8G): slice s runs on XCD s % 8, the XCD's slices one after the other
+  const int64_t ng = (p.n + RPW - 1) / RPW;
   const int slice = SLICED ? (int)(bid_x() % 8 + 8 * (bid_x() / (8 * ng))) : 0;
-  const int64_t rl = (SLICED ? (int64_t)(bid_x() / 8) % ng : (int64_t)bid_x()) * 4 + w;  // row of this launch
-  if (rl >= p.n) return;  // a whole wave leaves; the kernel has no barrier
+  const int64_t rw = (SLICED ? (int64_t)(bid_x() / 8) % ng : (int64_t)bid_x()) * RPW + w * QPW;  // the wave's first row
+  if (rw >= p.n) return;  // a whole wave leaves; the kernel has no barrier
+  const int64_t rl_raw = rw + qh;  // row of this launch (this lane's half)
+  const bool rvalid = rl_raw < p.n;  // a second row past the end computes on the first's and stores nothing
+  const int64_t rl = rvalid ? rl_raw : rw;
   const int64_t r = SLICED ? p.r0 + rl : rl;
 
   // this lane's 8 dims of q: fp32 values (QK32) or bf16 pairs
@@ -136,25 +149,27 @@ __global__ __launch_bounds__(256) void gather_attn_kernel(GatherParams p) {
   const int len = e_end - e_begin;
 
   const int nsteps = max(1, (len + ENT - 1) / ENT);
-  const int64_t res = SLICED ? max((int64_t)1, p.resident / kGatherSlices) : p.resident;
+  // rows resident at once (waves x rows per wave)
+  const int64_t res = (SLICED ? max((int64_t)1, p.resident / kGatherSlices) : p.resident) * QPW;
   const int s0 = rl < res ? 0 : (int)(((rl - res) * nsteps / res) % nsteps);
-  // entry st * ENT + l of the part, in lane l < ENT (-1 past it or out of range)
+  // entry st * ENT + l of the part, in the row's lane qbase + l, l < ENT (-1 past it or out of range)
   auto entry = [&](int st) {  // (range-checked where it is used)
-    const int e = st * ENT + (lane & (ENT - 1));
-    return (lane < ENT && e < len) ? il[e] : -1;
+    const int li = lane - qbase;
+    const int e = st * ENT + (li & (ENT - 1));
+    return (li < ENT && e < len) ? il[e] : -1;
   };
   int next_id = entry(s0);  // each step's entries are read one step ahead
   for (int sc = 0, st = s0; sc < nsteps; ++sc) {
     const int myid = next_id < p.nk ? next_id : -1;
     st = st + 1 == nsteps ? 0 : st + 1;
     if (sc + 1 < nsteps) next_id = entry(st);
-    // key 8 it + ks of the step: its score and its V dims
+    // key SLOTS it + ks of the step: its score and its V dims
     float s[NIT];
     float vf[NIT][8];     // V32: the V dims of key slot it
     uint32_t vw[NIT][4];  // otherwise the same dims as bf16 pairs
 #pragma unroll
     for (int it = 0; it < NIT; ++it) {
-      const int id = __shfl(myid, 8 * it + ks);
+      const int id = __shfl(myid, qbase + SLOTS * it + ks);
       const int64_t rid = id >= 0 ? id : 0;  // a masked entry reads row 0; its score is dropped
       float part = 0.f;
       if constexpr (QK32) {
@@ -195,7 +210,7 @@ __global__ __launch_bounds__(256) void gather_attn_kernel(GatherParams p) {
     float mx = s[0];
 #pragma unroll
     for (int it = 1; it < NIT; ++it) mx = fmaxf(mx, s[it]);
-    mx = slots_max(mx);
+    mx = slots_max<LANES>(mx);
     const float m_new = fmaxf(m_run, mx);
     const float m_use = m_new == -__builtin_inff() ? 0.f : m_new;
     const float alpha = __builtin_amdgcn_exp2f((m_run - m_use) * p.c);
@@ -217,20 +232,21 @@ __global__ __launch_bounds__(256) void gather_attn_kernel(GatherParams p) {
         }
       }
     }
-    l_run = l_run * alpha + slots_sum(lsum);
+    l_run = l_run * alpha + slots_sum<LANES>(lsum);
     m_run = m_new;
   }
 
-  // sum the 8 key slots' partial outputs; lanes of slot 0 store dims 8 dg .. 8 dg + 7
+  // sum the key slots' partial outputs; lanes of slot 0 store dims 8 dg .. 8 dg + 7
 #pragma unroll
-  for (int d = 0; d < 8; ++d) acc[d] = slots_sum(acc[d]);
+  for (int d = 0; d < 8; ++d) acc[d] = slots_sum<LANES>(acc[d]);
+  if (!rvalid) return;
   if constexpr (SLICED) {  // the slice's unnormalised sum, its maximum and its sum of weights
     float* pr = p.part + (rl * kGatherSlices + slice) * 66;
     if (ks == 0) {
       *reinterpret_cast<f32x4*>(pr + 8 * dg) = f32x4{acc[0], acc[1], acc[2], acc[3]};
       *reinterpret_cast<f32x4*>(pr + 8 * dg + 4) = f32x4{acc[4], acc[5], acc[6], acc[7]};
     }
-    if (lane == 0) {
+    if (lane == qbase) {
       pr[64] = m_run;
       pr[65] = l_run;
     }
@@ -324,6 +340,7 @@ static bool to_dev(const saf3r_rows* s, RowsDev* d, const char* name, bool fp32 
 
 constexpr int kGatherStep = 32;        // list entries per walk step
 constexpr int kGatherStepSliced = 16;  // the same in sliced mode (a slice's 64 entries in 4 steps)
+constexpr int kGatherSlicedRows = 2;   // sliced mode: rows per wave
 constexpr int64_t kGatherChunkRows = 65536;  // sliced mode: rows per pair of launches
 
 // waves of this kernel the device holds at once (for the walk order; 1 if unknown)
@@ -341,7 +358,7 @@ template <bool QK32, bool V32, bool O32>
 static void launch_gather_o(GatherParams p, bool sliced, hipStream_t st) {
   const unsigned rows4 = (unsigned)((p.n + 3) / 4);
   if (sliced) {
-    auto kernel = gather_attn_kernel<QK32, V32, O32, kGatherStepSliced, true>;
+    auto kernel = gather_attn_kernel<QK32, V32, O32, kGatherStepSliced, true, kGatherSlicedRows>;
     p.resident = resident_waves(kernel);
     // rows in chunks: one chunk's partial results (138 MB) stay in the memory-side cache between
     // its two kernels, and the workspace holds one chunk
@@ -349,12 +366,13 @@ static void launch_gather_o(GatherParams p, bool sliced, hipStream_t st) {
     for (int64_t r0 = 0; r0 < n; r0 += kGatherChunkRows) {
       p.r0 = r0;
       p.n = (int)(n - r0 < kGatherChunkRows ? n - r0 : kGatherChunkRows);
+      const unsigned gs = (unsigned)((p.n + 4 * kGatherSlicedRows - 1) / (4 * kGatherSlicedRows));
       const unsigned g4 = (unsigned)((p.n + 3) / 4);
-      hipLaunchKernelGGL(kernel, dim3(g4 * kGatherSlices), dim3(256), 0, st, p);
+      hipLaunchKernelGGL(kernel, dim3(gs * kGatherSlices), dim3(256), 0, st, p);
       hipLaunchKernelGGL(gather_merge_kernel<O32>, dim3(g4), dim3(256), 0, st, p);
     }
   } else {
-    auto kernel = gather_attn_kernel<QK32, V32, O32, kGatherStep, false>;
+    auto kernel = gather_attn_kernel<QK32, V32, O32, kGatherStep, false, 1>;
     p.resident = resident_waves(kernel);
     hipLaunchKernelGGL(kernel, dim3(rows4), dim3(256), 0, st, p);
   }
