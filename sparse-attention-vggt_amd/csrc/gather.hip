@@ -6,23 +6,23 @@
 //      shares one list across rows), :173-258 (online-softmax variant for TopK > 2048).
 // The work is one gathered K row and one V row per (query, listed key): bound by the cache
 // bandwidth of those row reads, not by arithmetic (a list is one query's own, so there is no
-// matrix product to share between queries). One wave owns one query row and walks its list in
-// steps of ENT entries with an fp32 online softmax, so any list length is handled by the same
-// kernel. Lane l serves key slot ks = l / 8 of every group of 8 keys and dims 8 dg .. 8 dg + 7
-// (dg = l % 8): 8 lanes read a K or V row together (32 bytes each of an fp32 K row, 16 of a bf16
-// row), so one load instruction moves 8 whole rows, and the 8 partial dot products of a row are
-// summed by three DPP steps inside the 8 lanes. Entries < 0 or >= num_keys are skipped. q and k
+// matrix product to share between queries). A wave owns two query rows (32 lanes each) and walks
+// their lists in steps of ENT entries with an fp32 online softmax, so any list length is handled by
+// the same kernel. Lane l of a row's 32 serves key slot ks = l / 8 of every group of 4 keys and dims
+// 8 dg .. 8 dg + 7 (dg = l % 8): 8 lanes read a K or V row together (32 bytes each of an fp32 K row,
+// 16 of a bf16 row), so one load instruction moves 8 whole rows (4 of each query), and the 8 partial
+// dot products of a row are summed by three DPP steps inside the 8 lanes. Entries < 0 or >= num_keys are skipped. q and k
 // are bf16 or fp32 rows (the reference's kernel upcasts either); v and out are bf16 or fp32 rows
 // (the reference writes out in v.dtype from its fp32 accumulator).
 //
 // Walk order: the rows are shared by many queries (at the dino-head shape each key row is in about
 // 512 lists), but a list spans every frame, far more than an L2 holds. So the waves resident at one
-// moment walk the same window of list positions: wave r starts its walk at step
-// s0 = max(0, r - C) * nsteps / C (mod nsteps), C = the waves the GPU holds at once (from the
-// kernel's occupancy). Waves are dispatched in row order and take about the same time, so when
-// wave r starts, the waves still running started one step time apart per C / nsteps rows and stand
-// at the step r does: every resident wave reads the rows of the same few steps. The order depends
-// on r alone, so results are run-to-run identical.
+// moment walk the same window of list positions: row r starts its walk at step
+// s0 = max(0, r - C) * nsteps / C (mod nsteps), C = the rows the GPU holds at once (resident waves,
+// from the kernel's occupancy, times rows per wave). Waves are dispatched in row order and take
+// about the same time, so when row r starts, the rows still running started one step time apart per
+// C / nsteps rows and stand at the step r does: every resident wave reads the rows of the same few
+// steps. The order depends on r alone, so results are run-to-run identical.
 #include "common.h"
 
 namespace saf3r {
@@ -340,7 +340,7 @@ static bool to_dev(const saf3r_rows* s, RowsDev* d, const char* name, bool fp32 
 
 constexpr int kGatherStep = 32;        // list entries per walk step
 constexpr int kGatherStepSliced = 16;  // the same in sliced mode (a slice's 64 entries in 4 steps)
-constexpr int kGatherSlicedRows = 2;   // sliced mode: rows per wave
+constexpr int kGatherRows = 2;  // rows per wave (both modes)
 constexpr int64_t kGatherChunkRows = 65536;  // sliced mode: rows per pair of launches
 
 // waves of this kernel the device holds at once (for the walk order; 1 if unknown)
@@ -356,9 +356,8 @@ static int64_t resident_waves(K kernel) {
 
 template <bool QK32, bool V32, bool O32>
 static void launch_gather_o(GatherParams p, bool sliced, hipStream_t st) {
-  const unsigned rows4 = (unsigned)((p.n + 3) / 4);
   if (sliced) {
-    auto kernel = gather_attn_kernel<QK32, V32, O32, kGatherStepSliced, true, kGatherSlicedRows>;
+    auto kernel = gather_attn_kernel<QK32, V32, O32, kGatherStepSliced, true, kGatherRows>;
     p.resident = resident_waves(kernel);
     // rows in chunks: one chunk's partial results (138 MB) stay in the memory-side cache between
     // its two kernels, and the workspace holds one chunk
@@ -366,15 +365,15 @@ static void launch_gather_o(GatherParams p, bool sliced, hipStream_t st) {
     for (int64_t r0 = 0; r0 < n; r0 += kGatherChunkRows) {
       p.r0 = r0;
       p.n = (int)(n - r0 < kGatherChunkRows ? n - r0 : kGatherChunkRows);
-      const unsigned gs = (unsigned)((p.n + 4 * kGatherSlicedRows - 1) / (4 * kGatherSlicedRows));
+      const unsigned gs = (unsigned)((p.n + 4 * kGatherRows - 1) / (4 * kGatherRows));
       const unsigned g4 = (unsigned)((p.n + 3) / 4);
       hipLaunchKernelGGL(kernel, dim3(gs * kGatherSlices), dim3(256), 0, st, p);
       hipLaunchKernelGGL(gather_merge_kernel<O32>, dim3(g4), dim3(256), 0, st, p);
     }
   } else {
-    auto kernel = gather_attn_kernel<QK32, V32, O32, kGatherStep, false, 1>;
+    auto kernel = gather_attn_kernel<QK32, V32, O32, kGatherStep, false, kGatherRows>;
     p.resident = resident_waves(kernel);
-    hipLaunchKernelGGL(kernel, dim3(rows4), dim3(256), 0, st, p);
+    hipLaunchKernelGGL(kernel, dim3((unsigned)((p.n + 4 * kGatherRows - 1) / (4 * kGatherRows))), dim3(256), 0, st, p);
   }
 }
 
