@@ -30,13 +30,13 @@
 // the pairs at 128 frames on random-init weights).
 //
 // Decomposition: a workgroup of 4 waves owns 128 query blocks (32 per wave) of one head and a
-// range of frames. Each frame's key records (NBf rows of 256 bytes, contiguous) are copied once
+// group of frames (or a piece of one, below). Each frame's key records (NBf rows of 256 bytes, contiguous) are copied once
 // per workgroup into a 4-stage LDS ring (3 stages for 32-block frames) by LDS-DMA loads, 16-byte chunks
 // XOR-swizzled by row so that the 32 rows a fragment read touches fall into 16 distinct chunk
 // columns. Per frame a wave runs S^T = K . Q^T for the frame's key blocks (padded to 32 rows)
 // against its 32 queries: lane (col, half) holds query col and 16 key rows 8 g + 4 half + r; each
 // tagged value is inserted into a sorted list of the KL best (one max and KL - 1 med3 per value),
-// the two halves merge their lists through v_permlane32_swap, and the gaps of the merged list
+// the two halves exchange their lists through v_permlane32_swap and merge, and the gaps of the merged list
 // decide the pair. A lane's own values carry tag v (its value index 4 g + r); entries taken from the
 // other half get tag bit 4 set, so a half-0 lane reads key 8 (t & 15) / 4 + 4 (t >> 4) + (t & 3)
 // back from tag t. The key scales and the frames' largest key norms are staged in LDS once per
@@ -244,14 +244,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KL <= 9 ? 4
       default: wait_vm<0>(); break;
     }
   };
-  // K fragments of frame g (ring stage g % kSelRing) and its 12 matrix products
   // LDS byte offsets of this lane's eight fragment chunks in a stage (one register each)
   uint32_t koff[2][4];
 #pragma unroll
   for (int pc = 0; pc < 2; ++pc)
 #pragma unroll
     for (int st = 0; st < 4; ++st) koff[pc][st] = (uint32_t)sel_chunk(kr, 8 * pc + 4 * half + st);
-  auto products = [&](int stage) {  // the frame in ring stage `stage`
+  auto products = [&](int stage) {  // K fragments of the frame in ring stage `stage`, 12 matrix products
     const char* stg = ring + stage * kStage;
     f16x8 kf[2][4];
 #pragma unroll
